@@ -1,0 +1,269 @@
+/*
+ * k3x_hip_moe.h -- C ABI of the MI355X (gfx950) routed-expert MoE layer.
+ *
+ * Plain C: opaque handles, plain pointers and sizes, int status codes.  No
+ * exception crosses this boundary and no torch type appears in it.  Every
+ * entry point validates its arguments before it touches device state
+ * (fail-closed), and returns one of the k3x_status values, which are the
+ * numeric values of k3x::ErrorCode (runtime/include/k3x/status.hpp:9-31).
+ *
+ * Pointer conventions: parameters documented "host" are CPU memory, "device"
+ * are HIP device memory of the context's device.  All device work is
+ * enqueued on the context's stream; entry points return after enqueueing
+ * unless documented otherwise.  Errors detected by kernels (non-finite input,
+ * invalid router scores) are latched in a per-context status word that
+ * k3x_hip_ctx_synchronize() returns and clears; a latched error makes every
+ * later kernel of the context skip its work until it is read.
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * the rsb1813/project-k3x tree).
+ */
+#ifndef K3X_HIP_MOE_H
+#define K3X_HIP_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K3X_HIP_ABI_VERSION 1
+
+/* k3x::ErrorCode values (runtime/include/k3x/status.hpp:9-31). */
+enum k3x_status {
+    K3X_OK = 0,
+    K3X_ERR_INVALID_EXTENT = 9,
+    K3X_ERR_TENSOR_NOT_FOUND = 14,
+    K3X_ERR_INVALID_MXFP4 = 15,
+    K3X_ERR_INVALID_STATE = 16,
+    K3X_ERR_BACKEND_UNAVAILABLE = 17,
+};
+
+/* GLU activation policy.  SiTU: runtime/src/ops.cpp:20-30.
+ * SwiGLU: silu(g) * u with silu from runtime/src/model.cpp:60-61. */
+enum k3x_glu { K3X_GLU_SWIGLU = 0, K3X_GLU_SITU = 1 };
+
+/* Renormalisation of the selected router scores.
+ * FLOAT:  runtime/src/routing_policy.cpp:146-157 (synthetic/resident path).
+ * DOUBLE: runtime/src/official_moe.cpp:235-242 (official path). */
+enum k3x_renorm { K3X_RENORM_FLOAT = 0, K3X_RENORM_DOUBLE = 1 };
+
+/* Matrices of one expert, as addressed by the debug/read-back entry points. */
+enum k3x_matrix { K3X_MATRIX_GATE = 0, K3X_MATRIX_UP = 1, K3X_MATRIX_DOWN = 2 };
+
+/* Streams of the portable synthetic generator (k3x_hip_bank_fill_synthetic):
+ * stream id = (kind << 32) | expert index. */
+enum k3x_synth_stream {
+    K3X_STREAM_GATE_CODES = 1,
+    K3X_STREAM_GATE_SCALES = 2,
+    K3X_STREAM_UP_CODES = 3,
+    K3X_STREAM_UP_SCALES = 4,
+    K3X_STREAM_DOWN_CODES = 5,
+    K3X_STREAM_DOWN_SCALES = 6,
+    K3X_STREAM_ROUTER = 7,
+    K3X_STREAM_BIAS = 8,
+    K3X_STREAM_SHARED_GATE = 9,
+    K3X_STREAM_SHARED_UP = 10,
+    K3X_STREAM_SHARED_DOWN = 11,
+    K3X_STREAM_INPUT = 12,
+};
+
+typedef struct k3x_hip_ctx k3x_hip_ctx;
+typedef struct k3x_hip_bank k3x_hip_bank;
+
+/* Shape of one MoE layer.  hidden and inter must be multiples of 128,
+ * group_size must be 32 (the CUDA backend's contract,
+ * runtime/cuda/backend_cuda.cu:1865-1867), shared_inter is 0 (no shared
+ * expert) or a multiple of 128. */
+typedef struct k3x_hip_layer_desc {
+    uint32_t hidden;
+    uint32_t inter;
+    uint32_t experts;
+    uint32_t group_size;
+    uint32_t shared_inter;
+} k3x_hip_layer_desc;
+
+/* Per-call parameters of the layer.  Mirrors the scalar arguments of
+ * ComputeBackend::resident_mxfp4_moe_layer (runtime/include/k3x/
+ * backend.hpp:369-375) plus the router controls that runtime/src/
+ * model.cpp:917-1010 applies on the host. */
+typedef struct k3x_hip_moe_params {
+    uint32_t tokens;          /* T, rows of x */
+    uint32_t top_k;           /* natural Top-K, 1..64 and <= experts */
+    float routed_scale;       /* multiplies renormalised weights */
+    float rms_epsilon;        /* > 0 */
+    uint32_t glu;             /* enum k3x_glu */
+    float situ_beta;          /* > 0, SiTU only */
+    uint32_t has_situ_linear; /* SiTU only */
+    float situ_linear_beta;   /* > 0 when has_situ_linear */
+    uint32_t renorm;          /* enum k3x_renorm */
+} k3x_hip_moe_params;
+
+/* Optional device buffers that receive intermediates of k3x_hip_moe_forward;
+ * any member may be NULL.  Shapes use T = tokens, K = top_k, E = experts,
+ * H = hidden, I = inter, S = shared_inter. */
+typedef struct k3x_hip_moe_taps {
+    uint16_t* normed_x;          /* [T][H] bf16 bits, RMSNorm output */
+    float* logits;               /* [T][E] */
+    uint32_t* ids;               /* [T][K] router order */
+    float* weights;              /* [T][K] contributions */
+    uint32_t* counts;            /* [E] pairs per expert */
+    uint32_t* offsets;           /* [E+1] expert-major CSR offsets */
+    uint32_t* pair_token;        /* [T*K] CSR rows -> token */
+    uint32_t* pair_slot;         /* [T*K] CSR rows -> router slot */
+    uint32_t* first_use;         /* [E] min(token*K+slot), 0xffffffff unused */
+    uint32_t* n_active;          /* [1] experts with at least one pair */
+    uint32_t* active_first_use;  /* [E] active experts in first-use order */
+    uint16_t* act;               /* [T*K][I] bf16 bits, CSR row order */
+    float* expert_out;           /* [T][K][H] per-pair down projections */
+    float* shared_out;           /* [T][H] shared expert output */
+    float* out_f32;              /* [T][H] output before the bf16 cast */
+} k3x_hip_moe_taps;
+
+/* Descriptor of the seeded synthetic bank (no reference counterpart: the
+ * reference's benches read converted checkpoints).  Codes are uniform over
+ * the 16 E2M1 codes, scale bytes uniform over [scale_lo, scale_hi], normal
+ * tensors are Irwin-Hall(12) approximations of N(0, sigma^2). */
+typedef struct k3x_hip_synth_desc {
+    uint64_t seed;
+    uint32_t scale_lo;
+    uint32_t scale_hi;
+    float router_sigma;
+    float bias_sigma;
+    float shared_sigma;
+    float gamma_value;
+} k3x_hip_synth_desc;
+
+/* Counters, after BackendRuntimeStats (runtime/include/k3x/backend.hpp:50-129). */
+typedef struct k3x_hip_stats {
+    uint64_t forward_calls;
+    uint64_t kernel_launches;
+    uint64_t scratch_bytes;
+    uint64_t resident_weight_bytes;
+    uint64_t weight_h2d_bytes;
+    uint64_t experts_resident;
+} k3x_hip_stats;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Replaces make_cuda_backend (runtime/include/k3x/backend.hpp:465-466;
+ * runtime/cuda/backend_cuda.cu:5264-5367): one device, one stream. */
+int k3x_hip_ctx_create(int device, k3x_hip_ctx** out);
+int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx);
+/* Enqueue on a caller-owned hipStream_t (NULL = the device's null stream). */
+int k3x_hip_ctx_set_stream(k3x_hip_ctx* ctx, void* hip_stream);
+/* Back to the context's own non-blocking stream (the default). */
+int k3x_hip_ctx_use_own_stream(k3x_hip_ctx* ctx);
+void* k3x_hip_ctx_stream(k3x_hip_ctx* ctx);
+/* Waits for the stream, returns and clears the latched kernel status.
+ * Replaces the cudaStreamSynchronize at the end of each backend call
+ * (e.g. runtime/cuda/backend_cuda.cu:2421). */
+int k3x_hip_ctx_synchronize(k3x_hip_ctx* ctx);
+/* Replaces ComputeBackend::runtime_stats (backend.hpp:331). */
+int k3x_hip_ctx_stats(k3x_hip_ctx* ctx, k3x_hip_stats* out);
+const char* k3x_hip_status_name(int status); /* error_code_name, status.hpp:33-56 */
+
+/* ---- resident expert bank ------------------------------------------------ */
+
+/* Replaces ResidentWeightTable (runtime/cuda/resident_weights.cuh:19-25,
+ * resident_weights.cu:107-166): the whole layer's bank is allocated once in
+ * HBM in the gfx950 tile layout and admitted expert by expert. */
+int k3x_hip_bank_create(k3x_hip_ctx* ctx, const k3x_hip_layer_desc* desc,
+                        k3x_hip_bank** out);
+int k3x_hip_bank_destroy(k3x_hip_bank* bank);
+/* Admits one expert from host memory in the K3X reference layout (packed
+ * [rows][cols/2], low nibble = even column; scales [rows][cols/32] E8M0),
+ * gate/up [inter x hidden], down [hidden x inter].  tensor_ids are the
+ * residency identities (non-zero, unique within the bank), as in
+ * Mxfp4WeightView::tensor_id (backend.hpp:150-157).  Scale byte 0xFF is
+ * rejected with K3X_ERR_INVALID_MXFP4 (runtime/src/ops.cpp:46-49).
+ * Synchronous. */
+int k3x_hip_bank_upload_expert(k3x_hip_bank* bank, uint32_t expert,
+                               const uint64_t tensor_ids[3],
+                               const uint8_t* gate_packed,
+                               const uint8_t* gate_scales,
+                               const uint8_t* up_packed,
+                               const uint8_t* up_scales,
+                               const uint8_t* down_packed,
+                               const uint8_t* down_scales);
+/* Finds the expert/matrix admitted under tensor_id (host). */
+int k3x_hip_bank_find(k3x_hip_bank* bank, uint64_t tensor_id,
+                      uint32_t* expert, uint32_t* matrix);
+/* Shared expert, host bf16 bits: gate/up [shared_inter x hidden],
+ * down [hidden x shared_inter] (Bf16MlpView, backend.hpp:165-169). */
+int k3x_hip_bank_upload_shared(k3x_hip_bank* bank, const uint16_t* gate,
+                               const uint16_t* up, const uint16_t* down);
+/* Router weight fp32 [experts x hidden], correction bias fp32 [experts],
+ * RMSNorm weight fp32 [hidden]; host memory (router_weight /
+ * correction_bias of runtime/src/model.cpp:918-922). */
+int k3x_hip_bank_upload_router(k3x_hip_bank* bank, const float* weight,
+                               const float* bias, const float* gamma);
+/* Same, from device memory (no host round trip). */
+int k3x_hip_bank_set_router_device(k3x_hip_bank* bank, const float* weight,
+                                   const float* bias, const float* gamma);
+/* Fills every expert, the router, the bias, gamma and the shared expert
+ * from the seeded generator on the device (identical to the oracle's
+ * generator, so the CPU checker can regenerate any expert). */
+int k3x_hip_bank_fill_synthetic(k3x_hip_bank* bank,
+                                const k3x_hip_synth_desc* desc);
+/* Fills a device bf16 tensor of n elements with the seeded normal generator
+ * (stream K3X_STREAM_INPUT). */
+int k3x_hip_synth_normal_bf16(k3x_hip_ctx* ctx, uint64_t seed,
+                              uint64_t stream, float sigma, size_t n,
+                              uint16_t* out);
+/* Debug read-back: rows [row0, row0+nrows) of one matrix, dequantised to
+ * fp32 by the same conversion the GEMM kernels use, into device memory
+ * out [nrows][cols].  Replaces decode_mxfp4 (runtime/src/ops.cpp:32-55)
+ * for the bit-exact weight check. */
+int k3x_hip_bank_dequant_rows(k3x_hip_bank* bank, uint32_t expert,
+                              uint32_t matrix, uint32_t row0, uint32_t nrows,
+                              float* out);
+uint64_t k3x_hip_bank_bytes(const k3x_hip_bank* bank);
+
+/* ---- the layer ----------------------------------------------------------- */
+
+/* One routed-expert MoE layer over T tokens with device routing:
+ *   xn  = bf16(RMSNorm(x) * gamma)                        (ops.cpp:10-18)
+ *   ids, w = natural Top-K of sigmoid(W_r xn) + bias,
+ *            renormalised, * routed_scale    (model.cpp:917-1009,
+ *            routing_policy.cpp:31-160 / official_moe.cpp:211-245)
+ *   expert-major grouping                          (expert_major.cpp:10-54)
+ *   y[t][k] = down(bf16(GLU(gate xn, up xn)))   (backend_cpu.cpp:124-154)
+ *   out = bf16(sum_k w[t][k] y[t][k] + shared(xn))  (backend_cpu.cpp:295-301,
+ *                                                    model.cpp:1145)
+ * x: device bf16 [T][hidden]; out: device bf16 [T][hidden]; taps optional.
+ * Replaces ComputeBackend::resident_mxfp4_moe_layer (backend.hpp:369-375,
+ * runtime/cuda/backend_cuda.cu:1789-2545) for a latent-free layer with
+ * routing on the device.  Asynchronous. */
+int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                        const k3x_hip_moe_params* params, const uint16_t* x,
+                        uint16_t* out, const k3x_hip_moe_taps* taps);
+
+/* The same layer with host-decided routes (the reference's own contract:
+ * routing on the host, model.cpp:917-1010): xn is the already-normalised
+ * bf16 input [T][hidden], ids/weights device [T][K] in router order.  Routes
+ * must not repeat an expert within a token and weights must be finite
+ * (checked on the host copy passed in host_ids/host_weights, which may be
+ * NULL to skip the check).  Replaces ComputeBackend::mxfp4_situ_moe
+ * (backend.hpp:364-368) batched over tokens.  Asynchronous. */
+int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                               const k3x_hip_moe_params* params,
+                               const uint16_t* xn, const uint32_t* ids,
+                               const float* weights, const uint32_t* host_ids,
+                               const float* host_weights, uint16_t* out,
+                               const k3x_hip_moe_taps* taps);
+
+/* Expert-major grouping of device ids [T][K] into the CSR taps (counts,
+ * offsets, pair_token, pair_slot, first_use, n_active, active_first_use must
+ * be non-NULL).  Replaces build_expert_major_plan
+ * (runtime/include/k3x/expert_major.hpp:33-34, expert_major.cpp:10-54).
+ * Asynchronous. */
+int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids,
+                              uint32_t tokens, uint32_t top_k,
+                              uint32_t experts, const k3x_hip_moe_taps* taps);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,577 @@
+/*
+ * k3x_oracle.c -- CPU restatement of the K3X routed-expert MoE-layer path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels.  The product
+ * never links or calls it.  Compiled with -ffp-contract=off so every float
+ * and double operation below rounds exactly where it is written.
+ *
+ * Reference citations are file:line in the rsb1813/project-k3x tree.
+ */
+#include "k3x_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* bf16                                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Round-to-nearest-even to bf16, kept in a float; NaN stays quiet NaN.
+ * Restates runtime/src/official_moe.cpp:18-26. */
+float k3xo_round_bf16(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    if ((bits & 0x7f800000u) == 0x7f800000u) {
+        if (bits & 0x007fffffu) bits |= 0x00400000u;
+        bits &= 0xffff0000u;
+    } else {
+        bits += 0x7fffu + ((bits >> 16) & 1u);
+        bits &= 0xffff0000u;
+    }
+    memcpy(&value, &bits, 4);
+    return value;
+}
+
+uint16_t k3xo_bf16_bits(float value) {
+    const float rounded = k3xo_round_bf16(value);
+    uint32_t bits;
+    memcpy(&bits, &rounded, 4);
+    return (uint16_t)(bits >> 16);
+}
+
+/* runtime/src/official_moe.cpp:135-137 */
+float k3xo_bf16_to_f32(uint16_t word) {
+    const uint32_t bits = (uint32_t)word << 16;
+    float value;
+    memcpy(&value, &bits, 4);
+    return value;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MXFP4                                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* E2M1 code -> value, low nibble = even column.  runtime/src/ops.cpp:40-43 */
+static const float k_e2m1[16] = {
+    0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+    -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f,
+};
+
+static int mxfp4_contract_ok(size_t packed_len, size_t scales_len,
+                             size_t rows, size_t cols, size_t group) {
+    /* runtime/src/ops.cpp:36-39 */
+    if (!rows || !cols || !group || cols % group || cols % 2) return 0;
+    if (rows > ((size_t)-1) / cols) return 0;
+    if (packed_len != rows * cols / 2) return 0;
+    if (scales_len != rows * cols / group) return 0;
+    return 1;
+}
+
+static int scales_ok(const uint8_t* scales, size_t n) {
+    /* runtime/src/ops.cpp:46-49: 0xFF (E8M0 NaN) is rejected. */
+    for (size_t i = 0; i < n; ++i)
+        if (scales[i] == 0xffu) return 0;
+    return 1;
+}
+
+static void decode_row(const uint8_t* packed, const uint8_t* scales,
+                       size_t row, size_t cols, size_t group, float* out) {
+    const size_t base = row * cols;
+    for (size_t c = 0; c < cols; ++c) {
+        const size_t index = base + c;
+        const uint8_t pair = packed[index / 2];
+        const uint8_t code = (index % 2) ? (uint8_t)(pair >> 4)
+                                         : (uint8_t)(pair & 0x0fu);
+        const int exponent = (int)scales[index / group] - 127;
+        out[c] = ldexpf(k_e2m1[code], exponent);
+    }
+}
+
+/* runtime/src/ops.cpp:32-55 */
+int k3xo_decode_mxfp4(const uint8_t* packed, size_t packed_len,
+                      const uint8_t* scales, size_t scales_len, size_t rows,
+                      size_t cols, size_t group_size, float* out) {
+    if (!mxfp4_contract_ok(packed_len, scales_len, rows, cols, group_size) ||
+        !scales_ok(scales, scales_len))
+        return K3XO_INVALID_MXFP4;
+    for (size_t r = 0; r < rows; ++r)
+        decode_row(packed, scales, r, cols, group_size, out + r * cols);
+    return K3XO_OK;
+}
+
+/* y[r] = float(sum_c double(x[c]) * W[r][c]), sequential in c.
+ * runtime/src/ops.cpp:57-76 (decoded row by row instead of materialising
+ * the whole matrix; same values, same order, same result). */
+int k3xo_mxfp4_matvec(const float* input, size_t input_len,
+                      const uint8_t* packed, size_t packed_len,
+                      const uint8_t* scales, size_t scales_len, size_t rows,
+                      size_t cols, size_t group_size, float* out) {
+    if (input_len != cols) return K3XO_INVALID_MXFP4;
+    if (!mxfp4_contract_ok(packed_len, scales_len, rows, cols, group_size) ||
+        !scales_ok(scales, scales_len))
+        return K3XO_INVALID_MXFP4;
+    float* row_values = (float*)malloc(cols * sizeof(float));
+    if (!row_values) return K3XO_INVALID_MXFP4;
+    for (size_t r = 0; r < rows; ++r) {
+        decode_row(packed, scales, r, cols, group_size, row_values);
+        double sum = 0.0;
+        for (size_t c = 0; c < cols; ++c)
+            sum += (double)input[c] * (double)row_values[c];
+        out[r] = (float)sum;
+    }
+    free(row_values);
+    return K3XO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Canonical double reduction shared with the HIP kernels                   */
+/* ------------------------------------------------------------------------ */
+
+#define K3XO_CANON_LANES 256
+
+/* Pairwise tree: tree(p, n) = tree(p, n/2) + tree(p + n/2, n/2).  This is
+ * what an xor-butterfly over 64 lanes followed by (w0+w1)+(w2+w3) across
+ * four waves produces. */
+static double tree_sum(const double* p, size_t n) {
+    if (n == 1) return p[0];
+    return tree_sum(p, n / 2) + tree_sum(p + n / 2, n / 2);
+}
+
+/* 256 strided partials (lane i sums elements i, i+256, ... sequentially),
+ * then the pairwise tree.  Canonical order; no reference counterpart. */
+double k3xo_canon_dot(const float* a, const float* b, size_t n) {
+    double partial[K3XO_CANON_LANES];
+    for (size_t lane = 0; lane < K3XO_CANON_LANES; ++lane) {
+        double sum = 0.0;
+        for (size_t k = lane; k < n; k += K3XO_CANON_LANES)
+            sum += (double)a[k] * (double)b[k];
+        partial[lane] = sum;
+    }
+    return tree_sum(partial, K3XO_CANON_LANES);
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm and GLU                                                          */
+/* ------------------------------------------------------------------------ */
+
+static void rms_scale(float* out, const float* in, const float* weight,
+                      size_t n, float epsilon, double squares) {
+    /* runtime/src/ops.cpp:14-17 */
+    const float inverse =
+        1.0f / sqrtf((float)(squares / (double)n) + epsilon);
+    for (size_t i = 0; i < n; ++i) out[i] = in[i] * inverse * weight[i];
+}
+
+/* runtime/src/ops.cpp:10-18 (sequential double sum of squares). */
+void k3xo_rms_norm(float* out, const float* in, const float* weight, size_t n,
+                   float epsilon) {
+    double squares = 0.0;
+    for (size_t i = 0; i < n; ++i) squares += (double)in[i] * in[i];
+    rms_scale(out, in, weight, n, epsilon, squares);
+}
+
+/* Same as k3xo_rms_norm with the canonical order for the sum of squares. */
+void k3xo_rms_norm_canon(float* out, const float* in, const float* weight,
+                         size_t n, float epsilon) {
+    rms_scale(out, in, weight, n, epsilon, k3xo_canon_dot(in, in, n));
+}
+
+/* SiTU-GLU: runtime/src/ops.cpp:20-30.
+ * SwiGLU:   silu(g)*u, silu(v) = v * sigmoid(v): runtime/src/model.cpp:60-61. */
+void k3xo_glu(float* out, const float* gate, const float* up, size_t n,
+              int kind, float beta, int has_linear, float linear_beta) {
+    for (size_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        const float sigmoid = 1.0f / (1.0f + expf(-g));
+        if (kind == K3XO_GLU_SITU) {
+            const float bounded_gate = beta * tanhf(g / beta) * sigmoid;
+            const float bounded_up =
+                has_linear ? linear_beta * tanhf(up[i] / linear_beta) : up[i];
+            out[i] = bounded_gate * bounded_up;
+        } else {
+            out[i] = (g * sigmoid) * up[i];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Router                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Correctly rounded expf evaluated in double: x = k*ln2 + r, Taylor series
+ * of degree 13 on |r| <= ln2/2 (truncation < 5e-18), one rounding to float.
+ * The HIP router evaluates the identical operation sequence. */
+float k3xo_expf_cr(float x) {
+    if (x != x) return x;
+    if (x > 100.0f) return INFINITY;
+    if (x < -110.0f) return 0.0f;
+    const double xd = (double)x;
+    const double k = rint(xd * 1.4426950408889634);
+    double r = fma(-k, 6.93147180369123816490e-01, xd);
+    r = fma(-k, 1.90821492927058770002e-10, r);
+    double p = 1.6059043836821614599e-10;          /* 1/13! */
+    p = fma(p, r, 2.0876756987868098979e-09);       /* 1/12! */
+    p = fma(p, r, 2.5052108385441718775e-08);       /* 1/11! */
+    p = fma(p, r, 2.7557319223985890653e-07);       /* 1/10! */
+    p = fma(p, r, 2.7557319223985890653e-06);       /* 1/9!  */
+    p = fma(p, r, 2.4801587301587301587e-05);       /* 1/8!  */
+    p = fma(p, r, 1.9841269841269841270e-04);       /* 1/7!  */
+    p = fma(p, r, 1.3888888888888888889e-03);       /* 1/6!  */
+    p = fma(p, r, 8.3333333333333333333e-03);       /* 1/5!  */
+    p = fma(p, r, 4.1666666666666666667e-02);       /* 1/4!  */
+    p = fma(p, r, 1.6666666666666666667e-01);       /* 1/3!  */
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    return (float)ldexp(p, (int)k);
+}
+
+/* sigmoid(v) = 1 / (1 + exp(-v)) in float.  runtime/src/model.cpp:60,
+ * runtime/src/official_moe.cpp:221. */
+float k3xo_sigmoid(float x, int mode) {
+    const float e = mode == K3XO_SIGMOID_CR ? k3xo_expf_cr(-x) : expf(-x);
+    return 1.0f / (1.0f + e);
+}
+
+/* logits[e] = float(sum_h double(W[e][h]) * x[h]).
+ * SEQ:   runtime/src/backend_cpu.cpp:33-41 (dense_matvec, fp32 router W,
+ *        called from runtime/src/model.cpp:919-921).
+ * CANON: the order of the HIP router kernel. */
+void k3xo_router_logits(const float* weight, const float* x, size_t experts,
+                        size_t hidden, int order, float* logits) {
+    for (size_t e = 0; e < experts; ++e) {
+        const float* row = weight + e * hidden;
+        double sum;
+        if (order == K3XO_ORDER_CANON) {
+            sum = k3xo_canon_dot(row, x, hidden);
+        } else {
+            sum = 0.0;
+            for (size_t h = 0; h < hidden; ++h)
+                sum += (double)row[h] * (double)x[h];
+        }
+        logits[e] = (float)sum;
+    }
+}
+
+static int finitef(float v) { return isfinite(v) != 0; }
+
+/* Sigmoid scores, bias-adjusted natural Top-K (ties -> lower expert index),
+ * renormalised contributions times routed_scale.
+ * Selection: runtime/src/routing_policy.cpp:76-87 (stable_sort descending),
+ *            runtime/src/official_moe.cpp:224-233 (explicit tie comparator).
+ * FLOAT renorm + validation: runtime/src/routing_policy.cpp:40-50,89-95,
+ *            146-157; routed_scale: runtime/src/model.cpp:1004-1009.
+ * DOUBLE renorm + validation: runtime/src/official_moe.cpp:214-242. */
+int k3xo_route(const float* logits, const float* bias, size_t experts,
+               size_t top_k, int renorm, float routed_scale, int sigmoid_mode,
+               uint32_t* ids, float* weights, float* scores) {
+    const int dims_error =
+        renorm == K3XO_RENORM_DOUBLE ? K3XO_INVALID_EXTENT : K3XO_INVALID_STATE;
+    if (!experts || !top_k || top_k > experts) return dims_error;
+    float* adjusted = (float*)malloc(experts * sizeof(float));
+    unsigned char* taken = (unsigned char*)calloc(experts, 1);
+    int status = K3XO_OK;
+    if (!adjusted || !taken) {
+        status = dims_error;
+        goto done;
+    }
+    for (size_t e = 0; e < experts; ++e) {
+        if (renorm == K3XO_RENORM_DOUBLE &&
+            (!finitef(logits[e]) || !finitef(bias[e]))) {
+            status = K3XO_INVALID_EXTENT;
+            goto done;
+        }
+        scores[e] = k3xo_sigmoid(logits[e], sigmoid_mode);
+        if (renorm == K3XO_RENORM_FLOAT &&
+            (!finitef(scores[e]) || scores[e] < 0.0f || scores[e] > 1.0f ||
+             !finitef(bias[e]))) {
+            status = K3XO_INVALID_STATE;
+            goto done;
+        }
+        adjusted[e] = scores[e] + bias[e];
+        if (renorm == K3XO_RENORM_FLOAT && !finitef(adjusted[e])) {
+            status = K3XO_INVALID_STATE;
+            goto done;
+        }
+    }
+    for (size_t slot = 0; slot < top_k; ++slot) {
+        size_t best = experts;
+        for (size_t e = 0; e < experts; ++e) {
+            if (taken[e]) continue;
+            if (best == experts || adjusted[e] > adjusted[best]) best = e;
+        }
+        taken[best] = 1;
+        ids[slot] = (uint32_t)best;
+    }
+    if (renorm == K3XO_RENORM_DOUBLE) {
+        double total = 0.0;
+        for (size_t slot = 0; slot < top_k; ++slot) total += scores[ids[slot]];
+        if (!isfinite(total) || total <= 0.0) {
+            status = K3XO_INVALID_EXTENT;
+            goto done;
+        }
+        for (size_t slot = 0; slot < top_k; ++slot)
+            weights[slot] =
+                (float)((double)scores[ids[slot]] / total) * routed_scale;
+    } else {
+        float denominator = 0.0f;
+        for (size_t slot = 0; slot < top_k; ++slot)
+            denominator += scores[ids[slot]];
+        if (!finitef(denominator) || denominator <= 0.0f) {
+            status = K3XO_INVALID_STATE;
+            goto done;
+        }
+        for (size_t slot = 0; slot < top_k; ++slot)
+            weights[slot] = (scores[ids[slot]] / denominator) * routed_scale;
+    }
+done:
+    free(adjusted);
+    free(taken);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Expert-major grouping                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* Groups in first-use order (scan tokens, then router slots); assignments
+ * inside a group in (token, slot) order.  runtime/src/expert_major.cpp:10-54.
+ * Routes have a fixed length top_k here (natural Top-K). */
+int k3xo_expert_major_plan(const uint32_t* ids, const float* contributions,
+                           size_t tokens, size_t top_k, size_t* n_groups,
+                           uint32_t* group_expert, uint32_t* group_start,
+                           uint32_t* assign_token, uint32_t* assign_slot,
+                           float* assign_contribution) {
+    if (!tokens || !top_k) return K3XO_INVALID_EXTENT;
+    const size_t pairs = tokens * top_k;
+    for (size_t t = 0; t < tokens; ++t) {
+        for (size_t s = 0; s < top_k; ++s) {
+            if (!finitef(contributions[t * top_k + s])) return K3XO_INVALID_STATE;
+            for (size_t q = 0; q < s; ++q)
+                if (ids[t * top_k + q] == ids[t * top_k + s])
+                    return K3XO_INVALID_STATE;
+        }
+    }
+    /* First-use group order. */
+    size_t groups = 0;
+    uint32_t* group_of_pair = (uint32_t*)malloc(pairs * sizeof(uint32_t));
+    uint32_t* sizes = (uint32_t*)calloc(pairs, sizeof(uint32_t));
+    if (!group_of_pair || !sizes) {
+        free(group_of_pair);
+        free(sizes);
+        return K3XO_INVALID_EXTENT;
+    }
+    for (size_t p = 0; p < pairs; ++p) {
+        size_t g = 0;
+        while (g < groups && group_expert[g] != ids[p]) ++g;
+        if (g == groups) group_expert[groups++] = ids[p];
+        group_of_pair[p] = (uint32_t)g;
+        ++sizes[g];
+    }
+    group_start[0] = 0;
+    for (size_t g = 0; g < groups; ++g) group_start[g + 1] = group_start[g] + sizes[g];
+    memset(sizes, 0, pairs * sizeof(uint32_t));
+    for (size_t p = 0; p < pairs; ++p) {
+        const uint32_t g = group_of_pair[p];
+        const uint32_t at = group_start[g] + sizes[g]++;
+        assign_token[at] = (uint32_t)(p / top_k);
+        assign_slot[at] = (uint32_t)(p % top_k);
+        assign_contribution[at] = contributions[p];
+    }
+    *n_groups = groups;
+    free(group_of_pair);
+    free(sizes);
+    return K3XO_OK;
+}
+
+/* The ascending-expert CSR form of the same grouping, plus each expert's
+ * first-use key min(token*top_k + slot); sorting active experts by that key
+ * reproduces the group order of k3xo_expert_major_plan. */
+int k3xo_expert_major_csr(const uint32_t* ids, size_t tokens, size_t top_k,
+                          size_t experts, uint32_t* counts, uint32_t* offsets,
+                          uint32_t* pair_token, uint32_t* pair_slot,
+                          uint32_t* first_use, uint32_t* n_active,
+                          uint32_t* active_ascending,
+                          uint32_t* active_first_use) {
+    if (!tokens || !top_k || !experts) return K3XO_INVALID_EXTENT;
+    const size_t pairs = tokens * top_k;
+    memset(counts, 0, experts * sizeof(uint32_t));
+    for (size_t e = 0; e < experts; ++e) first_use[e] = 0xffffffffu;
+    for (size_t p = 0; p < pairs; ++p) {
+        if (ids[p] >= experts) return K3XO_INVALID_STATE;
+        ++counts[ids[p]];
+        if (first_use[ids[p]] == 0xffffffffu) first_use[ids[p]] = (uint32_t)p;
+    }
+    offsets[0] = 0;
+    uint32_t active = 0;
+    for (size_t e = 0; e < experts; ++e) {
+        offsets[e + 1] = offsets[e] + counts[e];
+        if (counts[e]) active_ascending[active++] = (uint32_t)e;
+    }
+    uint32_t* fill = (uint32_t*)calloc(experts, sizeof(uint32_t));
+    if (!fill) return K3XO_INVALID_EXTENT;
+    for (size_t p = 0; p < pairs; ++p) {
+        const uint32_t e = ids[p];
+        const uint32_t at = offsets[e] + fill[e]++;
+        pair_token[at] = (uint32_t)(p / top_k);
+        pair_slot[at] = (uint32_t)(p % top_k);
+    }
+    free(fill);
+    /* Insertion sort of the active experts by first-use key. */
+    for (uint32_t i = 0; i < active; ++i) active_first_use[i] = active_ascending[i];
+    for (uint32_t i = 1; i < active; ++i) {
+        const uint32_t v = active_first_use[i];
+        uint32_t j = i;
+        while (j > 0 && first_use[active_first_use[j - 1]] > first_use[v]) {
+            active_first_use[j] = active_first_use[j - 1];
+            --j;
+        }
+        active_first_use[j] = v;
+    }
+    *n_active = active;
+    return K3XO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Expert FFN, shared expert, ordered mix                                   */
+/* ------------------------------------------------------------------------ */
+
+/* gate/up GEMV -> GLU -> (optional bf16 rounding of the activation) -> down.
+ * runtime/src/backend_cpu.cpp:124-154 (mxfp4_situ_mlp_group, one expert);
+ * runtime/src/official_moe.cpp:82-103 for the same composition.  act_out,
+ * when non-NULL, receives the activation fed to the down projection. */
+int k3xo_expert_ffn(const float* x, size_t hidden, size_t inter,
+                    const uint8_t* gate_packed, const uint8_t* gate_scales,
+                    const uint8_t* up_packed, const uint8_t* up_scales,
+                    const uint8_t* down_packed, const uint8_t* down_scales,
+                    int glu, float beta, int has_linear, float linear_beta,
+                    int round_act, float* act_out, float* out) {
+    const size_t gate_len = inter * hidden / 2, gate_scale_len = inter * hidden / 32;
+    float* gate = (float*)malloc(inter * sizeof(float));
+    float* up = (float*)malloc(inter * sizeof(float));
+    float* act = (float*)malloc(inter * sizeof(float));
+    int status = K3XO_INVALID_MXFP4;
+    if (!gate || !up || !act) goto done;
+    status = k3xo_mxfp4_matvec(x, hidden, gate_packed, gate_len, gate_scales,
+                               gate_scale_len, inter, hidden, 32, gate);
+    if (status) goto done;
+    status = k3xo_mxfp4_matvec(x, hidden, up_packed, gate_len, up_scales,
+                               gate_scale_len, inter, hidden, 32, up);
+    if (status) goto done;
+    k3xo_glu(act, gate, up, inter, glu, beta, has_linear, linear_beta);
+    if (round_act)
+        for (size_t i = 0; i < inter; ++i) act[i] = k3xo_round_bf16(act[i]);
+    if (act_out) memcpy(act_out, act, inter * sizeof(float));
+    status = k3xo_mxfp4_matvec(act, inter, down_packed, hidden * inter / 2,
+                               down_scales, hidden * inter / 32, hidden, inter,
+                               32, out);
+done:
+    free(gate);
+    free(up);
+    free(act);
+    return status;
+}
+
+/* Double-accumulated bf16-weight GEMV without output rounding.
+ * runtime/src/official_moe.cpp:39-59 minus the final round_bf16 (the
+ * layer here keeps the shared projections in fp32). */
+void k3xo_bf16_matvec(const float* x, const uint16_t* weight, size_t rows,
+                      size_t cols, float* out) {
+    for (size_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        const uint16_t* row = weight + r * cols;
+        for (size_t c = 0; c < cols; ++c)
+            sum += (double)k3xo_bf16_to_f32(row[c]) * (double)x[c];
+        out[r] = (float)sum;
+    }
+}
+
+/* Shared expert: runtime/src/official_moe.cpp:105-117 (bf16 weights) with
+ * the activation optionally rounded to bf16 before the down projection. */
+void k3xo_shared_ffn(const float* x, size_t hidden, size_t inter,
+                     const uint16_t* gate, const uint16_t* up,
+                     const uint16_t* down, int glu, float beta, int has_linear,
+                     float linear_beta, int round_act, float* out) {
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    float* a = (float*)malloc(inter * sizeof(float));
+    if (!g || !u || !a) goto done;
+    k3xo_bf16_matvec(x, gate, inter, hidden, g);
+    k3xo_bf16_matvec(x, up, inter, hidden, u);
+    k3xo_glu(a, g, u, inter, glu, beta, has_linear, linear_beta);
+    if (round_act)
+        for (size_t i = 0; i < inter; ++i) a[i] = k3xo_round_bf16(a[i]);
+    k3xo_bf16_matvec(a, down, hidden, inter, out);
+done:
+    free(g);
+    free(u);
+    free(a);
+}
+
+/* mixed[h] = sum over slots in router order of w[slot] * y[slot][h], float,
+ * starting from 0.  runtime/src/backend_cpu.cpp:295-301, model.cpp:1127-1138. */
+void k3xo_ordered_mix(const float* expert_out, const float* weights,
+                      size_t top_k, size_t width, float* mixed) {
+    for (size_t h = 0; h < width; ++h) mixed[h] = 0.0f;
+    for (size_t slot = 0; slot < top_k; ++slot)
+        for (size_t h = 0; h < width; ++h)
+            mixed[h] += weights[slot] * expert_out[slot * width + h];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Portable synthetic inputs (no reference counterpart)                     */
+/* ------------------------------------------------------------------------ */
+
+/* SplitMix64 output function (Steele, Lea & Flood, OOPSLA 2014). */
+uint64_t k3xo_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+#define K3XO_GAMMA 0x9e3779b97f4a7c15ull
+
+uint64_t k3xo_stream_key(uint64_t seed, uint64_t stream) {
+    return k3xo_mix64(seed + K3XO_GAMMA * (stream + 1));
+}
+
+static uint64_t word_at(uint64_t key, uint64_t index) {
+    return k3xo_mix64(key + K3XO_GAMMA * (index + 1));
+}
+
+/* Packed E2M1 bytes: byte p is byte (p % 8) of word p / 8, so both nibbles
+ * are uniform over the 16 codes. */
+void k3xo_synth_codes(uint64_t key, size_t nbytes, uint8_t* out) {
+    for (size_t p = 0; p < nbytes; ++p)
+        out[p] = (uint8_t)(word_at(key, p >> 3) >> ((p & 7) * 8));
+}
+
+/* E8M0 scale bytes uniform over [lo, hi]. */
+void k3xo_synth_scales(uint64_t key, size_t n, uint32_t lo, uint32_t hi,
+                       uint8_t* out) {
+    const uint64_t span = (uint64_t)(hi - lo + 1);
+    for (size_t i = 0; i < n; ++i)
+        out[i] = (uint8_t)(lo + (uint32_t)(word_at(key, i) % span));
+}
+
+/* Irwin-Hall(12) approximation of N(0, sigma^2): twelve 16-bit uniforms from
+ * three words, summed as integers; every float step is exact except the
+ * final multiply by sigma. */
+static float normal_at(uint64_t key, size_t i, float sigma) {
+    int32_t sum = 0;
+    for (int j = 0; j < 3; ++j) {
+        const uint64_t w = word_at(key, 3 * (uint64_t)i + (uint64_t)j);
+        for (int q = 0; q < 4; ++q) sum += (int32_t)((w >> (16 * q)) & 0xffffu);
+    }
+    return ((float)(sum - 393216) * 0x1p-16f) * sigma;
+}
+
+void k3xo_synth_normal(uint64_t key, size_t n, float sigma, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = normal_at(key, i, sigma);
+}
+
+void k3xo_synth_normal_bf16(uint64_t key, size_t n, float sigma,
+                            uint16_t* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = k3xo_bf16_bits(normal_at(key, i, sigma));
+}

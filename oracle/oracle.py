@@ -1,0 +1,440 @@
+"""ctypes bindings for the CPU checker libraries.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py.  The product path never imports this module.
+
+* ``Oracle`` wraps ``oracle/liboracle.so``, the C restatement of the reference
+  path (k3x_oracle.c, every function cites the reference file:line it follows).
+* ``RefLib`` wraps ``oracle/_ref/libk3x_ref.so``, the reference's own CPU
+  sources compiled in place by ``oracle/Makefile`` (absent unless built).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libk3x_ref.so")
+
+OK, INVALID_EXTENT, INVALID_MXFP4, INVALID_STATE = 0, 9, 15, 16
+GLU_SWIGLU, GLU_SITU = 0, 1
+RENORM_FLOAT, RENORM_DOUBLE = 0, 1
+SIGMOID_REF, SIGMOID_CR = 0, 1
+ORDER_SEQ, ORDER_CANON = 0, 1
+
+_f32p = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+_u16p = C.POINTER(C.c_uint16)
+_u32p = C.POINTER(C.c_uint32)
+_sz = C.c_size_t
+
+
+def _p(a: np.ndarray, ptype):
+    return a.ctypes.data_as(ptype)
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def bf16_to_f32(words: np.ndarray) -> np.ndarray:
+    return (np.asarray(words, dtype=np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(a: np.ndarray) -> np.ndarray:
+    """RNE to bf16 kept in float32 (official_moe.cpp:18-26), vectorised."""
+    bits = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (bits & 0x7F800000) == 0x7F800000
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    special = np.where((bits & 0x007FFFFF) != 0, bits | 0x00400000, bits)
+    special = (special & 0xFFFF0000).astype(np.uint32)
+    return np.where(nan, special, rounded).view(np.float32)
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    return (round_bf16(a).view(np.uint32) >> 16).astype(np.uint16)
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(path)
+        L.k3xo_round_bf16.restype = C.c_float
+        L.k3xo_round_bf16.argtypes = [C.c_float]
+        L.k3xo_expf_cr.restype = C.c_float
+        L.k3xo_expf_cr.argtypes = [C.c_float]
+        L.k3xo_sigmoid.restype = C.c_float
+        L.k3xo_sigmoid.argtypes = [C.c_float, C.c_int]
+        L.k3xo_canon_dot.restype = C.c_double
+        L.k3xo_canon_dot.argtypes = [_f32p, _f32p, _sz]
+        L.k3xo_decode_mxfp4.argtypes = [_u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
+        L.k3xo_mxfp4_matvec.argtypes = [_f32p, _sz, _u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
+        L.k3xo_rms_norm.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
+        L.k3xo_rms_norm_canon.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
+        L.k3xo_glu.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_int, C.c_float, C.c_int, C.c_float]
+        L.k3xo_router_logits.argtypes = [_f32p, _f32p, _sz, _sz, C.c_int, _f32p]
+        L.k3xo_route.argtypes = [_f32p, _f32p, _sz, _sz, C.c_int, C.c_float, C.c_int,
+                                 _u32p, _f32p, _f32p]
+        L.k3xo_expert_major_plan.argtypes = [_u32p, _f32p, _sz, _sz, C.POINTER(_sz), _u32p,
+                                             _u32p, _u32p, _u32p, _f32p]
+        L.k3xo_expert_major_csr.argtypes = [_u32p, _sz, _sz, _sz, _u32p, _u32p, _u32p, _u32p,
+                                            _u32p, _u32p, _u32p, _u32p]
+        L.k3xo_expert_ffn.argtypes = [_f32p, _sz, _sz, _u8p, _u8p, _u8p, _u8p, _u8p, _u8p,
+                                      C.c_int, C.c_float, C.c_int, C.c_float, C.c_int,
+                                      _f32p, _f32p]
+        L.k3xo_bf16_matvec.argtypes = [_f32p, _u16p, _sz, _sz, _f32p]
+        L.k3xo_shared_ffn.argtypes = [_f32p, _sz, _sz, _u16p, _u16p, _u16p, C.c_int,
+                                      C.c_float, C.c_int, C.c_float, C.c_int, _f32p]
+        L.k3xo_ordered_mix.argtypes = [_f32p, _f32p, _sz, _sz, _f32p]
+        L.k3xo_mix64.restype = C.c_uint64
+        L.k3xo_mix64.argtypes = [C.c_uint64]
+        L.k3xo_stream_key.restype = C.c_uint64
+        L.k3xo_stream_key.argtypes = [C.c_uint64, C.c_uint64]
+        L.k3xo_synth_codes.argtypes = [C.c_uint64, _sz, _u8p]
+        L.k3xo_synth_scales.argtypes = [C.c_uint64, _sz, C.c_uint32, C.c_uint32, _u8p]
+        L.k3xo_synth_normal.argtypes = [C.c_uint64, _sz, C.c_float, _f32p]
+        L.k3xo_synth_normal_bf16.argtypes = [C.c_uint64, _sz, C.c_float, _u16p]
+
+    # -- scalar helpers ----------------------------------------------------
+    def expf_cr(self, x: float) -> float:
+        return self.lib.k3xo_expf_cr(x)
+
+    def sigmoid(self, x: float, mode: int = SIGMOID_CR) -> float:
+        return self.lib.k3xo_sigmoid(x, mode)
+
+    # -- MXFP4 -------------------------------------------------------------
+    def decode_mxfp4(self, packed, scales, rows, cols, group=32):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.zeros(rows * cols, np.float32)
+        st = self.lib.k3xo_decode_mxfp4(_p(packed, _u8p), packed.size, _p(scales, _u8p),
+                                        scales.size, rows, cols, group, _p(out, _f32p))
+        return st, out.reshape(rows, cols)
+
+    def mxfp4_matvec(self, x, packed, scales, rows, cols, group=32):
+        x = f32(x)
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.zeros(rows, np.float32)
+        st = self.lib.k3xo_mxfp4_matvec(_p(x, _f32p), x.size, _p(packed, _u8p), packed.size,
+                                        _p(scales, _u8p), scales.size, rows, cols, group,
+                                        _p(out, _f32p))
+        return st, out
+
+    # -- element-wise -----------------------------------------------------
+    def rms_norm(self, x, w, eps, canon=False):
+        x, w = f32(x), f32(w)
+        out = np.zeros_like(x)
+        fn = self.lib.k3xo_rms_norm_canon if canon else self.lib.k3xo_rms_norm
+        fn(_p(out, _f32p), _p(x, _f32p), _p(w, _f32p), x.size, eps)
+        return out
+
+    def glu(self, gate, up, kind=GLU_SWIGLU, beta=4.0, linear=None):
+        gate, up = f32(gate), f32(up)
+        out = np.zeros_like(gate)
+        self.lib.k3xo_glu(_p(out, _f32p), _p(gate, _f32p), _p(up, _f32p), gate.size, kind,
+                          beta, int(linear is not None), linear or 0.0)
+        return out
+
+    # -- router -------------------------------------------------------------
+    def canon_dot(self, a, b):
+        a, b = f32(a), f32(b)
+        return self.lib.k3xo_canon_dot(_p(a, _f32p), _p(b, _f32p), a.size)
+
+    def router_logits(self, W, x, order=ORDER_CANON):
+        W, x = f32(W), f32(x)
+        E, H = W.shape
+        out = np.zeros(E, np.float32)
+        self.lib.k3xo_router_logits(_p(W, _f32p), _p(x, _f32p), E, H, order, _p(out, _f32p))
+        return out
+
+    def route(self, logits, bias, top_k, renorm=RENORM_FLOAT, routed_scale=1.0,
+              sigmoid=SIGMOID_CR):
+        logits, bias = f32(logits), f32(bias)
+        E = logits.size
+        ids = np.zeros(top_k, np.uint32)
+        w = np.zeros(top_k, np.float32)
+        scores = np.zeros(E, np.float32)
+        st = self.lib.k3xo_route(_p(logits, _f32p), _p(bias, _f32p), E, top_k, renorm,
+                                 routed_scale, sigmoid, _p(ids, _u32p), _p(w, _f32p),
+                                 _p(scores, _f32p))
+        return st, ids, w, scores
+
+    # -- grouping -------------------------------------------------------------
+    def expert_major_plan(self, ids, contributions):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        c = f32(contributions)
+        T, K = ids.shape
+        P = T * K
+        n = _sz(0)
+        ge = np.zeros(P, np.uint32)
+        gs = np.zeros(P + 1, np.uint32)
+        at = np.zeros(P, np.uint32)
+        asl = np.zeros(P, np.uint32)
+        ac = np.zeros(P, np.float32)
+        st = self.lib.k3xo_expert_major_plan(_p(ids, _u32p), _p(c, _f32p), T, K, C.byref(n),
+                                             _p(ge, _u32p), _p(gs, _u32p), _p(at, _u32p),
+                                             _p(asl, _u32p), _p(ac, _f32p))
+        g = n.value
+        return st, dict(group_expert=ge[:g], group_start=gs[:g + 1], token=at, slot=asl,
+                        contribution=ac)
+
+    def expert_major_csr(self, ids, experts):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        T, K = ids.shape
+        P = T * K
+        counts = np.zeros(experts, np.uint32)
+        offsets = np.zeros(experts + 1, np.uint32)
+        pt = np.zeros(P, np.uint32)
+        ps = np.zeros(P, np.uint32)
+        fu = np.zeros(experts, np.uint32)
+        na = np.zeros(1, np.uint32)
+        aa = np.zeros(experts, np.uint32)
+        af = np.zeros(experts, np.uint32)
+        st = self.lib.k3xo_expert_major_csr(_p(ids, _u32p), T, K, experts, _p(counts, _u32p),
+                                            _p(offsets, _u32p), _p(pt, _u32p), _p(ps, _u32p),
+                                            _p(fu, _u32p), _p(na, _u32p), _p(aa, _u32p),
+                                            _p(af, _u32p))
+        n = int(na[0])
+        return st, dict(counts=counts, offsets=offsets, pair_token=pt, pair_slot=ps,
+                        first_use=fu, n_active=n, active_ascending=aa[:n],
+                        active_first_use=af[:n])
+
+    # -- expert FFN / layer pieces -------------------------------------------
+    def expert_ffn(self, x, ex, hidden, inter, glu=GLU_SWIGLU, beta=4.0, linear=None,
+                   round_act=True):
+        x = f32(x)
+        out = np.zeros(hidden, np.float32)
+        act = np.zeros(inter, np.float32)
+        arrs = [np.ascontiguousarray(ex[k], dtype=np.uint8) for k in
+                ("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+                 "down_scales")]
+        st = self.lib.k3xo_expert_ffn(_p(x, _f32p), hidden, inter,
+                                      *[_p(a, _u8p) for a in arrs], glu, beta,
+                                      int(linear is not None), linear or 0.0, int(round_act),
+                                      _p(act, _f32p), _p(out, _f32p))
+        return st, act, out
+
+    def bf16_matvec(self, x, w_bits):
+        x = f32(x)
+        w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+        rows, cols = w.shape
+        out = np.zeros(rows, np.float32)
+        self.lib.k3xo_bf16_matvec(_p(x, _f32p), _p(w, _u16p), rows, cols, _p(out, _f32p))
+        return out
+
+    def shared_ffn(self, x, gate, up, down, glu=GLU_SWIGLU, beta=4.0, linear=None,
+                   round_act=True):
+        x = f32(x)
+        gate, up, down = (np.ascontiguousarray(a, dtype=np.uint16) for a in (gate, up, down))
+        inter, hidden = gate.shape
+        out = np.zeros(hidden, np.float32)
+        self.lib.k3xo_shared_ffn(_p(x, _f32p), hidden, inter, _p(gate, _u16p), _p(up, _u16p),
+                                 _p(down, _u16p), glu, beta, int(linear is not None),
+                                 linear or 0.0, int(round_act), _p(out, _f32p))
+        return out
+
+    def ordered_mix(self, expert_out, weights):
+        y = f32(expert_out)
+        w = f32(weights)
+        K, width = y.shape
+        out = np.zeros(width, np.float32)
+        self.lib.k3xo_ordered_mix(_p(y, _f32p), _p(w, _f32p), K, width, _p(out, _f32p))
+        return out
+
+    # -- synthetic inputs -----------------------------------------------------
+    def stream_key(self, seed: int, stream: int) -> int:
+        return self.lib.k3xo_stream_key(seed, stream)
+
+    def synth_codes(self, key, nbytes):
+        out = np.zeros(nbytes, np.uint8)
+        self.lib.k3xo_synth_codes(key, nbytes, _p(out, _u8p))
+        return out
+
+    def synth_scales(self, key, n, lo, hi):
+        out = np.zeros(n, np.uint8)
+        self.lib.k3xo_synth_scales(key, n, lo, hi, _p(out, _u8p))
+        return out
+
+    def synth_normal(self, key, n, sigma):
+        out = np.zeros(n, np.float32)
+        self.lib.k3xo_synth_normal(key, n, sigma, _p(out, _f32p))
+        return out
+
+    def synth_normal_bf16(self, key, n, sigma):
+        out = np.zeros(n, np.uint16)
+        self.lib.k3xo_synth_normal_bf16(key, n, sigma, _p(out, _u16p))
+        return out
+
+
+class _ExpertBytes(C.Structure):
+    _fields_ = [(n, _u8p) for n in ("gate_packed", "gate_scales", "up_packed", "up_scales",
+                                   "down_packed", "down_scales")]
+
+
+def expert_struct(ex) -> tuple[_ExpertBytes, list]:
+    keep = [np.ascontiguousarray(ex[k], dtype=np.uint8) for k in
+            ("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+             "down_scales")]
+    return _ExpertBytes(*[_p(a, _u8p) for a in keep]), keep
+
+
+class RefLib:
+    """The reference's own CPU path (compiled from its sources by the Makefile)."""
+
+    def __init__(self, path: str = REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.k3xr_decode_mxfp4.argtypes = [_u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
+        L.k3xr_mxfp4_matvec.argtypes = [_f32p, _sz, _u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
+        L.k3xr_rms_norm.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
+        L.k3xr_situ_glu.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float, C.c_int, C.c_float]
+        L.k3xr_route_official_logits.argtypes = [_f32p, _f32p, _sz, _sz, _u32p, _f32p, _f32p]
+        L.k3xr_select_routing_natural.argtypes = [_f32p, _f32p, _sz, _sz, _u32p, _f32p]
+        L.k3xr_expert_major_plan.argtypes = [_u32p, _f32p, _sz, _sz, C.POINTER(_sz), _u32p,
+                                             _u32p, _u32p, _u32p, _f32p]
+        L.k3xr_dense_matvec.argtypes = [_f32p, _f32p, _sz, _sz, _f32p]
+        EB = C.POINTER(_ExpertBytes)
+        L.k3xr_mxfp4_situ_mlp_group.argtypes = [_f32p, _sz, _sz, EB, _sz, C.c_float, C.c_int,
+                                                C.c_float, _f32p]
+        L.k3xr_mxfp4_situ_moe.argtypes = [_f32p, _sz, _sz, EB, _f32p, _sz, C.c_float, C.c_int,
+                                          C.c_float, _f32p]
+        L.k3xr_moe_layer_token.argtypes = [_f32p, _f32p, C.c_float, _f32p, _f32p, _sz, _sz, _sz,
+                                           _sz, C.c_float, EB, _f32p, _f32p, _f32p, _sz,
+                                           C.c_float, C.c_int, C.c_float, _u32p, _f32p]
+
+    def decode_mxfp4(self, packed, scales, rows, cols, group=32):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.zeros(rows * cols, np.float32)
+        st = self.lib.k3xr_decode_mxfp4(_p(packed, _u8p), packed.size, _p(scales, _u8p),
+                                        scales.size, rows, cols, group, _p(out, _f32p))
+        return st, out.reshape(rows, cols)
+
+    def mxfp4_matvec(self, x, packed, scales, rows, cols, group=32):
+        x = f32(x)
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.uint8)
+        out = np.zeros(rows, np.float32)
+        st = self.lib.k3xr_mxfp4_matvec(_p(x, _f32p), x.size, _p(packed, _u8p), packed.size,
+                                        _p(scales, _u8p), scales.size, rows, cols, group,
+                                        _p(out, _f32p))
+        return st, out
+
+    def rms_norm(self, x, w, eps):
+        x, w = f32(x), f32(w)
+        out = np.zeros_like(x)
+        self.lib.k3xr_rms_norm(_p(out, _f32p), _p(x, _f32p), _p(w, _f32p), x.size, eps)
+        return out
+
+    def situ_glu(self, gate, up, beta, linear=None):
+        gate, up = f32(gate), f32(up)
+        out = np.zeros_like(gate)
+        self.lib.k3xr_situ_glu(_p(out, _f32p), _p(gate, _f32p), _p(up, _f32p), gate.size, beta,
+                               int(linear is not None), linear or 0.0)
+        return out
+
+    def route_official_logits(self, logits, correction, top_k):
+        logits, correction = f32(logits), f32(correction)
+        E = logits.size
+        ids = np.zeros(top_k, np.uint32)
+        c = np.zeros(top_k, np.float32)
+        s = np.zeros(E, np.float32)
+        st = self.lib.k3xr_route_official_logits(_p(logits, _f32p), _p(correction, _f32p), E,
+                                                 top_k, _p(ids, _u32p), _p(c, _f32p),
+                                                 _p(s, _f32p))
+        return st, ids, c, s
+
+    def select_routing(self, scores, bias, top_k):
+        scores, bias = f32(scores), f32(bias)
+        ids = np.zeros(top_k, np.uint32)
+        w = np.zeros(top_k, np.float32)
+        st = self.lib.k3xr_select_routing_natural(_p(scores, _f32p), _p(bias, _f32p),
+                                                  scores.size, top_k, _p(ids, _u32p),
+                                                  _p(w, _f32p))
+        return st, ids, w
+
+    def expert_major_plan(self, ids, contributions):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        c = f32(contributions)
+        T, K = ids.shape
+        P = T * K
+        n = _sz(0)
+        ge = np.zeros(P, np.uint32)
+        gs = np.zeros(P + 1, np.uint32)
+        at = np.zeros(P, np.uint32)
+        asl = np.zeros(P, np.uint32)
+        ac = np.zeros(P, np.float32)
+        st = self.lib.k3xr_expert_major_plan(_p(ids, _u32p), _p(c, _f32p), T, K, C.byref(n),
+                                             _p(ge, _u32p), _p(gs, _u32p), _p(at, _u32p),
+                                             _p(asl, _u32p), _p(ac, _f32p))
+        g = n.value
+        return st, dict(group_expert=ge[:g], group_start=gs[:g + 1], token=at, slot=asl,
+                        contribution=ac)
+
+    def dense_matvec(self, x, W):
+        x, W = f32(x), f32(W)
+        rows, cols = W.shape
+        out = np.zeros(rows, np.float32)
+        st = self.lib.k3xr_dense_matvec(_p(x, _f32p), _p(W, _f32p), rows, cols, _p(out, _f32p))
+        return st, out
+
+    def mxfp4_situ_mlp_group(self, x, experts, hidden, inter, beta, linear=None):
+        x = f32(x)
+        structs, keep = zip(*[expert_struct(e) for e in experts])
+        arr = (_ExpertBytes * len(structs))(*structs)
+        out = np.zeros((len(structs), hidden), np.float32)
+        st = self.lib.k3xr_mxfp4_situ_mlp_group(_p(x, _f32p), hidden, inter, arr, len(structs),
+                                                beta, int(linear is not None), linear or 0.0,
+                                                _p(out, _f32p))
+        del keep
+        return st, out
+
+    def moe_layer_token(self, x, gamma, eps, router, bias, experts_by_id, hidden, inter,
+                        top_k, routed_scale, shared=None, beta=4.0, linear=None):
+        """One token through the reference CPU composition; experts_by_id is a
+        list indexed by expert id (entries for unrouted experts may be None
+        only if they are never selected)."""
+        x, gamma, router, bias = f32(x), f32(gamma), f32(router), f32(bias)
+        E = bias.size
+        zero = dict(gate_packed=np.zeros(1, np.uint8), gate_scales=np.zeros(1, np.uint8),
+                    up_packed=np.zeros(1, np.uint8), up_scales=np.zeros(1, np.uint8),
+                    down_packed=np.zeros(1, np.uint8), down_scales=np.zeros(1, np.uint8))
+        structs, keep = zip(*[expert_struct(e if e is not None else zero)
+                              for e in experts_by_id])
+        arr = (_ExpertBytes * E)(*structs)
+        ids = np.zeros(top_k, np.uint32)
+        out = np.zeros(hidden, np.float32)
+        if shared is not None:
+            sg, su, sd = (f32(a) for a in shared)
+            s_inter = sg.shape[0]
+        else:
+            sg = su = sd = np.zeros(1, np.float32)
+            s_inter = 0
+        st = self.lib.k3xr_moe_layer_token(_p(x, _f32p), _p(gamma, _f32p), eps,
+                                           _p(router, _f32p), _p(bias, _f32p), E, hidden, inter,
+                                           top_k, routed_scale, arr, _p(sg, _f32p),
+                                           _p(su, _f32p), _p(sd, _f32p), s_inter, beta,
+                                           int(linear is not None), linear or 0.0,
+                                           _p(ids, _u32p), _p(out, _f32p))
+        del keep
+        return st, ids, out
+
+
+@dataclass
+class SynthSpec:
+    """Seeded synthetic layer description shared by tests and bench."""
+    seed: int
+    hidden: int
+    inter: int
+    experts: int
+    top_k: int
+    shared_inter: int
+    scale_lo: int
+    scale_hi: int

@@ -1,0 +1,268 @@
+// ref_shim.cpp -- C entry points over the reference's own CPU sources.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together
+// with the reference's unmodified CPU sources (runtime/src/{ops,
+// routing_policy,expert_major,official_moe,backend_cpu,profile}.cpp, read
+// in place under /root/reference) into oracle/_ref/libk3x_ref.so.  Tests use
+// it to pin the C restatement in k3x_oracle.c; bench.py may time it as the
+// CPU baseline.  Nothing from the reference is copied into this repository.
+#include "k3x/backend.hpp"
+#include "k3x/expert_major.hpp"
+#include "k3x/official_moe.hpp"
+#include "k3x/ops.hpp"
+#include "k3x/routing_policy.hpp"
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <optional>
+#include <span>
+#include <vector>
+
+namespace {
+
+std::optional<float> linear_of(int has_linear, float linear_beta) {
+    if (has_linear) return linear_beta;
+    return std::nullopt;
+}
+
+std::span<const std::byte> bytes(const std::uint8_t* data, std::size_t n) {
+    return {reinterpret_cast<const std::byte*>(data), n};
+}
+
+k3x::ComputeBackend& cpu_backend() {
+    static std::unique_ptr<k3x::ComputeBackend> backend = k3x::make_cpu_backend();
+    return *backend;
+}
+
+// One expert in the K3X reference layout: packed [rows][cols/2] (low nibble
+// first) and scales [rows][cols/32] for gate, up and down.
+struct ExpertBytes {
+    const std::uint8_t* gate_packed;
+    const std::uint8_t* gate_scales;
+    const std::uint8_t* up_packed;
+    const std::uint8_t* up_scales;
+    const std::uint8_t* down_packed;
+    const std::uint8_t* down_scales;
+};
+
+k3x::Mxfp4MlpView expert_view(const ExpertBytes& e, std::size_t hidden,
+                              std::size_t inter, std::uint64_t id_base) {
+    const auto gate_n = inter * hidden;
+    return {
+        {id_base + 1, bytes(e.gate_packed, gate_n / 2),
+         bytes(e.gate_scales, gate_n / 32), inter, hidden, 32},
+        {id_base + 2, bytes(e.up_packed, gate_n / 2),
+         bytes(e.up_scales, gate_n / 32), inter, hidden, 32},
+        {id_base + 3, bytes(e.down_packed, gate_n / 2),
+         bytes(e.down_scales, gate_n / 32), hidden, inter, 32},
+    };
+}
+
+}  // namespace
+
+extern "C" {
+
+int k3xr_decode_mxfp4(const std::uint8_t* packed, std::size_t packed_len,
+                      const std::uint8_t* scales, std::size_t scales_len,
+                      std::size_t rows, std::size_t cols, std::size_t group,
+                      float* out) {
+    auto result = k3x::decode_mxfp4(bytes(packed, packed_len),
+                                    bytes(scales, scales_len), rows, cols, group);
+    if (!result) return static_cast<int>(result.error());
+    std::memcpy(out, result.value().data(), result.value().size() * sizeof(float));
+    return 0;
+}
+
+int k3xr_mxfp4_matvec(const float* input, std::size_t input_len,
+                      const std::uint8_t* packed, std::size_t packed_len,
+                      const std::uint8_t* scales, std::size_t scales_len,
+                      std::size_t rows, std::size_t cols, std::size_t group,
+                      float* out) {
+    auto result = k3x::mxfp4_matmul({input, input_len}, bytes(packed, packed_len),
+                                    bytes(scales, scales_len), rows, cols, group);
+    if (!result) return static_cast<int>(result.error());
+    std::memcpy(out, result.value().data(), rows * sizeof(float));
+    return 0;
+}
+
+void k3xr_rms_norm(float* out, const float* in, const float* weight,
+                   std::size_t n, float epsilon) {
+    k3x::rms_norm({out, n}, {in, n}, {weight, n}, epsilon);
+}
+
+void k3xr_situ_glu(float* out, const float* gate, const float* up,
+                   std::size_t n, float beta, int has_linear,
+                   float linear_beta) {
+    k3x::situ_glu({out, n}, {gate, n}, {up, n}, beta,
+                  linear_of(has_linear, linear_beta));
+}
+
+int k3xr_route_official_logits(const float* logits, const float* correction,
+                               std::size_t experts, std::size_t top_k,
+                               std::uint32_t* ids, float* contributions,
+                               float* scores) {
+    auto route = k3x::route_official_moe_logits({logits, experts},
+                                                {correction, experts}, top_k);
+    if (!route) return static_cast<int>(route.error());
+    for (std::size_t i = 0; i < top_k; ++i) {
+        ids[i] = route.value().expert_ids[i];
+        contributions[i] = route.value().contributions[i];
+    }
+    std::memcpy(scores, route.value().scores.data(), experts * sizeof(float));
+    return 0;
+}
+
+int k3xr_select_routing_natural(const float* scores, const float* bias,
+                                std::size_t experts, std::size_t top_k,
+                                std::uint32_t* ids, float* weights) {
+    auto decision = k3x::select_routing(
+        {scores, experts}, {bias, experts}, top_k,
+        k3x::RoutingPolicyConfig{.mode = k3x::RoutingMode::natural});
+    if (!decision) return static_cast<int>(decision.error());
+    for (std::size_t i = 0; i < top_k; ++i) {
+        ids[i] = static_cast<std::uint32_t>(decision.value().expert_ids[i]);
+        weights[i] = decision.value().normalized_weights[i];
+    }
+    return 0;
+}
+
+int k3xr_expert_major_plan(const std::uint32_t* ids, const float* contributions,
+                           std::size_t tokens, std::size_t top_k,
+                           std::size_t* n_groups, std::uint32_t* group_expert,
+                           std::uint32_t* group_start,
+                           std::uint32_t* assign_token,
+                           std::uint32_t* assign_slot,
+                           float* assign_contribution) {
+    std::vector<k3x::ExpertMajorTokenRoute> routes(tokens);
+    for (std::size_t t = 0; t < tokens; ++t) {
+        routes[t].expert_ids.assign(ids + t * top_k, ids + (t + 1) * top_k);
+        routes[t].contributions.assign(contributions + t * top_k,
+                                       contributions + (t + 1) * top_k);
+    }
+    auto plan = k3x::build_expert_major_plan(routes);
+    if (!plan) return static_cast<int>(plan.error());
+    std::size_t at = 0;
+    group_start[0] = 0;
+    for (std::size_t g = 0; g < plan.value().groups.size(); ++g) {
+        const auto& group = plan.value().groups[g];
+        group_expert[g] = group.expert_id;
+        for (const auto& a : group.assignments) {
+            assign_token[at] = static_cast<std::uint32_t>(a.token_index);
+            assign_slot[at] = static_cast<std::uint32_t>(a.router_slot);
+            assign_contribution[at] = a.contribution;
+            ++at;
+        }
+        group_start[g + 1] = static_cast<std::uint32_t>(at);
+    }
+    *n_groups = plan.value().groups.size();
+    return 0;
+}
+
+// CpuBackend::dense_matvec (runtime/src/backend_cpu.cpp:23-46).
+int k3xr_dense_matvec(const float* input, const float* weight, std::size_t rows,
+                      std::size_t cols, float* out) {
+    auto r = cpu_backend().dense_matvec({input, cols},
+                                        k3x::DenseWeightView{7, {weight, rows * cols}, rows, cols},
+                                        0, k3x::ProfilePhase::decode);
+    if (!r) return static_cast<int>(r.error());
+    std::memcpy(out, r.value().data(), rows * sizeof(float));
+    return 0;
+}
+
+// CpuBackend::mxfp4_situ_mlp_group for a list of experts sharing one input
+// (runtime/src/backend_cpu.cpp:124-154).  Output: [n_experts][hidden].
+int k3xr_mxfp4_situ_mlp_group(const float* input, std::size_t hidden,
+                              std::size_t inter, const ExpertBytes* experts,
+                              std::size_t n_experts, float beta,
+                              int has_linear, float linear_beta, float* out) {
+    std::vector<k3x::Mxfp4MlpView> views;
+    for (std::size_t e = 0; e < n_experts; ++e)
+        views.push_back(expert_view(experts[e], hidden, inter, 16 * (e + 1)));
+    auto r = cpu_backend().mxfp4_situ_mlp_group(
+        {input, hidden}, views, beta, linear_of(has_linear, linear_beta), 0,
+        k3x::ProfilePhase::decode);
+    if (!r) return static_cast<int>(r.error());
+    for (std::size_t e = 0; e < n_experts; ++e)
+        std::memcpy(out + e * hidden, r.value()[e].data(), hidden * sizeof(float));
+    return 0;
+}
+
+// CpuBackend::mxfp4_situ_moe (runtime/src/backend_cpu.cpp:266-303).
+int k3xr_mxfp4_situ_moe(const float* input, std::size_t hidden,
+                        std::size_t inter, const ExpertBytes* experts,
+                        const float* contributions, std::size_t n_experts,
+                        float beta, int has_linear, float linear_beta,
+                        float* out) {
+    std::vector<k3x::Mxfp4MlpView> views;
+    for (std::size_t e = 0; e < n_experts; ++e)
+        views.push_back(expert_view(experts[e], hidden, inter, 16 * (e + 1)));
+    auto r = cpu_backend().mxfp4_situ_moe(
+        {input, hidden}, views, {contributions, n_experts}, beta,
+        linear_of(has_linear, linear_beta), 0, k3x::ProfilePhase::decode);
+    if (!r) return static_cast<int>(r.error());
+    std::memcpy(out, r.value().data(), hidden * sizeof(float));
+    return 0;
+}
+
+// The reference CPU composition of one token of the latent-free layer:
+// rms_norm (ops.cpp:10-18) -> router dense_matvec (model.cpp:919-921) ->
+// sigmoid (model.cpp:60) -> select_routing natural (routing_policy.cpp) ->
+// contributions * routed_scale (model.cpp:1004-1009) -> mxfp4_situ_moe
+// (backend_cpu.cpp:266-303) + dense_situ_mlp shared expert
+// (backend_cpu.cpp:107-122), added as in model.cpp:1145.
+// `experts` is indexed by expert id.  Returns the routed ids as well.
+int k3xr_moe_layer_token(const float* x, const float* gamma, float epsilon,
+                         const float* router, const float* bias,
+                         std::size_t n_experts, std::size_t hidden,
+                         std::size_t inter, std::size_t top_k,
+                         float routed_scale, const ExpertBytes* experts,
+                         const float* shared_gate, const float* shared_up,
+                         const float* shared_down, std::size_t shared_inter,
+                         float beta, int has_linear, float linear_beta,
+                         std::uint32_t* ids_out, float* out) {
+    std::vector<float> normed(hidden);
+    k3x::rms_norm(normed, {x, hidden}, {gamma, hidden}, epsilon);
+    auto logits = cpu_backend().dense_matvec(
+        normed, k3x::DenseWeightView{5, {router, n_experts * hidden}, n_experts, hidden},
+        0, k3x::ProfilePhase::decode);
+    if (!logits) return static_cast<int>(logits.error());
+    std::vector<float> scores(n_experts);
+    for (std::size_t e = 0; e < n_experts; ++e)
+        scores[e] = 1.0F / (1.0F + std::exp(-logits.value()[e]));
+    auto decision = k3x::select_routing(
+        scores, {bias, n_experts}, top_k,
+        k3x::RoutingPolicyConfig{.mode = k3x::RoutingMode::natural});
+    if (!decision) return static_cast<int>(decision.error());
+    std::vector<k3x::Mxfp4MlpView> views;
+    std::vector<float> contributions;
+    for (std::size_t slot = 0; slot < top_k; ++slot) {
+        const auto id = decision.value().expert_ids[slot];
+        ids_out[slot] = static_cast<std::uint32_t>(id);
+        views.push_back(expert_view(experts[id], hidden, inter, 16 * (slot + 1)));
+        contributions.push_back(decision.value().normalized_weights[slot] * routed_scale);
+    }
+    auto mixed = cpu_backend().mxfp4_situ_moe(
+        normed, views, contributions, beta, linear_of(has_linear, linear_beta),
+        0, k3x::ProfilePhase::decode);
+    if (!mixed) return static_cast<int>(mixed.error());
+    std::vector<float> zero_out(hidden);
+    if (shared_inter) {
+        const k3x::DenseMlpView shared{
+            {1001, {shared_gate, shared_inter * hidden}, shared_inter, hidden},
+            {1002, {shared_up, shared_inter * hidden}, shared_inter, hidden},
+            {1003, {shared_down, hidden * shared_inter}, hidden, shared_inter},
+        };
+        auto s = cpu_backend().dense_situ_mlp(
+            normed, shared, beta, linear_of(has_linear, linear_beta), 0,
+            k3x::ProfilePhase::decode);
+        if (!s) return static_cast<int>(s.error());
+        zero_out = std::move(s.value());
+    }
+    for (std::size_t h = 0; h < hidden; ++h) out[h] = mixed.value()[h] + zero_out[h];
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,73 @@
+// k3x_internal.hpp -- host-side state behind the C ABI handles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/k3x_hip_moe.h"
+
+struct k3x_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipStream_t own_stream = nullptr;
+    uint32_t* status = nullptr;  // device word, latched kernel errors
+    // Grow-only scratch (replaces runtime/cuda/device_memory.cuh:44-61).
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    uint64_t forward_calls = 0;
+    uint64_t kernel_launches = 0;
+    uint64_t weight_h2d_bytes = 0;
+};
+
+// Geometry of the tile layout for one matrix family of the bank.
+struct MatrixGeom {
+    uint32_t rows = 0;    // output rows
+    uint32_t cols = 0;    // K
+    uint32_t kt = 0;      // cols / 128
+    uint32_t ks = 0;      // ceil(kt / 4) scale dword groups
+};
+
+struct k3x_hip_bank {
+    k3x_hip_ctx* ctx = nullptr;
+    k3x_hip_layer_desc desc{};
+    MatrixGeom gate;  // [inter x hidden]; gate and up share one interleaved layout
+    MatrixGeom down;  // [hidden x inter]
+    MatrixGeom sgate; // shared [shared_inter x hidden]
+    MatrixGeom sdown; // shared [hidden x shared_inter]
+    // Routed experts, expert-major.  Gate/up codes: [I/16][H/128][2][64] x16B.
+    // Gate/up scales: [I/16][ks][2][64] dwords.  Down codes: [H/16][I/128][64]
+    // x16B; down scales: [H/16][ks][64] dwords.
+    uint8_t* gu_codes = nullptr;
+    uint32_t* gu_scales = nullptr;
+    uint8_t* dn_codes = nullptr;
+    uint32_t* dn_scales = nullptr;
+    size_t gu_codes_per_expert = 0;   // bytes
+    size_t gu_scales_per_expert = 0;  // dwords
+    size_t dn_codes_per_expert = 0;   // bytes
+    size_t dn_scales_per_expert = 0;  // dwords
+    // Shared expert bf16.  Gate/up: [S/16][H/128][2][4][64] x16B;
+    // down: [H/16][S/128][4][64] x16B.
+    uint8_t* sh_gu = nullptr;
+    uint8_t* sh_dn = nullptr;
+    float* router_w = nullptr;   // [E][H]
+    float* router_bias = nullptr;
+    float* gamma = nullptr;
+    bool router_ready = false;
+    bool shared_ready = false;
+    std::vector<uint8_t> expert_ready;
+    std::unordered_map<uint64_t, uint32_t> tensor_ids;  // id -> expert*4+matrix
+    uint64_t device_bytes = 0;
+};
+
+namespace k3x_hip {
+
+inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }
+
+// Makes sure ctx->scratch holds at least `bytes`; grow-only.
+int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
+
+}  // namespace k3x_hip

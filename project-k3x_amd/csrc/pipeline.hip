@@ -1,0 +1,799 @@
+// pipeline.hip -- the MoE-layer kernels and the forward entry points.
+//
+//   rmsnorm_kernel   x -> xn = bf16(x * inv_rms * gamma)      (canonical fp64 sum)
+//   router_kernel    logits = W_r xn in fp64, canonical order  (bit-exact ids)
+//   topk_kernel      sigmoid + bias, natural Top-K, renorm * routed_scale
+//   group_kernel     expert-major CSR + first-use order         (bit-exact)
+//   expert_gemm      MXFP4/bf16 weights x bf16 activations on MFMA; gate/up
+//                    variant fuses the GLU, down variant scatters per pair
+//   combine_kernel   slot-ordered weighted sum + shared expert, bf16 cast
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "k3x_device.hpp"
+#include "k3x_internal.hpp"
+
+using namespace k3x_dev;
+
+namespace {
+
+__device__ inline void latch(uint32_t* status, uint32_t code) { atomicCAS(status, 0u, code); }
+
+// Canonical fp64 block reduction over 256 threads: xor butterfly inside each
+// wave (pairwise tree of 64), then (w0 + w1) + (w2 + w3).  Every thread gets
+// the result.
+__device__ inline double block_tree_sum(double v, double* red) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const double r = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: one block of 256 threads per token.  runtime/src/ops.cpp:10-18
+// with the canonical order for the sum of squares and the bf16 rounding of
+// the normalised activation.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const float* __restrict__ gamma,
+                                                      uint32_t H, float eps,
+                                                      uint16_t* __restrict__ xn,
+                                                      uint32_t* status) {
+    __shared__ double red[4];
+    if (*(volatile uint32_t*)status) return;
+    const uint16_t* xr = x + (size_t)blockIdx.x * H;
+    double s = 0.0;
+    int bad = 0;
+    for (uint32_t k = threadIdx.x; k < H; k += 256) {
+        const float v = bf16_to_f32(xr[k]);
+        bad |= !__builtin_isfinite(v);
+        s += (double)v * (double)v;
+    }
+    if (__syncthreads_or(bad)) {
+        if (threadIdx.x == 0) latch(status, K3X_ERR_INVALID_MXFP4);
+        return;
+    }
+    s = block_tree_sum(s, red);
+    const float mean = (float)__ddiv_rn(s, (double)H);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    uint16_t* out = xn + (size_t)blockIdx.x * H;
+    for (uint32_t k = threadIdx.x; k < H; k += 256)
+        out[k] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xr[k]), inv), gamma[k]));
+}
+
+// ---------------------------------------------------------------------------
+// Router logits in fp64, canonical order: thread i accumulates k = i, i+256,
+// ... sequentially, then block_tree_sum.  EPB experts x TPB tokens per block.
+// Logit semantics: runtime/src/model.cpp:919-921 / backend_cpu.cpp:33-41.
+// ---------------------------------------------------------------------------
+template <int EPB, int TPB>
+__global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ W,
+                                                     const uint16_t* __restrict__ xn,
+                                                     uint32_t E, uint32_t H, uint32_t T,
+                                                     float* __restrict__ logits,
+                                                     const uint32_t* status) {
+    __shared__ double red[4][EPB * TPB];
+    if (*(volatile const uint32_t*)status) return;
+    const uint32_t e0 = blockIdx.x * EPB, t0 = blockIdx.y * TPB;
+    double acc[EPB][TPB];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) acc[a][b] = 0.0;
+    for (uint32_t k = threadIdx.x; k < H; k += 256) {
+        float w[EPB], xv[TPB];
+#pragma unroll
+        for (int a = 0; a < EPB; ++a) w[a] = e0 + a < E ? W[(size_t)(e0 + a) * H + k] : 0.0f;
+#pragma unroll
+        for (int b = 0; b < TPB; ++b)
+            xv[b] = t0 + b < T ? bf16_to_f32(xn[(size_t)(t0 + b) * H + k]) : 0.0f;
+#pragma unroll
+        for (int a = 0; a < EPB; ++a)
+#pragma unroll
+            for (int b = 0; b < TPB; ++b) acc[a][b] += (double)w[a] * (double)xv[b];
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) {
+            double v = acc[a][b];
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+            if (lane == 0) red[wave][a * TPB + b] = v;
+        }
+    __syncthreads();
+    if (threadIdx.x < EPB * TPB) {
+        const int i = threadIdx.x, a = i / TPB, b = i % TPB;
+        if (e0 + a < E && t0 + b < T)
+            logits[(size_t)(t0 + b) * E + e0 + a] =
+                (float)((red[0][i] + red[1][i]) + (red[2][i] + red[3][i]));
+    }
+}
+
+// Sort key: larger adjusted score first, then lower expert index
+// (runtime/src/official_moe.cpp:226-232).  -0 is folded into +0 so that the
+// two compare equal as floats do.  Taken/absent entries are key 0.
+__device__ inline uint64_t topk_key(float adj, uint32_t e) {
+    const float a = adj == 0.0f ? 0.0f : adj;
+    const uint32_t u = __float_as_uint(a);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - e);
+}
+
+// ---------------------------------------------------------------------------
+// Top-K: one wave per token.  Scores, validation and renormalisation follow
+// runtime/src/routing_policy.cpp:40-95,146-157 (FLOAT) or
+// runtime/src/official_moe.cpp:214-242 (DOUBLE); contributions are then
+// multiplied by routed_scale (runtime/src/model.cpp:1004-1009).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logits,
+                                                  const float* __restrict__ bias, uint32_t E,
+                                                  uint32_t K, float routed_scale,
+                                                  uint32_t renorm, uint32_t* __restrict__ ids,
+                                                  float* __restrict__ weights,
+                                                  uint32_t* status) {
+    extern __shared__ uint64_t keys[];  // [E] keys then [E] scores
+    float* sc = reinterpret_cast<float*>(keys + E);
+    __shared__ uint32_t sel[64];
+    __shared__ float selsc[64];
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t t = blockIdx.x, lane = threadIdx.x;
+    uint32_t bad = 0;
+    for (uint32_t e = lane; e < E; e += 64) {
+        const float lg = logits[(size_t)t * E + e];
+        const float b = bias[e];
+        if (renorm == K3X_RENORM_DOUBLE && (!__builtin_isfinite(lg) || !__builtin_isfinite(b)))
+            bad = K3X_ERR_INVALID_EXTENT;
+        const float s = sigmoid_cr(lg);
+        const float adj = __fadd_rn(s, b);
+        if (renorm == K3X_RENORM_FLOAT &&
+            (!__builtin_isfinite(s) || s < 0.0f || s > 1.0f || !__builtin_isfinite(b) ||
+             !__builtin_isfinite(adj)))
+            bad = K3X_ERR_INVALID_STATE;
+        sc[e] = s;
+        keys[e] = topk_key(adj, e);
+    }
+    for (int d = 1; d < 64; d <<= 1) bad = max(bad, (uint32_t)__shfl_xor((int)bad, d));
+    if (bad) {
+        if (lane == 0) latch(status, bad);
+        return;
+    }
+    __syncthreads();
+    for (uint32_t slot = 0; slot < K; ++slot) {
+        uint64_t best = 0;
+        for (uint32_t e = lane; e < E; e += 64) best = max(best, keys[e]);
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint64_t o = __shfl_xor(best, d);
+            best = max(best, o);
+        }
+        const uint32_t win = 0xffffffffu - (uint32_t)best;
+        __syncthreads();
+        if (lane == 0) {
+            sel[slot] = win;
+            selsc[slot] = sc[win];
+            keys[win] = 0;
+        }
+        __syncthreads();
+    }
+    if (lane != 0) return;
+    if (renorm == K3X_RENORM_DOUBLE) {
+        double total = 0.0;
+        for (uint32_t s = 0; s < K; ++s) total = __dadd_rn(total, (double)selsc[s]);
+        if (!__builtin_isfinite(total) || !(total > 0.0)) {
+            latch(status, K3X_ERR_INVALID_EXTENT);
+            return;
+        }
+        for (uint32_t s = 0; s < K; ++s) {
+            ids[(size_t)t * K + s] = sel[s];
+            weights[(size_t)t * K + s] =
+                __fmul_rn((float)__ddiv_rn((double)selsc[s], total), routed_scale);
+        }
+    } else {
+        float den = 0.0f;
+        for (uint32_t s = 0; s < K; ++s) den = __fadd_rn(den, selsc[s]);
+        if (!__builtin_isfinite(den) || !(den > 0.0f)) {
+            latch(status, K3X_ERR_INVALID_STATE);
+            return;
+        }
+        for (uint32_t s = 0; s < K; ++s) {
+            ids[(size_t)t * K + s] = sel[s];
+            weights[(size_t)t * K + s] = __fmul_rn(__fdiv_rn(selsc[s], den), routed_scale);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expert-major grouping, one block of 1024 threads.  Produces the
+// ascending-expert CSR (counts, offsets, pair_token, pair_slot; rows of one
+// expert in (token, slot) order) plus first_use = min(token*K + slot) and the
+// active experts sorted by it, which is the group order of
+// build_expert_major_plan (runtime/src/expert_major.cpp:10-54).
+// Rows are ranked with per-step token bitmaps: tokens are taken 64 (or
+// 1024/K) at a time, each pair's rank inside its expert is the running count
+// plus the popcount of earlier tokens of the step that chose the expert.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void group_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets,
+    uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot,
+    uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
+    uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu, uint32_t* status) {
+    extern __shared__ uint32_t smem[];
+    uint32_t* cnt = smem;
+    uint32_t* fu = cnt + E;
+    uint32_t* run = fu + E;
+    uint32_t* mask = run + E;  // [E][2]
+    uint32_t* alist = mask + 2 * E;
+    __shared__ uint32_t na_s;
+    __shared__ int bad_s;
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t P = T * K;
+    if (tid == 0) bad_s = 0;
+    for (uint32_t e = tid; e < E; e += 1024) {
+        cnt[e] = 0;
+        fu[e] = 0xffffffffu;
+    }
+    __syncthreads();
+    for (uint32_t p = tid; p < P; p += 1024) {
+        const uint32_t e = ids[p];
+        if (e >= E) {
+            bad_s = 1;
+            continue;
+        }
+        atomicAdd(&cnt[e], 1u);
+        atomicMin(&fu[e], p);
+    }
+    __syncthreads();
+    if (bad_s) {
+        if (tid == 0) latch(status, K3X_ERR_INVALID_STATE);
+        return;
+    }
+    if (tid == 0) {
+        uint32_t acc = 0, na = 0;
+        for (uint32_t e = 0; e < E; ++e) {
+            offsets[e] = acc;
+            run[e] = acc;
+            acc += cnt[e];
+            if (cnt[e]) {
+                alist[na] = e;
+                active_asc[na++] = e;
+            }
+        }
+        offsets[E] = acc;
+        *n_active = na;
+        na_s = na;
+    }
+    __syncthreads();
+    const uint32_t na = na_s;
+    for (uint32_t a = tid; a < na; a += 1024) {
+        const uint32_t e = alist[a];
+        const uint32_t key = fu[e];
+        uint32_t rank = 0;
+        for (uint32_t b = 0; b < na; ++b) rank += fu[alist[b]] < key;
+        active_fu[rank] = e;
+    }
+    for (uint32_t e = tid; e < E; e += 1024) {
+        counts[e] = cnt[e];
+        first_use[e] = fu[e];
+    }
+    const uint32_t tps = min(64u, 1024u / K);  // tokens per step
+    for (uint32_t t0 = 0; t0 < T; t0 += tps) {
+        for (uint32_t e = tid; e < E; e += 1024) {
+            mask[2 * e] = 0;
+            mask[2 * e + 1] = 0;
+        }
+        __syncthreads();
+        const uint32_t tl = tid / K, s = tid % K, t = t0 + tl;
+        const bool valid = tl < tps && t < T;
+        uint32_t e = 0;
+        if (valid) {
+            e = ids[(size_t)t * K + s];
+            atomicOr(&mask[2 * e + (tl >> 5)], 1u << (tl & 31));
+        }
+        __syncthreads();
+        if (valid) {
+            const uint32_t lo = mask[2 * e], hi = mask[2 * e + 1];
+            const uint32_t below = tl < 32 ? __popc(lo & ((1u << tl) - 1u))
+                                           : __popc(lo) + __popc(hi & ((1u << (tl - 32)) - 1u));
+            const uint32_t r = run[e] + below;
+            pair_token[r] = t;
+            pair_slot[r] = s;
+        }
+        __syncthreads();
+        for (uint32_t q = tid; q < E; q += 1024) run[q] += __popc(mask[2 * q]) + __popc(mask[2 * q + 1]);
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped expert GEMM on v_mfma_f32_16x16x32_bf16.
+//
+// Work item of one wave: NT row blocks of 16 output rows (GATEUP: NT pairs of
+// 16 gate + 16 up rows) of one expert, for all of the expert's pair rows in
+// chunks of 16*MT, over the full K.  B (weights) is read straight from the
+// tile layout into registers -- MXFP4 codes dequantised by dequant8, bf16
+// used as is -- so every weight byte is fetched once per chunk.  A
+// (activations) is read per lane from the bf16 rows the lane's MFMA row maps
+// to (gathered through pair_token for gate/up).
+//
+// Accumulator layout (16x16 MFMA): lane l, element i holds row 4(l/16)+i of
+// the M (pair) dimension and column l%16 of the output rows.
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+    const uint8_t* codes;       // expert 0 base of the tile array
+    const uint32_t* scales;     // MXFP4 only
+    size_t codes_per_expert;    // bytes
+    size_t scales_per_expert;   // dwords
+    uint32_t kt, ks;            // K tiles, scale dword groups
+    uint32_t blocks_per_expert; // workgroups per expert
+    const uint16_t* a;          // activation rows (bf16)
+    uint32_t a_stride;          // elements per activation row
+    uint32_t gather;            // A row = pair_token[off+m] (1) or off+m (0)
+    const uint32_t* n_active;   // grouping (nullptr = single block of `tokens` rows)
+    const uint32_t* active;
+    const uint32_t* counts;
+    const uint32_t* offsets;
+    const uint32_t* pair_token;
+    const uint32_t* pair_slot;
+    uint32_t tokens;
+    uint32_t top_k;
+    uint16_t* act;              // GATEUP output [row][act_stride] bf16
+    uint32_t act_stride;
+    float* y;                   // down output [row][y_stride] fp32
+    uint32_t y_stride;
+    uint32_t scatter;           // y row = token*top_k + slot (1) or off+m (0)
+    GluParams glu;
+    const uint32_t* status;
+};
+
+template <bool FP4, bool GATEUP, int MT, int NT>
+__global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
+    if (*(volatile const uint32_t*)a.status) return;
+    const uint32_t eb = blockIdx.x / a.blocks_per_expert;
+    const uint32_t jb = blockIdx.x % a.blocks_per_expert;
+    uint32_t e = 0, cnt = a.tokens, off = 0;
+    if (a.active) {
+        if (eb >= *a.n_active) return;
+        e = a.active[eb];
+        cnt = a.counts[e];
+        off = a.offsets[e];
+    }
+    constexpr int S = GATEUP ? 2 : 1;  // tiles per row block and K step
+    constexpr int U = FP4 ? 1 : 4;     // 16-byte words per lane per tile
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t rb0 = (jb * 4 + wave) * NT;
+    const uint4* codes = reinterpret_cast<const uint4*>(a.codes + e * a.codes_per_expert);
+    const uint32_t* scales = FP4 ? a.scales + e * a.scales_per_expert : nullptr;
+
+    for (uint32_t m0 = 0; m0 < cnt; m0 += 16 * MT) {
+        const uint16_t* arow[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t row = m0 + 16 * mt + n;
+            arow[mt] = nullptr;
+            if (row < cnt) {
+                const uint32_t src = a.gather ? a.pair_token[off + row] : off + row;
+                arow[mt] = a.a + (size_t)src * a.a_stride + 32 * g;
+            }
+        }
+        f32x4 acc[MT][NT][S];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int w = 0; w < S; ++w) acc[mt][nt][w] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        for (uint32_t k = 0; k < a.kt; ++k) {
+            uint4 bt[NT][S][U];
+            float sc[NT][S];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int w = 0; w < S; ++w) {
+                    const size_t base = (((size_t)(rb0 + nt) * a.kt + k) * S + w) * U * 64 + lane;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) bt[nt][w][u] = codes[base + u * 64];
+                    if constexpr (FP4) {
+                        const uint32_t sw =
+                            scales[(((size_t)(rb0 + nt) * a.ks + k / 4) * S + w) * 64 + lane];
+                        sc[nt][w] = e8m0_to_f32((sw >> (8 * (k & 3))) & 0xffu);
+                    }
+                }
+            bf16x8 af[MT][4];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                if (arow[mt]) {
+                    const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)k * 128);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) af[mt][j] = as_bf16x8(p[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) af[mt][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int w = 0; w < S; ++w) {
+                        bf16x8 b;
+                        if constexpr (FP4) {
+                            const uint4 c = bt[nt][w][0];
+                            const uint32_t word = j == 0 ? c.x : j == 1 ? c.y : j == 2 ? c.z : c.w;
+                            b = dequant8(word, sc[nt][w]);
+                        } else {
+                            b = as_bf16x8(bt[nt][w][j]);
+                        }
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            acc[mt][nt][w] = mfma16x16x32(af[mt][j], b, acc[mt][nt][w]);
+                    }
+            }
+        }
+
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t row = m0 + 16 * mt + 4 * g + i;
+                    if (row >= cnt) continue;
+                    const uint32_t col = (rb0 + nt) * 16 + n;
+                    if constexpr (GATEUP) {
+                        const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
+                        a.act[(size_t)(off + row) * a.act_stride + col] = f32_to_bf16(v);
+                    } else {
+                        const uint32_t r = off + row;
+                        const size_t yrow = a.scatter
+                                                ? (size_t)a.pair_token[r] * a.top_k + a.pair_slot[r]
+                                                : (size_t)r;
+                        a.y[yrow * a.y_stride + col] = acc[mt][nt][0][i];
+                    }
+                }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// out[t][h] = bf16(sum_{slot in router order} w[t][slot] * y[t][slot][h]
+//                  + shared[t][h]), float mul then float add per term
+// (runtime/src/backend_cpu.cpp:295-301, runtime/src/model.cpp:1145).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
+                                                      const float* __restrict__ w,
+                                                      const float* __restrict__ shared,
+                                                      uint32_t K, uint32_t H,
+                                                      uint16_t* __restrict__ out,
+                                                      float* __restrict__ out_f32,
+                                                      const uint32_t* status) {
+    if (*(volatile const uint32_t*)status) return;
+    const uint32_t h = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    if (h >= H) return;
+    float mix = 0.0f;
+    for (uint32_t s = 0; s < K; ++s)
+        mix = __fadd_rn(mix, __fmul_rn(w[(size_t)t * K + s], y[((size_t)t * K + s) * H + h]));
+    const float v = shared ? __fadd_rn(mix, shared[(size_t)t * H + h]) : mix;
+    out[(size_t)t * H + h] = f32_to_bf16(v);
+    if (out_f32) out_f32[(size_t)t * H + h] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+struct Scratch {
+    uint16_t* xn;
+    float* logits;
+    uint32_t* ids;
+    float* weights;
+    uint32_t* counts;
+    uint32_t* offsets;
+    uint32_t* pair_token;
+    uint32_t* pair_slot;
+    uint32_t* first_use;
+    uint32_t* n_active;
+    uint32_t* active_asc;
+    uint32_t* active_fu;
+    uint16_t* act;
+    float* y;
+    uint16_t* sact;
+    float* sy;
+};
+
+// Lays the per-call buffers out in the context scratch; returns bytes needed
+// (base == nullptr only measures).
+size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, Scratch* s) {
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* p = base ? base + at : nullptr;
+        at += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    const size_t P = (size_t)T * K;
+    s->xn = (uint16_t*)take((size_t)T * d.hidden * 2);
+    s->logits = (float*)take((size_t)T * d.experts * 4);
+    s->ids = (uint32_t*)take(P * 4);
+    s->weights = (float*)take(P * 4);
+    s->counts = (uint32_t*)take((size_t)d.experts * 4);
+    s->offsets = (uint32_t*)take(((size_t)d.experts + 1) * 4);
+    s->pair_token = (uint32_t*)take(P * 4);
+    s->pair_slot = (uint32_t*)take(P * 4);
+    s->first_use = (uint32_t*)take((size_t)d.experts * 4);
+    s->n_active = (uint32_t*)take(4);
+    s->active_asc = (uint32_t*)take((size_t)d.experts * 4);
+    s->active_fu = (uint32_t*)take((size_t)d.experts * 4);
+    s->act = (uint16_t*)take(P * d.inter * 2);
+    s->y = (float*)take(P * d.hidden * 4);
+    s->sact = (uint16_t*)take((size_t)T * d.shared_inter * 2);
+    s->sy = (float*)take((size_t)T * d.hidden * 4);
+    return at;
+}
+
+bool finite_pos(float v) { return std::isfinite(v) && v > 0.0f; }
+
+int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p) {
+    const auto& d = bank->desc;
+    if (!p->tokens || p->tokens > (1u << 20) || !p->top_k || p->top_k > 64 ||
+        p->top_k > d.experts)
+        return K3X_ERR_INVALID_EXTENT;
+    if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
+        p->renorm > 1)
+        return K3X_ERR_INVALID_MXFP4;
+    if (p->glu == K3X_GLU_SITU &&
+        (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
+        return K3X_ERR_INVALID_MXFP4;
+    for (uint8_t r : bank->expert_ready)
+        if (!r) return K3X_ERR_INVALID_STATE;
+    if (d.shared_inter && !bank->shared_ready) return K3X_ERR_INVALID_STATE;
+    return K3X_OK;
+}
+
+int launched(k3x_hip_ctx* ctx, unsigned n) {
+    ctx->kernel_launches += n;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
+                 uint32_t* counts, uint32_t* offsets, uint32_t* pair_token, uint32_t* pair_slot,
+                 uint32_t* first_use, uint32_t* n_active, uint32_t* active_asc,
+                 uint32_t* active_fu) {
+    const size_t lds = (size_t)E * 6 * 4;
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), lds, ctx->stream, ids, T, K, E, counts,
+                       offsets, pair_token, pair_slot, first_use, n_active, active_asc, active_fu,
+                       ctx->status);
+    return launched(ctx, 1);
+}
+
+template <bool FP4, bool GATEUP, int MT, int NT>
+void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32_t rows) {
+    g.blocks_per_expert = rows / 16 / (4 * NT);
+    hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT>), dim3(experts_in_grid * g.blocks_per_expert),
+                       dim3(256), 0, ctx->stream, g);
+}
+
+// Grouping, expert GEMMs, shared expert, combine.  xn is the bf16 input of
+// the experts; ids/weights [T][K] device.
+int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+             const Scratch& s, const uint16_t* xn, const uint32_t* ids, const float* weights,
+             uint16_t* out, float* out_f32) {
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens, K = p->top_k;
+    int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
+                          s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu);
+    if (st) return st;
+    const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
+    const bool wide = T > 16;  // more than one 16-row MFMA tile per expert possible
+    GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+
+    GemmArgs g{};
+    g.status = ctx->status;
+    g.glu = glu;
+    g.top_k = K;
+    // Routed gate/up + GLU.
+    g.codes = bank->gu_codes;
+    g.scales = bank->gu_scales;
+    g.codes_per_expert = bank->gu_codes_per_expert;
+    g.scales_per_expert = bank->gu_scales_per_expert;
+    g.kt = bank->gate.kt;
+    g.ks = bank->gate.ks;
+    g.a = xn;
+    g.a_stride = d.hidden;
+    g.gather = 1;
+    g.n_active = s.n_active;
+    g.active = s.active_asc;
+    g.counts = s.counts;
+    g.offsets = s.offsets;
+    g.pair_token = s.pair_token;
+    g.pair_slot = s.pair_slot;
+    g.act = s.act;
+    g.act_stride = d.inter;
+    if (wide) launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
+    else launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
+    // Shared gate/up + GLU (single block of T rows).
+    if (d.shared_inter) {
+        GemmArgs sg = g;
+        sg.codes = bank->sh_gu;
+        sg.scales = nullptr;
+        sg.codes_per_expert = 0;
+        sg.kt = bank->sgate.kt;
+        sg.gather = 0;
+        sg.n_active = nullptr;
+        sg.active = nullptr;
+        sg.tokens = T;
+        sg.act = s.sact;
+        sg.act_stride = d.shared_inter;
+        if (wide) launch_gemm<false, true, 4, 1>(ctx, sg, 1, d.shared_inter);
+        else launch_gemm<false, true, 1, 1>(ctx, sg, 1, d.shared_inter);
+    }
+    // Routed down, scattered to [token][slot].
+    GemmArgs dn = g;
+    dn.codes = bank->dn_codes;
+    dn.scales = bank->dn_scales;
+    dn.codes_per_expert = bank->dn_codes_per_expert;
+    dn.scales_per_expert = bank->dn_scales_per_expert;
+    dn.kt = bank->down.kt;
+    dn.ks = bank->down.ks;
+    dn.a = s.act;
+    dn.a_stride = d.inter;
+    dn.gather = 0;
+    dn.y = s.y;
+    dn.y_stride = d.hidden;
+    dn.scatter = 1;
+    if (wide) launch_gemm<true, false, 4, 2>(ctx, dn, max_active, d.hidden);
+    else launch_gemm<true, false, 1, 2>(ctx, dn, max_active, d.hidden);
+    if (d.shared_inter) {
+        GemmArgs sd = dn;
+        sd.codes = bank->sh_dn;
+        sd.scales = nullptr;
+        sd.codes_per_expert = 0;
+        sd.kt = bank->sdown.kt;
+        sd.a = s.sact;
+        sd.a_stride = d.shared_inter;
+        sd.n_active = nullptr;
+        sd.active = nullptr;
+        sd.tokens = T;
+        sd.y = s.sy;
+        sd.scatter = 0;
+        if (wide) launch_gemm<false, false, 4, 2>(ctx, sd, 1, d.hidden);
+        else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden);
+    }
+    hipLaunchKernelGGL(combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0,
+                       ctx->stream, s.y, weights, d.shared_inter ? s.sy : nullptr, K, d.hidden,
+                       out, out_f32, ctx->status);
+    return launched(ctx, d.shared_inter ? 5 : 3);
+}
+
+int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+              const Scratch& s, const uint16_t* xn, const uint32_t* ids, const float* weights,
+              const k3x_hip_moe_taps* taps) {
+    if (!taps) return K3X_OK;
+    const auto& d = bank->desc;
+    const size_t T = p->tokens, K = p->top_k, P = T * K, E = d.experts;
+    struct Item { void* dst; const void* src; size_t bytes; };
+    const Item items[] = {
+        {taps->normed_x, xn, T * d.hidden * 2},
+        {taps->logits, s.logits, T * E * 4},
+        {taps->ids, ids, P * 4},
+        {taps->weights, weights, P * 4},
+        {taps->counts, s.counts, E * 4},
+        {taps->offsets, s.offsets, (E + 1) * 4},
+        {taps->pair_token, s.pair_token, P * 4},
+        {taps->pair_slot, s.pair_slot, P * 4},
+        {taps->first_use, s.first_use, E * 4},
+        {taps->n_active, s.n_active, 4},
+        {taps->active_first_use, s.active_fu, E * 4},
+        {taps->act, s.act, P * d.inter * 2},
+        {taps->expert_out, s.y, P * d.hidden * 4},
+        {taps->shared_out, d.shared_inter ? s.sy : nullptr, T * d.hidden * 4},
+    };
+    for (const auto& it : items) {
+        if (!it.dst || !it.src || it.dst == it.src) continue;
+        if (hipMemcpyAsync(it.dst, it.src, it.bytes, hipMemcpyDeviceToDevice, ctx->stream) !=
+            hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+    }
+    return K3X_OK;
+}
+
+int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, Scratch* s) {
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, s);
+    int st = k3x_hip::ensure_scratch(ctx, need);
+    if (st) return st;
+    carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, s);
+    return K3X_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                        const uint16_t* x, uint16_t* out, const k3x_hip_moe_taps* taps) {
+    if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    int st = validate_params(bank, p);
+    if (st) return st;
+    if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
+    Scratch s;
+    if ((st = prepare(ctx, bank, p, &s))) return st;
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens, K = p->top_k;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, bank->gamma,
+                       d.hidden, p->rms_epsilon, s.xn, ctx->status);
+    if (T <= 4) {
+        hipLaunchKernelGGL((router_kernel<1, 4>), dim3(d.experts, 1), dim3(256), 0, ctx->stream,
+                           bank->router_w, s.xn, d.experts, d.hidden, T, s.logits, ctx->status);
+    } else {
+        hipLaunchKernelGGL((router_kernel<4, 8>), dim3((d.experts + 3) / 4, (T + 7) / 8),
+                           dim3(256), 0, ctx->stream, bank->router_w, s.xn, d.experts, d.hidden,
+                           T, s.logits, ctx->status);
+    }
+    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)d.experts * 12, ctx->stream,
+                       s.logits, bank->router_bias, d.experts, K, p->routed_scale, p->renorm,
+                       s.ids, s.weights, ctx->status);
+    if ((st = launched(ctx, 3))) return st;
+    if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr)))
+        return st;
+    ++ctx->forward_calls;
+    return copy_taps(ctx, bank, p, s, s.xn, s.ids, s.weights, taps);
+}
+
+int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                               const k3x_hip_moe_params* p, const uint16_t* xn,
+                               const uint32_t* ids, const float* weights,
+                               const uint32_t* host_ids, const float* host_weights,
+                               uint16_t* out, const k3x_hip_moe_taps* taps) {
+    if (!ctx || !bank || !p || !xn || !ids || !weights || !out || bank->ctx != ctx)
+        return K3X_ERR_INVALID_EXTENT;
+    int st = validate_params(bank, p);
+    if (st) return st;
+    const uint32_t T = p->tokens, K = p->top_k, E = bank->desc.experts;
+    // Route contract of build_expert_major_plan (expert_major.cpp:21-36).
+    if (host_ids) {
+        for (uint32_t t = 0; t < T; ++t)
+            for (uint32_t s = 0; s < K; ++s) {
+                const uint32_t e = host_ids[(size_t)t * K + s];
+                if (e >= E) return K3X_ERR_INVALID_STATE;
+                for (uint32_t q = 0; q < s; ++q)
+                    if (host_ids[(size_t)t * K + q] == e) return K3X_ERR_INVALID_STATE;
+            }
+    }
+    if (host_weights)
+        for (size_t i = 0; i < (size_t)T * K; ++i)
+            if (!std::isfinite(host_weights[i])) return K3X_ERR_INVALID_STATE;
+    Scratch s;
+    if ((st = prepare(ctx, bank, p, &s))) return st;
+    if ((st = run_tail(ctx, bank, p, s, xn, ids, weights, out, taps ? taps->out_f32 : nullptr)))
+        return st;
+    ++ctx->forward_calls;
+    return copy_taps(ctx, bank, p, s, xn, ids, weights, taps);
+}
+
+int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t tokens,
+                              uint32_t top_k, uint32_t experts, const k3x_hip_moe_taps* t) {
+    if (!ctx || !ids || !t || !tokens || !top_k || top_k > 64 || !experts || experts > 4096 ||
+        !t->counts || !t->offsets || !t->pair_token || !t->pair_slot || !t->first_use ||
+        !t->n_active || !t->active_first_use)
+        return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    int st = k3x_hip::ensure_scratch(ctx, (size_t)experts * 4);
+    if (st) return st;
+    return launch_group(ctx, ids, tokens, top_k, experts, t->counts, t->offsets, t->pair_token,
+                        t->pair_slot, t->first_use, t->n_active,
+                        static_cast<uint32_t*>(ctx->scratch), t->active_first_use);
+}
+
+}  // extern "C"

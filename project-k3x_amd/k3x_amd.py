@@ -1,0 +1,322 @@
+"""ctypes binding of libk3x_hip_moe.so (the C ABI in include/k3x_hip_moe.h).
+
+torch is used only for device memory and the stream: tensors are passed to
+the library as raw device pointers.  There is no fallback: if the HIP library
+is missing, or no GPU is present, construction raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libk3x_hip_moe.so")
+
+OK = 0
+ERR_INVALID_EXTENT = 9
+ERR_TENSOR_NOT_FOUND = 14
+ERR_INVALID_MXFP4 = 15
+ERR_INVALID_STATE = 16
+ERR_BACKEND_UNAVAILABLE = 17
+
+GLU_SWIGLU, GLU_SITU = 0, 1
+RENORM_FLOAT, RENORM_DOUBLE = 0, 1
+MATRIX_GATE, MATRIX_UP, MATRIX_DOWN = 0, 1, 2
+
+STREAM_GATE_CODES = 1
+STREAM_GATE_SCALES = 2
+STREAM_UP_CODES = 3
+STREAM_UP_SCALES = 4
+STREAM_DOWN_CODES = 5
+STREAM_DOWN_SCALES = 6
+STREAM_ROUTER = 7
+STREAM_BIAS = 8
+STREAM_SHARED_GATE = 9
+STREAM_SHARED_UP = 10
+STREAM_SHARED_DOWN = 11
+STREAM_INPUT = 12
+
+
+def stream_id(kind: int, expert: int = 0) -> int:
+    return (kind << 32) | expert
+
+
+class K3xError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what} failed: status {status} ({_name(status)})")
+
+
+def _name(status: int) -> str:
+    return {0: "OK", 9: "INVALID_EXTENT", 14: "TENSOR_NOT_FOUND", 15: "INVALID_MXFP4",
+            16: "INVALID_STATE", 17: "BACKEND_UNAVAILABLE"}.get(status, "UNKNOWN")
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("inter", C.c_uint32), ("experts", C.c_uint32),
+                ("group_size", C.c_uint32), ("shared_inter", C.c_uint32)]
+
+
+class MoeParams(C.Structure):
+    _fields_ = [("tokens", C.c_uint32), ("top_k", C.c_uint32), ("routed_scale", C.c_float),
+                ("rms_epsilon", C.c_float), ("glu", C.c_uint32), ("situ_beta", C.c_float),
+                ("has_situ_linear", C.c_uint32), ("situ_linear_beta", C.c_float),
+                ("renorm", C.c_uint32)]
+
+
+TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair_token",
+              "pair_slot", "first_use", "n_active", "active_first_use", "act", "expert_out",
+              "shared_out", "out_f32"]
+
+
+class MoeTaps(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in TAP_FIELDS]
+
+
+class SynthDesc(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("scale_lo", C.c_uint32), ("scale_hi", C.c_uint32),
+                ("router_sigma", C.c_float), ("bias_sigma", C.c_float),
+                ("shared_sigma", C.c_float), ("gamma_value", C.c_float)]
+
+
+class Stats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("forward_calls", "kernel_launches", "scratch_bytes",
+                                         "resident_weight_bytes", "weight_h2d_bytes",
+                                         "experts_resident")]
+
+
+_vp = C.c_void_p
+_LIB = None
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "k3x_hip_status_name": (C.c_char_p, [C.c_int]),
+    "k3x_hip_ctx_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "k3x_hip_ctx_destroy": (C.c_int, [_vp]),
+    "k3x_hip_ctx_set_stream": (C.c_int, [_vp, _vp]),
+    "k3x_hip_ctx_use_own_stream": (C.c_int, [_vp]),
+    "k3x_hip_ctx_stream": (_vp, [_vp]),
+    "k3x_hip_ctx_synchronize": (C.c_int, [_vp]),
+    "k3x_hip_ctx_stats": (C.c_int, [_vp, C.POINTER(Stats)]),
+    "k3x_hip_bank_create": (C.c_int, [_vp, C.POINTER(LayerDesc), C.POINTER(_vp)]),
+    "k3x_hip_bank_destroy": (C.c_int, [_vp]),
+    "k3x_hip_bank_upload_expert": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64), _vp, _vp,
+                                             _vp, _vp, _vp, _vp]),
+    "k3x_hip_bank_find": (C.c_int, [_vp, C.c_uint64, C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint32)]),
+    "k3x_hip_bank_upload_shared": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "k3x_hip_bank_upload_router": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "k3x_hip_bank_set_router_device": (C.c_int, [_vp, _vp, _vp, _vp]),
+    "k3x_hip_bank_fill_synthetic": (C.c_int, [_vp, C.POINTER(SynthDesc)]),
+    "k3x_hip_synth_normal_bf16": (C.c_int, [_vp, C.c_uint64, C.c_uint64, C.c_float, C.c_size_t,
+                                            _vp]),
+    "k3x_hip_bank_dequant_rows": (C.c_int, [_vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                            _vp]),
+    "k3x_hip_bank_bytes": (C.c_uint64, [_vp]),
+    "k3x_hip_moe_forward": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp,
+                                      C.POINTER(MoeTaps)]),
+    "k3x_hip_moe_forward_routed": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp, _vp, _vp,
+                                             _vp, _vp, C.POINTER(MoeTaps)]),
+    "k3x_hip_expert_major_plan": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
+                                            C.POINTER(MoeTaps)]),
+}
+
+EXPORTED = sorted(_SIGS)
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Loads the HIP library and declares every entry point; raises if absent."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing: build it with `make -C project-k3x_amd` "
+                "(or __graft_entry__.build())")
+        lib = C.CDLL(path)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = lib
+    return _LIB
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise K3xError(status, what)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a torch tensor (None passes through)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def host_ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Context:
+    def __init__(self, device: int = 0, use_torch_stream: bool = True):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("no HIP device: the MoE layer has no CPU path")
+        self.lib = load()
+        h = _vp()
+        check(self.lib.k3x_hip_ctx_create(device, C.byref(h)), "k3x_hip_ctx_create")
+        self.handle = h
+        self.device = device
+        if use_torch_stream:
+            with torch.cuda.device(device):
+                s = torch.cuda.current_stream().cuda_stream
+            check(self.lib.k3x_hip_ctx_set_stream(h, _vp(s)), "k3x_hip_ctx_set_stream")
+
+    def synchronize(self) -> int:
+        return self.lib.k3x_hip_ctx_synchronize(self.handle)
+
+    def stats(self) -> Stats:
+        s = Stats()
+        check(self.lib.k3x_hip_ctx_stats(self.handle, C.byref(s)), "k3x_hip_ctx_stats")
+        return s
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.k3x_hip_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class LayerShape:
+    hidden: int
+    inter: int
+    experts: int
+    shared_inter: int = 0
+    group_size: int = 32
+
+    def desc(self) -> LayerDesc:
+        return LayerDesc(self.hidden, self.inter, self.experts, self.group_size,
+                         self.shared_inter)
+
+    def routed_bytes_per_expert(self) -> int:
+        n = self.hidden * self.inter
+        return 3 * (n // 2 + n // 32)
+
+
+class Bank:
+    def __init__(self, ctx: Context, shape: LayerShape):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.shape = shape
+        h = _vp()
+        d = shape.desc()
+        check(self.lib.k3x_hip_bank_create(ctx.handle, C.byref(d), C.byref(h)),
+              "k3x_hip_bank_create")
+        self.handle = h
+
+    def fill_synthetic(self, seed: int, scale_lo: int, scale_hi: int, router_sigma=0.02,
+                       bias_sigma=0.1, shared_sigma=0.02, gamma=1.0) -> None:
+        d = SynthDesc(seed, scale_lo, scale_hi, router_sigma, bias_sigma, shared_sigma, gamma)
+        check(self.lib.k3x_hip_bank_fill_synthetic(self.handle, C.byref(d)),
+              "k3x_hip_bank_fill_synthetic")
+
+    def upload_expert(self, expert: int, ex: dict, tensor_ids=None) -> int:
+        import numpy as np
+        ids = tensor_ids or (3 * expert + 1, 3 * expert + 2, 3 * expert + 3)
+        arr = (C.c_uint64 * 3)(*ids)
+        keep = [np.ascontiguousarray(ex[k], dtype=np.uint8) for k in
+                ("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+                 "down_scales")]
+        return self.lib.k3x_hip_bank_upload_expert(self.handle, expert, arr,
+                                                   *[host_ptr(a) for a in keep])
+
+    def upload_shared(self, gate, up, down) -> int:
+        import numpy as np
+        g, u, d = (np.ascontiguousarray(a, dtype=np.uint16) for a in (gate, up, down))
+        return self.lib.k3x_hip_bank_upload_shared(self.handle, host_ptr(g), host_ptr(u),
+                                                   host_ptr(d))
+
+    def upload_router(self, weight, bias, gamma) -> int:
+        import numpy as np
+        w, b, g = (np.ascontiguousarray(a, dtype=np.float32) for a in (weight, bias, gamma))
+        return self.lib.k3x_hip_bank_upload_router(self.handle, host_ptr(w), host_ptr(b),
+                                                   host_ptr(g))
+
+    def find(self, tensor_id: int):
+        e, m = C.c_uint32(0), C.c_uint32(0)
+        st = self.lib.k3x_hip_bank_find(self.handle, tensor_id, C.byref(e), C.byref(m))
+        return st, e.value, m.value
+
+    def dequant_rows(self, expert: int, matrix: int, row0: int, nrows: int):
+        import torch
+        cols = self.shape.hidden if matrix != MATRIX_DOWN else self.shape.inter
+        out = torch.empty((nrows, cols), dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        check(self.lib.k3x_hip_bank_dequant_rows(self.handle, expert, matrix, row0, nrows,
+                                                 ptr(out)), "k3x_hip_bank_dequant_rows")
+        return out
+
+    def bytes(self) -> int:
+        return self.lib.k3x_hip_bank_bytes(self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.k3x_hip_bank_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def make_params(tokens, top_k, routed_scale=1.0, eps=1e-6, glu=GLU_SWIGLU, beta=4.0,
+                linear=None, renorm=RENORM_FLOAT) -> MoeParams:
+    return MoeParams(tokens, top_k, routed_scale, eps, glu, beta, int(linear is not None),
+                     linear or 0.0, renorm)
+
+
+def make_taps(tensors: dict | None) -> MoeTaps | None:
+    if not tensors:
+        return None
+    t = MoeTaps()
+    for k, v in tensors.items():
+        setattr(t, k, ptr(v))
+    return t
+
+
+def synth_normal_bf16(ctx: Context, seed: int, stream: int, sigma: float, out) -> None:
+    check(ctx.lib.k3x_hip_synth_normal_bf16(ctx.handle, seed, stream, sigma, out.numel(),
+                                            ptr(out)), "k3x_hip_synth_normal_bf16")
+
+
+def moe_forward(ctx: Context, bank: Bank, params: MoeParams, x, out, taps=None) -> int:
+    t = make_taps(taps)
+    return ctx.lib.k3x_hip_moe_forward(ctx.handle, bank.handle, C.byref(params), ptr(x),
+                                       ptr(out), C.byref(t) if t is not None else None)
+
+
+def moe_forward_routed(ctx: Context, bank: Bank, params: MoeParams, xn, ids, weights, out,
+                       host_ids=None, host_weights=None, taps=None) -> int:
+    t = make_taps(taps)
+    return ctx.lib.k3x_hip_moe_forward_routed(
+        ctx.handle, bank.handle, C.byref(params), ptr(xn), ptr(ids), ptr(weights),
+        host_ptr(host_ids), host_ptr(host_weights), ptr(out),
+        C.byref(t) if t is not None else None)
+
+
+def expert_major_plan(ctx: Context, ids, tokens, top_k, experts, taps: dict) -> int:
+    t = make_taps(taps)
+    return ctx.lib.k3x_hip_expert_major_plan(ctx.handle, ptr(ids), tokens, top_k, experts,
+                                             C.byref(t))
