@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-expert MoE layer on one MI355X.
+
+Workload (the configuration the headline metric is
+quoted on): the K3-shaped decode layer, T=2 tokens, H=7168, 384 MXFP4
+experts of I=2048, natural Top-16 with renormalised weights x2.5, one bf16
+shared expert of I=2048, input RMSNorm, routing on the device.  A "step" is
+one layer call.  Steps cycle over --layers resident banks (each 9 GB, a
+different seed: consecutive calls stream different weights, as consecutive
+layers of a decode pass do) and --inputs token pairs.
+
+Prints one JSON line.  value = microseconds per layer call (lower is better);
+the HBM figures use the bytes each call actually streams (distinct routed
+experts touched x 23,396,352 B + shared expert + router).  The same line
+carries the T=2048 prefill chunk as "prefill" and the reference
+CPU expert path, timed on this host, as "cpu_baseline".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "project-k3x_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MXFP4_PEAK_TFLOPS = 10100.0    # MI355X dense MXFP4 / FP6
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16
+
+H, I, E, K, S = 7168, 2048, 384, 16, 2048
+EXPERT_BYTES = 3 * (H * I // 2 + H * I // 32)          # 23,396,352
+GATE_UP_BYTES = 2 * (H * I // 2 + H * I // 32)         # 15,597,568
+DOWN_BYTES = H * I // 2 + H * I // 32                  # 7,798,784
+SHARED_GU_BYTES = 2 * S * H * 2                        # 58,720,256
+SHARED_DOWN_BYTES = H * S * 2                          # 29,360,128
+ROUTER_BYTES = E * H * 4 + E * 4 + H * 4               # weights + bias + gamma
+EXPERT_FLOPS = 2 * 3 * H * I                           # per (token, expert) pair
+SHARED_FLOPS = 2 * 3 * H * S                           # per token
+SEED, X_SEED = 0x4B3358, 0x5EED
+SCALE_LO, SCALE_HI = 119, 123
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--layers", type=int, default=4, help="resident layer banks to cycle")
+    ap.add_argument("--inputs", type=int, default=8, help="distinct token pairs to cycle")
+    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the layer and its resident "
+                                   "bank live on a single MI355X (--gpus 1)",
+                          "n_gpus": args.gpus}))
+        return 2
+    import numpy as np
+    import torch
+    import k3x_amd
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs an MI355X (no HIP device visible)")
+    dev = "cuda:0"
+    ctx = k3x_amd.Context(0)
+    shape = k3x_amd.LayerShape(H, I, E, S)
+    banks = []
+    for layer in range(args.layers):
+        b = k3x_amd.Bank(ctx, shape)
+        b.fill_synthetic(SEED + layer, SCALE_LO, SCALE_HI, 0.02, 0.1, 0.02, 1.0)
+        banks.append(b)
+    log(f"{args.layers} banks resident, {banks[0].bytes() / 1e9:.2f} GB each")
+
+    T = 2
+    xs = []
+    for i in range(args.inputs):
+        x = torch.empty((T, H), dtype=torch.int16, device=dev)
+        k3x_amd.synth_normal_bf16(ctx, X_SEED + i, k3x_amd.stream_id(k3x_amd.STREAM_INPUT), 1.0, x)
+        xs.append(x)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    params = k3x_amd.make_params(T, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
+                                 k3x_amd.RENORM_FLOAT)
+    combos = np.lcm(args.layers, args.inputs)
+
+    # Distinct experts each (layer, input) call touches, for the byte count.
+    active = {}
+    na = torch.empty(1, dtype=torch.int32, device=dev)
+    for i in range(combos):
+        lb, xi = i % args.layers, i % args.inputs
+        k3x_amd.check(k3x_amd.moe_forward(ctx, banks[lb], params, xs[xi], out,
+                                          {"n_active": na}), "moe_forward")
+        k3x_amd.check(ctx.synchronize(), "synchronize")
+        active[(lb, xi)] = int(na.item())
+    touched = [active[(i % args.layers, i % args.inputs)] for i in range(combos)]
+    mean_d = sum(touched) / len(touched)
+
+    def step(i: int) -> None:
+        st = k3x_amd.moe_forward(ctx, banks[i % args.layers], params, xs[i % args.inputs], out)
+        if st:
+            raise k3x_amd.K3xError(st, "moe_forward")
+
+    def run(n: int) -> float:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n):
+            step(i)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    run(args.warmup)
+    k3x_amd.check(ctx.synchronize(), "warmup")
+    log(f"timing {args.steps} steps")
+    elapsed = run(args.steps)
+    k3x_amd.check(ctx.synchronize(), "timed steps")
+    us = elapsed / args.steps * 1e6
+
+    # Same steps again with per-stage hipEvent pairs on the layer's stream.
+    ctx.set_profiling(True)
+    ctx.stage_times(reset=True)
+    prof_elapsed = run(args.steps)
+    stages = ctx.stage_times(reset=True)
+    ctx.set_profiling(False)
+    k3x_amd.check(ctx.synchronize(), "profiled steps")
+
+    routed_bytes = mean_d * EXPERT_BYTES
+    all_bytes = routed_bytes + SHARED_GU_BYTES + SHARED_DOWN_BYTES + ROUTER_BYTES + 2 * T * H * 2
+    stage_bytes = {
+        "gate_up": mean_d * GATE_UP_BYTES + T * H * 2,
+        "down": mean_d * DOWN_BYTES,
+        "shared_gate_up": SHARED_GU_BYTES,
+        "shared_down": SHARED_DOWN_BYTES,
+        "route": ROUTER_BYTES + T * H * 2,
+    }
+    stage_report = {}
+    for name, (ms, n) in stages.items():
+        if not n:
+            continue
+        avg_us = ms / n * 1e3
+        entry = {"avg_us": round(avg_us, 3), "launches": int(n)}
+        if name in stage_bytes:
+            entry["gbps"] = round(stage_bytes[name] / (avg_us * 1e-6) / 1e9, 1)
+        stage_report[name] = entry
+    dom = max(("gate_up", "down", "shared_gate_up", "shared_down"),
+              key=lambda s: stage_report.get(s, {}).get("avg_us", 0.0))
+    dom_us = stage_report[dom]["avg_us"]
+    achieved = stage_bytes[dom] / (dom_us * 1e-6) / 1e9
+
+    result = {
+        "metric": "MoE-layer µs @T=2 decode (HBM GB/s, %peak); MXFP4 TFLOPS @T=2048",
+        "value": round(us, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded generator; random-init weights of the K3 layer shape)",
+        "config": {"workload": "c3_decode_layer: T=2, H=7168, E=384 MXFP4 experts I=2048, "
+                               "Top-16 sigmoid+bias router x2.5, bf16 shared expert I=2048, "
+                               "RMSNorm, device routing",
+                   "tokens": T, "layers_cycled": args.layers, "inputs_cycled": args.inputs},
+        "tokens_per_s": round(T / (us * 1e-6), 1),
+        "experts_touched_mean": mean_d,
+        "hbm_gbps_routed": round(routed_bytes / (us * 1e-6) / 1e9, 1),
+        "hbm_frac_routed": round(routed_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_gbps_all": round(all_bytes / (us * 1e-6) / 1e9, 1),
+        "hbm_frac_all": round(all_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "profiled_us_per_layer": round(prof_elapsed / args.steps * 1e6, 3),
+        "stages": stage_report,
+        "roofline": {"bound": "hbm", "kernel": f"expert_gemm ({dom})",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+
+    if not args.no_prefill:
+        result["prefill"] = prefill(args, ctx, banks[0], k3x_amd, torch)
+    for b in banks:
+        b.close()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    ctx.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
+    """T=2048 tokens through the same layer shape."""
+    T = 2048
+    dev = "cuda:0"
+    x = torch.empty((T, H), dtype=torch.int16, device=dev)
+    k3x_amd.synth_normal_bf16(ctx, X_SEED + 1000, k3x_amd.stream_id(k3x_amd.STREAM_INPUT), 1.0, x)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    na = torch.empty(1, dtype=torch.int32, device=dev)
+    params = k3x_amd.make_params(T, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
+                                 k3x_amd.RENORM_FLOAT)
+    k3x_amd.check(k3x_amd.moe_forward(ctx, bank, params, x, out, {"n_active": na}), "prefill")
+    k3x_amd.check(ctx.synchronize(), "prefill")
+    d = int(na.item())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.prefill_steps):
+        k3x_amd.check(k3x_amd.moe_forward(ctx, bank, params, x, out), "prefill")
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / args.prefill_steps * 1e6
+    k3x_amd.check(ctx.synchronize(), "prefill")
+    routed_flops = T * K * EXPERT_FLOPS
+    all_flops = routed_flops + T * SHARED_FLOPS
+    bytes_ = d * EXPERT_BYTES + SHARED_GU_BYTES + SHARED_DOWN_BYTES + ROUTER_BYTES + 2 * T * H * 2
+    tflops = routed_flops / (us * 1e-6) / 1e12
+    floor_us = max(bytes_ / (HBM_PEAK_GBS * 1e9), routed_flops / (MXFP4_PEAK_TFLOPS * 1e12)) * 1e6
+    log(f"prefill T=2048: {us:.1f} us/layer")
+    return {"workload": "c5_prefill_chunk: T=2048, same layer", "tokens": T,
+            "steps": args.prefill_steps, "us_per_layer": round(us, 1),
+            "tokens_per_s": round(T / (us * 1e-6), 1), "experts_touched": d,
+            "routed_tflops": round(tflops, 2),
+            "all_tflops": round(all_flops / (us * 1e-6) / 1e12, 2),
+            "mxfp4_peak_frac": round(tflops / MXFP4_PEAK_TFLOPS, 4),
+            "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_floor_us": round(floor_us, 1),
+            "frac_of_floor": round(floor_us / us, 4)}
+
+
+def cpu_baseline() -> dict:
+    """The reference's own CPU path (oracle/_ref, built from its sources):
+    one T=2 decode layer call of layer 0, token by token through rms_norm ->
+    router dense_matvec -> sigmoid -> select_routing -> mxfp4_situ_moe +
+    dense_situ_mlp shared expert, single thread, as the reference runs it."""
+    import numpy as np
+    sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
+    from oracle import ORDER_SEQ, REF_SO, SIGMOID_REF, Oracle, RefLib, bf16_to_f32
+    from synth import CONFIGS, SynthLayer
+
+    kind = "reference" if os.path.exists(REF_SO) else "port"
+    o = Oracle()
+    cfg = CONFIGS[3]
+    layer = SynthLayer(o, cfg)
+    x = bf16_to_f32(layer.x_bits())
+    # Which experts the reference will select (same sequential-double router
+    # and libm sigmoid), so only those are generated on the host.
+    xn = [o.rms_norm(x[t], layer.gamma, cfg.eps) for t in range(cfg.tokens)]
+    ids = [o.route(o.router_logits(layer.router, xn[t], ORDER_SEQ), layer.bias, cfg.top_k,
+                   cfg.renorm, cfg.routed_scale, SIGMOID_REF)[1] for t in range(cfg.tokens)]
+    experts = [None] * cfg.experts
+    for e in sorted({int(e) for row in ids for e in row}):
+        experts[e] = layer.expert(e)
+    shared = tuple(bf16_to_f32(a) for a in layer.shared)
+    t0 = time.perf_counter()
+    if kind == "reference":
+        ref = RefLib()
+        for t in range(cfg.tokens):
+            st, _, _ = ref.moe_layer_token(x[t], layer.gamma, cfg.eps, layer.router, layer.bias,
+                                           experts, cfg.hidden, cfg.inter, cfg.top_k,
+                                           cfg.routed_scale, shared, beta=4.0)
+            if st:
+                raise RuntimeError(f"reference CPU layer failed: {st}")
+    else:
+        for t in range(cfg.tokens):
+            for s in range(cfg.top_k):
+                o.expert_ffn(xn[t], experts[int(ids[t][s])], cfg.hidden, cfg.inter)
+    sec = time.perf_counter() - t0
+    log(f"cpu baseline ({kind}): {sec:.2f} s per T=2 layer call")
+    return {"value": round(sec * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": kind,
+            "sample": "one c3 decode layer call (T=2, 32 routed pairs + shared expert), "
+                      "reference CPU composition, single thread"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -135,6 +135,18 @@ typedef struct k3x_hip_synth_desc {
     float gamma_value;
 } k3x_hip_synth_desc;
 
+/* Stages of k3x_hip_moe_forward timed by k3x_hip_ctx_set_profiling. */
+enum k3x_stage {
+    K3X_STAGE_ROUTE = 0,        /* RMSNorm, router logits, Top-K */
+    K3X_STAGE_GROUP = 1,        /* expert-major grouping */
+    K3X_STAGE_GATE_UP = 2,      /* routed MXFP4 gate/up + GLU */
+    K3X_STAGE_SHARED_GATE_UP = 3,
+    K3X_STAGE_DOWN = 4,         /* routed MXFP4 down projection */
+    K3X_STAGE_SHARED_DOWN = 5,
+    K3X_STAGE_COMBINE = 6,      /* slot-ordered mix + shared add + bf16 cast */
+    K3X_STAGE_COUNT = 7,
+};
+
 /* Counters, after BackendRuntimeStats (runtime/include/k3x/backend.hpp:50-129). */
 typedef struct k3x_hip_stats {
     uint64_t forward_calls;
@@ -163,6 +175,18 @@ int k3x_hip_ctx_synchronize(k3x_hip_ctx* ctx);
 /* Replaces ComputeBackend::runtime_stats (backend.hpp:331). */
 int k3x_hip_ctx_stats(k3x_hip_ctx* ctx, k3x_hip_stats* out);
 const char* k3x_hip_status_name(int status); /* error_code_name, status.hpp:33-56 */
+/* Per-stage device timing: when enabled, every stage that a forward call
+ * enqueues is bracketed by a hipEvent pair on the context stream (the
+ * reference brackets each launch with cudaEvent pairs and records
+ * ProfileEvent::device_nanoseconds, runtime/cuda/backend_cuda.cu:2251-2298,
+ * runtime/include/k3x/profile.hpp:32-42). */
+int k3x_hip_ctx_set_profiling(k3x_hip_ctx* ctx, int enabled);
+/* Waits for the stream, then adds the elapsed milliseconds and the number of
+ * timed launches of each stage since the last reset into ms[K3X_STAGE_COUNT]
+ * and launches[K3X_STAGE_COUNT] (host arrays, overwritten); reset != 0
+ * clears the totals afterwards. */
+int k3x_hip_ctx_stage_times(k3x_hip_ctx* ctx, double* ms, uint64_t* launches,
+                            int reset);
 
 /* ---- resident expert bank ------------------------------------------------ */
 

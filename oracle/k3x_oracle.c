@@ -256,16 +256,17 @@ void k3xo_router_logits(const float* weight, const float* x, size_t experts,
 
 static int finitef(float v) { return isfinite(v) != 0; }
 
-/* Sigmoid scores, bias-adjusted natural Top-K (ties -> lower expert index),
- * renormalised contributions times routed_scale.
+/* Bias-adjusted natural Top-K over given scores (ties -> lower expert
+ * index), renormalised contributions times routed_scale.
  * Selection: runtime/src/routing_policy.cpp:76-87 (stable_sort descending),
  *            runtime/src/official_moe.cpp:224-233 (explicit tie comparator).
- * FLOAT renorm + validation: runtime/src/routing_policy.cpp:40-50,89-95,
- *            146-157; routed_scale: runtime/src/model.cpp:1004-1009.
- * DOUBLE renorm + validation: runtime/src/official_moe.cpp:214-242. */
-int k3xo_route(const float* logits, const float* bias, size_t experts,
-               size_t top_k, int renorm, float routed_scale, int sigmoid_mode,
-               uint32_t* ids, float* weights, float* scores) {
+ * FLOAT renorm + validation: runtime/src/routing_policy.cpp:40-50,76-80,
+ *            89-95,146-157; routed_scale: runtime/src/model.cpp:1004-1009.
+ * DOUBLE renorm: runtime/src/official_moe.cpp:234-242 (its finiteness
+ *            checks on logits and bias are made by k3xo_route). */
+int k3xo_select(const float* scores, const float* bias, size_t experts,
+                size_t top_k, int renorm, float routed_scale, uint32_t* ids,
+                float* weights) {
     const int dims_error =
         renorm == K3XO_RENORM_DOUBLE ? K3XO_INVALID_EXTENT : K3XO_INVALID_STATE;
     if (!experts || !top_k || top_k > experts) return dims_error;
@@ -277,24 +278,22 @@ int k3xo_route(const float* logits, const float* bias, size_t experts,
         goto done;
     }
     for (size_t e = 0; e < experts; ++e) {
-        if (renorm == K3XO_RENORM_DOUBLE &&
-            (!finitef(logits[e]) || !finitef(bias[e]))) {
-            status = K3XO_INVALID_EXTENT;
-            goto done;
-        }
-        scores[e] = k3xo_sigmoid(logits[e], sigmoid_mode);
         if (renorm == K3XO_RENORM_FLOAT &&
             (!finitef(scores[e]) || scores[e] < 0.0f || scores[e] > 1.0f ||
              !finitef(bias[e]))) {
             status = K3XO_INVALID_STATE;
             goto done;
         }
+    }
+    for (size_t e = 0; e < experts; ++e) {
         adjusted[e] = scores[e] + bias[e];
         if (renorm == K3XO_RENORM_FLOAT && !finitef(adjusted[e])) {
             status = K3XO_INVALID_STATE;
             goto done;
         }
     }
+    /* Repeated arg-max with strict '>' keeps the lowest index among equal
+     * adjusted scores, which is the order a stable descending sort gives. */
     for (size_t slot = 0; slot < top_k; ++slot) {
         size_t best = experts;
         for (size_t e = 0; e < experts; ++e) {
@@ -329,6 +328,24 @@ done:
     free(adjusted);
     free(taken);
     return status;
+}
+
+/* Sigmoid scores of the logits, then k3xo_select.  Scores:
+ * runtime/src/model.cpp:923-925 (FLOAT convention, the synthetic path) and
+ * runtime/src/official_moe.cpp:214-223 (DOUBLE convention, which first
+ * rejects non-finite logits or bias with invalid_extent). */
+int k3xo_route(const float* logits, const float* bias, size_t experts,
+               size_t top_k, int renorm, float routed_scale, int sigmoid_mode,
+               uint32_t* ids, float* weights, float* scores) {
+    if (renorm == K3XO_RENORM_DOUBLE) {
+        if (!experts || !top_k || top_k > experts) return K3XO_INVALID_EXTENT;
+        for (size_t e = 0; e < experts; ++e)
+            if (!finitef(logits[e]) || !finitef(bias[e])) return K3XO_INVALID_EXTENT;
+    }
+    for (size_t e = 0; e < experts; ++e)
+        scores[e] = k3xo_sigmoid(logits[e], sigmoid_mode);
+    return k3xo_select(scores, bias, experts, top_k, renorm, routed_scale, ids,
+                       weights);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -75,6 +75,9 @@ float k3xo_sigmoid(float x, int mode);
 double k3xo_canon_dot(const float* a, const float* b, size_t n);
 void k3xo_router_logits(const float* weight, const float* x, size_t experts,
                         size_t hidden, int order, float* logits);
+int k3xo_select(const float* scores, const float* bias, size_t experts,
+                size_t top_k, int renorm, float routed_scale, uint32_t* ids,
+                float* weights);
 int k3xo_route(const float* logits, const float* bias, size_t experts,
                size_t top_k, int renorm, float routed_scale, int sigmoid_mode,
                uint32_t* ids, float* weights, float* scores);

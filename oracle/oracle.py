@@ -78,6 +78,7 @@ class Oracle:
         L.k3xo_rms_norm_canon.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
         L.k3xo_glu.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_int, C.c_float, C.c_int, C.c_float]
         L.k3xo_router_logits.argtypes = [_f32p, _f32p, _sz, _sz, C.c_int, _f32p]
+        L.k3xo_select.argtypes = [_f32p, _f32p, _sz, _sz, C.c_int, C.c_float, _u32p, _f32p]
         L.k3xo_route.argtypes = [_f32p, _f32p, _sz, _sz, C.c_int, C.c_float, C.c_int,
                                  _u32p, _f32p, _f32p]
         L.k3xo_expert_major_plan.argtypes = [_u32p, _f32p, _sz, _sz, C.POINTER(_sz), _u32p,
@@ -152,6 +153,14 @@ class Oracle:
         out = np.zeros(E, np.float32)
         self.lib.k3xo_router_logits(_p(W, _f32p), _p(x, _f32p), E, H, order, _p(out, _f32p))
         return out
+
+    def select(self, scores, bias, top_k, renorm=RENORM_FLOAT, routed_scale=1.0):
+        scores, bias = f32(scores), f32(bias)
+        ids = np.zeros(top_k, np.uint32)
+        w = np.zeros(top_k, np.float32)
+        st = self.lib.k3xo_select(_p(scores, _f32p), _p(bias, _f32p), scores.size, top_k,
+                                  renorm, routed_scale, _p(ids, _u32p), _p(w, _f32p))
+        return st, ids, w
 
     def route(self, logits, bias, top_k, renorm=RENORM_FLOAT, routed_scale=1.0,
               sigmoid=SIGMOID_CR):

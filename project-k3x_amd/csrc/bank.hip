@@ -251,6 +251,72 @@ int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes) {
     return K3X_OK;
 }
 
+namespace {
+
+hipEvent_t take_event(k3x_hip_ctx* ctx) {
+    if (!ctx->free_events.empty()) {
+        hipEvent_t e = ctx->free_events.back();
+        ctx->free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+}  // namespace
+
+// Marks kept pending before a forced read-back (bounds the event pool).
+constexpr size_t kMaxPendingMarks = 1u << 16;
+
+int begin_stage(k3x_hip_ctx* ctx, uint32_t stage) {
+    if (!ctx->profiling || stage >= K3X_STAGE_COUNT) return -1;
+    if (ctx->pending.size() >= kMaxPendingMarks && drain_stage_marks(ctx) != K3X_OK) return -1;
+    StageMark m{stage, take_event(ctx), take_event(ctx)};
+    if (!m.start || !m.stop || hipEventRecord(m.start, ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        if (m.start) ctx->free_events.push_back(m.start);
+        if (m.stop) ctx->free_events.push_back(m.stop);
+        return -1;
+    }
+    ctx->pending.push_back(m);
+    return (int)ctx->pending.size() - 1;
+}
+
+void end_stage(k3x_hip_ctx* ctx, int mark) {
+    if (mark < 0 || (size_t)mark >= ctx->pending.size()) return;
+    if (hipEventRecord(ctx->pending[mark].stop, ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        StageMark m = ctx->pending[mark];
+        ctx->pending.erase(ctx->pending.begin() + mark);
+        ctx->free_events.push_back(m.start);
+        ctx->free_events.push_back(m.stop);
+    }
+}
+
+int drain_stage_marks(k3x_hip_ctx* ctx) {
+    if (ctx->pending.empty()) return K3X_OK;
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    int st = K3X_OK;
+    for (const StageMark& m : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, m.start, m.stop) == hipSuccess) {
+            ctx->stage_ms[m.stage] += ms;
+            ctx->stage_launches[m.stage] += 1;
+        } else {
+            (void)hipGetLastError();
+            st = K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        ctx->free_events.push_back(m.start);
+        ctx->free_events.push_back(m.stop);
+    }
+    ctx->pending.clear();
+    return st;
+}
+
 }  // namespace k3x_hip
 
 extern "C" {
@@ -299,9 +365,35 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->status) (void)hipFree(ctx->status);
+    for (const StageMark& m : ctx->pending) {
+        (void)hipEventDestroy(m.start);
+        (void)hipEventDestroy(m.stop);
+    }
+    for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return K3X_OK;
+}
+
+int k3x_hip_ctx_set_profiling(k3x_hip_ctx* ctx, int enabled) {
+    if (!ctx) return K3X_ERR_INVALID_EXTENT;
+    ctx->profiling = enabled != 0;
+    return K3X_OK;
+}
+
+int k3x_hip_ctx_stage_times(k3x_hip_ctx* ctx, double* ms, uint64_t* launches, int reset) {
+    if (!ctx || !ms || !launches) return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    const int st = k3x_hip::drain_stage_marks(ctx);
+    for (int i = 0; i < K3X_STAGE_COUNT; ++i) {
+        ms[i] = ctx->stage_ms[i];
+        launches[i] = ctx->stage_launches[i];
+        if (reset) {
+            ctx->stage_ms[i] = 0.0;
+            ctx->stage_launches[i] = 0;
+        }
+    }
+    return st;
 }
 
 int k3x_hip_ctx_set_stream(k3x_hip_ctx* ctx, void* hip_stream) {

@@ -10,6 +10,13 @@
 
 #include "../../include/k3x_hip_moe.h"
 
+// One timed stage launch: a hipEvent pair recorded around it.
+struct StageMark {
+    uint32_t stage;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
 struct k3x_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -21,6 +28,12 @@ struct k3x_hip_ctx {
     uint64_t forward_calls = 0;
     uint64_t kernel_launches = 0;
     uint64_t weight_h2d_bytes = 0;
+    // Stage profiling (k3x_hip_ctx_set_profiling).
+    bool profiling = false;
+    std::vector<StageMark> pending;      // recorded, not yet read back
+    std::vector<hipEvent_t> free_events;
+    double stage_ms[K3X_STAGE_COUNT] = {};
+    uint64_t stage_launches[K3X_STAGE_COUNT] = {};
 };
 
 // Geometry of the tile layout for one matrix family of the bank.
@@ -69,5 +82,12 @@ inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BA
 
 // Makes sure ctx->scratch holds at least `bytes`; grow-only.
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
+
+// Brackets the launches made between begin and end with an event pair when
+// profiling is on.  begin_stage returns the index of the open mark or -1.
+int begin_stage(k3x_hip_ctx* ctx, uint32_t stage);
+void end_stage(k3x_hip_ctx* ctx, int mark);
+// Reads back every pending mark into the per-stage totals (synchronises).
+int drain_stage_marks(k3x_hip_ctx* ctx);
 
 }  // namespace k3x_hip

@@ -591,8 +591,12 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              uint16_t* out, float* out_f32) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
+    using k3x_hip::begin_stage;
+    using k3x_hip::end_stage;
+    int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
                           s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu);
+    end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     const bool wide = T > 16;  // more than one 16-row MFMA tile per expert possible
@@ -620,8 +624,10 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.pair_slot = s.pair_slot;
     g.act = s.act;
     g.act_stride = d.inter;
+    mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
     if (wide) launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
     else launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
+    end_stage(ctx, mark);
     // Shared gate/up + GLU (single block of T rows).
     if (d.shared_inter) {
         GemmArgs sg = g;
@@ -635,8 +641,10 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sg.tokens = T;
         sg.act = s.sact;
         sg.act_stride = d.shared_inter;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP);
         if (wide) launch_gemm<false, true, 4, 1>(ctx, sg, 1, d.shared_inter);
         else launch_gemm<false, true, 1, 1>(ctx, sg, 1, d.shared_inter);
+        end_stage(ctx, mark);
     }
     // Routed down, scattered to [token][slot].
     GemmArgs dn = g;
@@ -652,8 +660,10 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.y = s.y;
     dn.y_stride = d.hidden;
     dn.scatter = 1;
+    mark = begin_stage(ctx, K3X_STAGE_DOWN);
     if (wide) launch_gemm<true, false, 4, 2>(ctx, dn, max_active, d.hidden);
     else launch_gemm<true, false, 1, 2>(ctx, dn, max_active, d.hidden);
+    end_stage(ctx, mark);
     if (d.shared_inter) {
         GemmArgs sd = dn;
         sd.codes = bank->sh_dn;
@@ -667,12 +677,16 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sd.tokens = T;
         sd.y = s.sy;
         sd.scatter = 0;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN);
         if (wide) launch_gemm<false, false, 4, 2>(ctx, sd, 1, d.hidden);
         else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden);
+        end_stage(ctx, mark);
     }
+    mark = begin_stage(ctx, K3X_STAGE_COMBINE);
     hipLaunchKernelGGL(combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0,
                        ctx->stream, s.y, weights, d.shared_inter ? s.sy : nullptr, K, d.hidden,
                        out, out_f32, ctx->status);
+    end_stage(ctx, mark);
     return launched(ctx, d.shared_inter ? 5 : 3);
 }
 
@@ -731,6 +745,7 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     if ((st = prepare(ctx, bank, p, &s))) return st;
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
+    const int mark = k3x_hip::begin_stage(ctx, K3X_STAGE_ROUTE);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, bank->gamma,
                        d.hidden, p->rms_epsilon, s.xn, ctx->status);
     if (T <= 4) {
@@ -744,6 +759,7 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)d.experts * 12, ctx->stream,
                        s.logits, bank->router_bias, d.experts, K, p->routed_scale, p->renorm,
                        s.ids, s.weights, ctx->status);
+    k3x_hip::end_stage(ctx, mark);
     if ((st = launched(ctx, 3))) return st;
     if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr)))
         return st;

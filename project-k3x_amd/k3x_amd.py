@@ -21,6 +21,7 @@ ERR_INVALID_STATE = 16
 ERR_BACKEND_UNAVAILABLE = 17
 
 GLU_SWIGLU, GLU_SITU = 0, 1
+STAGES = ("route", "group", "gate_up", "shared_gate_up", "down", "shared_down", "combine")
 RENORM_FLOAT, RENORM_DOUBLE = 0, 1
 MATRIX_GATE, MATRIX_UP, MATRIX_DOWN = 0, 1, 2
 
@@ -99,6 +100,9 @@ _SIGS = {
     "k3x_hip_ctx_stream": (_vp, [_vp]),
     "k3x_hip_ctx_synchronize": (C.c_int, [_vp]),
     "k3x_hip_ctx_stats": (C.c_int, [_vp, C.POINTER(Stats)]),
+    "k3x_hip_ctx_set_profiling": (C.c_int, [_vp, C.c_int]),
+    "k3x_hip_ctx_stage_times": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_uint64),
+                                          C.c_int]),
     "k3x_hip_bank_create": (C.c_int, [_vp, C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "k3x_hip_bank_destroy": (C.c_int, [_vp]),
     "k3x_hip_bank_upload_expert": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64), _vp, _vp,
@@ -184,6 +188,19 @@ class Context:
         s = Stats()
         check(self.lib.k3x_hip_ctx_stats(self.handle, C.byref(s)), "k3x_hip_ctx_stats")
         return s
+
+    def set_profiling(self, enabled: bool) -> None:
+        check(self.lib.k3x_hip_ctx_set_profiling(self.handle, int(enabled)),
+              "k3x_hip_ctx_set_profiling")
+
+    def stage_times(self, reset: bool = True) -> dict:
+        """{stage: (total_ms, launches)} since the last reset (synchronises)."""
+        n = len(STAGES)
+        ms = (C.c_double * n)()
+        cnt = (C.c_uint64 * n)()
+        check(self.lib.k3x_hip_ctx_stage_times(self.handle, ms, cnt, int(reset)),
+              "k3x_hip_ctx_stage_times")
+        return {name: (ms[i], cnt[i]) for i, name in enumerate(STAGES)}
 
     def close(self) -> None:
         if self.handle:
