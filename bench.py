@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the routed-expert MoE layer on one MI355X.
 
-Workload (the configuration the headline metric is
+Workload (benchmark configuration 3 of 5, the one the headline metric is
 quoted on): the K3-shaped decode layer, T=2 tokens, H=7168, 384 MXFP4
 experts of I=2048, natural Top-16 with renormalised weights x2.5, one bf16
 shared expert of I=2048, input RMSNorm, routing on the device.  A "step" is

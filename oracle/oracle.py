@@ -314,6 +314,8 @@ class RefLib:
                                                 C.c_float, _f32p]
         L.k3xr_mxfp4_situ_moe.argtypes = [_f32p, _sz, _sz, EB, _f32p, _sz, C.c_float, C.c_int,
                                           C.c_float, _f32p]
+        L.k3xr_route_tokens.argtypes = [_f32p, _sz, _f32p, C.c_float, _f32p, _f32p, _sz, _sz,
+                                        _sz, C.c_float, C.c_int, _u32p, _f32p]
         L.k3xr_moe_layer_token.argtypes = [_f32p, _f32p, C.c_float, _f32p, _f32p, _sz, _sz, _sz,
                                            _sz, C.c_float, EB, _f32p, _f32p, _f32p, _sz,
                                            C.c_float, C.c_int, C.c_float, _u32p, _f32p]
@@ -404,6 +406,20 @@ class RefLib:
                                                 _p(out, _f32p))
         del keep
         return st, out
+
+    def route_tokens(self, x, gamma, eps, router, bias, top_k, routed_scale,
+                     round_normed=True):
+        """ids, weights [T][K] through the reference's routing functions."""
+        x, gamma, router, bias = f32(x), f32(gamma), f32(router), f32(bias)
+        T, H = x.shape
+        E = bias.size
+        ids = np.zeros((T, top_k), np.uint32)
+        w = np.zeros((T, top_k), np.float32)
+        st = self.lib.k3xr_route_tokens(_p(x, _f32p), T, _p(gamma, _f32p), eps,
+                                        _p(router, _f32p), _p(bias, _f32p), E, H, top_k,
+                                        routed_scale, int(round_normed), _p(ids, _u32p),
+                                        _p(w, _f32p))
+        return st, ids, w
 
     def moe_layer_token(self, x, gamma, eps, router, bias, experts_by_id, hidden, inter,
                         top_k, routed_scale, shared=None, beta=4.0, linear=None):

@@ -207,6 +207,55 @@ int k3xr_mxfp4_situ_moe(const float* input, std::size_t hidden,
     return 0;
 }
 
+// Routing of T tokens through the reference's functions: rms_norm
+// (ops.cpp:10-18), optionally rounded to bf16 as the official path rounds its
+// normalised hidden (official_moe.cpp:61-80; the rounding rule is
+// official_moe.cpp:18-26, whose function is file-local, so it is restated
+// here), router dense_matvec (model.cpp:919-921), the float sigmoid of
+// model.cpp:60 / :924, select_routing natural (routing_policy.cpp) and
+// contributions * routed_scale (model.cpp:1004-1009).  Outputs [T][K].
+int k3xr_route_tokens(const float* x, std::size_t tokens, const float* gamma,
+                      float epsilon, const float* router, const float* bias,
+                      std::size_t n_experts, std::size_t hidden,
+                      std::size_t top_k, float routed_scale, int round_normed,
+                      std::uint32_t* ids_out, float* weights_out) {
+    std::vector<float> normed(hidden);
+    for (std::size_t t = 0; t < tokens; ++t) {
+        k3x::rms_norm(normed, {x + t * hidden, hidden}, {gamma, hidden}, epsilon);
+        if (round_normed) {
+            for (auto& v : normed) {
+                std::uint32_t b;
+                std::memcpy(&b, &v, 4);
+                if ((b & 0x7f800000U) == 0x7f800000U) {
+                    if (b & 0x007fffffU) b |= 0x00400000U;
+                } else {
+                    b += 0x7fffU + ((b >> 16U) & 1U);
+                }
+                b &= 0xffff0000U;
+                std::memcpy(&v, &b, 4);
+            }
+        }
+        auto logits = cpu_backend().dense_matvec(
+            normed, k3x::DenseWeightView{5, {router, n_experts * hidden}, n_experts, hidden},
+            0, k3x::ProfilePhase::decode);
+        if (!logits) return static_cast<int>(logits.error());
+        std::vector<float> scores(n_experts);
+        for (std::size_t e = 0; e < n_experts; ++e)
+            scores[e] = 1.0F / (1.0F + std::exp(-logits.value()[e]));
+        auto decision = k3x::select_routing(
+            scores, {bias, n_experts}, top_k,
+            k3x::RoutingPolicyConfig{.mode = k3x::RoutingMode::natural});
+        if (!decision) return static_cast<int>(decision.error());
+        for (std::size_t k = 0; k < top_k; ++k) {
+            ids_out[t * top_k + k] =
+                static_cast<std::uint32_t>(decision.value().expert_ids[k]);
+            weights_out[t * top_k + k] =
+                decision.value().normalized_weights[k] * routed_scale;
+        }
+    }
+    return 0;
+}
+
 // The reference CPU composition of one token of the latent-free layer:
 // rms_norm (ops.cpp:10-18) -> router dense_matvec (model.cpp:919-921) ->
 // sigmoid (model.cpp:60) -> select_routing natural (routing_policy.cpp) ->

@@ -1,4 +1,4 @@
-"""Seeded synthetic layers of the BASELINE configurations, regenerated on the
+"""Seeded synthetic layers of the five benchmark configurations, regenerated on the
 CPU with the oracle's generator (bit-identical to the device fill of
 k3x_hip_bank_fill_synthetic), and the CPU reference of the whole layer.
 
@@ -19,6 +19,7 @@ STREAM_DOWN_CODES, STREAM_DOWN_SCALES = 5, 6
 STREAM_ROUTER, STREAM_BIAS = 7, 8
 STREAM_SHARED_GATE, STREAM_SHARED_UP, STREAM_SHARED_DOWN = 9, 10, 11
 STREAM_INPUT = 12
+STREAM_ZIPF_RANK = 13
 
 
 def sid(kind: int, expert: int = 0) -> int:
@@ -47,15 +48,22 @@ class Config:
     renorm: int = RENORM_FLOAT
     seed: int = 0x4B3358
     x_seed: int = 0x5EED
+    zipf_b0: float = 0.0   # > 0: bias[e] = b0 * rank(e)^-zipf_s instead of N(0, bias_sigma)
+    zipf_s: float = 1.1
     extra: dict = field(default_factory=dict)
 
 
-# BASELINE.json configs[0..4]; scale ranges and sigmas per SURVEY 8(d).
+# The five benchmark configurations (tiny layer, one expert, decode T=2,
+# verification window T=64, prefill T=2048); E8M0 scale ranges and sigmas as
+# the benchmark specification gives them, or chosen here where it does not.
 CONFIGS = {
     1: Config("c1_tiny", 1, 256, 512, 16, 4, 0, 121, 125),
     2: Config("c2_one_expert", 1, 7168, 2048, 1, 1, 0, 119, 123),
     3: Config("c3_decode", 2, 7168, 2048, 384, 16, 2048, 119, 123, routed_scale=2.5),
-    4: Config("c4_verify", 64, 7168, 2048, 384, 16, 2048, 119, 123, routed_scale=2.5),
+    # b0 = 0.45 puts the busiest expert at ~40 of the 64 tokens (calibrated
+    # once on this seed; the test asserts the resulting skew).
+    4: Config("c4_verify", 64, 7168, 2048, 384, 16, 2048, 119, 123, routed_scale=2.5,
+              zipf_b0=0.45),
     5: Config("c5_prefill", 2048, 7168, 2048, 384, 16, 2048, 119, 123, routed_scale=2.5),
 }
 
@@ -69,7 +77,14 @@ class SynthLayer:
         key = lambda kind, e=0: o.stream_key(c.seed, sid(kind, e))
         self.router = o.synth_normal(key(STREAM_ROUTER), c.experts * c.hidden,
                                      c.router_sigma).reshape(c.experts, c.hidden)
-        self.bias = o.synth_normal(key(STREAM_BIAS), c.experts, c.bias_sigma)
+        if c.zipf_b0 > 0:
+            # Zipf(s) over a seeded permutation of the expert ids: rank(e) is
+            # the 1-based position of e when a seeded normal draw is sorted.
+            u = o.synth_normal(key(STREAM_ZIPF_RANK), c.experts, 1.0)
+            rank = np.argsort(np.argsort(u, kind="stable"), kind="stable") + 1
+            self.bias = (c.zipf_b0 * rank.astype(np.float64) ** -c.zipf_s).astype(np.float32)
+        else:
+            self.bias = o.synth_normal(key(STREAM_BIAS), c.experts, c.bias_sigma)
         self.gamma = np.ones(c.hidden, np.float32)
         self.shared = None
         if c.shared_inter:

@@ -1,6 +1,6 @@
 """GPU parity of the HIP MoE layer against the CPU oracle (through the C ABI).
 
-Standards:
+Standards of the layer contract:
 * bit-exact: dequantised weights (fp32 bits, including -0.0 and overflow),
   RMSNorm output, router logits, Top-K ids and weights, expert-major CSR and
   first-use order;
@@ -112,7 +112,7 @@ def test_upload_rejects_reserved_scale(hip):
 
 
 # ---------------------------------------------------------------------------
-# Full layer on the seeded BASELINE configurations.
+# Full layer on the seeded benchmark configurations.
 # ---------------------------------------------------------------------------
 def run_layer(k3x_amd, ctx, cfg, bank, x_bits):
     dev = "cuda:0"
