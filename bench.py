@@ -142,6 +142,12 @@ def main() -> int:
         "shared_gate_up": SHARED_GU_BYTES,
         "shared_down": SHARED_DOWN_BYTES,
         "route": ROUTER_BYTES + T * H * 2,
+        # decode path: front = router + shared gate/up; gate_up = routed
+        # gate/up + shared down; down = routed down (+ combine reads).
+        "decode_front": ROUTER_BYTES + SHARED_GU_BYTES + T * H * 2,
+        "decode_select": SHARED_DOWN_BYTES,
+        "decode_gate_up": mean_d * GATE_UP_BYTES + T * H * 2,
+        "decode_down": mean_d * DOWN_BYTES,
     }
     stage_report = {}
     for name, (ms, n) in stages.items():
@@ -152,7 +158,8 @@ def main() -> int:
         if name in stage_bytes:
             entry["gbps"] = round(stage_bytes[name] / (avg_us * 1e-6) / 1e9, 1)
         stage_report[name] = entry
-    dom = max(("gate_up", "down", "shared_gate_up", "shared_down"),
+    dom = max(("gate_up", "down", "shared_gate_up", "shared_down", "decode_front",
+               "decode_select", "decode_gate_up", "decode_down"),
               key=lambda s: stage_report.get(s, {}).get("avg_us", 0.0))
     dom_us = stage_report[dom]["avg_us"]
     achieved = stage_bytes[dom] / (dom_us * 1e-6) / 1e9
@@ -182,7 +189,7 @@ def main() -> int:
         "hbm_frac_all": round(all_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "profiled_us_per_layer": round(prof_elapsed / args.steps * 1e6, 3),
         "stages": stage_report,
-        "roofline": {"bound": "hbm", "kernel": f"expert_gemm ({dom})",
+        "roofline": {"bound": "hbm", "kernel": dom,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
     }

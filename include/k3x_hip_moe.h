@@ -98,7 +98,15 @@ typedef struct k3x_hip_moe_params {
     uint32_t has_situ_linear; /* SiTU only */
     float situ_linear_beta;   /* > 0 when has_situ_linear */
     uint32_t renorm;          /* enum k3x_renorm */
+    uint32_t flags;           /* K3X_FLAG_* */
 } k3x_hip_moe_params;
+
+/* k3x_hip_moe_params.flags */
+enum k3x_flags {
+    /* Use the general multi-launch path even where the three-launch decode
+     * path (tokens <= 4) applies; both compute the same layer. */
+    K3X_FLAG_GENERAL_PATH = 1u,
+};
 
 /* Optional device buffers that receive intermediates of k3x_hip_moe_forward;
  * any member may be NULL.  Shapes use T = tokens, K = top_k, E = experts,
@@ -119,6 +127,7 @@ typedef struct k3x_hip_moe_taps {
     float* expert_out;           /* [T][K][H] per-pair down projections */
     float* shared_out;           /* [T][H] shared expert output */
     float* out_f32;              /* [T][H] output before the bf16 cast */
+    uint16_t* shared_act;        /* [T][S] bf16 bits, shared-expert GLU output */
 } k3x_hip_moe_taps;
 
 /* Descriptor of the seeded synthetic bank (no reference counterpart: the
@@ -144,7 +153,12 @@ enum k3x_stage {
     K3X_STAGE_DOWN = 4,         /* routed MXFP4 down projection */
     K3X_STAGE_SHARED_DOWN = 5,
     K3X_STAGE_COMBINE = 6,      /* slot-ordered mix + shared add + bf16 cast */
-    K3X_STAGE_COUNT = 7,
+    /* Decode path (T <= 4); its combine is K3X_STAGE_COMBINE. */
+    K3X_STAGE_DECODE_FRONT = 7,   /* RMSNorm, router logits, shared gate/up */
+    K3X_STAGE_DECODE_SELECT = 8,  /* Top-K, grouping, shared down */
+    K3X_STAGE_DECODE_GATE_UP = 9, /* routed gate/up + GLU */
+    K3X_STAGE_DECODE_DOWN = 10,   /* routed down */
+    K3X_STAGE_COUNT = 11,
 };
 
 /* Counters, after BackendRuntimeStats (runtime/include/k3x/backend.hpp:50-129). */
@@ -162,6 +176,8 @@ typedef struct k3x_hip_stats {
 /* Replaces make_cuda_backend (runtime/include/k3x/backend.hpp:465-466;
  * runtime/cuda/backend_cuda.cu:5264-5367): one device, one stream. */
 int k3x_hip_ctx_create(int device, k3x_hip_ctx** out);
+/* Fails with K3X_ERR_INVALID_STATE while banks created on the context are
+ * alive: destroy them first. */
 int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx);
 /* Enqueue on a caller-owned hipStream_t (NULL = the device's null stream). */
 int k3x_hip_ctx_set_stream(k3x_hip_ctx* ctx, void* hip_stream);

@@ -345,15 +345,19 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
     auto* ctx = new (std::nothrow) k3x_hip_ctx();
     if (!ctx) return K3X_ERR_BACKEND_UNAVAILABLE;
     ctx->device = device;
+    int lds = 0;
     if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
-        hipMemset(ctx->status, 0, 256) != hipSuccess) {
+        hipMemset(ctx->status, 0, 256) != hipSuccess ||
+        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
+            hipSuccess) {
         (void)hipGetLastError();
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
         if (ctx->status) (void)hipFree(ctx->status);
         delete ctx;
         return K3X_ERR_BACKEND_UNAVAILABLE;
     }
+    ctx->max_lds_per_block = (size_t)lds;
     ctx->stream = ctx->own_stream;
     *out = ctx;
     return K3X_OK;
@@ -361,6 +365,7 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
 
 int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     if (!ctx) return K3X_ERR_INVALID_EXTENT;
+    if (ctx->live_banks) return K3X_ERR_INVALID_STATE;  // destroy the banks first
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
@@ -477,6 +482,7 @@ int k3x_hip_bank_create(k3x_hip_ctx* ctx, const k3x_hip_layer_desc* desc, k3x_hi
         return st;
     }
     b->expert_ready.assign(E, 0);
+    ++ctx->live_banks;
     *out = b;
     return K3X_OK;
 }
@@ -486,6 +492,7 @@ int k3x_hip_bank_destroy(k3x_hip_bank* bank) {
     (void)hipSetDevice(bank->ctx->device);
     (void)hipStreamSynchronize(bank->ctx->stream);
     free_bank_memory(bank);
+    --bank->ctx->live_banks;
     delete bank;
     return K3X_OK;
 }

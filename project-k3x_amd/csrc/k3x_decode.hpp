@@ -1,0 +1,24 @@
+// k3x_decode.hpp -- the decode path (T <= kMaxDecodeTokens) of the layer.
+#pragma once
+
+#include "k3x_internal.hpp"
+
+namespace k3x_hip {
+
+constexpr int kMaxDecodeTokens = 4;
+
+// Whether the three-launch decode path handles this call.
+bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
+                     const k3x_hip_moe_params* p, const void* x);
+
+// RMSNorm, routing, grouping, experts, shared expert and combine of one
+// decode call; x is the raw bf16 input [T][H].  Asynchronous.
+int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                   const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32);
+
+// out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
+// + shared[t][h]) on the context stream (the combine of both paths).
+int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
+                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32);
+
+}  // namespace k3x_hip

@@ -22,12 +22,14 @@ struct k3x_hip_ctx {
     hipStream_t stream = nullptr;
     hipStream_t own_stream = nullptr;
     uint32_t* status = nullptr;  // device word, latched kernel errors
+    size_t max_lds_per_block = 65536;
     // Grow-only scratch (replaces runtime/cuda/device_memory.cuh:44-61).
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     uint64_t forward_calls = 0;
     uint64_t kernel_launches = 0;
     uint64_t weight_h2d_bytes = 0;
+    uint32_t live_banks = 0;  // banks created on this context and not destroyed
     // Stage profiling (k3x_hip_ctx_set_profiling).
     bool profiling = false;
     std::vector<StageMark> pending;      // recorded, not yet read back
@@ -77,6 +79,28 @@ struct k3x_hip_bank {
 };
 
 namespace k3x_hip {
+
+// Per-call device buffers of one forward call, carved from the context
+// scratch.  Shapes: T tokens, K slots, P = T*K pairs, E experts, H hidden,
+// I expert inter, S shared inter.
+struct LayerBuffers {
+    uint16_t* xn;          // [T][H] bf16, normalised input
+    float* logits;         // [T][E]
+    uint32_t* ids;         // [T][K]
+    float* weights;        // [T][K]
+    uint32_t* counts;      // [E]
+    uint32_t* offsets;     // [E+1]
+    uint32_t* pair_token;  // [P] CSR rows
+    uint32_t* pair_slot;   // [P]
+    uint32_t* first_use;   // [E]
+    uint32_t* n_active;    // [1]
+    uint32_t* active_asc;  // [E]
+    uint32_t* active_fu;   // [E]
+    uint16_t* act;         // [P][I] bf16, CSR row order
+    float* y;              // [T][K][H] per-pair down projections
+    uint16_t* sact;        // [T][S] bf16 shared activation
+    float* sy;             // [T][H] shared expert output
+};
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }
 

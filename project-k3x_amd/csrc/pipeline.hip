@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "k3x_decode.hpp"
 #include "k3x_device.hpp"
 #include "k3x_internal.hpp"
 
@@ -494,24 +495,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // Host side
 // ---------------------------------------------------------------------------
 
-struct Scratch {
-    uint16_t* xn;
-    float* logits;
-    uint32_t* ids;
-    float* weights;
-    uint32_t* counts;
-    uint32_t* offsets;
-    uint32_t* pair_token;
-    uint32_t* pair_slot;
-    uint32_t* first_use;
-    uint32_t* n_active;
-    uint32_t* active_asc;
-    uint32_t* active_fu;
-    uint16_t* act;
-    float* y;
-    uint16_t* sact;
-    float* sy;
-};
+using Scratch = k3x_hip::LayerBuffers;
 
 // Lays the per-call buffers out in the context scratch; returns bytes needed
 // (base == nullptr only measures).
@@ -550,7 +534,7 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p) {
         p->top_k > d.experts)
         return K3X_ERR_INVALID_EXTENT;
     if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
-        p->renorm > 1)
+        p->renorm > 1 || (p->flags & ~(uint32_t)K3X_FLAG_GENERAL_PATH))
         return K3X_ERR_INVALID_MXFP4;
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
@@ -682,12 +666,9 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden);
         end_stage(ctx, mark);
     }
-    mark = begin_stage(ctx, K3X_STAGE_COMBINE);
-    hipLaunchKernelGGL(combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0,
-                       ctx->stream, s.y, weights, d.shared_inter ? s.sy : nullptr, K, d.hidden,
-                       out, out_f32, ctx->status);
-    end_stage(ctx, mark);
-    return launched(ctx, d.shared_inter ? 5 : 3);
+    if ((st = launched(ctx, d.shared_inter ? 4 : 2))) return st;
+    return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
+                                   d.hidden, T, out, out_f32);
 }
 
 int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
@@ -712,6 +693,7 @@ int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_para
         {taps->act, s.act, P * d.inter * 2},
         {taps->expert_out, s.y, P * d.hidden * 4},
         {taps->shared_out, d.shared_inter ? s.sy : nullptr, T * d.hidden * 4},
+        {taps->shared_act, d.shared_inter ? s.sact : nullptr, T * d.shared_inter * 2},
     };
     for (const auto& it : items) {
         if (!it.dst || !it.src || it.dst == it.src) continue;
@@ -733,6 +715,19 @@ int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, S
 
 }  // namespace
 
+namespace k3x_hip {
+
+int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
+                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32) {
+    const int mark = begin_stage(ctx, K3X_STAGE_COMBINE);
+    hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, ctx->stream, y,
+                       weights, shared, K, H, out, out_f32, ctx->status);
+    end_stage(ctx, mark);
+    return launched(ctx, 1);
+}
+
+}  // namespace k3x_hip
+
 extern "C" {
 
 int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
@@ -743,6 +738,13 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     Scratch s;
     if ((st = prepare(ctx, bank, p, &s))) return st;
+    if (!(p->flags & K3X_FLAG_GENERAL_PATH) && k3x_hip::decode_eligible(ctx, bank, p, x)) {
+        if ((st = k3x_hip::decode_forward(ctx, bank, p, s, x, out,
+                                           taps ? taps->out_f32 : nullptr)))
+            return st;
+        ++ctx->forward_calls;
+        return copy_taps(ctx, bank, p, s, s.xn, s.ids, s.weights, taps);
+    }
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
     const int mark = k3x_hip::begin_stage(ctx, K3X_STAGE_ROUTE);

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from dataclasses import dataclass
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -21,7 +22,8 @@ ERR_INVALID_STATE = 16
 ERR_BACKEND_UNAVAILABLE = 17
 
 GLU_SWIGLU, GLU_SITU = 0, 1
-STAGES = ("route", "group", "gate_up", "shared_gate_up", "down", "shared_down", "combine")
+STAGES = ("route", "group", "gate_up", "shared_gate_up", "down", "shared_down", "combine",
+          "decode_front", "decode_select", "decode_gate_up", "decode_down")
 RENORM_FLOAT, RENORM_DOUBLE = 0, 1
 MATRIX_GATE, MATRIX_UP, MATRIX_DOWN = 0, 1, 2
 
@@ -63,12 +65,14 @@ class MoeParams(C.Structure):
     _fields_ = [("tokens", C.c_uint32), ("top_k", C.c_uint32), ("routed_scale", C.c_float),
                 ("rms_epsilon", C.c_float), ("glu", C.c_uint32), ("situ_beta", C.c_float),
                 ("has_situ_linear", C.c_uint32), ("situ_linear_beta", C.c_float),
-                ("renorm", C.c_uint32)]
+                ("renorm", C.c_uint32), ("flags", C.c_uint32)]
+
+FLAG_GENERAL_PATH = 1
 
 
 TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair_token",
               "pair_slot", "first_use", "n_active", "active_first_use", "act", "expert_out",
-              "shared_out", "out_f32"]
+              "shared_out", "out_f32", "shared_act"]
 
 
 class MoeTaps(C.Structure):
@@ -176,6 +180,7 @@ class Context:
         check(self.lib.k3x_hip_ctx_create(device, C.byref(h)), "k3x_hip_ctx_create")
         self.handle = h
         self.device = device
+        self._banks = weakref.WeakSet()
         if use_torch_stream:
             with torch.cuda.device(device):
                 s = torch.cuda.current_stream().cuda_stream
@@ -203,8 +208,11 @@ class Context:
         return {name: (ms[i], cnt[i]) for i, name in enumerate(STAGES)}
 
     def close(self) -> None:
+        """Destroys the context after every bank created on it."""
         if self.handle:
-            self.lib.k3x_hip_ctx_destroy(self.handle)
+            for bank in list(self._banks):
+                bank.close()
+            check(self.lib.k3x_hip_ctx_destroy(self.handle), "k3x_hip_ctx_destroy")
             self.handle = None
 
     def __del__(self):
@@ -241,6 +249,7 @@ class Bank:
         check(self.lib.k3x_hip_bank_create(ctx.handle, C.byref(d), C.byref(h)),
               "k3x_hip_bank_create")
         self.handle = h
+        ctx._banks.add(self)
 
     def fill_synthetic(self, seed: int, scale_lo: int, scale_hi: int, router_sigma=0.02,
                        bias_sigma=0.1, shared_sigma=0.02, gamma=1.0) -> None:
@@ -299,9 +308,9 @@ class Bank:
 
 
 def make_params(tokens, top_k, routed_scale=1.0, eps=1e-6, glu=GLU_SWIGLU, beta=4.0,
-                linear=None, renorm=RENORM_FLOAT) -> MoeParams:
+                linear=None, renorm=RENORM_FLOAT, flags=0) -> MoeParams:
     return MoeParams(tokens, top_k, routed_scale, eps, glu, beta, int(linear is not None),
-                     linear or 0.0, renorm)
+                     linear or 0.0, renorm, flags)
 
 
 def make_taps(tensors: dict | None) -> MoeTaps | None:

@@ -114,10 +114,12 @@ def test_upload_rejects_reserved_scale(hip):
 # ---------------------------------------------------------------------------
 # Full layer on the seeded benchmark configurations.
 # ---------------------------------------------------------------------------
-def run_layer(k3x_amd, ctx, cfg, bank, x_bits):
+def run_layer(k3x_amd, ctx, cfg, bank, x_bits, flags=0, per_pair=True, glu=None, linear=None):
+    """One forward call with taps.  per_pair=False skips the [T][K][H] expert
+    output tap (939 MB at T=2048)."""
     dev = "cuda:0"
     T, H, I, E, K = cfg.tokens, cfg.hidden, cfg.inter, cfg.experts, cfg.top_k
-    x = torch.from_numpy(x_bits.view(np.int16)).to(dev)
+    x = torch.from_numpy(np.ascontiguousarray(x_bits).view(np.int16)).to(dev)
     out = torch.empty((T, H), dtype=torch.int16, device=dev)
     z = lambda shape, dt: torch.empty(shape, dtype=dt, device=dev)
     taps = dict(normed_x=z((T, H), torch.int16), logits=z((T, E), torch.float32),
@@ -126,11 +128,15 @@ def run_layer(k3x_amd, ctx, cfg, bank, x_bits):
                 pair_token=z((T * K,), torch.int32), pair_slot=z((T * K,), torch.int32),
                 first_use=z((E,), torch.int32), n_active=z((1,), torch.int32),
                 active_first_use=z((E,), torch.int32), act=z((T * K, I), torch.int16),
-                expert_out=z((T, K, H), torch.float32), out_f32=z((T, H), torch.float32))
+                out_f32=z((T, H), torch.float32))
+    if per_pair:
+        taps["expert_out"] = z((T, K, H), torch.float32)
     if cfg.shared_inter:
         taps["shared_out"] = z((T, H), torch.float32)
-    params = k3x_amd.make_params(T, K, cfg.routed_scale, cfg.eps, cfg.glu, cfg.beta, cfg.linear,
-                                 cfg.renorm)
+        taps["shared_act"] = z((T, cfg.shared_inter), torch.int16)
+    params = k3x_amd.make_params(T, K, cfg.routed_scale, cfg.eps,
+                                 cfg.glu if glu is None else glu, cfg.beta,
+                                 cfg.linear if linear is None else linear, cfg.renorm, flags)
     st = k3x_amd.moe_forward(ctx, bank, params, x, out, taps)
     assert st == 0, st
     assert ctx.synchronize() == 0
@@ -139,27 +145,23 @@ def run_layer(k3x_amd, ctx, cfg, bank, x_bits):
     for k in ("ids", "counts", "offsets", "pair_token", "pair_slot", "first_use", "n_active",
               "active_first_use"):
         got[k] = got[k].view(np.uint32)
-    for k in ("normed_x", "act", "out"):
-        got[k] = got[k].view(np.uint16)
+    for k in ("normed_x", "act", "out", "shared_act"):
+        if k in got:
+            got[k] = got[k].view(np.uint16)
     return got
 
 
-def check_layer(oracle, layer, got, tokens_checked=None):
+def check_routing(oracle, layer, got, x_bits):
+    """RMSNorm, logits, Top-K ids and weights, grouping: all bit-exact."""
     cfg = layer.cfg
-    T, K, E = cfg.tokens, cfg.top_k, cfg.experts
-    x_bits = layer.x_bits()
-    # RMSNorm, bit-exact.
+    T, K, E = x_bits.shape[0], cfg.top_k, cfg.experts
     xn = layer.normed(x_bits)
     xn_bits = (xn.view(np.uint32) >> 16).astype(np.uint16)
     assert np.array_equal(got["normed_x"], xn_bits), "RMSNorm output differs"
-    say("rmsnorm bit-exact")
-    # Router logits, ids, weights: bit-exact.
     logits, ids, w = layer.route(xn)
     assert np.array_equal(got["logits"].view(np.uint32), logits.view(np.uint32)), "logits differ"
     assert np.array_equal(got["ids"], ids), "Top-K ids differ"
     assert np.array_equal(got["weights"].view(np.uint32), w.view(np.uint32)), "weights differ"
-    say("router logits / ids / weights bit-exact")
-    # Grouping: CSR + first-use order, bit-exact; same groups as the plan.
     st, csr = oracle.expert_major_csr(ids, E)
     assert st == 0
     for k in ("counts", "offsets", "first_use"):
@@ -173,12 +175,26 @@ def check_layer(oracle, layer, got, tokens_checked=None):
     st, plan = oracle.expert_major_plan(ids, w)
     assert st == 0
     assert np.array_equal(plan["group_expert"], csr["active_first_use"])
-    say(f"grouping bit-exact ({na} active experts)")
+    say(f"rmsnorm, logits, ids, weights, grouping bit-exact ({na} active experts)")
+    return xn, ids, w, csr
+
+
+def check_layer(oracle, layer, got, x_bits=None, tokens_checked=None):
+    cfg = layer.cfg
+    x_bits = layer.x_bits() if x_bits is None else x_bits
+    T, K = x_bits.shape[0], cfg.top_k
+    P = T * K
+    xn, ids, w, csr = check_routing(oracle, layer, got, x_bits)
     # Per-pair activations and outputs.
     tokens = range(T) if tokens_checked is None else tokens_checked
     act_ref, y_ref = layer.pair_outputs(xn, ids, tokens)
     act_gpu = got["act"]  # CSR rows
-    worst_act = 0
+    # Activations: the bf16 roundings of the GPU's fp32 sums and the oracle's
+    # double sums agree except near rounding boundaries (one ulp apart) and
+    # on values near zero, where the absolute accumulation error of gate/up
+    # (~2^-18 of the row's scale) spans more than one ulp; a layout or
+    # indexing error would be O(1) of the row's scale.
+    worst_act, multi = 0, 0
     for r in range(P):
         t, s = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
         if t not in tokens:
@@ -188,57 +204,132 @@ def check_layer(oracle, layer, got, tokens_checked=None):
         worst_act = max(worst_act, int(d.max()))
         frac = np.count_nonzero(d) / d.size
         assert frac < 0.02, f"pair ({t},{s}): {frac:.4f} of activations off"
-    assert worst_act <= 1, f"activation off by {worst_act} bf16 ulps"
-    say(f"activations within {worst_act} bf16 ulp")
-    # Down projection on the GPU's own activations (isolates the GEMM).
-    for r in range(P):
-        t, s = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
-        if t not in tokens:
-            continue
-        e = int(ids[t, s])
-        ex = layer.expert(e)
-        a = bf16_to_f32(act_gpu[r])
-        st, yd = oracle.mxfp4_matvec(a, ex["down_packed"], ex["down_scales"], cfg.hidden,
-                                     cfg.inter, 32)
-        np.testing.assert_allclose(got["expert_out"][t, s], yd, rtol=1e-4, atol=1e-4)
-    say("down projection matches on GPU activations")
-    # Against the fully independent CPU layer.
+        big = d > 1
+        multi += int(big.sum())
+        if big.any():
+            scale = float(np.abs(act_ref[t, s]).max())
+            diff = np.abs(bf16_to_f32(act_gpu[r]) - act_ref[t, s])[big]
+            assert (np.abs(act_ref[t, s][big]) <= 2.0 ** -6 * scale).all()
+            assert (diff <= 2.0 ** -12 * scale).all()
+    say(f"activations: max {worst_act} bf16 ulp, {multi} elements over 1 ulp (all near zero)")
+    if "expert_out" in got:
+        # Down projection on the GPU's own activations (isolates the GEMM).
+        for r in range(P):
+            t, s = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
+            if t not in tokens:
+                continue
+            ex = layer.expert(int(ids[t, s]))
+            a = bf16_to_f32(act_gpu[r])
+            st, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], cfg.hidden,
+                                        cfg.inter, 32)
+            yd = (W.astype(np.float64) @ a.astype(np.float64))
+            # fp32 accumulation over K terms: |error| <= K * 2^-24 * sum|a_k w_k|
+            # in the worst case; 2^-16 (K = 2048 -> 2^-13 worst, ~2^-18.5
+            # typical) flags any indexing or layout error, which is O(1).
+            bound = 2.0 ** -16 * (np.abs(W).astype(np.float64) @ np.abs(a).astype(np.float64))
+            err = np.abs(got["expert_out"][t, s].astype(np.float64) - yd)
+            assert (err <= bound + 1e-30).all(), f"pair ({t},{s}): max excess {(err - bound).max()}"
+        say("down projection within the fp32 accumulation bound on GPU activations")
+    # Against the fully independent CPU layer, element by element, with a
+    # bound that accounts for every source of difference: the activation
+    # elements whose bf16 rounding differs (GPU fp32 MFMA sums vs the
+    # oracle's double sums land on either side of a bf16 rounding boundary;
+    # each such element is one bf16 ulp apart, checked above), propagated
+    # through |W_down|; fp32 accumulation of the down projections (2^-15 of
+    # sum |w_rk a_k|; K = 2048 gives at most 2^-13, typically ~2^-18.5); and
+    # the float rounding of the slot-ordered combine on both sides.
     shared = layer.shared_out(xn, tokens)
-    if cfg.shared_inter:
-        for t in tokens:
-            np.testing.assert_allclose(got["shared_out"][t], shared[t], rtol=RTOL, atol=ATOL)
     out_ref = layer.combine(y_ref, w, shared, tokens)
+    row_of = {(int(csr["pair_token"][r]), int(csr["pair_slot"][r])): r for r in range(P)}
+    within = total = 0
+    u = 2.0 ** -24
     for t in tokens:
-        np.testing.assert_allclose(got["out_f32"][t], out_ref[t], rtol=RTOL, atol=ATOL)
-        ref_bits = bf16_bits(out_ref[t])
-        d = ulp_diff_bf16(got["out"][t], ref_bits)
-        near = np.abs(bf16_to_f32(got["out"][t]) - bf16_to_f32(ref_bits)) <= ATOL
-        bad = (d > 1) & ~near
-        assert not bad.any(), f"token {t}: {int(bad.sum())} bf16 outputs off by > 1 ulp"
-        say(f"token {t}: bf16 max ulp {int(d.max())} (all > 1 ulp within atol)")
-    # Combine on the GPU's own per-pair outputs: bit-exact.
-    comb = layer.combine(got["expert_out"], w,
-                         got["shared_out"] if cfg.shared_inter else np.zeros_like(got["out_f32"]))
-    assert np.array_equal(comb.view(np.uint32), got["out_f32"].view(np.uint32))
-    say("layer output within tolerance; ordered combine bit-exact")
+        bound = np.zeros(cfg.hidden)
+        mag = np.zeros(cfg.hidden)
+        for s_ in range(K):
+            ex = layer.expert(int(ids[t, s_]))
+            _, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], cfg.hidden,
+                                       cfg.inter, 32)
+            Wa = np.abs(W).astype(np.float64)
+            a_gpu = bf16_to_f32(act_gpu[row_of[(t, s_)]]).astype(np.float64)
+            da = np.abs(a_gpu - act_ref[t, s_].astype(np.float64))
+            ws = abs(float(w[t, s_]))
+            bound += ws * (Wa @ da + 2.0 ** -15 * (Wa @ np.abs(a_gpu)))
+            mag += ws * np.abs(y_ref[t, s_].astype(np.float64))
+        if cfg.shared_inter:
+            from oracle import GLU_SWIGLU
+            sg, su, sd = layer.shared
+            sa_ref = round_bf16_np(oracle, xn[t], sg, su, cfg)
+            sa_gpu = bf16_to_f32(got["shared_act"][t]).astype(np.float64)
+            dsa = np.abs(sa_gpu - sa_ref)
+            assert ulp_diff_bf16(got["shared_act"][t], bf16_bits(sa_ref.astype(np.float32))).max() <= 1
+            Wd = np.abs(bf16_to_f32(sd)).astype(np.float64)
+            bound += Wd @ dsa + 2.0 ** -15 * (Wd @ np.abs(sa_gpu))
+            mag += np.abs(shared[t].astype(np.float64))
+            np.testing.assert_array_less(
+                np.abs(got["shared_out"][t] - shared[t]) - (Wd @ dsa + 2.0 ** -15 * (Wd @ np.abs(sa_gpu))),
+                1e-30 + 4 * u * np.abs(shared[t]))
+        bound += 2 * (K + 1) * u * mag + 2 * u * np.abs(out_ref[t])
+        err = np.abs(got["out_f32"][t].astype(np.float64) - out_ref[t])
+        assert (err <= bound).all(), f"token {t}: {int((err > bound).sum())} outputs beyond the bound"
+        ok = np.abs(got["out_f32"][t] - out_ref[t]) <= ATOL + RTOL * np.abs(out_ref[t])
+        within += int(ok.sum())
+        total += ok.size
+        assert np.array_equal(got["out"][t], bf16_bits(got["out_f32"][t]))
+    frac = within / total
+    say(f"{len(tokens)} tokens within the propagated bound; {frac:.5f} of outputs within "
+        f"rtol {RTOL} / atol {ATOL}")
+    assert frac >= 0.99
+    if "expert_out" in got:
+        # Combine on the GPU's own per-pair outputs: bit-exact.
+        sh = got["shared_out"] if cfg.shared_inter else np.zeros_like(got["out_f32"])
+        comb = layer.combine(got["expert_out"], w, sh)
+        assert np.array_equal(comb.view(np.uint32), got["out_f32"].view(np.uint32))
+        say("ordered combine bit-exact")
 
 
-def make_bank(k3x_amd, ctx, cfg):
+def round_bf16_np(oracle, xn, gate, up, cfg):
+    """The oracle's shared-expert activation bf16(GLU(gate xn, up xn))."""
+    from oracle import round_bf16
+    g = oracle.bf16_matvec(xn, gate)
+    u = oracle.bf16_matvec(xn, up)
+    a = oracle.glu(g, u, cfg.glu, cfg.beta, cfg.linear)
+    return round_bf16(a).astype(np.float64)
+
+
+def make_bank(k3x_amd, ctx, cfg, layer=None):
     shape = k3x_amd.LayerShape(cfg.hidden, cfg.inter, cfg.experts, cfg.shared_inter)
     bank = k3x_amd.Bank(ctx, shape)
     bank.fill_synthetic(cfg.seed, cfg.scale_lo, cfg.scale_hi, cfg.router_sigma, cfg.bias_sigma,
                         cfg.shared_sigma, 1.0)
+    if cfg.zipf_b0 > 0:
+        assert bank.upload_router(layer.router, layer.bias, layer.gamma) == 0
     return bank
 
 
+@pytest.fixture(scope="module")
+def c3(hip, oracle):
+    from synth import CONFIGS, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = CONFIGS[3]
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    yield cfg, layer, bank
+    bank.close()
+
+
 @pytest.mark.parametrize("cid", [1, 3])
-def test_layer_parity(hip, oracle, cid):
+@pytest.mark.parametrize("general", [False, True], ids=["decode_path", "general_path"])
+def test_layer_parity(hip, oracle, cid, general, c3):
     from synth import CONFIGS, SynthLayer
     k3x_amd, ctx = hip
     cfg = CONFIGS[cid]
-    say(f"layer parity config {cid} ({cfg.name}) T={cfg.tokens} E={cfg.experts}")
-    bank = make_bank(k3x_amd, ctx, cfg)
-    layer = SynthLayer(oracle, cfg)
+    say(f"layer parity config {cid} ({cfg.name}) T={cfg.tokens} general={general}")
+    if cid == 3:
+        _, layer, bank = c3
+    else:
+        layer = SynthLayer(oracle, cfg)
+        bank = make_bank(k3x_amd, ctx, cfg)
     # Synthetic fill is bit-identical to the CPU generator (sampled rows).
     for e in (0, cfg.experts - 1):
         ex = layer.expert(e)
@@ -246,6 +337,148 @@ def test_layer_parity(hip, oracle, cid):
                                        ex["down_scales"][: 4 * cfg.inter // 32], 4, cfg.inter)
         got = to_np(bank.dequant_rows(e, 2, 0, 4))
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-    got = run_layer(k3x_amd, ctx, cfg, bank, layer.x_bits())
+    flags = k3x_amd.FLAG_GENERAL_PATH if general else 0
+    got = run_layer(k3x_amd, ctx, cfg, bank, layer.x_bits(), flags)
     check_layer(oracle, layer, got)
+    if cid != 3:
+        bank.close()
+
+
+def close_paths(a, b):
+    """Two fp32 results that differ in fp32 summation orders and, through
+    those, in a few bf16 activation roundings on each side: within 2^-10 of
+    each other in norm and element-wise within the layer tolerance on >= 97%
+    of elements (the misses are small outputs where a flipped activation
+    rounding is a large relative change; each path is checked element by
+    element against the oracle with a propagated bound in check_layer)."""
+    ok = np.abs(a - b) <= ATOL + RTOL * np.abs(b)
+    assert ok.mean() >= 0.97
+    assert np.linalg.norm(a - b) <= 2.0 ** -10 * np.linalg.norm(b)
+
+
+def close_acts(a, b):
+    """bf16 activations of two paths whose fp32 sums differ in order: equal
+    or one ulp apart except on values near zero (see check_layer)."""
+    d = ulp_diff_bf16(a, b)
+    assert np.count_nonzero(d) / d.size < 0.02
+    big = d > 1
+    if big.any():
+        fa, fb = bf16_to_f32(a).astype(np.float64), bf16_to_f32(b).astype(np.float64)
+        scale = np.abs(fb).max(axis=-1, keepdims=True) * np.ones_like(fb)
+        assert (np.abs(fb[big]) <= 2.0 ** -6 * scale[big]).all()
+        assert (np.abs(fa - fb)[big] <= 2.0 ** -12 * scale[big]).all()
+
+
+def test_decode_and_general_paths_agree(hip, c3):
+    """Both paths: normalisation, routing and grouping bit-identical; the
+    activations, per-pair outputs, shared expert and output agree to the
+    rounding of their different fp32 summation orders (the decode path splits
+    K ranges over waves)."""
+    k3x_amd, ctx = hip
+    cfg, layer, bank = c3
+    x = layer.x_bits()
+    a = run_layer(k3x_amd, ctx, cfg, bank, x, 0)
+    b = run_layer(k3x_amd, ctx, cfg, bank, x, k3x_amd.FLAG_GENERAL_PATH)
+    for k in ("normed_x", "logits", "ids", "weights", "counts", "offsets", "first_use",
+              "n_active", "active_first_use", "pair_token", "pair_slot"):
+        assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
+    close_acts(a["act"], b["act"])
+    close_acts(a["shared_act"], b["shared_act"])
+    close_paths(a["expert_out"], b["expert_out"])
+    close_paths(a["shared_out"], b["shared_out"])
+    close_paths(a["out_f32"], b["out_f32"])
+
+
+def test_repeated_decode_calls(hip, oracle, c3):
+    """Back-to-back decode calls with different inputs (the router ticket and
+    the combine counters must return to zero after every call), including a
+    T=1 call: each call's routing and grouping bit-exact, its output equal to
+    the general path's."""
+    from synth import sid, STREAM_INPUT
+    k3x_amd, ctx = hip
+    cfg, layer, bank = c3
+    import dataclasses
+    for i, T in enumerate((2, 2, 1, 2, 1)):
+        x = oracle.synth_normal_bf16(oracle.stream_key(cfg.x_seed + 100 + i, sid(STREAM_INPUT)),
+                                     T * cfg.hidden, 1.0).reshape(T, cfg.hidden)
+        c = dataclasses.replace(cfg, tokens=T)
+        a = run_layer(k3x_amd, ctx, c, bank, x, 0, per_pair=False)
+        b = run_layer(k3x_amd, ctx, c, bank, x, k3x_amd.FLAG_GENERAL_PATH, per_pair=False)
+        check_routing(oracle, layer, a, x)
+        close_acts(a["act"][: T * cfg.top_k], b["act"][: T * cfg.top_k])
+        close_paths(a["out_f32"], b["out_f32"])
+        say(f"call {i} (T={T}) ok")
+
+
+def test_decode_deterministic(hip, c3):
+    k3x_amd, ctx = hip
+    cfg, layer, bank = c3
+    x = layer.x_bits()
+    a = run_layer(k3x_amd, ctx, cfg, bank, x, 0, per_pair=False)
+    b = run_layer(k3x_amd, ctx, cfg, bank, x, 0, per_pair=False)
+    for k in a:
+        assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
+
+
+def test_c1_situ_against_reference_golden(hip, oracle):
+    """Config 1 with SiTU (beta 4, linear 25): device ids equal the ids the
+    reference's own CPU functions chose (tests/golden/c1_layer.npz), and the
+    output is within the bf16 contract's bound of the reference output."""
+    import os
+    from synth import CONFIGS, SynthLayer
+    from oracle import GLU_SITU
+    k3x_amd, ctx = hip
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "c1_layer.npz"))
+    cfg = CONFIGS[1]
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    import dataclasses
+    c8 = dataclasses.replace(cfg, tokens=8)
+    got = run_layer(k3x_amd, ctx, c8, bank, g["x_bits"], 0, glu=GLU_SITU, linear=25.0)
+    assert np.array_equal(got["ids"], g["ids"])
+    for t in range(8):
+        ref = g["out_situ_linear"][t]
+        assert np.linalg.norm(got["out_f32"][t] - ref) <= 2.0 ** -7 * np.linalg.norm(ref)
+    bank.close()
+
+
+def test_c4_verification_window(hip, oracle):
+    """Config 4: T=64, Zipf-skewed routing (0..~40 rows per expert).  Routing
+    and grouping bit-exact for all 1024 pairs; activations and outputs on a
+    sample of tokens."""
+    from synth import CONFIGS, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = CONFIGS[4]
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg, layer)
+    got = run_layer(k3x_amd, ctx, cfg, bank, layer.x_bits())
+    counts = got["counts"]
+    say(f"c4 rows per expert: max {counts.max()}, active {int((counts > 0).sum())}")
+    assert counts.max() >= 30
+    check_layer(oracle, layer, got, tokens_checked=[0, 17, 63])
+    bank.close()
+
+
+def test_c5_prefill_chunk(hip, oracle):
+    """Config 5: T=2048 prefill chunk.  Device Top-16 ids equal the ids the
+    reference's CPU functions chose (golden fixture); grouping bit-exact;
+    outputs on sampled tokens; permuting the tokens permutes the output bit
+    for bit (rows of the grouped GEMMs are independent)."""
+    import os
+    from synth import CONFIGS, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = CONFIGS[5]
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    x = layer.x_bits()
+    got = run_layer(k3x_amd, ctx, cfg, bank, x, per_pair=False)
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "routes_c5.npz"))
+    assert np.array_equal(got["ids"], g["ids"].astype(np.uint32))
+    say("c5 ids equal the reference's")
+    check_layer(oracle, layer, got, x, tokens_checked=[0, 1000, 2047])
+    perm = np.random.default_rng(5).permutation(cfg.tokens)
+    gp = run_layer(k3x_amd, ctx, cfg, bank, x[perm], per_pair=False)
+    assert np.array_equal(gp["out"], got["out"][perm])
+    assert np.array_equal(gp["out_f32"].view(np.uint32), got["out_f32"][perm].view(np.uint32))
+    say("c5 token permutation equivariance bit-exact")
     bank.close()
