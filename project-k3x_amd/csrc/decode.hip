@@ -1,26 +1,37 @@
-// decode.hip -- the decode path of the MoE layer (T <= 4 tokens), five
-// launches with no cross-workgroup synchronisation inside any of them:
+// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): six
+// launches on two streams, no cross-workgroup synchronisation inside any of
+// them.
 //
-//   decode_front_kernel   every block rebuilds xn = bf16(RMSNorm(x) * gamma)
-//                         in LDS.  Router blocks stream the fp32 router (one
-//                         wave per expert row, fp64, canonical order) into
-//                         logits; shared blocks run the bf16 shared-expert
-//                         gate/up + GLU with the K range split over 8 waves.
-//   decode_select_kernel  block 0: sigmoid + bias Top-K of every token and the
-//                         expert-major grouping; the other blocks run the
-//                         shared down projection (K split over 8 waves), so
-//                         the selection's latency hides behind that stream.
-//   decode_gateup_kernel  routed MXFP4 gate/up + GLU per active expert: four
-//                         16-row blocks per workgroup, K split over two waves
-//                         each, weights dequantised in registers.
-//   decode_down_kernel    routed MXFP4 down projection to per-pair fp32 rows.
-//   combine (pipeline.hip) out = bf16(sum over slots in router order of
-//                         w * y + shared).
+// Context stream (the routing chain):
+//   decode_router_kernel  every block rebuilds xn = bf16(RMSNorm(x) * gamma)
+//                         in LDS and streams the fp32 router, one wave per
+//                         expert row (fp64, canonical order), into logits.
+//   decode_select_kernel  sigmoid + bias Top-K of every token and the
+//                         expert-major grouping (one block).
+//   decode_gateup_kernel  routed MXFP4 gate/up + GLU per active expert, four
+//                         16-row blocks per workgroup (K split over two waves
+//                         when the extra waves still fit on the device at
+//                         once), weights dequantised in registers.
+//   decode_down_kernel    one workgroup per 16 output rows: its waves take
+//                         the active experts in turn (MXFP4 down projection
+//                         of each expert's pairs into LDS), then the block
+//                         forms out = bf16(sum over slots in router order of
+//                         w * y + shared) for its rows.
+// Side stream (the shared expert, which needs only xn):
+//   decode_shared_gateup_kernel  bf16 shared gate/up + GLU, one 16-row block
+//                         of S per workgroup, K split over 16 waves.
+//   decode_shared_down_kernel    bf16 shared down, one 16-row block of H per
+//                         workgroup, K split over four waves.
+// The side stream forks from the context stream at entry and joins it before
+// decode_down_kernel, so its ~90 MB stream overlaps the router and Top-K
+// steps, which leave most of the device idle.
 //
-// Numerics are identical to the general path in pipeline.hip: the same
-// canonical fp64 order for the RMS sum and the router logits, the same
-// Top-K keys and renormalisation, the same per-accumulator MFMA order for
-// the routed experts, the same slot-ordered combine.
+// The streaming loops keep one weight tile in flight per wave and few
+// registers, so that eight waves fit on each SIMD: for these HBM streams
+// the number of resident waves matters more than per-wave prefetch depth.
+// Numerics: the same canonical fp64 order for the RMS sum and the router
+// logits as the general path, the same Top-K keys and renormalisation, the
+// same slot-ordered combine; fp32 MFMA accumulation for the projections.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -55,13 +66,24 @@ __device__ inline uint64_t topk_key(float adj, uint32_t e) {
     return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - e);
 }
 
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint64_t o = __shfl_xor(v, d);
-        v = o > v ? o : v;
-    }
-    return v;
+// Maximum of v over the 64 lanes with DPP moves (quad permutes, row
+// rotates, row broadcasts): VALU latency instead of LDS-crossbar shuffles.
+// Rows not selected by a row_bcast keep their own value (max(v, v) = v).
+template <int Ctrl, int RowMask>
+__device__ inline uint32_t dpp_max_step(uint32_t x) {
+    const uint32_t y =
+        (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, Ctrl, RowMask, 0xf, false);
+    return x > y ? x : y;
+}
+
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+    v = dpp_max_step<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x124, 0xf>(v);  // row_ror:4
+    v = dpp_max_step<0x128, 0xf>(v);  // row_ror:8
+    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // Canonical combination of one lane's four partial sums (partials 4l..4l+3
@@ -98,56 +120,57 @@ __device__ inline uint32_t block_scan_excl(uint32_t v, uint32_t* wave_sums, uint
 }
 
 // ---------------------------------------------------------------------------
-// Front kernel: xn, router logits, shared gate/up
+// MXFP4 step helpers: one 128-K tile of S 16-row blocks (codes [S][64] x
+// 16 B, one E8M0 byte per lane per block), dequantised in registers and
+// multiplied by the activation slice av[4] (K = 32g + 8j .. +7 of the tile).
 // ---------------------------------------------------------------------------
-struct FrontArgs {
-    const uint16_t* x;
-    const float* gamma;
-    const float* router_w;
-    uint32_t T, H, E, S;
-    float eps;
-    uint32_t router_blocks;
-    const uint4* sh_gu;  // shared gate/up tiles [S/16][H/128][2][4][64] x 16 B
-    GluParams glu;
-    uint16_t* xn;        // [T][H] global copy (block 0 writes it)
-    float* logits;       // [T][E]
-    uint16_t* sact;      // [T][S] shared-expert activation
-    uint32_t* status;
-};
+__device__ inline f32x4 mxfp4_tile(const uint4& c, float scale, const uint4 av[4], f32x4 acc) {
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(av[j]), dequant8(cw[j], scale), acc);
+    return acc;
+}
 
-struct FrontShared {
+__device__ inline void load_act(const uint16_t* ap, bool arow, uint32_t k, uint4 av[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        av[j] = arow ? *reinterpret_cast<const uint4*>(ap + k * 128 + 8 * j) : make_uint4(0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// xn prologue of the router and shared gate/up kernels
+// ---------------------------------------------------------------------------
+struct NormShared {
     float inv[kMaxDecodeTokens];
     int bad;
-    f32x4 red[kFrontWaves][2][64];  // shared blocks: split-K partials
 };
 
-__global__ __launch_bounds__(kFrontThreads) void decode_front_kernel(FrontArgs a) {
-    extern __shared__ uint4 dyn_lds[];
-    uint16_t* s_x = reinterpret_cast<uint16_t*>(dyn_lds);  // [T][H]
-    __shared__ FrontShared sh;
-    if (*(volatile uint32_t*)a.status) return;
+// x -> LDS (16-byte chunks), inverse RMS per token from the sum of squares in
+// the canonical fp64 order, then xn = bf16(x * inv * gamma) in place; the
+// block then holds xn as [T][H] bf16 at s_x4.  Returns false when x holds a
+// non-finite value (latched into *status when status is non-null).  Needs
+// at least T waves; xn_out, when non-null, receives a global copy.
+template <int kThreads>
+__device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, uint32_t T, uint32_t H, float eps,
+                         uint4* s_x4, NormShared& ns, uint16_t* xn_out, uint32_t* status) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t T = a.T, H = a.H;
-
-    // -- 1. x -> LDS in 16-byte chunks; T*H/8 <= 3584 chunks. --------------
-    if (tid == 0) sh.bad = 0;
+    const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
+    if (tid == 0) ns.bad = 0;
     const uint32_t chunks = T * H / 8;
-    {
-        constexpr int kMaxIt = (kMaxDecodeTokens * 7168 / 8 + kFrontThreads - 1) / kFrontThreads;
-        uint4 v[kMaxIt];
+    for (uint32_t c0 = 0; c0 < chunks; c0 += 4 * kThreads) {
+        uint4 v[4];
 #pragma unroll
-        for (int it = 0; it < kMaxIt; ++it) {
-            const uint32_t c = tid + kFrontThreads * it;
-            if (c < chunks) v[it] = reinterpret_cast<const uint4*>(a.x)[c];
+        for (int it = 0; it < 4; ++it) {
+            const uint32_t c = c0 + tid + kThreads * it;
+            v[it] = c < chunks ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int it = 0; it < kMaxIt; ++it) {
-            const uint32_t c = tid + kFrontThreads * it;
-            if (c < chunks) dyn_lds[c] = v[it];
+        for (int it = 0; it < 4; ++it) {
+            const uint32_t c = c0 + tid + kThreads * it;
+            if (c < chunks) s_x4[c] = v[it];
         }
     }
     __syncthreads();
-    // -- 2. sum of squares in the canonical order; inverse RMS per token. ---
     if (wave < T) {
         const uint16_t* xr = s_x + (size_t)wave * H;
         double p[4] = {0.0, 0.0, 0.0, 0.0};
@@ -164,23 +187,22 @@ __global__ __launch_bounds__(kFrontThreads) void decode_front_kernel(FrontArgs a
         const double s = canon_reduce(p);
         bad = __any(bad);
         if (lane == 0) {
-            if (bad) sh.bad = 1;
+            if (bad) ns.bad = 1;
             const float mean = (float)__ddiv_rn(s, (double)H);
-            sh.inv[wave] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+            ns.inv[wave] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
         }
     }
     __syncthreads();
-    if (sh.bad) {
-        if (tid == 0) latch(a.status, K3X_ERR_INVALID_MXFP4);
-        return;
+    if (ns.bad) {
+        if (status && tid == 0) latch(status, K3X_ERR_INVALID_MXFP4);
+        return false;
     }
-    // -- 3. xn = bf16(x * inv * gamma) in place. ---------------------------
-    for (uint32_t c = tid; c < chunks; c += kFrontThreads) {
+    for (uint32_t c = tid; c < chunks; c += kThreads) {
         const uint32_t t = (c * 8) / H, k = (c * 8) % H;
-        const uint4 w = dyn_lds[c];
-        const float4 g0 = *reinterpret_cast<const float4*>(a.gamma + k);
-        const float4 g1 = *reinterpret_cast<const float4*>(a.gamma + k + 4);
-        const float inv = sh.inv[t];
+        const uint4 w = s_x4[c];
+        const float4 g0 = *reinterpret_cast<const float4*>(gamma + k);
+        const float4 g1 = *reinterpret_cast<const float4*>(gamma + k + 4);
+        const float inv = ns.inv[t];
         const uint32_t in[4] = {w.x, w.y, w.z, w.w};
         const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         uint32_t o[4];
@@ -192,68 +214,146 @@ __global__ __launch_bounds__(kFrontThreads) void decode_front_kernel(FrontArgs a
             o[q] = lo | (hi << 16);
         }
         const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
-        dyn_lds[c] = ov;
-        if (blockIdx.x == 0) reinterpret_cast<uint4*>(a.xn)[c] = ov;
+        s_x4[c] = ov;
+        if (xn_out) reinterpret_cast<uint4*>(xn_out)[c] = ov;
     }
     __syncthreads();
+    return true;
+}
 
-    if (blockIdx.x < a.router_blocks) {
-        // -- 4. router logits: wave -> expert row, fp64 canonical order. ---
-        const uint32_t e = blockIdx.x * kFrontWaves + wave;
-        if (e >= a.E) return;
-        const float* wr = a.router_w + (size_t)e * H;
-        double p[kMaxDecodeTokens][4];
+// ---------------------------------------------------------------------------
+// Router kernel: xn and router logits
+// ---------------------------------------------------------------------------
+struct RouterArgs {
+    const uint16_t* x;
+    const float* gamma;
+    const float* router_w;  // [E][H] fp32
+    uint32_t T, H, E;
+    float eps;
+    uint16_t* xn;           // [T][H] global copy (block 0 writes it)
+    float* logits;          // [T][E]
+    uint32_t* status;
+};
+
+constexpr int kRouterBatch = 14;  // float4 row loads per lane per buffer (two buffers)
+
+// One wave per expert row.  The wave's first two batches of row loads are
+// issued before the xn prologue, so the row fetch overlaps it; each partial
+// 4l + c still accumulates j = 0, 1, ... in order (canonical order).
+// TT bounds the token count (register arrays sized by it).
+template <int TT>
+__global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs a) {
+    extern __shared__ uint4 dyn_lds[];
+    __shared__ NormShared ns;
+    if (*(volatile uint32_t*)a.status) return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t T = a.T, H = a.H, J = H / 256;
+    const uint32_t e = blockIdx.x * kFrontWaves + wave;
+    const bool row = e < a.E;
+    const float* wr = a.router_w + (size_t)(row ? e : 0) * H + 4 * lane;
+    float4 wb[2][kRouterBatch];
 #pragma unroll
-        for (int t = 0; t < kMaxDecodeTokens; ++t)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) p[t][c] = 0.0;
-        const uint32_t J = H / 256;
-        constexpr int kBatch = 14;
-        for (uint32_t j0 = 0; j0 < J; j0 += kBatch) {
-            float4 w[kBatch];
+        for (int u = 0; u < kRouterBatch; ++u) {
+            const uint32_t j = b * kRouterBatch + u;
+            if (row && j < J) wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
+        }
+    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, ns,
+                                 blockIdx.x == 0 ? a.xn : nullptr, a.status))
+        return;
+    if (!row) return;
+    const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
+    double p[TT][4];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                if (j0 + u < J)
-                    w[u] = *reinterpret_cast<const float4*>(wr + 256 * (j0 + u) + 4 * lane);
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                if (j0 + u >= J) continue;
-                const float wv[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        for (int c = 0; c < 4; ++c) p[t][c] = 0.0;
+    for (uint32_t j0 = 0; j0 < J; j0 += 2 * kRouterBatch) {
 #pragma unroll
-                for (int t = 0; t < kMaxDecodeTokens; ++t) {
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int u = 0; u < kRouterBatch; ++u) {
+                const uint32_t j = j0 + b * kRouterBatch + u;
+                if (j >= J) continue;
+                const float wv[4] = {wb[b][u].x, wb[b][u].y, wb[b][u].z, wb[b][u].w};
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
                     if ((uint32_t)t >= T) continue;
-                    const uint2 xv = *reinterpret_cast<const uint2*>(
-                        s_x + (size_t)t * H + 256 * (j0 + u) + 4 * lane);
+                    const uint2 xv =
+                        *reinterpret_cast<const uint2*>(s_x + (size_t)t * H + 256 * j + 4 * lane);
                     const float f[4] = {lo_bf16(xv.x), hi_bf16(xv.x), lo_bf16(xv.y),
                                         hi_bf16(xv.y)};
 #pragma unroll
                     for (int c = 0; c < 4; ++c) p[t][c] += (double)wv[c] * (double)f[c];
                 }
             }
-        }
+            // Refill this buffer with the batch two ahead.
 #pragma unroll
-        for (int t = 0; t < kMaxDecodeTokens; ++t) {
-            if ((uint32_t)t >= T) continue;
-            const double v = canon_reduce(p[t]);
-            if (lane == 0) a.logits[(size_t)t * a.E + e] = (float)v;
+            for (int u = 0; u < kRouterBatch; ++u) {
+                const uint32_t j = j0 + (b + 2) * kRouterBatch + u;
+                if (j < J) wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
+            }
         }
-        return;
     }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        if ((uint32_t)t >= T) continue;
+        const double v = canon_reduce(p[t]);
+        if (lane == 0) a.logits[(size_t)t * a.E + e] = (float)v;
+    }
+}
 
-    // -- 5. shared expert gate/up + GLU: 16 rows, K split over 8 waves. ---
-    const uint32_t rb = blockIdx.x - a.router_blocks;
-    const uint32_t kt = H / 128;
-    const uint32_t k0 = wave * kt / kFrontWaves, k1 = (wave + 1) * kt / kFrontWaves;
+// ---------------------------------------------------------------------------
+// Shared expert (side stream): gate/up + GLU, then down
+// ---------------------------------------------------------------------------
+constexpr int kSharedGuWaves = 16;  // K split of one 16-row block of the shared gate/up
+constexpr int kSharedDnWaves = 4;   // K split of one 16-row block of the shared down
+
+struct SharedGateUpArgs {
+    const uint16_t* x;
+    const float* gamma;
+    uint32_t T, H, S;
+    float eps;
+    const uint4* sh_gu;  // shared gate/up tiles [S/16][H/128][2][4][64] x 16 B
+    GluParams glu;
+    uint16_t* sact;      // [T][S] bf16 shared activation
+    const uint32_t* status;
+};
+
+struct SharedGateUpLds {
+    NormShared ns;
+    f32x4 red[kSharedGuWaves][2][64];
+};
+
+// Workgroup = one 16-row block of S and the whole K = H range, split over
+// 16 waves (first weight tile requested before the xn prologue); the wave
+// partials are added in a fixed tree in LDS (wave w += wave w + h for
+// h = 8, 4, 2, 1) and the block writes sact = bf16(GLU(gate, up)) for its 16
+// columns.
+__global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kernel(
+    SharedGateUpArgs a) {
+    extern __shared__ uint4 dyn_lds[];
+    __shared__ SharedGateUpLds sh;
+    if (*(volatile const uint32_t*)a.status) return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, n = lane & 15;
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint32_t T = a.T, H = a.H, rb = blockIdx.x, kt = H / 128;
+    const uint32_t k0 = wave * kt / kSharedGuWaves, k1 = (wave + 1) * kt / kSharedGuWaves;
     const uint4* tiles = a.sh_gu + (size_t)rb * kt * 2 * 4 * 64 + lane;
-    const bool arow = n < T;
-    for (uint32_t k = k0; k < k1; ++k) {
-        uint4 b[2][4];
+    uint4 bn[2][4];
+    if (k0 < k1)
 #pragma unroll
         for (int w = 0; w < 2; ++w)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[w][j] = tiles[(((size_t)k * 2 + w) * 4 + j) * 64];
+            for (int j = 0; j < 4; ++j) bn[w][j] = tiles[(((size_t)k0 * 2 + w) * 4 + j) * 64];
+    // A non-finite x is reported by the router kernel.
+    if (!build_xn<64 * kSharedGuWaves>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr))
+        return;
+    const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const bool arow = n < T;
+    for (uint32_t k = k0; k < k1; ++k) {
         bf16x8 af[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -265,38 +365,86 @@ __global__ __launch_bounds__(kFrontThreads) void decode_front_kernel(FrontArgs a
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int w = 0; w < 2; ++w) acc[w] = mfma16x16x32(af[j], as_bf16x8(b[w][j]), acc[w]);
+            for (int w = 0; w < 2; ++w) acc[w] = mfma16x16x32(af[j], as_bf16x8(bn[w][j]), acc[w]);
+        if (k + 1 < k1)  // refill after use: one tile of registers
+#pragma unroll
+            for (int w = 0; w < 2; ++w)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    bn[w][j] = tiles[(((size_t)(k + 1) * 2 + w) * 4 + j) * 64];
     }
     sh.red[wave][0][lane] = acc[0];
     sh.red[wave][1][lane] = acc[1];
-    __syncthreads();
-    if (wave == 0) {
-        f32x4 r[2];
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const f32x4 s01 = sh.red[0][w][lane] + sh.red[1][w][lane];
-            const f32x4 s23 = sh.red[2][w][lane] + sh.red[3][w][lane];
-            const f32x4 s45 = sh.red[4][w][lane] + sh.red[5][w][lane];
-            const f32x4 s67 = sh.red[6][w][lane] + sh.red[7][w][lane];
-            r[w] = (s01 + s23) + (s45 + s67);
+    for (uint32_t h = kSharedGuWaves / 2; h >= 1; h /= 2) {
+        __syncthreads();
+        if (wave < h) {
+            sh.red[wave][0][lane] = sh.red[wave][0][lane] + sh.red[wave + h][0][lane];
+            sh.red[wave][1][lane] = sh.red[wave][1][lane] + sh.red[wave + h][1][lane];
         }
+    }
+    if (wave != 0) return;
+    const f32x4 gs = sh.red[0][0][lane], us = sh.red[0][1][lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t row = 4 * g + i;  // token
-            if (row >= T) continue;
-            const float v = glu(r[0][i], r[1][i], a.glu);
-            a.sact[(size_t)row * a.S + rb * 16 + n] = f32_to_bf16(v);
-        }
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = 4 * g + i;
+        if (t < T) a.sact[(size_t)t * a.S + rb * 16 + n] = f32_to_bf16(glu(gs[i], us[i], a.glu));
     }
 }
 
+struct SharedDownArgs {
+    const uint4* sh_dn;    // shared down tiles [H/16][S/128][4][64] x 16 B
+    const uint16_t* sact;  // [T][S]
+    uint32_t T, H, S;
+    float* sy;             // [T][H] shared expert output, fp32
+    const uint32_t* status;
+};
+
+// Workgroup = one 16-row block of H, K = S split over four waves (one tile
+// ahead in flight), partials added pairwise: (w0 + w1) + (w2 + w3).
+__global__ __launch_bounds__(64 * kSharedDnWaves) void decode_shared_down_kernel(SharedDownArgs a) {
+    __shared__ f32x4 red[kSharedDnWaves][64];
+    if (*(volatile const uint32_t*)a.status) return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t rb = blockIdx.x, skt = a.S / 128;
+    const uint32_t k0 = wave * skt / kSharedDnWaves, k1 = (wave + 1) * skt / kSharedDnWaves;
+    const uint4* tiles = a.sh_dn + (size_t)rb * skt * 4 * 64 + lane;
+    const bool arow = n < a.T;
+    const uint16_t* ap = a.sact + (size_t)(arow ? n : 0) * a.S + 32 * g;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 bn[4];
+    if (k0 < k1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bn[j] = tiles[((size_t)k0 * 4 + j) * 64];
+    for (uint32_t k = k0; k < k1; ++k) {
+        uint4 b[4], av[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = bn[j];
+        if (k + 1 < k1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bn[j] = tiles[((size_t)(k + 1) * 4 + j) * 64];
+        load_act(ap, arow, k, av);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(av[j]), as_bf16x8(b[j]), acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    const f32x4 tot = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t t = 4 * g + q;
+        if (t < a.T) a.sy[(size_t)t * a.H + rb * 16 + n] = tot[q];
+    }
+}
 // ---------------------------------------------------------------------------
-// Select kernel: Top-K + grouping (block 0), shared down (other blocks)
+// Select kernel: Top-K + expert-major grouping (one block)
 // ---------------------------------------------------------------------------
 struct SelectArgs {
     const float* logits;
     const float* bias;
-    uint32_t T, H, E, K, S;
+    uint32_t T, E, K;
     float routed_scale;
     uint32_t renorm;
     uint32_t* ids;       // [T][K]
@@ -309,25 +457,19 @@ struct SelectArgs {
     uint32_t* n_active;
     uint32_t* active_asc;
     uint32_t* active_fu;
-    const uint4* sh_dn;  // shared down tiles [H/16][S/128][4][64] x 16 B
-    const uint16_t* sact;
-    float* shared_y;     // [T][H]
+    uint4* arec;         // [E] per active slot: {expert, rows, offset, row tokens}
     uint32_t* status;
 };
 
 struct SelectShared {
     int bad;
     uint32_t wave_sums[kFrontWaves];
-    union {
-        struct {
-            uint32_t ids[kMaxDecodeTokens * 64];
-            uint32_t cnt[kKeysPerLane * 64];
-            uint32_t fu[kKeysPerLane * 64];
-            uint32_t off[kKeysPerLane * 64];
-            uint32_t active[kMaxDecodeTokens * 64];
-        } g;
-        f32x4 red[kFrontWaves][64];
-    } u;
+    uint32_t ids[kMaxDecodeTokens * 64];
+    uint32_t cnt[kKeysPerLane * 64];
+    uint32_t fu[kKeysPerLane * 64];
+    uint32_t off[kKeysPerLane * 64];
+    uint32_t active[kMaxDecodeTokens * 64];
+    uint32_t ptok[kMaxDecodeTokens * 64];
 };
 
 // Top-K of one token by one wave: keys held 8 per lane, popped K times.
@@ -386,11 +528,21 @@ __device__ void topk_token(const SelectArgs& a, uint32_t t, SelectShared& sh) {
     float selsc = 0.0f;  // lane s < K keeps the score of slot s
     uint32_t selid = 0;
     for (uint32_t s = 0; s < K; ++s) {
-        const uint64_t best = wave_max_u64(key[0]);
-        const uint32_t win = 0xffffffffu - (uint32_t)best;
-        const bool mine = key[0] == best;
-        const int wlane = __ffsll((unsigned long long)__ballot(mine)) - 1;
-        const float wsc = __shfl(score[0], wlane);
+        // Largest head: first the score half of the key, then, among lanes
+        // whose heads tie on it, the expert half (a larger value there is a
+        // lower expert index).
+        const uint32_t hi = (uint32_t)(key[0] >> 32);
+        const uint32_t mhi = wave_max_u32(hi);
+        uint64_t tie = __ballot(hi == mhi);
+        if (__popcll(tie) > 1) {
+            const uint32_t lo = hi == mhi ? (uint32_t)key[0] : 0u;
+            const uint32_t mlo = wave_max_u32(lo);
+            tie = __ballot(hi == mhi && lo == mlo);
+        }
+        const int wlane = __ffsll((unsigned long long)tie) - 1;
+        const uint32_t win = 0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wlane);
+        const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[0]), wlane));
+        const bool mine = lane == wlane;
         if ((uint32_t)lane == s) {
             selsc = wsc;
             selid = win;
@@ -408,7 +560,7 @@ __device__ void topk_token(const SelectArgs& a, uint32_t t, SelectShared& sh) {
     float den_f = 0.0f;
     double den_d = 0.0;
     for (uint32_t s = 0; s < K; ++s) {
-        const float v = __shfl(selsc, s);
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selsc), s));
         den_f = __fadd_rn(den_f, v);
         den_d = __dadd_rn(den_d, (double)v);
     }
@@ -431,7 +583,7 @@ __device__ void topk_token(const SelectArgs& a, uint32_t t, SelectShared& sh) {
                             : __fmul_rn(__fdiv_rn(selsc, den_f), a.routed_scale);
         a.ids[(size_t)t * K + lane] = selid;
         a.weights[(size_t)t * K + lane] = w;
-        sh.u.g.ids[t * K + lane] = selid;
+        sh.ids[t * K + lane] = selid;
     }
 }
 
@@ -443,29 +595,29 @@ __device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
     const uint32_t tid = threadIdx.x;
     const uint32_t P = a.T * a.K, E = a.E;
     for (uint32_t e = tid; e < E; e += kFrontThreads) {
-        sh.u.g.cnt[e] = 0;
-        sh.u.g.fu[e] = 0xffffffffu;
+        sh.cnt[e] = 0;
+        sh.fu[e] = 0xffffffffu;
     }
     __syncthreads();
     if (tid < P) {
-        const uint32_t e = sh.u.g.ids[tid];
-        atomicAdd(&sh.u.g.cnt[e], 1u);
-        atomicMin(&sh.u.g.fu[e], tid);
+        const uint32_t e = sh.ids[tid];
+        atomicAdd(&sh.cnt[e], 1u);
+        atomicMin(&sh.fu[e], tid);
     }
     __syncthreads();
     // E <= 512: one expert per thread.
-    const uint32_t c = tid < E ? sh.u.g.cnt[tid] : 0u;
+    const uint32_t c = tid < E ? sh.cnt[tid] : 0u;
     uint32_t total = 0, na = 0;
     const uint32_t excl = block_scan_excl(c, sh.wave_sums, &total);
     const uint32_t aidx = block_scan_excl(c ? 1u : 0u, sh.wave_sums, &na);
     if (tid < E) {
-        sh.u.g.off[tid] = excl;
+        sh.off[tid] = excl;
         a.offsets[tid] = excl;
         a.counts[tid] = c;
-        a.first_use[tid] = sh.u.g.fu[tid];
+        a.first_use[tid] = sh.fu[tid];
         if (c) {
             a.active_asc[aidx] = tid;
-            sh.u.g.active[aidx] = tid;
+            sh.active[aidx] = tid;
         }
     }
     if (tid == 0) {
@@ -474,18 +626,26 @@ __device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
     }
     __syncthreads();
     if (tid < P) {
-        const uint32_t e = sh.u.g.ids[tid];
+        const uint32_t e = sh.ids[tid];
         uint32_t rank = 0;
-        for (uint32_t q = 0; q < tid; ++q) rank += sh.u.g.ids[q] == e;
-        const uint32_t r = sh.u.g.off[e] + rank;
+        for (uint32_t q = 0; q < tid; ++q) rank += sh.ids[q] == e;
+        const uint32_t r = sh.off[e] + rank;
         a.pair_token[r] = tid / a.K;
         a.pair_slot[r] = tid % a.K;
+        sh.ptok[r] = tid / a.K;
+    }
+    __syncthreads();
+    if (tid < na) {  // record of active slot tid: rows' tokens packed 8 bits each
+        const uint32_t e = sh.active[tid], c = sh.cnt[e], o = sh.off[e];
+        uint32_t toks = 0;
+        for (uint32_t q = 0; q < c && q < 4; ++q) toks |= sh.ptok[o + q] << (8 * q);
+        a.arec[tid] = make_uint4(e, c, o, toks);
     }
     if (tid < na) {
-        const uint32_t e = sh.u.g.active[tid];
-        const uint32_t key = sh.u.g.fu[e];
+        const uint32_t e = sh.active[tid];
+        const uint32_t key = sh.fu[e];
         uint32_t rank = 0;
-        for (uint32_t b = 0; b < na; ++b) rank += sh.u.g.fu[sh.u.g.active[b]] < key;
+        for (uint32_t b = 0; b < na; ++b) rank += sh.fu[sh.active[b]] < key;
         a.active_fu[rank] = e;
     }
 }
@@ -493,50 +653,13 @@ __device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
 __global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a) {
     __shared__ SelectShared sh;
     if (*(volatile uint32_t*)a.status) return;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (blockIdx.x == 0) {
-        if (tid == 0) sh.bad = 0;
-        __syncthreads();
-        if (wave < a.T) topk_token(a, wave, sh);
-        __syncthreads();
-        if (sh.bad) return;
-        group_pairs(a, sh);
-        return;
-    }
-    // Shared down: one 16-row block per workgroup, K split over 8 waves.
-    const uint32_t rb = blockIdx.x - 1;
-    const uint32_t kt = a.S / 128;
-    const uint32_t k0 = wave * kt / kFrontWaves, k1 = (wave + 1) * kt / kFrontWaves;
-    const uint32_t g = lane >> 4, n = lane & 15;
-    const uint4* tiles = a.sh_dn + (size_t)rb * kt * 4 * 64 + lane;
-    const bool arow = n < a.T;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k = k0; k < k1; ++k) {
-        uint4 b[4], av[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            b[j] = tiles[((size_t)k * 4 + j) * 64];
-            av[j] = arow ? *reinterpret_cast<const uint4*>(a.sact + (size_t)n * a.S + k * 128 +
-                                                           32 * g + 8 * j)
-                         : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(av[j]), as_bf16x8(b[j]), acc);
-    }
-    sh.u.red[wave][lane] = acc;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    if (tid == 0) sh.bad = 0;
     __syncthreads();
-    if (wave == 0) {
-        const f32x4 s01 = sh.u.red[0][lane] + sh.u.red[1][lane];
-        const f32x4 s23 = sh.u.red[2][lane] + sh.u.red[3][lane];
-        const f32x4 s45 = sh.u.red[4][lane] + sh.u.red[5][lane];
-        const f32x4 s67 = sh.u.red[6][lane] + sh.u.red[7][lane];
-        const f32x4 r = (s01 + s23) + (s45 + s67);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t row = 4 * g + i;
-            if (row < a.T) a.shared_y[(size_t)row * a.H + rb * 16 + n] = r[i];
-        }
-    }
+    if (wave < a.T) topk_token(a, wave, sh);
+    __syncthreads();
+    if (sh.bad) return;
+    group_pairs(a, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -551,145 +674,179 @@ struct GateUpArgs {
     uint32_t I, H;
     const uint16_t* xn;        // [T][H]
     const uint32_t* n_active;
-    const uint32_t* active;
-    const uint32_t* counts;
-    const uint32_t* offsets;
-    const uint32_t* pair_token;
+    const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
     uint16_t* act;             // [pairs][I] bf16, CSR row order
     GluParams glu;
     const uint32_t* status;
 };
 
-// One MXFP4 K-range of a 16-row block: codes/scales from the tile layout,
-// activations from rows `ap` (lanes with arow), MFMAs into acc.  Tiles are
-// loaded one ahead of the MFMAs that consume them.
-template <int S>
-__device__ inline void mxfp4_krange(const uint4* codes, const uint32_t* scales, uint32_t k0,
-                                    uint32_t k1, const uint16_t* ap, bool arow, f32x4* acc) {
-    if (k0 >= k1) return;
-    uint4 cn[S], an[4];
-#pragma unroll
-    for (int w = 0; w < S; ++w) cn[w] = codes[(size_t)k0 * 64 * S + 64 * w];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        an[j] = arow ? *reinterpret_cast<const uint4*>(ap + k0 * 128 + 8 * j) : make_uint4(0, 0, 0, 0);
-    for (uint32_t k = k0; k < k1; ++k) {
-        uint4 c[S], av[4];
-#pragma unroll
-        for (int w = 0; w < S; ++w) c[w] = cn[w];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = an[j];
-        uint32_t sw[S];
-#pragma unroll
-        for (int w = 0; w < S; ++w) sw[w] = scales[(size_t)(k >> 2) * 64 * S + 64 * w];
-        if (k + 1 < k1) {
-#pragma unroll
-            for (int w = 0; w < S; ++w) cn[w] = codes[(size_t)(k + 1) * 64 * S + 64 * w];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                an[j] = arow ? *reinterpret_cast<const uint4*>(ap + (k + 1) * 128 + 8 * j)
-                             : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int w = 0; w < S; ++w) {
-            const float sc = e8m0_to_f32((sw[w] >> (8 * (k & 3))) & 0xffu);
-            const uint32_t cw[4] = {c[w].x, c[w].y, c[w].z, c[w].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[w] = mfma16x16x32(as_bf16x8(av[j]), dequant8(cw[j], sc), acc[w]);
-        }
-    }
-}
-
-// Workgroup = 8 waves: four 16-row blocks, each block's K range split over
-// waves w and w + 4 (first half, second half); the halves are added in that
-// order before the GLU.
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 6))) void
-decode_gateup_kernel(GateUpArgs a) {
-    __shared__ f32x4 red[4][2][64];
-    if (*(volatile const uint32_t*)a.status) return;
+// Workgroup = 4 * KS waves: four 16-row blocks; with KS = 2 each block's K
+// range is split over waves w and w + 4 (first half, second half), added in
+// that order before the GLU.
+template <int KS>
+__global__ __launch_bounds__(256 * KS) void decode_gateup_kernel(GateUpArgs a) {
+    __shared__ f32x4 red[KS == 2 ? 4 : 1][2][64];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t per_expert = a.I / 64;
     const uint32_t ai = blockIdx.x / per_expert;
-    if (ai >= *a.n_active) return;
-    const uint32_t e = a.active[ai];
-    const uint32_t cnt = a.counts[e], off = a.offsets[e];
+    // Status, active count and this slot's record in one round trip (the
+    // record of an inactive slot is not used).
+    const uint32_t st = *(volatile const uint32_t*)a.status;
+    const uint32_t na = *a.n_active;
+    const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
+    if (st || ai >= na) return;
+    const uint32_t e = rec.x;
     const uint32_t rb = (blockIdx.x % per_expert) * 4 + (wave & 3);
     const uint32_t half = wave >> 2;
     const uint32_t kt = a.kt;
     // Split on a scale-group boundary, never past the last tile.
-    const uint32_t kmid = min(kt, (kt / 2 + 3) & ~3u);
+    const uint32_t kmid = KS == 1 ? kt : min(kt, (kt / 2 + 3) & ~3u);
     const uint32_t k0 = half ? kmid : 0, k1 = half ? kt : kmid;
     const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
     const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
-    const bool arow = n < cnt;
-    const uint16_t* ap = arow ? a.xn + (size_t)a.pair_token[off + n] * a.H + 32 * g : a.xn;
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    mxfp4_krange<2>(codes, scales, k0, k1, ap, arow, acc);
-    if (half) {
-        red[wave & 3][0][lane] = acc[0];
-        red[wave & 3][1][lane] = acc[1];
+    const uint32_t cnt = rec.y, off = rec.z;
+    if (k0 < k1) {
+        uint4 cn0 = codes[(size_t)k0 * 128], cn1 = codes[(size_t)k0 * 128 + 64];
+        const bool arow = n < cnt;
+        const uint16_t* ap = a.xn + (size_t)(arow ? (rec.w >> (8 * n)) & 0xffu : 0u) * a.H + 32 * g;
+        uint32_t sw0 = 0, sw1 = 0;
+        for (uint32_t k = k0; k < k1; ++k) {
+            const uint4 c0 = cn0, c1 = cn1;
+            if (k + 1 < k1) {
+                cn0 = codes[(size_t)(k + 1) * 128];
+                cn1 = codes[(size_t)(k + 1) * 128 + 64];
+            }
+            if ((k & 3) == 0 || k == k0) {
+                sw0 = scales[(size_t)(k >> 2) * 128];
+                sw1 = scales[(size_t)(k >> 2) * 128 + 64];
+            }
+            uint4 av[4];
+            load_act(ap, arow, k, av);
+            acc[0] = mxfp4_tile(c0, e8m0_to_f32((sw0 >> (8 * (k & 3))) & 0xffu), av, acc[0]);
+            acc[1] = mxfp4_tile(c1, e8m0_to_f32((sw1 >> (8 * (k & 3))) & 0xffu), av, acc[1]);
+        }
     }
-    __syncthreads();
-    if (half) return;
-    const f32x4 gsum = acc[0] + red[wave][0][lane];
-    const f32x4 usum = acc[1] + red[wave][1][lane];
+    if (KS == 2) {
+        if (half) {
+            red[wave & 3][0][lane] = acc[0];
+            red[wave & 3][1][lane] = acc[1];
+        }
+        __syncthreads();
+        if (half) return;
+        acc[0] = acc[0] + red[wave & 3][0][lane];
+        acc[1] = acc[1] + red[wave & 3][1][lane];
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = 4 * g + i;
         if (row >= cnt) continue;
-        const float v = glu(gsum[i], usum[i], a.glu);
+        const float v = glu(acc[0][i], acc[1][i], a.glu);
         a.act[(size_t)(off + row) * a.I + rb * 16 + n] = f32_to_bf16(v);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Routed down projection -> per-pair fp32 rows
+// Routed down projection and slot-ordered combine
 // ---------------------------------------------------------------------------
+constexpr int kMaxDecodePairs = 256;
+
 struct DownArgs {
     const uint4* dn_codes;     // expert 0 base, tiles [H/16][I/128][64] x 16 B
     const uint32_t* dn_scales; // [H/16][ks][64]
     size_t codes_per_expert;
     size_t scales_per_expert;
     uint32_t kt, ks;           // I/128, scale groups
-    uint32_t I, H, K;
+    uint32_t I, H, T, K;
     const uint16_t* act;       // [pairs][I] CSR order
     const uint32_t* n_active;
-    const uint32_t* active;
-    const uint32_t* counts;
-    const uint32_t* offsets;
+    const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
     const uint32_t* pair_token;
     const uint32_t* pair_slot;
-    float* y;                  // [T][K][H]
+    const float* weights;      // [T][K]
+    const float* shared_y;     // [T][H] shared expert output (null: no shared expert)
+    float* y;                  // [T][K][H] per-pair outputs (kept for inspection)
+    uint16_t* out;             // [T][H] bf16
+    float* out_f32;            // optional
     const uint32_t* status;
 };
 
-// Workgroup = 4 waves, one 16-row block each, the whole K range.
-__global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
+// Workgroup = 16 waves and one 16-row block of the output.  Wave w projects
+// active experts w, w + 16, ... as one stream of (expert, tile) steps (every
+// pair of an expert in one pass over its tiles, the next step's codes in
+// flight).  The block then sums over slots in router order:
+// out[t][h] = bf16(sum_s w[t][s] * y[t][s][h] + shared[t][h]), float mul then
+// float add per term (runtime/src/backend_cpu.cpp:295-301,
+// runtime/src/model.cpp:1145).
+constexpr int kDownWaves = 16;
+
+__global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
+    __shared__ float ys[kMaxDecodePairs][16];
+    __shared__ uint32_t rowof[kMaxDecodePairs];
+    __shared__ uint32_t s_e[kMaxDecodePairs], s_cnt[kMaxDecodePairs], s_off[kMaxDecodePairs];
     if (*(volatile const uint32_t*)a.status) return;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t per_expert = a.H / 64;
-    const uint32_t ai = blockIdx.x / per_expert;
-    if (ai >= *a.n_active) return;
-    const uint32_t e = a.active[ai];
-    const uint32_t cnt = a.counts[e], off = a.offsets[e];
-    const uint32_t rb = (blockIdx.x % per_expert) * 4 + wave;
+    const uint32_t rb = blockIdx.x;
+    const uint32_t P = a.T * a.K;
+    const uint32_t na = *a.n_active;
+    // Stage the active experts and the (token, slot) -> CSR row map.
+    for (uint32_t i = tid; i < na; i += 64 * kDownWaves) {
+        const uint4 rec = a.arec[i];
+        s_e[i] = rec.x;
+        s_cnt[i] = rec.y;
+        s_off[i] = rec.z;
+    }
+    for (uint32_t r = tid; r < P; r += 64 * kDownWaves)
+        rowof[a.pair_token[r] * a.K + a.pair_slot[r]] = r;
+    __syncthreads();
+
+    // Routed experts: wave w streams experts w, w + 16, ...
     const uint32_t kt = a.kt;
-    const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
-    const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
-    const bool arow = n < cnt;
-    const uint16_t* ap = a.act + (size_t)(off + (arow ? n : 0)) * a.I + 32 * g;
-    f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-    mxfp4_krange<1>(codes, scales, 0, kt, ap, arow, acc);
+    const uint32_t nexp = na > wave ? (na - wave + kDownWaves - 1) / kDownWaves : 0;
+    const uint32_t steps = nexp * kt;
+    auto code_at = [&](uint32_t s) {
+        const uint32_t e = s_e[wave + kDownWaves * (s / kt)];
+        return a.dn_codes[e * a.codes_per_expert + ((size_t)rb * kt + s % kt) * 64 + lane];
+    };
+    uint4 cn = steps ? code_at(0) : make_uint4(0, 0, 0, 0);
+    uint32_t sw = 0;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s = 0; s < steps; ++s) {
+        const uint32_t i = wave + kDownWaves * (s / kt), k = s % kt;
+        const uint4 c = cn;
+        if (s + 1 < steps) cn = code_at(s + 1);
+        const uint32_t e = s_e[i], cnt = s_cnt[i], off = s_off[i];
+        if ((k & 3) == 0)
+            sw = a.dn_scales[e * a.scales_per_expert + ((size_t)rb * a.ks + k / 4) * 64 + lane];
+        const bool arow = n < cnt;
+        uint4 av[4];
+        load_act(a.act + (size_t)(off + (arow ? n : 0)) * a.I + 32 * g, arow, k, av);
+        acc = mxfp4_tile(c, e8m0_to_f32((sw >> (8 * (k & 3))) & 0xffu), av, acc);
+        if (k == kt - 1) {  // expert done: its pair rows -> LDS (and y)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = 4 * g + i;
-        if (row >= cnt) continue;
-        const uint32_t r = off + row;
-        const size_t yrow = (size_t)a.pair_token[r] * a.K + a.pair_slot[r];
-        a.y[yrow * a.H + rb * 16 + n] = acc[0][i];
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t row = 4 * g + q;
+                if (row < cnt) {
+                    const uint32_t r = off + row;
+                    ys[r][n] = acc[q];
+                    a.y[((size_t)a.pair_token[r] * a.K + a.pair_slot[r]) * a.H + rb * 16 + n] =
+                        acc[q];
+                }
+            }
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < a.T * 16; i += 64 * kDownWaves) {
+        const uint32_t t = i / 16, c = i % 16, h = rb * 16 + c;
+        float mix = 0.0f;
+        for (uint32_t s = 0; s < a.K; ++s)
+            mix = __fadd_rn(mix, __fmul_rn(a.weights[(size_t)t * a.K + s], ys[rowof[t * a.K + s]][c]));
+        const float v = a.shared_y ? __fadd_rn(mix, a.shared_y[(size_t)t * a.H + h]) : mix;
+        a.out[(size_t)t * a.H + h] = f32_to_bf16(v);
+        if (a.out_f32) a.out_f32[(size_t)t * a.H + h] = v;
     }
 }
 
@@ -697,53 +854,103 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DownArgs a) {
 
 namespace k3x_hip {
 
+namespace {
+
+size_t router_lds(uint32_t T, uint32_t H) { return (size_t)T * H * 2 + sizeof(NormShared); }
+size_t shared_gateup_lds(uint32_t T, uint32_t H) {
+    return (size_t)T * H * 2 + sizeof(SharedGateUpLds);
+}
+
+}  // namespace
+
 bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
                      const k3x_hip_moe_params* p, const void* x) {
     const auto& d = bank->desc;
     if (reinterpret_cast<uintptr_t>(x) % 16) return false;  // 16-byte input loads
-    const size_t lds = (size_t)p->tokens * d.hidden * 2 + sizeof(FrontShared);
+    const size_t lds = std::max(router_lds(p->tokens, d.hidden),
+                                shared_gateup_lds(p->tokens, d.hidden));
     return p->tokens <= (uint32_t)kMaxDecodeTokens && lds <= ctx->max_lds_per_block &&
-           d.hidden % 256 == 0 && d.hidden <= 7168 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
-           p->top_k <= 64 && p->tokens * p->top_k <= 256 && d.inter % 64 == 0 &&
-           d.hidden % 64 == 0;
+           d.hidden % 256 == 0 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
+           p->top_k <= 64 && p->tokens * p->top_k <= (uint32_t)kMaxDecodePairs &&
+           d.inter % 64 == 0 && d.shared_inter % 256 == 0;
 }
 
+// Launch order: the router, Top-K/grouping and routed gate/up run on the
+// context stream; the shared expert, which needs only xn, runs on the
+// context's side stream from a fork event recorded at entry, so it overlaps
+// the latency-bound router and Top-K steps.  The routed down/combine kernel
+// waits for the side stream's join event.  The next call's side work is
+// ordered after this call's combine by its own fork event, so the per-call
+// buffers are never written while still being read.
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                    const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32) {
     const auto& d = bank->desc;
-    const uint32_t T = p->tokens, K = p->top_k;
+    const uint32_t T = p->tokens, K = p->top_k, S = d.shared_inter;
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+    hipStream_t main = ctx->stream, side = ctx->side_stream;
+    if (S && (hipEventRecord(ctx->fork_event, main) != hipSuccess ||
+              hipStreamWaitEvent(side, ctx->fork_event, 0) != hipSuccess))
+        return K3X_ERR_BACKEND_UNAVAILABLE;
 
-    FrontArgs f{};
-    f.x = x;
-    f.gamma = bank->gamma;
-    f.router_w = bank->router_w;
-    f.T = T;
-    f.H = d.hidden;
-    f.E = d.experts;
-    f.S = d.shared_inter;
-    f.eps = p->rms_epsilon;
-    f.router_blocks = (d.experts + kFrontWaves - 1) / kFrontWaves;
-    f.sh_gu = reinterpret_cast<const uint4*>(bank->sh_gu);
-    f.glu = glu;
-    f.xn = b.xn;
-    f.logits = b.logits;
-    f.sact = b.sact;
-    f.status = ctx->status;
-    const size_t lds = (size_t)T * d.hidden * 2;
-    int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT);
-    hipLaunchKernelGGL(decode_front_kernel, dim3(f.router_blocks + d.shared_inter / 16),
-                       dim3(kFrontThreads), lds, ctx->stream, f);
-    end_stage(ctx, mark);
+    RouterArgs r{};
+    r.x = x;
+    r.gamma = bank->gamma;
+    r.router_w = bank->router_w;
+    r.T = T;
+    r.H = d.hidden;
+    r.E = d.experts;
+    r.eps = p->rms_epsilon;
+    r.xn = b.xn;
+    r.logits = b.logits;
+    r.status = ctx->status;
+    const dim3 router_grid((d.experts + kFrontWaves - 1) / kFrontWaves);
+    int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT, main);
+    if (T <= 2)
+        hipLaunchKernelGGL((decode_router_kernel<2>), router_grid, dim3(kFrontThreads),
+                           (size_t)T * d.hidden * 2, main, r);
+    else
+        hipLaunchKernelGGL((decode_router_kernel<kMaxDecodeTokens>), router_grid,
+                           dim3(kFrontThreads), (size_t)T * d.hidden * 2, main, r);
+    end_stage(ctx, mark, main);
+
+    if (S) {
+        SharedGateUpArgs sg{};
+        sg.x = x;
+        sg.gamma = bank->gamma;
+        sg.T = T;
+        sg.H = d.hidden;
+        sg.S = S;
+        sg.eps = p->rms_epsilon;
+        sg.sh_gu = reinterpret_cast<const uint4*>(bank->sh_gu);
+        sg.glu = glu;
+        sg.sact = b.sact;
+        sg.status = ctx->status;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP, side);
+        hipLaunchKernelGGL(decode_shared_gateup_kernel, dim3(S / 16), dim3(64 * kSharedGuWaves),
+                           (size_t)T * d.hidden * 2, side, sg);
+        end_stage(ctx, mark, side);
+        SharedDownArgs sd{};
+        sd.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
+        sd.sact = b.sact;
+        sd.T = T;
+        sd.H = d.hidden;
+        sd.S = S;
+        sd.sy = b.sy;
+        sd.status = ctx->status;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN, side);
+        hipLaunchKernelGGL(decode_shared_down_kernel, dim3(d.hidden / 16),
+                           dim3(64 * kSharedDnWaves), 0, side, sd);
+        end_stage(ctx, mark, side);
+        if (hipEventRecord(ctx->join_event, side) != hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+    }
 
     SelectArgs sa{};
     sa.logits = b.logits;
     sa.bias = bank->router_bias;
     sa.T = T;
-    sa.H = d.hidden;
     sa.E = d.experts;
     sa.K = K;
-    sa.S = d.shared_inter;
     sa.routed_scale = p->routed_scale;
     sa.renorm = p->renorm;
     sa.ids = b.ids;
@@ -756,14 +963,11 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     sa.n_active = b.n_active;
     sa.active_asc = b.active_asc;
     sa.active_fu = b.active_fu;
-    sa.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
-    sa.sact = b.sact;
-    sa.shared_y = b.sy;
+    sa.arec = b.arec;
     sa.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT);
-    hipLaunchKernelGGL(decode_select_kernel, dim3(1 + (d.shared_inter ? d.hidden / 16 : 0)),
-                       dim3(kFrontThreads), 0, ctx->stream, sa);
-    end_stage(ctx, mark);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT, main);
+    hipLaunchKernelGGL(decode_select_kernel, dim3(1), dim3(kFrontThreads), 0, main, sa);
+    end_stage(ctx, mark, main);
 
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     GateUpArgs gu{};
@@ -777,18 +981,30 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.H = d.hidden;
     gu.xn = b.xn;
     gu.n_active = b.n_active;
-    gu.active = b.active_asc;
-    gu.counts = b.counts;
-    gu.offsets = b.offsets;
-    gu.pair_token = b.pair_token;
+    gu.arec = b.arec;
     gu.act = b.act;
     gu.glu = glu;
     gu.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
-    hipLaunchKernelGGL(decode_gateup_kernel, dim3(max_active * (d.inter / 64)), dim3(512), 0,
-                       ctx->stream, gu);
-    end_stage(ctx, mark);
+    // Split K over two waves only while every workgroup of the launch fits
+    // on the device at once; otherwise the extra waves run as a second,
+    // partly empty round.
+    if (!ctx->gateup_split_blocks) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_gateup_kernel<2>, 512,
+                                                         0) != hipSuccess)
+            (void)hipGetLastError();
+        ctx->gateup_split_blocks = (uint32_t)std::max(per_cu, 0) * ctx->cu_count + 1;
+    }
+    const uint32_t gu_blocks = max_active * (d.inter / 64);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP, main);
+    if (gu_blocks < ctx->gateup_split_blocks)
+        hipLaunchKernelGGL((decode_gateup_kernel<2>), dim3(gu_blocks), dim3(512), 0, main, gu);
+    else
+        hipLaunchKernelGGL((decode_gateup_kernel<1>), dim3(gu_blocks), dim3(256), 0, main, gu);
+    end_stage(ctx, mark, main);
 
+    if (S && hipStreamWaitEvent(main, ctx->join_event, 0) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
     dn.dn_scales = bank->dn_scales;
@@ -798,24 +1014,25 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.ks = bank->down.ks;
     dn.I = d.inter;
     dn.H = d.hidden;
+    dn.T = T;
     dn.K = K;
     dn.act = b.act;
     dn.n_active = b.n_active;
-    dn.active = b.active_asc;
-    dn.counts = b.counts;
-    dn.offsets = b.offsets;
+    dn.arec = b.arec;
     dn.pair_token = b.pair_token;
     dn.pair_slot = b.pair_slot;
+    dn.weights = b.weights;
+    dn.shared_y = S ? b.sy : nullptr;
     dn.y = b.y;
+    dn.out = out;
+    dn.out_f32 = out_f32;
     dn.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
-    hipLaunchKernelGGL(decode_down_kernel, dim3(max_active * (d.hidden / 64)), dim3(256), 0,
-                       ctx->stream, dn);
-    end_stage(ctx, mark);
-    ctx->kernel_launches += 4;
-    if (hipGetLastError() != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    return launch_combine(ctx, b.y, b.weights, d.shared_inter ? b.sy : nullptr, K, d.hidden, T,
-                          out, out_f32);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN, main);
+    hipLaunchKernelGGL(decode_down_kernel, dim3(d.hidden / 16), dim3(64 * kDownWaves), 0, main,
+                       dn);
+    end_stage(ctx, mark, main);
+    ctx->kernel_launches += S ? 6 : 4;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 
 }  // namespace k3x_hip

@@ -523,6 +523,7 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->y = (float*)take(P * d.hidden * 4);
     s->sact = (uint16_t*)take((size_t)T * d.shared_inter * 2);
     s->sy = (float*)take((size_t)T * d.hidden * 4);
+    s->arec = (uint4*)take((size_t)d.experts * 16);
     return at;
 }
 
