@@ -1,4 +1,4 @@
-// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): six
+// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): seven
 // launches on two streams, no cross-workgroup synchronisation inside any of
 // them.
 //
@@ -8,27 +8,26 @@
 //                         expert row (fp64, canonical order), into logits.
 //   decode_select_kernel  sigmoid + bias Top-K of every token and the
 //                         expert-major grouping (one block).
-//   decode_gateup_kernel  routed MXFP4 gate/up + GLU per active expert, four
-//                         16-row blocks per workgroup (K split over two waves
-//                         when the extra waves still fit on the device at
-//                         once), weights dequantised in registers.
-//   decode_down_kernel    one workgroup per 16 output rows: its waves take
-//                         the active experts in turn (MXFP4 down projection
-//                         of each expert's pairs into LDS), then the block
-//                         forms out = bf16(sum over slots in router order of
-//                         w * y + shared) for its rows.
+//   decode_gateup_kernel  routed MXFP4 gate/up + GLU: one wave per (active
+//                         expert, 16-row block), weights dequantised in
+//                         registers.
+//   decode_down_kernel    routed MXFP4 down projection: one wave per (active
+//                         expert, 16-row block) -> per-pair rows y.
+//   decode_combine_kernel out = bf16(sum over slots in router order of w * y
+//                         + shared).
 // Side stream (the shared expert, which needs only xn):
 //   decode_shared_gateup_kernel  bf16 shared gate/up + GLU, one 16-row block
 //                         of S per workgroup, K split over 16 waves.
 //   decode_shared_down_kernel    bf16 shared down, one 16-row block of H per
 //                         workgroup, K split over four waves.
 // The side stream forks from the context stream at entry and joins it before
-// decode_down_kernel, so its ~90 MB stream overlaps the router and Top-K
-// steps, which leave most of the device idle.
+// the combine, so its ~90 MB overlap the router and Top-K steps, which leave
+// most of the device idle.
 //
-// The streaming loops keep one weight tile in flight per wave and few
-// registers, so that eight waves fit on each SIMD: for these HBM streams
-// the number of resident waves matters more than per-wave prefetch depth.
+// Streaming loops keep several steps of loads in flight per wave with no
+// branch around a weight load (indices clamped instead), so the compiler's
+// in-order wait on the vector-memory counter never waits for a later step.
+// Work units of one wave spread evenly over the CUs.
 // Numerics: the same canonical fp64 order for the RMS sum and the router
 // logits as the general path, the same Top-K keys and renormalisation, the
 // same slot-ordered combine; fp32 MFMA accumulation for the projections.
@@ -131,11 +130,25 @@ __device__ inline f32x4 mxfp4_tile(const uint4& c, float scale, const uint4 av[4
     return acc;
 }
 
+// Activation slice for K tile k, loaded only by the lanes whose MFMA row is
+// used: row m of an MFMA result depends only on row m of A, and unused rows
+// are never stored, so the other lanes' registers may hold anything.  Issued
+// before a step's weight loads, so that the weight loads of later steps,
+// which every path issues, stay counted behind a step's own loads and the
+// compiler can wait for one step while later steps remain in flight.
 __device__ inline void load_act(const uint16_t* ap, bool arow, uint32_t k, uint4 av[4]) {
+    if (arow)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        av[j] = arow ? *reinterpret_cast<const uint4*>(ap + k * 128 + 8 * j) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < 4; ++j) av[j] = *reinterpret_cast<const uint4*>(ap + k * 128 + 8 * j);
 }
+
+// Wave index as a wave-uniform (scalar) value.
+__device__ inline uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Latched error word as left by earlier launches: a plain load from a
+// uniform address (a scalar load, counted apart from the vector loads, so
+// that checking it does not wait for weight prefetches already issued).
+__device__ inline uint32_t prior_status(const uint32_t* status) { return *status; }
 
 // ---------------------------------------------------------------------------
 // xn prologue of the router and shared gate/up kernels
@@ -145,30 +158,37 @@ struct NormShared {
     int bad;
 };
 
-// x -> LDS (16-byte chunks), inverse RMS per token from the sum of squares in
-// the canonical fp64 order, then xn = bf16(x * inv * gamma) in place; the
-// block then holds xn as [T][H] bf16 at s_x4.  Returns false when x holds a
-// non-finite value (latched into *status when status is non-null).  Needs
-// at least T waves; xn_out, when non-null, receives a global copy.
+// x and gamma -> LDS in one batch of 16-byte loads, inverse RMS per token
+// from the sum of squares in the canonical fp64 order, then xn = bf16(x *
+// inv * gamma) in place; the block then holds xn as [T][H] bf16 at s_x4
+// (gamma follows as [H] fp32).  Returns false when x holds a non-finite
+// value (latched into *status when status is non-null).  Needs at least T
+// waves; xn_out, when non-null, receives a global copy.
 template <int kThreads>
-__device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, uint32_t T, uint32_t H, float eps,
-                         uint4* s_x4, NormShared& ns, uint16_t* xn_out, uint32_t* status) {
+__device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, uint32_t T,
+                                         uint32_t H, float eps, uint4* s_x4, NormShared& ns,
+                                         uint16_t* xn_out, uint32_t* status) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
+    const uint32_t chunks = T * H / 8;          // x chunks; gamma chunks follow
+    const uint32_t all = chunks + H / 4;
+    const float* s_g = reinterpret_cast<const float*>(s_x4 + chunks);
     if (tid == 0) ns.bad = 0;
-    const uint32_t chunks = T * H / 8;
-    for (uint32_t c0 = 0; c0 < chunks; c0 += 4 * kThreads) {
-        uint4 v[4];
+    constexpr int kLoads = 8;
+    for (uint32_t c0 = 0; c0 < all; c0 += kLoads * kThreads) {
+        // One unconditional load and store per slot (slots past the end
+        // copy the last chunk again, the same value to the same place): no
+        // branch, so the loads are all in flight together.
+        uint4 v[kLoads];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const uint32_t c = c0 + tid + kThreads * it;
-            v[it] = c < chunks ? reinterpret_cast<const uint4*>(x)[c] : make_uint4(0, 0, 0, 0);
+        for (int it = 0; it < kLoads; ++it) {
+            const uint32_t c = min(c0 + tid + kThreads * it, all - 1);
+            const uint4* src = c < chunks ? reinterpret_cast<const uint4*>(x) + c
+                                          : reinterpret_cast<const uint4*>(gamma) + (c - chunks);
+            v[it] = *src;
         }
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const uint32_t c = c0 + tid + kThreads * it;
-            if (c < chunks) s_x4[c] = v[it];
-        }
+        for (int it = 0; it < kLoads; ++it) s_x4[min(c0 + tid + kThreads * it, all - 1)] = v[it];
     }
     __syncthreads();
     if (wave < T) {
@@ -200,8 +220,8 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
     for (uint32_t c = tid; c < chunks; c += kThreads) {
         const uint32_t t = (c * 8) / H, k = (c * 8) % H;
         const uint4 w = s_x4[c];
-        const float4 g0 = *reinterpret_cast<const float4*>(gamma + k);
-        const float4 g1 = *reinterpret_cast<const float4*>(gamma + k + 4);
+        const float4 g0 = *reinterpret_cast<const float4*>(s_g + k);
+        const float4 g1 = *reinterpret_cast<const float4*>(s_g + k + 4);
         const float inv = ns.inv[t];
         const uint32_t in[4] = {w.x, w.y, w.z, w.w};
         const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
@@ -220,6 +240,9 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
     __syncthreads();
     return true;
 }
+
+// Dynamic LDS of a block that runs build_xn: x [T][H] bf16 + gamma [H] fp32.
+inline size_t xn_lds_bytes(uint32_t T, uint32_t H) { return (size_t)T * H * 2 + (size_t)H * 4; }
 
 // ---------------------------------------------------------------------------
 // Router kernel: xn and router logits
@@ -245,20 +268,23 @@ template <int TT>
 __global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs a) {
     extern __shared__ uint4 dyn_lds[];
     __shared__ NormShared ns;
-    if (*(volatile uint32_t*)a.status) return;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.T, H = a.H, J = H / 256;
     const uint32_t e = blockIdx.x * kFrontWaves + wave;
     const bool row = e < a.E;
+    // Loads are unconditional (a row past E reads row 0, a batch index past
+    // the row end reads its last chunk; neither is used), so that they are
+    // all in flight together.
     const float* wr = a.router_w + (size_t)(row ? e : 0) * H + 4 * lane;
     float4 wb[2][kRouterBatch];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int u = 0; u < kRouterBatch; ++u) {
-            const uint32_t j = b * kRouterBatch + u;
-            if (row && j < J) wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
+            const uint32_t j = min((uint32_t)(b * kRouterBatch + u), J - 1);
+            wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
         }
+    if (prior_status(a.status)) return;
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, ns,
                                  blockIdx.x == 0 ? a.xn : nullptr, a.status))
         return;
@@ -288,12 +314,13 @@ __global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs
                     for (int c = 0; c < 4; ++c) p[t][c] += (double)wv[c] * (double)f[c];
                 }
             }
-            // Refill this buffer with the batch two ahead.
+            // Refill this buffer with the batch two ahead (clamped).
+            if (j0 + (b + 2) * kRouterBatch < J)
 #pragma unroll
-            for (int u = 0; u < kRouterBatch; ++u) {
-                const uint32_t j = j0 + (b + 2) * kRouterBatch + u;
-                if (j < J) wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
-            }
+                for (int u = 0; u < kRouterBatch; ++u) {
+                    const uint32_t j = min(j0 + (b + 2) * kRouterBatch + u, J - 1);
+                    wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
+                }
         }
     }
 #pragma unroll
@@ -335,43 +362,53 @@ __global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kern
     SharedGateUpArgs a) {
     extern __shared__ uint4 dyn_lds[];
     __shared__ SharedGateUpLds sh;
-    if (*(volatile const uint32_t*)a.status) return;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t T = a.T, H = a.H, rb = blockIdx.x, kt = H / 128;
     const uint32_t k0 = wave * kt / kSharedGuWaves, k1 = (wave + 1) * kt / kSharedGuWaves;
+    const uint32_t N = k1 - k0;
     const uint4* tiles = a.sh_gu + (size_t)rb * kt * 2 * 4 * 64 + lane;
-    uint4 bn[2][4];
-    if (k0 < k1)
+    // Two tiles of registers in flight, the first two requested before the
+    // xn prologue; refills clamped to the last tile (no branch in the loop).
+    constexpr int PD = 2;
+    uint4 bn[PD][2][4];
+    auto load = [&](uint4 (&b)[2][4], uint32_t k) {
 #pragma unroll
         for (int w = 0; w < 2; ++w)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bn[w][j] = tiles[(((size_t)k0 * 2 + w) * 4 + j) * 64];
+            for (int j = 0; j < 4; ++j) b[w][j] = tiles[(((size_t)k * 2 + w) * 4 + j) * 64];
+    };
+    if (N)
+#pragma unroll
+        for (int d = 0; d < PD; ++d) load(bn[d], k0 + min((uint32_t)d, N - 1));
+    if (prior_status(a.status)) return;
     // A non-finite x is reported by the router kernel.
     if (!build_xn<64 * kSharedGuWaves>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr))
         return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
+    const uint16_t* xrow = s_x + (size_t)(n < T ? n : 0) * H + 32 * g;  // unused rows: row 0
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    const bool arow = n < T;
-    for (uint32_t k = k0; k < k1; ++k) {
+    auto step = [&](const uint4 (&b)[2][4], uint32_t k) {
         bf16x8 af[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (arow)
-                v = *reinterpret_cast<const uint4*>(s_x + (size_t)n * H + k * 128 + 32 * g + 8 * j);
-            af[j] = as_bf16x8(v);
-        }
+        for (int j = 0; j < 4; ++j) af[j] = as_bf16x8(*reinterpret_cast<const uint4*>(xrow + k * 128 + 8 * j));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int w = 0; w < 2; ++w) acc[w] = mfma16x16x32(af[j], as_bf16x8(bn[w][j]), acc[w]);
-        if (k + 1 < k1)  // refill after use: one tile of registers
+            for (int w = 0; w < 2; ++w) acc[w] = mfma16x16x32(af[j], as_bf16x8(b[w][j]), acc[w]);
+    };
+    if (N) {
+        uint32_t kb = 0;
+        for (; kb + PD <= N; kb += PD) {
 #pragma unroll
-            for (int w = 0; w < 2; ++w)
+            for (int d = 0; d < PD; ++d) {
+                step(bn[d], k0 + kb + d);
+                load(bn[d], k0 + min(kb + d + PD, N - 1));
+            }
+        }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    bn[w][j] = tiles[(((size_t)(k + 1) * 2 + w) * 4 + j) * 64];
+        for (int d = 0; d < PD; ++d)
+            if (kb + d < N) step(bn[d], k0 + kb + d);
     }
     sh.red[wave][0][lane] = acc[0];
     sh.red[wave][1][lane] = acc[1];
@@ -400,33 +437,52 @@ struct SharedDownArgs {
     const uint32_t* status;
 };
 
-// Workgroup = one 16-row block of H, K = S split over four waves (one tile
-// ahead in flight), partials added pairwise: (w0 + w1) + (w2 + w3).
+// Workgroup = one 16-row block of H, K = S split over four waves (up to
+// four tiles in flight per wave, refills clamped to the last tile), partials
+// added pairwise: (w0 + w1) + (w2 + w3).
 __global__ __launch_bounds__(64 * kSharedDnWaves) void decode_shared_down_kernel(SharedDownArgs a) {
     __shared__ f32x4 red[kSharedDnWaves][64];
-    if (*(volatile const uint32_t*)a.status) return;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (prior_status(a.status)) return;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t rb = blockIdx.x, skt = a.S / 128;
     const uint32_t k0 = wave * skt / kSharedDnWaves, k1 = (wave + 1) * skt / kSharedDnWaves;
+    const uint32_t N = k1 - k0;
     const uint4* tiles = a.sh_dn + (size_t)rb * skt * 4 * 64 + lane;
     const bool arow = n < a.T;
     const uint16_t* ap = a.sact + (size_t)(arow ? n : 0) * a.S + 32 * g;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    uint4 bn[4];
-    if (k0 < k1)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bn[j] = tiles[((size_t)k0 * 4 + j) * 64];
-    for (uint32_t k = k0; k < k1; ++k) {
+    constexpr int PD = 4;
+    struct Step {
         uint4 b[4], av[4];
+    };
+    auto load = [&](Step& r, uint32_t k) {
+        load_act(ap, arow, k, r.av);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = bn[j];
-        if (k + 1 < k1)
+        for (int j = 0; j < 4; ++j) r.b[j] = tiles[((size_t)k * 4 + j) * 64];
+    };
+    auto step = [&](const Step& r) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bn[j] = tiles[((size_t)(k + 1) * 4 + j) * 64];
-        load_act(ap, arow, k, av);
+        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(r.av[j]), as_bf16x8(r.b[j]), acc);
+    };
+    if (N) {
+        Step r[PD];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(av[j]), as_bf16x8(b[j]), acc);
+        for (int d = 0; d < PD; ++d) {
+            r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
+            load(r[d], k0 + min((uint32_t)d, N - 1));
+        }
+        uint32_t kb = 0;
+        for (; kb + PD <= N; kb += PD) {
+#pragma unroll
+            for (int d = 0; d < PD; ++d) {
+                step(r[d]);
+                load(r[d], k0 + min(kb + d + PD, N - 1));
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < PD; ++d)
+            if (kb + d < N) step(r[d]);
     }
     red[wave][lane] = acc;
     __syncthreads();
@@ -652,7 +708,7 @@ __device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
 
 __global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a) {
     __shared__ SelectShared sh;
-    if (*(volatile uint32_t*)a.status) return;
+    if (prior_status(a.status)) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
     if (tid == 0) sh.bad = 0;
     __syncthreads();
@@ -680,64 +736,72 @@ struct GateUpArgs {
     const uint32_t* status;
 };
 
-// Workgroup = 4 * KS waves: four 16-row blocks; with KS = 2 each block's K
-// range is split over waves w and w + 4 (first half, second half), added in
-// that order before the GLU.
-template <int KS>
-__global__ __launch_bounds__(256 * KS) void decode_gateup_kernel(GateUpArgs a) {
-    __shared__ f32x4 red[KS == 2 ? 4 : 1][2][64];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Registers of one gate/up step (one 128-K tile of the gate and the up
+// block): codes, the scale dwords of the tile's group, the activation slice.
+struct GuStep {
+    uint4 c0, c1;
+    uint32_t s0, s1;
+    uint4 av[4];
+};
+
+__device__ inline void gu_load(GuStep& r, const uint4* codes, const uint32_t* scales,
+                               const uint16_t* ap, bool arow, uint32_t k) {
+    load_act(ap, arow, k, r.av);
+    r.c0 = codes[(size_t)k * 128];
+    r.c1 = codes[(size_t)k * 128 + 64];
+    r.s0 = scales[(size_t)(k >> 2) * 128];
+    r.s1 = scales[(size_t)(k >> 2) * 128 + 64];
+}
+
+// One wave per workgroup and per unit of work: active slot ai = block / (I /
+// 16), 16-row block rb = block % (I / 16), the whole K range.  Units this
+// small spread evenly over the CUs (with four-wave workgroups, 29 active
+// experts put four workgroups on some CUs and three on others, and the
+// fourth, youngest, finishes a third later).  PD steps of loads in flight: a
+// step's registers are refilled with step k + PD right after use (clamped to
+// the last step, so the loop body has no branch around a weight load), full
+// groups of PD steps in the loop and the remainder after it.
+template <int PD>
+__global__ __launch_bounds__(64) void decode_gateup_kernel(GateUpArgs a) {
+    const uint32_t lane = threadIdx.x;
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t per_expert = a.I / 64;
-    const uint32_t ai = blockIdx.x / per_expert;
+    const uint32_t per_expert = a.I / 16;
+    const uint32_t ai = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
     // Status, active count and this slot's record in one round trip (the
     // record of an inactive slot is not used).
-    const uint32_t st = *(volatile const uint32_t*)a.status;
+    const uint32_t st = prior_status(a.status);
     const uint32_t na = *a.n_active;
     const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
     if (st || ai >= na) return;
-    const uint32_t e = rec.x;
-    const uint32_t rb = (blockIdx.x % per_expert) * 4 + (wave & 3);
-    const uint32_t half = wave >> 2;
+    const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
     const uint32_t kt = a.kt;
-    // Split on a scale-group boundary, never past the last tile.
-    const uint32_t kmid = KS == 1 ? kt : min(kt, (kt / 2 + 3) & ~3u);
-    const uint32_t k0 = half ? kmid : 0, k1 = half ? kt : kmid;
     const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
     const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
+    const bool arow = n < cnt;
+    const uint16_t* ap = a.xn + (size_t)(arow ? (rec.w >> (8 * n)) & 0xffu : 0u) * a.H + 32 * g;
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    const uint32_t cnt = rec.y, off = rec.z;
-    if (k0 < k1) {
-        uint4 cn0 = codes[(size_t)k0 * 128], cn1 = codes[(size_t)k0 * 128 + 64];
-        const bool arow = n < cnt;
-        const uint16_t* ap = a.xn + (size_t)(arow ? (rec.w >> (8 * n)) & 0xffu : 0u) * a.H + 32 * g;
-        uint32_t sw0 = 0, sw1 = 0;
-        for (uint32_t k = k0; k < k1; ++k) {
-            const uint4 c0 = cn0, c1 = cn1;
-            if (k + 1 < k1) {
-                cn0 = codes[(size_t)(k + 1) * 128];
-                cn1 = codes[(size_t)(k + 1) * 128 + 64];
-            }
-            if ((k & 3) == 0 || k == k0) {
-                sw0 = scales[(size_t)(k >> 2) * 128];
-                sw1 = scales[(size_t)(k >> 2) * 128 + 64];
-            }
-            uint4 av[4];
-            load_act(ap, arow, k, av);
-            acc[0] = mxfp4_tile(c0, e8m0_to_f32((sw0 >> (8 * (k & 3))) & 0xffu), av, acc[0]);
-            acc[1] = mxfp4_tile(c1, e8m0_to_f32((sw1 >> (8 * (k & 3))) & 0xffu), av, acc[1]);
+    GuStep r[PD];
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+        r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
+        gu_load(r[d], codes, scales, ap, arow, min((uint32_t)d, kt - 1));
+    }
+    auto step = [&](const GuStep& q, uint32_t k) {
+        const uint32_t sh = 8 * (k & 3);
+        acc[0] = mxfp4_tile(q.c0, e8m0_to_f32((q.s0 >> sh) & 0xffu), q.av, acc[0]);
+        acc[1] = mxfp4_tile(q.c1, e8m0_to_f32((q.s1 >> sh) & 0xffu), q.av, acc[1]);
+    };
+    uint32_t kb = 0;
+    for (; kb + PD <= kt; kb += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            step(r[d], kb + d);
+            gu_load(r[d], codes, scales, ap, arow, min(kb + d + PD, kt - 1));
         }
     }
-    if (KS == 2) {
-        if (half) {
-            red[wave & 3][0][lane] = acc[0];
-            red[wave & 3][1][lane] = acc[1];
-        }
-        __syncthreads();
-        if (half) return;
-        acc[0] = acc[0] + red[wave & 3][0][lane];
-        acc[1] = acc[1] + red[wave & 3][1][lane];
-    }
+#pragma unroll
+    for (int d = 0; d < PD; ++d)
+        if (kb + d < kt) step(r[d], kb + d);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = 4 * g + i;
@@ -748,106 +812,129 @@ __global__ __launch_bounds__(256 * KS) void decode_gateup_kernel(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Routed down projection and slot-ordered combine
+// Routed down projection -> per-pair rows; slot-ordered combine
 // ---------------------------------------------------------------------------
-constexpr int kMaxDecodePairs = 256;
-
 struct DownArgs {
     const uint4* dn_codes;     // expert 0 base, tiles [H/16][I/128][64] x 16 B
     const uint32_t* dn_scales; // [H/16][ks][64]
     size_t codes_per_expert;
     size_t scales_per_expert;
     uint32_t kt, ks;           // I/128, scale groups
-    uint32_t I, H, T, K;
+    uint32_t I, H, K;
     const uint16_t* act;       // [pairs][I] CSR order
     const uint32_t* n_active;
     const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
     const uint32_t* pair_token;
     const uint32_t* pair_slot;
-    const float* weights;      // [T][K]
-    const float* shared_y;     // [T][H] shared expert output (null: no shared expert)
-    float* y;                  // [T][K][H] per-pair outputs (kept for inspection)
-    uint16_t* out;             // [T][H] bf16
-    float* out_f32;            // optional
+    float* y;                  // [T][K][H] per-pair outputs
     const uint32_t* status;
 };
 
-// Workgroup = 16 waves and one 16-row block of the output.  Wave w projects
-// active experts w, w + 16, ... as one stream of (expert, tile) steps (every
-// pair of an expert in one pass over its tiles, the next step's codes in
-// flight).  The block then sums over slots in router order:
-// out[t][h] = bf16(sum_s w[t][s] * y[t][s][h] + shared[t][h]), float mul then
-// float add per term (runtime/src/backend_cpu.cpp:295-301,
-// runtime/src/model.cpp:1145).
-constexpr int kDownWaves = 16;
+// Registers of one down step: codes, the scale dword of the tile's group,
+// the activation slice.
+struct DnStep {
+    uint4 c;
+    uint32_t s;
+    uint4 av[4];
+};
 
-__global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
-    __shared__ float ys[kMaxDecodePairs][16];
-    __shared__ uint32_t rowof[kMaxDecodePairs];
-    __shared__ uint32_t s_e[kMaxDecodePairs], s_cnt[kMaxDecodePairs], s_off[kMaxDecodePairs];
-    if (*(volatile const uint32_t*)a.status) return;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// One wave per workgroup and unit: active slot ai = block / (H / 16),
+// 16-row block rb = block % (H / 16), the whole K = I range with PD steps of
+// loads in flight (as the gate/up kernel); the rows of the slot's pairs go
+// to y.
+template <int PD>
+__global__ __launch_bounds__(64) void decode_down_kernel(DownArgs a) {
+    const uint32_t lane = threadIdx.x;
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t rb = blockIdx.x;
-    const uint32_t P = a.T * a.K;
+    const uint32_t per_expert = a.H / 16;
+    const uint32_t ai = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
+    const uint32_t st = prior_status(a.status);
     const uint32_t na = *a.n_active;
-    // Stage the active experts and the (token, slot) -> CSR row map.
-    for (uint32_t i = tid; i < na; i += 64 * kDownWaves) {
-        const uint4 rec = a.arec[i];
-        s_e[i] = rec.x;
-        s_cnt[i] = rec.y;
-        s_off[i] = rec.z;
-    }
-    for (uint32_t r = tid; r < P; r += 64 * kDownWaves)
-        rowof[a.pair_token[r] * a.K + a.pair_slot[r]] = r;
-    __syncthreads();
-
-    // Routed experts: wave w streams experts w, w + 16, ...
+    const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
+    if (st || ai >= na) return;
+    const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
     const uint32_t kt = a.kt;
-    const uint32_t nexp = na > wave ? (na - wave + kDownWaves - 1) / kDownWaves : 0;
-    const uint32_t steps = nexp * kt;
-    auto code_at = [&](uint32_t s) {
-        const uint32_t e = s_e[wave + kDownWaves * (s / kt)];
-        return a.dn_codes[e * a.codes_per_expert + ((size_t)rb * kt + s % kt) * 64 + lane];
+    const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
+    const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
+    const bool arow = n < cnt;
+    const uint16_t* ap = a.act + (size_t)(off + (arow ? n : 0u)) * a.I + 32 * g;
+    auto load = [&](DnStep& r, uint32_t k) {
+        load_act(ap, arow, k, r.av);
+        r.c = codes[(size_t)k * 64];
+        r.s = scales[(size_t)(k >> 2) * 64];
     };
-    uint4 cn = steps ? code_at(0) : make_uint4(0, 0, 0, 0);
-    uint32_t sw = 0;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t s = 0; s < steps; ++s) {
-        const uint32_t i = wave + kDownWaves * (s / kt), k = s % kt;
-        const uint4 c = cn;
-        if (s + 1 < steps) cn = code_at(s + 1);
-        const uint32_t e = s_e[i], cnt = s_cnt[i], off = s_off[i];
-        if ((k & 3) == 0)
-            sw = a.dn_scales[e * a.scales_per_expert + ((size_t)rb * a.ks + k / 4) * 64 + lane];
-        const bool arow = n < cnt;
-        uint4 av[4];
-        load_act(a.act + (size_t)(off + (arow ? n : 0)) * a.I + 32 * g, arow, k, av);
-        acc = mxfp4_tile(c, e8m0_to_f32((sw >> (8 * (k & 3))) & 0xffu), av, acc);
-        if (k == kt - 1) {  // expert done: its pair rows -> LDS (and y)
+    DnStep r[PD];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t row = 4 * g + q;
-                if (row < cnt) {
-                    const uint32_t r = off + row;
-                    ys[r][n] = acc[q];
-                    a.y[((size_t)a.pair_token[r] * a.K + a.pair_slot[r]) * a.H + rb * 16 + n] =
-                        acc[q];
-                }
-            }
-            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < PD; ++d) {
+        r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
+        load(r[d], min((uint32_t)d, kt - 1));
+    }
+    uint32_t kb = 0;
+    for (; kb + PD <= kt; kb += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            const uint32_t k = kb + d;
+            acc = mxfp4_tile(r[d].c, e8m0_to_f32((r[d].s >> (8 * (k & 3))) & 0xffu), r[d].av, acc);
+            load(r[d], min(k + PD, kt - 1));
         }
     }
-    __syncthreads();
-    for (uint32_t i = tid; i < a.T * 16; i += 64 * kDownWaves) {
-        const uint32_t t = i / 16, c = i % 16, h = rb * 16 + c;
-        float mix = 0.0f;
-        for (uint32_t s = 0; s < a.K; ++s)
-            mix = __fadd_rn(mix, __fmul_rn(a.weights[(size_t)t * a.K + s], ys[rowof[t * a.K + s]][c]));
-        const float v = a.shared_y ? __fadd_rn(mix, a.shared_y[(size_t)t * a.H + h]) : mix;
-        a.out[(size_t)t * a.H + h] = f32_to_bf16(v);
-        if (a.out_f32) a.out_f32[(size_t)t * a.H + h] = v;
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+        const uint32_t k = kb + d;
+        if (k < kt)
+            acc = mxfp4_tile(r[d].c, e8m0_to_f32((r[d].s >> (8 * (k & 3))) & 0xffu), r[d].av, acc);
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t row = 4 * g + q;
+        if (row < cnt) {
+            const uint32_t rr = off + row;
+            a.y[((size_t)a.pair_token[rr] * a.K + a.pair_slot[rr]) * a.H + rb * 16 + n] = acc[q];
+        }
+    }
+}
+
+struct CombineArgs {
+    const float* y;         // [T][K][H]
+    const float* weights;   // [T][K]
+    const float* shared_y;  // [T][H] or null
+    uint32_t K, H;
+    uint16_t* out;          // [T][H] bf16
+    float* out_f32;         // optional
+    const uint32_t* status;
+};
+
+// out[t][h] = bf16(sum over slots s in router order of w[t][s] * y[t][s][h]
+// + shared[t][h]), float mul then float add per term
+// (runtime/src/backend_cpu.cpp:295-301, runtime/src/model.cpp:1145).  The
+// loads of a group of 16 slots are issued together (indices clamped, so
+// there is no branch around them).  Grid (H / 256, T).
+constexpr int kCombineBatch = 16;
+
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+    if (prior_status(a.status)) return;
+    const uint32_t t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
+    if (h >= a.H) return;
+    const float* yr = a.y + (size_t)t * a.K * a.H + h;
+    const float* wr = a.weights + (size_t)t * a.K;
+    const float sh = a.shared_y ? a.shared_y[(size_t)t * a.H + h] : 0.0f;
+    float mix = 0.0f;
+    for (uint32_t s0 = 0; s0 < a.K; s0 += kCombineBatch) {
+        float yv[kCombineBatch], wv[kCombineBatch];
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) {
+            const uint32_t s = min(s0 + u, a.K - 1);
+            yv[u] = yr[(size_t)s * a.H];
+            wv[u] = wr[s];
+        }
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u)
+            if (s0 + u < a.K) mix = __fadd_rn(mix, __fmul_rn(wv[u], yv[u]));
+    }
+    const float v = a.shared_y ? __fadd_rn(mix, sh) : mix;
+    a.out[(size_t)t * a.H + h] = f32_to_bf16(v);
+    if (a.out_f32) a.out_f32[(size_t)t * a.H + h] = v;
 }
 
 }  // namespace
@@ -856,10 +943,16 @@ namespace k3x_hip {
 
 namespace {
 
-size_t router_lds(uint32_t T, uint32_t H) { return (size_t)T * H * 2 + sizeof(NormShared); }
+size_t router_lds(uint32_t T, uint32_t H) { return xn_lds_bytes(T, H) + sizeof(NormShared); }
 size_t shared_gateup_lds(uint32_t T, uint32_t H) {
-    return (size_t)T * H * 2 + sizeof(SharedGateUpLds);
+    return xn_lds_bytes(T, H) + sizeof(SharedGateUpLds);
 }
+
+// Steps of loads in flight per wave in the routed gate/up and down loops.
+constexpr int kGateUpDepth = 3;
+constexpr int kDownDepth = 4;
+// Pairs the decode path handles (T * K).
+constexpr uint32_t kMaxDecodePairs = 256;
 
 }  // namespace
 
@@ -905,12 +998,13 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     r.status = ctx->status;
     const dim3 router_grid((d.experts + kFrontWaves - 1) / kFrontWaves);
     int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT, main);
+    const size_t xn_lds = xn_lds_bytes(T, d.hidden);
     if (T <= 2)
-        hipLaunchKernelGGL((decode_router_kernel<2>), router_grid, dim3(kFrontThreads),
-                           (size_t)T * d.hidden * 2, main, r);
+        hipLaunchKernelGGL((decode_router_kernel<2>), router_grid, dim3(kFrontThreads), xn_lds,
+                           main, r);
     else
         hipLaunchKernelGGL((decode_router_kernel<kMaxDecodeTokens>), router_grid,
-                           dim3(kFrontThreads), (size_t)T * d.hidden * 2, main, r);
+                           dim3(kFrontThreads), xn_lds, main, r);
     end_stage(ctx, mark, main);
 
     if (S) {
@@ -927,7 +1021,7 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
         sg.status = ctx->status;
         mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP, side);
         hipLaunchKernelGGL(decode_shared_gateup_kernel, dim3(S / 16), dim3(64 * kSharedGuWaves),
-                           (size_t)T * d.hidden * 2, side, sg);
+                           xn_lds, side, sg);
         end_stage(ctx, mark, side);
         SharedDownArgs sd{};
         sd.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
@@ -985,26 +1079,12 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.act = b.act;
     gu.glu = glu;
     gu.status = ctx->status;
-    // Split K over two waves only while every workgroup of the launch fits
-    // on the device at once; otherwise the extra waves run as a second,
-    // partly empty round.
-    if (!ctx->gateup_split_blocks) {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_gateup_kernel<2>, 512,
-                                                         0) != hipSuccess)
-            (void)hipGetLastError();
-        ctx->gateup_split_blocks = (uint32_t)std::max(per_cu, 0) * ctx->cu_count + 1;
-    }
-    const uint32_t gu_blocks = max_active * (d.inter / 64);
+    const uint32_t gu_blocks = max_active * (d.inter / 16);
     mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP, main);
-    if (gu_blocks < ctx->gateup_split_blocks)
-        hipLaunchKernelGGL((decode_gateup_kernel<2>), dim3(gu_blocks), dim3(512), 0, main, gu);
-    else
-        hipLaunchKernelGGL((decode_gateup_kernel<1>), dim3(gu_blocks), dim3(256), 0, main, gu);
+    hipLaunchKernelGGL((decode_gateup_kernel<kGateUpDepth>), dim3(gu_blocks), dim3(64), 0, main,
+                       gu);
     end_stage(ctx, mark, main);
 
-    if (S && hipStreamWaitEvent(main, ctx->join_event, 0) != hipSuccess)
-        return K3X_ERR_BACKEND_UNAVAILABLE;
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
     dn.dn_scales = bank->dn_scales;
@@ -1014,24 +1094,35 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.ks = bank->down.ks;
     dn.I = d.inter;
     dn.H = d.hidden;
-    dn.T = T;
     dn.K = K;
     dn.act = b.act;
     dn.n_active = b.n_active;
     dn.arec = b.arec;
     dn.pair_token = b.pair_token;
     dn.pair_slot = b.pair_slot;
-    dn.weights = b.weights;
-    dn.shared_y = S ? b.sy : nullptr;
     dn.y = b.y;
-    dn.out = out;
-    dn.out_f32 = out_f32;
     dn.status = ctx->status;
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN, main);
-    hipLaunchKernelGGL(decode_down_kernel, dim3(d.hidden / 16), dim3(64 * kDownWaves), 0, main,
-                       dn);
+    hipLaunchKernelGGL((decode_down_kernel<kDownDepth>), dim3(max_active * (d.hidden / 16)),
+                       dim3(64), 0, main, dn);
     end_stage(ctx, mark, main);
-    ctx->kernel_launches += S ? 6 : 4;
+
+    if (S && hipStreamWaitEvent(main, ctx->join_event, 0) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    CombineArgs cb{};
+    cb.y = b.y;
+    cb.weights = b.weights;
+    cb.shared_y = S ? b.sy : nullptr;
+    cb.K = K;
+    cb.H = d.hidden;
+    cb.out = out;
+    cb.out_f32 = out_f32;
+    cb.status = ctx->status;
+    mark = begin_stage(ctx, K3X_STAGE_COMBINE, main);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0, main,
+                       cb);
+    end_stage(ctx, mark, main);
+    ctx->kernel_launches += S ? 7 : 5;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 

@@ -29,9 +29,6 @@ struct k3x_hip_ctx {
     uint32_t* status = nullptr;  // device word, latched kernel errors
     size_t max_lds_per_block = 65536;
     uint32_t cu_count = 256;
-    // Workgroups of the K-split decode gate/up kernel the device holds at
-    // once, plus one (0 = not measured yet).
-    uint32_t gateup_split_blocks = 0;
     // Grow-only scratch (replaces runtime/cuda/device_memory.cuh:44-61).
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
