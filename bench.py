@@ -142,9 +142,10 @@ def main() -> int:
         "shared_gate_up": SHARED_GU_BYTES,
         "shared_down": SHARED_DOWN_BYTES,
         "route": ROUTER_BYTES + T * H * 2,
-        # decode path: front = xn + router logits; the shared expert runs on
-        # the side stream under the shared_gate_up / shared_down stages.
-        "decode_front": ROUTER_BYTES + T * H * 2,
+        # decode path: front = router + shared gate/up blocks; select =
+        # Top-K block + shared down blocks.
+        "decode_front": ROUTER_BYTES + SHARED_GU_BYTES + T * H * 2,
+        "decode_select": SHARED_DOWN_BYTES,
         "decode_gate_up": mean_d * GATE_UP_BYTES + T * H * 2,
         "decode_down": mean_d * DOWN_BYTES,
     }
@@ -158,7 +159,7 @@ def main() -> int:
             entry["gbps"] = round(stage_bytes[name] / (avg_us * 1e-6) / 1e9, 1)
         stage_report[name] = entry
     dom = max(("gate_up", "down", "shared_gate_up", "shared_down", "decode_front",
-               "decode_gate_up", "decode_down"),
+               "decode_select", "decode_gate_up", "decode_down"),
               key=lambda s: stage_report.get(s, {}).get("avg_us", 0.0))
     dom_us = stage_report[dom]["avg_us"]
     achieved = stage_bytes[dom] / (dom_us * 1e-6) / 1e9

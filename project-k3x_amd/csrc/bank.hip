@@ -272,11 +272,11 @@ hipEvent_t take_event(k3x_hip_ctx* ctx) {
 // Marks kept pending before a forced read-back (bounds the event pool).
 constexpr size_t kMaxPendingMarks = 1u << 16;
 
-int begin_stage(k3x_hip_ctx* ctx, uint32_t stage, hipStream_t stream) {
+int begin_stage(k3x_hip_ctx* ctx, uint32_t stage) {
     if (!ctx->profiling || stage >= K3X_STAGE_COUNT) return -1;
     if (ctx->pending.size() >= kMaxPendingMarks && drain_stage_marks(ctx) != K3X_OK) return -1;
     StageMark m{stage, take_event(ctx), take_event(ctx)};
-    if (!m.start || !m.stop || hipEventRecord(m.start, stream ? stream : ctx->stream) != hipSuccess) {
+    if (!m.start || !m.stop || hipEventRecord(m.start, ctx->stream) != hipSuccess) {
         (void)hipGetLastError();
         if (m.start) ctx->free_events.push_back(m.start);
         if (m.stop) ctx->free_events.push_back(m.stop);
@@ -286,9 +286,9 @@ int begin_stage(k3x_hip_ctx* ctx, uint32_t stage, hipStream_t stream) {
     return (int)ctx->pending.size() - 1;
 }
 
-void end_stage(k3x_hip_ctx* ctx, int mark, hipStream_t stream) {
+void end_stage(k3x_hip_ctx* ctx, int mark) {
     if (mark < 0 || (size_t)mark >= ctx->pending.size()) return;
-    if (hipEventRecord(ctx->pending[mark].stop, stream ? stream : ctx->stream) != hipSuccess) {
+    if (hipEventRecord(ctx->pending[mark].stop, ctx->stream) != hipSuccess) {
         (void)hipGetLastError();
         StageMark m = ctx->pending[mark];
         ctx->pending.erase(ctx->pending.begin() + mark);
@@ -299,9 +299,7 @@ void end_stage(k3x_hip_ctx* ctx, int mark, hipStream_t stream) {
 
 int drain_stage_marks(k3x_hip_ctx* ctx) {
     if (ctx->pending.empty()) return K3X_OK;
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess ||
-        hipStreamSynchronize(ctx->side_stream) != hipSuccess)
-        return K3X_ERR_BACKEND_UNAVAILABLE;
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     int st = K3X_OK;
     for (const StageMark& m : ctx->pending) {
         float ms = 0.0f;
@@ -349,9 +347,6 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
     ctx->device = device;
     int lds = 0, cus = 0;
     if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->fork_event, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->join_event, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
         hipMemset(ctx->status, 0, 256) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
@@ -359,9 +354,6 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
-        if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
-        if (ctx->fork_event) (void)hipEventDestroy(ctx->fork_event);
-        if (ctx->join_event) (void)hipEventDestroy(ctx->join_event);
         if (ctx->status) (void)hipFree(ctx->status);
         delete ctx;
         return K3X_ERR_BACKEND_UNAVAILABLE;
@@ -378,7 +370,6 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     if (ctx->live_banks) return K3X_ERR_INVALID_STATE;  // destroy the banks first
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->status) (void)hipFree(ctx->status);
     for (const StageMark& m : ctx->pending) {
@@ -387,9 +378,6 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     }
     for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
-    if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
-    if (ctx->fork_event) (void)hipEventDestroy(ctx->fork_event);
-    if (ctx->join_event) (void)hipEventDestroy(ctx->join_event);
     delete ctx;
     return K3X_OK;
 }

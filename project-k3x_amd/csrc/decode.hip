@@ -1,13 +1,15 @@
-// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): seven
-// launches on two streams, no cross-workgroup synchronisation inside any of
-// them.
+// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): five
+// launches, no cross-workgroup synchronisation inside any of them.
 //
-// Context stream (the routing chain):
-//   decode_router_kernel  every block rebuilds xn = bf16(RMSNorm(x) * gamma)
-//                         in LDS and streams the fp32 router, one wave per
-//                         expert row (fp64, canonical order), into logits.
-//   decode_select_kernel  sigmoid + bias Top-K of every token and the
-//                         expert-major grouping (one block).
+//   decode_front_kernel   router blocks rebuild xn = bf16(RMSNorm(x) * gamma)
+//                         in LDS and stream the fp32 router, one wave per
+//                         expert row (fp64, canonical order), into logits;
+//                         shared blocks (same xn prologue) stream the bf16
+//                         shared-expert gate/up, K split over the waves, and
+//                         write the shared activation bf16(GLU(gate, up)).
+//   decode_select_kernel  block 0: sigmoid + bias Top-K of every token and
+//                         the expert-major grouping; the other blocks stream
+//                         the bf16 shared down projection.
 //   decode_gateup_kernel  routed MXFP4 gate/up + GLU: one wave per (active
 //                         expert, 16-row block), weights dequantised in
 //                         registers.
@@ -15,13 +17,8 @@
 //                         expert, 16-row block) -> per-pair rows y.
 //   decode_combine_kernel out = bf16(sum over slots in router order of w * y
 //                         + shared).
-// Side stream (the shared expert, which needs only xn):
-//   decode_shared_gateup_kernel  bf16 shared gate/up + GLU, one 16-row block
-//                         of S per workgroup, K split over 16 waves.
-//   decode_shared_down_kernel    bf16 shared down, one 16-row block of H per
-//                         workgroup, K split over four waves.
-// The side stream forks from the context stream at entry and joins it before
-// the combine, so its ~90 MB overlap the router and Top-K steps, which leave
+// The shared expert needs only xn, so it rides along as extra workgroups of
+// the two latency-bound launches (router, Top-K), whose own blocks leave
 // most of the device idle.
 //
 // Streaming loops keep several steps of loads in flight per wave with no
@@ -245,32 +242,41 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
 inline size_t xn_lds_bytes(uint32_t T, uint32_t H) { return (size_t)T * H * 2 + (size_t)H * 4; }
 
 // ---------------------------------------------------------------------------
-// Router kernel: xn and router logits
+// Front kernel: xn, router logits (router blocks) and the shared expert's
+// gate/up + GLU (shared blocks)
 // ---------------------------------------------------------------------------
-struct RouterArgs {
+struct FrontArgs {
     const uint16_t* x;
     const float* gamma;
     const float* router_w;  // [E][H] fp32
-    uint32_t T, H, E;
+    uint32_t T, H, E, S;
     float eps;
+    uint32_t router_blocks;
+    const uint4* sh_gu;     // shared gate/up tiles [S/16][H/128][2][4][64] x 16 B
+    GluParams glu;
     uint16_t* xn;           // [T][H] global copy (block 0 writes it)
     float* logits;          // [T][E]
+    uint16_t* sact;         // [T][S] bf16 shared activation
     uint32_t* status;
 };
 
 constexpr int kRouterBatch = 14;  // float4 row loads per lane per buffer (two buffers)
 
-// One wave per expert row.  The wave's first two batches of row loads are
-// issued before the xn prologue, so the row fetch overlaps it; each partial
-// 4l + c still accumulates j = 0, 1, ... in order (canonical order).
-// TT bounds the token count (register arrays sized by it).
+struct FrontLds {
+    NormShared ns;
+    f32x4 red[kFrontWaves][2][64];  // shared blocks: K-split partials
+};
+
+// Router block: one wave per expert row.  The wave's first two batches of
+// row loads are issued before the xn prologue, so the row fetch overlaps
+// it; each partial 4l + c still accumulates j = 0, 1, ... in order (the
+// canonical order).  TT bounds the token count (register arrays sized by it).
 template <int TT>
-__global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs a) {
-    extern __shared__ uint4 dyn_lds[];
-    __shared__ NormShared ns;
+__device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, uint4* dyn_lds,
+                                             NormShared& ns) {
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.T, H = a.H, J = H / 256;
-    const uint32_t e = blockIdx.x * kFrontWaves + wave;
+    const uint32_t e = blk * kFrontWaves + wave;
     const bool row = e < a.E;
     // Loads are unconditional (a row past E reads row 0, a batch index past
     // the row end reads its last chunk; neither is used), so that they are
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs
         }
     if (prior_status(a.status)) return;
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, ns,
-                                 blockIdx.x == 0 ? a.xn : nullptr, a.status))
+                                 blk == 0 ? a.xn : nullptr, a.status))
         return;
     if (!row) return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
@@ -331,45 +337,20 @@ __global__ __launch_bounds__(kFrontThreads) void decode_router_kernel(RouterArgs
     }
 }
 
-// ---------------------------------------------------------------------------
-// Shared expert (side stream): gate/up + GLU, then down
-// ---------------------------------------------------------------------------
-constexpr int kSharedGuWaves = 16;  // K split of one 16-row block of the shared gate/up
-constexpr int kSharedDnWaves = 4;   // K split of one 16-row block of the shared down
-
-struct SharedGateUpArgs {
-    const uint16_t* x;
-    const float* gamma;
-    uint32_t T, H, S;
-    float eps;
-    const uint4* sh_gu;  // shared gate/up tiles [S/16][H/128][2][4][64] x 16 B
-    GluParams glu;
-    uint16_t* sact;      // [T][S] bf16 shared activation
-    const uint32_t* status;
-};
-
-struct SharedGateUpLds {
-    NormShared ns;
-    f32x4 red[kSharedGuWaves][2][64];
-};
-
-// Workgroup = one 16-row block of S and the whole K = H range, split over
-// 16 waves (first weight tile requested before the xn prologue); the wave
-// partials are added in a fixed tree in LDS (wave w += wave w + h for
-// h = 8, 4, 2, 1) and the block writes sact = bf16(GLU(gate, up)) for its 16
-// columns.
-__global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kernel(
-    SharedGateUpArgs a) {
-    extern __shared__ uint4 dyn_lds[];
-    __shared__ SharedGateUpLds sh;
+// Shared gate/up block: one 16-row block rb of S and the whole K = H range,
+// split over the eight waves (two tiles of registers in flight per wave, the
+// first two requested before the xn prologue, refills clamped to the last
+// tile); the wave partials are added in a fixed tree in LDS (wave w += wave
+// w + h for h = 4, 2, 1) and the block writes sact = bf16(GLU(gate, up)) for
+// its 16 columns.
+__device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t rb,
+                                                    uint4* dyn_lds, FrontLds& sh) {
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t T = a.T, H = a.H, rb = blockIdx.x, kt = H / 128;
-    const uint32_t k0 = wave * kt / kSharedGuWaves, k1 = (wave + 1) * kt / kSharedGuWaves;
+    const uint32_t T = a.T, H = a.H, kt = H / 128;
+    const uint32_t k0 = wave * kt / kFrontWaves, k1 = (wave + 1) * kt / kFrontWaves;
     const uint32_t N = k1 - k0;
     const uint4* tiles = a.sh_gu + (size_t)rb * kt * 2 * 4 * 64 + lane;
-    // Two tiles of registers in flight, the first two requested before the
-    // xn prologue; refills clamped to the last tile (no branch in the loop).
     constexpr int PD = 2;
     uint4 bn[PD][2][4];
     auto load = [&](uint4 (&b)[2][4], uint32_t k) {
@@ -382,8 +363,8 @@ __global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kern
 #pragma unroll
         for (int d = 0; d < PD; ++d) load(bn[d], k0 + min((uint32_t)d, N - 1));
     if (prior_status(a.status)) return;
-    // A non-finite x is reported by the router kernel.
-    if (!build_xn<64 * kSharedGuWaves>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr))
+    // A non-finite x is reported by the router blocks.
+    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr))
         return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
     const uint16_t* xrow = s_x + (size_t)(n < T ? n : 0) * H + 32 * g;  // unused rows: row 0
@@ -391,7 +372,8 @@ __global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kern
     auto step = [&](const uint4 (&b)[2][4], uint32_t k) {
         bf16x8 af[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) af[j] = as_bf16x8(*reinterpret_cast<const uint4*>(xrow + k * 128 + 8 * j));
+        for (int j = 0; j < 4; ++j)
+            af[j] = as_bf16x8(*reinterpret_cast<const uint4*>(xrow + k * 128 + 8 * j));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -413,7 +395,7 @@ __global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kern
     sh.red[wave][0][lane] = acc[0];
     sh.red[wave][1][lane] = acc[1];
 #pragma unroll
-    for (uint32_t h = kSharedGuWaves / 2; h >= 1; h /= 2) {
+    for (uint32_t h = kFrontWaves / 2; h >= 1; h /= 2) {
         __syncthreads();
         if (wave < h) {
             sh.red[wave][0][lane] = sh.red[wave][0][lane] + sh.red[wave + h][0][lane];
@@ -429,73 +411,21 @@ __global__ __launch_bounds__(64 * kSharedGuWaves) void decode_shared_gateup_kern
     }
 }
 
-struct SharedDownArgs {
-    const uint4* sh_dn;    // shared down tiles [H/16][S/128][4][64] x 16 B
-    const uint16_t* sact;  // [T][S]
-    uint32_t T, H, S;
-    float* sy;             // [T][H] shared expert output, fp32
-    const uint32_t* status;
-};
-
-// Workgroup = one 16-row block of H, K = S split over four waves (up to
-// four tiles in flight per wave, refills clamped to the last tile), partials
-// added pairwise: (w0 + w1) + (w2 + w3).
-__global__ __launch_bounds__(64 * kSharedDnWaves) void decode_shared_down_kernel(SharedDownArgs a) {
-    __shared__ f32x4 red[kSharedDnWaves][64];
-    if (prior_status(a.status)) return;
-    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
-    const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t rb = blockIdx.x, skt = a.S / 128;
-    const uint32_t k0 = wave * skt / kSharedDnWaves, k1 = (wave + 1) * skt / kSharedDnWaves;
-    const uint32_t N = k1 - k0;
-    const uint4* tiles = a.sh_dn + (size_t)rb * skt * 4 * 64 + lane;
-    const bool arow = n < a.T;
-    const uint16_t* ap = a.sact + (size_t)(arow ? n : 0) * a.S + 32 * g;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int PD = 4;
-    struct Step {
-        uint4 b[4], av[4];
-    };
-    auto load = [&](Step& r, uint32_t k) {
-        load_act(ap, arow, k, r.av);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r.b[j] = tiles[((size_t)k * 4 + j) * 64];
-    };
-    auto step = [&](const Step& r) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(r.av[j]), as_bf16x8(r.b[j]), acc);
-    };
-    if (N) {
-        Step r[PD];
-#pragma unroll
-        for (int d = 0; d < PD; ++d) {
-            r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
-            load(r[d], k0 + min((uint32_t)d, N - 1));
-        }
-        uint32_t kb = 0;
-        for (; kb + PD <= N; kb += PD) {
-#pragma unroll
-            for (int d = 0; d < PD; ++d) {
-                step(r[d]);
-                load(r[d], k0 + min(kb + d + PD, N - 1));
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < PD; ++d)
-            if (kb + d < N) step(r[d]);
-    }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    const f32x4 tot = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t t = 4 * g + q;
-        if (t < a.T) a.sy[(size_t)t * a.H + rb * 16 + n] = tot[q];
-    }
+// Blocks [0, router_blocks) are router blocks, the rest shared gate/up
+// blocks (16-row block rb = block - router_blocks).
+template <int TT>
+__global__ __launch_bounds__(kFrontThreads) void decode_front_kernel(FrontArgs a) {
+    extern __shared__ uint4 dyn_lds[];
+    __shared__ FrontLds sh;
+    if (blockIdx.x < a.router_blocks)
+        router_block<TT>(a, blockIdx.x, dyn_lds, sh.ns);
+    else
+        shared_gateup_block(a, blockIdx.x - a.router_blocks, dyn_lds, sh);
 }
+
 // ---------------------------------------------------------------------------
-// Select kernel: Top-K + expert-major grouping (one block)
+// Select kernel: Top-K + expert-major grouping (block 0) and the shared
+// expert's down projection (the other blocks)
 // ---------------------------------------------------------------------------
 struct SelectArgs {
     const float* logits;
@@ -514,6 +444,10 @@ struct SelectArgs {
     uint32_t* active_asc;
     uint32_t* active_fu;
     uint4* arec;         // [E] per active slot: {expert, rows, offset, row tokens}
+    const uint4* sh_dn;  // shared down tiles [H/16][S/128][4][64] x 16 B
+    const uint16_t* sact;  // [T][S]
+    uint32_t H, S;
+    float* sy;           // [T][H] shared expert output, fp32
     uint32_t* status;
 };
 
@@ -706,16 +640,87 @@ __device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
     }
 }
 
+// Shared down block: one 16-row block rb of H, K = S split over the eight
+// waves (up to two tiles in flight per wave, refills clamped to the last
+// tile), partials added in a fixed tree in LDS (wave w += wave w + h for
+// h = 4, 2, 1).
+__device__ __forceinline__ void shared_down_block(const SelectArgs& a, uint32_t rb,
+                                                  f32x4 (&red)[kFrontWaves][64]) {
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t skt = a.S / 128;
+    const uint32_t k0 = wave * skt / kFrontWaves, k1 = (wave + 1) * skt / kFrontWaves;
+    const uint32_t N = k1 - k0;
+    const uint4* tiles = a.sh_dn + (size_t)rb * skt * 4 * 64 + lane;
+    const bool arow = n < a.T;
+    const uint16_t* ap = a.sact + (size_t)(arow ? n : 0) * a.S + 32 * g;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    constexpr int PD = 2;
+    struct Step {
+        uint4 b[4], av[4];
+    };
+    auto load = [&](Step& r, uint32_t k) {
+        load_act(ap, arow, k, r.av);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.b[j] = tiles[((size_t)k * 4 + j) * 64];
+    };
+    auto step = [&](const Step& r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(r.av[j]), as_bf16x8(r.b[j]), acc);
+    };
+    if (N) {
+        Step r[PD];
+#pragma unroll
+        for (int d = 0; d < PD; ++d) {
+            r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
+            load(r[d], k0 + min((uint32_t)d, N - 1));
+        }
+        uint32_t kb = 0;
+        for (; kb + PD <= N; kb += PD) {
+#pragma unroll
+            for (int d = 0; d < PD; ++d) {
+                step(r[d]);
+                load(r[d], k0 + min(kb + d + PD, N - 1));
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < PD; ++d)
+            if (kb + d < N) step(r[d]);
+    }
+    red[wave][lane] = acc;
+#pragma unroll
+    for (uint32_t h = kFrontWaves / 2; h >= 1; h /= 2) {
+        __syncthreads();
+        if (wave < h) red[wave][lane] = red[wave][lane] + red[wave + h][lane];
+    }
+    if (wave != 0) return;
+    const f32x4 tot = red[0][lane];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t t = 4 * g + q;
+        if (t < a.T) a.sy[(size_t)t * a.H + rb * 16 + n] = tot[q];
+    }
+}
+
+union SelectLds {
+    SelectShared sel;
+    f32x4 red[kFrontWaves][64];
+};
+
 __global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a) {
-    __shared__ SelectShared sh;
+    __shared__ SelectLds sh;
     if (prior_status(a.status)) return;
+    if (blockIdx.x) {
+        shared_down_block(a, blockIdx.x - 1, sh.red);
+        return;
+    }
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
-    if (tid == 0) sh.bad = 0;
+    if (tid == 0) sh.sel.bad = 0;
     __syncthreads();
-    if (wave < a.T) topk_token(a, wave, sh);
+    if (wave < a.T) topk_token(a, wave, sh.sel);
     __syncthreads();
-    if (sh.bad) return;
-    group_pairs(a, sh);
+    if (sh.sel.bad) return;
+    group_pairs(a, sh.sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -943,10 +948,7 @@ namespace k3x_hip {
 
 namespace {
 
-size_t router_lds(uint32_t T, uint32_t H) { return xn_lds_bytes(T, H) + sizeof(NormShared); }
-size_t shared_gateup_lds(uint32_t T, uint32_t H) {
-    return xn_lds_bytes(T, H) + sizeof(SharedGateUpLds);
-}
+size_t front_lds(uint32_t T, uint32_t H) { return xn_lds_bytes(T, H) + sizeof(FrontLds); }
 
 // Steps of loads in flight per wave in the routed gate/up and down loops.
 constexpr int kGateUpDepth = 3;
@@ -960,84 +962,50 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
                      const k3x_hip_moe_params* p, const void* x) {
     const auto& d = bank->desc;
     if (reinterpret_cast<uintptr_t>(x) % 16) return false;  // 16-byte input loads
-    const size_t lds = std::max(router_lds(p->tokens, d.hidden),
-                                shared_gateup_lds(p->tokens, d.hidden));
+    const size_t lds = front_lds(p->tokens, d.hidden);
     return p->tokens <= (uint32_t)kMaxDecodeTokens && lds <= ctx->max_lds_per_block &&
            d.hidden % 256 == 0 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
            p->top_k <= 64 && p->tokens * p->top_k <= (uint32_t)kMaxDecodePairs &&
            d.inter % 64 == 0 && d.shared_inter % 256 == 0;
 }
 
-// Launch order: the router, Top-K/grouping and routed gate/up run on the
-// context stream; the shared expert, which needs only xn, runs on the
-// context's side stream from a fork event recorded at entry, so it overlaps
-// the latency-bound router and Top-K steps.  The routed down/combine kernel
-// waits for the side stream's join event.  The next call's side work is
-// ordered after this call's combine by its own fork event, so the per-call
-// buffers are never written while still being read.
+// Five launches on the context stream.  The shared expert, which needs only
+// xn, rides along as extra workgroups of the two latency-bound launches: its
+// gate/up blocks beside the router blocks, its down blocks beside the Top-K
+// block, so its ~90 MB stream while those steps wait on latency.
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                    const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k, S = d.shared_inter;
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
-    hipStream_t main = ctx->stream, side = ctx->side_stream;
-    if (S && (hipEventRecord(ctx->fork_event, main) != hipSuccess ||
-              hipStreamWaitEvent(side, ctx->fork_event, 0) != hipSuccess))
-        return K3X_ERR_BACKEND_UNAVAILABLE;
+    hipStream_t main = ctx->stream;
 
-    RouterArgs r{};
-    r.x = x;
-    r.gamma = bank->gamma;
-    r.router_w = bank->router_w;
-    r.T = T;
-    r.H = d.hidden;
-    r.E = d.experts;
-    r.eps = p->rms_epsilon;
-    r.xn = b.xn;
-    r.logits = b.logits;
-    r.status = ctx->status;
-    const dim3 router_grid((d.experts + kFrontWaves - 1) / kFrontWaves);
-    int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT, main);
+    FrontArgs f{};
+    f.x = x;
+    f.gamma = bank->gamma;
+    f.router_w = bank->router_w;
+    f.T = T;
+    f.H = d.hidden;
+    f.E = d.experts;
+    f.S = S;
+    f.eps = p->rms_epsilon;
+    f.router_blocks = (d.experts + kFrontWaves - 1) / kFrontWaves;
+    f.sh_gu = reinterpret_cast<const uint4*>(bank->sh_gu);
+    f.glu = glu;
+    f.xn = b.xn;
+    f.logits = b.logits;
+    f.sact = b.sact;
+    f.status = ctx->status;
+    const dim3 front_grid(f.router_blocks + S / 16);
     const size_t xn_lds = xn_lds_bytes(T, d.hidden);
+    int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT);
     if (T <= 2)
-        hipLaunchKernelGGL((decode_router_kernel<2>), router_grid, dim3(kFrontThreads), xn_lds,
-                           main, r);
+        hipLaunchKernelGGL((decode_front_kernel<2>), front_grid, dim3(kFrontThreads), xn_lds,
+                           main, f);
     else
-        hipLaunchKernelGGL((decode_router_kernel<kMaxDecodeTokens>), router_grid,
-                           dim3(kFrontThreads), xn_lds, main, r);
-    end_stage(ctx, mark, main);
-
-    if (S) {
-        SharedGateUpArgs sg{};
-        sg.x = x;
-        sg.gamma = bank->gamma;
-        sg.T = T;
-        sg.H = d.hidden;
-        sg.S = S;
-        sg.eps = p->rms_epsilon;
-        sg.sh_gu = reinterpret_cast<const uint4*>(bank->sh_gu);
-        sg.glu = glu;
-        sg.sact = b.sact;
-        sg.status = ctx->status;
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP, side);
-        hipLaunchKernelGGL(decode_shared_gateup_kernel, dim3(S / 16), dim3(64 * kSharedGuWaves),
-                           xn_lds, side, sg);
-        end_stage(ctx, mark, side);
-        SharedDownArgs sd{};
-        sd.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
-        sd.sact = b.sact;
-        sd.T = T;
-        sd.H = d.hidden;
-        sd.S = S;
-        sd.sy = b.sy;
-        sd.status = ctx->status;
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN, side);
-        hipLaunchKernelGGL(decode_shared_down_kernel, dim3(d.hidden / 16),
-                           dim3(64 * kSharedDnWaves), 0, side, sd);
-        end_stage(ctx, mark, side);
-        if (hipEventRecord(ctx->join_event, side) != hipSuccess)
-            return K3X_ERR_BACKEND_UNAVAILABLE;
-    }
+        hipLaunchKernelGGL((decode_front_kernel<kMaxDecodeTokens>), front_grid,
+                           dim3(kFrontThreads), xn_lds, main, f);
+    end_stage(ctx, mark);
 
     SelectArgs sa{};
     sa.logits = b.logits;
@@ -1058,10 +1026,16 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     sa.active_asc = b.active_asc;
     sa.active_fu = b.active_fu;
     sa.arec = b.arec;
+    sa.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
+    sa.sact = b.sact;
+    sa.H = d.hidden;
+    sa.S = S;
+    sa.sy = b.sy;
     sa.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT, main);
-    hipLaunchKernelGGL(decode_select_kernel, dim3(1), dim3(kFrontThreads), 0, main, sa);
-    end_stage(ctx, mark, main);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT);
+    hipLaunchKernelGGL(decode_select_kernel, dim3(1 + (S ? d.hidden / 16 : 0)),
+                       dim3(kFrontThreads), 0, main, sa);
+    end_stage(ctx, mark);
 
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     GateUpArgs gu{};
@@ -1080,10 +1054,10 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.glu = glu;
     gu.status = ctx->status;
     const uint32_t gu_blocks = max_active * (d.inter / 16);
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP, main);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
     hipLaunchKernelGGL((decode_gateup_kernel<kGateUpDepth>), dim3(gu_blocks), dim3(64), 0, main,
                        gu);
-    end_stage(ctx, mark, main);
+    end_stage(ctx, mark);
 
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
@@ -1102,13 +1076,11 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.pair_slot = b.pair_slot;
     dn.y = b.y;
     dn.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN, main);
+    mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
     hipLaunchKernelGGL((decode_down_kernel<kDownDepth>), dim3(max_active * (d.hidden / 16)),
                        dim3(64), 0, main, dn);
-    end_stage(ctx, mark, main);
+    end_stage(ctx, mark);
 
-    if (S && hipStreamWaitEvent(main, ctx->join_event, 0) != hipSuccess)
-        return K3X_ERR_BACKEND_UNAVAILABLE;
     CombineArgs cb{};
     cb.y = b.y;
     cb.weights = b.weights;
@@ -1118,11 +1090,11 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     cb.out = out;
     cb.out_f32 = out_f32;
     cb.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_COMBINE, main);
+    mark = begin_stage(ctx, K3X_STAGE_COMBINE);
     hipLaunchKernelGGL(decode_combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0, main,
                        cb);
-    end_stage(ctx, mark, main);
-    ctx->kernel_launches += S ? 7 : 5;
+    end_stage(ctx, mark);
+    ctx->kernel_launches += 5;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 

@@ -21,11 +21,6 @@ struct k3x_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipStream_t own_stream = nullptr;
-    // Second stream of the decode path (shared expert) and its fork/join
-    // events; default priority, created with the context.
-    hipStream_t side_stream = nullptr;
-    hipEvent_t fork_event = nullptr;
-    hipEvent_t join_event = nullptr;
     uint32_t* status = nullptr;  // device word, latched kernel errors
     size_t max_lds_per_block = 65536;
     uint32_t cu_count = 256;
@@ -116,12 +111,10 @@ inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BA
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
 
 // Brackets the launches made between begin and end with an event pair when
-// profiling is on, recorded on `stream` (null: the context stream).
-// begin_stage returns the index of the open mark or -1.
-int begin_stage(k3x_hip_ctx* ctx, uint32_t stage, hipStream_t stream = nullptr);
-void end_stage(k3x_hip_ctx* ctx, int mark, hipStream_t stream = nullptr);
-// Reads back every pending mark into the per-stage totals (synchronises the
-// context and side streams).
+// profiling is on.  begin_stage returns the index of the open mark or -1.
+int begin_stage(k3x_hip_ctx* ctx, uint32_t stage);
+void end_stage(k3x_hip_ctx* ctx, int mark);
+// Reads back every pending mark into the per-stage totals (synchronises).
 int drain_stage_marks(k3x_hip_ctx* ctx);
 
 }  // namespace k3x_hip
