@@ -835,69 +835,75 @@ struct DownArgs {
     const uint32_t* status;
 };
 
-// Registers of one down step: codes, the scale dword of the tile's group,
-// the activation slice.
-struct DnStep {
-    uint4 c;
-    uint32_t s;
-    uint4 av[4];
-};
+// Workgroup = kDownWaves waves of one active slot ai, wave w taking 16-row
+// block rb = (block % (H / 64)) * 4 + w.  The slot's activation rows (cnt
+// rows of I bf16) are copied into LDS once by the whole block; their loads
+// are issued first, then each wave's code tiles (the whole K range, I <=
+// 2048) and scale dwords, all in flight together, so that a unit costs
+// about one memory round trip.  Every load is unconditional (indices
+// clamped; a clamped activation chunk is stored again with its own value),
+// so the compiler keeps them all in flight.  The rows of the slot's pairs
+// go to y.
+constexpr int kDownWaves = 4;
+constexpr int kDownTiles = 16;      // K tiles of the down projection: I <= 2048
+constexpr int kDownActLoads = 4;    // 16-byte activation loads per thread
 
-// One wave per workgroup and unit: active slot ai = block / (H / 16),
-// 16-row block rb = block % (H / 16), the whole K = I range with PD steps of
-// loads in flight (as the gate/up kernel); the rows of the slot's pairs go
-// to y.
-template <int PD>
-__global__ __launch_bounds__(64) void decode_down_kernel(DownArgs a) {
-    const uint32_t lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
+    extern __shared__ uint4 s_act4[];  // [cnt][I] bf16
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t per_expert = a.H / 16;
-    const uint32_t ai = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
+    const uint32_t per_expert = a.H / (16 * kDownWaves);
+    const uint32_t ai = blockIdx.x / per_expert;
+    const uint32_t rb = (blockIdx.x % per_expert) * kDownWaves + wave;
     const uint32_t st = prior_status(a.status);
     const uint32_t na = *a.n_active;
     const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
     if (st || ai >= na) return;
     const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
     const uint32_t kt = a.kt;
+    // 1. Activation rows: chunks c < cnt * I / 8 (at most kDownActLoads per
+    //    thread, checked by the host).
+    const uint32_t chunks = cnt * (a.I / 8);
+    const uint4* src = reinterpret_cast<const uint4*>(a.act + (size_t)off * a.I);
+    uint4 v[kDownActLoads];
+#pragma unroll
+    for (int i = 0; i < kDownActLoads; ++i) v[i] = src[min(tid + 64 * kDownWaves * i, chunks - 1)];
+    // 2. Code tiles and scale dwords of this wave's 16-row block.
     const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
     const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
-    const bool arow = n < cnt;
-    const uint16_t* ap = a.act + (size_t)(off + (arow ? n : 0u)) * a.I + 32 * g;
-    auto load = [&](DnStep& r, uint32_t k) {
-        load_act(ap, arow, k, r.av);
-        r.c = codes[(size_t)k * 64];
-        r.s = scales[(size_t)(k >> 2) * 64];
-    };
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    DnStep r[PD];
+    uint4 c[kDownTiles];
+    uint32_t sw[kDownTiles / 4];
 #pragma unroll
-    for (int d = 0; d < PD; ++d) {
-        r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
-        load(r[d], min((uint32_t)d, kt - 1));
-    }
-    uint32_t kb = 0;
-    for (; kb + PD <= kt; kb += PD) {
+    for (int i = 0; i < kDownTiles; ++i) c[i] = codes[(size_t)min((uint32_t)i, kt - 1) * 64];
 #pragma unroll
-        for (int d = 0; d < PD; ++d) {
-            const uint32_t k = kb + d;
-            acc = mxfp4_tile(r[d].c, e8m0_to_f32((r[d].s >> (8 * (k & 3))) & 0xffu), r[d].av, acc);
-            load(r[d], min(k + PD, kt - 1));
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < PD; ++d) {
-        const uint32_t k = kb + d;
-        if (k < kt)
-            acc = mxfp4_tile(r[d].c, e8m0_to_f32((r[d].s >> (8 * (k & 3))) & 0xffu), r[d].av, acc);
-    }
+    for (int i = 0; i < kDownTiles / 4; ++i) sw[i] = scales[(size_t)min((uint32_t)i, a.ks - 1) * 64];
+    // 3. Pair rows of the outputs (needed at the end).
+    uint32_t yrow[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t row = 4 * g + q;
-        if (row < cnt) {
-            const uint32_t rr = off + row;
-            a.y[((size_t)a.pair_token[rr] * a.K + a.pair_slot[rr]) * a.H + rb * 16 + n] = acc[q];
+        const uint32_t r = off + min(4 * g + q, cnt - 1);
+        yrow[q] = a.pair_token[r] * a.K + a.pair_slot[r];
+    }
+#pragma unroll
+    for (int i = 0; i < kDownActLoads; ++i) s_act4[min(tid + 64 * kDownWaves * i, chunks - 1)] = v[i];
+    __syncthreads();
+    const uint16_t* s_act = reinterpret_cast<const uint16_t*>(s_act4);
+    const uint16_t* arow = s_act + (size_t)(n < cnt ? n : 0) * a.I + 32 * g;  // unused rows: row 0
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kDownTiles; ++i) {
+        if ((uint32_t)i < kt) {
+            uint4 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[j] = *reinterpret_cast<const uint4*>(arow + (size_t)i * 128 + 8 * j);
+            const float sc = e8m0_to_f32((sw[i / 4] >> (8 * (i & 3))) & 0xffu);
+            acc = mxfp4_tile(c[i], sc, av, acc);
         }
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (4 * g + q < cnt) a.y[(size_t)yrow[q] * a.H + rb * 16 + n] = acc[q];
 }
 
 struct CombineArgs {
@@ -952,7 +958,6 @@ size_t front_lds(uint32_t T, uint32_t H) { return xn_lds_bytes(T, H) + sizeof(Fr
 
 // Steps of loads in flight per wave in the routed gate/up and down loops.
 constexpr int kGateUpDepth = 3;
-constexpr int kDownDepth = 4;
 // Pairs the decode path handles (T * K).
 constexpr uint32_t kMaxDecodePairs = 256;
 
@@ -966,7 +971,10 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
     return p->tokens <= (uint32_t)kMaxDecodeTokens && lds <= ctx->max_lds_per_block &&
            d.hidden % 256 == 0 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
            p->top_k <= 64 && p->tokens * p->top_k <= (uint32_t)kMaxDecodePairs &&
-           d.inter % 64 == 0 && d.shared_inter % 256 == 0;
+           d.inter % 128 == 0 && d.inter <= 128 * kDownTiles &&
+           d.hidden % (16 * kDownWaves) == 0 &&
+           (size_t)p->tokens * d.inter / 8 <= (size_t)64 * kDownWaves * kDownActLoads &&
+           d.shared_inter % 256 == 0;
 }
 
 // Five launches on the context stream.  The shared expert, which needs only
@@ -1077,8 +1085,8 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.y = b.y;
     dn.status = ctx->status;
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
-    hipLaunchKernelGGL((decode_down_kernel<kDownDepth>), dim3(max_active * (d.hidden / 16)),
-                       dim3(64), 0, main, dn);
+    hipLaunchKernelGGL(decode_down_kernel, dim3(max_active * (d.hidden / (16 * kDownWaves))),
+                       dim3(64 * kDownWaves), (size_t)T * d.inter * 2, main, dn);
     end_stage(ctx, mark);
 
     CombineArgs cb{};
