@@ -741,34 +741,22 @@ struct GateUpArgs {
     const uint32_t* status;
 };
 
-// Registers of one gate/up step (one 128-K tile of the gate and the up
-// block): codes, the scale dwords of the tile's group, the activation slice.
-struct GuStep {
-    uint4 c0, c1;
-    uint32_t s0, s1;
-    uint4 av[4];
-};
+// Workgroup = one unit (active slot ai = block / (I / 16), 16-row block rb =
+// block % (I / 16)) with the K range split over kGuWaves waves of at most
+// kGuTiles tiles each.  The xn rows of the slot's tokens are copied into LDS
+// by the whole block; their loads are issued first, then each wave's gate
+// and up code tiles and scale dwords, all in flight together (unconditional
+// loads, clamped indices), so a unit costs about one memory round trip.
+// Wave partials are added in a fixed tree in LDS (wave w += wave w + h for
+// h = 4, 2, 1) before the GLU.
+constexpr int kGuWaves = 8;
+constexpr int kGuTiles = 8;       // K tiles per wave: H <= 128 * 8 * 8
+constexpr int kGuActLoads = 7;    // 16-byte xn loads per thread: T * H / 8 <= 7 * 512
 
-__device__ inline void gu_load(GuStep& r, const uint4* codes, const uint32_t* scales,
-                               const uint16_t* ap, bool arow, uint32_t k) {
-    load_act(ap, arow, k, r.av);
-    r.c0 = codes[(size_t)k * 128];
-    r.c1 = codes[(size_t)k * 128 + 64];
-    r.s0 = scales[(size_t)(k >> 2) * 128];
-    r.s1 = scales[(size_t)(k >> 2) * 128 + 64];
-}
-
-// One wave per workgroup and per unit of work: active slot ai = block / (I /
-// 16), 16-row block rb = block % (I / 16), the whole K range.  Units this
-// small spread evenly over the CUs (with four-wave workgroups, 29 active
-// experts put four workgroups on some CUs and three on others, and the
-// fourth, youngest, finishes a third later).  PD steps of loads in flight: a
-// step's registers are refilled with step k + PD right after use (clamped to
-// the last step, so the loop body has no branch around a weight load), full
-// groups of PD steps in the loop and the remainder after it.
-template <int PD>
-__global__ __launch_bounds__(64) void decode_gateup_kernel(GateUpArgs a) {
-    const uint32_t lane = threadIdx.x;
+__global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs a) {
+    extern __shared__ uint4 s_x4[];  // [cnt][H] bf16
+    __shared__ f32x4 red[kGuWaves][2][64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t per_expert = a.I / 16;
     const uint32_t ai = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
@@ -778,41 +766,75 @@ __global__ __launch_bounds__(64) void decode_gateup_kernel(GateUpArgs a) {
     const uint32_t na = *a.n_active;
     const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
     if (st || ai >= na) return;
-    const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
-    const uint32_t kt = a.kt;
+    const uint32_t e = rec.x, cnt = rec.y, toks = rec.w;
+    const uint32_t H = a.H, kt = a.kt;
+    // 1. xn rows of the slot's tokens (cnt <= 4 rows): chunk c of row r.
+    const uint32_t rowc = H / 8, chunks = cnt * rowc;
+    uint4 v[kGuActLoads];
+#pragma unroll
+    for (int i = 0; i < kGuActLoads; ++i) {
+        const uint32_t c = min(tid + 64 * kGuWaves * i, chunks - 1);
+        const uint32_t r = (c >= rowc) + (c >= 2 * rowc) + (c >= 3 * rowc);
+        const uint32_t tok = (toks >> (8 * r)) & 0xffu;
+        v[i] = reinterpret_cast<const uint4*>(a.xn + (size_t)tok * H)[c - r * rowc];
+    }
+    // 2. This wave's K tiles [k0, k1) of the gate and up blocks, and the
+    //    scale dwords of the (at most three) groups they touch.
+    const uint32_t k0 = wave * kt / kGuWaves, k1 = (wave + 1) * kt / kGuWaves;
+    const uint32_t N = k1 - k0;
     const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
     const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
-    const bool arow = n < cnt;
-    const uint16_t* ap = a.xn + (size_t)(arow ? (rec.w >> (8 * n)) & 0xffu : 0u) * a.H + 32 * g;
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    GuStep r[PD];
+    uint4 c0[kGuTiles], c1[kGuTiles];
+    uint32_t s0[3], s1[3];
 #pragma unroll
-    for (int d = 0; d < PD; ++d) {
-        r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
-        gu_load(r[d], codes, scales, ap, arow, min((uint32_t)d, kt - 1));
+    for (int i = 0; i < kGuTiles; ++i) {
+        const size_t k = min(k0 + i, kt - 1);  // tiles past k1 are loaded, not used
+        c0[i] = codes[k * 128];
+        c1[i] = codes[k * 128 + 64];
     }
-    auto step = [&](const GuStep& q, uint32_t k) {
-        const uint32_t sh = 8 * (k & 3);
-        acc[0] = mxfp4_tile(q.c0, e8m0_to_f32((q.s0 >> sh) & 0xffu), q.av, acc[0]);
-        acc[1] = mxfp4_tile(q.c1, e8m0_to_f32((q.s1 >> sh) & 0xffu), q.av, acc[1]);
-    };
-    uint32_t kb = 0;
-    for (; kb + PD <= kt; kb += PD) {
 #pragma unroll
-        for (int d = 0; d < PD; ++d) {
-            step(r[d], kb + d);
-            gu_load(r[d], codes, scales, ap, arow, min(kb + d + PD, kt - 1));
+    for (int i = 0; i < 3; ++i) {
+        const size_t grp = min(k0 / 4 + i, a.ks - 1);
+        s0[i] = scales[grp * 128];
+        s1[i] = scales[grp * 128 + 64];
+    }
+#pragma unroll
+    for (int i = 0; i < kGuActLoads; ++i) s_x4[min(tid + 64 * kGuWaves * i, chunks - 1)] = v[i];
+    __syncthreads();
+    const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
+    const uint16_t* xrow = s_x + (size_t)(n < cnt ? n : 0) * H + 32 * g;  // unused rows: row 0
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < kGuTiles; ++i) {
+        if ((uint32_t)i < N) {
+            const uint32_t k = k0 + i, gi = (k >> 2) - (k0 >> 2), sh = 8 * (k & 3);
+            const uint32_t w0 = gi == 0 ? s0[0] : gi == 1 ? s0[1] : s0[2];
+            const uint32_t w1 = gi == 0 ? s1[0] : gi == 1 ? s1[1] : s1[2];
+            uint4 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[j] = *reinterpret_cast<const uint4*>(xrow + (size_t)k * 128 + 8 * j);
+            acc[0] = mxfp4_tile(c0[i], e8m0_to_f32((w0 >> sh) & 0xffu), av, acc[0]);
+            acc[1] = mxfp4_tile(c1[i], e8m0_to_f32((w1 >> sh) & 0xffu), av, acc[1]);
         }
     }
+    red[wave][0][lane] = acc[0];
+    red[wave][1][lane] = acc[1];
 #pragma unroll
-    for (int d = 0; d < PD; ++d)
-        if (kb + d < kt) step(r[d], kb + d);
+    for (uint32_t h = kGuWaves / 2; h >= 1; h /= 2) {
+        __syncthreads();
+        if (wave < h) {
+            red[wave][0][lane] = red[wave][0][lane] + red[wave + h][0][lane];
+            red[wave][1][lane] = red[wave][1][lane] + red[wave + h][1][lane];
+        }
+    }
+    if (wave != 0) return;
+    const f32x4 gs = red[0][0][lane], us = red[0][1][lane];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = 4 * g + i;
-        if (row >= cnt) continue;
-        const float v = glu(acc[0][i], acc[1][i], a.glu);
-        a.act[(size_t)(off + row) * a.I + rb * 16 + n] = f32_to_bf16(v);
+        if (row < cnt)
+            a.act[(size_t)(rec.z + row) * a.I + rb * 16 + n] = f32_to_bf16(glu(gs[i], us[i], a.glu));
     }
 }
 
@@ -956,8 +978,6 @@ namespace {
 
 size_t front_lds(uint32_t T, uint32_t H) { return xn_lds_bytes(T, H) + sizeof(FrontLds); }
 
-// Steps of loads in flight per wave in the routed gate/up and down loops.
-constexpr int kGateUpDepth = 3;
 // Pairs the decode path handles (T * K).
 constexpr uint32_t kMaxDecodePairs = 256;
 
@@ -972,6 +992,8 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
            d.hidden % 256 == 0 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
            p->top_k <= 64 && p->tokens * p->top_k <= (uint32_t)kMaxDecodePairs &&
            d.inter % 128 == 0 && d.inter <= 128 * kDownTiles &&
+           d.hidden <= 128 * kGuWaves * kGuTiles &&
+           (size_t)p->tokens * d.hidden / 8 <= (size_t)64 * kGuWaves * kGuActLoads &&
            d.hidden % (16 * kDownWaves) == 0 &&
            (size_t)p->tokens * d.inter / 8 <= (size_t)64 * kDownWaves * kDownActLoads &&
            d.shared_inter % 256 == 0;
@@ -1063,8 +1085,8 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.status = ctx->status;
     const uint32_t gu_blocks = max_active * (d.inter / 16);
     mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
-    hipLaunchKernelGGL((decode_gateup_kernel<kGateUpDepth>), dim3(gu_blocks), dim3(64), 0, main,
-                       gu);
+    hipLaunchKernelGGL(decode_gateup_kernel, dim3(gu_blocks), dim3(64 * kGuWaves),
+                       (size_t)T * d.hidden * 2, main, gu);
     end_stage(ctx, mark);
 
     DownArgs dn{};
