@@ -160,11 +160,16 @@ struct NormShared {
 // inv * gamma) in place; the block then holds xn as [T][H] bf16 at s_x4
 // (gamma follows as [H] fp32).  Returns false when x holds a non-finite
 // value (latched into *status when status is non-null).  Needs at least T
-// waves; xn_out, when non-null, receives a global copy.
-template <int kThreads>
+// waves; xn_out, when non-null, receives a global copy.  mid() runs once
+// the first batch of x / gamma loads is issued (the caller's weight
+// prefetch goes there: vector loads complete in order, so loads issued
+// before x / gamma would delay the prologue); then the latched error word of
+// earlier launches is checked (false, for the whole block, when it is set).
+template <int kThreads, typename Mid>
 __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, uint32_t T,
                                          uint32_t H, float eps, uint4* s_x4, NormShared& ns,
-                                         uint16_t* xn_out, uint32_t* status) {
+                                         uint16_t* xn_out, uint32_t* status,
+                                         const uint32_t* prior, Mid&& mid) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
     const uint32_t chunks = T * H / 8;          // x chunks; gamma chunks follow
@@ -183,6 +188,10 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
             const uint4* src = c < chunks ? reinterpret_cast<const uint4*>(x) + c
                                           : reinterpret_cast<const uint4*>(gamma) + (c - chunks);
             v[it] = *src;
+        }
+        if (c0 == 0) {
+            mid();
+            if (prior_status(prior)) return false;
         }
 #pragma unroll
         for (int it = 0; it < kLoads; ++it) s_x4[min(c0 + tid + kThreads * it, all - 1)] = v[it];
@@ -261,38 +270,44 @@ struct FrontArgs {
 };
 
 constexpr int kRouterBatch = 14;  // float4 row loads per lane per buffer (two buffers)
+constexpr int kRouterRows = 4;    // router rows per router block (waves 0-3; all 8 build xn)
+constexpr int kSharedGuDepth = 2; // shared gate/up tiles in flight per wave
 
 struct FrontLds {
     NormShared ns;
     f32x4 red[kFrontWaves][2][64];  // shared blocks: K-split partials
 };
 
-// Router block: one wave per expert row.  The wave's first two batches of
-// row loads are issued before the xn prologue, so the row fetch overlaps
-// it; each partial 4l + c still accumulates j = 0, 1, ... in order (the
+// Router block: waves 0-3 take one expert row each (fewer fp64 row waves
+// per SIMD), all eight build xn.  A row wave's first two batches of row
+// loads are issued right after the xn prologue's loads, so the row fetch
+// overlaps the prologue;
+// each partial 4l + c still accumulates j = 0, 1, ... in order (the
 // canonical order).  TT bounds the token count (register arrays sized by it).
 template <int TT>
 __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, uint4* dyn_lds,
                                              NormShared& ns) {
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.T, H = a.H, J = H / 256;
-    const uint32_t e = blk * kFrontWaves + wave;
-    const bool row = e < a.E;
+    const uint32_t e = blk * kRouterRows + wave;
+    const bool row = wave < (uint32_t)kRouterRows && e < a.E;
     // Loads are unconditional (a row past E reads row 0, a batch index past
     // the row end reads its last chunk; neither is used), so that they are
     // all in flight together.
     const float* wr = a.router_w + (size_t)(row ? e : 0) * H + 4 * lane;
     float4 wb[2][kRouterBatch];
+    auto prefetch = [&]() {
+        if (wave < (uint32_t)kRouterRows)  // wave-uniform
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int u = 0; u < kRouterBatch; ++u) {
-            const uint32_t j = min((uint32_t)(b * kRouterBatch + u), J - 1);
-            wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
-        }
-    if (prior_status(a.status)) return;
+                for (int u = 0; u < kRouterBatch; ++u) {
+                    const uint32_t j = min((uint32_t)(b * kRouterBatch + u), J - 1);
+                    wb[b][u] = *reinterpret_cast<const float4*>(wr + 256 * j);
+                }
+    };
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, ns,
-                                 blk == 0 ? a.xn : nullptr, a.status))
+                                 blk == 0 ? a.xn : nullptr, a.status, a.status, prefetch))
         return;
     if (!row) return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
@@ -338,9 +353,9 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
 }
 
 // Shared gate/up block: one 16-row block rb of S and the whole K = H range,
-// split over the eight waves (two tiles of registers in flight per wave, the
-// first two requested before the xn prologue, refills clamped to the last
-// tile); the wave partials are added in a fixed tree in LDS (wave w += wave
+// split over the eight waves (kSharedGuDepth tiles of registers in flight
+// per wave, the first ones requested during the xn prologue, refills
+// clamped to the last tile); the wave partials are added in a fixed tree in LDS (wave w += wave
 // w + h for h = 4, 2, 1) and the block writes sact = bf16(GLU(gate, up)) for
 // its 16 columns.
 __device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t rb,
@@ -351,7 +366,7 @@ __device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t
     const uint32_t k0 = wave * kt / kFrontWaves, k1 = (wave + 1) * kt / kFrontWaves;
     const uint32_t N = k1 - k0;
     const uint4* tiles = a.sh_gu + (size_t)rb * kt * 2 * 4 * 64 + lane;
-    constexpr int PD = 2;
+    constexpr int PD = kSharedGuDepth;
     uint4 bn[PD][2][4];
     auto load = [&](uint4 (&b)[2][4], uint32_t k) {
 #pragma unroll
@@ -359,12 +374,13 @@ __device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[w][j] = tiles[(((size_t)k * 2 + w) * 4 + j) * 64];
     };
-    if (N)
+    auto prefetch = [&]() {
 #pragma unroll
-        for (int d = 0; d < PD; ++d) load(bn[d], k0 + min((uint32_t)d, N - 1));
-    if (prior_status(a.status)) return;
+        for (int d = 0; d < PD; ++d) load(bn[d], min(k0 + d, kt - 1));
+    };
     // A non-finite x is reported by the router blocks.
-    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr))
+    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr,
+                                 a.status, prefetch))
         return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
     const uint16_t* xrow = s_x + (size_t)(n < T ? n : 0) * H + 32 * g;  // unused rows: row 0
@@ -466,7 +482,10 @@ struct SelectShared {
 // Scores, validation and renormalisation as runtime/src/routing_policy.cpp
 // :40-95,146-157 (FLOAT) or runtime/src/official_moe.cpp:214-242 (DOUBLE),
 // then * routed_scale (runtime/src/model.cpp:1004-1009).
-__device__ void topk_token(const SelectArgs& a, uint32_t t, SelectShared& sh) {
+// lg / bv: the token's logits and the bias of experts lane + 64 i (loaded
+// by the caller, before its status check).
+__device__ void topk_token(const SelectArgs& a, uint32_t t, const float (&lgv)[kKeysPerLane],
+                           const float (&bv)[kKeysPerLane], SelectShared& sh) {
     const int lane = threadIdx.x & 63;
     const uint32_t E = a.E, K = a.K;
     uint64_t key[kKeysPerLane];
@@ -478,8 +497,8 @@ __device__ void topk_token(const SelectArgs& a, uint32_t t, SelectShared& sh) {
         key[i] = 0;
         score[i] = 0.0f;
         if (e < E) {
-            const float lg = a.logits[(size_t)t * E + e];
-            const float b = a.bias[e];
+            const float lg = lgv[i];
+            const float b = bv[i];
             if (a.renorm == K3X_RENORM_DOUBLE &&
                 (!__builtin_isfinite(lg) || !__builtin_isfinite(b)))
                 bad = K3X_ERR_INVALID_EXTENT;
@@ -668,25 +687,24 @@ __device__ __forceinline__ void shared_down_block(const SelectArgs& a, uint32_t 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc = mfma16x16x32(as_bf16x8(r.av[j]), as_bf16x8(r.b[j]), acc);
     };
-    if (N) {
-        Step r[PD];
+    Step r[PD];
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+        r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
+        load(r[d], min(k0 + d, skt - 1));
+    }
+    if (prior_status(a.status)) return;  // the same value for the whole block
+    uint32_t kb = 0;
+    for (; kb + PD <= N; kb += PD) {
 #pragma unroll
         for (int d = 0; d < PD; ++d) {
-            r[d].av[0] = r[d].av[1] = r[d].av[2] = r[d].av[3] = make_uint4(0, 0, 0, 0);
-            load(r[d], k0 + min((uint32_t)d, N - 1));
+            step(r[d]);
+            load(r[d], min(k0 + kb + d + PD, skt - 1));
         }
-        uint32_t kb = 0;
-        for (; kb + PD <= N; kb += PD) {
-#pragma unroll
-            for (int d = 0; d < PD; ++d) {
-                step(r[d]);
-                load(r[d], k0 + min(kb + d + PD, N - 1));
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < PD; ++d)
-            if (kb + d < N) step(r[d]);
     }
+#pragma unroll
+    for (int d = 0; d < PD; ++d)
+        if (kb + d < N) step(r[d]);
     red[wave][lane] = acc;
 #pragma unroll
     for (uint32_t h = kFrontWaves / 2; h >= 1; h /= 2) {
@@ -709,15 +727,25 @@ union SelectLds {
 
 __global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a) {
     __shared__ SelectLds sh;
-    if (prior_status(a.status)) return;
     if (blockIdx.x) {
         shared_down_block(a, blockIdx.x - 1, sh.red);
         return;
     }
-    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    // The token's logits and the bias (wave t < T takes token t), loaded
+    // unconditionally (indices clamped) before the status check.
+    float lgv[kKeysPerLane], bv[kKeysPerLane];
+    const uint32_t t = min(wave, a.T - 1);
+#pragma unroll
+    for (int i = 0; i < kKeysPerLane; ++i) {
+        const uint32_t e = min(lane + 64u * i, a.E - 1);
+        lgv[i] = a.logits[(size_t)t * a.E + e];
+        bv[i] = a.bias[e];
+    }
+    if (prior_status(a.status)) return;
     if (tid == 0) sh.sel.bad = 0;
     __syncthreads();
-    if (wave < a.T) topk_token(a, wave, sh.sel);
+    if (wave < a.T) topk_token(a, wave, lgv, bv, sh.sel);
     __syncthreads();
     if (sh.sel.bad) return;
     group_pairs(a, sh.sel);
@@ -1019,7 +1047,7 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     f.E = d.experts;
     f.S = S;
     f.eps = p->rms_epsilon;
-    f.router_blocks = (d.experts + kFrontWaves - 1) / kFrontWaves;
+    f.router_blocks = (d.experts + kRouterRows - 1) / kRouterRows;
     f.sh_gu = reinterpret_cast<const uint4*>(bank->sh_gu);
     f.glu = glu;
     f.xn = b.xn;
