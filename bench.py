@@ -40,6 +40,13 @@ ROUTER_BYTES = E * H * 4 + E * 4 + H * 4               # weights + bias + gamma
 EXPERT_FLOPS = 2 * 3 * H * I                           # per (token, expert) pair
 SHARED_FLOPS = 2 * 3 * H * S                           # per token
 SEED, X_SEED = 0x4B3358, 0x5EED
+TRAFFIC_JSON_REL = "profiles/decode_c3_hbm_traffic.json"
+CALIB_BYTES = 256 << 20   # plain device copy used to scale the PMC byte counters
+# Bench stage -> kernel it times (for the PMC traffic of the dominant stage).
+STAGE_KERNEL = {"decode_front": "decode_front_kernel", "decode_select": "decode_select_kernel",
+                "decode_gate_up": "decode_gateup_kernel", "decode_down": "decode_down_kernel",
+                "combine": "decode_combine_kernel", "gate_up": "expert_gemm",
+                "down": "expert_gemm"}
 SCALE_LO, SCALE_HI = 119, 123
 
 
@@ -57,11 +64,19 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--prefill-steps", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
+                         "(counter calibration), then decode layer calls")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the FETCH_SIZE and WRITE_SIZE pass outputs into " + TRAFFIC_JSON_REL)
     return ap.parse_args()
 
 
 def main() -> int:
     args = parse()
+    if args.traffic_from:
+        print(json.dumps(traffic_from(*args.traffic_from)))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the layer and its resident "
                                    "bank live on a single MI355X (--gpus 1)",
@@ -93,6 +108,21 @@ def main() -> int:
     params = k3x_amd.make_params(T, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
                                  k3x_amd.RENORM_FLOAT)
     combos = np.lcm(args.layers, args.inputs)
+    if args.pmc_pass:
+        src = torch.empty(CALIB_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # the calibration copy: reads and writes CALIB_BYTES
+        torch.cuda.synchronize()
+        for i in range(max(args.steps, 8)):
+            k3x_amd.check(k3x_amd.moe_forward(ctx, banks[i % args.layers], params,
+                                              xs[i % args.inputs], out), "moe_forward")
+        k3x_amd.check(ctx.synchronize(), "pmc pass")
+        for b in banks:
+            b.close()
+        ctx.close()
+        log("pmc pass done")
+        return 0
 
     # Distinct experts each (layer, input) call touches, for the byte count.
     active = {}
@@ -163,6 +193,13 @@ def main() -> int:
               key=lambda s: stage_report.get(s, {}).get("avg_us", 0.0))
     dom_us = stage_report[dom]["avg_us"]
     achieved = stage_bytes[dom] / (dom_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, TRAFFIC_JSON_REL)
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            kern = json.load(f)["kernels"].get(STAGE_KERNEL.get(dom, ""))
+        if kern:
+            traffic = kern["hbm_bytes_per_dispatch"]
 
     result = {
         "metric": "MoE-layer µs @T=2 decode (HBM GB/s, %peak); MXFP4 TFLOPS @T=2048",
@@ -191,7 +228,9 @@ def main() -> int:
         "stages": stage_report,
         "roofline": {"bound": "hbm", "kernel": dom,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": round(stage_bytes[dom]),
+                     "traffic_source": TRAFFIC_JSON_REL if traffic else None},
     }
 
     if not args.no_prefill:
@@ -240,6 +279,58 @@ def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
             "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_floor_us": round(floor_us, 1),
             "frac_of_floor": round(floor_us / us, 4)}
+
+
+def traffic_from(fetch_dir: str, write_dir: str) -> dict:
+    """Per-dispatch HBM bytes of each decode kernel from two rocprofv3 --pmc
+    passes over `bench.py --pmc-pass` (FETCH_SIZE, then WRITE_SIZE, KiB per
+    dispatch), each scaled by what the same counter reads for the pass's
+    plain CALIB_BYTES device copy.  Writes TRAFFIC_JSON_REL."""
+    import csv
+    import glob
+    import statistics
+
+    def read(d: str, counter: str) -> dict:
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        per = {}
+        for fn in files:
+            with open(fn) as f:
+                for r in csv.DictReader(f):
+                    if r["Counter_Name"] != counter:
+                        continue
+                    name = r["Kernel_Name"]
+                    key = next((k for k in set(STAGE_KERNEL.values()) if k in name), None)
+                    if key is None and "copyBuffer" in name:
+                        key = "calibration_copy"
+                    if key:
+                        per.setdefault(key, []).append(float(r["Counter_Value"]))
+        return per
+
+    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    # The calibration copy is the largest copyBuffer dispatch of the pass.
+    cf, cw = max(fetch["calibration_copy"]), max(write["calibration_copy"])
+    kf, kw = CALIB_BYTES / (cf * 1024), CALIB_BYTES / (cw * 1024)
+    kernels = {}
+    for k in sorted(set(fetch) & set(write) - {"calibration_copy"}):
+        mf, mw = statistics.median(fetch[k]), statistics.median(write[k])
+        kernels[k] = {"dispatches": len(fetch[k]), "fetch_kib_median": round(mf, 1),
+                      "write_kib_median": round(mw, 1),
+                      "hbm_bytes_per_dispatch": round(mf * 1024 * kf + mw * 1024 * kw)}
+    out = {"workload": "bench.py --pmc-pass (c3 decode layer, T=2, banks cycled)",
+           "commands": ["rocprofv3 --pmc FETCH_SIZE --output-format csv -d <FETCH_DIR> -o run -- "
+                        "python3 bench.py --pmc-pass --steps 64",
+                        "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <WRITE_DIR> -o run -- "
+                        "python3 bench.py --pmc-pass --steps 64",
+                        "python3 bench.py --traffic-from <FETCH_DIR> <WRITE_DIR>"],
+           "calibration": {"copy_bytes": CALIB_BYTES, "fetch_kib": cf, "write_kib": cw,
+                           "fetch_scale": round(kf, 4), "write_scale": round(kw, 4)},
+           "kernels": kernels}
+    with open(os.path.join(ROOT, TRAFFIC_JSON_REL), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    return out
 
 
 def cpu_baseline() -> dict:
