@@ -103,8 +103,8 @@ typedef struct k3x_hip_moe_params {
 
 /* k3x_hip_moe_params.flags */
 enum k3x_flags {
-    /* Use the general multi-launch path even where the three-launch decode
-     * path (tokens <= 4) applies; both compute the same layer. */
+    /* Use the general multi-launch path even where the decode path
+     * (tokens <= 4) applies; both compute the same layer. */
     K3X_FLAG_GENERAL_PATH = 1u,
 };
 
