@@ -18,6 +18,10 @@ namespace k3x_dev {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+// Native 4 x 32-bit vector.  Register arrays that are carried around a loop
+// must use it rather than HIP's uint4 (a struct of unions), which the
+// compiler then keeps in scratch memory.
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
 constexpr int kWave = 64;
 constexpr int kTileRows = 16;
@@ -54,6 +58,7 @@ __device__ inline bf16x8 dequant8(uint32_t codes, float scale) {
 }
 
 __device__ inline bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ inline bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -1,0 +1,63 @@
+// k3x_gemm.hpp -- the wide expert GEMM (many rows per expert: prefill and
+// verification windows), shared by the general forward path.
+#pragma once
+
+#include <cstdint>
+
+#include "k3x_device.hpp"
+#include "k3x_internal.hpp"
+
+namespace k3x_hip {
+
+// One grouped GEMM launch.  Rows of expert e are the CSR rows [offsets[e],
+// offsets[e] + counts[e]); the launch's work items are the 128-row chunks
+// (e << 16 | chunk) of items[0, *n_items).  With items == nullptr there is
+// one "expert" of `tokens` rows at offset 0 (the shared expert) and item c
+// is its chunk c.
+struct WideGemmArgs {
+    const uint8_t* codes;        // expert 0 base of the tile array
+    const uint32_t* scales;      // MXFP4 only
+    size_t codes_per_expert;     // bytes
+    size_t scales_per_expert;    // dwords
+    uint32_t kt, ks;             // K tiles (K / 128), scale dword groups
+    uint32_t nrb;                // 16-row blocks of the output (N / 16)
+    const uint16_t* a;           // activation rows, bf16
+    uint32_t a_stride;           // elements per activation row
+    uint32_t gather;             // A row = pair_token[off + m] (1) or off + m (0)
+    const uint32_t* items;       // routed: (expert << 16 | chunk) work items
+    const uint32_t* n_items;
+    const uint32_t* counts;
+    const uint32_t* offsets;
+    const uint32_t* pair_token;
+    const uint32_t* pair_slot;
+    uint32_t tokens;
+    uint32_t top_k;
+    uint16_t* act;               // gate/up output [row][act_stride] bf16
+    uint32_t act_stride;
+    float* y;                    // down output [row][y_stride] fp32
+    uint32_t y_stride;
+    uint32_t scatter;            // y row = token * top_k + slot (1) or off + m (0)
+    k3x_dev::GluParams glu;
+    const uint32_t* status;
+};
+
+enum WideKind {
+    kWideRoutedGateUp = 0,  // MXFP4 gate + up, GLU -> bf16 act
+    kWideRoutedDown = 1,    // MXFP4 down -> fp32 y (scattered per pair)
+    kWideSharedGateUp = 2,  // bf16 gate + up, GLU -> bf16 act
+    kWideSharedDown = 3,    // bf16 down -> fp32 y
+};
+
+// Rows per workgroup chunk of the wide GEMM.
+constexpr uint32_t kWideRows = 128;
+
+// Output 16-row blocks one workgroup covers for `kind` (the launch needs
+// nrb to be a multiple of it).
+uint32_t wide_rb_per_block(WideKind kind);
+
+// Enqueues one wide GEMM on the context stream: max_items row chunks (an
+// upper bound of *n_items for the routed kinds) x the output row blocks,
+// one workgroup each.
+int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items);
+
+}  // namespace k3x_hip

@@ -103,6 +103,8 @@ struct LayerBuffers {
     float* sy;             // [T][H] shared expert output
     uint4* arec;           // [E] decode path: per active slot {expert, rows, CSR offset,
                            //     tokens of the rows, 8 bits each}
+    uint32_t* witems;      // wide GEMM work items (expert << 16 | 128-row chunk)
+    uint32_t* n_witems;    // [1]
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }

@@ -6,6 +6,7 @@
 //   group_kernel     expert-major CSR + first-use order         (bit-exact)
 //   expert_gemm      MXFP4/bf16 weights x bf16 activations on MFMA; gate/up
 //                    variant fuses the GLU, down variant scatters per pair
+//                    (few rows per expert; many rows: grouped_gemm.hip)
 //   combine_kernel   slot-ordered weighted sum + shared expert, bf16 cast
 #include <hip/hip_runtime.h>
 
@@ -15,6 +16,7 @@
 
 #include "k3x_decode.hpp"
 #include "k3x_device.hpp"
+#include "k3x_gemm.hpp"
 #include "k3x_internal.hpp"
 
 using namespace k3x_dev;
@@ -220,13 +222,17 @@ __global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logi
 // Rows are ranked with per-step token bitmaps: tokens are taken 64 (or
 // 1024/K) at a time, each pair's rank inside its expert is the running count
 // plus the popcount of earlier tokens of the step that chose the expert.
+// With witems non-null it also lists the (expert << 16 | row chunk) work
+// items of the wide GEMM, chunks of chunk_rows rows, in ascending expert order.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void group_kernel(
     const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
     uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets,
     uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot,
     uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
-    uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu, uint32_t* status) {
+    uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu,
+    uint32_t* __restrict__ witems, uint32_t* __restrict__ n_witems, uint32_t chunk_rows,
+    uint32_t* status) {
     extern __shared__ uint32_t smem[];
     uint32_t* cnt = smem;
     uint32_t* fu = cnt + E;
@@ -259,18 +265,22 @@ __global__ __launch_bounds__(1024) void group_kernel(
         return;
     }
     if (tid == 0) {
-        uint32_t acc = 0, na = 0;
+        uint32_t acc = 0, na = 0, ni = 0;
         for (uint32_t e = 0; e < E; ++e) {
             offsets[e] = acc;
             run[e] = acc;
             acc += cnt[e];
             if (cnt[e]) {
+                // Work items of the wide GEMM: (expert, row chunk).
+                if (witems)
+                    for (uint32_t c = 0; c * chunk_rows < cnt[e]; ++c) witems[ni++] = (e << 16) | c;
                 alist[na] = e;
                 active_asc[na++] = e;
             }
         }
         offsets[E] = acc;
         *n_active = na;
+        if (witems) *n_witems = ni;
         na_s = na;
     }
     __syncthreads();
@@ -496,9 +506,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 
 using Scratch = k3x_hip::LayerBuffers;
+using k3x_hip::begin_stage;
+using k3x_hip::end_stage;
+
+// Tokens from which the general path runs the wide grouped GEMM.
+constexpr uint32_t kWideMinTokens = 128;
 
 // Lays the per-call buffers out in the context scratch; returns bytes needed
 // (base == nullptr only measures).
+// Upper bound of the wide GEMM's (expert, chunk) items: every pair row in a
+// full chunk plus at most one partial chunk per active expert.
+uint32_t wide_max_items(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
+    const uint64_t P = (uint64_t)T * K;
+    return (uint32_t)(P / k3x_hip::kWideRows + std::min<uint64_t>(d.experts, P));
+}
+
 size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, Scratch* s) {
     size_t at = 0;
     auto take = [&](size_t bytes) {
@@ -524,6 +546,8 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->sact = (uint16_t*)take((size_t)T * d.shared_inter * 2);
     s->sy = (float*)take((size_t)T * d.hidden * 4);
     s->arec = (uint4*)take((size_t)d.experts * 16);
+    s->witems = (uint32_t*)take((size_t)wide_max_items(d, T, K) * 4);
+    s->n_witems = (uint32_t*)take(4);
     return at;
 }
 
@@ -554,11 +578,11 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
                  uint32_t* counts, uint32_t* offsets, uint32_t* pair_token, uint32_t* pair_slot,
                  uint32_t* first_use, uint32_t* n_active, uint32_t* active_asc,
-                 uint32_t* active_fu) {
+                 uint32_t* active_fu, uint32_t* witems = nullptr, uint32_t* n_witems = nullptr) {
     const size_t lds = (size_t)E * 6 * 4;
     hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), lds, ctx->stream, ids, T, K, E, counts,
                        offsets, pair_token, pair_slot, first_use, n_active, active_asc, active_fu,
-                       ctx->status);
+                       witems, n_witems, k3x_hip::kWideRows, ctx->status);
     return launched(ctx, 1);
 }
 
@@ -569,6 +593,113 @@ void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32
                        dim3(256), 0, ctx->stream, g);
 }
 
+// Many rows per expert: the wide grouped GEMM (128-row chunks, activations
+// staged in LDS) for the routed and the shared expert.  Shapes it needs: K
+// tile counts even, output rows a multiple of the workgroup's row blocks,
+// element offsets of the activation rows below 2^32.
+bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
+    using k3x_hip::wide_rb_per_block;
+    const uint64_t rows = (uint64_t)T * K;
+    return T >= kWideMinTokens && d.hidden % 256 == 0 && d.inter % 256 == 0 &&
+           (d.inter / 16) % wide_rb_per_block(k3x_hip::kWideRoutedGateUp) == 0 &&
+           (d.hidden / 16) % wide_rb_per_block(k3x_hip::kWideRoutedDown) == 0 &&
+           (!d.shared_inter ||
+            (d.shared_inter % 256 == 0 &&
+             (d.shared_inter / 16) % wide_rb_per_block(k3x_hip::kWideSharedGateUp) == 0 &&
+             (d.hidden / 16) % wide_rb_per_block(k3x_hip::kWideSharedDown) == 0)) &&
+           rows * std::max(d.hidden, std::max(d.inter, d.shared_inter)) < (1ull << 32);
+}
+
+int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+             const Scratch& s, const uint16_t* xn, const GluParams& glu) {
+    using namespace k3x_hip;
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens, K = p->top_k;
+    // Routed: one workgroup column per (expert, 128-row chunk) item the
+    // grouping listed (up to wide_max_items); shared: one per chunk of T.
+    const uint32_t all_chunks = (T + kWideRows - 1) / kWideRows;
+    const uint32_t routed_chunks = wide_max_items(d, T, K);
+    WideGemmArgs g{};
+    g.items = s.witems;
+    g.n_items = s.n_witems;
+    g.status = ctx->status;
+    g.glu = glu;
+    g.top_k = K;
+    g.counts = s.counts;
+    g.offsets = s.offsets;
+    g.pair_token = s.pair_token;
+    g.pair_slot = s.pair_slot;
+    g.codes = bank->gu_codes;
+    g.scales = bank->gu_scales;
+    g.codes_per_expert = bank->gu_codes_per_expert;
+    g.scales_per_expert = bank->gu_scales_per_expert;
+    g.kt = bank->gate.kt;
+    g.ks = bank->gate.ks;
+    g.nrb = d.inter / 16;
+    g.a = xn;
+    g.a_stride = d.hidden;
+    g.gather = 1;
+    g.act = s.act;
+    g.act_stride = d.inter;
+    int mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
+    int st = launch_wide_gemm(ctx, kWideRoutedGateUp, g, routed_chunks);
+    end_stage(ctx, mark);
+    if (st) return st;
+    if (d.shared_inter) {
+        WideGemmArgs sg = g;
+        sg.codes = bank->sh_gu;
+        sg.scales = nullptr;
+        sg.codes_per_expert = 0;
+        sg.kt = bank->sgate.kt;
+        sg.nrb = d.shared_inter / 16;
+        sg.gather = 0;
+        sg.items = nullptr;
+        sg.tokens = T;
+        sg.act = s.sact;
+        sg.act_stride = d.shared_inter;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP);
+        st = launch_wide_gemm(ctx, kWideSharedGateUp, sg, all_chunks);
+        end_stage(ctx, mark);
+        if (st) return st;
+    }
+    WideGemmArgs dn = g;
+    dn.codes = bank->dn_codes;
+    dn.scales = bank->dn_scales;
+    dn.codes_per_expert = bank->dn_codes_per_expert;
+    dn.scales_per_expert = bank->dn_scales_per_expert;
+    dn.kt = bank->down.kt;
+    dn.ks = bank->down.ks;
+    dn.nrb = d.hidden / 16;
+    dn.a = s.act;
+    dn.a_stride = d.inter;
+    dn.gather = 0;
+    dn.act = nullptr;
+    dn.y = s.y;
+    dn.y_stride = d.hidden;
+    dn.scatter = 1;
+    mark = begin_stage(ctx, K3X_STAGE_DOWN);
+    st = launch_wide_gemm(ctx, kWideRoutedDown, dn, routed_chunks);
+    end_stage(ctx, mark);
+    if (st) return st;
+    if (d.shared_inter) {
+        WideGemmArgs sd = dn;
+        sd.codes = bank->sh_dn;
+        sd.scales = nullptr;
+        sd.codes_per_expert = 0;
+        sd.kt = bank->sdown.kt;
+        sd.a = s.sact;
+        sd.a_stride = d.shared_inter;
+        sd.items = nullptr;
+        sd.tokens = T;
+        sd.y = s.sy;
+        sd.scatter = 0;
+        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN);
+        st = launch_wide_gemm(ctx, kWideSharedDown, sd, all_chunks);
+        end_stage(ctx, mark);
+    }
+    return st;
+}
+
 // Grouping, expert GEMMs, shared expert, combine.  xn is the bf16 input of
 // the experts; ids/weights [T][K] device.
 int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
@@ -576,16 +707,20 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              uint16_t* out, float* out_f32) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
-    using k3x_hip::begin_stage;
-    using k3x_hip::end_stage;
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
-                          s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu);
+                          s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu,
+                          s.witems, s.n_witems);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     const bool wide = T > 16;  // more than one 16-row MFMA tile per expert possible
     GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+    if (use_wide_gemm(d, T, K)) {
+        if ((st = run_wide(ctx, bank, p, s, xn, glu))) return st;
+        return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
+                                       d.hidden, T, out, out_f32);
+    }
 
     GemmArgs g{};
     g.status = ctx->status;
