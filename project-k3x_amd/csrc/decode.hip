@@ -207,7 +207,7 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 bad |= !__builtin_isfinite(f[c]);
-                p[c] += (double)f[c] * (double)f[c];
+                p[c] = __builtin_fma((double)f[c], (double)f[c], p[c]);  // exact product
             }
         }
         const double s = canon_reduce(p);
@@ -332,7 +332,7 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
                     const float f[4] = {lo_bf16(xv.x), hi_bf16(xv.x), lo_bf16(xv.y),
                                         hi_bf16(xv.y)};
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) p[t][c] += (double)wv[c] * (double)f[c];
+                    for (int c = 0; c < 4; ++c) p[t][c] = __builtin_fma((double)wv[c], (double)f[c], p[t][c]);
                 }
             }
             // Refill this buffer with the batch two ahead (clamped).

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     for (uint32_t k = threadIdx.x; k < H; k += 256) {
         const float v = bf16_to_f32(xr[k]);
         bad |= !__builtin_isfinite(v);
-        s += (double)v * (double)v;
+        s = __builtin_fma((double)v, (double)v, s);  // exact product: fused == separate
     }
     if (__syncthreads_or(bad)) {
         if (threadIdx.x == 0) latch(status, K3X_ERR_INVALID_MXFP4);
@@ -100,7 +100,8 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ W
 #pragma unroll
         for (int a = 0; a < EPB; ++a)
 #pragma unroll
-            for (int b = 0; b < TPB; ++b) acc[a][b] += (double)w[a] * (double)xv[b];
+            for (int b = 0; b < TPB; ++b)
+                acc[a][b] = __builtin_fma((double)w[a], (double)xv[b], acc[a][b]);
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -120,6 +121,117 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ W
                 (float)((red[0][i] + red[1][i]) + (red[2][i] + red[3][i]));
     }
 }
+
+// ---------------------------------------------------------------------------
+// Router logits for many tokens: the same fp64 canonical order as
+// router_kernel (thread i sums k = i, i + 256, ... in sequence; then the
+// balanced pairwise tree over the 256 thread partials in thread order), for
+// an EPB x TPB (expert x token) tile per block of 256 threads.
+//   * W and xn rows are clamped to valid rows, so every load is issued
+//     unconditionally and the in-order vector-memory counter lets DEPTH
+//     k-steps of loads stay in flight behind the multiply-adds.
+//   * The 64 per-thread partials are reduced across the wave by halving
+//     exchanges: at the step over lane bit m, each lane keeps half of its
+//     outputs and adds the partner lane's copy of them.  Addition is
+//     commutative, so each sum is bit-identical to the xor butterfly's and the
+//     wave's lane L ends with output bitrev6(L).
+// Products fp32 x bf16 are exact in fp64 (24 + 8 significand bits), so the
+// fused multiply-add rounds exactly as the separate multiply and add do.
+// ---------------------------------------------------------------------------
+template <int EPB, int TPB, int DEPTH>
+__global__ __launch_bounds__(256) void router_tile_kernel(const float* __restrict__ W,
+                                                          const uint16_t* __restrict__ xn,
+                                                          uint32_t E, uint32_t H, uint32_t T,
+                                                          float* __restrict__ logits,
+                                                          const uint32_t* status) {
+    static_assert(EPB * TPB == 64, "one output per lane after the wave reduction");
+    __shared__ double red[4][64];
+    if (*(volatile const uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t e0 = blockIdx.x * EPB, t0 = blockIdx.y * TPB;
+    const uint32_t nj = H / 256;  // k-steps every thread takes
+    const float* wrow[EPB];
+    const uint16_t* xrow[TPB];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a) wrow[a] = W + (size_t)min(e0 + a, E - 1) * H + tid;
+#pragma unroll
+    for (int b = 0; b < TPB; ++b) xrow[b] = xn + (size_t)min(t0 + b, T - 1) * H + tid;
+    double acc[EPB][TPB];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) acc[a][b] = 0.0;
+    auto step = [&](const float* wv, const uint16_t* xv) {
+        double wd[EPB], xd[TPB];
+#pragma unroll
+        for (int a = 0; a < EPB; ++a) wd[a] = (double)wv[a];
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) xd[b] = (double)bf16_to_f32(xv[b]);
+#pragma unroll
+        for (int a = 0; a < EPB; ++a)
+#pragma unroll
+            for (int b = 0; b < TPB; ++b) acc[a][b] = __builtin_fma(wd[a], xd[b], acc[a][b]);
+    };
+    if (nj) {
+        float wv[DEPTH][EPB];
+        uint16_t xv[DEPTH][TPB];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const uint32_t j = min((uint32_t)d, nj - 1) * 256;
+#pragma unroll
+            for (int a = 0; a < EPB; ++a) wv[d][a] = wrow[a][j];
+#pragma unroll
+            for (int b = 0; b < TPB; ++b) xv[d][b] = xrow[b][j];
+        }
+        for (uint32_t jb = 0; jb < nj; jb += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                if (jb + d < nj) step(wv[d], xv[d]);  // block-uniform
+                const uint32_t j = min(jb + d + DEPTH, nj - 1) * 256;
+#pragma unroll
+                for (int a = 0; a < EPB; ++a) wv[d][a] = wrow[a][j];
+#pragma unroll
+                for (int b = 0; b < TPB; ++b) xv[d][b] = xrow[b][j];
+            }
+        }
+    }
+    if (tid < H % 256) {  // the last, partial k-step
+        float wv[EPB];
+        uint16_t xv[TPB];
+#pragma unroll
+        for (int a = 0; a < EPB; ++a) wv[a] = wrow[a][nj * 256];
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) xv[b] = xrow[b][nj * 256];
+        step(wv, xv);
+    }
+    // Output o = b * EPB + a (consecutive experts of one token adjacent).
+    double v[64];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) v[b * EPB + a] = acc[a][b];
+#pragma unroll
+    for (int m = 1, cnt = 64; m < 64; m <<= 1, cnt >>= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int i = 0; i < cnt / 2; ++i) {
+            const double keep = upper ? v[cnt / 2 + i] : v[i];
+            const double send = upper ? v[i] : v[cnt / 2 + i];
+            v[i] = keep + __shfl_xor(send, m);
+        }
+    }
+    const uint32_t o = __builtin_bitreverse32(lane) >> 26;
+    red[wave][o] = v[0];
+    __syncthreads();
+    if (tid < 64) {
+        const uint32_t a = tid % EPB, b = tid / EPB;
+        if (e0 + a < E && t0 + b < T)
+            logits[(size_t)(t0 + b) * E + e0 + a] =
+                (float)((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]));
+    }
+}
+
+constexpr int kRouterEpb = 8, kRouterTpb = 8;  // router_tile_kernel tile for T > 4
 
 // Sort key: larger adjusted score first, then lower expert index
 // (runtime/src/official_moe.cpp:226-232).  -0 is folded into +0 so that the
@@ -890,7 +1002,9 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
         hipLaunchKernelGGL((router_kernel<1, 4>), dim3(d.experts, 1), dim3(256), 0, ctx->stream,
                            bank->router_w, s.xn, d.experts, d.hidden, T, s.logits, ctx->status);
     } else {
-        hipLaunchKernelGGL((router_kernel<4, 8>), dim3((d.experts + 3) / 4, (T + 7) / 8),
+        hipLaunchKernelGGL((router_tile_kernel<kRouterEpb, kRouterTpb, 4>),
+                           dim3((d.experts + kRouterEpb - 1) / kRouterEpb,
+                                (T + kRouterTpb - 1) / kRouterTpb),
                            dim3(256), 0, ctx->stream, bank->router_w, s.xn, d.experts, d.hidden,
                            T, s.logits, ctx->status);
     }
