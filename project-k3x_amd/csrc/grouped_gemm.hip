@@ -2,19 +2,24 @@
 // chunks, verification windows) on bf16 MFMA, MXFP4 weights dequantised in
 // registers.
 //
-// Workgroup = 4 or 8 waves, one 128-row chunk of one expert's rows (a work item
+// Workgroup = 8 waves, one 128-row chunk of one expert's rows (a work item
 // listed by the grouping, so large experts spread over many workgroups) x
 // NT 16-row output blocks per wave (gate/up: NT pairs of 16 gate + 16 up
 // rows).  Per K tile (128 K):
 //   * the chunk's activation rows (gathered through pair_token for the
-//     routed gate/up) are staged in LDS, double-buffered, rows padded to
-//     272 B so the MFMA operand reads of 16 lanes hit 16 different banks;
+//     routed gate/up) arrive in LDS by buffer loads that write LDS directly
+//     (no registers), into a ring of kStages tiles; each row's 16-byte chunks
+//     are XOR-swizzled by the row index, so the MFMA operand reads of 16 lanes
+//     (16 rows, one column chunk) hit 16 different bank groups;
 //   * each wave dequantises its weight fragments once (v_cvt_scalef32_pk_
 //     bf16_fp4 per code byte) and feeds each to the MFMAs of all eight
 //     16-row tiles of the chunk (tiles past the chunk's rows are skipped);
-//   * weights are prefetched DEPTH tiles ahead in registers, activations one
-//     tile ahead; every load is unconditional (indices clamped) so the
-//     compiler's in-order vector-memory waits never wait on later tiles.
+//   * software pipeline: step k multiplies tile k, then requests activation
+//     and weight tile k + 3, then waits until only the requests of steps
+//     k - 1 and k are outstanding (the vector-memory counter retires in issue
+//     order) and meets the other waves at a barrier.  Tile k + 1 was
+//     requested at step k - 2, so it is in LDS and registers; each request
+//     has two steps of multiplies to arrive in.
 // The weights of an expert are read once per 128-row chunk.  The N blocks of
 // one expert are numbered to land on one XCD, so its activation rows are
 // fetched into that XCD's L2 once.
@@ -23,49 +28,85 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "k3x_gemm.hpp"
 
 using namespace k3x_dev;
 using k3x_hip::kWideRows;
+using k3x_hip::kWideStages;
 using k3x_hip::WideGemmArgs;
 
 namespace {
 
-constexpr int kMTiles = kWideRows / 16;  // MFMA row tiles per chunk
-constexpr int kPitch = 128 + 8;          // LDS row pitch, bf16 elements
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMTiles = kWideRows / 16;          // MFMA row tiles per chunk
+constexpr int kTileChunks = kWideRows * 16;      // 16-byte chunks per activation tile
+constexpr int kALoads = kTileChunks / kThreads;  // LDS-direct loads per wave per tile
+static_assert(kALoads * kThreads == kTileChunks, "whole activation tile per step");
 
 __device__ inline uint32_t prior_status(const uint32_t* status) { return *status; }
 __device__ inline uint32_t wave_index() {
     return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
-// OCC: minimum workgroups per CU the registers must allow (OCC * WAVES / 4
-// waves per SIMD: two waves per SIMD keep one wave's loads in flight while
-// the other multiplies); the 8 x NT x S accumulators are independent MFMA
-// chains.
-template <bool FP4, bool GATEUP, int WAVES, int NT, int DEPTH, int OCC>
-__global__ __launch_bounds__(64 * WAVES, OCC) void wide_gemm(WideGemmArgs a) {
-    constexpr int kThreads = 64 * WAVES;
-    constexpr int kARowStep = kThreads / 16;            // 16 threads per 128-column row
-    constexpr int kALoads = kWideRows / kARowStep;      // 16-byte activation loads per thread per tile
-    __shared__ u32x4 s_a4[2][kWideRows * kPitch / 8];
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Vector-memory requests one wave issues at pipeline step k (activation tile
+// + weight tile; the MXFP4 scale dwords cover four K tiles and are requested
+// at steps with k % 4 == 0).
+template <bool FP4, int NT, int S, int U>
+constexpr int step_loads(int d) {
+    return kALoads + NT * S * U + ((FP4 && d == 0) ? NT * S : 0);
+}
+
+// Waits until at most N of this wave's vector-memory requests are
+// outstanding and all its LDS operations are done, then meets the workgroup.
+// The memory clobber keeps the compiler from moving loads or LDS accesses
+// across it.
+template <int N>
+__device__ inline void wait_and_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// End of pipeline step d (= k % 4): only the requests of steps k - 1 and k
+// may stay outstanding.  d is a constant once the step loop is unrolled.
+template <bool FP4, int NT, int S, int U>
+__device__ inline void end_step(int d) {
+    switch (d) {
+        case 0: wait_and_barrier<step_loads<FP4, NT, S, U>(3) + step_loads<FP4, NT, S, U>(0)>(); break;
+        case 1: wait_and_barrier<step_loads<FP4, NT, S, U>(0) + step_loads<FP4, NT, S, U>(1)>(); break;
+        case 2: wait_and_barrier<step_loads<FP4, NT, S, U>(1) + step_loads<FP4, NT, S, U>(2)>(); break;
+        default: wait_and_barrier<step_loads<FP4, NT, S, U>(2) + step_loads<FP4, NT, S, U>(3)>(); break;
+    }
+}
+
+template <bool FP4, bool GATEUP, int NT>
+__global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
+    __shared__ u32x4 s_a4[kWideStages * kTileChunks];  // 128 KiB ring
     constexpr int S = GATEUP ? 2 : 1;  // matrices per output row block (gate, up)
     constexpr int U = FP4 ? 1 : 4;     // 16-byte words per lane per tile
+    static_assert(kWideStages == 4, "the step schedule below is written for four stages");
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const uint32_t g = lane >> 4, n = lane & 15;
-    // One workgroup per (work item, output block set) on a 1-D grid.
-    // Consecutive workgroups go to the eight XCDs in turn; renumber so that
-    // each XCD takes a contiguous range of logical blocks (the blocks of one
-    // item share an L2).
-    const uint32_t nb = gridDim.x, xcd = blockIdx.x % 8, per = nb / 8, rem = nb % 8;
-    const uint32_t lb = xcd * per + min(xcd, rem) + blockIdx.x / 8;
-    const uint32_t nblk = a.nrb / (WAVES * NT);
-    const uint32_t item = lb / nblk, jb = lb % nblk;
+    // One workgroup per (work item, output block set) on a 1-D grid sized
+    // for the most items the grouping can list; the first nvalid workgroups
+    // carry the listed items.  Consecutive workgroups go to the eight XCDs in
+    // turn; renumber those nvalid so that each XCD takes an equal,
+    // contiguous range of logical blocks (the blocks of one item share an
+    // L2), and the unused tail of the grid is spread over all XCDs instead
+    // of idling whole XCDs.
     if (prior_status(a.status)) return;
+    const uint32_t nblk = a.nrb / (kWaves * NT);
+    const uint32_t nvalid = a.items ? min(*a.n_items * nblk, gridDim.x) : gridDim.x;
+    if (blockIdx.x >= nvalid) return;
+    const uint32_t xcd = blockIdx.x % 8, per = nvalid / 8, rem = nvalid % 8;
+    const uint32_t lb = xcd * per + min(xcd, rem) + blockIdx.x / 8;
+    const uint32_t item = lb / nblk, jb = lb % nblk;
     uint32_t e = 0, cnt = a.tokens, off = 0, m0 = item * kWideRows;
     if (a.items) {
-        if (item >= *a.n_items) return;
         const uint32_t it = a.items[item];
         e = it >> 16;
         m0 = (it & 0xffffu) * kWideRows;
@@ -73,73 +114,103 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void wide_gemm(WideGemmArgs a) {
         off = a.offsets[e];
     }
     if (m0 >= cnt) return;
-    const uint32_t kt = a.kt;
-    const uint32_t rb0 = (jb * WAVES + wave) * NT;
-    const u32x4* codes = reinterpret_cast<const u32x4*>(a.codes + e * a.codes_per_expert) + lane;
-    const uint32_t* scales = FP4 ? a.scales + e * a.scales_per_expert + lane : nullptr;
+    const uint32_t kt = a.kt;  // multiple of kWideStages (checked on the host)
+    const uint32_t rows = min(cnt - m0, kWideRows);
+    const uint32_t rb0 = (jb * kWaves + wave) * NT;
+    // Weights of expert e through buffer resources: the per-lane offset is
+    // the only vector register; block, tile and matrix offsets are scalar
+    // (rb0 is wave-uniform), and reads past the expert's extent return 0.
+    // Extent of one expert's tile array: nrb blocks x kt tiles x S x U KiB.
+    const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(a.codes + e * a.codes_per_expert), (short)0,
+        a.nrb * kt * (S * U * 1024u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+        FP4 ? const_cast<uint32_t*>(a.scales + e * a.scales_per_expert) : nullptr, (short)0,
+        FP4 ? (uint32_t)(a.scales_per_expert * 4) : 0u, 0x00020000);
+    const uint32_t lane16 = lane * 16, lane4 = lane * 4;
 
-    // Weight stages: codes bc[d][nt][w][u] and scale dwords bs[d][nt][w] of
-    // K tile k for stage d = k % DEPTH.  Plain arrays indexed only inside
-    // fully unrolled loops, so they live in registers.
+    // Activation tile loads: wave w's load q fills LDS rows 16 w + 4 q .. + 3
+    // (1 KiB: lane l writes row 16 w + 4 q + l / 16, position l % 16).  The
+    // position p of row r holds the row's 16-byte chunk p ^ (r % 16).  Rows
+    // past the chunk's end repeat its last row (they are never stored).
+    const __amdgpu_buffer_rsrc_t arsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.a), (short)0, a.a_bytes, 0x00020000);
+    uint32_t aoff[kALoads];
+#pragma unroll
+    for (int q = 0; q < kALoads; ++q) {
+        const uint32_t r = 16 * wave + 4 * q + (lane >> 4);
+        const uint32_t rr = off + m0 + min(r, rows - 1);
+        const uint32_t src = a.gather ? a.pair_token[rr] : rr;
+        aoff[q] = (src * a.a_stride + ((lane & 15) ^ (r & 15)) * 8) * 2;
+    }
+    // MFMA operand position of lane (n, g), 8-column group j of row n:
+    // chunk 4 g + j, swizzled.
+    uint32_t apos[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) apos[j] = n * 16 + ((4 * g + j) ^ n);
+
+    // Weight stages: codes bc[d][nt][w][u] of K tile k in stage d = k % 4
+    // (three are live at a time: tiles k .. k + 2 while tile k is
+    // multiplied); scale dwords of the four tiles kb .. kb + 3 in sc (current
+    // block) and scn (next block).  Plain arrays indexed only inside fully
+    // unrolled loops, so they live in registers.
+#define WIDE_LOAD_A(k, buf)                                                                  \
+    _Pragma("unroll") for (int q = 0; q < kALoads; ++q)                                      \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                            \
+            arsrc, (lds_ptr_t)&s_a4[(buf) * kTileChunks + (16 * wave + 4 * q) * 16], 16,      \
+            aoff[q], (k) * 256, 0, 0);
 #define WIDE_LOAD_B(d, k)                                                                    \
-    _Pragma("unroll") for (int nt = 0; nt < NT; ++nt)                                      \
-        _Pragma("unroll") for (int w = 0; w < S; ++w) {                                    \
-            const size_t base_ = (((size_t)(rb0 + nt) * kt + (k)) * S + w) * U * 64;       \
-            _Pragma("unroll") for (int u = 0; u < U; ++u) bc[d][nt][w][u] =                \
-                codes[base_ + u * 64];                                                       \
-            if constexpr (FP4)                                                               \
-                bs[d][nt][w] = scales[(((size_t)(rb0 + nt) * a.ks + (k) / 4) * S + w) * 64]; \
+    _Pragma("unroll") for (int nt = 0; nt < NT; ++nt)                                        \
+        _Pragma("unroll") for (int w = 0; w < S; ++w) {                                      \
+            const uint32_t base_ = (((rb0 + nt) * kt + (k)) * S + w) * U * 1024;             \
+            _Pragma("unroll") for (int u = 0; u < U; ++u) bc[d][nt][w][u] =                  \
+                __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane16, base_ + u * 1024, 0);   \
         }
-#define WIDE_LOAD_A(k)                                                                       \
-    _Pragma("unroll") for (int i = 0; i < kALoads; ++i) av[i] =                            \
-        *reinterpret_cast<const u32x4*>(a.a + asrc[i] + (size_t)(k) * 128);
-#define WIDE_STORE_A(buf)                                                                    \
-    _Pragma("unroll") for (int i = 0; i < kALoads; ++i)                                    \
-        s_a4[buf][((arow + kARowStep * i) * kPitch + acol) / 8] = av[i];
+#define WIDE_LOAD_SCALES(dst, k)                                                             \
+    if constexpr (FP4) {                                                                     \
+        _Pragma("unroll") for (int nt = 0; nt < NT; ++nt)                                    \
+            _Pragma("unroll") for (int w = 0; w < S; ++w) dst[nt][w] =                        \
+                __builtin_amdgcn_raw_buffer_load_b32(                                        \
+                    srsrc, lane4, (((rb0 + nt) * a.ks + (k) / 4) * S + w) * 256, 0);          \
+    }
+#define WIDE_ORDER() asm volatile("" ::: "memory")
 
-    // This thread's activation chunks: rows arow + kARowStep i, columns acol..+7.
-    const uint32_t arow = tid / 16, acol = (tid % 16) * 8;
-    {
-        const uint32_t rows = min(cnt - m0, kWideRows);
-        uint32_t asrc[kALoads];
+    // MT = row tiles multiplied: all eight, or the first four when the chunk
+    // has at most 64 rows (a workgroup-uniform choice made once, so the step
+    // loop has no branches; tiles past the chunk's rows hold copies of its
+    // last row and are not stored).
+    auto run = [&](auto mt_count) {
+        constexpr int MT = decltype(mt_count)::value;
+        f32x4 acc[MT][NT][S];
 #pragma unroll
-        for (int i = 0; i < kALoads; ++i) {
-            const uint32_t r = m0 + min(arow + kARowStep * i, rows - 1);  // clamped: valid row
-            const uint32_t src = a.gather ? a.pair_token[off + r] : off + r;
-            asrc[i] = src * a.a_stride + acol;
-        }
-        f32x4 acc[kMTiles][NT][S];
-#pragma unroll
-        for (int mt = 0; mt < kMTiles; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                 for (int w = 0; w < S; ++w) acc[mt][nt][w] = f32x4{0.f, 0.f, 0.f, 0.f};
+        u32x4 bc[kWideStages][NT][S][U];
+        uint32_t sc[NT][S], scn[NT][S];
 
-        u32x4 bc[DEPTH][NT][S][U];
-        uint32_t bs[DEPTH][NT][S];
-        u32x4 av[kALoads];
-        WIDE_LOAD_A(0)
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            WIDE_LOAD_B(d, min((uint32_t)d, kt - 1))
-        }
-        WIDE_STORE_A(0)
-        WIDE_LOAD_A(min(1u, kt - 1))
-        __syncthreads();
+        // Prologue = steps -3 .. -1 of the schedule: step s requests
+        // activation and weight tile s + 3 (the scales of tiles 0..3 with
+        // step -3's).
+        WIDE_LOAD_A(0u, 0)
+        WIDE_LOAD_B(0, 0u)
+        WIDE_LOAD_SCALES(sc, 0u)
+        WIDE_ORDER();
+        WIDE_LOAD_A(1u, 1)
+        WIDE_LOAD_B(1, 1u)
+        WIDE_ORDER();
+        WIDE_LOAD_A(2u, 2)
+        WIDE_LOAD_B(2, 2u)
+        // Steps -2 and -1 may stay in flight; tile 0 (step -3) has arrived.
+        wait_and_barrier<2 * (kALoads + NT * S * U)>();
 
-        // kt is a multiple of DEPTH (checked on the host): no branch in the
-        // loop body.  Step k: stage tile k + 1 (loaded during step k - 1)
-        // into the other LDS buffer, request tile k + 2, multiply tile k,
-        // refill this weight stage with tile k + DEPTH.
-        for (uint32_t kb = 0; kb < kt; kb += DEPTH) {
+        for (uint32_t kb = 0; kb < kt; kb += kWideStages) {
 #pragma unroll
-            for (int d = 0; d < DEPTH; ++d) {
+            for (int d = 0; d < kWideStages; ++d) {
                 const uint32_t k = kb + d;
-                WIDE_STORE_A((k + 1) & 1)  // at the last step: a copy of the last tile, unused
-                WIDE_LOAD_A(min(k + 2, kt - 1))
-                const uint16_t* sa =
-                    reinterpret_cast<const uint16_t*>(s_a4[k & 1]) + n * kPitch + 32 * g;
+                const u32x4* sa = s_a4 + d * kTileChunks;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     bf16x8 bw[NT][S];
@@ -149,32 +220,49 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void wide_gemm(WideGemmArgs a) {
                         for (int w = 0; w < S; ++w) {
                             if constexpr (FP4) {
                                 const uint32_t word = bc[d][nt][w][0][j];
-                                bw[nt][w] = dequant8(
-                                    word, e8m0_to_f32((bs[d][nt][w] >> (8 * (k & 3))) & 0xffu));
+                                bw[nt][w] = dequant8(word, e8m0_to_f32((sc[nt][w] >> (8 * d)) & 0xffu));
                             } else {
                                 bw[nt][w] = as_bf16x8(bc[d][nt][w][j]);
                             }
                         }
 #pragma unroll
-                    for (int mt = 0; mt < kMTiles; ++mt) {
-                        if ((uint32_t)(16 * mt) < rows) {  // workgroup-uniform
-                            const bf16x8 af =
-                                *reinterpret_cast<const bf16x8*>(sa + 16 * mt * kPitch + 8 * j);
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const bf16x8 af = as_bf16x8(sa[mt * 256 + apos[j]]);
 #pragma unroll
-                            for (int nt = 0; nt < NT; ++nt)
+                        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-                                for (int w = 0; w < S; ++w)
-                                    acc[mt][nt][w] = mfma16x16x32(af, bw[nt][w], acc[mt][nt][w]);
-                        }
+                            for (int w = 0; w < S; ++w)
+                                acc[mt][nt][w] = mfma16x16x32(af, bw[nt][w], acc[mt][nt][w]);
                     }
                 }
-                WIDE_LOAD_B(d, min(k + DEPTH, kt - 1))
-                __syncthreads();
+                // Step k's requests: tile k + 3 into the LDS buffer and
+                // weight stage tile k - 1 used (all waves passed the barrier
+                // after multiplying it); past the end they repeat the last
+                // tile (the loads stay unconditional, the count exact).  The
+                // next block's scales ride with the block's first step.
+                WIDE_LOAD_A(min(k + 3, kt - 1), (d + 3) % kWideStages)
+                WIDE_LOAD_B((d + 3) % kWideStages, min(k + 3, kt - 1))
+                if (d == 0) WIDE_LOAD_SCALES(scn, min(k + 4, kt - 1))
+                // Tile k + 1 (requested at step k - 2) is in LDS once only
+                // steps k - 1 and k are outstanding.
+                end_step<FP4, NT, S, U>(d);
+            }
+            if constexpr (FP4) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int w = 0; w < S; ++w) sc[nt][w] = scn[nt][w];
             }
         }
+        // The repeated last-tile requests of the final steps land before the
+        // workgroup's LDS can be handed on.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
 #pragma unroll
-        for (int mt = 0; mt < kMTiles; ++mt)
+        for (int mt = 0; mt < MT; ++mt) {
+            // One row tile at a time: keeps the scatter-index loads of later
+            // tiles from being hoisted while all accumulators are live.
+            WIDE_ORDER();
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -187,24 +275,29 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void wide_gemm(WideGemmArgs a) {
                         const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
                         a.act[(size_t)r * a.act_stride + col] = f32_to_bf16(v);
                     } else {
-                        const size_t yrow = a.scatter ? (size_t)a.pair_token[r] * a.top_k + a.pair_slot[r]
-                                                      : (size_t)r;
+                        const size_t yrow = a.scatter
+                                                ? (size_t)a.pair_token[r] * a.top_k + a.pair_slot[r]
+                                                : (size_t)r;
                         a.y[yrow * a.y_stride + col] = acc[mt][nt][0][i];
                     }
                 }
-    }
+        }
+    };
+    if (rows > kWideRows / 2)
+        run(std::integral_constant<int, kMTiles>{});
+    else
+        run(std::integral_constant<int, kMTiles / 2>{});
 }
 
-#undef WIDE_LOAD_B
 #undef WIDE_LOAD_A
-#undef WIDE_STORE_A
+#undef WIDE_LOAD_B
+#undef WIDE_LOAD_SCALES
+#undef WIDE_ORDER
 
-// Waves per workgroup and output 16-row blocks per wave (WAVES * NT per
-// workgroup): the more output rows a workgroup covers, the fewer times the
-// chunk's activation rows are streamed from L2.
-constexpr int kWavesRouted = 8, kWavesShared = 4;
+// Output 16-row blocks per wave (kWaves * NT per workgroup): the more output
+// rows a workgroup covers, the fewer times the chunk's activation rows are
+// streamed from L2.
 constexpr int kNtRoutedGateUp = 2, kNtRoutedDown = 4, kNtSharedGateUp = 1, kNtSharedDown = 2;
-constexpr int kDepth = 2;
 
 }  // namespace
 
@@ -212,33 +305,33 @@ namespace k3x_hip {
 
 uint32_t wide_rb_per_block(WideKind kind) {
     switch (kind) {
-        case kWideRoutedGateUp: return kWavesRouted * kNtRoutedGateUp;
-        case kWideRoutedDown: return kWavesRouted * kNtRoutedDown;
-        case kWideSharedGateUp: return kWavesShared * kNtSharedGateUp;
-        default: return kWavesShared * kNtSharedDown;
+        case kWideRoutedGateUp: return kWaves * kNtRoutedGateUp;
+        case kWideRoutedDown: return kWaves * kNtRoutedDown;
+        case kWideSharedGateUp: return kWaves * kNtSharedGateUp;
+        default: return kWaves * kNtSharedDown;
     }
 }
 
 int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items) {
     const uint32_t per = wide_rb_per_block(kind);
-    if (a.nrb % per || a.kt % kDepth || !max_items) return K3X_ERR_INVALID_EXTENT;
+    if (a.nrb % per || a.kt % kWideStages || !a.kt || !max_items) return K3X_ERR_INVALID_EXTENT;
     const dim3 grid(max_items * (a.nrb / per));
     switch (kind) {
         case kWideRoutedGateUp:
-            hipLaunchKernelGGL((wide_gemm<true, true, kWavesRouted, kNtRoutedGateUp, kDepth, 1>),
-                               grid, dim3(64 * kWavesRouted), 0, ctx->stream, a);
+            hipLaunchKernelGGL((wide_gemm<true, true, kNtRoutedGateUp>), grid, dim3(kThreads), 0,
+                               ctx->stream, a);
             break;
         case kWideRoutedDown:
-            hipLaunchKernelGGL((wide_gemm<true, false, kWavesRouted, kNtRoutedDown, kDepth, 1>),
-                               grid, dim3(64 * kWavesRouted), 0, ctx->stream, a);
+            hipLaunchKernelGGL((wide_gemm<true, false, kNtRoutedDown>), grid, dim3(kThreads), 0,
+                               ctx->stream, a);
             break;
         case kWideSharedGateUp:
-            hipLaunchKernelGGL((wide_gemm<false, true, kWavesShared, kNtSharedGateUp, kDepth, 2>),
-                               grid, dim3(64 * kWavesShared), 0, ctx->stream, a);
+            hipLaunchKernelGGL((wide_gemm<false, true, kNtSharedGateUp>), grid, dim3(kThreads), 0,
+                               ctx->stream, a);
             break;
         default:
-            hipLaunchKernelGGL((wide_gemm<false, false, kWavesShared, kNtSharedDown, kDepth, 2>),
-                               grid, dim3(64 * kWavesShared), 0, ctx->stream, a);
+            hipLaunchKernelGGL((wide_gemm<false, false, kNtSharedDown>), grid, dim3(kThreads), 0,
+                               ctx->stream, a);
             break;
     }
     ctx->kernel_launches += 1;

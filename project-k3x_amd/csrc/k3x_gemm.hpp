@@ -23,6 +23,7 @@ struct WideGemmArgs {
     uint32_t nrb;                // 16-row blocks of the output (N / 16)
     const uint16_t* a;           // activation rows, bf16
     uint32_t a_stride;           // elements per activation row
+    uint32_t a_bytes;            // bytes readable from a (loads past it read 0)
     uint32_t gather;             // A row = pair_token[off + m] (1) or off + m (0)
     const uint32_t* items;       // routed: (expert << 16 | chunk) work items
     const uint32_t* n_items;
@@ -50,6 +51,9 @@ enum WideKind {
 
 // Rows per workgroup chunk of the wide GEMM.
 constexpr uint32_t kWideRows = 128;
+// K tiles (128 K each) in flight per workgroup; every K extent must be a
+// multiple of 128 * kWideStages.
+constexpr uint32_t kWideStages = 4;
 
 // Output 16-row blocks one workgroup covers for `kind` (the launch needs
 // nrb to be a multiple of it).

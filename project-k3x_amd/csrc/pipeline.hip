@@ -711,15 +711,19 @@ void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32
 // element offsets of the activation rows below 2^32.
 bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
     using k3x_hip::wide_rb_per_block;
+    constexpr uint32_t kq = 128 * k3x_hip::kWideStages;  // K extents: whole pipeline blocks
     const uint64_t rows = (uint64_t)T * K;
-    return T >= kWideMinTokens && d.hidden % 256 == 0 && d.inter % 256 == 0 &&
+    // Activation and weight byte offsets are 32-bit (buffer loads).
+    return T >= kWideMinTokens && d.hidden % kq == 0 && d.inter % kq == 0 &&
            (d.inter / 16) % wide_rb_per_block(k3x_hip::kWideRoutedGateUp) == 0 &&
            (d.hidden / 16) % wide_rb_per_block(k3x_hip::kWideRoutedDown) == 0 &&
            (!d.shared_inter ||
-            (d.shared_inter % 256 == 0 &&
+            (d.shared_inter % kq == 0 &&
              (d.shared_inter / 16) % wide_rb_per_block(k3x_hip::kWideSharedGateUp) == 0 &&
              (d.hidden / 16) % wide_rb_per_block(k3x_hip::kWideSharedDown) == 0)) &&
-           rows * std::max(d.hidden, std::max(d.inter, d.shared_inter)) < (1ull << 32);
+           rows * std::max(d.hidden, std::max(d.inter, d.shared_inter)) * 2 < (1ull << 32) &&
+           // weight byte offsets within one matrix pair are 32-bit as well
+           (uint64_t)std::max(d.inter, d.shared_inter) * d.hidden * 4 < (1ull << 32);
 }
 
 int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
@@ -750,6 +754,7 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.nrb = d.inter / 16;
     g.a = xn;
     g.a_stride = d.hidden;
+    g.a_bytes = T * d.hidden * 2;
     g.gather = 1;
     g.act = s.act;
     g.act_stride = d.inter;
@@ -784,6 +789,7 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.nrb = d.hidden / 16;
     dn.a = s.act;
     dn.a_stride = d.inter;
+    dn.a_bytes = T * K * d.inter * 2;
     dn.gather = 0;
     dn.act = nullptr;
     dn.y = s.y;
@@ -801,6 +807,7 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sd.kt = bank->sdown.kt;
         sd.a = s.sact;
         sd.a_stride = d.shared_inter;
+        sd.a_bytes = T * d.shared_inter * 2;
         sd.items = nullptr;
         sd.tokens = T;
         sd.y = s.sy;
