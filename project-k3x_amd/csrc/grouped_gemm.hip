@@ -8,12 +8,12 @@
 // rows).  Per K tile (128 K):
 //   * the chunk's activation rows (gathered through pair_token for the
 //     routed gate/up) arrive in LDS by buffer loads that write LDS directly
-//     (no registers), into a ring of kStages tiles; each row's 16-byte chunks
+//     (no registers), into a ring of kWideStages tiles; each row's 16-byte chunks
 //     are XOR-swizzled by the row index, so the MFMA operand reads of 16 lanes
 //     (16 rows, one column chunk) hit 16 different bank groups;
 //   * each wave dequantises its weight fragments once (v_cvt_scalef32_pk_
-//     bf16_fp4 per code byte) and feeds each to the MFMAs of all eight
-//     16-row tiles of the chunk (tiles past the chunk's rows are skipped);
+//     bf16_fp4 per code byte) and feeds each to the MFMAs of the chunk's
+//     eight 16-row tiles (four when the chunk has at most 64 rows);
 //   * software pipeline: step k multiplies tile k, then requests activation
 //     and weight tile k + 3, then waits until only the requests of steps
 //     k - 1 and k are outstanding (the vector-memory counter retires in issue
@@ -86,6 +86,7 @@ __device__ inline void end_step(int d) {
 template <bool FP4, bool GATEUP, int NT>
 __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     __shared__ u32x4 s_a4[kWideStages * kTileChunks];  // 128 KiB ring
+    __shared__ uint32_t s_yrow[kWideRows];              // down: output row of each chunk row
     constexpr int S = GATEUP ? 2 : 1;  // matrices per output row block (gate, up)
     constexpr int U = FP4 ? 1 : 4;     // 16-byte words per lane per tile
     static_assert(kWideStages == 4, "the step schedule below is written for four stages");
@@ -142,6 +143,14 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         const uint32_t rr = off + m0 + min(r, rows - 1);
         const uint32_t src = a.gather ? a.pair_token[rr] : rr;
         aoff[q] = (src * a.a_stride + ((lane & 15) ^ (r & 15)) * 8) * 2;
+    }
+    // Down: the output row of chunk row tid % 128 (the pair's token * top_k
+    // + slot, or the row itself), requested now so that it has arrived by
+    // the epilogue; it goes through LDS to the lanes that store the row.
+    uint32_t yv = 0;
+    if constexpr (!GATEUP) {
+        const uint32_t r = off + m0 + min(tid % kWideRows, rows - 1);
+        yv = a.scatter ? a.pair_token[r] * a.top_k + a.pair_slot[r] : r;
     }
     // MFMA operand position of lane (n, g), 8-column group j of row n:
     // chunk 4 g + j, swizzled.
@@ -258,11 +267,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         // workgroup's LDS can be handed on.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+        if constexpr (!GATEUP) {
+            if (tid < kWideRows) s_yrow[tid] = yv;
+            __syncthreads();
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            // One row tile at a time: keeps the scatter-index loads of later
-            // tiles from being hoisted while all accumulators are live.
-            WIDE_ORDER();
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -275,10 +285,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                         const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
                         a.act[(size_t)r * a.act_stride + col] = f32_to_bf16(v);
                     } else {
-                        const size_t yrow = a.scatter
-                                                ? (size_t)a.pair_token[r] * a.top_k + a.pair_slot[r]
-                                                : (size_t)r;
-                        a.y[yrow * a.y_stride + col] = acc[mt][nt][0][i];
+                        a.y[(size_t)s_yrow[row] * a.y_stride + col] = acc[mt][nt][0][i];
                     }
                 }
         }
