@@ -404,7 +404,9 @@ int k3xo_expert_major_plan(const uint32_t* ids, const float* contributions,
 
 /* The ascending-expert CSR form of the same grouping, plus each expert's
  * first-use key min(token*top_k + slot); sorting active experts by that key
- * reproduces the group order of k3xo_expert_major_plan. */
+ * reproduces the group order of k3xo_expert_major_plan.  Rejects what the
+ * plan rejects about ids: out of range, or one expert twice in one token
+ * (runtime/src/expert_major.cpp:30-35). */
 int k3xo_expert_major_csr(const uint32_t* ids, size_t tokens, size_t top_k,
                           size_t experts, uint32_t* counts, uint32_t* offsets,
                           uint32_t* pair_token, uint32_t* pair_slot,
@@ -417,6 +419,10 @@ int k3xo_expert_major_csr(const uint32_t* ids, size_t tokens, size_t top_k,
     for (size_t e = 0; e < experts; ++e) first_use[e] = 0xffffffffu;
     for (size_t p = 0; p < pairs; ++p) {
         if (ids[p] >= experts) return K3XO_INVALID_STATE;
+        for (size_t q = p - p % top_k; q < p; ++q)
+            if (ids[q] == ids[p]) return K3XO_INVALID_STATE;
+    }
+    for (size_t p = 0; p < pairs; ++p) {
         ++counts[ids[p]];
         if (first_use[ids[p]] == 0xffffffffu) first_use[ids[p]] = (uint32_t)p;
     }

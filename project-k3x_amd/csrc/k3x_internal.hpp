@@ -105,6 +105,7 @@ struct LayerBuffers {
                            //     tokens of the rows, 8 bits each}
     uint32_t* witems;      // wide GEMM work items (expert << 16 | 128-row chunk)
     uint32_t* n_witems;    // [1]
+    uint8_t* gscratch;     // grouping: per-chunk counts and first uses, pair ranks
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }

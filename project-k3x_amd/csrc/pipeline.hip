@@ -326,115 +326,203 @@ __global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logi
 }
 
 // ---------------------------------------------------------------------------
-// Expert-major grouping, one block of 1024 threads.  Produces the
-// ascending-expert CSR (counts, offsets, pair_token, pair_slot; rows of one
-// expert in (token, slot) order) plus first_use = min(token*K + slot) and the
-// active experts sorted by it, which is the group order of
-// build_expert_major_plan (runtime/src/expert_major.cpp:10-54).
-// Rows are ranked with per-step token bitmaps: tokens are taken 64 (or
-// 1024/K) at a time, each pair's rank inside its expert is the running count
-// plus the popcount of earlier tokens of the step that chose the expert.
-// With witems non-null it also lists the (expert << 16 | row chunk) work
-// items of the wide GEMM, chunks of chunk_rows rows, in ascending expert order.
+// Expert-major grouping in three launches.  Produces the ascending-expert CSR
+// (counts, offsets, pair_token, pair_slot; rows of one expert in (token,
+// slot) order) plus first_use = min(token*K + slot) and the active experts
+// sorted by it, which is the group order of build_expert_major_plan
+// (runtime/src/expert_major.cpp:10-54).  Tokens are taken in chunks of
+// tps = min(64, 1024 / K):
+//   group_count_kernel    one workgroup per chunk: checks the ids (< E, no
+//                         expert twice in one token: invalid_state, as
+//                         expert_major.cpp:30-35), ranks each pair among the
+//                         chunk's pairs of its expert (popcount of earlier
+//                         tokens in a per-expert token bitmap), and writes
+//                         the chunk's per-expert count and first use;
+//   group_scan_kernel     one workgroup: per expert, the running row base of
+//                         every chunk, its count and first use; CSR offsets,
+//                         the active lists, and (witems non-null) the wide
+//                         GEMM's (expert << 16 | row chunk) work items in
+//                         ascending expert order;
+//   group_scatter_kernel  one workgroup per chunk: row offsets[e] +
+//                         base[chunk][e] + rank gets (token, slot).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void group_kernel(
-    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
-    uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets,
-    uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot,
-    uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
-    uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu,
-    uint32_t* __restrict__ witems, uint32_t* __restrict__ n_witems, uint32_t chunk_rows,
-    uint32_t* status) {
+__device__ inline uint32_t group_tps(uint32_t K) { return min(64u, 1024u / K); }
+
+__global__ __launch_bounds__(1024) void group_count_kernel(const uint32_t* __restrict__ ids,
+                                                           uint32_t T, uint32_t K, uint32_t E,
+                                                           uint32_t* __restrict__ chunk_cnt,
+                                                           uint32_t* __restrict__ chunk_fu,
+                                                           uint8_t* __restrict__ rank,
+                                                           uint32_t* status) {
     extern __shared__ uint32_t smem[];
-    uint32_t* cnt = smem;
-    uint32_t* fu = cnt + E;
-    uint32_t* run = fu + E;
-    uint32_t* mask = run + E;  // [E][2]
-    uint32_t* alist = mask + 2 * E;
-    __shared__ uint32_t na_s;
-    __shared__ int bad_s;
+    uint32_t* s_ids = smem;          // [1024] the chunk's ids
+    uint32_t* mask = s_ids + 1024;   // [E][2] token bitmap per expert
+    uint32_t* fu = mask + 2 * E;     // [E]
     if (*(volatile uint32_t*)status) return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t P = T * K;
-    if (tid == 0) bad_s = 0;
+    const uint32_t tid = threadIdx.x, c = blockIdx.x, tps = group_tps(K);
+    const uint32_t tl = tid / K, s = tid % K, t = c * tps + tl;
+    const bool valid = tl < tps && t < T;
+    const uint32_t p = t * K + s;
     for (uint32_t e = tid; e < E; e += 1024) {
-        cnt[e] = 0;
+        mask[2 * e] = 0;
+        mask[2 * e + 1] = 0;
         fu[e] = 0xffffffffu;
     }
+    const uint32_t e = valid ? ids[p] : 0u;
+    s_ids[tid] = e;
     __syncthreads();
-    for (uint32_t p = tid; p < P; p += 1024) {
-        const uint32_t e = ids[p];
-        if (e >= E) {
-            bad_s = 1;
-            continue;
-        }
-        atomicAdd(&cnt[e], 1u);
-        atomicMin(&fu[e], p);
-    }
-    __syncthreads();
-    if (bad_s) {
+    int bad = valid && e >= E;
+    if (valid)
+        for (uint32_t q = 0; q < s; ++q) bad |= s_ids[tl * K + q] == e;
+    if (__syncthreads_or(bad)) {
         if (tid == 0) latch(status, K3X_ERR_INVALID_STATE);
         return;
     }
-    if (tid == 0) {
-        uint32_t acc = 0, na = 0, ni = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            offsets[e] = acc;
-            run[e] = acc;
-            acc += cnt[e];
-            if (cnt[e]) {
-                // Work items of the wide GEMM: (expert, row chunk).
-                if (witems)
-                    for (uint32_t c = 0; c * chunk_rows < cnt[e]; ++c) witems[ni++] = (e << 16) | c;
-                alist[na] = e;
-                active_asc[na++] = e;
-            }
-        }
-        offsets[E] = acc;
-        *n_active = na;
-        if (witems) *n_witems = ni;
-        na_s = na;
+    if (valid) {
+        atomicOr(&mask[2 * e + (tl >> 5)], 1u << (tl & 31));
+        atomicMin(&fu[e], p);
     }
     __syncthreads();
-    const uint32_t na = na_s;
-    for (uint32_t a = tid; a < na; a += 1024) {
-        const uint32_t e = alist[a];
-        const uint32_t key = fu[e];
-        uint32_t rank = 0;
-        for (uint32_t b = 0; b < na; ++b) rank += fu[alist[b]] < key;
-        active_fu[rank] = e;
+    if (valid) {
+        const uint32_t lo = mask[2 * e], hi = mask[2 * e + 1];
+        rank[p] = (uint8_t)(tl < 32 ? __popc(lo & ((1u << tl) - 1u))
+                                    : __popc(lo) + __popc(hi & ((1u << (tl - 32)) - 1u)));
     }
+    for (uint32_t q = tid; q < E; q += 1024) {
+        chunk_cnt[(size_t)c * E + q] = __popc(mask[2 * q]) + __popc(mask[2 * q + 1]);
+        chunk_fu[(size_t)c * E + q] = fu[q];
+    }
+}
+
+// Exclusive scan of one 64-bit value per thread over a 1024-thread block;
+// returns this thread's prefix, *total gets the block total.
+__device__ inline uint64_t block_exclusive_scan(uint64_t v, uint64_t* red, uint64_t* total) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint64_t x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t y = __shfl_up(x, d);
+        if (lane >= (uint32_t)d) x += y;
+    }
+    if (lane == 63) red[wave] = x;
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t w = lane < 16 ? red[lane] : 0;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const uint64_t y = __shfl_up(w, d);
+            if (lane >= (uint32_t)d) w += y;
+        }
+        if (lane < 16) red[16 + lane] = w;
+    }
+    __syncthreads();
+    const uint64_t before = (wave ? red[16 + wave - 1] : 0) + x - v;
+    *total = red[31];
+    __syncthreads();
+    return before;
+}
+
+// Per-expert fields packed for one scan: rows (bits 0..26), wide GEMM items
+// (27..47), active flag (48..60).
+constexpr uint32_t kScanItemShift = 27, kScanActiveShift = 48;
+
+__global__ __launch_bounds__(1024) void group_scan_kernel(
+    uint32_t T, uint32_t K, uint32_t E, uint32_t* __restrict__ chunk_cnt,
+    const uint32_t* __restrict__ chunk_fu, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
+    uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
+    uint32_t* __restrict__ active_fu, uint32_t* __restrict__ witems,
+    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint32_t* status) {
+    extern __shared__ uint32_t smem[];
+    uint32_t* s_cnt = smem;          // [E]
+    uint32_t* s_fu = s_cnt + E;      // [E]
+    uint32_t* s_alist = s_fu + E;    // [E] active experts, ascending
+    __shared__ uint64_t red[32];
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x, nch = (T + group_tps(K) - 1) / group_tps(K);
+    // Running base of every chunk, per expert (chunks loaded 16 at a time).
     for (uint32_t e = tid; e < E; e += 1024) {
-        counts[e] = cnt[e];
-        first_use[e] = fu[e];
+        uint32_t acc = 0, f = 0xffffffffu;
+        for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
+            uint32_t v[16], g[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t c = min(c0 + i, nch - 1);
+                v[i] = chunk_cnt[(size_t)c * E + e];
+                g[i] = chunk_fu[(size_t)c * E + e];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (c0 + i >= nch) break;
+                chunk_cnt[(size_t)(c0 + i) * E + e] = acc;
+                acc += v[i];
+                f = min(f, g[i]);
+            }
+        }
+        s_cnt[e] = acc;
+        s_fu[e] = f;
     }
-    const uint32_t tps = min(64u, 1024u / K);  // tokens per step
-    for (uint32_t t0 = 0; t0 < T; t0 += tps) {
-        for (uint32_t e = tid; e < E; e += 1024) {
-            mask[2 * e] = 0;
-            mask[2 * e + 1] = 0;
-        }
-        __syncthreads();
-        const uint32_t tl = tid / K, s = tid % K, t = t0 + tl;
-        const bool valid = tl < tps && t < T;
-        uint32_t e = 0;
-        if (valid) {
-            e = ids[(size_t)t * K + s];
-            atomicOr(&mask[2 * e + (tl >> 5)], 1u << (tl & 31));
-        }
-        __syncthreads();
-        if (valid) {
-            const uint32_t lo = mask[2 * e], hi = mask[2 * e + 1];
-            const uint32_t below = tl < 32 ? __popc(lo & ((1u << tl) - 1u))
-                                           : __popc(lo) + __popc(hi & ((1u << (tl - 32)) - 1u));
-            const uint32_t r = run[e] + below;
-            pair_token[r] = t;
-            pair_slot[r] = s;
-        }
-        __syncthreads();
-        for (uint32_t q = tid; q < E; q += 1024) run[q] += __popc(mask[2 * q]) + __popc(mask[2 * q + 1]);
-        __syncthreads();
+    __syncthreads();
+    // Thread tid owns experts [tid * per, tid * per + per).
+    const uint32_t per = (E + 1023) / 1024, e0 = tid * per;
+    uint64_t mine = 0;
+    for (uint32_t i = 0; i < per; ++i) {
+        const uint32_t e = e0 + i;
+        if (e >= E) break;
+        const uint64_t c = s_cnt[e];
+        mine += c | ((c + chunk_rows - 1) / chunk_rows) << kScanItemShift |
+                (uint64_t)(c != 0) << kScanActiveShift;
     }
+    uint64_t total;
+    uint64_t pre = block_exclusive_scan(mine, red, &total);
+    for (uint32_t i = 0; i < per; ++i) {
+        const uint32_t e = e0 + i;
+        if (e >= E) break;
+        const uint32_t c = s_cnt[e];
+        const uint32_t row = (uint32_t)(pre & ((1ull << kScanItemShift) - 1));
+        const uint32_t item = (uint32_t)((pre >> kScanItemShift) & ((1ull << 21) - 1));
+        const uint32_t act = (uint32_t)(pre >> kScanActiveShift);
+        offsets[e] = row;
+        counts[e] = c;
+        first_use[e] = s_fu[e];
+        if (c) {
+            active_asc[act] = e;
+            s_alist[act] = e;
+            if (witems)
+                for (uint32_t q = 0; q * chunk_rows < c; ++q) witems[item + q] = (e << 16) | q;
+        }
+        pre += c | (uint64_t)((c + chunk_rows - 1) / chunk_rows) << kScanItemShift |
+               (uint64_t)(c != 0) << kScanActiveShift;
+    }
+    const uint32_t na = (uint32_t)(total >> kScanActiveShift);
+    if (tid == 0) {
+        offsets[E] = (uint32_t)(total & ((1ull << kScanItemShift) - 1));
+        *n_active = na;
+        if (witems) *n_witems = (uint32_t)((total >> kScanItemShift) & ((1ull << 21) - 1));
+    }
+    __syncthreads();
+    // First uses are distinct pair indices: ranks are a permutation.
+    for (uint32_t a = tid; a < na; a += 1024) {
+        const uint32_t e = s_alist[a], key = s_fu[e];
+        uint32_t r = 0;
+        for (uint32_t b = 0; b < na; ++b) r += s_fu[s_alist[b]] < key;
+        active_fu[r] = e;
+    }
+}
+
+__global__ __launch_bounds__(1024) void group_scatter_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    const uint32_t* __restrict__ chunk_base, const uint8_t* __restrict__ rank,
+    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ pair_token,
+    uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x, c = blockIdx.x, tps = group_tps(K);
+    const uint32_t tl = tid / K, s = tid % K, t = c * tps + tl;
+    if (tl >= tps || t >= T) return;
+    const uint32_t p = t * K + s, e = ids[p];
+    const uint32_t r = offsets[e] + chunk_base[(size_t)c * E + e] + rank[p];
+    pair_token[r] = t;
+    pair_slot[r] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -633,6 +721,12 @@ uint32_t wide_max_items(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
     return (uint32_t)(P / k3x_hip::kWideRows + std::min<uint64_t>(d.experts, P));
 }
 
+// Scratch bytes of the grouping: per-chunk counts and first uses, pair ranks.
+size_t group_scratch_bytes(uint32_t T, uint32_t K, uint32_t E) {
+    const size_t tps = std::min(64u, 1024u / K), nch = (T + tps - 1) / tps;
+    return 2 * nch * E * 4 + (((size_t)T * K + 255) & ~(size_t)255);
+}
+
 size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, Scratch* s) {
     size_t at = 0;
     auto take = [&](size_t bytes) {
@@ -660,6 +754,7 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->arec = (uint4*)take((size_t)d.experts * 16);
     s->witems = (uint32_t*)take((size_t)wide_max_items(d, T, K) * 4);
     s->n_witems = (uint32_t*)take(4);
+    s->gscratch = take(group_scratch_bytes(T, K, d.experts));
     return at;
 }
 
@@ -687,15 +782,24 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 
+
 int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
                  uint32_t* counts, uint32_t* offsets, uint32_t* pair_token, uint32_t* pair_slot,
                  uint32_t* first_use, uint32_t* n_active, uint32_t* active_asc,
-                 uint32_t* active_fu, uint32_t* witems = nullptr, uint32_t* n_witems = nullptr) {
-    const size_t lds = (size_t)E * 6 * 4;
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), lds, ctx->stream, ids, T, K, E, counts,
-                       offsets, pair_token, pair_slot, first_use, n_active, active_asc, active_fu,
-                       witems, n_witems, k3x_hip::kWideRows, ctx->status);
-    return launched(ctx, 1);
+                 uint32_t* active_fu, uint8_t* gscratch, uint32_t* witems = nullptr,
+                 uint32_t* n_witems = nullptr) {
+    const uint32_t tps = std::min(64u, 1024u / K), nch = (T + tps - 1) / tps;
+    uint32_t* chunk_cnt = reinterpret_cast<uint32_t*>(gscratch);
+    uint32_t* chunk_fu = chunk_cnt + (size_t)nch * E;
+    uint8_t* rank = reinterpret_cast<uint8_t*>(chunk_fu + (size_t)nch * E);
+    hipLaunchKernelGGL(group_count_kernel, dim3(nch), dim3(1024), (size_t)(1024 + 3 * E) * 4,
+                       ctx->stream, ids, T, K, E, chunk_cnt, chunk_fu, rank, ctx->status);
+    hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(1024), (size_t)3 * E * 4, ctx->stream, T,
+                       K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active, active_asc,
+                       active_fu, witems, n_witems, k3x_hip::kWideRows, ctx->status);
+    hipLaunchKernelGGL(group_scatter_kernel, dim3(nch), dim3(1024), 0, ctx->stream, ids, T, K, E,
+                       chunk_cnt, rank, offsets, pair_token, pair_slot, ctx->status);
+    return launched(ctx, 3);
 }
 
 template <bool FP4, bool GATEUP, int MT, int NT>
@@ -829,7 +933,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
                           s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu,
-                          s.witems, s.n_witems);
+                          s.gscratch, s.witems, s.n_witems);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -1059,16 +1163,20 @@ int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
 
 int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t tokens,
                               uint32_t top_k, uint32_t experts, const k3x_hip_moe_taps* t) {
-    if (!ctx || !ids || !t || !tokens || !top_k || top_k > 64 || !experts || experts > 4096 ||
+    if (!ctx || !ids || !t || !tokens || tokens > (1u << 20) || !top_k || top_k > 64 ||
+        !experts || experts > 4096 ||
         !t->counts || !t->offsets || !t->pair_token || !t->pair_slot || !t->first_use ||
         !t->n_active || !t->active_first_use)
         return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    int st = k3x_hip::ensure_scratch(ctx, (size_t)experts * 4);
+    // Scratch: the ascending active list, then the grouping's own buffers.
+    const size_t asc = ((size_t)experts * 4 + 255) & ~(size_t)255;
+    int st = k3x_hip::ensure_scratch(ctx, asc + group_scratch_bytes(tokens, top_k, experts));
     if (st) return st;
+    uint8_t* base = static_cast<uint8_t*>(ctx->scratch);
     return launch_group(ctx, ids, tokens, top_k, experts, t->counts, t->offsets, t->pair_token,
-                        t->pair_slot, t->first_use, t->n_active,
-                        static_cast<uint32_t*>(ctx->scratch), t->active_first_use);
+                        t->pair_slot, t->first_use, t->n_active, reinterpret_cast<uint32_t*>(base),
+                        t->active_first_use, base + asc);
 }
 
 }  // extern "C"

@@ -318,6 +318,8 @@ def make_taps(tensors: dict | None) -> MoeTaps | None:
         return None
     t = MoeTaps()
     for k, v in tensors.items():
+        if k not in TAP_FIELDS:  # a plain attribute would be ignored by the library
+            raise ValueError(f"unknown tap {k!r}; taps are {TAP_FIELDS}")
         setattr(t, k, ptr(v))
     return t
 

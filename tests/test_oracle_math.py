@@ -206,6 +206,17 @@ def test_expert_major_csr_rejects_out_of_range(oracle):
     assert st == INVALID_STATE
 
 
+def test_expert_major_csr_rejects_what_the_plan_rejects(oracle):
+    # One expert twice in one token: the plan's rejection
+    # (tests/cpp/test_expert_major.cpp:68-100); the CSR form agrees, and the
+    # same expert in two different tokens stays valid.
+    ids = np.array([[3, 1], [1, 3]], np.uint32)
+    assert oracle.expert_major_csr(ids, 4)[0] == 0
+    dup = np.array([[3, 1], [2, 2]], np.uint32)
+    assert oracle.expert_major_csr(dup, 4)[0] == INVALID_STATE
+    assert oracle.expert_major_plan(dup, np.full((2, 2), 0.5))[0] == INVALID_STATE
+
+
 def test_splitmix64_known_answer(oracle):
     """The generator's word i of key k is SplitMix64's output i after seeding
     with k (Steele, Lea & Flood 2014): mix(k + (i+1) * golden).  Published
