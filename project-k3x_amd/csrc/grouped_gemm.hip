@@ -8,9 +8,12 @@
 // rows).  Per K tile (128 K):
 //   * the chunk's activation rows (gathered through pair_token for the
 //     routed gate/up) arrive in LDS by buffer loads that write LDS directly
-//     (no registers), into a ring of kWideStages tiles; each row's 16-byte chunks
-//     are XOR-swizzled by the row index, so the MFMA operand reads of 16 lanes
-//     (16 rows, one column chunk) hit 16 different bank groups;
+//     (no registers), into a ring of kWideStages tiles.  A tile is stored as
+//     32 KiB of row quads: rows 4q .. 4q + 3 fill 1 KiB, 16-byte chunk c of
+//     row r at (r / 4) KiB + (c ^ (r / 4 % 4)) * 64 + (r % 4) * 16, a layout
+//     measured at the ds_read_b128 rate of a linear read for the MFMA
+//     operand pattern (16 lanes = 16 rows of one chunk), where row-major
+//     XOR or padded layouts take about 1.4x as long;
 //   * each wave dequantises its weight fragments once (v_cvt_scalef32_pk_
 //     bf16_fp4 per code byte) and feeds each to the MFMAs of the chunk's
 //     eight 16-row tiles (four when the chunk has at most 64 rows);
@@ -130,19 +133,19 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         FP4 ? (uint32_t)(a.scales_per_expert * 4) : 0u, 0x00020000);
     const uint32_t lane16 = lane * 16, lane4 = lane * 4;
 
-    // Activation tile loads: wave w's load q fills LDS rows 16 w + 4 q .. + 3
-    // (1 KiB: lane l writes row 16 w + 4 q + l / 16, position l % 16).  The
-    // position p of row r holds the row's 16-byte chunk p ^ (r % 16).  Rows
+    // Activation tile loads: wave w's load q fills the row quad 4 w + q
+    // (rows 16 w + 4 q .. + 3, 1 KiB: lane l writes row 16 w + 4 q + l % 4 at
+    // position l / 4, which holds the row's 16-byte chunk (l / 4) ^ q).  Rows
     // past the chunk's end repeat its last row (they are never stored).
     const __amdgpu_buffer_rsrc_t arsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.a), (short)0, a.a_bytes, 0x00020000);
     uint32_t aoff[kALoads];
 #pragma unroll
     for (int q = 0; q < kALoads; ++q) {
-        const uint32_t r = 16 * wave + 4 * q + (lane >> 4);
+        const uint32_t r = 16 * wave + 4 * q + (lane & 3);
         const uint32_t rr = off + m0 + min(r, rows - 1);
         const uint32_t src = a.gather ? a.pair_token[rr] : rr;
-        aoff[q] = (src * a.a_stride + ((lane & 15) ^ (r & 15)) * 8) * 2;
+        aoff[q] = (src * a.a_stride + ((lane >> 2) ^ q) * 8) * 2;
     }
     // Down: the output row of chunk row tid % 128 (the pair's token * top_k
     // + slot, or the row itself), requested now so that it has arrived by
@@ -152,11 +155,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         const uint32_t r = off + m0 + min(tid % kWideRows, rows - 1);
         yv = a.scatter ? a.pair_token[r] * a.top_k + a.pair_slot[r] : r;
     }
-    // MFMA operand position of lane (n, g), 8-column group j of row n:
-    // chunk 4 g + j, swizzled.
+    // MFMA operand of lane (n, g), 8-column group j: row n (+ 16 per row
+    // tile, 4 KiB), chunk 4 g + j; in 16-byte units.
     uint32_t apos[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) apos[j] = n * 16 + ((4 * g + j) ^ n);
+    for (int j = 0; j < 4; ++j) apos[j] = (n >> 2) * 64 + (4 * g + (j ^ (n >> 2))) * 4 + (n & 3);
 
     // Weight stages: codes bc[d][nt][w][u] of K tile k in stage d = k % 4
     // (three are live at a time: tiles k .. k + 2 while tile k is

@@ -682,6 +682,18 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 //                  + shared[t][h]), float mul then float add per term
 // (runtime/src/backend_cpu.cpp:295-301, runtime/src/model.cpp:1145).
 // ---------------------------------------------------------------------------
+// VEC adjacent h per thread; the slots' loads are issued in batches of 16
+// ahead of the slot-ordered multiply-adds.  H % VEC == 0.
+template <int VEC>
+struct CombineVec;
+template <>
+struct CombineVec<1> { typedef float T; };
+template <>
+struct CombineVec<2> { typedef float2 T; };
+template <>
+struct CombineVec<4> { typedef float4 T; };
+
+template <int VEC>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
                                                       const float* __restrict__ w,
                                                       const float* __restrict__ shared,
@@ -689,17 +701,48 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
                                                       uint16_t* __restrict__ out,
                                                       float* __restrict__ out_f32,
                                                       const uint32_t* status) {
+    typedef typename CombineVec<VEC>::T vec_t;
+    constexpr uint32_t kBatch = 16;
     if (*(volatile const uint32_t*)status) return;
-    const uint32_t h = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t h = (blockIdx.x * 256 + threadIdx.x) * VEC;
     const uint32_t t = blockIdx.y;
     if (h >= H) return;
-    float mix = 0.0f;
-    for (uint32_t s = 0; s < K; ++s)
-        mix = __fadd_rn(mix, __fmul_rn(w[(size_t)t * K + s], y[((size_t)t * K + s) * H + h]));
-    const float v = shared ? __fadd_rn(mix, shared[(size_t)t * H + h]) : mix;
-    out[(size_t)t * H + h] = f32_to_bf16(v);
-    if (out_f32) out_f32[(size_t)t * H + h] = v;
+    const float* yt = y + (size_t)t * K * H + h;
+    const float* wt = w + (size_t)t * K;
+    float mix[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) mix[c] = 0.0f;
+    for (uint32_t s0 = 0; s0 < K; s0 += kBatch) {
+        vec_t v[kBatch];
+        float ws[kBatch];
+#pragma unroll
+        for (uint32_t i = 0; i < kBatch; ++i) {
+            const uint32_t s = min(s0 + i, K - 1);  // clamped: loads stay unconditional
+            v[i] = *reinterpret_cast<const vec_t*>(yt + (size_t)s * H);
+            ws[i] = wt[s];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kBatch; ++i) {
+            if (s0 + i >= K) break;
+            const float* vi = reinterpret_cast<const float*>(&v[i]);
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) mix[c] = __fadd_rn(mix[c], __fmul_rn(ws[i], vi[c]));
+        }
+    }
+    if (shared) {
+        const vec_t sh = *reinterpret_cast<const vec_t*>(shared + (size_t)t * H + h);
+        const float* sv = reinterpret_cast<const float*>(&sh);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) mix[c] = __fadd_rn(mix[c], sv[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+        out[(size_t)t * H + h + c] = f32_to_bf16(mix[c]);
+        if (out_f32) out_f32[(size_t)t * H + h + c] = mix[c];
+    }
 }
+
+constexpr int kCombineVec = 1;  // h per thread of combine_kernel
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -1079,7 +1122,7 @@ namespace k3x_hip {
 int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
                    uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32) {
     const int mark = begin_stage(ctx, K3X_STAGE_COMBINE);
-    hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, ctx->stream, y,
+    hipLaunchKernelGGL(combine_kernel<kCombineVec>, dim3((H / kCombineVec + 255) / 256, T), dim3(256), 0, ctx->stream, y,
                        weights, shared, K, H, out, out_f32, ctx->status);
     end_stage(ctx, mark);
     return launched(ctx, 1);
