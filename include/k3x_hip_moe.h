@@ -285,7 +285,9 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
  * bf16 input [T][hidden], ids/weights device [T][K] in router order.  Routes
  * must not repeat an expert within a token and weights must be finite
  * (checked on the host copy passed in host_ids/host_weights, which may be
- * NULL to skip the check).  Replaces ComputeBackend::mxfp4_situ_moe
+ * NULL to skip the check).  With host_ids, only the routed slots must hold
+ * admitted experts (K3X_ERR_INVALID_STATE otherwise); without, every slot of
+ * the bank must.  Replaces ComputeBackend::mxfp4_situ_moe
  * (backend.hpp:364-368) batched over tokens.  Asynchronous. */
 int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                                const k3x_hip_moe_params* params,

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <iterator>
 #include <new>
 
 #include "k3x_device.hpp"
@@ -527,6 +528,11 @@ int k3x_hip_bank_upload_expert(k3x_hip_bank* bank, uint32_t expert, const uint64
             if (s[i] == 0xffu) return K3X_ERR_INVALID_MXFP4;
     k3x_hip_ctx* ctx = bank->ctx;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    // The slot is about to be overwritten: whatever it held is no longer
+    // resident (its ids stop resolving to it, even if the upload fails).
+    bank->expert_ready[expert] = 0;
+    for (auto it = bank->tensor_ids.begin(); it != bank->tensor_ids.end();)
+        it = it->second / 4 == expert ? bank->tensor_ids.erase(it) : std::next(it);
     // Staging buffer holding the six source arrays, each 256-byte aligned so
     // the re-tile kernels can read 16-byte vectors.
     const uint8_t* host[6] = {gate_packed, gate_scales, up_packed, up_scales, down_packed,

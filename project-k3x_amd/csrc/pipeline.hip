@@ -803,7 +803,10 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
 
 bool finite_pos(float v) { return std::isfinite(v) && v > 0.0f; }
 
-int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p) {
+// all_experts: every bank slot must be admitted (routes decided on the
+// device may pick any); host routes check their own slots instead.
+int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                    bool all_experts = true) {
     const auto& d = bank->desc;
     if (!p->tokens || p->tokens > (1u << 20) || !p->top_k || p->top_k > 64 ||
         p->top_k > d.experts)
@@ -814,8 +817,9 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p) {
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
         return K3X_ERR_INVALID_MXFP4;
-    for (uint8_t r : bank->expert_ready)
-        if (!r) return K3X_ERR_INVALID_STATE;
+    if (all_experts)
+        for (uint8_t r : bank->expert_ready)
+            if (!r) return K3X_ERR_INVALID_STATE;
     if (d.shared_inter && !bank->shared_ready) return K3X_ERR_INVALID_STATE;
     return K3X_OK;
 }
@@ -1180,15 +1184,16 @@ int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                                uint16_t* out, const k3x_hip_moe_taps* taps) {
     if (!ctx || !bank || !p || !xn || !ids || !weights || !out || bank->ctx != ctx)
         return K3X_ERR_INVALID_EXTENT;
-    int st = validate_params(bank, p);
+    int st = validate_params(bank, p, host_ids == nullptr);
     if (st) return st;
     const uint32_t T = p->tokens, K = p->top_k, E = bank->desc.experts;
-    // Route contract of build_expert_major_plan (expert_major.cpp:21-36).
+    // Route contract of build_expert_major_plan (expert_major.cpp:21-36);
+    // a routed slot must hold an admitted expert.
     if (host_ids) {
         for (uint32_t t = 0; t < T; ++t)
             for (uint32_t s = 0; s < K; ++s) {
                 const uint32_t e = host_ids[(size_t)t * K + s];
-                if (e >= E) return K3X_ERR_INVALID_STATE;
+                if (e >= E || !bank->expert_ready[e]) return K3X_ERR_INVALID_STATE;
                 for (uint32_t q = 0; q < s; ++q)
                     if (host_ids[(size_t)t * K + q] == e) return K3X_ERR_INVALID_STATE;
             }

@@ -1,0 +1,182 @@
+// k3x_hip_backend.hpp -- C++20 host side of the MI355X MoE layer: the
+// expert-execution methods of the K3X runtime's ComputeBackend
+// (runtime/include/k3x/backend.hpp:326-462) with the same names, argument
+// meaning and error behaviour, running on libk3x_hip_moe.so through its C ABI
+// (include/k3x_hip_moe.h).
+//
+// Contract, as the reference's backends:
+//   * inputs are borrowed host spans, valid for the call; results come back
+//     by value after the device work has finished (every method is
+//     synchronous);
+//   * no exceptions cross the interface: failures are Result::failure with an
+//     ErrorCode, and argument checks run before anything is uploaded or
+//     launched;
+//   * experts are resident: the first use of an expert (keyed by the
+//     tensor_id of its three matrices) admits it into a bank slot of its
+//     layer; later uses find it there (ResidentWeightTable::acquire,
+//     runtime/cuda/resident_weights.cu:107-166).  When every slot is taken,
+//     the least recently used expert not needed by the current call is
+//     replaced.
+// Numerics: the layer's rounding points -- the input and the GLU output are
+// rounded to bf16 (round to nearest even), matrix products accumulate in
+// fp32, the per-expert outputs and the slot-ordered mix stay fp32 -- where
+// the reference CPU backend keeps fp32 inputs and double sums.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <span>
+#include <string>
+#include <string_view>
+#include <utility>
+#include <vector>
+
+namespace k3x_amd {
+
+// Same enumerators in the same order (hence the same values) as
+// k3x::ErrorCode (runtime/include/k3x/status.hpp:9-31); the C ABI's status
+// codes are these values.
+enum class ErrorCode {
+    ok,
+    io_error,
+    bad_magic,
+    unsupported_version,
+    unsupported_required_feature,
+    non_executable_artifact,
+    superblock_crc_mismatch,
+    truncated_file,
+    invalid_directory,
+    invalid_extent,
+    data_crc_mismatch,
+    auxiliary_crc_mismatch,
+    directory_sha256_mismatch,
+    root_sha256_mismatch,
+    tensor_not_found,
+    invalid_mxfp4,
+    invalid_state,
+    backend_unavailable,
+    storage_unavailable,
+    unsupported_architecture,
+};
+
+const char* error_code_name(ErrorCode code);
+
+// A value or an error code with a message (the interface of k3x::Result,
+// status.hpp:58-76).
+template <typename T>
+class Result {
+public:
+    static Result success(T value) { return Result(std::move(value)); }
+    static Result failure(ErrorCode code, std::string message = {}) {
+        return Result(code, std::move(message));
+    }
+    explicit operator bool() const { return value_.has_value(); }
+    T& value() { return *value_; }
+    const T& value() const { return *value_; }
+    ErrorCode error() const { return error_; }
+    const std::string& message() const { return message_; }
+
+private:
+    explicit Result(T value) : value_(std::move(value)) {}
+    Result(ErrorCode code, std::string message) : error_(code), message_(std::move(message)) {}
+    std::optional<T> value_;
+    ErrorCode error_{ErrorCode::ok};
+    std::string message_;
+};
+
+enum class ProfilePhase { prefill, decode };  // runtime/include/k3x/profile.hpp:11
+
+// One MXFP4 matrix in the K3X layout: packed [rows][cols/2] (low nibble =
+// even column), scales [rows][cols/group_size] E8M0 (backend.hpp:150-157).
+struct Mxfp4WeightView {
+    std::uint64_t tensor_id;
+    std::span<const std::byte> packed;
+    std::span<const std::byte> scales;
+    std::size_t rows;
+    std::size_t cols;
+    std::size_t group_size;
+};
+
+// gate [I x H], up [I x H], down [out x I] (backend.hpp:315-319).
+struct Mxfp4MlpView {
+    Mxfp4WeightView gate;
+    Mxfp4WeightView up;
+    Mxfp4WeightView down;
+};
+
+struct HipBackendOptions {
+    int device = 0;
+    // Bank slots per (layer, hidden, intermediate) shape; each slot holds
+    // one expert (hidden * intermediate * 3 * 17 / 32 bytes, 23.4 MB at
+    // 7168 x 2048).
+    std::uint32_t resident_experts = 64;
+};
+
+struct HipBackendStats {
+    std::uint64_t calls = 0;             // method calls that reached the device
+    std::uint64_t layer_calls = 0;       // library layer calls they made
+    std::uint64_t kernel_launches = 0;
+    std::uint64_t experts_admitted = 0;  // slot uploads
+    std::uint64_t residency_hits = 0;    // experts found resident
+    std::uint64_t weight_h2d_bytes = 0;
+};
+
+class HipMoeBackend {
+public:
+    ~HipMoeBackend();
+    HipMoeBackend(const HipMoeBackend&) = delete;
+    HipMoeBackend& operator=(const HipMoeBackend&) = delete;
+
+    // One token through each expert: outputs[e] = down(GLU(gate x, up x))
+    // (backend.hpp:348-351, backend_cpu.cpp:124-154).
+    Result<std::vector<std::vector<float>>> mxfp4_situ_mlp_group(
+        std::span<const float> input, std::span<const Mxfp4MlpView> experts, float situ_beta,
+        std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase);
+    // batch_size tokens (rows of inputs) through one expert: outputs[t]
+    // (backend.hpp:352-356, backend_cpu.cpp:156-189).
+    Result<std::vector<std::vector<float>>> mxfp4_situ_mlp_batch(
+        std::span<const float> inputs, std::size_t batch_size, Mxfp4MlpView expert,
+        float situ_beta, std::optional<float> situ_linear, std::uint32_t layer,
+        ProfilePhase phase);
+    // token_count tokens through every expert: outputs[e] = the token_count
+    // outputs of expert e, concatenated (backend.hpp:357-363,
+    // backend_cpu.cpp:191-264).
+    Result<std::vector<std::vector<float>>> mxfp4_situ_mlp_grid(
+        std::span<const float> inputs, std::size_t token_count,
+        std::span<const Mxfp4MlpView> experts, float situ_beta, std::optional<float> situ_linear,
+        std::uint32_t layer, ProfilePhase phase);
+    // One token: sum over slots, in slot order, of contributions[k] *
+    // expert k's output (backend.hpp:364-368, backend_cpu.cpp:266-303).
+    Result<std::vector<float>> mxfp4_situ_moe(std::span<const float> input,
+                                              std::span<const Mxfp4MlpView> experts,
+                                              std::span<const float> contributions,
+                                              float situ_beta, std::optional<float> situ_linear,
+                                              std::uint32_t layer, ProfilePhase phase);
+    // mxfp4_situ_moe for token_count tokens in one layer call: token t mixes
+    // experts[routes[t * top_k + k]] with contributions[t * top_k + k],
+    // k = 0 .. top_k - 1 (no expert twice in one token); returns
+    // [token_count][hidden].  The batched call the reference's expert-major
+    // verification block makes one group at a time (model.cpp:313-356).
+    Result<std::vector<float>> mxfp4_situ_moe_tokens(
+        std::span<const float> inputs, std::size_t token_count, std::size_t top_k,
+        std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> routes,
+        std::span<const float> contributions, float situ_beta, std::optional<float> situ_linear,
+        std::uint32_t layer, ProfilePhase phase);
+
+    HipBackendStats runtime_stats() const noexcept;
+    std::string_view device_name() const noexcept;
+
+    struct Impl;
+
+private:
+    friend Result<std::unique_ptr<HipMoeBackend>> make_hip_backend(const HipBackendOptions&);
+    explicit HipMoeBackend(std::unique_ptr<Impl> impl);
+    std::unique_ptr<Impl> impl_;
+};
+
+// The factory beside make_cuda_backend (backend.hpp:465-466).
+Result<std::unique_ptr<HipMoeBackend>> make_hip_backend(const HipBackendOptions& options = {});
+
+}  // namespace k3x_amd

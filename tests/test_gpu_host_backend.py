@@ -1,0 +1,24 @@
+"""GPU run of the C++ host side's test program (tests/cpp/test_hip_backend.cpp):
+HipMoeBackend's group / batch / grid / mix methods against the oracle, the
+reference's rejections, residency hits and replacement.  Exit status 0 is a
+pass; any other status names the failed check (see the program)."""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "tests", "cpp", "test_hip_backend")
+
+
+def test_hip_backend_program():
+    assert os.path.exists(EXE), "tests/cpp/test_hip_backend not built (__graft_entry__.build())"
+    print("[gpu-test] tests/cpp/test_hip_backend", flush=True)
+    r = subprocess.run([EXE], capture_output=True, text=True, timeout=110)
+    sys.stdout.write(r.stdout)
+    assert r.returncode == 0, f"exit {r.returncode}: {r.stdout[-2000:]} {r.stderr[-2000:]}"

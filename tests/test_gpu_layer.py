@@ -111,6 +111,31 @@ def test_upload_rejects_reserved_scale(hip):
     bank.close()
 
 
+def test_upload_replaces_slot_identity(hip):
+    """A slot uploaded again holds the new expert only: the old tensor ids stop
+    resolving to it and may be admitted into another slot (exact residency,
+    runtime/cuda/resident_weights.cu:107-166)."""
+    k3x_amd, ctx = hip
+    bank = k3x_amd.Bank(ctx, k3x_amd.LayerShape(hidden=128, inter=128, experts=2))
+    n = 128 * 128
+    ex = dict(gate_packed=np.zeros(n // 2, np.uint8), gate_scales=np.full(n // 32, 127, np.uint8),
+              up_packed=np.zeros(n // 2, np.uint8), up_scales=np.full(n // 32, 127, np.uint8),
+              down_packed=np.zeros(n // 2, np.uint8), down_scales=np.full(n // 32, 127, np.uint8))
+    assert bank.upload_expert(0, ex, tensor_ids=(11, 12, 13)) == 0
+    assert bank.upload_expert(0, ex, tensor_ids=(21, 22, 23)) == 0
+    for tid in (11, 12, 13):
+        assert bank.find(tid)[0] == k3x_amd.ERR_TENSOR_NOT_FOUND
+    assert bank.find(22) == (0, 0, 1)
+    assert bank.upload_expert(1, ex, tensor_ids=(11, 12, 13)) == 0
+    assert bank.find(13) == (0, 1, 2)
+    # Arguments are checked before the slot is touched: a rejected upload
+    # leaves its expert resident.
+    ex["gate_scales"][0] = 0xFF
+    assert bank.upload_expert(1, ex, tensor_ids=(31, 32, 33)) == k3x_amd.ERR_INVALID_MXFP4
+    assert bank.find(11) == (0, 1, 0)
+    bank.close()
+
+
 # ---------------------------------------------------------------------------
 # Full layer on the seeded benchmark configurations.
 # ---------------------------------------------------------------------------
