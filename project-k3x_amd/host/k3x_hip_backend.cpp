@@ -195,11 +195,18 @@ struct HipMoeBackend::Impl {
             }
             if (victim == n) return ErrorCode::backend_unavailable;  // more experts than slots
             const std::uint64_t tid[3] = {e.gate.tensor_id, e.up.tensor_id, e.down.tensor_id};
-            b.slots[victim] = Slot{};
             const int st = k3x_hip_bank_upload_expert(
                 b.bank, (std::uint32_t)victim, tid, bytes(e.gate.packed), bytes(e.gate.scales),
                 bytes(e.up.packed), bytes(e.up.scales), bytes(e.down.packed), bytes(e.down.scales));
-            if (st) return code_of(st);
+            if (st) {
+                // Rejected arguments leave the slot as it was; a failure
+                // after the slot was touched leaves it empty.
+                std::uint32_t at = 0, m = 0;
+                if (b.slots[victim].ids[0] &&
+                    (k3x_hip_bank_find(b.bank, b.slots[victim].ids[0], &at, &m) != 0 || at != victim))
+                    b.slots[victim] = Slot{};
+                return code_of(st);
+            }
             std::copy(tid, tid + 3, b.slots[victim].ids);
             pinned[victim] = 1;
             slot[i] = (std::uint32_t)victim;
