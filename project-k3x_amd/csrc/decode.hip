@@ -152,6 +152,7 @@ __device__ inline uint32_t prior_status(const uint32_t* status) { return *status
 // ---------------------------------------------------------------------------
 struct NormShared {
     float inv[kMaxDecodeTokens];
+    double part[kFrontWaves];  // per-wave sums of squares
     int bad;
 };
 
@@ -177,6 +178,9 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
     const float* s_g = reinterpret_cast<const float*>(s_x4 + chunks);
     if (tid == 0) ns.bad = 0;
     constexpr int kLoads = 8;
+    // Every block of the launch reads the same x and gamma: each starts at
+    // its own offset so that they do not all request the same lines at once.
+    const uint32_t rot = (blockIdx.x * 613u) % all;
     for (uint32_t c0 = 0; c0 < all; c0 += kLoads * kThreads) {
         // One unconditional load and store per slot (slots past the end
         // copy the last chunk again, the same value to the same place): no
@@ -184,7 +188,7 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         uint4 v[kLoads];
 #pragma unroll
         for (int it = 0; it < kLoads; ++it) {
-            const uint32_t c = min(c0 + tid + kThreads * it, all - 1);
+            const uint32_t c = (min(c0 + tid + kThreads * it, all - 1) + rot) % all;
             const uint4* src = c < chunks ? reinterpret_cast<const uint4*>(x) + c
                                           : reinterpret_cast<const uint4*>(gamma) + (c - chunks);
             v[it] = *src;
@@ -194,29 +198,53 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
             if (prior_status(prior)) return false;
         }
 #pragma unroll
-        for (int it = 0; it < kLoads; ++it) s_x4[min(c0 + tid + kThreads * it, all - 1)] = v[it];
+        for (int it = 0; it < kLoads; ++it)
+            s_x4[(min(c0 + tid + kThreads * it, all - 1) + rot) % all] = v[it];
     }
     __syncthreads();
-    if (wave < T) {
-        const uint16_t* xr = s_x + (size_t)wave * H;
-        double p[4] = {0.0, 0.0, 0.0, 0.0};
+    // Sum of squares per token in the canonical order -- partial q (of 256)
+    // sums the elements 256 j + q over j in sequence, then the balanced
+    // pairwise tree over q -- spread over nw = 4 (T <= 2) or 2 waves per
+    // token: wave u of token t owns partials [256 u / nw, 256 (u + 1) / nw),
+    // reduces them across lanes (the tree's lower levels) and the top levels
+    // add the wave sums.  Every tree node adds the same two children as a
+    // one-wave reduction (canon_reduce), so the sum is bit-identical.
+    static_assert(kThreads / 64 >= 2 * kMaxDecodeTokens, "two waves per token");
+    const uint32_t nw = T <= 2 ? 4 : 2, t = wave / nw, u = wave % nw;
+    if (t < T) {
+        const uint16_t* xr = s_x + (size_t)t * H;
+        double v;
         int bad = 0;
-        for (uint32_t j = 0; j < H / 256; ++j) {
-            const uint2 w = *reinterpret_cast<const uint2*>(xr + 256 * j + 4 * lane);
-            const float f[4] = {lo_bf16(w.x), hi_bf16(w.x), lo_bf16(w.y), hi_bf16(w.y)};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                bad |= !__builtin_isfinite(f[c]);
-                p[c] = __builtin_fma((double)f[c], (double)f[c], p[c]);  // exact product
+        if (nw == 4) {
+            double p = 0.0;
+            for (uint32_t j = 0; j < H / 256; ++j) {
+                const float f = bf16_to_f32(xr[256 * j + 64 * u + lane]);
+                bad |= !__builtin_isfinite(f);
+                p = __builtin_fma((double)f, (double)f, p);  // exact product
             }
+            v = p;
+        } else {
+            double p0 = 0.0, p1 = 0.0;
+            for (uint32_t j = 0; j < H / 256; ++j) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(xr + 256 * j + 128 * u + 2 * lane);
+                const float f0 = lo_bf16(w), f1 = hi_bf16(w);
+                bad |= !__builtin_isfinite(f0) | !__builtin_isfinite(f1);
+                p0 = __builtin_fma((double)f0, (double)f0, p0);
+                p1 = __builtin_fma((double)f1, (double)f1, p1);
+            }
+            v = p0 + p1;
         }
-        const double s = canon_reduce(p);
-        bad = __any(bad);
-        if (lane == 0) {
-            if (bad) ns.bad = 1;
-            const float mean = (float)__ddiv_rn(s, (double)H);
-            ns.inv[wave] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
-        }
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+        if (__any(bad) && lane == 0) ns.bad = 1;
+        if (lane == 0) ns.part[wave] = v;
+    }
+    __syncthreads();
+    if (tid < T) {
+        const double* q = ns.part + tid * nw;
+        const double s = nw == 4 ? (q[0] + q[1]) + (q[2] + q[3]) : q[0] + q[1];
+        const float mean = (float)__ddiv_rn(s, (double)H);
+        ns.inv[tid] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     }
     __syncthreads();
     if (ns.bad) {
