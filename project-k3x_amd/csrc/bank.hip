@@ -160,7 +160,7 @@ int check_launch(k3x_hip_ctx* ctx, unsigned launches = 1) {
 void free_bank_memory(k3x_hip_bank* b) {
     for (void* p : {(void*)b->gu_codes, (void*)b->gu_scales, (void*)b->dn_codes,
                     (void*)b->dn_scales, (void*)b->sh_gu, (void*)b->sh_dn, (void*)b->router_w,
-                    (void*)b->router_bias, (void*)b->gamma})
+                    (void*)b->router_wp, (void*)b->router_bias, (void*)b->gamma})
         if (p) (void)hipFree(p);
 }
 
@@ -471,6 +471,9 @@ int k3x_hip_bank_create(k3x_hip_ctx* ctx, const k3x_hip_layer_desc* desc, k3x_hi
     st = st ? st : alloc(&b->dn_codes, E * b->dn_codes_per_expert, &b->device_bytes);
     st = st ? st : alloc(&b->dn_scales, E * b->dn_scales_per_expert * 4, &b->device_bytes);
     st = st ? st : alloc(&b->router_w, E * d.hidden * sizeof(float), &b->device_bytes);
+    if (k3x_hip::router_mfma_eligible(d.hidden))
+        st = st ? st : alloc(&b->router_wp, k3x_hip::router_wp_floats(d.experts) * sizeof(float),
+                             &b->device_bytes);
     st = st ? st : alloc(&b->router_bias, E * sizeof(float), &b->device_bytes);
     st = st ? st : alloc(&b->gamma, (size_t)d.hidden * sizeof(float), &b->device_bytes);
     if (d.shared_inter) {
@@ -627,7 +630,7 @@ int k3x_hip_bank_upload_router(k3x_hip_bank* bank, const float* weight, const fl
         hipMemcpyAsync(bank->router_bias, bias, d.experts * 4, hipMemcpyHostToDevice,
                        ctx->stream) ||
         hipMemcpyAsync(bank->gamma, gamma, d.hidden * 4, hipMemcpyHostToDevice, ctx->stream) ||
-        hipStreamSynchronize(ctx->stream))
+        k3x_hip::permute_router(bank) || hipStreamSynchronize(ctx->stream))
         return K3X_ERR_BACKEND_UNAVAILABLE;
     bank->router_ready = true;
     return K3X_OK;
@@ -638,11 +641,13 @@ int k3x_hip_bank_set_router_device(k3x_hip_bank* bank, const float* weight, cons
     if (!bank || !weight || !bias || !gamma) return K3X_ERR_INVALID_EXTENT;
     const auto& d = bank->desc;
     k3x_hip_ctx* ctx = bank->ctx;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     if (hipMemcpyAsync(bank->router_w, weight, (size_t)d.experts * d.hidden * 4,
                        hipMemcpyDeviceToDevice, ctx->stream) ||
         hipMemcpyAsync(bank->router_bias, bias, d.experts * 4, hipMemcpyDeviceToDevice,
                        ctx->stream) ||
-        hipMemcpyAsync(bank->gamma, gamma, d.hidden * 4, hipMemcpyDeviceToDevice, ctx->stream))
+        hipMemcpyAsync(bank->gamma, gamma, d.hidden * 4, hipMemcpyDeviceToDevice, ctx->stream) ||
+        k3x_hip::permute_router(bank))
         return K3X_ERR_BACKEND_UNAVAILABLE;
     bank->router_ready = true;
     return K3X_OK;
@@ -669,6 +674,7 @@ int k3x_hip_bank_fill_synthetic(k3x_hip_bank* bank, const k3x_hip_synth_desc* s)
     hipLaunchKernelGGL(fill_const_f32, dim3(blocks_for(d.hidden)), dim3(kThreads), 0,
                        ctx->stream, (size_t)d.hidden, s->gamma_value, bank->gamma);
     st = check_launch(ctx, 3);
+    st = st ? st : k3x_hip::permute_router(bank);
     if (!st && d.shared_inter) {
         const uint16_t* none3[3] = {nullptr, nullptr, nullptr};
         st = retile_shared(bank, none3, s->seed, s->shared_sigma);

@@ -70,6 +70,7 @@ struct k3x_hip_bank {
     uint8_t* sh_gu = nullptr;
     uint8_t* sh_dn = nullptr;
     float* router_w = nullptr;   // [E][H]
+    float* router_wp = nullptr;  // [E/16][256][16][4][8] tile/residue-major router_w (H <= 8192)
     float* router_bias = nullptr;
     float* gamma = nullptr;
     bool router_ready = false;
@@ -106,12 +107,22 @@ struct LayerBuffers {
     uint32_t* witems;      // wide GEMM work items (expert << 16 | 128-row chunk)
     uint32_t* n_witems;    // [1]
     uint8_t* gscratch;     // grouping: per-chunk counts and first uses, pair ranks
+    uint16_t* xp;          // [T/16][256][16][4][8] bf16 tile/residue-major xn (in y's bytes)
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }
 
 // Makes sure ctx->scratch holds at least `bytes`; grow-only.
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
+
+// Refreshes bank->router_wp from bank->router_w on the context stream (a
+// no-op when the hidden size has no residue-major copy).
+int permute_router(k3x_hip_bank* bank);
+
+// Whether a bank of this hidden size keeps the residue-major router copy,
+// and that copy's size in floats (experts padded to 16).
+bool router_mfma_eligible(uint32_t hidden);
+size_t router_wp_floats(uint32_t experts);
 
 // Brackets the launches made between begin and end with an event pair when
 // profiling is on.  begin_stage returns the index of the open mark or -1.

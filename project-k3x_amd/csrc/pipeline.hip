@@ -44,31 +44,88 @@ __device__ inline double block_tree_sum(double v, double* red) {
 // with the canonical order for the sum of squares and the bf16 rounding of
 // the normalised activation.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kNormRegHidden = 8192;  // rows up to this stay in registers
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const float* __restrict__ gamma,
                                                       uint32_t H, float eps,
                                                       uint16_t* __restrict__ xn,
+                                                      uint16_t* __restrict__ xp,
                                                       uint32_t* status) {
     __shared__ double red[4];
     if (*(volatile uint32_t*)status) return;
     const uint16_t* xr = x + (size_t)blockIdx.x * H;
+    uint16_t* out = xn + (size_t)blockIdx.x * H;
+    const uint32_t tid = threadIdx.x;
+    if (H > kNormRegHidden) {
+        double s = 0.0;
+        int bad = 0;
+        for (uint32_t k = tid; k < H; k += 256) {
+            const float v = bf16_to_f32(xr[k]);
+            bad |= !__builtin_isfinite(v);
+            s = __builtin_fma((double)v, (double)v, s);  // exact product: fused == separate
+        }
+        if (__syncthreads_or(bad)) {
+            if (tid == 0) latch(status, K3X_ERR_INVALID_MXFP4);
+            return;
+        }
+        s = block_tree_sum(s, red);
+        const float mean = (float)__ddiv_rn(s, (double)H);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+        for (uint32_t k = tid; k < H; k += 256)
+            out[k] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xr[k]), inv), gamma[k]));
+        return;
+    }
+    // The whole row in registers: this thread's k = tid + 256 j, j < 32.
+    // Loads past the row read 0 (buffer range check), and the +0 terms they
+    // add after the row's last term leave the sum of squares unchanged.
+    const __amdgpu_buffer_rsrc_t xs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xr), (short)0, H * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t gs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), (short)0, H * 4, 0x00020000);
+    uint16_t xb[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) xb[j] = __builtin_amdgcn_raw_buffer_load_b16(xs, tid * 2, j * 512, 0);
     double s = 0.0;
     int bad = 0;
-    for (uint32_t k = threadIdx.x; k < H; k += 256) {
-        const float v = bf16_to_f32(xr[k]);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float v = bf16_to_f32(xb[j]);
         bad |= !__builtin_isfinite(v);
-        s = __builtin_fma((double)v, (double)v, s);  // exact product: fused == separate
+        s = __builtin_fma((double)v, (double)v, s);
     }
     if (__syncthreads_or(bad)) {
-        if (threadIdx.x == 0) latch(status, K3X_ERR_INVALID_MXFP4);
+        if (tid == 0) latch(status, K3X_ERR_INVALID_MXFP4);
         return;
     }
     s = block_tree_sum(s, red);
     const float mean = (float)__ddiv_rn(s, (double)H);
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
-    uint16_t* out = xn + (size_t)blockIdx.x * H;
-    for (uint32_t k = threadIdx.x; k < H; k += 256)
-        out[k] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xr[k]), inv), gamma[k]));
+    uint32_t b[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float g = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gs, tid * 4, j * 1024, 0));
+        b[j] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xb[j]), inv), g));
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        if (tid + 256u * j < H) out[tid + 256 * j] = (uint16_t)b[j];
+    if (!xp) return;
+    // Tile- and residue-major copy for router_mfma_kernel: k = tid + 256 j
+    // with j = 4m + q goes to slot 8q + m of this token's 32 terms of
+    // residue tid in its 16-token tile.
+    u32x4* dst = reinterpret_cast<u32x4*>(
+        xp + ((size_t)(blockIdx.x / 16) * 256 + tid) * (16 * 32) + (blockIdx.x % 16) * 32);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int s0 = 8 * c + 2 * h, s1 = s0 + 1;  // slots -> j = 4m + q
+            w[h] = b[4 * (s0 % 8) + s0 / 8] | b[4 * (s1 % 8) + s1 / 8] << 16;
+        }
+        dst[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -232,6 +289,172 @@ __global__ __launch_bounds__(256) void router_tile_kernel(const float* __restric
 }
 
 constexpr int kRouterEpb = 8, kRouterTpb = 8;  // router_tile_kernel tile for T > 4
+
+// ---------------------------------------------------------------------------
+// Router logits on the fp64 matrix cores.
+//
+// Tile- and residue-major operands: for residue i (k = i + 256 j), j = 4m + q
+// and 16-row tiles (e = 16 et + n, t = 16 tt + n),
+//   Wp[et][i][n][q][m] = W[e][k]   fp32, m < 8 (k >= H and e >= E padded with 0)
+//   xp[tt][i][n][q][m] = xn[t][k]  bf16
+// so lane l of a wave (row n = l % 16, q = l / 16) reads the 8 terms m of its
+// (n, q) with one 32-byte (W) / 16-byte (x) load per residue, and one
+// residue of a tile is a contiguous 2 KiB (W) / 1 KiB (x): consecutive
+// residues, and the waves working on them, spread over the L2 channels.
+//
+// v_mfma_f64_16x16x4f64 computes D(e, t) = C(e, t) + sum_q A(e, q) B(q, t) as
+// the sequential chain of fused multiply-adds q = 0, 1, 2, 3, so chaining the
+// NM matrix ops m = 0 .. NM-1 from C = +0 visits j = 4m + q in order: exactly
+// the sequential per-residue sum of router_tile_kernel.  A padded term adds
+// 0 * 0 = +0 to a partial that is never -0 (it starts at +0 and a sum that
+// cancels rounds to +0), so it changes nothing.  Products fp32 x bf16 are
+// exact in fp64.  The 256 residue partials then meet in the same balanced
+// pairwise tree over i: each wave folds its R = 256 / WPB consecutive residues
+// with a binary carry stack (pairs (2a, 2a+1), then pairs of pairs, ...), and
+// the block joins the WPB wave subtrees in tree order through LDS.
+// One block per 16-expert x 16-token tile; D(e, t) lands in lane
+// 16 (e % 4) + t, register e / 4.
+// ---------------------------------------------------------------------------
+constexpr int kRouterRes = 256;     // residues of k
+constexpr int kRouterSlot = 32;     // padded terms per residue (4 q x 8 m)
+constexpr uint32_t kRouterMaxHidden = kRouterRes * kRouterSlot;
+constexpr uint32_t kRouterTileRes = 16 * kRouterSlot;  // elements of one tile residue
+constexpr int kRouterWaves = 4;     // waves per block of router_mfma_kernel
+constexpr int kRouterChains = 2;    // residues per wave in flight on the matrix core
+constexpr uint32_t kRouterMfmaMinTokens = 256;
+
+__global__ __launch_bounds__(256) void permute_router_kernel(const float* __restrict__ W,
+                                                             uint32_t E, uint32_t H,
+                                                             float* __restrict__ Wp) {
+    const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t et = (uint32_t)(o / (kRouterRes * kRouterTileRes));
+    if (et >= (E + 15) / 16) return;
+    const uint32_t r = (uint32_t)(o % (kRouterRes * kRouterTileRes));
+    const uint32_t i = r / kRouterTileRes, n = (r / kRouterSlot) % 16;
+    const uint32_t q = (r / 8) % 4, m = r % 8;
+    const uint32_t e = 16 * et + n, k = i + kRouterRes * (4 * m + q);
+    Wp[o] = e < E && k < H ? W[(size_t)e * H + k] : 0.0f;
+}
+
+typedef __attribute__((ext_vector_type(4))) double f64x4;
+
+template <int NM, int WPB>
+__global__ __launch_bounds__(64 * WPB) void router_mfma_kernel(const float* __restrict__ Wp,
+                                                               const uint16_t* __restrict__ xp,
+                                                               uint32_t E, uint32_t T,
+                                                               float* __restrict__ logits,
+                                                               const uint32_t* status) {
+    constexpr int R = kRouterRes / WPB;  // residues per wave
+    constexpr int G = R / 16;            // groups of 16 residues per wave
+    constexpr int LG = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : G == 8 ? 3 : 4;
+    constexpr int C = kRouterChains;     // residues whose chains run interleaved
+    constexpr int LC = C == 1 ? 0 : C == 2 ? 1 : 2;
+    constexpr int D = 2 * C > 4 ? 2 * C : 4;  // residues of loads in flight
+    static_assert(NM >= 1 && NM <= 8 && (1 << LG) == G && R % 16 == 0, "tile shape");
+    static_assert((1 << LC) == C && D % C == 0 && 16 % D == 0, "chains");
+    __shared__ f64x4 red[WPB > 1 ? WPB - 1 : 1][64];
+    if (*(volatile const uint32_t*)status) return;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar offsets
+    const uint32_t e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+    const uint32_t row = lane % 16, q = lane / 16;
+    // Per-block resources over this block's two tiles.  Rows past E read
+    // the zero padding, rows past T whatever the padded scratch holds: either
+    // only reaches outputs that are not stored.
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(Wp + (size_t)blockIdx.x * kRouterRes * kRouterTileRes), (short)0,
+        kRouterRes * kRouterTileRes * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(xp + (size_t)blockIdx.y * kRouterRes * kRouterTileRes), (short)0,
+        kRouterRes * kRouterTileRes * 2, 0x00020000);
+    const uint32_t wv = row * (kRouterSlot * 4) + q * 32;
+    const uint32_t xv = row * (kRouterSlot * 2) + q * 16;
+    const uint32_t i0 = wave * R;
+    u32x4 wa[D], wb[D], xa[D];
+    auto load = [&](int slot, uint32_t i) {
+        wa[slot] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv, i * (kRouterTileRes * 4), 0);
+        wb[slot] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + 16, i * (kRouterTileRes * 4), 0);
+        xa[slot] = __builtin_amdgcn_raw_buffer_load_b128(xr, xv, i * (kRouterTileRes * 2), 0);
+    };
+    auto wterm = [&](int slot, int m) {
+        return (double)__uint_as_float(m < 4 ? wa[slot][m] : wb[slot][m - 4]);
+    };
+    auto xterm = [&](int slot, int m) {
+        const uint32_t xw = xa[slot][m / 2];
+        return (double)__uint_as_float(m % 2 ? xw & 0xffff0000u : xw << 16);
+    };
+    // Partials of C consecutive residues, their matrix-op chains interleaved.
+    auto partials = [&](int r0, f64x4* p) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) p[c] = f64x4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                p[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(wterm((r0 + c) % D, m),
+                                                            xterm((r0 + c) % D, m), p[c], 0, 0, 0);
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, i0 + d);
+    f64x4 so[LG > 0 ? LG : 1];
+    f64x4 v;
+    for (int g = 0; g < G; ++g) {
+        f64x4 st[4];
+#pragma unroll
+        for (int r = 0; r < 16; r += C) {
+            f64x4 p[C];
+            partials(r, p);
+            // Scheduling fences keep the refill of these slots D residues
+            // ahead of its use (the scheduler would otherwise sink it).
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < C; ++c) load((r + c) % D, min(i0 + 16 * g + r + c + D, i0 + R - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            // Residues r .. r+C-1 (r a multiple of C) form a subtree; fold it,
+            // then carry it into the levels above.
+#pragma unroll
+            for (int w = 1; w < C; w *= 2)
+#pragma unroll
+                for (int c = 0; c < C; c += 2 * w) p[c] = p[c] + p[c + w];
+            v = p[0];
+#pragma unroll
+            for (int L = LC; L < 4; ++L) {
+                if (!((r >> L) & 1)) {
+                    st[L] = v;
+                    break;
+                }
+                v = st[L] + v;
+            }
+        }
+        // v: the subtree of group g; carry it into the levels above.
+#pragma unroll
+        for (int L = 0; L < LG; ++L) {
+            if (!((g >> L) & 1)) {
+                so[L] = v;
+                break;
+            }
+            v = so[L] + v;
+        }
+    }
+    // v: this wave's subtree of R residues.
+    if (wave) red[wave - 1][lane] = v;
+    __syncthreads();
+    if (wave) return;
+    if constexpr (WPB == 2) {
+        v = v + red[0][lane];
+    } else if constexpr (WPB == 4) {
+        v = (v + red[0][lane]) + (red[1][lane] + red[2][lane]);
+    } else if constexpr (WPB == 8) {
+        v = ((v + red[0][lane]) + (red[1][lane] + red[2][lane])) +
+            ((red[3][lane] + red[4][lane]) + (red[5][lane] + red[6][lane]));
+    }
+    const uint32_t t = t0 + row;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t e = e0 + 4 * r + q;
+        if (e < E && t < T) logits[(size_t)t * E + e] = (float)v[r];
+    }
+}
 
 // Sort key: larger adjusted score first, then lower expert index
 // (runtime/src/official_moe.cpp:226-232).  -0 is folded into +0 so that the
@@ -791,7 +1014,11 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->active_asc = (uint32_t*)take((size_t)d.experts * 4);
     s->active_fu = (uint32_t*)take((size_t)d.experts * 4);
     s->act = (uint16_t*)take(P * d.inter * 2);
-    s->y = (float*)take(P * d.hidden * 4);
+    // y is first written by the down projection, after the router: the
+    // residue-major xn copy of router_mfma_kernel lives in the same bytes.
+    const size_t xp_bytes = (size_t)(T + 15) / 16 * kRouterRes * kRouterTileRes * 2;
+    s->y = (float*)take(std::max(P * d.hidden * 4, xp_bytes));
+    s->xp = reinterpret_cast<uint16_t*>(s->y);
     s->sact = (uint16_t*)take((size_t)T * d.shared_inter * 2);
     s->sy = (float*)take((size_t)T * d.hidden * 4);
     s->arec = (uint4*)take((size_t)d.experts * 16);
@@ -1123,6 +1350,21 @@ int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, S
 
 namespace k3x_hip {
 
+int permute_router(k3x_hip_bank* bank) {
+    const auto& d = bank->desc;
+    if (!bank->router_wp) return K3X_OK;
+    const size_t n = router_wp_floats(d.experts);
+    hipLaunchKernelGGL(permute_router_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       bank->ctx->stream, bank->router_w, d.experts, d.hidden, bank->router_wp);
+    return launched(bank->ctx, 1);
+}
+
+bool router_mfma_eligible(uint32_t hidden) { return hidden <= kRouterMaxHidden; }
+
+size_t router_wp_floats(uint32_t experts) {
+    return (size_t)(experts + 15) / 16 * kRouterRes * kRouterTileRes;
+}
+
 int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
                    uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32) {
     const int mark = begin_stage(ctx, K3X_STAGE_COMBINE);
@@ -1154,9 +1396,26 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
     const int mark = k3x_hip::begin_stage(ctx, K3X_STAGE_ROUTE);
+    const bool mfma_router = bank->router_wp && T >= kRouterMfmaMinTokens;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, bank->gamma,
-                       d.hidden, p->rms_epsilon, s.xn, ctx->status);
-    if (T <= 4) {
+                       d.hidden, p->rms_epsilon, s.xn, mfma_router ? s.xp : nullptr,
+                       ctx->status);
+    if (mfma_router) {
+        const dim3 grid((d.experts + 15) / 16, (T + 15) / 16);
+        const uint32_t nm = (d.hidden + 4 * kRouterRes - 1) / (4 * kRouterRes);
+        switch (nm) {
+#define K3X_ROUTER_NM(n)                                                                        \
+    case n:                                                                                     \
+        hipLaunchKernelGGL((router_mfma_kernel<n, kRouterWaves>), grid, dim3(64 * kRouterWaves), \
+                           0, ctx->stream, bank->router_wp, s.xp, d.experts, T, s.logits,       \
+                           ctx->status);                                                        \
+        break;
+            K3X_ROUTER_NM(1) K3X_ROUTER_NM(2) K3X_ROUTER_NM(3) K3X_ROUTER_NM(4)
+            K3X_ROUTER_NM(5) K3X_ROUTER_NM(6) K3X_ROUTER_NM(7) K3X_ROUTER_NM(8)
+#undef K3X_ROUTER_NM
+            default: return K3X_ERR_INVALID_EXTENT;
+        }
+    } else if (T <= 4) {
         hipLaunchKernelGGL((router_kernel<1, 4>), dim3(d.experts, 1), dim3(256), 0, ctx->stream,
                            bank->router_w, s.xn, d.experts, d.hidden, T, s.logits, ctx->status);
     } else {

@@ -279,6 +279,12 @@ class Bank:
         return self.lib.k3x_hip_bank_upload_router(self.handle, host_ptr(w), host_ptr(b),
                                                    host_ptr(g))
 
+    def set_router_device(self, weight, bias, gamma) -> int:
+        """Router weights [E][H], bias [E], gamma [H] from fp32 device tensors
+        (queued on the context stream)."""
+        return self.lib.k3x_hip_bank_set_router_device(self.handle, ptr(weight), ptr(bias),
+                                                       ptr(gamma))
+
     def find(self, tensor_id: int):
         e, m = C.c_uint32(0), C.c_uint32(0)
         st = self.lib.k3x_hip_bank_find(self.handle, tensor_id, C.byref(e), C.byref(m))

@@ -332,6 +332,34 @@ def make_bank(k3x_amd, ctx, cfg, layer=None):
     return bank
 
 
+# Router on the fp64 matrix cores (T >= 256, H <= 8192) and its fallback:
+# ragged expert and token tiles, hidden sizes with padded terms, and every
+# path that writes the router weights (synthetic fill, host upload, device
+# copy) refreshes the residue-major copy the matrix-core router reads.
+@pytest.mark.parametrize("T,H,E", [(256, 1152, 20), (300, 7168, 40), (272, 8192, 16),
+                                   (257, 128, 33), (260, 8320, 18)],
+                         ids=["h1152", "h7168", "h8192", "h128", "h8320_fallback"])
+def test_router_shapes(hip, oracle, T, H, E):
+    from synth import Config, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = Config(f"router_{T}_{H}_{E}", T, H, 128, E, 4, 0, 119, 123, routed_scale=2.5)
+    say(f"router shape T={T} H={H} E={E}")
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    x = layer.x_bits()
+    check_routing(oracle, layer, run_layer(k3x_amd, ctx, cfg, bank, x, per_pair=False), x)
+    rng = np.random.default_rng(T + H + E)
+    layer.router = (rng.standard_normal((E, H)) * 0.03).astype(np.float32)
+    assert bank.upload_router(layer.router, layer.bias, layer.gamma) == 0
+    check_routing(oracle, layer, run_layer(k3x_amd, ctx, cfg, bank, x, per_pair=False), x)
+    layer.router = (rng.standard_normal((E, H)) * 0.01).astype(np.float32)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to("cuda:0")
+    w, b, g = dev(layer.router), dev(layer.bias), dev(layer.gamma)
+    assert bank.set_router_device(w, b, g) == 0
+    check_routing(oracle, layer, run_layer(k3x_amd, ctx, cfg, bank, x, per_pair=False), x)
+    bank.close()
+
+
 @pytest.fixture(scope="module")
 def c3(hip, oracle):
     from synth import CONFIGS, SynthLayer
