@@ -187,10 +187,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     }
 #define WIDE_ORDER() asm volatile("" ::: "memory")
 
-    // MT = row tiles multiplied: all eight, or the first four when the chunk
-    // has at most 64 rows (a workgroup-uniform choice made once, so the step
-    // loop has no branches; tiles past the chunk's rows hold copies of its
-    // last row and are not stored).
+    // MT = row tiles multiplied: the chunk's rows rounded up to 64, 96 or
+    // 128 rows, see the dispatch at the end (a workgroup-uniform choice made
+    // once, so the step loop has no branches; tiles past the chunk's rows
+    // hold copies of its last row and are not stored).
     auto run = [&](auto mt_count) {
         constexpr int MT = decltype(mt_count)::value;
         f32x4 acc[MT][NT][S];
@@ -267,34 +267,76 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
             }
         }
         // The repeated last-tile requests of the final steps land before the
-        // workgroup's LDS can be handed on.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // ring is reused for the output tile below.
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 
+        // Epilogue through LDS: the waves write their accumulators (GLU ->
+        // bf16 for gate/up, fp32 for down) into the ring as row-major rows of
+        // this workgroup's kCols output columns, then every lane stores 16
+        // contiguous bytes of a row, so a wave writes whole 128-byte lines
+        // where the accumulator layout (4 rows x 16 columns per store) wrote
+        // 32- or 64-byte pieces of four rows.  Row pitch = row bytes + 16:
+        // the four row groups of a write land 16 banks apart.  Down tiles
+        // larger than the ring go in passes of RP rows.
+        constexpr uint32_t kCols = kWaves * NT * 16;
+        constexpr uint32_t kEs = GATEUP ? 2 : 4;                    // output element bytes
+        constexpr uint32_t kChunks = kCols * kEs / 16;              // 16-byte chunks per row
+        constexpr uint32_t kPitch = kCols * kEs + 16;               // staged row bytes
+        constexpr uint32_t kRing = sizeof(s_a4);
+        constexpr uint32_t RP0 = kRing / kPitch / 16 * 16;
+        constexpr uint32_t RP = RP0 < MT * 16 ? RP0 : MT * 16;     // rows per pass
+        static_assert(RP >= 16, "one row tile per pass at least");
+        uint8_t* stage = reinterpret_cast<uint8_t*>(s_a4);
         if constexpr (!GATEUP) {
             if (tid < kWideRows) s_yrow[tid] = yv;
-            __syncthreads();
         }
+        const uint32_t col0 = jb * kCols;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+        for (uint32_t p0 = 0; p0 < MT * 16; p0 += RP) {
+            if (p0) __syncthreads();  // the previous pass has been copied out
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int mt = 0; mt < MT; ++mt) {
+                if (mt * 16 < (int)p0 || mt * 16 >= (int)(p0 + RP)) continue;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t row = 16 * mt + 4 * g + i;
-                    if (row >= rows) continue;
-                    const uint32_t col = (rb0 + nt) * 16 + n;
-                    const uint32_t r = off + m0 + row;
-                    if constexpr (GATEUP) {
-                        const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
-                        a.act[(size_t)r * a.act_stride + col] = f32_to_bf16(v);
-                    } else {
-                        a.y[(size_t)s_yrow[row] * a.y_stride + col] = acc[mt][nt][0][i];
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t row = 16 * mt + 4 * g + i - p0;
+                        const uint32_t col = (wave * NT + nt) * 16 + n;
+                        if constexpr (GATEUP) {
+                            const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
+                            *reinterpret_cast<uint16_t*>(stage + row * kPitch + col * 2) =
+                                f32_to_bf16(v);
+                        } else {
+                            *reinterpret_cast<float*>(stage + row * kPitch + col * 4) =
+                                acc[mt][nt][0][i];
+                        }
                     }
+            }
+            __syncthreads();
+            const uint32_t prow = min(rows - min(rows, p0), RP);  // valid rows of this pass
+            for (uint32_t c = tid; c < prow * kChunks; c += kThreads) {
+                const uint32_t row = c / kChunks, ch = c % kChunks;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * kPitch + ch * 16);
+                if constexpr (GATEUP) {
+                    uint16_t* dst = a.act + (size_t)(off + m0 + p0 + row) * a.act_stride + col0;
+                    *reinterpret_cast<u32x4*>(dst + ch * 8) = v;
+                } else {
+                    float* dst = a.y + (size_t)s_yrow[p0 + row] * a.y_stride + col0;
+                    *reinterpret_cast<u32x4*>(dst + ch * 4) = v;
                 }
+            }
         }
     };
-    if (rows > kWideRows / 2)
+    // Four, six or eight row tiles; the routed gate/up kernel (the most
+    // registers) keeps to four or eight: a third variant there makes the
+    // register allocator spill inside the step loop.  (Two tiles as a fourth
+    // variant does the same in the others.)
+    constexpr bool kSix = !(FP4 && GATEUP);
+    if (rows > kWideRows * 3 / 4 || (!kSix && rows > kWideRows / 2))
         run(std::integral_constant<int, kMTiles>{});
+    else if (kSix && rows > kWideRows / 2)
+        run(std::integral_constant<int, kSix ? kMTiles * 3 / 4 : kMTiles>{});
     else
         run(std::integral_constant<int, kMTiles / 2>{});
 }
@@ -325,6 +367,10 @@ uint32_t wide_rb_per_block(WideKind kind) {
 int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items) {
     const uint32_t per = wide_rb_per_block(kind);
     if (a.nrb % per || a.kt % kWideStages || !a.kt || !max_items) return K3X_ERR_INVALID_EXTENT;
+    // The epilogue stores 16-byte row pieces.
+    const bool gu = kind == kWideRoutedGateUp || kind == kWideSharedGateUp;
+    if (gu ? ((uintptr_t)a.act % 16 || a.act_stride % 8) : ((uintptr_t)a.y % 16 || a.y_stride % 4))
+        return K3X_ERR_INVALID_EXTENT;
     const dim3 grid(max_items * (a.nrb / per));
     switch (kind) {
         case kWideRoutedGateUp:

@@ -107,9 +107,14 @@ struct GluParams {
     float linear_beta;
 };
 
-// SiTU-GLU (runtime/src/ops.cpp:20-30) or SwiGLU (silu(g) * u).
+// SiTU-GLU (runtime/src/ops.cpp:20-30) or SwiGLU (silu(g) * u).  The gate
+// sigmoid 1 / (1 + exp(-g)) runs on the hardware exp2 and reciprocal (about
+// one ulp each, far inside the bf16 rounding that follows): it is evaluated
+// for every element of a GEMM epilogue, where the library expf and IEEE
+// divide made the epilogue a sizeable share of the kernel.  g -> -inf gives
+// exp2 = inf and a sigmoid of 0; NaN propagates.
 __device__ inline float glu(float g, float u, const GluParams& p) {
-    const float sig = 1.0f / (1.0f + expf(-g));
+    const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f));
     if (p.kind == 1) {
         const float bg = p.beta * tanhf(g / p.beta) * sig;
         const float bu = p.has_linear ? p.linear_beta * tanhf(u / p.linear_beta) : u;
