@@ -237,8 +237,10 @@ namespace k3x_hip {
 
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes) {
     if (bytes <= ctx->scratch_bytes) return K3X_OK;
-    // The old scratch may still be read by enqueued kernels.
-    if (hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    // The old scratch may still be read by enqueued kernels (on either stream).
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->side_stream) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;
@@ -348,6 +350,9 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
     ctx->device = device;
     int lds = 0, cus = 0;
     if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
         hipMemset(ctx->status, 0, 256) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
@@ -355,6 +360,9 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
         (void)hipGetLastError();
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+        if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+        if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+        if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
         if (ctx->status) (void)hipFree(ctx->status);
         delete ctx;
         return K3X_ERR_BACKEND_UNAVAILABLE;
@@ -371,6 +379,7 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     if (ctx->live_banks) return K3X_ERR_INVALID_STATE;  // destroy the banks first
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->status) (void)hipFree(ctx->status);
     for (const StageMark& m : ctx->pending) {
@@ -379,6 +388,9 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     }
     for (hipEvent_t e : ctx->free_events) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
+    if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+    if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
     delete ctx;
     return K3X_OK;
 }

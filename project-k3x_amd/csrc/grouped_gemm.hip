@@ -24,8 +24,9 @@
 //     requested at step k - 2, so it is in LDS and registers; each request
 //     has two steps of multiplies to arrive in.
 // The weights of an expert are read once per 128-row chunk.  The N blocks of
-// one expert are numbered to land on one XCD, so its activation rows are
-// fetched into that XCD's L2 once.
+// one item are numbered to land on one XCD, so its activation rows are
+// fetched into that XCD's L2 once; the grouping deals the items to the XCDs'
+// ranges by size, so the XCDs get equal work.
 // Epilogues: GLU -> bf16 act (gate/up), fp32 rows scattered to the pair's
 // (token, slot) row (routed down) or the token row (shared down).
 #include <hip/hip_runtime.h>
@@ -364,7 +365,9 @@ uint32_t wide_rb_per_block(WideKind kind) {
     }
 }
 
-int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items) {
+int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items,
+                     hipStream_t stream) {
+    if (!stream) stream = ctx->stream;
     const uint32_t per = wide_rb_per_block(kind);
     if (a.nrb % per || a.kt % kWideStages || !a.kt || !max_items) return K3X_ERR_INVALID_EXTENT;
     // The epilogue stores 16-byte row pieces.
@@ -375,19 +378,19 @@ int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uin
     switch (kind) {
         case kWideRoutedGateUp:
             hipLaunchKernelGGL((wide_gemm<true, true, kNtRoutedGateUp>), grid, dim3(kThreads), 0,
-                               ctx->stream, a);
+                               stream, a);
             break;
         case kWideRoutedDown:
             hipLaunchKernelGGL((wide_gemm<true, false, kNtRoutedDown>), grid, dim3(kThreads), 0,
-                               ctx->stream, a);
+                               stream, a);
             break;
         case kWideSharedGateUp:
             hipLaunchKernelGGL((wide_gemm<false, true, kNtSharedGateUp>), grid, dim3(kThreads), 0,
-                               ctx->stream, a);
+                               stream, a);
             break;
         default:
             hipLaunchKernelGGL((wide_gemm<false, false, kNtSharedDown>), grid, dim3(kThreads), 0,
-                               ctx->stream, a);
+                               stream, a);
             break;
     }
     ctx->kernel_launches += 1;

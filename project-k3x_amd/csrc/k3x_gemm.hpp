@@ -59,9 +59,10 @@ constexpr uint32_t kWideStages = 4;
 // nrb to be a multiple of it).
 uint32_t wide_rb_per_block(WideKind kind);
 
-// Enqueues one wide GEMM on the context stream: max_items row chunks (an
-// upper bound of *n_items for the routed kinds) x the output row blocks,
-// one workgroup each.
-int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items);
+// Enqueues one wide GEMM on `stream` (the context stream when null):
+// max_items row chunks (an upper bound of *n_items for the routed kinds) x
+// the output row blocks, one workgroup each.
+int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items,
+                     hipStream_t stream = nullptr);
 
 }  // namespace k3x_hip

@@ -21,6 +21,10 @@ struct k3x_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipStream_t own_stream = nullptr;
+    // Second stream for the shared expert's wide GEMMs (default priority),
+    // forked from and joined back into `stream` with these events.
+    hipStream_t side_stream = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     uint32_t* status = nullptr;  // device word, latched kernel errors
     size_t max_lds_per_block = 65536;
     uint32_t cu_count = 256;

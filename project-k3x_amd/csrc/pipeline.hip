@@ -564,8 +564,8 @@ __global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logi
 //   group_scan_kernel     one workgroup: per expert, the running row base of
 //                         every chunk, its count and first use; CSR offsets,
 //                         the active lists, and (witems non-null) the wide
-//                         GEMM's (expert << 16 | row chunk) work items in
-//                         ascending expert order;
+//                         GEMM's (expert << 16 | row chunk) work items,
+//                         dealt by size class over the XCDs' list segments;
 //   group_scatter_kernel  one workgroup per chunk: row offsets[e] +
 //                         base[chunk][e] + rank gets (token, slot).
 // ---------------------------------------------------------------------------
@@ -705,23 +705,67 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(
         const uint32_t row = (uint32_t)(pre & ((1ull << kScanItemShift) - 1));
         const uint32_t item = (uint32_t)((pre >> kScanItemShift) & ((1ull << 21) - 1));
         const uint32_t act = (uint32_t)(pre >> kScanActiveShift);
+        (void)item;
         offsets[e] = row;
         counts[e] = c;
         first_use[e] = s_fu[e];
         if (c) {
             active_asc[act] = e;
             s_alist[act] = e;
-            if (witems)
-                for (uint32_t q = 0; q * chunk_rows < c; ++q) witems[item + q] = (e << 16) | q;
         }
         pre += c | (uint64_t)((c + chunk_rows - 1) / chunk_rows) << kScanItemShift |
                (uint64_t)(c != 0) << kScanActiveShift;
     }
     const uint32_t na = (uint32_t)(total >> kScanActiveShift);
+    const uint32_t n_items = (uint32_t)((total >> kScanItemShift) & ((1ull << 21) - 1));
     if (tid == 0) {
         offsets[E] = (uint32_t)(total & ((1ull << kScanItemShift) - 1));
         *n_active = na;
-        if (witems) *n_witems = (uint32_t)((total >> kScanItemShift) & ((1ull << 21) - 1));
+        if (witems) *n_witems = n_items;
+    }
+    if (witems) {
+        // Wide GEMM work items, balanced over the XCDs.  Rank k orders the
+        // items by size class -- full chunks and partial chunks of > 3/4,
+        // then > 1/2, then <= 1/2 of chunk_rows (a chunk's time follows its
+        // row tiles) -- and by expert within a class.  Item k goes to list
+        // segment k % 8, position k / 8: the GEMM hands each XCD one
+        // contiguous eighth of the list, so every XCD gets the same mix.
+        auto cls = [&](uint32_t c) -> uint32_t {  // class of an expert's last chunk
+            const uint32_t last = c - (c - 1) / chunk_rows * chunk_rows;
+            return last * 4 > chunk_rows * 3 ? 0u : last * 2 > chunk_rows ? 1u : 2u;
+        };
+        auto counts3 = [&](uint32_t c) -> uint64_t {  // class counts, 24 | 16 | 16 bits
+            if (!c) return 0;
+            const uint32_t nq = (c + chunk_rows - 1) / chunk_rows, k = cls(c);
+            return (uint64_t)(nq - 1 + (k == 0)) | (uint64_t)(k == 1) << 24 |
+                   (uint64_t)(k == 2) << 40;
+        };
+        uint64_t mine3 = 0;
+        for (uint32_t i = 0; i < per; ++i)
+            if (e0 + i < E) mine3 += counts3(s_cnt[e0 + i]);
+        uint64_t total3;
+        uint64_t pre3 = block_exclusive_scan(mine3, red, &total3);
+        const uint32_t n0 = (uint32_t)(total3 & 0xffffffu), n1 = (uint32_t)((total3 >> 24) & 0xffffu);
+        const uint32_t q8 = n_items / 8, r8 = n_items % 8;
+        auto place = [&](uint32_t k) {  // list position of rank k
+            const uint32_t x = k % 8;
+            return x * q8 + min(x, r8) + k / 8;
+        };
+        for (uint32_t i = 0; i < per; ++i) {
+            const uint32_t e = e0 + i;
+            if (e >= E) break;
+            const uint32_t c = s_cnt[e];
+            if (c) {
+                const uint32_t nq = (c + chunk_rows - 1) / chunk_rows, k = cls(c);
+                const uint32_t p0 = (uint32_t)(pre3 & 0xffffffu);
+                for (uint32_t q = 0; q + 1 < nq; ++q) witems[place(p0 + q)] = (e << 16) | q;
+                const uint32_t kl = k == 0   ? p0 + nq - 1
+                                    : k == 1 ? n0 + (uint32_t)((pre3 >> 24) & 0xffffu)
+                                             : n0 + n1 + (uint32_t)(pre3 >> 40);
+                witems[place(kl)] = (e << 16) | (nq - 1);
+            }
+            pre3 += counts3(c);
+        }
     }
     __syncthreads();
     // First uses are distinct pair indices: ranks are a permutation.
@@ -1104,16 +1148,13 @@ bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
            (uint64_t)std::max(d.inter, d.shared_inter) * d.hidden * 4 < (1ull << 32);
 }
 
-int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
-             const Scratch& s, const uint16_t* xn, const GluParams& glu) {
-    using namespace k3x_hip;
+// Arguments of the routed gate/up launch; the other three derive from them.
+k3x_hip::WideGemmArgs wide_gate_up_args(k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
+                                        const k3x_hip_moe_params* p, const Scratch& s,
+                                        const uint16_t* xn, const GluParams& glu) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
-    // Routed: one workgroup column per (expert, 128-row chunk) item the
-    // grouping listed (up to wide_max_items); shared: one per chunk of T.
-    const uint32_t all_chunks = (T + kWideRows - 1) / kWideRows;
-    const uint32_t routed_chunks = wide_max_items(d, T, K);
-    WideGemmArgs g{};
+    k3x_hip::WideGemmArgs g{};
     g.items = s.witems;
     g.n_items = s.n_witems;
     g.status = ctx->status;
@@ -1136,27 +1177,69 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.gather = 1;
     g.act = s.act;
     g.act_stride = d.inter;
+    return g;
+}
+
+// The shared expert on the wide GEMM: gate/up + GLU -> sact, down -> sy, on
+// `stream` (stage marks only on the context stream).
+int run_shared_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                    const Scratch& s, const uint16_t* xn, const GluParams& glu,
+                    hipStream_t stream) {
+    using namespace k3x_hip;
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens;
+    const uint32_t all_chunks = (T + kWideRows - 1) / kWideRows;
+    const bool marks = stream == ctx->stream;
+    WideGemmArgs sg = wide_gate_up_args(ctx, bank, p, s, xn, glu);
+    sg.codes = bank->sh_gu;
+    sg.scales = nullptr;
+    sg.codes_per_expert = 0;
+    sg.kt = bank->sgate.kt;
+    sg.nrb = d.shared_inter / 16;
+    sg.gather = 0;
+    sg.items = nullptr;
+    sg.tokens = T;
+    sg.act = s.sact;
+    sg.act_stride = d.shared_inter;
+    int mark = marks ? begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP) : -1;
+    int st = launch_wide_gemm(ctx, kWideSharedGateUp, sg, all_chunks, stream);
+    end_stage(ctx, mark);
+    if (st) return st;
+    WideGemmArgs sd = sg;
+    sd.codes = bank->sh_dn;
+    sd.kt = bank->sdown.kt;
+    sd.nrb = d.hidden / 16;
+    sd.a = s.sact;
+    sd.a_stride = d.shared_inter;
+    sd.a_bytes = T * d.shared_inter * 2;
+    sd.act = nullptr;
+    sd.y = s.sy;
+    sd.y_stride = d.hidden;
+    sd.scatter = 0;
+    mark = marks ? begin_stage(ctx, K3X_STAGE_SHARED_DOWN) : -1;
+    st = launch_wide_gemm(ctx, kWideSharedDown, sd, all_chunks, stream);
+    end_stage(ctx, mark);
+    return st;
+}
+
+// Routed gate/up + GLU, then down; with shared_inline the shared expert's
+// GEMMs run on the context stream after each routed one.
+int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+             const Scratch& s, const uint16_t* xn, const GluParams& glu, bool shared_inline) {
+    using namespace k3x_hip;
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens, K = p->top_k;
+    // Routed: one workgroup column per (expert, 128-row chunk) item the
+    // grouping listed (up to wide_max_items).
+    const uint32_t routed_chunks = wide_max_items(d, T, K);
+    WideGemmArgs g = wide_gate_up_args(ctx, bank, p, s, xn, glu);
     int mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
     int st = launch_wide_gemm(ctx, kWideRoutedGateUp, g, routed_chunks);
     end_stage(ctx, mark);
     if (st) return st;
-    if (d.shared_inter) {
-        WideGemmArgs sg = g;
-        sg.codes = bank->sh_gu;
-        sg.scales = nullptr;
-        sg.codes_per_expert = 0;
-        sg.kt = bank->sgate.kt;
-        sg.nrb = d.shared_inter / 16;
-        sg.gather = 0;
-        sg.items = nullptr;
-        sg.tokens = T;
-        sg.act = s.sact;
-        sg.act_stride = d.shared_inter;
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP);
-        st = launch_wide_gemm(ctx, kWideSharedGateUp, sg, all_chunks);
-        end_stage(ctx, mark);
-        if (st) return st;
-    }
+    if (shared_inline && d.shared_inter &&
+        (st = run_shared_wide(ctx, bank, p, s, xn, glu, ctx->stream)))
+        return st;
     WideGemmArgs dn = g;
     dn.codes = bank->dn_codes;
     dn.scales = bank->dn_scales;
@@ -1176,24 +1259,6 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     mark = begin_stage(ctx, K3X_STAGE_DOWN);
     st = launch_wide_gemm(ctx, kWideRoutedDown, dn, routed_chunks);
     end_stage(ctx, mark);
-    if (st) return st;
-    if (d.shared_inter) {
-        WideGemmArgs sd = dn;
-        sd.codes = bank->sh_dn;
-        sd.scales = nullptr;
-        sd.codes_per_expert = 0;
-        sd.kt = bank->sdown.kt;
-        sd.a = s.sact;
-        sd.a_stride = d.shared_inter;
-        sd.a_bytes = T * d.shared_inter * 2;
-        sd.items = nullptr;
-        sd.tokens = T;
-        sd.y = s.sy;
-        sd.scatter = 0;
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN);
-        st = launch_wide_gemm(ctx, kWideSharedDown, sd, all_chunks);
-        end_stage(ctx, mark);
-    }
     return st;
 }
 
@@ -1204,6 +1269,40 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              uint16_t* out, float* out_f32) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
+    GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+    // Wide path with a shared expert: its GEMMs depend only on xn, so they
+    // go to the side stream now and run beside the grouping and the routed
+    // GEMMs (filling the small grouping launches and the routed GEMMs'
+    // tails); the context stream waits for them before the combine, and on
+    // every early return (they read and write this call's scratch).  With
+    // stage profiling on, everything stays on the context stream.
+    const bool wide_path = use_wide_gemm(d, T, K);
+    const bool side = wide_path && d.shared_inter && !ctx->profiling && ctx->side_stream;
+    struct Join {
+        k3x_hip_ctx* ctx;
+        bool armed = false;
+        int join() {
+            if (!armed) return K3X_OK;
+            armed = false;
+            return hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0) == hipSuccess
+                       ? K3X_OK
+                       : K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        ~Join() { (void)join(); }
+    } joiner{ctx};
+    if (side) {
+        if (hipEventRecord(ctx->fork_ev, ctx->stream) != hipSuccess ||
+            hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0) != hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        const int sst = run_shared_wide(ctx, bank, p, s, xn, glu, ctx->side_stream);
+        if (hipEventRecord(ctx->join_ev, ctx->side_stream) != hipSuccess) {
+            // Without the event, order the streams the blunt way.
+            (void)hipStreamSynchronize(ctx->side_stream);
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        joiner.armed = true;
+        if (sst) return sst;
+    }
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
                           s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu,
@@ -1212,9 +1311,9 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     const bool wide = T > 16;  // more than one 16-row MFMA tile per expert possible
-    GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
-    if (use_wide_gemm(d, T, K)) {
-        if ((st = run_wide(ctx, bank, p, s, xn, glu))) return st;
+    if (wide_path) {
+        if ((st = run_wide(ctx, bank, p, s, xn, glu, !side))) return st;
+        if ((st = joiner.join())) return st;
         return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
                                        d.hidden, T, out, out_f32);
     }
