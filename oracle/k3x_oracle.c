@@ -543,6 +543,157 @@ void k3xo_ordered_mix(const float* expert_out, const float* weights,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Official K3 MoE FFN (Stable LatentMoE): runtime/src/official_moe.cpp     */
+/* ------------------------------------------------------------------------ */
+
+/* bf16 GEMV, double accumulation in column order, bf16-rounded output.
+ * runtime/src/official_moe.cpp:39-59. */
+void k3xo_bf16_matvec_rounded(const float* x, const uint16_t* weight,
+                              size_t rows, size_t cols, float* out) {
+    k3xo_bf16_matvec(x, weight, rows, cols, out);
+    for (size_t r = 0; r < rows; ++r) out[r] = k3xo_round_bf16(out[r]);
+}
+
+/* RMSNorm with a bf16 weight and bf16-rounded output, sequential double
+ * sum of squares.  runtime/src/official_moe.cpp:61-80. */
+void k3xo_official_norm(const float* in, const uint16_t* weight, size_t n,
+                        float epsilon, float* out) {
+    double squares = 0.0;
+    for (size_t i = 0; i < n; ++i) squares += (double)in[i] * in[i];
+    const float inverse = 1.0f / sqrtf((float)(squares / (double)n) + epsilon);
+    for (size_t i = 0; i < n; ++i)
+        out[i] = k3xo_round_bf16(in[i] * inverse * k3xo_bf16_to_f32(weight[i]));
+}
+
+/* Two-source attention-residual mix and post-norm feeding the router:
+ * sources (block residual, prefix sum) rounded to bf16, one softmax score
+ * each (normalised source . residual_norm . residual_proj, double), the
+ * bf16-rounded mix, then the post-norm.  runtime/src/official_moe.cpp:156-209. */
+int k3xo_official_prepare(const float* prefix, const float* block_residual,
+                          size_t width, const uint16_t* residual_norm,
+                          const uint16_t* residual_proj,
+                          const uint16_t* post_norm, float epsilon,
+                          float* hidden) {
+    if (!width || !(epsilon > 0.0f)) return K3XO_INVALID_EXTENT;
+    float* v0 = (float*)malloc(width * sizeof(float));
+    float* v1 = (float*)malloc(width * sizeof(float));
+    float* mix = (float*)malloc(width * sizeof(float));
+    int status = K3XO_INVALID_EXTENT;
+    if (!v0 || !v1 || !mix) goto done;
+    for (size_t i = 0; i < width; ++i) {
+        v0[i] = k3xo_round_bf16(block_residual[i]);
+        v1[i] = k3xo_round_bf16(prefix[i]);
+    }
+    float score[2];
+    for (int row = 0; row < 2; ++row) {
+        const float* v = row ? v1 : v0;
+        double squares = 0.0;
+        for (size_t i = 0; i < width; ++i) squares += (double)v[i] * v[i];
+        const float inverse =
+            1.0f / sqrtf((float)(squares / (double)width) + epsilon);
+        double sc = 0.0;
+        for (size_t i = 0; i < width; ++i)
+            sc += (double)(v[i] * inverse) * (double)k3xo_bf16_to_f32(residual_norm[i]) *
+                  (double)k3xo_bf16_to_f32(residual_proj[i]);
+        score[row] = (float)sc;
+    }
+    const float maximum = score[0] > score[1] ? score[0] : score[1];
+    float p0 = expf(score[0] - maximum), p1 = expf(score[1] - maximum);
+    const float denominator = p0 + p1;
+    p0 /= denominator;
+    p1 /= denominator;
+    for (size_t i = 0; i < width; ++i) mix[i] = k3xo_round_bf16(p0 * v0[i] + p1 * v1[i]);
+    k3xo_official_norm(mix, post_norm, width, epsilon, hidden);
+    status = K3XO_OK;
+done:
+    free(v0);
+    free(v1);
+    free(mix);
+    return status;
+}
+
+/* Shared FFN with bf16-rounded gate, up and down outputs.
+ * runtime/src/official_moe.cpp:105-117. */
+void k3xo_official_shared(const float* x, size_t hidden, size_t inter,
+                          const uint16_t* gate, const uint16_t* up,
+                          const uint16_t* down, int glu, float beta,
+                          int has_linear, float linear_beta, float* out) {
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    float* a = (float*)malloc(inter * sizeof(float));
+    if (g && u && a) {
+        k3xo_bf16_matvec_rounded(x, gate, inter, hidden, g);
+        k3xo_bf16_matvec_rounded(x, up, inter, hidden, u);
+        k3xo_glu(a, g, u, inter, glu, beta, has_linear, linear_beta);
+        k3xo_bf16_matvec_rounded(a, down, hidden, inter, out);
+    }
+    free(g);
+    free(u);
+    free(a);
+}
+
+/* One token of the official FFN around experts of hidden `latent`:
+ * latent = bf16(routed_down . hidden); expert outputs bf16-rounded; mixed =
+ * bf16(sum over slots in route order of c * y); routed = bf16(routed_up .
+ * norm(mixed)); out = bf16(bf16(prefix) + bf16(routed + shared)).
+ * runtime/src/official_moe.cpp:271-344 (official_moe_cpu) with :82-103
+ * (expert_ffn). */
+int k3xo_official_ffn(const float* hidden, const float* prefix, size_t width,
+                      size_t latent, size_t inter, size_t shared_inter,
+                      const uint16_t* routed_down, const uint16_t* routed_norm,
+                      const uint16_t* routed_up, const uint16_t* shared_gate,
+                      const uint16_t* shared_up, const uint16_t* shared_down,
+                      const uint8_t* const* experts, const float* contributions,
+                      size_t top_k, float epsilon, int glu, float beta,
+                      int has_linear, float linear_beta, float* latent_out,
+                      float* expert_out, float* mixed_out, float* routed_out,
+                      float* shared_out, float* out) {
+    float* lat = (float*)malloc(latent * sizeof(float));
+    float* y = (float*)malloc(top_k * latent * sizeof(float));
+    float* mixed = (float*)malloc(latent * sizeof(float));
+    float* normed = (float*)malloc(latent * sizeof(float));
+    float* routed = (float*)malloc(width * sizeof(float));
+    float* shared = (float*)calloc(width, sizeof(float));
+    int status = K3XO_INVALID_MXFP4;
+    if (!lat || !y || !mixed || !normed || !routed || !shared) goto done;
+    k3xo_bf16_matvec_rounded(hidden, routed_down, latent, width, lat);
+    if (shared_inter)
+        k3xo_official_shared(hidden, width, shared_inter, shared_gate, shared_up,
+                             shared_down, glu, beta, has_linear, linear_beta, shared);
+    for (size_t slot = 0; slot < top_k; ++slot) {
+        const uint8_t* const* e = experts + 6 * slot;
+        status = k3xo_expert_ffn(lat, latent, inter, e[0], e[1], e[2], e[3], e[4],
+                                 e[5], glu, beta, has_linear, linear_beta, 0, NULL,
+                                 y + slot * latent);
+        if (status) goto done;
+        for (size_t i = 0; i < latent; ++i)
+            y[slot * latent + i] = k3xo_round_bf16(y[slot * latent + i]);
+    }
+    k3xo_ordered_mix(y, contributions, top_k, latent, mixed);
+    for (size_t i = 0; i < latent; ++i) mixed[i] = k3xo_round_bf16(mixed[i]);
+    k3xo_official_norm(mixed, routed_norm, latent, epsilon, normed);
+    k3xo_bf16_matvec_rounded(normed, routed_up, width, latent, routed);
+    for (size_t i = 0; i < width; ++i) {
+        const float combined = k3xo_round_bf16(routed[i] + shared[i]);
+        out[i] = k3xo_round_bf16(k3xo_round_bf16(prefix[i]) + combined);
+    }
+    if (latent_out) memcpy(latent_out, lat, latent * sizeof(float));
+    if (expert_out) memcpy(expert_out, y, top_k * latent * sizeof(float));
+    if (mixed_out) memcpy(mixed_out, mixed, latent * sizeof(float));
+    if (routed_out) memcpy(routed_out, routed, width * sizeof(float));
+    if (shared_out) memcpy(shared_out, shared, width * sizeof(float));
+    status = K3XO_OK;
+done:
+    free(lat);
+    free(y);
+    free(mixed);
+    free(normed);
+    free(routed);
+    free(shared);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Portable synthetic inputs (no reference counterpart)                     */
 /* ------------------------------------------------------------------------ */
 

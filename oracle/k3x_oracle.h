@@ -111,6 +111,34 @@ void k3xo_shared_ffn(const float* x, size_t hidden, size_t inter,
 void k3xo_ordered_mix(const float* expert_out, const float* weights,
                       size_t top_k, size_t width, float* mixed);
 
+/* ---- official K3 MoE FFN (Stable LatentMoE) -----------------------------*/
+void k3xo_bf16_matvec_rounded(const float* x, const uint16_t* weight,
+                              size_t rows, size_t cols, float* out);
+void k3xo_official_norm(const float* in, const uint16_t* weight, size_t n,
+                        float epsilon, float* out);
+int k3xo_official_prepare(const float* prefix, const float* block_residual,
+                          size_t width, const uint16_t* residual_norm,
+                          const uint16_t* residual_proj,
+                          const uint16_t* post_norm, float epsilon,
+                          float* hidden);
+void k3xo_official_shared(const float* x, size_t hidden, size_t inter,
+                          const uint16_t* gate, const uint16_t* up,
+                          const uint16_t* down, int glu, float beta,
+                          int has_linear, float linear_beta, float* out);
+/* experts: per routed slot, six pointers (gate packed, gate scales, up
+ * packed, up scales, down packed, down scales) of an expert of hidden L.
+ * Intermediate outputs may be NULL. */
+int k3xo_official_ffn(const float* hidden, const float* prefix, size_t width,
+                      size_t latent, size_t inter, size_t shared_inter,
+                      const uint16_t* routed_down, const uint16_t* routed_norm,
+                      const uint16_t* routed_up, const uint16_t* shared_gate,
+                      const uint16_t* shared_up, const uint16_t* shared_down,
+                      const uint8_t* const* experts, const float* contributions,
+                      size_t top_k, float epsilon, int glu, float beta,
+                      int has_linear, float linear_beta, float* latent_out,
+                      float* expert_out, float* mixed_out, float* routed_out,
+                      float* shared_out, float* out);
+
 /* ---- portable synthetic inputs (no reference counterpart) ---------------*/
 uint64_t k3xo_mix64(uint64_t z);
 uint64_t k3xo_stream_key(uint64_t seed, uint64_t stream);

@@ -92,6 +92,15 @@ class Oracle:
         L.k3xo_shared_ffn.argtypes = [_f32p, _sz, _sz, _u16p, _u16p, _u16p, C.c_int,
                                       C.c_float, C.c_int, C.c_float, C.c_int, _f32p]
         L.k3xo_ordered_mix.argtypes = [_f32p, _f32p, _sz, _sz, _f32p]
+        L.k3xo_bf16_matvec_rounded.argtypes = [_f32p, _u16p, _sz, _sz, _f32p]
+        L.k3xo_official_norm.argtypes = [_f32p, _u16p, _sz, C.c_float, _f32p]
+        L.k3xo_official_prepare.argtypes = [_f32p, _f32p, _sz, _u16p, _u16p, _u16p, C.c_float,
+                                            _f32p]
+        L.k3xo_official_shared.argtypes = [_f32p, _sz, _sz, _u16p, _u16p, _u16p, C.c_int,
+                                           C.c_float, C.c_int, C.c_float, _f32p]
+        L.k3xo_official_ffn.argtypes = ([_f32p, _f32p, _sz, _sz, _sz, _sz] + [_u16p] * 6 +
+                                        [C.POINTER(_u8p), _f32p, _sz, C.c_float, C.c_int,
+                                         C.c_float, C.c_int, C.c_float] + [_f32p] * 6)
         L.k3xo_mix64.restype = C.c_uint64
         L.k3xo_mix64.argtypes = [C.c_uint64]
         L.k3xo_stream_key.restype = C.c_uint64
@@ -256,6 +265,76 @@ class Oracle:
         self.lib.k3xo_ordered_mix(_p(y, _f32p), _p(w, _f32p), K, width, _p(out, _f32p))
         return out
 
+    # -- official K3 MoE FFN (official_moe.cpp:39-344) -----------------------
+    def bf16_matvec_rounded(self, x, w_bits):
+        x = f32(x)
+        w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+        rows, cols = w.shape
+        out = np.zeros(rows, np.float32)
+        self.lib.k3xo_bf16_matvec_rounded(_p(x, _f32p), _p(w, _u16p), rows, cols,
+                                          _p(out, _f32p))
+        return out
+
+    def official_norm(self, x, w_bits, eps):
+        x = f32(x)
+        w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+        out = np.zeros(x.size, np.float32)
+        self.lib.k3xo_official_norm(_p(x, _f32p), _p(w, _u16p), x.size, eps, _p(out, _f32p))
+        return out
+
+    def official_prepare(self, prefix, residual, residual_norm, residual_proj, post_norm, eps):
+        prefix, residual = f32(prefix), f32(residual)
+        ws = [np.ascontiguousarray(a, dtype=np.uint16) for a in
+              (residual_norm, residual_proj, post_norm)]
+        out = np.zeros(prefix.size, np.float32)
+        st = self.lib.k3xo_official_prepare(_p(prefix, _f32p), _p(residual, _f32p), prefix.size,
+                                            *[_p(a, _u16p) for a in ws], eps, _p(out, _f32p))
+        return st, out
+
+    def official_shared(self, x, gate, up, down, glu=GLU_SITU, beta=4.0, linear=25.0):
+        x = f32(x)
+        gate, up, down = (np.ascontiguousarray(a, dtype=np.uint16) for a in (gate, up, down))
+        inter, hidden = gate.shape
+        out = np.zeros(hidden, np.float32)
+        self.lib.k3xo_official_shared(_p(x, _f32p), hidden, inter, _p(gate, _u16p),
+                                      _p(up, _u16p), _p(down, _u16p), glu, beta,
+                                      int(linear is not None), linear or 0.0, _p(out, _f32p))
+        return out
+
+    def official_ffn(self, hidden, prefix, weights, experts, contributions, eps,
+                     glu=GLU_SITU, beta=4.0, linear=25.0):
+        """One token.  weights: dict of bf16-word arrays routed_down [L][H],
+        routed_norm [L], routed_up [H][L], shared_gate/up [Is][H] and
+        shared_down [H][Is] (Is may be 0); experts: the routed experts (dicts of
+        the six MXFP4 arrays, hidden L) in slot order.  Returns status and a
+        dict of latent, expert_out, mixed, routed, shared, out."""
+        hidden, prefix = f32(hidden), f32(prefix)
+        w = {k: np.ascontiguousarray(v, dtype=np.uint16) for k, v in weights.items()}
+        L, H = w["routed_down"].shape
+        Is = w["shared_gate"].shape[0] if "shared_gate" in w else 0
+        if not Is:
+            for k in ("shared_gate", "shared_up", "shared_down"):
+                w[k] = np.zeros(1, np.uint16)
+        keep = [np.ascontiguousarray(e[k], dtype=np.uint8) for e in experts for k in
+                ("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+                 "down_scales")]
+        I = experts[0]["gate_packed"].size * 2 // L
+        ptrs = (_u8p * len(keep))(*[_p(a, _u8p) for a in keep])
+        c = f32(contributions)
+        K = c.size
+        out = {k: np.zeros(n, np.float32) for k, n in
+               (("latent", L), ("expert_out", K * L), ("mixed", L), ("routed", H),
+                ("shared", H), ("out", H))}
+        st = self.lib.k3xo_official_ffn(
+            _p(hidden, _f32p), _p(prefix, _f32p), H, L, I, Is,
+            *[_p(w[k], _u16p) for k in ("routed_down", "routed_norm", "routed_up",
+                                         "shared_gate", "shared_up", "shared_down")],
+            ptrs, _p(c, _f32p), K, eps, glu, beta, int(linear is not None), linear or 0.0,
+            *[_p(out[k], _f32p) for k in ("latent", "expert_out", "mixed", "routed",
+                                           "shared", "out")])
+        out["expert_out"] = out["expert_out"].reshape(K, L)
+        return st, out
+
     # -- synthetic inputs -----------------------------------------------------
     def stream_key(self, seed: int, stream: int) -> int:
         return self.lib.k3xo_stream_key(seed, stream)
@@ -316,6 +395,9 @@ class RefLib:
                                           C.c_float, _f32p]
         L.k3xr_route_tokens.argtypes = [_f32p, _sz, _f32p, C.c_float, _f32p, _f32p, _sz, _sz,
                                         _sz, C.c_float, C.c_int, _u32p, _f32p]
+        L.k3xr_official_moe.argtypes = ([_f32p, _f32p] + [_sz] * 6 + [_u16p] * 4 + [_f32p] +
+                                        [_u16p] * 6 + [EB, C.c_float, C.c_float, C.c_int,
+                                                       C.c_float, _f32p, _u32p] + [_f32p] * 7)
         L.k3xr_moe_layer_token.argtypes = [_f32p, _f32p, C.c_float, _f32p, _f32p, _sz, _sz, _sz,
                                            _sz, C.c_float, EB, _f32p, _f32p, _f32p, _sz,
                                            C.c_float, C.c_int, C.c_float, _u32p, _f32p]
@@ -450,6 +532,45 @@ class RefLib:
                                            _p(ids, _u32p), _p(out, _f32p))
         del keep
         return st, ids, out
+
+
+    def official_moe(self, prefix, residual, weights, experts, top_k, eps, beta=4.0,
+                     linear=25.0):
+        """One token through the reference's prepare, route and official_moe_cpu
+        (official_moe.cpp:156-344).  weights: bf16-word arrays residual_norm [H],
+        residual_proj [H], post_norm [H], router [E][H], routed_down [L][H],
+        routed_norm [L], routed_up [H][L], shared_gate/up [Is][H],
+        shared_down [H][Is]; correction fp32 [E]; experts: E expert dicts."""
+        prefix, residual = f32(prefix), f32(residual)
+        w = {k: np.ascontiguousarray(v, dtype=np.uint16) for k, v in weights.items()
+             if k != "correction"}
+        corr = f32(weights["correction"])
+        E, H = w["router"].shape
+        L = w["routed_down"].shape[0]
+        Is = w["shared_gate"].shape[0]
+        I = experts[0]["gate_packed"].size * 2 // L
+        structs, keep = zip(*[expert_struct(e) for e in experts])
+        arr = (_ExpertBytes * E)(*structs)
+        ids = np.zeros(top_k, np.uint32)
+        res = {k: np.zeros(n, np.float32) for k, n in
+               (("hidden", H), ("contributions", top_k), ("latent", L),
+                ("expert_out", top_k * L), ("mixed", L), ("routed", H), ("shared", H),
+                ("out", H))}
+        st = self.lib.k3xr_official_moe(
+            _p(prefix, _f32p), _p(residual, _f32p), H, L, I, Is, E, top_k,
+            *[_p(w[k], _u16p) for k in ("residual_norm", "residual_proj", "post_norm",
+                                         "router")],
+            _p(corr, _f32p),
+            *[_p(w[k], _u16p) for k in ("routed_down", "routed_norm", "routed_up",
+                                         "shared_gate", "shared_up", "shared_down")],
+            arr, eps, beta, int(linear is not None), linear or 0.0,
+            _p(res["hidden"], _f32p), _p(ids, _u32p),
+            *[_p(res[k], _f32p) for k in ("contributions", "latent", "expert_out", "mixed",
+                                           "routed", "shared", "out")])
+        del keep
+        res["ids"] = ids
+        res["expert_out"] = res["expert_out"].reshape(top_k, L)
+        return st, res
 
 
 @dataclass

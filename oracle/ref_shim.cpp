@@ -314,4 +314,67 @@ int k3xr_moe_layer_token(const float* x, const float* gamma, float epsilon,
     return 0;
 }
 
+// Official K3 MoE FFN for one token (runtime/src/official_moe.cpp:271-344):
+// the reference prepares the hidden from (prefix, block residual), routes it
+// through the bf16 router with the correction, and runs the latent experts.
+// Widths: H hidden, L latent (experts' hidden), I expert inter, Is shared
+// inter, E experts (experts[] holds E ExpertBytes of hidden L).  Outputs:
+// hidden [H], ids/contributions [K], latent [L], expert_out [K][L],
+// mixed [L], routed [H], shared [H], out [H].
+int k3xr_official_moe(const float* prefix, const float* block_residual, std::size_t hidden,
+                      std::size_t latent, std::size_t inter, std::size_t shared_inter,
+                      std::size_t experts_n, std::size_t top_k,
+                      const std::uint16_t* residual_norm, const std::uint16_t* residual_proj,
+                      const std::uint16_t* post_norm, const std::uint16_t* router,
+                      const float* correction, const std::uint16_t* routed_down,
+                      const std::uint16_t* routed_norm, const std::uint16_t* routed_up,
+                      const std::uint16_t* shared_gate, const std::uint16_t* shared_up,
+                      const std::uint16_t* shared_down, const ExpertBytes* experts,
+                      float epsilon, float beta, int has_linear, float linear_beta,
+                      float* hidden_out, std::uint32_t* ids, float* contributions,
+                      float* latent_out, float* expert_out, float* mixed_out,
+                      float* routed_out, float* shared_out, float* out) {
+    std::vector<k3x::OfficialExpertView> views;
+    views.reserve(experts_n);
+    for (std::size_t e = 0; e < experts_n; ++e)
+        views.push_back({static_cast<std::uint32_t>(e),
+                         expert_view(experts[e], latent, inter, 100 * (e + 1))});
+    const k3x::OfficialMoeWeights weights{
+        {{residual_norm, hidden}},
+        {{residual_proj, hidden}, 1, hidden},
+        {{post_norm, hidden}},
+        {{router, experts_n * hidden}, experts_n, hidden},
+        {correction, experts_n},
+        {{routed_down, latent * hidden}, latent, hidden},
+        {{routed_norm, latent}},
+        {{routed_up, hidden * latent}, hidden, latent},
+        {{{shared_gate, shared_inter * hidden}, shared_inter, hidden},
+         {{shared_up, shared_inter * hidden}, shared_inter, hidden},
+         {{shared_down, hidden * shared_inter}, hidden, shared_inter}},
+        views,
+    };
+    k3x::OfficialMoeInput input{{prefix, prefix + hidden},
+                                {block_residual, block_residual + hidden}};
+    auto h = k3x::prepare_official_moe_input(input, weights, epsilon);
+    if (!h) return static_cast<int>(h.error());
+    auto route = k3x::route_official_moe(h.value(), weights.router, weights.correction, top_k);
+    if (!route) return static_cast<int>(route.error());
+    auto result = k3x::official_moe_cpu(input, weights, route.value(), epsilon, beta,
+                                        linear_of(has_linear, linear_beta));
+    if (!result) return static_cast<int>(result.error());
+    const auto& r = result.value();
+    std::memcpy(hidden_out, r.hidden.data(), hidden * sizeof(float));
+    for (std::size_t k = 0; k < top_k; ++k) {
+        ids[k] = route.value().expert_ids[k];
+        contributions[k] = route.value().contributions[k];
+        std::memcpy(expert_out + k * latent, r.expert_outputs[k].data(), latent * sizeof(float));
+    }
+    std::memcpy(latent_out, r.latent.data(), latent * sizeof(float));
+    std::memcpy(mixed_out, r.mixed_latent.data(), latent * sizeof(float));
+    std::memcpy(routed_out, r.routed.data(), hidden * sizeof(float));
+    std::memcpy(shared_out, r.shared.data(), hidden * sizeof(float));
+    std::memcpy(out, r.output.data(), hidden * sizeof(float));
+    return 0;
+}
+
 }  // extern "C"
