@@ -106,6 +106,10 @@ enum k3x_flags {
     /* Use the general multi-launch path even where the decode path
      * (tokens <= 4) applies; both compute the same layer. */
     K3X_FLAG_GENERAL_PATH = 1u,
+    /* Round each expert output to bf16 before the slot-ordered mix, as the
+     * official layer does (runtime/src/official_moe.cpp:99-101, :318-326);
+     * runs the general path. */
+    K3X_FLAG_ROUND_EXPERT_OUT = 2u,
 };
 
 /* Optional device buffers that receive intermediates of k3x_hip_moe_forward;
@@ -304,6 +308,89 @@ int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
 int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids,
                               uint32_t tokens, uint32_t top_k,
                               uint32_t experts, const k3x_hip_moe_taps* taps);
+
+/* ---- official K3 MoE FFN (Stable LatentMoE) ------------------------------ */
+
+/* The official layer wraps a bank of experts that run at the latent width L
+ * (the bank's hidden): routed_down [L][H] bf16 -> experts -> slot-ordered
+ * mix -> routed_norm RMSNorm -> routed_up [H][L] bf16, plus a bf16 shared
+ * FFN at H (shared_inter Is, the reference's two shared experts side by
+ * side) and the prefix add (runtime/src/official_moe.cpp:271-344;
+ * OfficialMoeFfnView, runtime/include/k3x/backend.hpp:171-176). */
+typedef struct k3x_hip_official k3x_hip_official;
+
+typedef struct k3x_hip_official_desc {
+    uint32_t hidden;        /* H, multiple of 128 */
+    uint32_t shared_inter;  /* Is, 0 (none) or a multiple of 128 */
+} k3x_hip_official_desc;
+
+/* Optional device buffers for intermediates of k3x_hip_official_ffn (any may
+ * be NULL).  T tokens, K top_k, E experts, L latent, H hidden. */
+typedef struct k3x_hip_official_taps {
+    float* logits;         /* [T][E] (device routing only) */
+    uint32_t* ids;         /* [T][K] route order */
+    float* contributions;  /* [T][K] */
+    uint16_t* latent;      /* [T][L] bf16 bits, routed_down output */
+    float* expert_out;     /* [T][K][L] expert outputs before their bf16 rounding */
+    uint16_t* mixed;       /* [T][L] bf16 bits, slot-ordered mix */
+    float* routed;         /* [T][H] routed_up output before rounding */
+    float* shared;         /* [T][H] shared FFN output before rounding */
+} k3x_hip_official_taps;
+
+/* experts: a bank of hidden L (its own shared expert unused); the official
+ * layer keeps a reference to it and must be destroyed first. */
+int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
+                            const k3x_hip_official_desc* desc,
+                            k3x_hip_official** out);
+int k3x_hip_official_destroy(k3x_hip_official* official);
+
+/* Host bf16 words: routed_down [L][H], routed_norm [L], routed_up [H][L];
+ * shared gate, up [Is][H] and down [H][Is] (NULL when Is = 0).
+ * OfficialMoeFfnView (backend.hpp:171-176).  Synchronous. */
+int k3x_hip_official_upload_ffn(k3x_hip_official* official, const uint16_t* routed_down,
+                                const uint16_t* routed_norm, const uint16_t* routed_up,
+                                const uint16_t* shared_gate, const uint16_t* shared_up,
+                                const uint16_t* shared_down);
+
+/* Host: bf16 words residual_norm [H], residual_proj [H], post_norm [H],
+ * router [E][H]; fp32 correction [E].  OfficialMoeRoutePrepareView
+ * (backend.hpp:184-189) plus the router correction.  Synchronous. */
+int k3x_hip_official_upload_route(k3x_hip_official* official, const uint16_t* residual_norm,
+                                  const uint16_t* residual_proj, const uint16_t* post_norm,
+                                  const uint16_t* router, const float* correction);
+
+/* Seeded synthetic weights for both uploads (no reference counterpart):
+ * dense matrices and the router ~ N(0, sigma^2) in bf16, the three norm
+ * vectors 1, residual_proj ~ N(0, proj_sigma^2), correction ~
+ * N(0, correction_sigma^2).  Synchronous. */
+int k3x_hip_official_fill_synthetic(k3x_hip_official* official, uint64_t seed, float sigma,
+                                    float router_sigma, float proj_sigma,
+                                    float correction_sigma);
+
+/* Route preparation for T tokens: the two-source attention-residual mix and
+ * post-norm (official_moe.cpp:156-209) -> hidden bf16 [T][H], and, when
+ * logits is non-NULL, the router logits [T][E] over it (official_moe.cpp:
+ * 247-269).  prefix and block_residual device fp32 [T][H].  Replaces
+ * ComputeBackend::prepare_official_moe_route (backend.hpp:384-389) with the
+ * hidden kept on the device.  Asynchronous. */
+int k3x_hip_official_prepare(k3x_hip_ctx* ctx, k3x_hip_official* official, uint32_t tokens,
+                             float rms_epsilon, const float* prefix,
+                             const float* block_residual, uint16_t* hidden, float* logits);
+
+/* The FFN for T tokens: hidden bf16 [T][H] (prepared), prefix fp32 [T][H];
+ * the route as device ids [T][K] + contributions [T][K], or ids ==
+ * contributions == NULL to route on the device (router logits over hidden,
+ * sigmoid + correction, natural Top-K, contributions s / sum s in double:
+ * official_moe.cpp:211-245).  out bf16 [T][H] = bf16(bf16(prefix) +
+ * bf16(routed + shared)).  params: tokens, top_k, rms_epsilon and the GLU
+ * (SiTU for the reference's layer); routed_scale, renorm and flags are not
+ * used.  Replaces ComputeBackend::official_mxfp4_moe_ffn
+ * (backend.hpp:376-383) batched over tokens.  Asynchronous. */
+int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* official,
+                         const k3x_hip_moe_params* params, const uint16_t* hidden,
+                         const float* prefix, const uint32_t* ids,
+                         const float* contributions, uint16_t* out,
+                         const k3x_hip_official_taps* taps);
 
 #ifdef __cplusplus
 }

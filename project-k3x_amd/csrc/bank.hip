@@ -235,6 +235,25 @@ int retile_shared(k3x_hip_bank* b, const uint16_t* src[3], uint64_t seed, float 
 
 namespace k3x_hip {
 
+int retile_bf16_matrix(k3x_hip_ctx* ctx, const uint16_t* src, uint64_t key, float sigma,
+                       uint32_t rows, uint32_t cols, uint32_t S, uint32_t which, uint4* dst) {
+    const size_t n = (size_t)(rows / 16) * (cols / 128) * 256;
+    hipLaunchKernelGGL(retile_bf16, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, src, key,
+                       sigma, rows, cols, cols / 128, S, which, dst);
+    return check_launch(ctx);
+}
+
+int fill_normal_f32_dev(k3x_hip_ctx* ctx, uint64_t key, size_t n, float sigma, float* out) {
+    hipLaunchKernelGGL(fill_normal_f32, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, key, n,
+                       sigma, out);
+    return check_launch(ctx);
+}
+
+int fill_const_f32_dev(k3x_hip_ctx* ctx, size_t n, float v, float* out) {
+    hipLaunchKernelGGL(fill_const_f32, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, n, v, out);
+    return check_launch(ctx);
+}
+
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes) {
     if (bytes <= ctx->scratch_bytes) return K3X_OK;
     // The old scratch may still be read by enqueued kernels (on either stream).

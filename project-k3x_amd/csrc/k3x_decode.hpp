@@ -19,6 +19,7 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
 // out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
 // + shared[t][h]) on the context stream (the combine of both paths).
 int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
-                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32);
+                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32,
+                   bool round_y = false);
 
 }  // namespace k3x_hip

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "../../include/k3x_hip_moe.h"
+#include "k3x_device.hpp"
 
 // One timed stage launch: a hipEvent pair recorded around it.
 struct StageMark {
@@ -122,6 +123,32 @@ int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
 // Refreshes bank->router_wp from bank->router_w on the context stream (a
 // no-op when the hidden size has no residue-major copy).
 int permute_router(k3x_hip_bank* bank);
+
+// Bank-side helpers for other weight holders (official.hip), on the context
+// stream: retile a bf16 matrix [rows][cols] (src on the device, or NULL for
+// the seeded N(0, sigma) generator under `key`) into the tile layout as
+// matrix `which` of S interleaved ones; seeded normal and constant fp32 fills.
+int retile_bf16_matrix(k3x_hip_ctx* ctx, const uint16_t* src, uint64_t key, float sigma,
+                       uint32_t rows, uint32_t cols, uint32_t S, uint32_t which, uint4* dst);
+int fill_normal_f32_dev(k3x_hip_ctx* ctx, uint64_t key, size_t n, float sigma, float* out);
+int fill_const_f32_dev(k3x_hip_ctx* ctx, size_t n, float v, float* out);
+
+// Launchers shared with the official layer (official.hip), all on the
+// context stream unless a stream is given: RMSNorm (bf16 in/out, fp32 gamma),
+// router logits (fp32 W [E][H], fp64 canonical order), natural Top-K with
+// renormalisation, and dense bf16 projections in the bank's tile layout
+// (gate/up pair [I/16][H/128][2][4][64] -> GLU -> bf16 act [T][I]; one
+// matrix [N/16][K/128][4][64] -> fp32 [T][N]).
+int launch_rmsnorm(k3x_hip_ctx* ctx, const uint16_t* x, const float* gamma, uint32_t T,
+                   uint32_t H, float eps, uint16_t* xn);
+int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const uint16_t* xn, uint32_t E,
+                         uint32_t H, uint32_t T, float* logits);
+int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E, uint32_t K,
+                uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids, float* weights);
+int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
+                  uint32_t T, const k3x_dev::GluParams& glu, uint16_t* act, hipStream_t stream);
+int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
+               uint32_t T, float* y, hipStream_t stream);
 
 // Whether a bank of this hidden size keeps the residue-major router copy,
 // and that copy's size in floats (experts padded to 16).

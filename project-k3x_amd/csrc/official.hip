@@ -1,0 +1,520 @@
+// official.hip -- the official K3 MoE FFN (Stable LatentMoE) around a bank of
+// experts at the latent width, after runtime/src/official_moe.cpp:156-344.
+//
+//   prepare   hidden = post_norm(bf16(p0 bf16(residual) + p1 bf16(prefix))),
+//             p = softmax of the two sources' scores (official_prepare_kernel);
+//             router logits over hidden (the layer's router kernels)
+//   route     sigmoid + correction, natural Top-K, s / sum s (topk_kernel)
+//   latent    bf16(routed_down . hidden)                 (dense GEMM + rounding)
+//   experts   the bank's grouped MXFP4 path on latent; each expert output
+//             rounded to bf16 before the slot-ordered mix; mixed rounded
+//   norm      RMSNorm(mixed, routed_norm)                (rmsnorm_kernel)
+//   routed    routed_up . norm; shared FFN on hidden     (dense GEMMs)
+//   out       bf16(bf16(prefix) + bf16(bf16(routed) + bf16(shared)))
+//
+// Sums run in the layer's own orders (fp64 canonical for the norms and the
+// router, fp32 MFMA for the projections), not the reference's sequential
+// double ones; the reference's checks on this layer hold at 2e-2.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "k3x_decode.hpp"
+#include "k3x_device.hpp"
+#include "k3x_gemm.hpp"
+#include "k3x_internal.hpp"
+
+using namespace k3x_dev;
+
+struct k3x_hip_official {
+    k3x_hip_ctx* ctx = nullptr;
+    k3x_hip_bank* bank = nullptr;  // experts at the latent width
+    uint32_t H = 0, L = 0, E = 0, I_s = 0;
+    // Dense bf16 matrices in the bank's tile layout.
+    uint4* routed_down = nullptr;  // [L/16][H/128][4][64]
+    uint4* routed_up = nullptr;    // [H/16][L/128][4][64]
+    uint4* shared_gu = nullptr;    // [Is/16][H/128][2][4][64]
+    uint4* shared_dn = nullptr;    // [H/16][Is/128][4][64]
+    // bf16 vectors and the router held as fp32 (exact).
+    float* routed_norm = nullptr;    // [L]
+    float* residual_norm = nullptr;  // [H]
+    float* residual_proj = nullptr;  // [H]
+    float* post_norm = nullptr;      // [H]
+    float* router = nullptr;         // [E][H]
+    float* correction = nullptr;     // [E]
+    bool ffn_ready = false, route_ready = false;
+    // Per-call buffers (grow-only; the bank's forward uses the context scratch).
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+namespace {
+
+constexpr int kThreads = 256;
+inline unsigned blocks_for(size_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
+
+__device__ inline void latch(uint32_t* status, uint32_t code) { atomicCAS(status, 0u, code); }
+__device__ inline float bf16_round(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
+
+// Canonical fp64 block sum over 256 threads (xor butterfly in each wave, then
+// (w0 + w1) + (w2 + w3)); every thread gets the result.
+__device__ inline double block_sum(double v, double* red) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const double r = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return r;
+}
+
+// One 256-thread block per token.  runtime/src/official_moe.cpp:156-209:
+// both sources rounded to bf16; per source inv = 1 / sqrt(float(sum v^2 / H)
+// + eps) and score = sum (double)(v * inv) * norm * proj; p = softmax of the
+// two scores in float; mix = bf16(p0 v0 + p1 v1); hidden = bf16(mix * inv' *
+// post_norm) with inv' from mix's own sum of squares (:61-80).  Sums of
+// thread i run over k = i, i + 256, ... in order, then the canonical tree.
+__global__ __launch_bounds__(kThreads) void official_prepare_kernel(
+    const float* __restrict__ prefix, const float* __restrict__ residual,
+    const float* __restrict__ res_norm, const float* __restrict__ res_proj,
+    const float* __restrict__ post_norm, uint32_t H, float eps, uint16_t* __restrict__ hidden,
+    uint32_t* status) {
+    extern __shared__ float s_mix[];  // [H]
+    __shared__ double red[4];
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x;
+    const float* src[2] = {residual + (size_t)blockIdx.x * H, prefix + (size_t)blockIdx.x * H};
+    float inv[2], score[2];
+    int bad = 0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        double sq = 0.0;
+        for (uint32_t k = tid; k < H; k += kThreads) {
+            const float v = bf16_round(src[r][k]);
+            bad |= !__builtin_isfinite(src[r][k]);
+            sq = __builtin_fma((double)v, (double)v, sq);  // exact product: fused == separate
+        }
+        sq = block_sum(sq, red);
+        inv[r] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+        double sc = 0.0;
+        for (uint32_t k = tid; k < H; k += kThreads) {
+            const float v = bf16_round(src[r][k]);
+            const double term =
+                ((double)__fmul_rn(v, inv[r]) * (double)res_norm[k]) * (double)res_proj[k];
+            sc = sc + term;
+        }
+        score[r] = (float)block_sum(sc, red);
+    }
+    if (__syncthreads_or(bad)) {
+        if (tid == 0) latch(status, K3X_ERR_INVALID_EXTENT);
+        return;
+    }
+    const float mx = score[0] >= score[1] ? score[0] : score[1];
+    float p0 = expf_cr(__fsub_rn(score[0], mx)), p1 = expf_cr(__fsub_rn(score[1], mx));
+    const float den = __fadd_rn(p0, p1);
+    p0 = __fdiv_rn(p0, den);
+    p1 = __fdiv_rn(p1, den);
+    double sq = 0.0;
+    for (uint32_t k = tid; k < H; k += kThreads) {
+        const float m = bf16_round(__fadd_rn(__fmul_rn(p0, bf16_round(src[0][k])),
+                                             __fmul_rn(p1, bf16_round(src[1][k]))));
+        s_mix[k] = m;
+        sq = __builtin_fma((double)m, (double)m, sq);
+    }
+    sq = block_sum(sq, red);
+    const float inv2 = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+    uint16_t* out = hidden + (size_t)blockIdx.x * H;
+    for (uint32_t k = tid; k < H; k += kThreads)
+        out[k] = f32_to_bf16(__fmul_rn(__fmul_rn(s_mix[k], inv2), post_norm[k]));
+}
+
+// fp32 values rounded to bf16 in place (synthetic bf16 weights held as fp32).
+__global__ void round_in_place_kernel(float* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) p[i] = bf16_round(p[i]);
+}
+
+// bf16 bits of fp32 values.
+__global__ void round_bf16_kernel(const float* __restrict__ in, size_t n,
+                                  uint16_t* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(in[i]);
+}
+
+// out = bf16(bf16(prefix) + bf16(bf16(routed) + bf16(shared)))
+// (runtime/src/official_moe.cpp:336-340; no shared FFN: shared = 0).
+__global__ void official_out_kernel(const float* __restrict__ prefix,
+                                    const float* __restrict__ routed,
+                                    const float* __restrict__ shared, size_t n,
+                                    uint16_t* __restrict__ out, const uint32_t* status) {
+    if (*(volatile const uint32_t*)status) return;
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float sh = shared ? bf16_round(shared[i]) : 0.0f;
+    const float combined = bf16_round(__fadd_rn(bf16_round(routed[i]), sh));
+    out[i] = f32_to_bf16(__fadd_rn(bf16_round(prefix[i]), combined));
+}
+
+// bf16 words -> fp32 on the host (exact).
+std::vector<float> widen(const uint16_t* w, size_t n) {
+    std::vector<float> f(n);
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t b = (uint32_t)w[i] << 16;
+        std::memcpy(&f[i], &b, 4);
+    }
+    return f;
+}
+
+bool finite_bf16(const uint16_t* w, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if ((w[i] & 0x7f80u) == 0x7f80u) return false;
+    return true;
+}
+
+template <typename T>
+int alloc(T** p, size_t bytes) {
+    if (!bytes) return K3X_OK;
+    if (hipMalloc((void**)p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    }
+    return K3X_OK;
+}
+
+void free_all(k3x_hip_official* o) {
+    for (void* p : {(void*)o->routed_down, (void*)o->routed_up, (void*)o->shared_gu,
+                    (void*)o->shared_dn, (void*)o->routed_norm, (void*)o->residual_norm,
+                    (void*)o->residual_proj, (void*)o->post_norm, (void*)o->router,
+                    (void*)o->correction, o->scratch})
+        if (p) (void)hipFree(p);
+}
+
+// Upload of a host bf16 matrix [rows][cols] into tiles (matrix `which` of S).
+int upload_matrix(k3x_hip_official* o, const uint16_t* host, uint32_t rows, uint32_t cols,
+                  uint32_t S, uint32_t which, uint4* dst) {
+    k3x_hip_ctx* ctx = o->ctx;
+    const size_t n = (size_t)rows * cols;
+    uint16_t* staging = nullptr;
+    if (alloc(&staging, n * 2)) return K3X_ERR_BACKEND_UNAVAILABLE;
+    int st = hipMemcpyAsync(staging, host, n * 2, hipMemcpyHostToDevice, ctx->stream) == hipSuccess
+                 ? K3X_OK
+                 : K3X_ERR_BACKEND_UNAVAILABLE;
+    if (!st) st = k3x_hip::retile_bf16_matrix(ctx, staging, 0, 0.0f, rows, cols, S, which, dst);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
+    (void)hipFree(staging);
+    if (!st) ctx->weight_h2d_bytes += n * 2;
+    return st;
+}
+
+int upload_vector(k3x_hip_official* o, const uint16_t* host, size_t n, float* dst) {
+    const std::vector<float> f = widen(host, n);
+    if (hipMemcpy(dst, f.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    o->ctx->weight_h2d_bytes += n * 2;
+    return K3X_OK;
+}
+
+// Per-call buffer layout of k3x_hip_official_ffn; returns bytes (base null:
+// measure only).
+struct FfnBuffers {
+    float* logits;        // [T][E] (device route)
+    uint32_t* ids;        // [T][K]
+    float* contrib;       // [T][K]
+    float* latent_f32;    // [T][L]
+    uint16_t* latent;     // [T][L]
+    uint16_t* mixed;      // [T][L]
+    uint16_t* normed;     // [T][L]
+    float* routed;        // [T][H]
+    uint16_t* sact;       // [T][Is]
+    float* shared;        // [T][H]
+};
+
+size_t carve(uint8_t* base, const k3x_hip_official* o, uint32_t T, uint32_t K, FfnBuffers* b) {
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* p = base ? base + at : nullptr;
+        at += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    b->logits = (float*)take((size_t)T * o->E * 4);
+    b->ids = (uint32_t*)take((size_t)T * K * 4);
+    b->contrib = (float*)take((size_t)T * K * 4);
+    b->latent_f32 = (float*)take((size_t)T * o->L * 4);
+    b->latent = (uint16_t*)take((size_t)T * o->L * 2);
+    b->mixed = (uint16_t*)take((size_t)T * o->L * 2);
+    b->normed = (uint16_t*)take((size_t)T * o->L * 2);
+    b->routed = (float*)take((size_t)T * o->H * 4);
+    b->sact = (uint16_t*)take((size_t)T * std::max(o->I_s, 1u) * 2);
+    b->shared = (float*)take((size_t)T * o->H * 4);
+    return at;
+}
+
+int ensure(k3x_hip_official* o, size_t bytes) {
+    if (bytes <= o->scratch_bytes) return K3X_OK;
+    // Enqueued work of an earlier call may still use the old buffers.
+    if (hipStreamSynchronize(o->ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    if (o->scratch) (void)hipFree(o->scratch);
+    o->scratch = nullptr;
+    o->scratch_bytes = 0;
+    const size_t rounded = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    if (alloc(&o->scratch, rounded)) return K3X_ERR_BACKEND_UNAVAILABLE;
+    o->scratch_bytes = rounded;
+    return K3X_OK;
+}
+
+int copy_d2d(k3x_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!dst || dst == src) return K3X_OK;
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream) == hipSuccess
+               ? K3X_OK
+               : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+int launched(k3x_hip_ctx* ctx, unsigned n) {
+    ctx->kernel_launches += n;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+}  // namespace
+
+extern "C" {
+
+int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
+                            const k3x_hip_official_desc* desc, k3x_hip_official** out) {
+    if (!ctx || !experts || !desc || !out || experts->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    *out = nullptr;
+    const uint32_t H = desc->hidden, Is = desc->shared_inter, L = experts->desc.hidden;
+    if (!H || H % 128 || Is % 128 || L % 128) return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    auto* o = new (std::nothrow) k3x_hip_official();
+    if (!o) return K3X_ERR_BACKEND_UNAVAILABLE;
+    o->ctx = ctx;
+    o->bank = experts;
+    o->H = H;
+    o->L = L;
+    o->E = experts->desc.experts;
+    o->I_s = Is;
+    int st = K3X_OK;
+    st = st ? st : alloc(&o->routed_down, (size_t)L * H * 2);
+    st = st ? st : alloc(&o->routed_up, (size_t)H * L * 2);
+    st = st ? st : alloc(&o->shared_gu, (size_t)2 * Is * H * 2);
+    st = st ? st : alloc(&o->shared_dn, (size_t)H * Is * 2);
+    st = st ? st : alloc(&o->routed_norm, (size_t)L * 4);
+    st = st ? st : alloc(&o->residual_norm, (size_t)H * 4);
+    st = st ? st : alloc(&o->residual_proj, (size_t)H * 4);
+    st = st ? st : alloc(&o->post_norm, (size_t)H * 4);
+    st = st ? st : alloc(&o->router, (size_t)o->E * H * 4);
+    st = st ? st : alloc(&o->correction, (size_t)o->E * 4);
+    if (st) {
+        free_all(o);
+        delete o;
+        return st;
+    }
+    ++experts->ctx->live_banks;  // keeps the context alive as a bank would
+    *out = o;
+    return K3X_OK;
+}
+
+int k3x_hip_official_destroy(k3x_hip_official* o) {
+    if (!o) return K3X_ERR_INVALID_EXTENT;
+    (void)hipSetDevice(o->ctx->device);
+    (void)hipStreamSynchronize(o->ctx->stream);
+    free_all(o);
+    --o->ctx->live_banks;
+    delete o;
+    return K3X_OK;
+}
+
+int k3x_hip_official_upload_ffn(k3x_hip_official* o, const uint16_t* routed_down,
+                                const uint16_t* routed_norm, const uint16_t* routed_up,
+                                const uint16_t* shared_gate, const uint16_t* shared_up,
+                                const uint16_t* shared_down) {
+    if (!o || !routed_down || !routed_norm || !routed_up) return K3X_ERR_INVALID_EXTENT;
+    const size_t HL = (size_t)o->H * o->L, HS = (size_t)o->H * o->I_s;
+    if (o->I_s && (!shared_gate || !shared_up || !shared_down)) return K3X_ERR_INVALID_EXTENT;
+    // Validation before any device write (the reference's views are finite bf16).
+    if (!finite_bf16(routed_down, HL) || !finite_bf16(routed_up, HL) ||
+        !finite_bf16(routed_norm, o->L) ||
+        (o->I_s && (!finite_bf16(shared_gate, HS) || !finite_bf16(shared_up, HS) ||
+                    !finite_bf16(shared_down, HS))))
+        return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(o->ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    o->ffn_ready = false;
+    int st = upload_matrix(o, routed_down, o->L, o->H, 1, 0, o->routed_down);
+    st = st ? st : upload_matrix(o, routed_up, o->H, o->L, 1, 0, o->routed_up);
+    st = st ? st : upload_vector(o, routed_norm, o->L, o->routed_norm);
+    if (o->I_s) {
+        st = st ? st : upload_matrix(o, shared_gate, o->I_s, o->H, 2, 0, o->shared_gu);
+        st = st ? st : upload_matrix(o, shared_up, o->I_s, o->H, 2, 1, o->shared_gu);
+        st = st ? st : upload_matrix(o, shared_down, o->H, o->I_s, 1, 0, o->shared_dn);
+    }
+    if (!st) o->ffn_ready = true;
+    return st;
+}
+
+int k3x_hip_official_upload_route(k3x_hip_official* o, const uint16_t* residual_norm,
+                                  const uint16_t* residual_proj, const uint16_t* post_norm,
+                                  const uint16_t* router, const float* correction) {
+    if (!o || !residual_norm || !residual_proj || !post_norm || !router || !correction)
+        return K3X_ERR_INVALID_EXTENT;
+    const size_t H = o->H, EH = (size_t)o->E * o->H;
+    if (!finite_bf16(residual_norm, H) || !finite_bf16(residual_proj, H) ||
+        !finite_bf16(post_norm, H) || !finite_bf16(router, EH))
+        return K3X_ERR_INVALID_EXTENT;
+    for (uint32_t e = 0; e < o->E; ++e)
+        if (!std::isfinite(correction[e])) return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(o->ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    o->route_ready = false;
+    int st = upload_vector(o, residual_norm, H, o->residual_norm);
+    st = st ? st : upload_vector(o, residual_proj, H, o->residual_proj);
+    st = st ? st : upload_vector(o, post_norm, H, o->post_norm);
+    st = st ? st : upload_vector(o, router, EH, o->router);
+    if (!st && hipMemcpy(o->correction, correction, (size_t)o->E * 4, hipMemcpyHostToDevice) !=
+                   hipSuccess)
+        st = K3X_ERR_BACKEND_UNAVAILABLE;
+    if (!st) o->route_ready = true;
+    return st;
+}
+
+int k3x_hip_official_fill_synthetic(k3x_hip_official* o, uint64_t seed, float sigma,
+                                    float router_sigma, float proj_sigma,
+                                    float correction_sigma) {
+    if (!o) return K3X_ERR_INVALID_EXTENT;
+    k3x_hip_ctx* ctx = o->ctx;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    auto key = [&](uint64_t stream) { return stream_key(seed, stream << 32); };
+    // Streams of this generator: 1..4 dense, 5..7 vectors, 8 router, 9 correction.
+    int st = k3x_hip::retile_bf16_matrix(ctx, nullptr, key(1), sigma, o->L, o->H, 1, 0,
+                                         o->routed_down);
+    st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(2), sigma, o->H, o->L, 1, 0,
+                                               o->routed_up);
+    if (o->I_s) {
+        st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(3), sigma, o->I_s, o->H, 2,
+                                                   0, o->shared_gu);
+        st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(4), sigma, o->I_s, o->H, 2,
+                                                   1, o->shared_gu);
+        st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(5), sigma, o->H, o->I_s, 1,
+                                                   0, o->shared_dn);
+    }
+    st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->L, 1.0f, o->routed_norm);
+    st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->H, 1.0f, o->residual_norm);
+    st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->H, 1.0f, o->post_norm);
+    st = st ? st : k3x_hip::fill_normal_f32_dev(ctx, key(6), o->H, proj_sigma, o->residual_proj);
+    st = st ? st : k3x_hip::fill_normal_f32_dev(ctx, key(8), (size_t)o->E * o->H, router_sigma,
+                                                 o->router);
+    st = st ? st : k3x_hip::fill_normal_f32_dev(ctx, key(9), o->E, correction_sigma,
+                                                 o->correction);
+    // The router and residual_proj hold bf16 values in this layer.
+    if (!st) {
+        const size_t eh = (size_t)o->E * o->H;
+        hipLaunchKernelGGL(round_in_place_kernel, dim3(blocks_for(eh)), dim3(kThreads), 0,
+                           ctx->stream, o->router, eh);
+        hipLaunchKernelGGL(round_in_place_kernel, dim3(blocks_for(o->H)), dim3(kThreads), 0,
+                           ctx->stream, o->residual_proj, (size_t)o->H);
+        st = launched(ctx, 2);
+    }
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
+    if (!st) o->ffn_ready = o->route_ready = true;
+    return st;
+}
+
+int k3x_hip_official_prepare(k3x_hip_ctx* ctx, k3x_hip_official* o, uint32_t T, float eps,
+                             const float* prefix, const float* block_residual, uint16_t* hidden,
+                             float* logits) {
+    if (!ctx || !o || o->ctx != ctx || !prefix || !block_residual || !hidden || !T)
+        return K3X_ERR_INVALID_EXTENT;
+    if (!std::isfinite(eps) || !(eps > 0.0f)) return K3X_ERR_INVALID_EXTENT;
+    if (!o->route_ready) return K3X_ERR_INVALID_STATE;
+    if ((size_t)o->H * 4 > ctx->max_lds_per_block) return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    hipLaunchKernelGGL(official_prepare_kernel, dim3(T), dim3(kThreads), (size_t)o->H * 4,
+                       ctx->stream, prefix, block_residual, o->residual_norm, o->residual_proj,
+                       o->post_norm, o->H, eps, hidden, ctx->status);
+    int st = launched(ctx, 1);
+    if (!st && logits) st = k3x_hip::launch_router_logits(ctx, o->router, hidden, o->E, o->H, T, logits);
+    return st;
+}
+
+int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_moe_params* p,
+                         const uint16_t* hidden, const float* prefix, const uint32_t* ids,
+                         const float* contributions, uint16_t* out,
+                         const k3x_hip_official_taps* taps) {
+    if (!ctx || !o || o->ctx != ctx || !p || !hidden || !prefix || !out)
+        return K3X_ERR_INVALID_EXTENT;
+    if ((ids == nullptr) != (contributions == nullptr)) return K3X_ERR_INVALID_EXTENT;
+    const uint32_t T = p->tokens, K = p->top_k;
+    if (!T || !K || K > 64 || K > o->E) return K3X_ERR_INVALID_EXTENT;
+    if (!std::isfinite(p->rms_epsilon) || !(p->rms_epsilon > 0.0f)) return K3X_ERR_INVALID_EXTENT;
+    if (!o->ffn_ready || (!ids && !o->route_ready)) return K3X_ERR_INVALID_STATE;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    FfnBuffers b;
+    int st = ensure(o, carve(nullptr, o, T, K, &b));
+    if (st) return st;
+    carve(static_cast<uint8_t*>(o->scratch), o, T, K, &b);
+    const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+    // Route (official_moe.cpp:211-269): logits over hidden, sigmoid +
+    // correction, natural Top-K, contributions s / sum s in double.
+    if (!ids) {
+        st = k3x_hip::launch_router_logits(ctx, o->router, hidden, o->E, o->H, T, b.logits);
+        st = st ? st : k3x_hip::launch_topk(ctx, b.logits, o->correction, o->E, K, T, 1.0f,
+                                            K3X_RENORM_DOUBLE, b.ids, b.contrib);
+        if (st) return st;
+        ids = b.ids;
+        contributions = b.contrib;
+    }
+    // latent = bf16(routed_down . hidden) (official_moe.cpp:305).
+    st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, b.latent_f32, ctx->stream);
+    if (st) return st;
+    hipLaunchKernelGGL(round_bf16_kernel, dim3(blocks_for((size_t)T * o->L)), dim3(kThreads), 0,
+                       ctx->stream, b.latent_f32, (size_t)T * o->L, b.latent);
+    if ((st = launched(ctx, 1))) return st;
+    // Experts on the latent: the bank's grouped path, each expert output
+    // rounded to bf16 before the slot-ordered mix, the mix rounded
+    // (official_moe.cpp:82-103, :313-326).
+    k3x_hip_moe_params ep = *p;
+    ep.routed_scale = 1.0f;
+    ep.renorm = K3X_RENORM_DOUBLE;
+    ep.flags = K3X_FLAG_ROUND_EXPERT_OUT;
+    k3x_hip_moe_taps et{};
+    if (taps) et.expert_out = taps->expert_out;
+    st = k3x_hip_moe_forward_routed(ctx, o->bank, &ep, b.latent, ids, contributions, nullptr,
+                                    nullptr, b.mixed, taps ? &et : nullptr);
+    if (st) return st;
+    // routed = routed_up . RMSNorm(mixed, routed_norm) (official_moe.cpp:327-333).
+    st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon, b.normed);
+    st = st ? st : k3x_hip::dense_down(ctx, o->routed_up, o->H, o->L, b.normed, T, b.routed,
+                                       ctx->stream);
+    // Shared FFN on hidden (official_moe.cpp:105-117, :307).
+    if (!st && o->I_s) {
+        st = k3x_hip::dense_gate_up(ctx, o->shared_gu, o->I_s, o->H, hidden, T, glu, b.sact,
+                                    ctx->stream);
+        st = st ? st : k3x_hip::dense_down(ctx, o->shared_dn, o->H, o->I_s, b.sact, T, b.shared,
+                                           ctx->stream);
+    }
+    if (st) return st;
+    const size_t n = (size_t)T * o->H;
+    hipLaunchKernelGGL(official_out_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream,
+                       prefix, b.routed, o->I_s ? b.shared : nullptr, n, out, ctx->status);
+    if ((st = launched(ctx, 1))) return st;
+    if (taps) {
+        st = copy_d2d(ctx, taps->ids, ids, (size_t)T * K * 4);
+        st = st ? st : copy_d2d(ctx, taps->contributions, contributions, (size_t)T * K * 4);
+        if (!st && taps->logits && ids == b.ids)
+            st = copy_d2d(ctx, taps->logits, b.logits, (size_t)T * o->E * 4);
+        st = st ? st : copy_d2d(ctx, taps->latent, b.latent, (size_t)T * o->L * 2);
+        st = st ? st : copy_d2d(ctx, taps->mixed, b.mixed, (size_t)T * o->L * 2);
+        st = st ? st : copy_d2d(ctx, taps->routed, b.routed, n * 4);
+        if (!st && taps->shared) {
+            st = o->I_s ? copy_d2d(ctx, taps->shared, b.shared, n * 4)
+                        : k3x_hip::fill_const_f32_dev(ctx, n, 0.0f, taps->shared);
+        }
+    }
+    return st;
+}
+
+}  // extern "C"

@@ -967,6 +967,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
                                                       uint32_t K, uint32_t H,
                                                       uint16_t* __restrict__ out,
                                                       float* __restrict__ out_f32,
+                                                      uint32_t round_y,
                                                       const uint32_t* status) {
     typedef typename CombineVec<VEC>::T vec_t;
     constexpr uint32_t kBatch = 16;
@@ -993,7 +994,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
             if (s0 + i >= K) break;
             const float* vi = reinterpret_cast<const float*>(&v[i]);
 #pragma unroll
-            for (int c = 0; c < VEC; ++c) mix[c] = __fadd_rn(mix[c], __fmul_rn(ws[i], vi[c]));
+            for (int c = 0; c < VEC; ++c) {
+                // The official layer rounds each expert output to bf16 first
+                // (runtime/src/official_moe.cpp:99-101).
+                const float yv = round_y ? __uint_as_float((uint32_t)f32_to_bf16(vi[c]) << 16)
+                                         : vi[c];
+                mix[c] = __fadd_rn(mix[c], __fmul_rn(ws[i], yv));
+            }
         }
     }
     if (shared) {
@@ -1083,7 +1090,8 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         p->top_k > d.experts)
         return K3X_ERR_INVALID_EXTENT;
     if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
-        p->renorm > 1 || (p->flags & ~(uint32_t)K3X_FLAG_GENERAL_PATH))
+        p->renorm > 1 ||
+        (p->flags & ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)))
         return K3X_ERR_INVALID_MXFP4;
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
@@ -1315,7 +1323,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         if ((st = run_wide(ctx, bank, p, s, xn, glu, !side))) return st;
         if ((st = joiner.join())) return st;
         return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
-                                       d.hidden, T, out, out_f32);
+                                       d.hidden, T, out, out_f32,
+                                       (p->flags & K3X_FLAG_ROUND_EXPERT_OUT) != 0);
     }
 
     GemmArgs g{};
@@ -1400,7 +1409,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     }
     if ((st = launched(ctx, d.shared_inter ? 4 : 2))) return st;
     return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
-                                   d.hidden, T, out, out_f32);
+                                   d.hidden, T, out, out_f32,
+                                       (p->flags & K3X_FLAG_ROUND_EXPERT_OUT) != 0);
 }
 
 int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
@@ -1460,15 +1470,118 @@ int permute_router(k3x_hip_bank* bank) {
 
 bool router_mfma_eligible(uint32_t hidden) { return hidden <= kRouterMaxHidden; }
 
+int launch_rmsnorm(k3x_hip_ctx* ctx, const uint16_t* x, const float* gamma, uint32_t T,
+                   uint32_t H, float eps, uint16_t* xn) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, gamma, H, eps, xn,
+                       (uint16_t*)nullptr, ctx->status);
+    return launched(ctx, 1);
+}
+
+int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const uint16_t* xn, uint32_t E,
+                         uint32_t H, uint32_t T, float* logits) {
+    if (T <= 4)
+        hipLaunchKernelGGL((router_kernel<1, 4>), dim3(E, 1), dim3(256), 0, ctx->stream, W, xn, E,
+                           H, T, logits, ctx->status);
+    else
+        hipLaunchKernelGGL((router_tile_kernel<kRouterEpb, kRouterTpb, 4>),
+                           dim3((E + kRouterEpb - 1) / kRouterEpb, (T + kRouterTpb - 1) / kRouterTpb),
+                           dim3(256), 0, ctx->stream, W, xn, E, H, T, logits, ctx->status);
+    return launched(ctx, 1);
+}
+
+int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E, uint32_t K,
+                uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids, float* weights) {
+    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)E * 12, ctx->stream, logits, bias,
+                       E, K, routed_scale, renorm, ids, weights, ctx->status);
+    return launched(ctx, 1);
+}
+
+// Dense bf16 projections in the bank's tile layout: the wide grouped GEMM
+// (one item per 128-row chunk of the T rows) from kWideMinTokens rows when
+// the shapes fit it, else expert_gemm over the T rows as one block.
+bool dense_wide_ok(WideKind kind, uint32_t N, uint32_t K, uint32_t T) {
+    return T >= kWideMinTokens && K % (128 * kWideStages) == 0 &&
+           (N / 16) % wide_rb_per_block(kind) == 0 && N % 16 == 0 &&
+           (uint64_t)T * std::max(N, K) * 4 < (1ull << 32) && (uint64_t)N * K * 4 < (1ull << 32);
+}
+
+int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
+                  uint32_t T, const GluParams& glu, uint16_t* act, hipStream_t stream) {
+    if (!T || I % 64 || H % 128) return K3X_ERR_INVALID_EXTENT;
+    if (dense_wide_ok(kWideSharedGateUp, I, H, T)) {
+        WideGemmArgs g{};
+        g.codes = reinterpret_cast<const uint8_t*>(tiles);
+        g.kt = H / 128;
+        g.nrb = I / 16;
+        g.a = x;
+        g.a_stride = H;
+        g.a_bytes = T * H * 2;
+        g.tokens = T;
+        g.act = act;
+        g.act_stride = I;
+        g.glu = glu;
+        g.status = ctx->status;
+        return launch_wide_gemm(ctx, kWideSharedGateUp, g, (T + kWideRows - 1) / kWideRows, stream);
+    }
+    if (stream != ctx->stream) return K3X_ERR_INVALID_EXTENT;
+    GemmArgs g{};
+    g.codes = reinterpret_cast<const uint8_t*>(tiles);
+    g.kt = H / 128;
+    g.a = x;
+    g.a_stride = H;
+    g.tokens = T;
+    g.act = act;
+    g.act_stride = I;
+    g.glu = glu;
+    g.status = ctx->status;
+    if (T > 16) launch_gemm<false, true, 4, 1>(ctx, g, 1, I);
+    else launch_gemm<false, true, 1, 1>(ctx, g, 1, I);
+    return launched(ctx, 1);
+}
+
+int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
+               uint32_t T, float* y, hipStream_t stream) {
+    if (!T || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
+    if (dense_wide_ok(kWideSharedDown, N, K, T)) {
+        WideGemmArgs g{};
+        g.codes = reinterpret_cast<const uint8_t*>(tiles);
+        g.kt = K / 128;
+        g.nrb = N / 16;
+        g.a = a;
+        g.a_stride = K;
+        g.a_bytes = T * K * 2;
+        g.tokens = T;
+        g.y = y;
+        g.y_stride = N;
+        g.status = ctx->status;
+        return launch_wide_gemm(ctx, kWideSharedDown, g, (T + kWideRows - 1) / kWideRows, stream);
+    }
+    if (stream != ctx->stream) return K3X_ERR_INVALID_EXTENT;
+    GemmArgs g{};
+    g.codes = reinterpret_cast<const uint8_t*>(tiles);
+    g.kt = K / 128;
+    g.a = a;
+    g.a_stride = K;
+    g.tokens = T;
+    g.y = y;
+    g.y_stride = N;
+    g.status = ctx->status;
+    if (T > 16) launch_gemm<false, false, 4, 2>(ctx, g, 1, N);
+    else launch_gemm<false, false, 1, 2>(ctx, g, 1, N);
+    return launched(ctx, 1);
+}
+
 size_t router_wp_floats(uint32_t experts) {
     return (size_t)(experts + 15) / 16 * kRouterRes * kRouterTileRes;
 }
 
 int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const float* shared,
-                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32) {
+                   uint32_t K, uint32_t H, uint32_t T, uint16_t* out, float* out_f32,
+                   bool round_y) {
     const int mark = begin_stage(ctx, K3X_STAGE_COMBINE);
-    hipLaunchKernelGGL(combine_kernel<kCombineVec>, dim3((H / kCombineVec + 255) / 256, T), dim3(256), 0, ctx->stream, y,
-                       weights, shared, K, H, out, out_f32, ctx->status);
+    hipLaunchKernelGGL(combine_kernel<kCombineVec>, dim3((H / kCombineVec + 255) / 256, T),
+                       dim3(256), 0, ctx->stream, y, weights, shared, K, H, out, out_f32,
+                       (uint32_t)round_y, ctx->status);
     end_stage(ctx, mark);
     return launched(ctx, 1);
 }
@@ -1485,7 +1598,8 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     Scratch s;
     if ((st = prepare(ctx, bank, p, &s))) return st;
-    if (!(p->flags & K3X_FLAG_GENERAL_PATH) && k3x_hip::decode_eligible(ctx, bank, p, x)) {
+    if (!(p->flags & (K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)) &&
+        k3x_hip::decode_eligible(ctx, bank, p, x)) {
         if ((st = k3x_hip::decode_forward(ctx, bank, p, s, x, out,
                                            taps ? taps->out_f32 : nullptr)))
             return st;

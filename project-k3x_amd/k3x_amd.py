@@ -68,6 +68,7 @@ class MoeParams(C.Structure):
                 ("renorm", C.c_uint32), ("flags", C.c_uint32)]
 
 FLAG_GENERAL_PATH = 1
+FLAG_ROUND_EXPERT_OUT = 2
 
 
 TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair_token",
@@ -77,6 +78,18 @@ TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair
 
 class MoeTaps(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in TAP_FIELDS]
+
+
+OFFICIAL_TAP_FIELDS = ["logits", "ids", "contributions", "latent", "expert_out", "mixed",
+                       "routed", "shared"]
+
+
+class OfficialTaps(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in OFFICIAL_TAP_FIELDS]
+
+
+class OfficialDesc(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("shared_inter", C.c_uint32)]
 
 
 class SynthDesc(C.Structure):
@@ -128,6 +141,15 @@ _SIGS = {
                                              _vp, _vp, C.POINTER(MoeTaps)]),
     "k3x_hip_expert_major_plan": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
                                             C.POINTER(MoeTaps)]),
+    "k3x_hip_official_create": (C.c_int, [_vp, _vp, C.POINTER(OfficialDesc), C.POINTER(_vp)]),
+    "k3x_hip_official_destroy": (C.c_int, [_vp]),
+    "k3x_hip_official_upload_ffn": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "k3x_hip_official_upload_route": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "k3x_hip_official_fill_synthetic": (C.c_int, [_vp, C.c_uint64, C.c_float, C.c_float,
+                                                  C.c_float, C.c_float]),
+    "k3x_hip_official_prepare": (C.c_int, [_vp, _vp, C.c_uint32, C.c_float, _vp, _vp, _vp, _vp]),
+    "k3x_hip_official_ffn": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp, _vp, _vp, _vp,
+                                       C.POINTER(OfficialTaps)]),
 }
 
 EXPORTED = sorted(_SIGS)
@@ -210,6 +232,8 @@ class Context:
     def close(self) -> None:
         """Destroys the context after every bank created on it."""
         if self.handle:
+            for off in list(getattr(self, "_officials", ())):
+                off.close()
             for bank in list(self._banks):
                 bank.close()
             check(self.lib.k3x_hip_ctx_destroy(self.handle), "k3x_hip_ctx_destroy")
@@ -304,6 +328,76 @@ class Bank:
     def close(self) -> None:
         if self.handle:
             self.lib.k3x_hip_bank_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Official:
+    """The official K3 MoE FFN around a bank of experts at the latent width
+    (k3x_hip_official_*); host weights are bf16 words (uint16 numpy arrays)."""
+
+    def __init__(self, ctx: Context, experts: Bank, hidden: int, shared_inter: int):
+        import weakref
+        self.ctx, self.lib, self.experts = ctx, ctx.lib, experts
+        self.hidden, self.shared_inter = hidden, shared_inter
+        h = _vp()
+        d = OfficialDesc(hidden, shared_inter)
+        check(self.lib.k3x_hip_official_create(ctx.handle, experts.handle, C.byref(d),
+                                               C.byref(h)), "k3x_hip_official_create")
+        self.handle = h
+        if not hasattr(ctx, "_officials"):
+            ctx._officials = weakref.WeakSet()
+        ctx._officials.add(self)
+
+    def upload_ffn(self, routed_down, routed_norm, routed_up, shared_gate=None, shared_up=None,
+                   shared_down=None) -> int:
+        import numpy as np
+        arrs = [None if a is None else np.ascontiguousarray(a, dtype=np.uint16)
+                for a in (routed_down, routed_norm, routed_up, shared_gate, shared_up,
+                          shared_down)]
+        return self.lib.k3x_hip_official_upload_ffn(self.handle, *[host_ptr(a) for a in arrs])
+
+    def upload_route(self, residual_norm, residual_proj, post_norm, router, correction) -> int:
+        import numpy as np
+        arrs = [np.ascontiguousarray(a, dtype=np.uint16) for a in
+                (residual_norm, residual_proj, post_norm, router)]
+        corr = np.ascontiguousarray(correction, dtype=np.float32)
+        return self.lib.k3x_hip_official_upload_route(self.handle, *[host_ptr(a) for a in arrs],
+                                                      host_ptr(corr))
+
+    def fill_synthetic(self, seed: int, sigma=0.02, router_sigma=0.02, proj_sigma=0.05,
+                       correction_sigma=0.1) -> None:
+        check(self.lib.k3x_hip_official_fill_synthetic(self.handle, seed, sigma, router_sigma,
+                                                       proj_sigma, correction_sigma),
+              "k3x_hip_official_fill_synthetic")
+
+    def prepare(self, tokens, eps, prefix, residual, hidden, logits=None) -> int:
+        return self.lib.k3x_hip_official_prepare(self.ctx.handle, self.handle, tokens, eps,
+                                                 ptr(prefix), ptr(residual), ptr(hidden),
+                                                 ptr(logits))
+
+    def ffn(self, params: "MoeParams", hidden, prefix, out, ids=None, contributions=None,
+            taps=None) -> int:
+        t = None
+        if taps:
+            t = OfficialTaps()
+            for k, v in taps.items():
+                if k not in OFFICIAL_TAP_FIELDS:
+                    raise ValueError(f"unknown tap {k!r}; taps are {OFFICIAL_TAP_FIELDS}")
+                setattr(t, k, ptr(v))
+        return self.lib.k3x_hip_official_ffn(self.ctx.handle, self.handle, C.byref(params),
+                                             ptr(hidden), ptr(prefix), ptr(ids),
+                                             ptr(contributions), ptr(out),
+                                             C.byref(t) if t is not None else None)
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.k3x_hip_official_destroy(self.handle)
             self.handle = None
 
     def __del__(self):
