@@ -12,8 +12,9 @@ layers of a decode pass do) and --inputs token pairs.
 Prints one JSON line.  value = microseconds per layer call (lower is better);
 the HBM figures use the bytes each call actually streams (distinct routed
 experts touched x 23,396,352 B + shared expert + router).  The same line
-carries the T=2048 prefill chunk as "prefill" and the reference
-CPU expert path, timed on this host, as "cpu_baseline".
+carries the T=2048 prefill chunk as "prefill", the official K3
+MoE FFN (Stable LatentMoE, at its own shapes) as "official", and the
+reference CPU expert path, timed on this host, as "cpu_baseline".
 """
 from __future__ import annotations
 
@@ -63,6 +64,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--inputs", type=int, default=8, help="distinct token pairs to cycle")
     ap.add_argument("--prefill-steps", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--official-steps", type=int, default=200,
+                    help="decode steps of the official layer leg (T=2048 runs 5)")
+    ap.add_argument("--no-official", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
@@ -237,6 +241,8 @@ def main() -> int:
         result["prefill"] = prefill(args, ctx, banks[0], k3x_amd, torch)
     for b in banks:
         b.close()
+    if not args.no_official:
+        result["official"] = official(args, ctx, k3x_amd, torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     ctx.close()
@@ -279,6 +285,68 @@ def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
             "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_floor_us": round(floor_us, 1),
             "frac_of_floor": round(floor_us / us, 4)}
+
+
+# The official K3 MoE FFN (Stable LatentMoE): hidden 7168, latent 3584, 896
+# MXFP4 experts of 3072 at the latent width, Top-16, bf16 shared FFN of 6144.
+OH, OL, OI, OE, OK, OS = 7168, 3584, 3072, 896, 16, 6144
+O_EXPERT_BYTES = 3 * (OL * OI // 2 + OL * OI // 32)                 # 17,547,264
+O_DENSE_BYTES = 2 * OL * OH * 2 + 3 * OS * OH * 2                   # routed down/up + shared
+O_ROUTE_BYTES = OE * OH * 4 + OE * 4 + 3 * OH * 4 + OL * 4          # router, vectors
+
+
+def official(args, ctx, k3x_amd, torch) -> dict:
+    """The official layer at its own shapes: prepare (two-source mix, router
+    logits) + FFN (route, latent projection, experts, routed_norm, routed_up,
+    shared FFN, output) per step, on synthetic weights; T=2 decode and a
+    T=2048 prefill chunk."""
+    dev = "cuda:0"
+    bank = k3x_amd.Bank(ctx, k3x_amd.LayerShape(OL, OI, OE, 0))
+    bank.fill_synthetic(SEED + 100, SCALE_LO, SCALE_HI, 0.02, 0.1, 0.02, 1.0)
+    off = k3x_amd.Official(ctx, bank, OH, OS)
+    off.fill_synthetic(SEED + 101, 0.02, 0.02, 0.05, 0.1)
+    out = {"workload": "official K3 MoE FFN: H=7168, latent 3584, E=896 MXFP4 experts of "
+                       "I=3072, Top-16, shared FFN 6144; prepare + FFN per step",
+           "data": "synthetic weights and inputs"}
+    for T, n in ((2, args.official_steps), (2048, 5)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(T)
+        prefix = torch.randn((T, OH), device=dev, generator=g)
+        residual = torch.randn((T, OH), device=dev, generator=g)
+        hidden = torch.empty((T, OH), dtype=torch.int16, device=dev)
+        y = torch.empty((T, OH), dtype=torch.int16, device=dev)
+        ids = torch.empty((T, OK), dtype=torch.int32, device=dev)
+        params = k3x_amd.make_params(T, OK, 1.0, 1e-5, k3x_amd.GLU_SITU, 4.0, 25.0,
+                                     k3x_amd.RENORM_DOUBLE)
+
+        def step(taps=None):
+            k3x_amd.check(off.prepare(T, 1e-5, prefix, residual, hidden), "official prepare")
+            k3x_amd.check(off.ffn(params, hidden, prefix, y, taps=taps), "official ffn")
+
+        step({"ids": ids})
+        for _ in range(3):
+            step()
+        k3x_amd.check(ctx.synchronize(), "official")
+        touched = int(torch.unique(ids).numel())
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / n * 1e6
+        k3x_amd.check(ctx.synchronize(), "official")
+        bytes_ = touched * O_EXPERT_BYTES + O_DENSE_BYTES + O_ROUTE_BYTES + 4 * T * OH * 4
+        flops = T * (OK * 2 * 3 * OL * OI + 2 * (2 * OL * OH + 3 * OS * OH) + 2 * OE * OH)
+        key = "decode_t2" if T == 2 else "prefill_t2048"
+        out[key] = {"tokens": T, "steps": n, "us_per_layer": round(us, 1),
+                    "experts_touched": touched, "bytes": bytes_,
+                    "hbm_gbps": round(bytes_ / (us * 1e-6) / 1e9, 1),
+                    "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "tflops": round(flops / (us * 1e-6) / 1e12, 2)}
+        log(f"official T={T}: {us:.1f} us/layer ({touched} experts)")
+    off.close()
+    bank.close()
+    return out
 
 
 def traffic_from(fetch_dir: str, write_dir: str) -> dict:

@@ -53,35 +53,6 @@ __device__ inline void latch(uint32_t* status, uint32_t code) { atomicCAS(status
 __device__ inline float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Sort key: larger adjusted score first, then lower expert index
-// (runtime/src/official_moe.cpp:226-232).  -0 folds into +0; 0 = no entry.
-__device__ inline uint64_t topk_key(float adj, uint32_t e) {
-    const float a = adj == 0.0f ? 0.0f : adj;
-    const uint32_t u = __float_as_uint(a);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - e);
-}
-
-// Maximum of v over the 64 lanes with DPP moves (quad permutes, row
-// rotates, row broadcasts): VALU latency instead of LDS-crossbar shuffles.
-// Rows not selected by a row_bcast keep their own value (max(v, v) = v).
-template <int Ctrl, int RowMask>
-__device__ inline uint32_t dpp_max_step(uint32_t x) {
-    const uint32_t y =
-        (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, Ctrl, RowMask, 0xf, false);
-    return x > y ? x : y;
-}
-
-__device__ inline uint32_t wave_max_u32(uint32_t v) {
-    v = dpp_max_step<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x124, 0xf>(v);  // row_ror:4
-    v = dpp_max_step<0x128, 0xf>(v);  // row_ror:8
-    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 // Canonical combination of one lane's four partial sums (partials 4l..4l+3
 // of the 256-way strided order) and the 64-lane butterfly: the pairwise tree
 // over all 256 partials.
@@ -506,107 +477,17 @@ struct SelectShared {
     uint32_t ptok[kMaxDecodeTokens * 64];
 };
 
-// Top-K of one token by one wave: keys held 8 per lane, popped K times.
-// Scores, validation and renormalisation as runtime/src/routing_policy.cpp
-// :40-95,146-157 (FLOAT) or runtime/src/official_moe.cpp:214-242 (DOUBLE),
-// then * routed_scale (runtime/src/model.cpp:1004-1009).
+// Top-K of one token by one wave (topk_wave, 8 keys per lane); the ids and
+// weights go to the outputs and to the block's grouping.
 // lg / bv: the token's logits and the bias of experts lane + 64 i (loaded
 // by the caller, before its status check).
 __device__ void topk_token(const SelectArgs& a, uint32_t t, const float (&lgv)[kKeysPerLane],
                            const float (&bv)[kKeysPerLane], SelectShared& sh) {
     const int lane = threadIdx.x & 63;
-    const uint32_t E = a.E, K = a.K;
-    uint64_t key[kKeysPerLane];
-    float score[kKeysPerLane];
-    uint32_t bad = 0;
-#pragma unroll
-    for (int i = 0; i < kKeysPerLane; ++i) {
-        const uint32_t e = lane + 64u * i;
-        key[i] = 0;
-        score[i] = 0.0f;
-        if (e < E) {
-            const float lg = lgv[i];
-            const float b = bv[i];
-            if (a.renorm == K3X_RENORM_DOUBLE &&
-                (!__builtin_isfinite(lg) || !__builtin_isfinite(b)))
-                bad = K3X_ERR_INVALID_EXTENT;
-            const float s = sigmoid_cr(lg);
-            const float adj = __fadd_rn(s, b);
-            if (a.renorm == K3X_RENORM_FLOAT &&
-                (!__builtin_isfinite(s) || s < 0.0f || s > 1.0f || !__builtin_isfinite(b) ||
-                 !__builtin_isfinite(adj)))
-                bad = K3X_ERR_INVALID_STATE;
-            score[i] = s;
-            key[i] = topk_key(adj, e);
-        }
-    }
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) bad = max(bad, (uint32_t)__shfl_xor((int)bad, d));
-    if (bad) {
-        if (lane == 0) {
-            latch(a.status, bad);
-            sh.bad = 1;
-        }
-        return;
-    }
-    // Local selection sort, descending: the lane's head is key[0].
-#pragma unroll
-    for (int i = 0; i < kKeysPerLane; ++i)
-#pragma unroll
-        for (int j = i + 1; j < kKeysPerLane; ++j)
-            if (key[j] > key[i]) {
-                const uint64_t tk = key[i];
-                key[i] = key[j];
-                key[j] = tk;
-                const float ts = score[i];
-                score[i] = score[j];
-                score[j] = ts;
-            }
-    float selsc = 0.0f;  // lane s < K keeps the score of slot s
-    uint32_t selid = 0;
-    for (uint32_t s = 0; s < K; ++s) {
-        // Largest head: first the score half of the key, then, among lanes
-        // whose heads tie on it, the expert half (a larger value there is a
-        // lower expert index).
-        const uint32_t hi = (uint32_t)(key[0] >> 32);
-        const uint32_t mhi = wave_max_u32(hi);
-        uint64_t tie = __ballot(hi == mhi);
-        if (__popcll(tie) > 1) {
-            const uint32_t lo = hi == mhi ? (uint32_t)key[0] : 0u;
-            const uint32_t mlo = wave_max_u32(lo);
-            tie = __ballot(hi == mhi && lo == mlo);
-        }
-        const int wlane = __ffsll((unsigned long long)tie) - 1;
-        const uint32_t win = 0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wlane);
-        const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[0]), wlane));
-        const bool mine = lane == wlane;
-        if ((uint32_t)lane == s) {
-            selsc = wsc;
-            selid = win;
-        }
-        if (mine) {
-#pragma unroll
-            for (int i = 0; i < kKeysPerLane - 1; ++i) {
-                key[i] = key[i + 1];
-                score[i] = score[i + 1];
-            }
-            key[kKeysPerLane - 1] = 0;
-        }
-    }
-    // Renormalise in slot order (sequential sums as the reference).
-    float den_f = 0.0f;
-    double den_d = 0.0;
-    for (uint32_t s = 0; s < K; ++s) {
-        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selsc), s));
-        den_f = __fadd_rn(den_f, v);
-        den_d = __dadd_rn(den_d, (double)v);
-    }
-    uint32_t err = 0;
-    if (a.renorm == K3X_RENORM_DOUBLE) {
-        if (!__builtin_isfinite(den_d) || !(den_d > 0.0)) err = K3X_ERR_INVALID_EXTENT;
-    } else if (!__builtin_isfinite(den_f) || !(den_f > 0.0f)) {
-        err = K3X_ERR_INVALID_STATE;
-    }
+    uint32_t selid;
+    float w;
+    const uint32_t err = topk_wave<kKeysPerLane>(lgv, bv, a.E, a.K, a.renorm == K3X_RENORM_DOUBLE,
+                                                 a.routed_scale, &selid, &w);
     if (err) {
         if (lane == 0) {
             latch(a.status, err);
@@ -614,13 +495,10 @@ __device__ void topk_token(const SelectArgs& a, uint32_t t, const float (&lgv)[k
         }
         return;
     }
-    if ((uint32_t)lane < K) {
-        const float w = a.renorm == K3X_RENORM_DOUBLE
-                            ? __fmul_rn((float)__ddiv_rn((double)selsc, den_d), a.routed_scale)
-                            : __fmul_rn(__fdiv_rn(selsc, den_f), a.routed_scale);
-        a.ids[(size_t)t * K + lane] = selid;
-        a.weights[(size_t)t * K + lane] = w;
-        sh.ids[t * K + lane] = selid;
+    if ((uint32_t)lane < a.K) {
+        a.ids[(size_t)t * a.K + lane] = selid;
+        a.weights[(size_t)t * a.K + lane] = w;
+        sh.ids[t * a.K + lane] = selid;
     }
 }
 

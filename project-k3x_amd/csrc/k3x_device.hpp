@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/k3x_hip_moe.h"
+
 namespace k3x_dev {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -98,6 +100,140 @@ __device__ inline float expf_cr(float x) {
 __device__ inline float sigmoid_cr(float v) {
     const float t = __fadd_rn(1.0f, expf_cr(-v));
     return __fdiv_rn(1.0f, t);
+}
+
+// Sort key: larger adjusted score first, then lower expert index
+// (runtime/src/official_moe.cpp:226-232).  -0 folds into +0; 0 = no entry.
+__device__ inline uint64_t topk_key(float adj, uint32_t e) {
+    const float a = adj == 0.0f ? 0.0f : adj;
+    const uint32_t u = __float_as_uint(a);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - e);
+}
+
+// Maximum of v over the 64 lanes with DPP moves (quad permutes, row
+// rotates, row broadcasts): VALU latency instead of LDS-crossbar shuffles.
+// Rows not selected by a row_bcast keep their own value (max(v, v) = v).
+template <int Ctrl, int RowMask>
+__device__ inline uint32_t dpp_max_step(uint32_t x) {
+    const uint32_t y =
+        (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, Ctrl, RowMask, 0xf, false);
+    return x > y ? x : y;
+}
+
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+    v = dpp_max_step<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x124, 0xf>(v);  // row_ror:4
+    v = dpp_max_step<0x128, 0xf>(v);  // row_ror:8
+    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Top-K of one token by one wave, KPL keys per lane (lane + 64 i: expert
+// E + ... absent), given the token's logits lgv and the bias bv of those
+// experts.  Scores, validation and renormalisation as
+// runtime/src/routing_policy.cpp:40-95,146-157 (renorm_double false) or
+// runtime/src/official_moe.cpp:214-242 (true), then * routed_scale
+// (runtime/src/model.cpp:1004-1009).  Each lane sorts its keys; each slot
+// takes the largest head by a DPP wave maximum of the score half of the key
+// (ties on it resolved by a second maximum of the expert half), and the
+// winning lane pops its head.  Returns 0 or the error code (the same on
+// every lane); lane s < K then holds slot s's expert and weight.
+template <int KPL>
+__device__ inline uint32_t topk_wave(const float (&lgv)[KPL], const float (&bv)[KPL], uint32_t E,
+                                     uint32_t K, bool renorm_double, float routed_scale,
+                                     uint32_t* selid_out, float* weight_out) {
+    constexpr uint32_t kErrExtent = K3X_ERR_INVALID_EXTENT, kErrState = K3X_ERR_INVALID_STATE;
+    const int lane = threadIdx.x & 63;
+    uint64_t key[KPL];
+    float score[KPL];
+    uint32_t bad = 0;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+        const uint32_t e = lane + 64u * i;
+        key[i] = 0;
+        score[i] = 0.0f;
+        if (e < E) {
+            const float lg = lgv[i];
+            const float b = bv[i];
+            if (renorm_double && (!__builtin_isfinite(lg) || !__builtin_isfinite(b)))
+                bad = kErrExtent;
+            const float s = sigmoid_cr(lg);
+            const float adj = __fadd_rn(s, b);
+            if (!renorm_double &&
+                (!__builtin_isfinite(s) || s < 0.0f || s > 1.0f || !__builtin_isfinite(b) ||
+                 !__builtin_isfinite(adj)))
+                bad = kErrState;
+            score[i] = s;
+            key[i] = topk_key(adj, e);
+        }
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) bad = max(bad, (uint32_t)__shfl_xor((int)bad, d));
+    if (bad) return bad;
+    // Local selection sort, descending: the lane's head is key[0].
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+#pragma unroll
+        for (int j = i + 1; j < KPL; ++j)
+            if (key[j] > key[i]) {
+                const uint64_t tk = key[i];
+                key[i] = key[j];
+                key[j] = tk;
+                const float ts = score[i];
+                score[i] = score[j];
+                score[j] = ts;
+            }
+    float selsc = 0.0f;  // lane s < K keeps the score of slot s
+    uint32_t selid = 0;
+    for (uint32_t s = 0; s < K; ++s) {
+        // Largest head: first the score half of the key, then, among lanes
+        // whose heads tie on it, the expert half (a larger value there is a
+        // lower expert index).
+        const uint32_t hi = (uint32_t)(key[0] >> 32);
+        const uint32_t mhi = wave_max_u32(hi);
+        uint64_t tie = __ballot(hi == mhi);
+        if (__popcll(tie) > 1) {
+            const uint32_t lo = hi == mhi ? (uint32_t)key[0] : 0u;
+            const uint32_t mlo = wave_max_u32(lo);
+            tie = __ballot(hi == mhi && lo == mlo);
+        }
+        const int wlane = __ffsll((unsigned long long)tie) - 1;
+        const uint32_t win =
+            0xffffffffu - (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wlane);
+        const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[0]), wlane));
+        if ((uint32_t)lane == s) {
+            selsc = wsc;
+            selid = win;
+        }
+        if (lane == wlane) {
+#pragma unroll
+            for (int i = 0; i < KPL - 1; ++i) {
+                key[i] = key[i + 1];
+                score[i] = score[i + 1];
+            }
+            key[KPL - 1] = 0;
+        }
+    }
+    // Renormalise in slot order (sequential sums as the reference).
+    float den_f = 0.0f;
+    double den_d = 0.0;
+    for (uint32_t s = 0; s < K; ++s) {
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selsc), s));
+        den_f = __fadd_rn(den_f, v);
+        den_d = __dadd_rn(den_d, (double)v);
+    }
+    if (renorm_double) {
+        if (!__builtin_isfinite(den_d) || !(den_d > 0.0)) return kErrExtent;
+    } else if (!__builtin_isfinite(den_f) || !(den_f > 0.0f)) {
+        return kErrState;
+    }
+    *selid_out = selid;
+    *weight_out = renorm_double ? __fmul_rn((float)__ddiv_rn((double)selsc, den_d), routed_scale)
+                                : __fmul_rn(__fdiv_rn(selsc, den_f), routed_scale);
+    return 0;
 }
 
 struct GluParams {

@@ -141,14 +141,26 @@ int fill_const_f32_dev(k3x_hip_ctx* ctx, size_t n, float v, float* out);
 // matrix [N/16][K/128][4][64] -> fp32 [T][N]).
 int launch_rmsnorm(k3x_hip_ctx* ctx, const uint16_t* x, const float* gamma, uint32_t T,
                    uint32_t H, float eps, uint16_t* xn);
-int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const uint16_t* xn, uint32_t E,
-                         uint32_t H, uint32_t T, float* logits);
+// Router logits; with the residue-major router copy Wp (router_wp_floats)
+// and router_uses_mfma(H, T), on the matrix cores through xp, a scratch of
+// router_xp_bytes(T) that receives the residue-major copy of xn.
+int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const float* Wp, const uint16_t* xn,
+                         uint16_t* xp, uint32_t E, uint32_t H, uint32_t T, float* logits);
+// The residue-major copy Wp (router_wp_floats(E) floats) of a router [E][H].
+int permute_router_matrix(k3x_hip_ctx* ctx, const float* W, uint32_t E, uint32_t H, float* Wp);
+bool router_uses_mfma(uint32_t H, uint32_t T);
+size_t router_xp_bytes(uint32_t T);
 int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E, uint32_t K,
                 uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids, float* weights);
 int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
                   uint32_t T, const k3x_dev::GluParams& glu, uint16_t* act, hipStream_t stream);
+// Up to kDenseDirectTokens rows the projections run as a split-K GEMV on
+// any stream, and dense_down can round its output to bf16 itself (y_bf16;
+// y is then unused); above, y_bf16 must be null and the narrow GEMM runs on
+// the context stream only.
+constexpr uint32_t kDenseDirectTokens = 16;
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
-               uint32_t T, float* y, hipStream_t stream);
+               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr);
 
 // Whether a bank of this hidden size keeps the residue-major router copy,
 // and that copy's size in floats (experts padded to 16).

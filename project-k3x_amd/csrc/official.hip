@@ -45,11 +45,17 @@ struct k3x_hip_official {
     float* residual_proj = nullptr;  // [H]
     float* post_norm = nullptr;      // [H]
     float* router = nullptr;         // [E][H]
+    float* router_wp = nullptr;      // residue-major copy (H <= 8192; matrix-core router)
     float* correction = nullptr;     // [E]
     bool ffn_ready = false, route_ready = false;
-    // Per-call buffers (grow-only; the bank's forward uses the context scratch).
+    // Per-call buffers (grow-only; the bank's forward uses the context scratch)
+    // and the residue-major copy of hidden for the matrix-core router.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    uint16_t* xp = nullptr;
+    size_t xp_bytes = 0;
+    // The shared FFN runs on the context's side stream between these.
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 };
 
 namespace {
@@ -133,6 +139,81 @@ __global__ __launch_bounds__(kThreads) void official_prepare_kernel(
         out[k] = f32_to_bf16(__fmul_rn(__fmul_rn(s_mix[k], inv2), post_norm[k]));
 }
 
+// The same computation with every row this thread touches in registers
+// (H <= 8192: thread tid holds k = tid + 256 j, j < 32).  All loads are
+// issued before the first sum; loads past the row read 0 through the buffer
+// resource, and their zero terms come after the row's last term, leaving
+// every sum unchanged.
+constexpr uint32_t kPrepRegHidden = 8192;
+
+__global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
+    const float* __restrict__ prefix, const float* __restrict__ residual,
+    const float* __restrict__ res_norm, const float* __restrict__ res_proj,
+    const float* __restrict__ post_norm, uint32_t H, float eps, uint16_t* __restrict__ hidden,
+    uint32_t* status) {
+    __shared__ double red[4];
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x;
+    auto rsrc = [&](const float* base) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, H * 4,
+                                                 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t r0 = rsrc(residual + (size_t)blockIdx.x * H);
+    const __amdgpu_buffer_rsrc_t r1 = rsrc(prefix + (size_t)blockIdx.x * H);
+    const __amdgpu_buffer_rsrc_t rn = rsrc(res_norm), rp = rsrc(res_proj), pn = rsrc(post_norm);
+    float v[2][32], nw[32], pw[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        v[0][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r0, tid * 4, j * 1024, 0));
+        v[1][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r1, tid * 4, j * 1024, 0));
+        nw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rn, tid * 4, j * 1024, 0));
+        pw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, tid * 4, j * 1024, 0));
+    }
+    int bad = 0;
+    float inv[2], score[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        double sq = 0.0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            bad |= !__builtin_isfinite(v[r][j]);
+            v[r][j] = bf16_round(v[r][j]);
+            sq = __builtin_fma((double)v[r][j], (double)v[r][j], sq);
+        }
+        sq = block_sum(sq, red);
+        inv[r] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+        double sc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            sc = sc + ((double)__fmul_rn(v[r][j], inv[r]) * (double)nw[j]) * (double)pw[j];
+        score[r] = (float)block_sum(sc, red);
+    }
+    if (__syncthreads_or(bad)) {
+        if (tid == 0) latch(status, K3X_ERR_INVALID_EXTENT);
+        return;
+    }
+    const float mx = score[0] >= score[1] ? score[0] : score[1];
+    float p0 = expf_cr(__fsub_rn(score[0], mx)), p1 = expf_cr(__fsub_rn(score[1], mx));
+    const float den = __fadd_rn(p0, p1);
+    p0 = __fdiv_rn(p0, den);
+    p1 = __fdiv_rn(p1, den);
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        nw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pn, tid * 4, j * 1024, 0));
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        v[0][j] = bf16_round(__fadd_rn(__fmul_rn(p0, v[0][j]), __fmul_rn(p1, v[1][j])));
+        sq = __builtin_fma((double)v[0][j], (double)v[0][j], sq);
+    }
+    sq = block_sum(sq, red);
+    const float inv2 = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+    uint16_t* out = hidden + (size_t)blockIdx.x * H;
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        if (tid + 256u * j < H) out[tid + 256 * j] = f32_to_bf16(__fmul_rn(__fmul_rn(v[0][j], inv2), nw[j]));
+}
+
 // fp32 values rounded to bf16 in place (synthetic bf16 weights held as fp32).
 __global__ void round_in_place_kernel(float* __restrict__ p, size_t n) {
     const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
@@ -191,8 +272,45 @@ void free_all(k3x_hip_official* o) {
     for (void* p : {(void*)o->routed_down, (void*)o->routed_up, (void*)o->shared_gu,
                     (void*)o->shared_dn, (void*)o->routed_norm, (void*)o->residual_norm,
                     (void*)o->residual_proj, (void*)o->post_norm, (void*)o->router,
-                    (void*)o->correction, o->scratch})
+                    (void*)o->router_wp, (void*)o->correction, o->scratch, (void*)o->xp})
         if (p) (void)hipFree(p);
+    if (o->fork_ev) (void)hipEventDestroy(o->fork_ev);
+    if (o->join_ev) (void)hipEventDestroy(o->join_ev);
+}
+
+// Work of an earlier call may still use the per-call buffers on either stream.
+int drain(k3x_hip_official* o) {
+    k3x_hip_ctx* ctx = o->ctx;
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess ||
+        (ctx->side_stream && hipStreamSynchronize(ctx->side_stream) != hipSuccess))
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    return K3X_OK;
+}
+
+// Router logits of hidden [T][H]: on the matrix cores through the
+// residue-major copies from router_uses_mfma rows on, else the vector kernels
+// (the same canonical fp64 logits either way).
+int route_logits(k3x_hip_official* o, const uint16_t* hidden, uint32_t T, float* logits) {
+    k3x_hip_ctx* ctx = o->ctx;
+    const bool mfma = o->router_wp && k3x_hip::router_uses_mfma(o->H, T);
+    if (mfma) {
+        const size_t need = k3x_hip::router_xp_bytes(T);
+        if (need > o->xp_bytes) {
+            if (drain(o)) return K3X_ERR_BACKEND_UNAVAILABLE;
+            if (o->xp) (void)hipFree(o->xp);
+            o->xp = nullptr;
+            o->xp_bytes = 0;
+            if (alloc(&o->xp, need)) return K3X_ERR_BACKEND_UNAVAILABLE;
+            o->xp_bytes = need;
+        }
+    }
+    return k3x_hip::launch_router_logits(ctx, o->router, mfma ? o->router_wp : nullptr, hidden,
+                                         o->xp, o->E, o->H, T, logits);
+}
+
+int permute(k3x_hip_official* o) {
+    return o->router_wp ? k3x_hip::permute_router_matrix(o->ctx, o->router, o->E, o->H, o->router_wp)
+                        : K3X_OK;
 }
 
 // Upload of a host bf16 matrix [rows][cols] into tiles (matrix `which` of S).
@@ -257,8 +375,7 @@ size_t carve(uint8_t* base, const k3x_hip_official* o, uint32_t T, uint32_t K, F
 
 int ensure(k3x_hip_official* o, size_t bytes) {
     if (bytes <= o->scratch_bytes) return K3X_OK;
-    // Enqueued work of an earlier call may still use the old buffers.
-    if (hipStreamSynchronize(o->ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    if (drain(o)) return K3X_ERR_BACKEND_UNAVAILABLE;
     if (o->scratch) (void)hipFree(o->scratch);
     o->scratch = nullptr;
     o->scratch_bytes = 0;
@@ -309,7 +426,12 @@ int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
     st = st ? st : alloc(&o->residual_proj, (size_t)H * 4);
     st = st ? st : alloc(&o->post_norm, (size_t)H * 4);
     st = st ? st : alloc(&o->router, (size_t)o->E * H * 4);
+    if (k3x_hip::router_mfma_eligible(H))
+        st = st ? st : alloc(&o->router_wp, k3x_hip::router_wp_floats(o->E) * 4);
     st = st ? st : alloc(&o->correction, (size_t)o->E * 4);
+    if (!st && (hipEventCreateWithFlags(&o->fork_ev, hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&o->join_ev, hipEventDisableTiming) != hipSuccess))
+        st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (st) {
         free_all(o);
         delete o;
@@ -323,7 +445,7 @@ int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
 int k3x_hip_official_destroy(k3x_hip_official* o) {
     if (!o) return K3X_ERR_INVALID_EXTENT;
     (void)hipSetDevice(o->ctx->device);
-    (void)hipStreamSynchronize(o->ctx->stream);
+    (void)drain(o);
     free_all(o);
     --o->ctx->live_banks;
     delete o;
@@ -377,6 +499,8 @@ int k3x_hip_official_upload_route(k3x_hip_official* o, const uint16_t* residual_
     if (!st && hipMemcpy(o->correction, correction, (size_t)o->E * 4, hipMemcpyHostToDevice) !=
                    hipSuccess)
         st = K3X_ERR_BACKEND_UNAVAILABLE;
+    st = st ? st : permute(o);
+    if (hipStreamSynchronize(o->ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (!st) o->route_ready = true;
     return st;
 }
@@ -418,6 +542,7 @@ int k3x_hip_official_fill_synthetic(k3x_hip_official* o, uint64_t seed, float si
                            ctx->stream, o->residual_proj, (size_t)o->H);
         st = launched(ctx, 2);
     }
+    st = st ? st : permute(o);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (!st) o->ffn_ready = o->route_ready = true;
     return st;
@@ -430,13 +555,19 @@ int k3x_hip_official_prepare(k3x_hip_ctx* ctx, k3x_hip_official* o, uint32_t T, 
         return K3X_ERR_INVALID_EXTENT;
     if (!std::isfinite(eps) || !(eps > 0.0f)) return K3X_ERR_INVALID_EXTENT;
     if (!o->route_ready) return K3X_ERR_INVALID_STATE;
-    if ((size_t)o->H * 4 > ctx->max_lds_per_block) return K3X_ERR_INVALID_EXTENT;
+    if (o->H > kPrepRegHidden && (size_t)o->H * 4 > ctx->max_lds_per_block)
+        return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    hipLaunchKernelGGL(official_prepare_kernel, dim3(T), dim3(kThreads), (size_t)o->H * 4,
-                       ctx->stream, prefix, block_residual, o->residual_norm, o->residual_proj,
-                       o->post_norm, o->H, eps, hidden, ctx->status);
+    if (o->H <= kPrepRegHidden)
+        hipLaunchKernelGGL(official_prepare_reg_kernel, dim3(T), dim3(kThreads), 0, ctx->stream,
+                           prefix, block_residual, o->residual_norm, o->residual_proj,
+                           o->post_norm, o->H, eps, hidden, ctx->status);
+    else
+        hipLaunchKernelGGL(official_prepare_kernel, dim3(T), dim3(kThreads), (size_t)o->H * 4,
+                           ctx->stream, prefix, block_residual, o->residual_norm,
+                           o->residual_proj, o->post_norm, o->H, eps, hidden, ctx->status);
     int st = launched(ctx, 1);
-    if (!st && logits) st = k3x_hip::launch_router_logits(ctx, o->router, hidden, o->E, o->H, T, logits);
+    if (!st && logits) st = route_logits(o, hidden, T, logits);
     return st;
 }
 
@@ -457,22 +588,66 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     if (st) return st;
     carve(static_cast<uint8_t*>(o->scratch), o, T, K, &b);
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
+    // Shared FFN on hidden (official_moe.cpp:105-117, :307): on the side
+    // stream beside the route and the experts when the projections run as
+    // GEMVs (few rows: the routed kernels leave the device half idle), joined
+    // before the output; in line otherwise.
+    const bool side = o->I_s && T <= k3x_hip::kDenseDirectTokens && ctx->side_stream &&
+                      !ctx->profiling;
+    struct Join {
+        k3x_hip_official* o;
+        bool armed = false;
+        int join() {
+            if (!armed) return K3X_OK;
+            armed = false;
+            return hipStreamWaitEvent(o->ctx->stream, o->join_ev, 0) == hipSuccess
+                       ? K3X_OK
+                       : K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        ~Join() { (void)join(); }
+    } joiner{o};
+    auto shared_ffn = [&](hipStream_t stream) {
+        int r = k3x_hip::dense_gate_up(ctx, o->shared_gu, o->I_s, o->H, hidden, T, glu, b.sact,
+                                       stream);
+        return r ? r : k3x_hip::dense_down(ctx, o->shared_dn, o->H, o->I_s, b.sact, T, b.shared,
+                                           stream);
+    };
+    if (side) {
+        if (hipEventRecord(o->fork_ev, ctx->stream) != hipSuccess ||
+            hipStreamWaitEvent(ctx->side_stream, o->fork_ev, 0) != hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        const int sst = shared_ffn(ctx->side_stream);
+        if (hipEventRecord(o->join_ev, ctx->side_stream) != hipSuccess) {
+            (void)hipStreamSynchronize(ctx->side_stream);
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        joiner.armed = true;
+        if (sst) return sst;
+    }
     // Route (official_moe.cpp:211-269): logits over hidden, sigmoid +
     // correction, natural Top-K, contributions s / sum s in double.
     if (!ids) {
-        st = k3x_hip::launch_router_logits(ctx, o->router, hidden, o->E, o->H, T, b.logits);
+        st = route_logits(o, hidden, T, b.logits);
         st = st ? st : k3x_hip::launch_topk(ctx, b.logits, o->correction, o->E, K, T, 1.0f,
                                             K3X_RENORM_DOUBLE, b.ids, b.contrib);
         if (st) return st;
         ids = b.ids;
         contributions = b.contrib;
     }
-    // latent = bf16(routed_down . hidden) (official_moe.cpp:305).
-    st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, b.latent_f32, ctx->stream);
-    if (st) return st;
-    hipLaunchKernelGGL(round_bf16_kernel, dim3(blocks_for((size_t)T * o->L)), dim3(kThreads), 0,
-                       ctx->stream, b.latent_f32, (size_t)T * o->L, b.latent);
-    if ((st = launched(ctx, 1))) return st;
+    // latent = bf16(routed_down . hidden) (official_moe.cpp:305); few rows
+    // round in the GEMV's own epilogue.
+    if (T <= k3x_hip::kDenseDirectTokens) {
+        st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, nullptr, ctx->stream,
+                                 b.latent);
+        if (st) return st;
+    } else {
+        st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, b.latent_f32,
+                                 ctx->stream);
+        if (st) return st;
+        hipLaunchKernelGGL(round_bf16_kernel, dim3(blocks_for((size_t)T * o->L)), dim3(kThreads),
+                           0, ctx->stream, b.latent_f32, (size_t)T * o->L, b.latent);
+        if ((st = launched(ctx, 1))) return st;
+    }
     // Experts on the latent: the bank's grouped path, each expert output
     // rounded to bf16 before the slot-ordered mix, the mix rounded
     // (official_moe.cpp:82-103, :313-326).
@@ -489,13 +664,8 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon, b.normed);
     st = st ? st : k3x_hip::dense_down(ctx, o->routed_up, o->H, o->L, b.normed, T, b.routed,
                                        ctx->stream);
-    // Shared FFN on hidden (official_moe.cpp:105-117, :307).
-    if (!st && o->I_s) {
-        st = k3x_hip::dense_gate_up(ctx, o->shared_gu, o->I_s, o->H, hidden, T, glu, b.sact,
-                                    ctx->stream);
-        st = st ? st : k3x_hip::dense_down(ctx, o->shared_dn, o->H, o->I_s, b.sact, T, b.shared,
-                                           ctx->stream);
-    }
+    if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
+    st = st ? st : joiner.join();
     if (st) return st;
     const size_t n = (size_t)T * o->H;
     hipLaunchKernelGGL(official_out_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream,

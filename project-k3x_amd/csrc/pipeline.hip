@@ -46,6 +46,24 @@ __device__ inline double block_tree_sum(double v, double* red) {
 // ---------------------------------------------------------------------------
 constexpr uint32_t kNormRegHidden = 8192;  // rows up to this stay in registers
 
+// Tile- and residue-major copy for router_mfma_kernel of token t's row held
+// as b[j] = x[tid + 256 j] (bf16 bits, 0 past the row): j = 4m + q goes to
+// slot 8q + m of the token's 32 terms of residue tid in its 16-token tile.
+__device__ inline void store_xp(uint16_t* xp, uint32_t t, uint32_t tid, const uint32_t (&b)[32]) {
+    u32x4* dst = reinterpret_cast<u32x4*>(xp + ((size_t)(t / 16) * 256 + tid) * (16 * 32) +
+                                          (t % 16) * 32);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int s0 = 8 * c + 2 * h, s1 = s0 + 1;  // slots -> j = 4m + q
+            w[h] = b[4 * (s0 % 8) + s0 / 8] | b[4 * (s1 % 8) + s1 / 8] << 16;
+        }
+        dst[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const float* __restrict__ gamma,
                                                       uint32_t H, float eps,
@@ -110,22 +128,20 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int j = 0; j < 32; ++j)
         if (tid + 256u * j < H) out[tid + 256 * j] = (uint16_t)b[j];
-    if (!xp) return;
-    // Tile- and residue-major copy for router_mfma_kernel: k = tid + 256 j
-    // with j = 4m + q goes to slot 8q + m of this token's 32 terms of
-    // residue tid in its 16-token tile.
-    u32x4* dst = reinterpret_cast<u32x4*>(
-        xp + ((size_t)(blockIdx.x / 16) * 256 + tid) * (16 * 32) + (blockIdx.x % 16) * 32);
+    if (xp) store_xp(xp, blockIdx.x, tid, b);
+}
+
+// The residue-major copy of a bf16 row [H <= 8192] for router_mfma_kernel,
+// one 256-thread block per token (inputs the router did not normalise).
+__global__ __launch_bounds__(256) void xp_pack_kernel(const uint16_t* __restrict__ x, uint32_t H,
+                                                      uint16_t* __restrict__ xp) {
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(x + (size_t)blockIdx.x * H), (short)0, H * 2, 0x00020000);
+    uint32_t b[32];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        uint32_t w[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int s0 = 8 * c + 2 * h, s1 = s0 + 1;  // slots -> j = 4m + q
-            w[h] = b[4 * (s0 % 8) + s0 / 8] | b[4 * (s1 % 8) + s1 / 8] << 16;
-        }
-        dst[c] = u32x4{w[0], w[1], w[2], w[3]};
-    }
+    for (int j = 0; j < 32; ++j)
+        b[j] = __builtin_amdgcn_raw_buffer_load_b16(xs, threadIdx.x * 2, j * 512, 0);
+    store_xp(xp, blockIdx.x, threadIdx.x, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -175,6 +191,74 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ W
         const int i = threadIdx.x, a = i / TPB, b = i % TPB;
         if (e0 + a < E && t0 + b < T)
             logits[(size_t)(t0 + b) * E + e0 + a] =
+                (float)((red[0][i] + red[1][i]) + (red[2][i] + red[3][i]));
+    }
+}
+
+// The same logits for H <= 8192 and T <= TPB with every load a thread needs
+// -- its 32 residue terms of EPB expert rows and of the TPB token rows --
+// issued before the first multiply-add (the loop above waits on each step's
+// loads in turn).  Buffer loads: rows and terms past the ends read 0, and
+// their +0 terms come after the last real one, leaving each partial
+// unchanged (a partial started at +0 is never -0).
+template <int EPB, int TPB>
+__global__ __launch_bounds__(256) void router_reg_kernel(const float* __restrict__ W,
+                                                         const uint16_t* __restrict__ xn,
+                                                         uint32_t E, uint32_t H, uint32_t T,
+                                                         float* __restrict__ logits,
+                                                         const uint32_t* status) {
+    __shared__ double red[4][EPB * TPB];
+    if (*(volatile const uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x, e0 = blockIdx.x * EPB;
+    float w[EPB][32];
+    uint32_t xb[TPB][32];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a) {
+        const uint32_t e = min(e0 + a, E - 1);
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(W + (size_t)e * H), (short)0, e0 + a < E ? H * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            w[a][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, tid * 4, j * 1024, 0));
+    }
+#pragma unroll
+    for (int b = 0; b < TPB; ++b) {
+        const uint32_t t = min((uint32_t)b, T - 1);
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(xn + (size_t)t * H), (short)0, (uint32_t)b < T ? H * 2 : 0,
+            0x00020000);
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            xb[b][j] = __builtin_amdgcn_raw_buffer_load_b16(r, tid * 2, j * 512, 0);
+    }
+    double acc[EPB][TPB];
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) acc[a][b] = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+#pragma unroll
+        for (int a = 0; a < EPB; ++a)
+#pragma unroll
+            for (int b = 0; b < TPB; ++b)
+                acc[a][b] = __builtin_fma((double)w[a][j], (double)bf16_to_f32((uint16_t)xb[b][j]),
+                                          acc[a][b]);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int a = 0; a < EPB; ++a)
+#pragma unroll
+        for (int b = 0; b < TPB; ++b) {
+            double v = acc[a][b];
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+            if (lane == 0) red[wave][a * TPB + b] = v;
+        }
+    __syncthreads();
+    if (threadIdx.x < EPB * TPB) {
+        const int i = threadIdx.x, a = i / TPB, b = i % TPB;
+        if (e0 + a < E && (uint32_t)b < T)
+            logits[(size_t)b * E + e0 + a] =
                 (float)((red[0][i] + red[1][i]) + (red[2][i] + red[3][i]));
     }
 }
@@ -456,16 +540,6 @@ __global__ __launch_bounds__(64 * WPB) void router_mfma_kernel(const float* __re
     }
 }
 
-// Sort key: larger adjusted score first, then lower expert index
-// (runtime/src/official_moe.cpp:226-232).  -0 is folded into +0 so that the
-// two compare equal as floats do.  Taken/absent entries are key 0.
-__device__ inline uint64_t topk_key(float adj, uint32_t e) {
-    const float a = adj == 0.0f ? 0.0f : adj;
-    const uint32_t u = __float_as_uint(a);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - e);
-}
-
 // ---------------------------------------------------------------------------
 // Top-K: one wave per token.  Scores, validation and renormalisation follow
 // runtime/src/routing_policy.cpp:40-95,146-157 (FLOAT) or
@@ -545,6 +619,39 @@ __global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logi
             ids[(size_t)t * K + s] = sel[s];
             weights[(size_t)t * K + s] = __fmul_rn(__fdiv_rn(selsc[s], den), routed_scale);
         }
+    }
+}
+
+// The same Top-K with each lane's keys in registers (E <= 64 KPL): one wave
+// per token, topk_wave's sorted lane lists and DPP wave maxima; every logit
+// and bias load is issued before the status check.
+template <int KPL>
+__global__ __launch_bounds__(64) void topk_reg_kernel(const float* __restrict__ logits,
+                                                      const float* __restrict__ bias, uint32_t E,
+                                                      uint32_t K, float routed_scale,
+                                                      uint32_t renorm, uint32_t* __restrict__ ids,
+                                                      float* __restrict__ weights,
+                                                      uint32_t* status) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x;
+    float lv[KPL], bv[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+        const uint32_t e = min(lane + 64u * i, E - 1);
+        lv[i] = logits[(size_t)t * E + e];
+        bv[i] = bias[e];
+    }
+    if (*(volatile uint32_t*)status) return;
+    uint32_t selid;
+    float w;
+    const uint32_t err =
+        topk_wave<KPL>(lv, bv, E, K, renorm == K3X_RENORM_DOUBLE, routed_scale, &selid, &w);
+    if (err) {
+        if (lane == 0) latch(status, err);
+        return;
+    }
+    if (lane < K) {
+        ids[(size_t)t * K + lane] = selid;
+        weights[(size_t)t * K + lane] = w;
     }
 }
 
@@ -942,6 +1049,90 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                     }
                 }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Dense bf16 projection of a few rows (T <= 16) in the bank's tile layout:
+// one workgroup of kGemvWaves waves per 16 output rows (S = 2: 16 gate + 16
+// up rows); wave w takes the K tiles w, w + kGemvWaves, ..., with D tiles of
+// weight loads issued per step (indices clamped, activations of steps past
+// the last tile zeroed, so no load sits behind a branch).  The waves'
+// accumulators are summed in wave order through LDS.  Activations: lane l
+// reads token l % 16 (clamped to the last token and zeroed past it).
+// OUT: 0 fp32 y, 1 bf16 y, 2 bf16 GLU(gate, up) (S == 2).
+// ---------------------------------------------------------------------------
+constexpr int kGemvWaves = 16;
+constexpr uint32_t kGemvMaxTokens = k3x_hip::kDenseDirectTokens;
+
+struct GemvArgs {
+    const uint4* tiles;   // [N/16][kt][S][4][64]
+    uint32_t kt;          // K tiles
+    const uint16_t* x;    // [T][x_stride] bf16
+    uint32_t x_stride;
+    uint32_t tokens;
+    void* out;            // [T][out_stride]
+    uint32_t out_stride;
+    GluParams glu;
+    const uint32_t* status;
+};
+
+template <int S, int D, int OUT>
+__global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a) {
+    __shared__ f32x4 part[kGemvWaves][S][64];
+    if (*(volatile const uint32_t*)a.status) return;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const uint4* wt = a.tiles + (size_t)blockIdx.x * a.kt * S * 256 + lane;
+    const uint32_t row = min((uint32_t)n, a.tokens - 1);
+    const bool live_row = (uint32_t)n < a.tokens;
+    const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + 32 * g);
+    f32x4 acc[S];
+#pragma unroll
+    for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t k0 = wave; k0 < a.kt; k0 += kGemvWaves * D) {
+        uint4 b[D][S][4], xa[D][4];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const uint32_t k = min(k0 + d * kGemvWaves, a.kt - 1);
+#pragma unroll
+            for (int w = 0; w < S; ++w)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xa[d][j] = xr[(size_t)k * 16 + j];
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const bool live = live_row && k0 + d * kGemvWaves < a.kt;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 xv = live ? xa[d][j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int w = 0; w < S; ++w)
+                    acc[w] = mfma16x16x32(as_bf16x8(xv), as_bf16x8(b[d][w][j]), acc[w]);
+            }
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < S; ++w) part[wave][w][lane] = acc[w];
+    __syncthreads();
+    // Thread 16 t + c finishes output (t, c): lane 16 (t / 4) + c, element
+    // t % 4 of every wave's accumulator, summed in wave order.
+    const uint32_t t = threadIdx.x / 16, c = threadIdx.x % 16;
+    if (t >= a.tokens) return;
+    const uint32_t pl = 16 * (t / 4) + c, pi = t % 4;
+    float v[S];
+#pragma unroll
+    for (int w = 0; w < S; ++w) {
+        v[w] = part[0][w][pl][pi];
+#pragma unroll
+        for (int q = 1; q < kGemvWaves; ++q) v[w] = __fadd_rn(v[w], part[q][w][pl][pi]);
+    }
+    const size_t at = (size_t)t * a.out_stride + (size_t)blockIdx.x * 16 + c;
+    if constexpr (OUT == 0) static_cast<float*>(a.out)[at] = v[0];
+    else if constexpr (OUT == 1) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(v[0]);
+    else static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(glu(v[0], v[S - 1], a.glu));
 }
 
 // ---------------------------------------------------------------------------
@@ -1446,6 +1637,72 @@ int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_para
     return K3X_OK;
 }
 
+// Router logits of T rows of xn: router_mfma_kernel when the residue-major
+// router copy Wp is given (xp then already holds, or -- pack -- is made to
+// hold, the residue-major copy of xn), the register kernel for up to four
+// rows of at most kRouterMaxHidden, else the loop or tile kernel.  All of
+// them produce the same canonical fp64 logits.
+int launch_router(k3x_hip_ctx* ctx, const float* W, const float* Wp, const uint16_t* xn,
+                  uint16_t* xp, uint32_t E, uint32_t H, uint32_t T, float* logits,
+                  bool pack = false) {
+    if (Wp) {
+        if (H > kRouterMaxHidden) return K3X_ERR_INVALID_EXTENT;
+        if (pack)
+            hipLaunchKernelGGL(xp_pack_kernel, dim3(T), dim3(256), 0, ctx->stream, xn, H, xp);
+        const dim3 grid((E + 15) / 16, (T + 15) / 16);
+        const uint32_t nm = (H + 4 * kRouterRes - 1) / (4 * kRouterRes);
+        switch (nm) {
+#define K3X_ROUTER_NM(n)                                                                        \
+    case n:                                                                                     \
+        hipLaunchKernelGGL((router_mfma_kernel<n, kRouterWaves>), grid, dim3(64 * kRouterWaves), \
+                           0, ctx->stream, Wp, xp, E, T, logits, ctx->status);                  \
+        break;
+            K3X_ROUTER_NM(1) K3X_ROUTER_NM(2) K3X_ROUTER_NM(3) K3X_ROUTER_NM(4)
+            K3X_ROUTER_NM(5) K3X_ROUTER_NM(6) K3X_ROUTER_NM(7) K3X_ROUTER_NM(8)
+#undef K3X_ROUTER_NM
+            default: return K3X_ERR_INVALID_EXTENT;
+        }
+        return launched(ctx, pack ? 2 : 1);
+    }
+    if (T <= 4 && H <= kRouterMaxHidden) {
+        const dim3 grid((E + 1) / 2);
+        if (T == 1)
+            hipLaunchKernelGGL((router_reg_kernel<2, 1>), grid, dim3(256), 0, ctx->stream, W, xn,
+                               E, H, T, logits, ctx->status);
+        else if (T == 2)
+            hipLaunchKernelGGL((router_reg_kernel<2, 2>), grid, dim3(256), 0, ctx->stream, W, xn,
+                               E, H, T, logits, ctx->status);
+        else
+            hipLaunchKernelGGL((router_reg_kernel<2, 4>), grid, dim3(256), 0, ctx->stream, W, xn,
+                               E, H, T, logits, ctx->status);
+    } else if (T <= 4) {
+        hipLaunchKernelGGL((router_kernel<1, 4>), dim3(E, 1), dim3(256), 0, ctx->stream, W, xn, E,
+                           H, T, logits, ctx->status);
+    } else {
+        hipLaunchKernelGGL((router_tile_kernel<kRouterEpb, kRouterTpb, 4>),
+                           dim3((E + kRouterEpb - 1) / kRouterEpb, (T + kRouterTpb - 1) / kRouterTpb),
+                           dim3(256), 0, ctx->stream, W, xn, E, H, T, logits, ctx->status);
+    }
+    return launched(ctx, 1);
+}
+
+// Top-K of T rows of logits: the register kernel up to 1024 experts.
+int launch_topk_any(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E,
+                    uint32_t K, uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids,
+                    float* weights) {
+#define K3X_TOPK(kpl)                                                                          \
+    hipLaunchKernelGGL(topk_reg_kernel<kpl>, dim3(T), dim3(64), 0, ctx->stream, logits, bias, E, \
+                       K, routed_scale, renorm, ids, weights, ctx->status)
+    if (E <= 256) K3X_TOPK(4);
+    else if (E <= 512) K3X_TOPK(8);
+    else if (E <= 1024) K3X_TOPK(16);
+#undef K3X_TOPK
+    else
+        hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)E * 12, ctx->stream, logits,
+                           bias, E, K, routed_scale, renorm, ids, weights, ctx->status);
+    return launched(ctx, 1);
+}
+
 int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, Scratch* s) {
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, s);
@@ -1459,13 +1716,17 @@ int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, S
 
 namespace k3x_hip {
 
+int permute_router_matrix(k3x_hip_ctx* ctx, const float* W, uint32_t E, uint32_t H, float* Wp) {
+    const size_t n = router_wp_floats(E);
+    hipLaunchKernelGGL(permute_router_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       ctx->stream, W, E, H, Wp);
+    return launched(ctx, 1);
+}
+
 int permute_router(k3x_hip_bank* bank) {
     const auto& d = bank->desc;
     if (!bank->router_wp) return K3X_OK;
-    const size_t n = router_wp_floats(d.experts);
-    hipLaunchKernelGGL(permute_router_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       bank->ctx->stream, bank->router_w, d.experts, d.hidden, bank->router_wp);
-    return launched(bank->ctx, 1);
+    return permute_router_matrix(bank->ctx, bank->router_w, d.experts, d.hidden, bank->router_wp);
 }
 
 bool router_mfma_eligible(uint32_t hidden) { return hidden <= kRouterMaxHidden; }
@@ -1477,23 +1738,22 @@ int launch_rmsnorm(k3x_hip_ctx* ctx, const uint16_t* x, const float* gamma, uint
     return launched(ctx, 1);
 }
 
-int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const uint16_t* xn, uint32_t E,
-                         uint32_t H, uint32_t T, float* logits) {
-    if (T <= 4)
-        hipLaunchKernelGGL((router_kernel<1, 4>), dim3(E, 1), dim3(256), 0, ctx->stream, W, xn, E,
-                           H, T, logits, ctx->status);
-    else
-        hipLaunchKernelGGL((router_tile_kernel<kRouterEpb, kRouterTpb, 4>),
-                           dim3((E + kRouterEpb - 1) / kRouterEpb, (T + kRouterTpb - 1) / kRouterTpb),
-                           dim3(256), 0, ctx->stream, W, xn, E, H, T, logits, ctx->status);
-    return launched(ctx, 1);
+int launch_router_logits(k3x_hip_ctx* ctx, const float* W, const float* Wp, const uint16_t* xn,
+                         uint16_t* xp, uint32_t E, uint32_t H, uint32_t T, float* logits) {
+    return launch_router(ctx, W, Wp, xn, xp, E, H, T, logits, true);
+}
+
+bool router_uses_mfma(uint32_t H, uint32_t T) {
+    return H <= kRouterMaxHidden && T >= kRouterMfmaMinTokens;
+}
+
+size_t router_xp_bytes(uint32_t T) {
+    return (size_t)(T + 15) / 16 * kRouterRes * kRouterTileRes * 2;
 }
 
 int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E, uint32_t K,
                 uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids, float* weights) {
-    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)E * 12, ctx->stream, logits, bias,
-                       E, K, routed_scale, renorm, ids, weights, ctx->status);
-    return launched(ctx, 1);
+    return launch_topk_any(ctx, logits, bias, E, K, T, routed_scale, renorm, ids, weights);
 }
 
 // Dense bf16 projections in the bank's tile layout: the wide grouped GEMM
@@ -1523,6 +1783,12 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
         g.status = ctx->status;
         return launch_wide_gemm(ctx, kWideSharedGateUp, g, (T + kWideRows - 1) / kWideRows, stream);
     }
+    if (T <= kGemvMaxTokens) {
+        GemvArgs g{tiles, H / 128, x, H, T, act, I, glu, ctx->status};
+        hipLaunchKernelGGL((dense_gemv_kernel<2, 2, 2>), dim3(I / 16), dim3(64 * kGemvWaves), 0,
+                           stream, g);
+        return launched(ctx, 1);
+    }
     if (stream != ctx->stream) return K3X_ERR_INVALID_EXTENT;
     GemmArgs g{};
     g.codes = reinterpret_cast<const uint8_t*>(tiles);
@@ -1540,8 +1806,19 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
 }
 
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
-               uint32_t T, float* y, hipStream_t stream) {
+               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16) {
     if (!T || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
+    if (T <= kGemvMaxTokens) {
+        GemvArgs g{tiles, K / 128, a, K, T, y_bf16 ? (void*)y_bf16 : (void*)y, N, {}, ctx->status};
+        if (y_bf16)
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
+                               stream, g);
+        else
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
+                               stream, g);
+        return launched(ctx, 1);
+    }
+    if (y_bf16) return K3X_ERR_INVALID_EXTENT;
     if (dense_wide_ok(kWideSharedDown, N, K, T)) {
         WideGemmArgs g{};
         g.codes = reinterpret_cast<const uint8_t*>(tiles);
@@ -1613,36 +1890,13 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, bank->gamma,
                        d.hidden, p->rms_epsilon, s.xn, mfma_router ? s.xp : nullptr,
                        ctx->status);
-    if (mfma_router) {
-        const dim3 grid((d.experts + 15) / 16, (T + 15) / 16);
-        const uint32_t nm = (d.hidden + 4 * kRouterRes - 1) / (4 * kRouterRes);
-        switch (nm) {
-#define K3X_ROUTER_NM(n)                                                                        \
-    case n:                                                                                     \
-        hipLaunchKernelGGL((router_mfma_kernel<n, kRouterWaves>), grid, dim3(64 * kRouterWaves), \
-                           0, ctx->stream, bank->router_wp, s.xp, d.experts, T, s.logits,       \
-                           ctx->status);                                                        \
-        break;
-            K3X_ROUTER_NM(1) K3X_ROUTER_NM(2) K3X_ROUTER_NM(3) K3X_ROUTER_NM(4)
-            K3X_ROUTER_NM(5) K3X_ROUTER_NM(6) K3X_ROUTER_NM(7) K3X_ROUTER_NM(8)
-#undef K3X_ROUTER_NM
-            default: return K3X_ERR_INVALID_EXTENT;
-        }
-    } else if (T <= 4) {
-        hipLaunchKernelGGL((router_kernel<1, 4>), dim3(d.experts, 1), dim3(256), 0, ctx->stream,
-                           bank->router_w, s.xn, d.experts, d.hidden, T, s.logits, ctx->status);
-    } else {
-        hipLaunchKernelGGL((router_tile_kernel<kRouterEpb, kRouterTpb, 4>),
-                           dim3((d.experts + kRouterEpb - 1) / kRouterEpb,
-                                (T + kRouterTpb - 1) / kRouterTpb),
-                           dim3(256), 0, ctx->stream, bank->router_w, s.xn, d.experts, d.hidden,
-                           T, s.logits, ctx->status);
-    }
-    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(64), (size_t)d.experts * 12, ctx->stream,
-                       s.logits, bank->router_bias, d.experts, K, p->routed_scale, p->renorm,
-                       s.ids, s.weights, ctx->status);
+    st = launch_router(ctx, bank->router_w, mfma_router ? bank->router_wp : nullptr, s.xn, s.xp,
+                       d.experts, d.hidden, T, s.logits);
+    st = st ? st : launch_topk_any(ctx, s.logits, bank->router_bias, d.experts, K, T,
+                                   p->routed_scale, p->renorm, s.ids, s.weights);
+    if (st) return st;
     k3x_hip::end_stage(ctx, mark);
-    if ((st = launched(ctx, 3))) return st;
+    if ((st = launched(ctx, 1))) return st;
     if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr)))
         return st;
     ++ctx->forward_calls;

@@ -360,6 +360,25 @@ def test_router_shapes(hip, oracle, T, H, E):
     bank.close()
 
 
+# Few tokens on the general path: the register router (one, two and four
+# token rows; the loop kernel past 8192 hidden) and the register Top-K (8 and
+# 16 keys per lane; the LDS kernel past 1024 experts), all bit-exact.
+@pytest.mark.parametrize("T,H,E", [(1, 1152, 1000), (2, 7168, 600), (3, 8192, 300),
+                                   (4, 7168, 1030), (2, 8320, 700)],
+                         ids=["t1", "t2", "t3", "t4_e1030", "t2_h8320"])
+def test_router_few_tokens(hip, oracle, T, H, E):
+    from synth import Config, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = Config(f"route_{T}_{H}_{E}", T, H, 128, E, 8, 0, 119, 123, routed_scale=2.5)
+    say(f"few-token route T={T} H={H} E={E}")
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    x = layer.x_bits()
+    got = run_layer(k3x_amd, ctx, cfg, bank, x, k3x_amd.FLAG_GENERAL_PATH, per_pair=False)
+    check_routing(oracle, layer, got, x)
+    bank.close()
+
+
 @pytest.fixture(scope="module")
 def c3(hip, oracle):
     from synth import CONFIGS, SynthLayer

@@ -80,12 +80,16 @@ def build(k3x_amd, ctx, oracle, shape, seed):
 
 # (H, L, I, Is, E): the second shape puts routed_down and the shared FFN on
 # the wide grouped GEMM from 128 tokens; the third has no shared FFN.
+# The fourth has enough experts for the 16-keys-per-lane Top-K.  Few rows
+# run the projections as split-K GEMVs with the shared FFN on the side
+# stream, 300 rows the router on the matrix cores.
 SHAPES = {"small": (256, 128, 128, 128, 8), "wide": (1024, 512, 512, 512, 16),
-          "no_shared": (512, 256, 256, 0, 12)}
+          "no_shared": (512, 256, 256, 0, 12), "many": (256, 128, 128, 128, 600)}
 
 
 @pytest.mark.parametrize("name,T,K", [("small", 1, 4), ("small", 5, 3), ("wide", 2, 8),
-                                      ("wide", 160, 8), ("no_shared", 33, 4)])
+                                      ("wide", 160, 8), ("no_shared", 33, 4), ("many", 2, 8),
+                                      ("small", 300, 4)])
 def test_official_layer(hip, oracle, name, T, K):
     k3x_amd, ctx = hip
     H, L, I, Is, E = SHAPES[name]
