@@ -940,6 +940,8 @@ struct GemmArgs {
     const uint32_t* status;
 };
 
+constexpr int kGemmDepth = 4;  // K steps in flight per wave of a one-row-tile GEMM
+
 template <bool FP4, bool GATEUP, int MT, int NT>
 __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
     if (*(volatile const uint32_t*)a.status) return;
@@ -979,53 +981,63 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 #pragma unroll
                 for (int w = 0; w < S; ++w) acc[mt][nt][w] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        for (uint32_t k = 0; k < a.kt; ++k) {
-            uint4 bt[NT][S][U];
-            float sc[NT][S];
+        // One row tile: D K steps of loads issued together (steps past the
+        // last tile clamped, their activations zeroed), since a lone step's
+        // round trip would bound the wave.
+        constexpr int D = MT == 1 ? kGemmDepth : 1;
+        for (uint32_t k0 = 0; k0 < a.kt; k0 += D) {
+            uint4 bt[D][NT][S][U];
+            float sc[D][NT][S];
+            bf16x8 af[D][MT][4];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int w = 0; w < S; ++w) {
-                    const size_t base = (((size_t)(rb0 + nt) * a.kt + k) * S + w) * U * 64 + lane;
-#pragma unroll
-                    for (int u = 0; u < U; ++u) bt[nt][w][u] = codes[base + u * 64];
-                    if constexpr (FP4) {
-                        const uint32_t sw =
-                            scales[(((size_t)(rb0 + nt) * a.ks + k / 4) * S + w) * 64 + lane];
-                        sc[nt][w] = e8m0_to_f32((sw >> (8 * (k & 3))) & 0xffu);
-                    }
-                }
-            bf16x8 af[MT][4];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                if (arow[mt]) {
-                    const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)k * 128);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) af[mt][j] = as_bf16x8(p[j]);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) af[mt][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int d = 0; d < D; ++d) {
+                const uint32_t k = min(k0 + d, a.kt - 1);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                     for (int w = 0; w < S; ++w) {
-                        bf16x8 b;
-                        if constexpr (FP4) {
-                            const uint4 c = bt[nt][w][0];
-                            const uint32_t word = j == 0 ? c.x : j == 1 ? c.y : j == 2 ? c.z : c.w;
-                            b = dequant8(word, sc[nt][w]);
-                        } else {
-                            b = as_bf16x8(bt[nt][w][j]);
-                        }
+                        const size_t base = (((size_t)(rb0 + nt) * a.kt + k) * S + w) * U * 64 + lane;
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt)
-                            acc[mt][nt][w] = mfma16x16x32(af[mt][j], b, acc[mt][nt][w]);
+                        for (int u = 0; u < U; ++u) bt[d][nt][w][u] = codes[base + u * 64];
+                        if constexpr (FP4) {
+                            const uint32_t sw =
+                                scales[(((size_t)(rb0 + nt) * a.ks + k / 4) * S + w) * 64 + lane];
+                            sc[d][nt][w] = e8m0_to_f32((sw >> (8 * (k & 3))) & 0xffu);
+                        }
                     }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    if (arow[mt] && k0 + d < a.kt) {
+                        const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)k * 128);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) af[d][mt][j] = as_bf16x8(p[j]);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) af[d][mt][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
+                    }
+                }
             }
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                        for (int w = 0; w < S; ++w) {
+                            bf16x8 b;
+                            if constexpr (FP4) {
+                                const uint4 c = bt[d][nt][w][0];
+                                const uint32_t word = j == 0 ? c.x : j == 1 ? c.y : j == 2 ? c.z : c.w;
+                                b = dequant8(word, sc[d][nt][w]);
+                            } else {
+                                b = as_bf16x8(bt[d][nt][w][j]);
+                            }
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt)
+                                acc[mt][nt][w] = mfma16x16x32(af[d][mt][j], b, acc[mt][nt][w]);
+                        }
+                }
         }
 
 #pragma unroll
@@ -1083,10 +1095,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a)
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const uint4* wt = a.tiles + (size_t)blockIdx.x * a.kt * S * 256 + lane;
     const uint32_t row = min((uint32_t)n, a.tokens - 1);
     const bool live_row = (uint32_t)n < a.tokens;
     const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + 32 * g);
+    const uint32_t rb = blockIdx.x;
+    const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
     f32x4 acc[S];
 #pragma unroll
     for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1129,7 +1142,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a)
 #pragma unroll
         for (int q = 1; q < kGemvWaves; ++q) v[w] = __fadd_rn(v[w], part[q][w][pl][pi]);
     }
-    const size_t at = (size_t)t * a.out_stride + (size_t)blockIdx.x * 16 + c;
+    const size_t at = (size_t)t * a.out_stride + (size_t)rb * 16 + c;
     if constexpr (OUT == 0) static_cast<float*>(a.out)[at] = v[0];
     else if constexpr (OUT == 1) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(v[0]);
     else static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(glu(v[0], v[S - 1], a.glu));
@@ -1810,12 +1823,13 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
     if (!T || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
     if (T <= kGemvMaxTokens) {
         GemvArgs g{tiles, K / 128, a, K, T, y_bf16 ? (void*)y_bf16 : (void*)y, N, {}, ctx->status};
+        const dim3 grid(N / 16);
         if (y_bf16)
-            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
-                               stream, g);
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), grid, dim3(64 * kGemvWaves), 0, stream,
+                               g);
         else
-            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
-                               stream, g);
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0>), grid, dim3(64 * kGemvWaves), 0, stream,
+                               g);
         return launched(ctx, 1);
     }
     if (y_bf16) return K3X_ERR_INVALID_EXTENT;
