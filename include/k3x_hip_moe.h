@@ -320,8 +320,12 @@ int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids,
 typedef struct k3x_hip_official k3x_hip_official;
 
 typedef struct k3x_hip_official_desc {
-    uint32_t hidden;        /* H, multiple of 128 */
-    uint32_t shared_inter;  /* Is, 0 (none) or a multiple of 128 */
+    uint32_t hidden;          /* H, multiple of 128 */
+    uint32_t shared_inter;    /* Is, 0 (none) or a multiple of 128 */
+    uint32_t router_experts;  /* rows of the router: 0 (the bank's experts) with
+                                 a bank; without one (a route-only object:
+                                 uploads of the route and prepare only;
+                                 shared_inter 0), the router's row count */
 } k3x_hip_official_desc;
 
 /* Optional device buffers for intermediates of k3x_hip_official_ffn (any may
@@ -338,7 +342,11 @@ typedef struct k3x_hip_official_taps {
 } k3x_hip_official_taps;
 
 /* experts: a bank of hidden L (its own shared expert unused); the official
- * layer keeps a reference to it and must be destroyed first. */
+ * layer keeps a reference to it and must be destroyed first.  experts NULL
+ * makes a route-only object (desc->router_experts rows): upload_route,
+ * fill_synthetic and prepare work on it, upload_ffn and ffn return
+ * K3X_ERR_INVALID_STATE -- route preparation needs no experts, as
+ * prepare_official_moe_route (backend.hpp:384-389) takes none. */
 int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
                             const k3x_hip_official_desc* desc,
                             k3x_hip_official** out);

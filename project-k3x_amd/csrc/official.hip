@@ -403,10 +403,14 @@ extern "C" {
 
 int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
                             const k3x_hip_official_desc* desc, k3x_hip_official** out) {
-    if (!ctx || !experts || !desc || !out || experts->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    if (!ctx || !desc || !out || (experts && experts->ctx != ctx)) return K3X_ERR_INVALID_EXTENT;
     *out = nullptr;
-    const uint32_t H = desc->hidden, Is = desc->shared_inter, L = experts->desc.hidden;
-    if (!H || H % 128 || Is % 128 || L % 128) return K3X_ERR_INVALID_EXTENT;
+    // Without a bank: a route-only object (prepare and its router logits).
+    const uint32_t H = desc->hidden, Is = desc->shared_inter, L = experts ? experts->desc.hidden : 0;
+    const uint32_t E = experts ? experts->desc.experts : desc->router_experts;
+    if (!H || H % 128 || Is % 128 || L % 128 || !E) return K3X_ERR_INVALID_EXTENT;
+    if (experts ? desc->router_experts && desc->router_experts != E : Is != 0)
+        return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     auto* o = new (std::nothrow) k3x_hip_official();
     if (!o) return K3X_ERR_BACKEND_UNAVAILABLE;
@@ -414,7 +418,7 @@ int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
     o->bank = experts;
     o->H = H;
     o->L = L;
-    o->E = experts->desc.experts;
+    o->E = E;
     o->I_s = Is;
     int st = K3X_OK;
     st = st ? st : alloc(&o->routed_down, (size_t)L * H * 2);
@@ -437,7 +441,7 @@ int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
         delete o;
         return st;
     }
-    ++experts->ctx->live_banks;  // keeps the context alive as a bank would
+    ++ctx->live_banks;  // keeps the context alive as a bank would
     *out = o;
     return K3X_OK;
 }
@@ -457,6 +461,7 @@ int k3x_hip_official_upload_ffn(k3x_hip_official* o, const uint16_t* routed_down
                                 const uint16_t* shared_gate, const uint16_t* shared_up,
                                 const uint16_t* shared_down) {
     if (!o || !routed_down || !routed_norm || !routed_up) return K3X_ERR_INVALID_EXTENT;
+    if (!o->bank) return K3X_ERR_INVALID_STATE;
     const size_t HL = (size_t)o->H * o->L, HS = (size_t)o->H * o->I_s;
     if (o->I_s && (!shared_gate || !shared_up || !shared_down)) return K3X_ERR_INVALID_EXTENT;
     // Validation before any device write (the reference's views are finite bf16).
@@ -513,10 +518,14 @@ int k3x_hip_official_fill_synthetic(k3x_hip_official* o, uint64_t seed, float si
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     auto key = [&](uint64_t stream) { return stream_key(seed, stream << 32); };
     // Streams of this generator: 1..4 dense, 5..7 vectors, 8 router, 9 correction.
-    int st = k3x_hip::retile_bf16_matrix(ctx, nullptr, key(1), sigma, o->L, o->H, 1, 0,
+    int st = K3X_OK;
+    if (o->bank) {
+        st = k3x_hip::retile_bf16_matrix(ctx, nullptr, key(1), sigma, o->L, o->H, 1, 0,
                                          o->routed_down);
-    st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(2), sigma, o->H, o->L, 1, 0,
-                                               o->routed_up);
+        st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(2), sigma, o->H, o->L, 1, 0,
+                                                   o->routed_up);
+        st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->L, 1.0f, o->routed_norm);
+    }
     if (o->I_s) {
         st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(3), sigma, o->I_s, o->H, 2,
                                                    0, o->shared_gu);
@@ -525,7 +534,6 @@ int k3x_hip_official_fill_synthetic(k3x_hip_official* o, uint64_t seed, float si
         st = st ? st : k3x_hip::retile_bf16_matrix(ctx, nullptr, key(5), sigma, o->H, o->I_s, 1,
                                                    0, o->shared_dn);
     }
-    st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->L, 1.0f, o->routed_norm);
     st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->H, 1.0f, o->residual_norm);
     st = st ? st : k3x_hip::fill_const_f32_dev(ctx, o->H, 1.0f, o->post_norm);
     st = st ? st : k3x_hip::fill_normal_f32_dev(ctx, key(6), o->H, proj_sigma, o->residual_proj);
@@ -544,7 +552,10 @@ int k3x_hip_official_fill_synthetic(k3x_hip_official* o, uint64_t seed, float si
     }
     st = st ? st : permute(o);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
-    if (!st) o->ffn_ready = o->route_ready = true;
+    if (!st) {
+        o->ffn_ready = o->bank != nullptr;
+        o->route_ready = true;
+    }
     return st;
 }
 

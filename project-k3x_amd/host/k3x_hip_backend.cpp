@@ -98,12 +98,52 @@ struct HipMoeBackend::Impl {
     };
     Dev xn, ids, w, out, out_f32, pairs;
 
+    // Official layer: per layer, a route-only object for the preparation;
+    // per (layer, H, L, I, Is), the FFN object over a bank of latent experts.
+    // Dense weights are uploaded again when a tensor id or its host data
+    // changes.
+    struct WeightKey {
+        std::uint64_t id = 0;
+        const void* data = nullptr;
+        bool operator==(const WeightKey&) const = default;
+    };
+    struct OfficialRoute {
+        k3x_hip_official* obj = nullptr;
+        std::size_t H = 0, E = 0;
+        WeightKey keys[4];
+    };
+    struct OfficialFfn {
+        Bank bank;
+        k3x_hip_official* obj = nullptr;
+        WeightKey keys[6];
+    };
+    std::map<std::uint32_t, OfficialRoute> official_routes;
+    std::map<std::tuple<std::uint32_t, std::size_t, std::size_t, std::size_t, std::size_t>,
+             OfficialFfn>
+        official_ffns;
+    // The pending prepared token and its device hidden (bf16) and prefix.
+    bool prepared_active = false;
+    std::uint64_t prepared_generation = 0;
+    std::uint32_t prepared_layer = 0;
+    std::size_t prepared_width = 0;
+    Dev prep_prefix, prep_block, prep_hidden, prep_logits, o_hidden, o_prefix, o_ids, o_contrib,
+        o_out;
+
     ~Impl() {
+        for (auto& kv : official_ffns) {
+            k3x_hip_official_destroy(kv.second.obj);
+            k3x_hip_bank_destroy(kv.second.bank.bank);
+        }
+        for (auto& kv : official_routes) k3x_hip_official_destroy(kv.second.obj);
         for (auto& kv : banks) k3x_hip_bank_destroy(kv.second.bank);
-        for (Dev* d : {&xn, &ids, &w, &out, &out_f32, &pairs})
+        for (Dev* d : {&xn, &ids, &w, &out, &out_f32, &pairs, &prep_prefix, &prep_block,
+                       &prep_hidden, &prep_logits, &o_hidden, &o_prefix, &o_ids, &o_contrib,
+                       &o_out})
             if (d->p) (void)hipFree(d->p);
         if (ctx) k3x_hip_ctx_destroy(ctx);
     }
+
+    std::uint64_t owner() const { return reinterpret_cast<std::uintptr_t>(this); }
 
     ErrorCode ensure(Dev& d, std::size_t n) {
         if (d.bytes >= n) return ErrorCode::ok;
@@ -519,6 +559,303 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe_tokens(
     }
     ++impl_->stats.calls;
     return R::success(std::move(out));
+}
+
+// ---- official K3 MoE FFN ----------------------------------------------------
+
+namespace {
+
+bool finite_all(std::span<const float> v) {
+    return std::all_of(v.begin(), v.end(), [](float x) { return std::isfinite(x); });
+}
+
+bool finite_bf16_words(std::span<const std::uint16_t> v) {
+    return std::all_of(v.begin(), v.end(), [](std::uint16_t w) { return (w & 0x7f80u) != 0x7f80u; });
+}
+
+// backend_cuda.cu:3763-3768 / :3490-3495.
+bool valid_bf16(const Bf16WeightView& v) {
+    return v.tensor_id && v.rows && v.cols && mul_fits(v.rows, v.cols) &&
+           v.values.size() == v.rows * v.cols;
+}
+
+float bf16_word_to_f32(std::uint16_t w) {
+    const std::uint32_t u = (std::uint32_t)w << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+}  // namespace
+
+Result<OfficialMoeRoutePrepareResult> HipMoeBackend::prepare_official_moe_route(
+    std::span<const float> prefix, std::span<const float> block, OfficialMoeRoutePrepareView wv,
+    float epsilon, std::uint32_t layer, ProfilePhase) {
+    using R = Result<OfficialMoeRoutePrepareResult>;
+    Impl& m = *impl_;
+    const std::size_t H = prefix.size();
+    // backend_cuda.cu:3498-3512, :3520-3528, :3561-3568.
+    auto valid_h = [&](const Bf16WeightView& v, std::size_t rows) {
+        return valid_bf16(v) && v.rows == rows && v.cols == H;
+    };
+    if (prefix.empty() || prefix.size() != block.size() || !finite_all(prefix) ||
+        !finite_all(block) || !std::isfinite(epsilon) || epsilon <= 0.0f ||
+        !wv.residual_norm.tensor_id || wv.residual_norm.values.size() != H ||
+        !valid_h(wv.residual_proj, 1) || !wv.post_norm.tensor_id ||
+        wv.post_norm.values.size() != H || !valid_h(wv.router, wv.router.rows))
+        return R::failure(ErrorCode::invalid_extent);
+    const std::uint64_t tids[4] = {wv.residual_norm.tensor_id, wv.residual_proj.tensor_id,
+                                   wv.post_norm.tensor_id, wv.router.tensor_id};
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < i; ++j)
+            if (tids[i] == tids[j]) return R::failure(ErrorCode::invalid_extent);
+    if (!finite_bf16_words(wv.residual_norm.values) || !finite_bf16_words(wv.residual_proj.values) ||
+        !finite_bf16_words(wv.post_norm.values) || !finite_bf16_words(wv.router.values))
+        return R::failure(ErrorCode::invalid_extent);
+    const std::size_t E = wv.router.rows;
+    if (H % 128 || H > (1u << 20) || E > (1u << 20)) return R::failure(ErrorCode::backend_unavailable);
+    // A new preparation replaces a pending one (backend_cuda.cu:3609-3616).
+    m.prepared_active = false;
+    auto& rt = m.official_routes[layer];
+    if (rt.obj && (rt.H != H || rt.E != E)) {
+        k3x_hip_official_destroy(rt.obj);
+        rt = Impl::OfficialRoute{};
+    }
+    if (!rt.obj) {
+        k3x_hip_official_desc d{};
+        d.hidden = (std::uint32_t)H;
+        d.router_experts = (std::uint32_t)E;
+        if (int st = k3x_hip_official_create(m.ctx, nullptr, &d, &rt.obj)) {
+            rt.obj = nullptr;
+            return R::failure(code_of(st), "official_create");
+        }
+        rt.H = H;
+        rt.E = E;
+    }
+    const Impl::WeightKey keys[4] = {{tids[0], wv.residual_norm.values.data()},
+                                     {tids[1], wv.residual_proj.values.data()},
+                                     {tids[2], wv.post_norm.values.data()},
+                                     {tids[3], wv.router.values.data()}};
+    if (!std::equal(keys, keys + 4, rt.keys)) {
+        const std::vector<float> zero_correction(E, 0.0f);  // the route itself is the caller's
+        std::fill(rt.keys, rt.keys + 4, Impl::WeightKey{});
+        if (int st = k3x_hip_official_upload_route(rt.obj, wv.residual_norm.values.data(),
+                                                   wv.residual_proj.values.data(),
+                                                   wv.post_norm.values.data(),
+                                                   wv.router.values.data(), zero_correction.data()))
+            return R::failure(code_of(st), "official_upload_route");
+        std::copy(keys, keys + 4, rt.keys);
+        m.stats.weight_h2d_bytes += (3 * H + E * H) * 2;
+    }
+    for (auto [d, n] : {std::pair<Impl::Dev*, std::size_t>{&m.prep_prefix, H * 4},
+                        {&m.prep_block, H * 4}, {&m.prep_hidden, H * 2}, {&m.prep_logits, E * 4}})
+        if (ErrorCode c = m.ensure(*d, n); c != ErrorCode::ok) return R::failure(c);
+    if (hipMemcpy(m.prep_prefix.p, prefix.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m.prep_block.p, block.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return R::failure(ErrorCode::backend_unavailable);
+    int st = k3x_hip_official_prepare(m.ctx, rt.obj, 1, epsilon,
+                                      static_cast<const float*>(m.prep_prefix.p),
+                                      static_cast<const float*>(m.prep_block.p),
+                                      static_cast<std::uint16_t*>(m.prep_hidden.p),
+                                      static_cast<float*>(m.prep_logits.p));
+    if (!st) st = k3x_hip_ctx_synchronize(m.ctx);
+    if (st) return R::failure(code_of(st));
+    OfficialMoeRoutePrepareResult r;
+    r.executed = true;
+    r.router_logits.resize(E);
+    if (hipMemcpy(r.router_logits.data(), m.prep_logits.p, E * 4, hipMemcpyDeviceToHost) !=
+            hipSuccess ||
+        !finite_all(r.router_logits))
+        return R::failure(ErrorCode::backend_unavailable);
+    if (!++m.prepared_generation) ++m.prepared_generation;
+    m.prepared_active = true;
+    m.prepared_layer = layer;
+    m.prepared_width = H;
+    r.prepared = {m.owner(), m.prepared_generation};
+    ++m.stats.calls;
+    return R::success(std::move(r));
+}
+
+Result<bool> HipMoeBackend::discard_official_moe_prepared(OfficialMoePreparedToken token) {
+    Impl& m = *impl_;
+    if (!m.prepared_active || token.owner != m.owner() || token.generation != m.prepared_generation)
+        return Result<bool>::failure(ErrorCode::invalid_state);
+    m.prepared_active = false;
+    return Result<bool>::success(true);
+}
+
+Result<OfficialMoeFfnResult> HipMoeBackend::official_mxfp4_moe_ffn(
+    std::span<const float> hidden, std::span<const float> prefix, OfficialMoeFfnView weights,
+    std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+    std::span<const float> contributions, float epsilon, float situ_beta,
+    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    impl_->prepared_active = false;  // backend_cuda.cu:3723-3731
+    return official_ffn(hidden, prefix, std::nullopt, weights, experts, expert_ids, contributions,
+                        epsilon, situ_beta, situ_linear, layer);
+}
+
+Result<OfficialMoeFfnResult> HipMoeBackend::official_mxfp4_moe_ffn_prepared(
+    OfficialMoePreparedToken prepared, OfficialMoeFfnView weights,
+    std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+    std::span<const float> contributions, float epsilon, float situ_beta,
+    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    return official_ffn({}, {}, prepared, weights, experts, expert_ids, contributions, epsilon,
+                        situ_beta, situ_linear, layer);
+}
+
+// Checks as backend_cuda.cu:3769-3880 (invalid_mxfp4 for every rejected
+// argument); shapes the kernels do not run are backend_unavailable.
+Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
+    std::span<const float> hidden, std::span<const float> prefix,
+    std::optional<OfficialMoePreparedToken> prepared, const OfficialMoeFfnView& wv,
+    std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+    std::span<const float> contributions, float epsilon, float beta, std::optional<float> linear,
+    std::uint32_t layer) {
+    using R = Result<OfficialMoeFfnResult>;
+    Impl& m = *impl_;
+    const auto bad = [] { return R::failure(ErrorCode::invalid_mxfp4); };
+    if ((!prepared && (hidden.empty() || hidden.size() != prefix.size())) ||
+        (prepared && (!m.prepared_active || prepared->owner != m.owner() ||
+                      prepared->generation != m.prepared_generation ||
+                      m.prepared_layer != layer || !m.prepared_width)) ||
+        experts.empty() || experts.size() > 65535 || experts.size() != expert_ids.size() ||
+        experts.size() != contributions.size() ||
+        (!prepared && (!finite_all(hidden) || !finite_all(prefix))) ||
+        !finite_all(contributions) || !std::isfinite(epsilon) || epsilon <= 0.0f ||
+        !valid_situ(beta, linear) || !valid_bf16(wv.routed_down) || !valid_bf16(wv.routed_up) ||
+        !valid_bf16(wv.shared.gate) || !valid_bf16(wv.shared.up) || !valid_bf16(wv.shared.down) ||
+        !wv.routed_norm.tensor_id || wv.routed_norm.values.empty())
+        return bad();
+    const std::size_t H = prepared ? m.prepared_width : hidden.size();
+    const std::size_t L = wv.routed_down.rows, I = experts.front().gate.rows,
+                      out_w = experts.front().down.rows, Is = wv.shared.gate.rows;
+    if (wv.routed_down.cols != H || wv.routed_norm.values.size() != out_w ||
+        wv.routed_up.rows != H || wv.routed_up.cols != out_w || wv.shared.gate.cols != H ||
+        wv.shared.up.rows != Is || wv.shared.up.cols != H || wv.shared.down.rows != H ||
+        wv.shared.down.cols != Is)
+        return bad();
+    std::vector<std::uint64_t> tensor_ids;
+    auto insert = [&](std::uint64_t id) {
+        if (!id || std::find(tensor_ids.begin(), tensor_ids.end(), id) != tensor_ids.end())
+            return false;
+        tensor_ids.push_back(id);
+        return true;
+    };
+    if (!insert(wv.routed_down.tensor_id) || !insert(wv.routed_norm.tensor_id) ||
+        !insert(wv.routed_up.tensor_id) || !insert(wv.shared.gate.tensor_id) ||
+        !insert(wv.shared.up.tensor_id) || !insert(wv.shared.down.tensor_id))
+        return bad();
+    double sum = 0.0;
+    for (std::size_t k = 0; k < experts.size(); ++k) {
+        const Mxfp4MlpView& e = experts[k];
+        if (std::count(expert_ids.begin(), expert_ids.begin() + k, expert_ids[k]) ||
+            contributions[k] <= 0.0f || e.gate.cols != L || e.gate.rows != I || e.up.cols != L ||
+            e.up.rows != I || e.down.cols != I || e.down.rows != out_w || e.gate.group_size != 32 ||
+            e.up.group_size != 32 || e.down.group_size != 32 || !valid_mxfp4(L, e.gate) ||
+            !valid_mxfp4(L, e.up) || !valid_mxfp4(I, e.down) || !insert(e.gate.tensor_id) ||
+            !insert(e.up.tensor_id) || !insert(e.down.tensor_id))
+            return bad();
+        sum += contributions[k];
+    }
+    if (std::abs(sum - 1.0) > 1.0e-5) return bad();
+    // The official composition's routed width is the latent (official_moe.cpp:327-333).
+    if (out_w != L) return bad();
+    if (H % 128 || L % 128 || I % 128 || Is % 128 || experts.size() > kMaxSlotsPerToken ||
+        experts.size() > m.opt.resident_experts)
+        return R::failure(ErrorCode::backend_unavailable);
+    if (!finite_bf16_words(wv.routed_down.values) || !finite_bf16_words(wv.routed_up.values) ||
+        !finite_bf16_words(wv.routed_norm.values) || !finite_bf16_words(wv.shared.gate.values) ||
+        !finite_bf16_words(wv.shared.up.values) || !finite_bf16_words(wv.shared.down.values))
+        return bad();
+    if (prepared) m.prepared_active = false;  // consumed (backend_cuda.cu:3875-3878)
+    // The FFN object and its latent experts.
+    const auto key = std::make_tuple(layer, H, L, I, Is);
+    auto it = m.official_ffns.find(key);
+    if (it == m.official_ffns.end()) {
+        Impl::OfficialFfn f;
+        k3x_hip_layer_desc d{};
+        d.hidden = (std::uint32_t)L;
+        d.inter = (std::uint32_t)I;
+        d.experts = m.opt.resident_experts;
+        d.group_size = 32;
+        if (int st = k3x_hip_bank_create(m.ctx, &d, &f.bank.bank))
+            return R::failure(code_of(st), "bank_create");
+        f.bank.slots.resize(m.opt.resident_experts);
+        k3x_hip_official_desc od{};
+        od.hidden = (std::uint32_t)H;
+        od.shared_inter = (std::uint32_t)Is;
+        if (int st = k3x_hip_official_create(m.ctx, f.bank.bank, &od, &f.obj)) {
+            k3x_hip_bank_destroy(f.bank.bank);
+            return R::failure(code_of(st), "official_create");
+        }
+        it = m.official_ffns.emplace(key, std::move(f)).first;
+    }
+    Impl::OfficialFfn& f = it->second;
+    const Impl::WeightKey keys[6] = {
+        {wv.routed_down.tensor_id, wv.routed_down.values.data()},
+        {wv.routed_norm.tensor_id, wv.routed_norm.values.data()},
+        {wv.routed_up.tensor_id, wv.routed_up.values.data()},
+        {wv.shared.gate.tensor_id, wv.shared.gate.values.data()},
+        {wv.shared.up.tensor_id, wv.shared.up.values.data()},
+        {wv.shared.down.tensor_id, wv.shared.down.values.data()}};
+    if (!std::equal(keys, keys + 6, f.keys)) {
+        std::fill(f.keys, f.keys + 6, Impl::WeightKey{});
+        if (int st = k3x_hip_official_upload_ffn(
+                f.obj, wv.routed_down.values.data(), wv.routed_norm.values.data(),
+                wv.routed_up.values.data(), wv.shared.gate.values.data(),
+                wv.shared.up.values.data(), wv.shared.down.values.data()))
+            return R::failure(code_of(st), "official_upload_ffn");
+        std::copy(keys, keys + 6, f.keys);
+        m.stats.weight_h2d_bytes += (2 * L * H + L + 3 * Is * H) * 2;
+    }
+    std::vector<std::uint32_t> slot;
+    if (ErrorCode c = m.admit(f.bank, experts, slot); c != ErrorCode::ok) return R::failure(c);
+    const std::size_t K = experts.size();
+    for (auto [d, n] : {std::pair<Impl::Dev*, std::size_t>{&m.o_ids, K * 4}, {&m.o_contrib, K * 4},
+                        {&m.o_out, H * 2}, {&m.o_hidden, H * 2}, {&m.o_prefix, H * 4}})
+        if (ErrorCode c = m.ensure(*d, n); c != ErrorCode::ok) return R::failure(c);
+    const void* hid = m.prep_hidden.p;
+    const void* pre = m.prep_prefix.p;
+    if (!prepared) {
+        std::vector<std::uint16_t> hb(H);
+        for (std::size_t i = 0; i < H; ++i) hb[i] = to_bf16(hidden[i]);
+        if (hipMemcpy(m.o_hidden.p, hb.data(), H * 2, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(m.o_prefix.p, prefix.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return R::failure(ErrorCode::backend_unavailable);
+        hid = m.o_hidden.p;
+        pre = m.o_prefix.p;
+    }
+    if (hipMemcpy(m.o_ids.p, slot.data(), K * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m.o_contrib.p, contributions.data(), K * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return R::failure(ErrorCode::backend_unavailable);
+    k3x_hip_moe_params p{};
+    p.tokens = 1;
+    p.top_k = (std::uint32_t)K;
+    p.routed_scale = 1.0f;
+    p.rms_epsilon = epsilon;
+    p.glu = K3X_GLU_SITU;
+    p.situ_beta = beta;
+    p.has_situ_linear = linear.has_value();
+    p.situ_linear_beta = linear.value_or(0.0f);
+    p.renorm = K3X_RENORM_DOUBLE;
+    int st = k3x_hip_official_ffn(m.ctx, f.obj, &p, static_cast<const std::uint16_t*>(hid),
+                                  static_cast<const float*>(pre),
+                                  static_cast<const std::uint32_t*>(m.o_ids.p),
+                                  static_cast<const float*>(m.o_contrib.p),
+                                  static_cast<std::uint16_t*>(m.o_out.p), nullptr);
+    if (!st) st = k3x_hip_ctx_synchronize(m.ctx);
+    if (st) return R::failure(code_of(st));
+    std::vector<std::uint16_t> ob(H);
+    if (hipMemcpy(ob.data(), m.o_out.p, H * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return R::failure(ErrorCode::backend_unavailable);
+    OfficialMoeFfnResult r;
+    r.executed = true;
+    r.output.resize(H);
+    for (std::size_t i = 0; i < H; ++i) r.output[i] = bf16_word_to_f32(ob[i]);
+    r.selected_expert_ids.assign(expert_ids.begin(), expert_ids.end());
+    ++m.stats.calls;
+    ++m.stats.layer_calls;
+    return R::success(std::move(r));
 }
 
 HipBackendStats HipMoeBackend::runtime_stats() const noexcept {

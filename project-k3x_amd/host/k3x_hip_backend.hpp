@@ -106,6 +106,58 @@ struct Mxfp4MlpView {
     Mxfp4WeightView down;
 };
 
+// bf16 views of the official layer (backend.hpp:138-148, :165-176, :184-189):
+// values are bf16 words, row-major [rows][cols].
+struct Bf16WeightView {
+    std::span<const std::uint16_t> values;
+    std::size_t rows{};
+    std::size_t cols{};
+    std::uint64_t tensor_id{};
+};
+
+struct Bf16VectorView {
+    std::span<const std::uint16_t> values;
+    std::uint64_t tensor_id{};
+};
+
+struct Bf16MlpView {
+    Bf16WeightView gate;
+    Bf16WeightView up;
+    Bf16WeightView down;
+};
+
+struct OfficialMoeFfnView {
+    Bf16WeightView routed_down;
+    Bf16VectorView routed_norm;
+    Bf16WeightView routed_up;
+    Bf16MlpView shared;
+};
+
+struct OfficialMoeFfnResult {
+    bool executed{};
+    std::vector<float> output;
+    std::vector<std::uint32_t> selected_expert_ids;
+};
+
+struct OfficialMoeRoutePrepareView {
+    Bf16VectorView residual_norm;
+    Bf16WeightView residual_proj;
+    Bf16VectorView post_norm;
+    Bf16WeightView router;
+};
+
+struct OfficialMoePreparedToken {
+    std::uint64_t owner{};
+    std::uint64_t generation{};
+    bool operator==(const OfficialMoePreparedToken&) const = default;
+};
+
+struct OfficialMoeRoutePrepareResult {
+    bool executed{};
+    OfficialMoePreparedToken prepared;
+    std::vector<float> router_logits;
+};
+
 struct HipBackendOptions {
     int device = 0;
     // Bank slots per (layer, hidden, intermediate) shape; each slot holds
@@ -165,12 +217,49 @@ public:
         std::span<const float> contributions, float situ_beta, std::optional<float> situ_linear,
         std::uint32_t layer, ProfilePhase phase);
 
+    // The official K3 MoE FFN (Stable LatentMoE) for one token: hidden
+    // (the prepared, bf16-valued hidden; other values are rounded to bf16)
+    // -> routed_down -> the routed experts at the latent width, mixed in
+    // slot order -> routed_norm -> routed_up, plus the shared FFN and the
+    // prefix add (backend.hpp:376-383, official_moe.cpp:271-344).  Any
+    // pending prepared token is dropped.
+    Result<OfficialMoeFfnResult> official_mxfp4_moe_ffn(
+        std::span<const float> hidden, std::span<const float> prefix, OfficialMoeFfnView weights,
+        std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+        std::span<const float> contributions, float rms_epsilon, float situ_beta,
+        std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase);
+    // Route preparation (backend.hpp:384-389, official_moe.cpp:156-209,
+    // :247-269): the two-source mix and post-norm of prefix and
+    // block_residual into the hidden, kept on the device for the prepared
+    // FFN, and the router logits over it (canonical fp64 sums).  The token
+    // names that hidden until it is consumed, discarded or replaced.
+    Result<OfficialMoeRoutePrepareResult> prepare_official_moe_route(
+        std::span<const float> prefix, std::span<const float> block_residual,
+        OfficialMoeRoutePrepareView weights, float rms_epsilon, std::uint32_t layer,
+        ProfilePhase phase);
+    // The FFN on the prepared hidden and prefix (backend.hpp:390-395);
+    // consumes the token.
+    Result<OfficialMoeFfnResult> official_mxfp4_moe_ffn_prepared(
+        OfficialMoePreparedToken prepared, OfficialMoeFfnView weights,
+        std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+        std::span<const float> contributions, float rms_epsilon, float situ_beta,
+        std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase);
+    // Drops the prepared hidden (backend.hpp:396-399): invalid_state unless
+    // the token is the pending one.
+    Result<bool> discard_official_moe_prepared(OfficialMoePreparedToken prepared);
+
     HipBackendStats runtime_stats() const noexcept;
     std::string_view device_name() const noexcept;
 
     struct Impl;
 
 private:
+    Result<OfficialMoeFfnResult> official_ffn(
+        std::span<const float> hidden, std::span<const float> prefix,
+        std::optional<OfficialMoePreparedToken> prepared, const OfficialMoeFfnView& weights,
+        std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
+        std::span<const float> contributions, float rms_epsilon, float situ_beta,
+        std::optional<float> situ_linear, std::uint32_t layer);
     friend Result<std::unique_ptr<HipMoeBackend>> make_hip_backend(const HipBackendOptions&);
     explicit HipMoeBackend(std::unique_ptr<Impl> impl);
     std::unique_ptr<Impl> impl_;

@@ -89,7 +89,8 @@ class OfficialTaps(C.Structure):
 
 
 class OfficialDesc(C.Structure):
-    _fields_ = [("hidden", C.c_uint32), ("shared_inter", C.c_uint32)]
+    _fields_ = [("hidden", C.c_uint32), ("shared_inter", C.c_uint32),
+                ("router_experts", C.c_uint32)]
 
 
 class SynthDesc(C.Structure):
@@ -341,14 +342,18 @@ class Official:
     """The official K3 MoE FFN around a bank of experts at the latent width
     (k3x_hip_official_*); host weights are bf16 words (uint16 numpy arrays)."""
 
-    def __init__(self, ctx: Context, experts: Bank, hidden: int, shared_inter: int):
+    def __init__(self, ctx: Context, experts: Bank | None, hidden: int, shared_inter: int,
+                 router_experts: int = 0):
+        """experts None: a route-only object (upload_route, fill_synthetic,
+        prepare) whose router has router_experts rows."""
         import weakref
         self.ctx, self.lib, self.experts = ctx, ctx.lib, experts
         self.hidden, self.shared_inter = hidden, shared_inter
         h = _vp()
-        d = OfficialDesc(hidden, shared_inter)
-        check(self.lib.k3x_hip_official_create(ctx.handle, experts.handle, C.byref(d),
-                                               C.byref(h)), "k3x_hip_official_create")
+        d = OfficialDesc(hidden, shared_inter, router_experts)
+        check(self.lib.k3x_hip_official_create(ctx.handle, experts.handle if experts else None,
+                                               C.byref(d), C.byref(h)),
+              "k3x_hip_official_create")
         self.handle = h
         if not hasattr(ctx, "_officials"):
             ctx._officials = weakref.WeakSet()

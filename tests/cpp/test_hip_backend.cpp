@@ -108,6 +108,190 @@ bool identical(const std::vector<float>& a, const std::vector<float>& b) {
     return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * 4) == 0;
 }
 
+// ---- official K3 MoE FFN -----------------------------------------------------
+// A small official layer (hidden 256, latent 128, experts of 128, shared FFN
+// of 128, 8 router rows, Top-4) through prepare_official_moe_route and both
+// FFN methods, against the oracle's restatement of official_moe.cpp: logits
+// within 1e-4 of their scale (the device hidden may differ from the oracle's
+// by one bf16 ulp: canonical against sequential sums), the outputs within
+// atol = rtol = 2e-2 (the reference's parity tolerance for this layer); then
+// the prepared-token rules and the reference's rejections.
+constexpr std::size_t OH = 256, OL = 128, OI = 128, OS = 128, OE = 8, OK = 4;
+constexpr float kEps = 1e-5f;
+
+struct LatentExpert {
+    std::vector<std::byte> gp, gs, up, us, dp, ds;
+    std::uint64_t id;
+    Mxfp4MlpView view() const {
+        return {{id, gp, gs, OI, OL, G}, {id + 1, up, us, OI, OL, G}, {id + 2, dp, ds, OL, OI, G}};
+    }
+    const std::uint8_t* ptr(const std::vector<std::byte>& v) const {
+        return reinterpret_cast<const std::uint8_t*>(v.data());
+    }
+};
+
+LatentExpert make_latent_expert(std::uint64_t id) {
+    LatentExpert e;
+    e.id = id;
+    auto codes = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& b : v) b = std::byte(next_u32() & 0xff);
+        return v;
+    };
+    auto scales = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& b : v) b = std::byte(121 + next_u32() % 5);
+        return v;
+    };
+    e.gp = codes(OI * OL / 2);
+    e.gs = scales(OI * OL / G);
+    e.up = codes(OI * OL / 2);
+    e.us = scales(OI * OL / G);
+    e.dp = codes(OL * OI / 2);
+    e.ds = scales(OL * OI / G);
+    return e;
+}
+
+std::vector<std::uint16_t> bf16_normal(std::uint64_t stream, std::size_t n, float sigma) {
+    std::vector<std::uint16_t> v(n);
+    k3xo_synth_normal_bf16(k3xo_stream_key(0x0FF1C1A1ull, stream), n, sigma, v.data());
+    return v;
+}
+
+bool within(const std::vector<float>& got, const std::vector<float>& ref, float atol, float rtol,
+            const char* what) {
+    if (got.size() != ref.size()) {
+        std::printf("%s: size %zu, want %zu\n", what, got.size(), ref.size());
+        return false;
+    }
+    for (std::size_t i = 0; i < ref.size(); ++i)
+        if (!(std::fabs(got[i] - ref[i]) <= atol + rtol * std::fabs(ref[i]))) {
+            std::printf("%s: [%zu] %.9g, oracle %.9g\n", what, i, got[i], ref[i]);
+            return false;
+        }
+    return true;
+}
+
+int official_checks(k3x_amd::HipMoeBackend& be) {
+    using k3x_amd::Bf16VectorView;
+    using k3x_amd::Bf16WeightView;
+    std::vector<std::uint16_t> ones(OH, 0x3F80);  // the norm vectors: 1
+    const auto rp = bf16_normal(2, OH, 0.05f), router = bf16_normal(4, OE * OH, 0.05f);
+    const auto rdown = bf16_normal(5, OL * OH, 0.03f), rup = bf16_normal(6, OH * OL, 0.03f);
+    const auto sg = bf16_normal(7, OS * OH, 0.03f), su = bf16_normal(8, OS * OH, 0.03f),
+               sd = bf16_normal(9, OH * OS, 0.03f);
+    std::vector<std::uint16_t> rnorm(OL, 0x3F80);
+    std::vector<float> correction(OE);
+    k3xo_synth_normal(k3xo_stream_key(0x0FF1C1A1ull, 10), OE, 0.1f, correction.data());
+    std::vector<float> prefix(OH), block(OH);
+    k3xo_synth_normal(k3xo_stream_key(0x0FF1C1A1ull, 11), OH, 1.0f, prefix.data());
+    k3xo_synth_normal(k3xo_stream_key(0x0FF1C1A1ull, 12), OH, 1.0f, block.data());
+    std::vector<LatentExpert> ex;
+    for (std::size_t e = 0; e < OE; ++e) ex.push_back(make_latent_expert(1000 + 10 * e));
+
+    const k3x_amd::OfficialMoeRoutePrepareView rv{
+        Bf16VectorView{ones, 901}, Bf16WeightView{rp, 1, OH, 902}, Bf16VectorView{ones, 903},
+        Bf16WeightView{router, OE, OH, 904}};
+    const k3x_amd::OfficialMoeFfnView fv{
+        Bf16WeightView{rdown, OL, OH, 911}, Bf16VectorView{rnorm, 912},
+        Bf16WeightView{rup, OH, OL, 913},
+        {Bf16WeightView{sg, OS, OH, 914}, Bf16WeightView{su, OS, OH, 915},
+         Bf16WeightView{sd, OH, OS, 916}}};
+
+    // Oracle: hidden, logits, route, layer.
+    std::vector<float> hidden(OH), logits(OE), wf(OE * OH);
+    if (k3xo_official_prepare(prefix.data(), block.data(), OH, ones.data(), rp.data(), ones.data(),
+                              kEps, hidden.data()))
+        return 100;
+    for (std::size_t i = 0; i < wf.size(); ++i) wf[i] = k3xo_bf16_to_f32(router[i]);
+    k3xo_router_logits(wf.data(), hidden.data(), OE, OH, K3XO_ORDER_CANON, logits.data());
+
+    auto prep = be.prepare_official_moe_route(prefix, block, rv, kEps, 3, ProfilePhase::decode);
+    if (!prep || !prep.value().executed) return 101;
+    float lscale = 0.0f;
+    for (float l : logits) lscale = std::fmax(lscale, std::fabs(l));
+    if (!within(prep.value().router_logits, logits, 1e-4f * lscale, 0.0f, "official logits"))
+        return 102;
+    // Route on the host from the backend's logits, as official_layer.cpp:442-446.
+    std::vector<std::uint32_t> ids(OK);
+    std::vector<float> contrib(OK), scores(OE);
+    if (k3xo_route(prep.value().router_logits.data(), correction.data(), OE, OK,
+                   K3XO_RENORM_DOUBLE, 1.0f, K3XO_SIGMOID_REF, ids.data(), contrib.data(),
+                   scores.data()))
+        return 103;
+    std::vector<Mxfp4MlpView> sel;
+    std::vector<const std::uint8_t*> ptrs;
+    for (std::uint32_t id : ids) {
+        sel.push_back(ex[id].view());
+        const LatentExpert& e = ex[id];
+        for (const auto* v : {&e.gp, &e.gs, &e.up, &e.us, &e.dp, &e.ds}) ptrs.push_back(e.ptr(*v));
+    }
+    std::vector<float> want(OH);
+    if (k3xo_official_ffn(hidden.data(), prefix.data(), OH, OL, OI, OS, rdown.data(), rnorm.data(),
+                          rup.data(), sg.data(), su.data(), sd.data(), ptrs.data(), contrib.data(),
+                          OK, kEps, K3XO_GLU_SITU, kBeta, 1, kLinear, nullptr, nullptr, nullptr,
+                          nullptr, nullptr, want.data()))
+        return 104;
+    const auto token = prep.value().prepared;
+    auto moe = be.official_mxfp4_moe_ffn_prepared(token, fv, sel, ids, contrib, kEps, kBeta,
+                                                  kLinear, 3, ProfilePhase::decode);
+    if (!moe || !moe.value().executed || moe.value().selected_expert_ids != ids) return 105;
+    if (!within(moe.value().output, want, 2e-2f, 2e-2f, "official prepared ffn")) return 106;
+    // The token was consumed.
+    if (be.official_mxfp4_moe_ffn_prepared(token, fv, sel, ids, contrib, kEps, kBeta, kLinear, 3,
+                                           ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4 ||
+        be.discard_official_moe_prepared(token).error() != ErrorCode::invalid_state)
+        return 107;
+    // The unprepared method on the oracle's hidden: same bar.
+    auto direct = be.official_mxfp4_moe_ffn(hidden, prefix, fv, sel, ids, contrib, kEps, kBeta,
+                                            kLinear, 3, ProfilePhase::decode);
+    if (!direct || !within(direct.value().output, want, 2e-2f, 2e-2f, "official ffn")) return 108;
+    // A second preparation; discard works once; an unprepared FFN call drops
+    // a pending token; a token from another layer is rejected.
+    auto p2 = be.prepare_official_moe_route(prefix, block, rv, kEps, 3, ProfilePhase::decode);
+    if (!p2 || p2.value().prepared == token) return 109;
+    if (!be.discard_official_moe_prepared(p2.value().prepared) ||
+        be.discard_official_moe_prepared(p2.value().prepared).error() != ErrorCode::invalid_state)
+        return 110;
+    auto p3 = be.prepare_official_moe_route(prefix, block, rv, kEps, 3, ProfilePhase::decode);
+    if (!p3 || !be.official_mxfp4_moe_ffn(hidden, prefix, fv, sel, ids, contrib, kEps, kBeta,
+                                          kLinear, 3, ProfilePhase::decode))
+        return 111;
+    if (be.discard_official_moe_prepared(p3.value().prepared).error() != ErrorCode::invalid_state)
+        return 112;
+    auto p4 = be.prepare_official_moe_route(prefix, block, rv, kEps, 3, ProfilePhase::decode);
+    if (!p4 || be.official_mxfp4_moe_ffn_prepared(p4.value().prepared, fv, sel, ids, contrib, kEps,
+                                                  kBeta, kLinear, 4, ProfilePhase::decode)
+                       .error() != ErrorCode::invalid_mxfp4)
+        return 113;
+    // Rejections (backend_cuda.cu:3769-3880, :3498-3528).
+    std::vector<float> skew = contrib;
+    skew[0] += 0.01f;
+    if (be.official_mxfp4_moe_ffn(hidden, prefix, fv, sel, ids, skew, kEps, kBeta, kLinear, 3,
+                                  ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4)
+        return 114;
+    std::vector<std::uint32_t> dup = ids;
+    dup[1] = dup[0];
+    if (be.official_mxfp4_moe_ffn(hidden, prefix, fv, sel, dup, contrib, kEps, kBeta, kLinear, 3,
+                                  ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4)
+        return 115;
+    std::vector<float> short_block(block.begin(), block.end() - 1);
+    if (be.prepare_official_moe_route(prefix, short_block, rv, kEps, 3, ProfilePhase::decode)
+            .error() != ErrorCode::invalid_extent)
+        return 116;
+    auto rv_dup = rv;
+    rv_dup.router.tensor_id = rv.residual_norm.tensor_id;
+    if (be.prepare_official_moe_route(prefix, block, rv_dup, kEps, 3, ProfilePhase::decode)
+            .error() != ErrorCode::invalid_extent)
+        return 117;
+    std::printf("official: logits, prepared and direct FFN within 2e-2 of the oracle; token rules "
+                "and rejections as the reference\n");
+    return 0;
+}
+
 }  // namespace
 
 int main() {
@@ -294,6 +478,8 @@ int main() {
     if (backend->mxfp4_situ_mlp_group(x32, tiny, kBeta, kLinear, 14, ProfilePhase::decode).error() !=
         ErrorCode::backend_unavailable)
         return 85;
+
+    if (int rc = official_checks(*backend)) return rc;
 
     const auto s = backend->runtime_stats();
     std::printf("ok: %llu calls, %llu layer calls, %llu kernel launches, %llu admitted, %llu hits\n",

@@ -185,3 +185,37 @@ def test_official_layer(hip, oracle, name, T, K):
     assert off.ffn(params, hidden, prefix_d, out2, ids=taps["ids"]) == k3x_amd.ERR_INVALID_EXTENT
     off.close()
     bank.close()
+
+
+def test_route_only_object(hip, oracle):
+    """Without a bank the object prepares exactly as the full one; the FFN
+    methods are rejected as invalid state."""
+    k3x_amd, ctx = hip
+    H, L, I, Is, E = SHAPES["wide"]
+    T = 3
+    say(f"route-only official object H={H} E={E} T={T}")
+    w, experts, bank, off = build(k3x_amd, ctx, oracle, SHAPES["wide"], 5)
+    route = k3x_amd.Official(ctx, None, H, 0, router_experts=E)
+    args = (w["residual_norm"], w["residual_proj"], w["post_norm"], w["router"], w["correction"])
+    assert off.upload_route(*args) == 0 and route.upload_route(*args) == 0
+    dev = "cuda:0"
+    rng = np.random.default_rng(77)
+    prefix = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(dev)
+    residual = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(dev)
+    outs = []
+    for o in (off, route):
+        hidden = torch.empty((T, H), dtype=torch.int16, device=dev)
+        logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+        assert o.prepare(T, EPS, prefix, residual, hidden, logits) == 0
+        outs.append((to_np(hidden), to_np(logits)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    z16 = np.zeros(1, np.uint16)
+    assert route.upload_ffn(z16, z16, z16) == k3x_amd.ERR_INVALID_STATE
+    params = k3x_amd.make_params(T, 4, 1.0, EPS, k3x_amd.GLU_SITU, BETA, LINEAR,
+                                 k3x_amd.RENORM_DOUBLE)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    hidden = torch.empty((T, H), dtype=torch.int16, device=dev)
+    assert route.ffn(params, hidden, prefix, out) == k3x_amd.ERR_INVALID_STATE
+    route.close()
+    off.close()
+    bank.close()
