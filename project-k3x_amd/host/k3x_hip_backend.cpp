@@ -561,6 +561,74 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe_tokens(
     return R::success(std::move(out));
 }
 
+// ---- expert-major verification block -----------------------------------------
+
+Result<ExpertMajorBlockMoe> HipMoeBackend::expert_major_block_moe(
+    std::span<const float> latents, std::size_t positions,
+    std::span<const ExpertMajorTokenRoute> routes, std::span<const Mxfp4MlpView> experts,
+    float situ_beta, std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) {
+    using R = Result<ExpertMajorBlockMoe>;
+    if (routes.empty() || routes.size() != positions) return R::failure(ErrorCode::invalid_extent);
+    ExpertMajorBlockMoe res;
+    std::vector<std::uint32_t> seen;  // distinct experts of the block (the plan's groups)
+    for (const auto& r : routes) {
+        if (r.expert_ids.empty() || r.expert_ids.size() != r.contributions.size())
+            return R::failure(ErrorCode::invalid_extent);
+        for (std::size_t k = 0; k < r.expert_ids.size(); ++k) {
+            if (!std::isfinite(r.contributions[k]) ||
+                std::count(r.expert_ids.begin(), r.expert_ids.begin() + k, r.expert_ids[k]))
+                return R::failure(ErrorCode::invalid_state);
+            if (r.expert_ids[k] >= experts.size()) return R::failure(ErrorCode::invalid_extent);
+            if (std::find(seen.begin(), seen.end(), r.expert_ids[k]) == seen.end())
+                seen.push_back(r.expert_ids[k]);
+            ++res.assignments;
+        }
+    }
+    res.unique_experts = seen.size();
+    const std::size_t width_in = experts[seen.front()].gate.cols;
+    const std::size_t width_out = experts[seen.front()].down.rows;
+    if (!mul_fits(positions, width_in) || latents.size() != positions * width_in)
+        return R::failure(ErrorCode::invalid_mxfp4);
+    res.mixed.assign(positions * width_out, 0.0f);
+    // One grouped call per route width: positions of that width, their
+    // experts as a local list, routes as indices into it.
+    std::vector<std::size_t> widths;
+    for (const auto& r : routes)
+        if (std::find(widths.begin(), widths.end(), r.expert_ids.size()) == widths.end())
+            widths.push_back(r.expert_ids.size());
+    for (const std::size_t K : widths) {
+        std::vector<std::size_t> pos;
+        std::vector<Mxfp4MlpView> local;
+        std::vector<std::uint32_t> local_id, idx;
+        std::vector<float> contrib, in;
+        for (std::size_t p = 0; p < positions; ++p) {
+            if (routes[p].expert_ids.size() != K) continue;
+            pos.push_back(p);
+            in.insert(in.end(), latents.begin() + p * width_in,
+                      latents.begin() + (p + 1) * width_in);
+            for (std::size_t k = 0; k < K; ++k) {
+                const std::uint32_t id = routes[p].expert_ids[k];
+                auto at = std::find(local_id.begin(), local_id.end(), id);
+                if (at == local_id.end()) {
+                    local_id.push_back(id);
+                    local.push_back(experts[id]);
+                    at = local_id.end() - 1;
+                }
+                idx.push_back((std::uint32_t)(at - local_id.begin()));
+                contrib.push_back(routes[p].contributions[k]);
+            }
+        }
+        auto mixed = mxfp4_situ_moe_tokens(in, pos.size(), K, local, idx, contrib, situ_beta,
+                                           situ_linear, layer, phase);
+        if (!mixed) return R::failure(mixed.error(), mixed.message());
+        ++res.layer_calls;
+        for (std::size_t i = 0; i < pos.size(); ++i)
+            std::copy_n(mixed.value().data() + i * width_out, width_out,
+                        res.mixed.data() + pos[i] * width_out);
+    }
+    return R::success(std::move(res));
+}
+
 // ---- official K3 MoE FFN ----------------------------------------------------
 
 namespace {

@@ -158,6 +158,19 @@ struct OfficialMoeRoutePrepareResult {
     std::vector<float> router_logits;
 };
 
+// Same members as k3x::ExpertMajorTokenRoute (expert_major.hpp:12-15).
+struct ExpertMajorTokenRoute {
+    std::vector<std::uint32_t> expert_ids;
+    std::vector<float> contributions;
+};
+
+struct ExpertMajorBlockMoe {
+    std::vector<float> mixed;          // [positions][width]
+    std::uint64_t unique_experts = 0;  // groups of the block's expert-major plan
+    std::uint64_t assignments = 0;     // (position, slot) pairs
+    std::uint64_t layer_calls = 0;     // grouped layer calls made
+};
+
 struct HipBackendOptions {
     int device = 0;
     // Bank slots per (layer, hidden, intermediate) shape; each slot holds
@@ -247,6 +260,25 @@ public:
     // Drops the prepared hidden (backend.hpp:396-399): invalid_state unless
     // the token is the pending one.
     Result<bool> discard_official_moe_prepared(OfficialMoePreparedToken prepared);
+
+    // The routed experts of one layer of an expert-major verification block
+    // (model.cpp:278-345): position p's latent through the experts of
+    // routes[p], mixed in slot order with routes[p].contributions.
+    //   * The reference builds the block's expert-major plan and makes one
+    //     mxfp4_situ_mlp_batch per group. Here the block takes one grouped
+    //     layer call per distinct route width (normally exactly one).
+    //   * experts[id] is the view of expert id.
+    //   * Routes are checked as build_expert_major_plan checks them
+    //     (expert_major.cpp:10-54): invalid_extent for an empty block or
+    //     route, invalid_state for a non-finite contribution or an expert
+    //     twice in one route.
+    //   * unique_experts and assignments are the plan's group and
+    //     assignment counts (model.cpp:279-283).
+    Result<ExpertMajorBlockMoe> expert_major_block_moe(
+        std::span<const float> latents, std::size_t positions,
+        std::span<const ExpertMajorTokenRoute> routes, std::span<const Mxfp4MlpView> experts,
+        float situ_beta, std::optional<float> situ_linear, std::uint32_t layer,
+        ProfilePhase phase);
 
     HipBackendStats runtime_stats() const noexcept;
     std::string_view device_name() const noexcept;

@@ -457,6 +457,49 @@ int main() {
             .error() != ErrorCode::invalid_state)
         return 82;
 
+    // Expert-major verification block (model.cpp:278-345): four positions,
+    // routes by expert id of widths 2, 2, 1, 2 -> two grouped calls; the mix
+    // of each position against the oracle's per-expert outputs mixed in slot
+    // order (the reference's per-group batch + host mix), and the plan's
+    // group and assignment counts.
+    {
+        std::vector<float> xb(4 * H);
+        for (auto& v : xb) v = (float)((int)(next_u32() % 4001) - 2000) / 1000.0f;
+        std::vector<k3x_amd::ExpertMajorTokenRoute> br(4);
+        br[0] = {{2, 0}, {0.75f, 0.25f}};
+        br[1] = {{1, 2}, {0.5f, 0.5f}};
+        br[2] = {{0}, {1.0f}};
+        br[3] = {{0, 1}, {0.125f, 0.875f}};
+        auto blk = backend->expert_major_block_moe(xb, 4, br, three, kBeta, kLinear, 17,
+                                                   ProfilePhase::prefill);
+        if (!blk || blk.value().unique_experts != 3 || blk.value().assignments != 7 ||
+            blk.value().layer_calls != 2 || blk.value().mixed.size() != 4 * H)
+            return 86;
+        const Expert* byid[3] = {&e0, &e1, &e2};
+        for (int p = 0; p < 4; ++p) {
+            std::vector<float> want(H, 0.0f);
+            for (std::size_t k = 0; k < br[p].expert_ids.size(); ++k) {
+                const auto y = oracle_out(*byid[br[p].expert_ids[k]], xb.data() + p * H);
+                for (std::size_t h = 0; h < H; ++h) want[h] += br[p].contributions[k] * y[h];
+            }
+            const std::vector<float> got(blk.value().mixed.begin() + p * H,
+                                         blk.value().mixed.begin() + (p + 1) * H);
+            if (!close_to(got, want, "expert-major block")) return 87;
+        }
+        auto bad = br;
+        bad[1].expert_ids = {2, 2};
+        if (backend->expert_major_block_moe(xb, 4, bad, three, kBeta, kLinear, 17,
+                                            ProfilePhase::prefill)
+                .error() != ErrorCode::invalid_state)
+            return 88;
+        bad = br;
+        bad[2] = {};
+        if (backend->expert_major_block_moe(xb, 4, bad, three, kBeta, kLinear, 17,
+                                            ProfilePhase::prefill)
+                .error() != ErrorCode::invalid_extent)
+            return 89;
+    }
+
     // Residency under pressure: 4 slots, a fifth expert replaces the least
     // recently used one and results stay right.
     const Expert e3 = make_expert(410), e4 = make_expert(413);

@@ -18,6 +18,11 @@ METHODS = ["k3x_amd::make_hip_backend", "k3x_amd::HipMoeBackend::mxfp4_situ_mlp_
            "k3x_amd::HipMoeBackend::mxfp4_situ_mlp_batch",
            "k3x_amd::HipMoeBackend::mxfp4_situ_mlp_grid", "k3x_amd::HipMoeBackend::mxfp4_situ_moe",
            "k3x_amd::HipMoeBackend::mxfp4_situ_moe_tokens",
+           "k3x_amd::HipMoeBackend::expert_major_block_moe",
+           "k3x_amd::HipMoeBackend::official_mxfp4_moe_ffn",
+           "k3x_amd::HipMoeBackend::official_mxfp4_moe_ffn_prepared",
+           "k3x_amd::HipMoeBackend::prepare_official_moe_route",
+           "k3x_amd::HipMoeBackend::discard_official_moe_prepared",
            "k3x_amd::HipMoeBackend::runtime_stats", "k3x_amd::error_code_name"]
 
 
