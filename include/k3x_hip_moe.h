@@ -33,7 +33,16 @@ extern "C" {
 /* k3x::ErrorCode values (runtime/include/k3x/status.hpp:9-31). */
 enum k3x_status {
     K3X_OK = 0,
+    K3X_ERR_IO = 1,
+    K3X_ERR_BAD_MAGIC = 2,
+    K3X_ERR_UNSUPPORTED_VERSION = 3,
+    K3X_ERR_UNSUPPORTED_REQUIRED_FEATURE = 4,
+    K3X_ERR_SUPERBLOCK_CRC_MISMATCH = 6,
+    K3X_ERR_TRUNCATED_FILE = 7,
+    K3X_ERR_INVALID_DIRECTORY = 8,
     K3X_ERR_INVALID_EXTENT = 9,
+    K3X_ERR_DATA_CRC_MISMATCH = 10,
+    K3X_ERR_AUXILIARY_CRC_MISMATCH = 11,
     K3X_ERR_TENSOR_NOT_FOUND = 14,
     K3X_ERR_INVALID_MXFP4 = 15,
     K3X_ERR_INVALID_STATE = 16,
@@ -399,6 +408,55 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* official,
                          const float* prefix, const uint32_t* ids,
                          const float* contributions, uint16_t* out,
                          const k3x_hip_official_taps* taps);
+
+/* ---- K3X storage records -------------------------------------------------- */
+
+/* CRC32C (Castagnoli, reflected, preset and final inversion 0xFFFFFFFF) of
+ * `bytes` device bytes at `data` (16-byte aligned), computed on the device:
+ * the value runtime/src/crc32c.cpp:22-28 computes on the host, for data
+ * already in HBM.  Synchronous (the context stream is drained). */
+int k3x_hip_crc32c(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* crc);
+
+/* Uploads expert `expert` of the bank from six device extents in the K3X
+ * storage order -- gate codes, gate scales, up codes, up scales, down codes,
+ * down scales (runtime/src/storage_slice.cpp:56-73), each 16-byte aligned
+ * and of the bank's sizes -- after checking each against its CRC32C
+ * (crc32c[6] as the tensor records hold them, runtime/src/reader.cpp:98-99;
+ * NULL skips the check): K3X_ERR_DATA_CRC_MISMATCH or
+ * K3X_ERR_AUXILIARY_CRC_MISMATCH, slot untouched, on a mismatch; a scale
+ * byte 0xFF is K3X_ERR_INVALID_MXFP4.  Identities as
+ * k3x_hip_bank_upload_expert.  Synchronous. */
+int k3x_hip_bank_upload_expert_device(k3x_hip_bank* bank, uint32_t expert,
+                                      const uint64_t tensor_ids[3],
+                                      const uint8_t* const extents[6],
+                                      const uint32_t crc32c[6]);
+
+/* A K3X checkpoint opened for expert loads (K3X_FORMAT.md).  Opening reads
+ * and checks the superblock and the directories as Reader::open does
+ * (runtime/src/reader.cpp:414-560): magic, version, superblock CRC32C,
+ * required features, reserved bytes, finalized state and length, directory
+ * ranges and headers, model-config invariants, tensor record fields,
+ * distinct tensor ids; every tensor extent in range, 4 KiB aligned and
+ * disjoint from the others.  Status codes are the reader's (K3X_ERR_IO ..
+ * K3X_ERR_INVALID_EXTENT).  The directory and root SHA-256 digests are not
+ * checked. */
+typedef struct k3x_hip_storage k3x_hip_storage;
+int k3x_hip_storage_open(const char* path, k3x_hip_storage** out);
+int k3x_hip_storage_close(k3x_hip_storage* storage);
+
+/* load_storage_expert (runtime/src/storage_slice.cpp:42-92) into bank slot
+ * `expert`: the tensors model.layers.<layer>.feed_forward.experts.<id>.
+ * {gate,up,down}, found by the FNV-1a 64 hash of their names, must be
+ * native MXFP4 matrices of the bank's shape (gate/up [inter][hidden], down
+ * [hidden][inter]; K3X_ERR_INVALID_MXFP4) of that layer and expert; the
+ * artifact must carry the STORAGE_FIXTURE optional feature
+ * (K3X_ERR_INVALID_EXTENT otherwise).  The six extents are read in one batch
+ * into pinned host memory, copied to the device once, checked against their
+ * records' CRC32C on the device and uploaded with
+ * k3x_hip_bank_upload_expert_device; the slot's tensor ids are the records'.
+ * *bytes_read (may be NULL): the six extents' total.  Synchronous. */
+int k3x_hip_storage_upload_expert(k3x_hip_storage* storage, k3x_hip_bank* bank, uint32_t expert,
+                                  uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read);
 
 #ifdef __cplusplus
 }

@@ -749,3 +749,26 @@ void k3xo_synth_normal_bf16(uint64_t key, size_t n, float sigma,
                             uint16_t* out) {
     for (size_t i = 0; i < n; ++i) out[i] = k3xo_bf16_bits(normal_at(key, i, sigma));
 }
+
+/* ---- K3X storage records ------------------------------------------------- */
+/* runtime/src/crc32c.cpp:6-28 computes a byte table from the reflected
+ * Castagnoli polynomial and folds each byte; this restatement shifts one bit
+ * at a time (the definition the table tabulates). */
+uint32_t k3xo_crc32c(const uint8_t* data, size_t n) {
+    uint32_t crc = 0xffffffffu;
+    for (size_t i = 0; i < n; ++i) {
+        crc ^= data[i];
+        for (int b = 0; b < 8; ++b) crc = (crc >> 1) ^ (0x82f63b78u & (0u - (crc & 1u)));
+    }
+    return ~crc;
+}
+
+/* runtime/src/reader.cpp:405-412. */
+uint64_t k3xo_fnv1a64(const char* name) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (; *name; ++name) {
+        h ^= (unsigned char)*name;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}

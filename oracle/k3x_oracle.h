@@ -149,6 +149,13 @@ void k3xo_synth_normal(uint64_t key, size_t n, float sigma, float* out);
 void k3xo_synth_normal_bf16(uint64_t key, size_t n, float sigma,
                             uint16_t* out);
 
+/* ---- K3X storage records --------------------------------------------------*/
+/* CRC32C (Castagnoli, reflected polynomial 0x82F63B78, register preset and
+ * final inversion 0xFFFFFFFF), bit at a time: runtime/src/crc32c.cpp:6-28. */
+uint32_t k3xo_crc32c(const uint8_t* data, size_t n);
+/* FNV-1a 64 of a NUL-terminated name: runtime/src/reader.cpp:405-412. */
+uint64_t k3xo_fnv1a64(const char* name);
+
 #ifdef __cplusplus
 }
 #endif

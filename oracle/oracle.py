@@ -64,6 +64,10 @@ class Oracle:
         if not os.path.exists(path):
             raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
         L = self.lib = C.CDLL(path)
+        L.k3xo_crc32c.restype = C.c_uint32
+        L.k3xo_crc32c.argtypes = [_u8p, _sz]
+        L.k3xo_fnv1a64.restype = C.c_uint64
+        L.k3xo_fnv1a64.argtypes = [C.c_char_p]
         L.k3xo_round_bf16.restype = C.c_float
         L.k3xo_round_bf16.argtypes = [C.c_float]
         L.k3xo_expf_cr.restype = C.c_float
@@ -301,6 +305,14 @@ class Oracle:
                                       int(linear is not None), linear or 0.0, _p(out, _f32p))
         return out
 
+    def crc32c(self, data) -> int:
+        """CRC32C of a bytes-like object (runtime/src/crc32c.cpp:22-28)."""
+        a = np.frombuffer(bytes(data), dtype=np.uint8)
+        return int(self.lib.k3xo_crc32c(_p(np.ascontiguousarray(a), _u8p), a.size))
+
+    def fnv1a64(self, name: str) -> int:
+        return int(self.lib.k3xo_fnv1a64(name.encode()))
+
     def official_ffn(self, hidden, prefix, weights, experts, contributions, eps,
                      glu=GLU_SITU, beta=4.0, linear=25.0):
         """One token.  weights: dict of bf16-word arrays routed_down [L][H],
@@ -379,6 +391,8 @@ class RefLib:
         if not os.path.exists(path):
             raise FileNotFoundError(path)
         L = self.lib = C.CDLL(path)
+        L.k3xr_crc32c.restype = C.c_uint32
+        L.k3xr_crc32c.argtypes = [_u8p, _sz]
         L.k3xr_decode_mxfp4.argtypes = [_u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
         L.k3xr_mxfp4_matvec.argtypes = [_f32p, _sz, _u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
         L.k3xr_rms_norm.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
@@ -533,6 +547,10 @@ class RefLib:
         del keep
         return st, ids, out
 
+
+    def crc32c(self, data) -> int:
+        a = np.frombuffer(bytes(data), dtype=np.uint8)
+        return int(self.lib.k3xr_crc32c(_p(np.ascontiguousarray(a), _u8p), a.size))
 
     def official_moe(self, prefix, residual, weights, experts, top_k, eps, beta=4.0,
                      linear=25.0):

@@ -6,6 +6,7 @@
 // in place under /root/reference) into oracle/_ref/libk3x_ref.so.  Tests use
 // it to pin the C restatement in k3x_oracle.c; bench.py may time it as the
 // CPU baseline.  Nothing from the reference is copied into this repository.
+#include "k3x/checksums.hpp"
 #include "k3x/backend.hpp"
 #include "k3x/expert_major.hpp"
 #include "k3x/official_moe.hpp"
@@ -62,6 +63,15 @@ k3x::Mxfp4MlpView expert_view(const ExpertBytes& e, std::size_t hidden,
 }
 
 }  // namespace
+
+extern "C" {
+
+// runtime/src/crc32c.cpp:22-28.
+std::uint32_t k3xr_crc32c(const std::uint8_t* data, std::size_t n) {
+    return k3x::crc32c(std::as_bytes(std::span<const std::uint8_t>(data, n)));
+}
+
+}  // extern "C"
 
 extern "C" {
 

@@ -235,6 +235,12 @@ int retile_shared(k3x_hip_bank* b, const uint16_t* src[3], uint64_t seed, float 
 
 namespace k3x_hip {
 
+int retile_expert_device(k3x_hip_bank* b, uint32_t e, const uint8_t* const src[6]) {
+    const uint8_t* s[6];
+    for (int i = 0; i < 6; ++i) s[i] = src[i];
+    return retile_expert(b, e, s, 0, 0, 1);
+}
+
 int retile_bf16_matrix(k3x_hip_ctx* ctx, const uint16_t* src, uint64_t key, float sigma,
                        uint32_t rows, uint32_t cols, uint32_t S, uint32_t which, uint4* dst) {
     const size_t n = (size_t)(rows / 16) * (cols / 128) * 256;
@@ -401,6 +407,7 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->status) (void)hipFree(ctx->status);
+    k3x_hip::free_crc(ctx);
     for (const StageMark& m : ctx->pending) {
         (void)hipEventDestroy(m.start);
         (void)hipEventDestroy(m.stop);
@@ -597,6 +604,51 @@ int k3x_hip_bank_upload_expert(k3x_hip_bank* bank, uint32_t expert, const uint64
     for (int m = 0; m < 3; ++m) bank->tensor_ids[tensor_ids[m]] = expert * 4 + (uint32_t)m;
     bank->expert_ready[expert] = 1;
     ctx->weight_h2d_bytes += 3 * (pbytes + sbytes);
+    return K3X_OK;
+}
+
+int k3x_hip_bank_upload_expert_device(k3x_hip_bank* bank, uint32_t expert,
+                                      const uint64_t tensor_ids[3],
+                                      const uint8_t* const extents[6], const uint32_t crc32c[6]) {
+    if (!bank || !tensor_ids || !extents) return K3X_ERR_INVALID_MXFP4;
+    const auto& d = bank->desc;
+    if (expert >= d.experts) return K3X_ERR_INVALID_MXFP4;
+    for (int i = 0; i < 6; ++i)
+        if (!extents[i] || reinterpret_cast<uintptr_t>(extents[i]) % 16) return K3X_ERR_INVALID_EXTENT;
+    for (int m = 0; m < 3; ++m) {
+        if (!tensor_ids[m]) return K3X_ERR_INVALID_MXFP4;
+        for (int q = 0; q < m; ++q)
+            if (tensor_ids[q] == tensor_ids[m]) return K3X_ERR_INVALID_MXFP4;
+        auto it = bank->tensor_ids.find(tensor_ids[m]);
+        if (it != bank->tensor_ids.end() && it->second != expert * 4 + (uint32_t)m)
+            return K3X_ERR_INVALID_MXFP4;
+    }
+    k3x_hip_ctx* ctx = bank->ctx;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    const size_t n = (size_t)d.inter * d.hidden;
+    const size_t len[6] = {n / 2, n / 32, n / 2, n / 32, n / 2, n / 32};
+    // Integrity and validity before the slot is touched.
+    for (int i = 0; i < 6; ++i) {
+        if (crc32c) {
+            uint32_t c = 0;
+            if (int st = k3x_hip::crc32c_device(ctx, extents[i], len[i], &c)) return st;
+            if (c != crc32c[i])
+                return i % 2 ? K3X_ERR_AUXILIARY_CRC_MISMATCH : K3X_ERR_DATA_CRC_MISMATCH;
+        }
+        if (i % 2) {
+            bool ff = false;
+            if (int st = k3x_hip::any_ff_device(ctx, extents[i], len[i], &ff)) return st;
+            if (ff) return K3X_ERR_INVALID_MXFP4;
+        }
+    }
+    bank->expert_ready[expert] = 0;
+    for (auto it = bank->tensor_ids.begin(); it != bank->tensor_ids.end();)
+        it = it->second / 4 == expert ? bank->tensor_ids.erase(it) : std::next(it);
+    int st = k3x_hip::retile_expert_device(bank, expert, extents);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
+    if (st) return st;
+    for (int m = 0; m < 3; ++m) bank->tensor_ids[tensor_ids[m]] = expert * 4 + (uint32_t)m;
+    bank->expert_ready[expert] = 1;
     return K3X_OK;
 }
 

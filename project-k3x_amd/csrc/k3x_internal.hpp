@@ -42,6 +42,10 @@ struct k3x_hip_ctx {
     std::vector<hipEvent_t> free_events;
     double stage_ms[K3X_STAGE_COUNT] = {};
     uint64_t stage_launches[K3X_STAGE_COUNT] = {};
+    // CRC32C: device tables (uploaded at first use), chunk results, flag.
+    uint32_t* crc_tables = nullptr;
+    uint32_t* crc_chunks = nullptr;
+    size_t crc_chunk_cap = 0;
 };
 
 // Geometry of the tile layout for one matrix family of the bank.
@@ -161,6 +165,13 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
 constexpr uint32_t kDenseDirectTokens = 16;
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
                uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr);
+
+// CRC32C of device bytes (storage.hip); *crc the standard value.
+int crc32c_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* crc);
+// Whether any of `bytes` device bytes is 0xFF (MXFP4 scale validity).
+int any_ff_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, bool* found);
+void free_crc(k3x_hip_ctx* ctx);
+int retile_expert_device(k3x_hip_bank* b, uint32_t e, const uint8_t* const src[6]);
 
 // Whether a bank of this hidden size keeps the residue-major router copy,
 // and that copy's size in floats (experts padded to 16).

@@ -125,6 +125,13 @@ _SIGS = {
     "k3x_hip_bank_destroy": (C.c_int, [_vp]),
     "k3x_hip_bank_upload_expert": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64), _vp, _vp,
                                              _vp, _vp, _vp, _vp]),
+    "k3x_hip_crc32c": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(C.c_uint32)]),
+    "k3x_hip_storage_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
+    "k3x_hip_storage_close": (C.c_int, [_vp]),
+    "k3x_hip_storage_upload_expert": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
+                                                C.POINTER(C.c_uint64)]),
+    "k3x_hip_bank_upload_expert_device": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64),
+                                                    C.POINTER(_vp), C.POINTER(C.c_uint32)]),
     "k3x_hip_bank_find": (C.c_int, [_vp, C.c_uint64, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32)]),
     "k3x_hip_bank_upload_shared": (C.c_int, [_vp, _vp, _vp, _vp]),
@@ -212,6 +219,13 @@ class Context:
     def synchronize(self) -> int:
         return self.lib.k3x_hip_ctx_synchronize(self.handle)
 
+    def crc32c(self, data, nbytes: int | None = None) -> tuple[int, int]:
+        """(status, CRC32C) of a device tensor's bytes (k3x_hip_crc32c)."""
+        n = data.numel() * data.element_size() if nbytes is None else nbytes
+        out = C.c_uint32(0)
+        st = self.lib.k3x_hip_crc32c(self.handle, ptr(data), n, C.byref(out))
+        return st, out.value
+
     def stats(self) -> Stats:
         s = Stats()
         check(self.lib.k3x_hip_ctx_stats(self.handle, C.byref(s)), "k3x_hip_ctx_stats")
@@ -291,6 +305,14 @@ class Bank:
                  "down_scales")]
         return self.lib.k3x_hip_bank_upload_expert(self.handle, expert, arr,
                                                    *[host_ptr(a) for a in keep])
+
+    def upload_expert_device(self, expert: int, extents, tensor_ids, crcs=None) -> int:
+        """Six device extents (gate codes, gate scales, up codes, up scales,
+        down codes, down scales), checked against crcs (six CRC32C values)."""
+        ids = (C.c_uint64 * 3)(*tensor_ids)
+        ptrs = (_vp * 6)(*[ptr(e) for e in extents])
+        c = (C.c_uint32 * 6)(*crcs) if crcs is not None else None
+        return self.lib.k3x_hip_bank_upload_expert_device(self.handle, expert, ids, ptrs, c)
 
     def upload_shared(self, gate, up, down) -> int:
         import numpy as np
@@ -453,3 +475,26 @@ def expert_major_plan(ctx: Context, ids, tokens, top_k, experts, taps: dict) -> 
     t = make_taps(taps)
     return ctx.lib.k3x_hip_expert_major_plan(ctx.handle, ptr(ids), tokens, top_k, experts,
                                              C.byref(t))
+
+
+class Storage:
+    """A K3X checkpoint opened for expert loads (k3x_hip_storage_*).  Opening
+    is host work only; status() is the open's status code."""
+
+    def __init__(self, path: str):
+        self.lib = load()
+        h = _vp()
+        self.open_status = self.lib.k3x_hip_storage_open(path.encode(), C.byref(h))
+        self.handle = h if self.open_status == 0 else None
+
+    def upload_expert(self, bank: "Bank", slot: int, layer_id: int, expert_id: int):
+        """(status, bytes read) of load_storage_expert into bank slot `slot`."""
+        n = C.c_uint64(0)
+        st = self.lib.k3x_hip_storage_upload_expert(self.handle, bank.handle, slot, layer_id,
+                                                    expert_id, C.byref(n))
+        return st, n.value
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.k3x_hip_storage_close(self.handle)
+            self.handle = None
