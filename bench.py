@@ -13,8 +13,9 @@ Prints one JSON line.  value = microseconds per layer call (lower is better);
 the HBM figures use the bytes each call actually streams (distinct routed
 experts touched x 23,396,352 B + shared expert + router).  The same line
 carries the T=2048 prefill chunk as "prefill", the official K3
-MoE FFN (Stable LatentMoE, at its own shapes) as "official", and the
-reference CPU expert path, timed on this host, as "cpu_baseline".
+MoE FFN (Stable LatentMoE, at its own shapes) as "official", K3X storage
+expert loads and the device CRC32C as "storage", and the reference CPU
+expert path, timed on this host, as "cpu_baseline".
 """
 from __future__ import annotations
 
@@ -67,6 +68,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--official-steps", type=int, default=200,
                     help="decode steps of the official layer leg (T=2048 runs 5)")
     ap.add_argument("--no-official", action="store_true")
+    ap.add_argument("--no-storage", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
@@ -243,6 +245,8 @@ def main() -> int:
         b.close()
     if not args.no_official:
         result["official"] = official(args, ctx, k3x_amd, torch)
+    if not args.no_storage:
+        result["storage"] = storage(ctx, k3x_amd, torch, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     ctx.close()
@@ -346,6 +350,87 @@ def official(args, ctx, k3x_amd, torch) -> dict:
         log(f"official T={T}: {us:.1f} us/layer ({touched} experts)")
     off.close()
     bank.close()
+    return out
+
+
+def storage(ctx, k3x_amd, torch, cpu: bool) -> dict:
+    """K3X storage records: the device CRC32C over 256 MiB resident in HBM, and
+    load_storage_expert of official-shape experts (3 x 3072 x 3584 MXFP4,
+    17,547,264 B) from a K3X file in the page cache into bank slots (read into
+    pinned memory, one H2D copy, six CRC32C checks on the device, re-tile)."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from golden.k3x_fixture import expert_tensors, write_k3x
+    dev = "cuda:0"
+    n = 256 << 20
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    buf = torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev, generator=g)
+    k3x_amd.check(ctx.crc32c(buf)[0], "crc32c")
+    reps = 10
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        k3x_amd.check(ctx.crc32c(buf)[0], "crc32c")
+    crc_s = (time.perf_counter() - t0) / reps
+    out = {"crc32c": {"bytes": n, "us_per_call": round(crc_s * 1e6, 1),
+                      "gbps": round(n / crc_s / 1e9, 1),
+                      "hbm_frac": round(n / crc_s / 1e9 / HBM_PEAK_GBS, 4),
+                      "note": "whole call: kernel, 64 Ki chunk values to the host, host fold"}}
+    del buf
+
+    def dcrc(b: bytes) -> int:
+        t = torch.frombuffer(bytearray(b), dtype=torch.uint8).to(dev)
+        st, c = ctx.crc32c(t, len(b))
+        k3x_amd.check(st, "crc32c")
+        return c
+
+    L, I, E = OL, OI, 8
+    rng = torch.Generator().manual_seed(11)
+    tensors = []
+    for e in range(E):
+        ex = {f"{r}_packed": torch.randint(0, 256, (I * L // 2,), dtype=torch.uint8,
+                                           generator=rng).numpy()
+              for r in ("gate", "up", "down")}
+        ex.update({f"{r}_scales": torch.randint(119, 124, (I * L // 32,), dtype=torch.uint8,
+                                                generator=rng).numpy()
+                   for r in ("gate", "up", "down")})
+        tensors += expert_tensors(1, e, ex, I, L)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "experts.k3x")
+        write_k3x(path, tensors, dcrc)
+        bank = k3x_amd.Bank(ctx, k3x_amd.LayerShape(L, I, E, 0))
+        store = k3x_amd.Storage(path)
+        k3x_amd.check(store.open_status, "storage open")
+        for e in range(E):  # warm: page cache, pinned and device staging
+            k3x_amd.check(store.upload_expert(bank, e, 1, e)[0], "storage upload")
+        passes = 3
+        t0 = time.perf_counter()
+        for _ in range(passes):
+            for e in range(E):
+                st, nbytes = store.upload_expert(bank, e, 1, e)
+                k3x_amd.check(st, "storage upload")
+        per = (time.perf_counter() - t0) / (passes * E)
+        store.close()
+        bank.close()
+    out["expert_load"] = {"expert_bytes": nbytes, "experts": E, "passes": passes,
+                          "us_per_expert": round(per * 1e6, 1),
+                          "gbps": round(nbytes / per / 1e9, 2),
+                          "source": "K3X file in the page cache"}
+    if cpu:
+        # The reference's own crc32c.cpp (compiled in place into oracle/_ref),
+        # single thread, on 64 MiB of the same kind of data.
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        from oracle import RefLib
+        data = torch.randint(0, 256, (64 << 20,), dtype=torch.uint8, generator=rng).numpy()
+        ref = RefLib()
+        t0 = time.perf_counter()
+        ref.crc32c(data.tobytes())
+        cpu_s = time.perf_counter() - t0
+        out["crc32c"]["cpu_baseline"] = {"value": round(data.size / cpu_s / 1e9, 3),
+                                         "unit": "GB/s", "cores": 1, "kind": "reference",
+                                         "sample": "64 MiB, runtime/src/crc32c.cpp"}
+    log(f"storage: crc32c {out['crc32c']['gbps']} GB/s, expert load "
+        f"{out['expert_load']['us_per_expert']} us")
     return out
 
 

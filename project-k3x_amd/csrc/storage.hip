@@ -11,7 +11,8 @@
 //     length tabulated as four 256-entry byte tables (adv is linear);
 //   * the host folds the chunks from the preset register 0xFFFFFFFF with
 //     adv(., 4096), runs the tail (< 4 KiB) byte by byte, and inverts.
-// The kernel is bound by LDS table lookups (about 1.4 per byte) and HBM.
+// Each wave folds 16 sub-chunks itself (one value per 64 KiB reaches the
+// host).  The kernel is bound by LDS table lookups (about 1.4 per byte).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -29,14 +30,15 @@ namespace {
 constexpr uint32_t kPoly = 0x82f63b78u;  // reflected Castagnoli polynomial
 constexpr size_t kChunk = 4096;          // bytes per wave
 constexpr int kLevels = 6;               // wave tree: 64 B .. 2 KiB halves
-constexpr int kTables = 1 + kLevels;     // slicing + one advance table per level
+constexpr int kTables = 2 + kLevels;     // slicing, the tree levels, advance by 4 KiB
+constexpr int kSub = 16;                 // 4 KiB sub-chunks a wave folds (64 KiB chunks)
 constexpr int kCrcThreads = 256;
 
 // Host tables: T[k][256] slicing-by-4, and advance tables A_m[4][256] with
 // adv(r, m) = A_m[0][r & 255] ^ A_m[1][(r >> 8) & 255] ^ ...
 struct CrcTables {
     uint32_t slice[4][256];
-    uint32_t adv[kLevels + 1][4][256];  // m = 64 * 2^k, k = 0..5, then 4096
+    uint32_t adv[kLevels + 5][4][256];  // m = 64 * 2^k, k = 0..10 (4 KiB at 6, 64 KiB at 10)
 };
 
 uint32_t adv_apply(const uint32_t (&a)[4][256], uint32_t r) {
@@ -61,7 +63,7 @@ const CrcTables& host_tables() {
                 for (int m = 0; m < 64; ++m) r = c.slice[0][r & 255] ^ (r >> 8);
                 c.adv[0][b][x] = r;
             }
-        for (int k = 1; k <= kLevels; ++k)
+        for (int k = 1; k <= kLevels + 4; ++k)
             for (int b = 0; b < 4; ++b)
                 for (uint32_t x = 0; x < 256; ++x)
                     c.adv[k][b][x] = adv_apply(c.adv[k - 1], c.adv[k - 1][b][x]);
@@ -70,8 +72,11 @@ const CrcTables& host_tables() {
     return t;
 }
 
-// One wave per 4 KiB chunk (grid-stride over the chunks); tables in LDS:
-// [0] slicing, [1 + k] advance by 64 * 2^k bytes.
+// One wave per chunk of SUB 4 KiB sub-chunks (grid-stride over the
+// chunks); tables in LDS: [0] slicing, [1 + k] advance by 64 * 2^k bytes,
+// [1 + kLevels] advance by 4 KiB.  Each sub-chunk's raw CRC comes out of the
+// lane tree; lane 0 folds them in order: acc = adv(acc, 4 KiB) ^ sub.
+template <int SUB>
 __global__ __launch_bounds__(kCrcThreads) void crc32c_chunks_kernel(
     const uint8_t* __restrict__ data, size_t chunks, const uint32_t* __restrict__ tables,
     uint32_t* __restrict__ out) {
@@ -80,7 +85,10 @@ __global__ __launch_bounds__(kCrcThreads) void crc32c_chunks_kernel(
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (size_t c = (size_t)blockIdx.x * 4 + wave; c < chunks; c += (size_t)gridDim.x * 4) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(data + c * kChunk + lane * 64);
+      uint32_t acc = 0;
+      for (int sc = 0; sc < SUB; ++sc) {
+        const u32x4* p =
+            reinterpret_cast<const u32x4*>(data + (c * SUB + sc) * kChunk + lane * 64);
         u32x4 v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = p[i];
@@ -99,7 +107,11 @@ __global__ __launch_bounds__(kCrcThreads) void crc32c_chunks_kernel(
             r = t[1 + k][r & 255] ^ t[1 + k][256 + ((r >> 8) & 255)] ^
                 t[1 + k][512 + ((r >> 16) & 255)] ^ t[1 + k][768 + (r >> 24)] ^ right;
         }
-        if (lane == 0) out[c] = r;
+        const uint32_t* a = t[1 + kLevels];
+        acc = (a[acc & 255] ^ a[256 + ((acc >> 8) & 255)] ^ a[512 + ((acc >> 16) & 255)] ^
+               a[768 + (acc >> 24)]) ^ r;
+      }
+      if (lane == 0) out[c] = acc;
     }
 }
 
@@ -127,7 +139,7 @@ int ensure_crc(k3x_hip_ctx* ctx, size_t chunks) {
         const CrcTables& h = host_tables();
         std::vector<uint32_t> dev(kTables * 1024);
         std::memcpy(dev.data(), h.slice, 4096);
-        for (int k = 0; k < kLevels; ++k) std::memcpy(dev.data() + (1 + k) * 1024, h.adv[k], 4096);
+        for (int k = 0; k <= kLevels; ++k) std::memcpy(dev.data() + (1 + k) * 1024, h.adv[k], 4096);
         if (hipMalloc((void**)&ctx->crc_tables, dev.size() * 4) != hipSuccess) {
             (void)hipGetLastError();
             ctx->crc_tables = nullptr;
@@ -166,29 +178,40 @@ int crc32c_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* cr
     if (!ctx || (!data && bytes) || !crc) return K3X_ERR_INVALID_EXTENT;
     if (reinterpret_cast<uintptr_t>(data) % 16) return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    const size_t chunks = bytes / kChunk, tail = bytes % kChunk;
-    if (int st = ensure_crc(ctx, chunks)) return st;
+    // Whole 64 KiB chunks, then the remaining whole 4 KiB chunks, then the
+    // byte tail on the host.
+    const size_t big = bytes / (kChunk * kSub);
+    const size_t chunks = (bytes - big * kChunk * kSub) / kChunk;
+    const size_t tail = bytes % kChunk;
+    if (int st = ensure_crc(ctx, big + chunks)) return st;
     const auto* src = static_cast<const uint8_t*>(data);
-    std::vector<uint32_t> part(chunks);
+    std::vector<uint32_t> part(big + chunks);
     std::array<uint8_t, kChunk> tail_bytes{};
-    if (chunks) {
-        const size_t waves = (chunks + 3) / 4;
-        const unsigned grid = (unsigned)std::min<size_t>(waves, (size_t)ctx->cu_count * 8);
-        hipLaunchKernelGGL(crc32c_chunks_kernel, dim3(grid), dim3(kCrcThreads), 0, ctx->stream,
-                           src, chunks, ctx->crc_tables, ctx->crc_chunks);
-        ++ctx->kernel_launches;
+    auto grid = [&](size_t n) {
+        return dim3((unsigned)std::min<size_t>((n + 3) / 4, (size_t)ctx->cu_count * 8));
+    };
+    if (big)
+        hipLaunchKernelGGL(crc32c_chunks_kernel<kSub>, grid(big), dim3(kCrcThreads), 0,
+                           ctx->stream, src, big, ctx->crc_tables, ctx->crc_chunks);
+    if (chunks)
+        hipLaunchKernelGGL(crc32c_chunks_kernel<1>, grid(chunks), dim3(kCrcThreads), 0,
+                           ctx->stream, src + big * kChunk * kSub, chunks, ctx->crc_tables,
+                           ctx->crc_chunks + big);
+    if (big + chunks) {
+        ctx->kernel_launches += (big != 0) + (chunks != 0);
         if (hipGetLastError() != hipSuccess ||
-            hipMemcpyAsync(part.data(), ctx->crc_chunks, chunks * 4, hipMemcpyDeviceToHost,
-                           ctx->stream) != hipSuccess)
+            hipMemcpyAsync(part.data(), ctx->crc_chunks, (big + chunks) * 4,
+                           hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
             return K3X_ERR_BACKEND_UNAVAILABLE;
     }
-    if (tail && hipMemcpyAsync(tail_bytes.data(), src + chunks * kChunk, tail,
+    if (tail && hipMemcpyAsync(tail_bytes.data(), src + (big * kSub + chunks) * kChunk, tail,
                                hipMemcpyDeviceToHost, ctx->stream) != hipSuccess)
         return K3X_ERR_BACKEND_UNAVAILABLE;
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     const CrcTables& h = host_tables();
     uint32_t r = 0xffffffffu;
-    for (size_t c = 0; c < chunks; ++c) r = adv_apply(h.adv[kLevels], r) ^ part[c];
+    for (size_t c = 0; c < big; ++c) r = adv_apply(h.adv[kLevels + 4], r) ^ part[c];
+    for (size_t c = 0; c < chunks; ++c) r = adv_apply(h.adv[kLevels], r) ^ part[big + c];
     for (size_t i = 0; i < tail; ++i) r = h.slice[0][(r ^ tail_bytes[i]) & 255] ^ (r >> 8);
     *crc = ~r;
     return K3X_OK;
