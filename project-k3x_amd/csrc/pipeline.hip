@@ -1088,9 +1088,9 @@ struct GemvArgs {
     const uint32_t* status;
 };
 
-template <int S, int D, int OUT>
-__global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a) {
-    __shared__ f32x4 part[kGemvWaves][S][64];
+template <int S, int D, int OUT, int W = kGemvWaves>
+__global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
+    __shared__ f32x4 part[W][S][64];
     if (*(volatile const uint32_t*)a.status) return;
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1103,11 +1103,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a)
     f32x4 acc[S];
 #pragma unroll
     for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k0 = wave; k0 < a.kt; k0 += kGemvWaves * D) {
+    for (uint32_t k0 = wave; k0 < a.kt; k0 += W * D) {
         uint4 b[D][S][4], xa[D][4];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const uint32_t k = min(k0 + d * kGemvWaves, a.kt - 1);
+            const uint32_t k = min(k0 + d * W, a.kt - 1);
 #pragma unroll
             for (int w = 0; w < S; ++w)
 #pragma unroll
@@ -1117,7 +1117,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a)
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const bool live = live_row && k0 + d * kGemvWaves < a.kt;
+            const bool live = live_row && k0 + d * W < a.kt;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint4 xv = live ? xa[d][j] : make_uint4(0, 0, 0, 0);
@@ -1140,7 +1140,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void dense_gemv_kernel(GemvArgs a)
     for (int w = 0; w < S; ++w) {
         v[w] = part[0][w][pl][pi];
 #pragma unroll
-        for (int q = 1; q < kGemvWaves; ++q) v[w] = __fadd_rn(v[w], part[q][w][pl][pi]);
+        for (int q = 1; q < W; ++q) v[w] = __fadd_rn(v[w], part[q][w][pl][pi]);
     }
     const size_t at = (size_t)t * a.out_stride + (size_t)rb * 16 + c;
     if constexpr (OUT == 0) static_cast<float*>(a.out)[at] = v[0];
@@ -1798,8 +1798,14 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
     }
     if (T <= kGemvMaxTokens) {
         GemvArgs g{tiles, H / 128, x, H, T, act, I, glu, ctx->status};
-        hipLaunchKernelGGL((dense_gemv_kernel<2, 2, 2>), dim3(I / 16), dim3(64 * kGemvWaves), 0,
-                           stream, g);
+        // Beside the context stream: half-size workgroups, so that the
+        // other stream's launches find room on every compute unit.
+        if (stream == ctx->stream)
+            hipLaunchKernelGGL((dense_gemv_kernel<2, 2, 2>), dim3(I / 16), dim3(64 * kGemvWaves), 0,
+                               stream, g);
+        else
+            hipLaunchKernelGGL((dense_gemv_kernel<2, 2, 2, kGemvWaves / 2>), dim3(I / 16),
+                               dim3(32 * kGemvWaves), 0, stream, g);
         return launched(ctx, 1);
     }
     if (stream != ctx->stream) return K3X_ERR_INVALID_EXTENT;
@@ -1827,9 +1833,12 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
         if (y_bf16)
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), grid, dim3(64 * kGemvWaves), 0, stream,
                                g);
-        else
+        else if (stream == ctx->stream)
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0>), grid, dim3(64 * kGemvWaves), 0, stream,
                                g);
+        else
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0, kGemvWaves / 2>), grid,
+                               dim3(32 * kGemvWaves), 0, stream, g);
         return launched(ctx, 1);
     }
     if (y_bf16) return K3X_ERR_INVALID_EXTENT;
