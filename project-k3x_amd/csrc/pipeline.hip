@@ -678,7 +678,7 @@ __global__ __launch_bounds__(64) void topk_reg_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t group_tps(uint32_t K) { return min(64u, 1024u / K); }
 
-__global__ __launch_bounds__(1024) void group_count_kernel(const uint32_t* __restrict__ ids,
+__device__ inline bool group_count_body(uint32_t c, const uint32_t* __restrict__ ids,
                                                            uint32_t T, uint32_t K, uint32_t E,
                                                            uint32_t* __restrict__ chunk_cnt,
                                                            uint32_t* __restrict__ chunk_fu,
@@ -688,8 +688,8 @@ __global__ __launch_bounds__(1024) void group_count_kernel(const uint32_t* __res
     uint32_t* s_ids = smem;          // [1024] the chunk's ids
     uint32_t* mask = s_ids + 1024;   // [E][2] token bitmap per expert
     uint32_t* fu = mask + 2 * E;     // [E]
-    if (*(volatile uint32_t*)status) return;
-    const uint32_t tid = threadIdx.x, c = blockIdx.x, tps = group_tps(K);
+    if (*(volatile uint32_t*)status) return false;
+    const uint32_t tid = threadIdx.x, tps = group_tps(K);
     const uint32_t tl = tid / K, s = tid % K, t = c * tps + tl;
     const bool valid = tl < tps && t < T;
     const uint32_t p = t * K + s;
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(1024) void group_count_kernel(const uint32_t* __res
         for (uint32_t q = 0; q < s; ++q) bad |= s_ids[tl * K + q] == e;
     if (__syncthreads_or(bad)) {
         if (tid == 0) latch(status, K3X_ERR_INVALID_STATE);
-        return;
+        return false;
     }
     if (valid) {
         atomicOr(&mask[2 * e + (tl >> 5)], 1u << (tl & 31));
@@ -722,6 +722,14 @@ __global__ __launch_bounds__(1024) void group_count_kernel(const uint32_t* __res
         chunk_cnt[(size_t)c * E + q] = __popc(mask[2 * q]) + __popc(mask[2 * q + 1]);
         chunk_fu[(size_t)c * E + q] = fu[q];
     }
+    return true;
+}
+
+__global__ __launch_bounds__(1024) void group_count_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    uint32_t* __restrict__ chunk_cnt, uint32_t* __restrict__ chunk_fu,
+    uint8_t* __restrict__ rank, uint32_t* status) {
+    (void)group_count_body(blockIdx.x, ids, T, K, E, chunk_cnt, chunk_fu, rank, status);
 }
 
 // Exclusive scan of one 64-bit value per thread over a 1024-thread block;
@@ -756,7 +764,7 @@ __device__ inline uint64_t block_exclusive_scan(uint64_t v, uint64_t* red, uint6
 // (27..47), active flag (48..60).
 constexpr uint32_t kScanItemShift = 27, kScanActiveShift = 48;
 
-__global__ __launch_bounds__(1024) void group_scan_kernel(
+__device__ inline bool group_scan_body(
     uint32_t T, uint32_t K, uint32_t E, uint32_t* __restrict__ chunk_cnt,
     const uint32_t* __restrict__ chunk_fu, uint32_t* __restrict__ counts,
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
@@ -768,7 +776,7 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(
     uint32_t* s_fu = s_cnt + E;      // [E]
     uint32_t* s_alist = s_fu + E;    // [E] active experts, ascending
     __shared__ uint64_t red[32];
-    if (*(volatile uint32_t*)status) return;
+    if (*(volatile uint32_t*)status) return false;
     const uint32_t tid = threadIdx.x, nch = (T + group_tps(K) - 1) / group_tps(K);
     // Running base of every chunk, per expert (chunks loaded 16 at a time).
     for (uint32_t e = tid; e < E; e += 1024) {
@@ -882,6 +890,33 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(
         for (uint32_t b = 0; b < na; ++b) r += s_fu[s_alist[b]] < key;
         active_fu[r] = e;
     }
+    return true;
+}
+
+__global__ __launch_bounds__(1024) void group_scan_kernel(
+    uint32_t T, uint32_t K, uint32_t E, uint32_t* __restrict__ chunk_cnt,
+    const uint32_t* __restrict__ chunk_fu, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
+    uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
+    uint32_t* __restrict__ active_fu, uint32_t* __restrict__ witems,
+    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint32_t* status) {
+    (void)group_scan_body(T, K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active,
+                          active_asc, active_fu, witems, n_witems, chunk_rows, status);
+}
+
+__device__ inline void group_scatter_body(uint32_t c, 
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    const uint32_t* __restrict__ chunk_base, const uint8_t* __restrict__ rank,
+    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ pair_token,
+    uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x, tps = group_tps(K);
+    const uint32_t tl = tid / K, s = tid % K, t = c * tps + tl;
+    if (tl >= tps || t >= T) return;
+    const uint32_t p = t * K + s, e = ids[p];
+    const uint32_t r = offsets[e] + chunk_base[(size_t)c * E + e] + rank[p];
+    pair_token[r] = t;
+    pair_slot[r] = s;
 }
 
 __global__ __launch_bounds__(1024) void group_scatter_kernel(
@@ -889,14 +924,28 @@ __global__ __launch_bounds__(1024) void group_scatter_kernel(
     const uint32_t* __restrict__ chunk_base, const uint8_t* __restrict__ rank,
     const uint32_t* __restrict__ offsets, uint32_t* __restrict__ pair_token,
     uint32_t* __restrict__ pair_slot, uint32_t* status) {
-    if (*(volatile uint32_t*)status) return;
-    const uint32_t tid = threadIdx.x, c = blockIdx.x, tps = group_tps(K);
-    const uint32_t tl = tid / K, s = tid % K, t = c * tps + tl;
-    if (tl >= tps || t >= T) return;
-    const uint32_t p = t * K + s, e = ids[p];
-    const uint32_t r = offsets[e] + chunk_base[(size_t)c * E + e] + rank[p];
-    pair_token[r] = t;
-    pair_slot[r] = s;
+    group_scatter_body(blockIdx.x, ids, T, K, E, chunk_base, rank, offsets, pair_token, pair_slot,
+                       status);
+}
+
+// All T tokens in one chunk (T <= group_tps(K)): the three steps in one
+// workgroup, separated by barriers (the chunk values pass through global
+// memory written and read by this workgroup only).
+__global__ __launch_bounds__(1024) void group_single_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    uint32_t* __restrict__ chunk_cnt, uint32_t* __restrict__ chunk_fu, uint8_t* __restrict__ rank,
+    uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets,
+    uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
+    uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu,
+    uint32_t* __restrict__ witems, uint32_t* __restrict__ n_witems, uint32_t chunk_rows,
+    uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    if (!group_count_body(0, ids, T, K, E, chunk_cnt, chunk_fu, rank, status)) return;
+    __syncthreads();
+    if (!group_scan_body(T, K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active,
+                         active_asc, active_fu, witems, n_witems, chunk_rows, status))
+        return;
+    __syncthreads();
+    group_scatter_body(0, ids, T, K, E, chunk_cnt, rank, offsets, pair_token, pair_slot, status);
 }
 
 // ---------------------------------------------------------------------------
@@ -1322,6 +1371,13 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
     uint32_t* chunk_cnt = reinterpret_cast<uint32_t*>(gscratch);
     uint32_t* chunk_fu = chunk_cnt + (size_t)nch * E;
     uint8_t* rank = reinterpret_cast<uint8_t*>(chunk_fu + (size_t)nch * E);
+    if (nch == 1) {
+        hipLaunchKernelGGL(group_single_kernel, dim3(1), dim3(1024), (size_t)(1024 + 3 * E) * 4,
+                           ctx->stream, ids, T, K, E, chunk_cnt, chunk_fu, rank, counts, offsets,
+                           first_use, n_active, active_asc, active_fu, witems, n_witems,
+                           k3x_hip::kWideRows, pair_token, pair_slot, ctx->status);
+        return launched(ctx, 1);
+    }
     hipLaunchKernelGGL(group_count_kernel, dim3(nch), dim3(1024), (size_t)(1024 + 3 * E) * 4,
                        ctx->stream, ids, T, K, E, chunk_cnt, chunk_fu, rank, ctx->status);
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(1024), (size_t)3 * E * 4, ctx->stream, T,
