@@ -165,6 +165,12 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
 constexpr uint32_t kDenseDirectTokens = 16;
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
                uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr);
+// Up to kDenseDirectTokens rows on the context stream: y = tiles . a with the
+// official layer's output in the epilogue: routed = y (fp32) and out =
+// bf16(bf16(prefix) + bf16(bf16(y) + bf16(shared))) (shared may be null).
+int dense_down_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K,
+                      const uint16_t* a, uint32_t T, const float* prefix, const float* shared,
+                      float* routed, uint16_t* out);
 
 // CRC32C of device bytes (storage.hip); *crc the standard value.
 int crc32c_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* crc);

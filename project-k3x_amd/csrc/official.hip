@@ -673,15 +673,27 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     if (st) return st;
     // routed = routed_up . RMSNorm(mixed, routed_norm) (official_moe.cpp:327-333).
     st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon, b.normed);
-    st = st ? st : k3x_hip::dense_down(ctx, o->routed_up, o->H, o->L, b.normed, T, b.routed,
-                                       ctx->stream);
-    if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
-    st = st ? st : joiner.join();
-    if (st) return st;
     const size_t n = (size_t)T * o->H;
-    hipLaunchKernelGGL(official_out_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream,
-                       prefix, b.routed, o->I_s ? b.shared : nullptr, n, out, ctx->status);
-    if ((st = launched(ctx, 1))) return st;
+    if (T <= k3x_hip::kDenseDirectTokens) {
+        // Few rows: the output formula in the routed_up GEMV's epilogue, after
+        // the shared FFN (long finished on the side stream by now).
+        if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
+        st = st ? st : joiner.join();
+        st = st ? st : k3x_hip::dense_down_output(ctx, o->routed_up, o->H, o->L, b.normed, T,
+                                                  prefix, o->I_s ? b.shared : nullptr, b.routed,
+                                                  out);
+        if (st) return st;
+    } else {
+        st = st ? st : k3x_hip::dense_down(ctx, o->routed_up, o->H, o->L, b.normed, T, b.routed,
+                                           ctx->stream);
+        if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
+        st = st ? st : joiner.join();
+        if (st) return st;
+        hipLaunchKernelGGL(official_out_kernel, dim3(blocks_for(n)), dim3(kThreads), 0,
+                           ctx->stream, prefix, b.routed, o->I_s ? b.shared : nullptr, n, out,
+                           ctx->status);
+        if ((st = launched(ctx, 1))) return st;
+    }
     if (taps) {
         st = copy_d2d(ctx, taps->ids, ids, (size_t)T * K * 4);
         st = st ? st : copy_d2d(ctx, taps->contributions, contributions, (size_t)T * K * 4);

@@ -1120,7 +1120,9 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 // the last tile zeroed, so no load sits behind a branch).  The waves'
 // accumulators are summed in wave order through LDS.  Activations: lane l
 // reads token l % 16 (clamped to the last token and zeroed past it).
-// OUT: 0 fp32 y, 1 bf16 y, 2 bf16 GLU(gate, up) (S == 2).
+// OUT: 0 fp32 y, 1 bf16 y, 2 bf16 GLU(gate, up) (S == 2), 3 the official
+// layer's output bf16(bf16(prefix) + bf16(bf16(y) + bf16(shared))), y also
+// stored in fp32 (runtime/src/official_moe.cpp:336-340).
 // ---------------------------------------------------------------------------
 constexpr int kGemvWaves = 16;
 constexpr uint32_t kGemvMaxTokens = k3x_hip::kDenseDirectTokens;
@@ -1135,6 +1137,11 @@ struct GemvArgs {
     uint32_t out_stride;
     GluParams glu;
     const uint32_t* status;
+    // OUT 3 (the official layer's output): prefix, shared (may be null) and
+    // the fp32 projection (routed) at the output's [T][out_stride] layout.
+    const float* prefix;
+    const float* shared;
+    float* routed;
 };
 
 template <int S, int D, int OUT, int W = kGemvWaves>
@@ -1194,7 +1201,14 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     const size_t at = (size_t)t * a.out_stride + (size_t)rb * 16 + c;
     if constexpr (OUT == 0) static_cast<float*>(a.out)[at] = v[0];
     else if constexpr (OUT == 1) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(v[0]);
-    else static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(glu(v[0], v[S - 1], a.glu));
+    else if constexpr (OUT == 2) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(glu(v[0], v[S - 1], a.glu));
+    else {
+        auto r16 = [](float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); };
+        a.routed[at] = v[0];
+        const float sh = a.shared ? r16(a.shared[at]) : 0.0f;
+        const float combined = r16(__fadd_rn(r16(v[0]), sh));
+        static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(__fadd_rn(r16(a.prefix[at]), combined));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1828,6 +1842,16 @@ int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32
 // Dense bf16 projections in the bank's tile layout: the wide grouped GEMM
 // (one item per 128-row chunk of the T rows) from kWideMinTokens rows when
 // the shapes fit it, else expert_gemm over the T rows as one block.
+int dense_down_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K,
+                      const uint16_t* a, uint32_t T, const float* prefix, const float* shared,
+                      float* routed, uint16_t* out) {
+    if (!T || T > kGemvMaxTokens || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
+    GemvArgs g{tiles, K / 128, a, K, T, out, N, {}, ctx->status, prefix, shared, routed};
+    hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 3>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
+                       ctx->stream, g);
+    return launched(ctx, 1);
+}
+
 bool dense_wide_ok(WideKind kind, uint32_t N, uint32_t K, uint32_t T) {
     return T >= kWideMinTokens && K % (128 * kWideStages) == 0 &&
            (N / 16) % wide_rb_per_block(kind) == 0 && N % 16 == 0 &&
