@@ -96,14 +96,19 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     }
     // The whole row in registers: this thread's k = tid + 256 j, j < 32.
     // Loads past the row read 0 (buffer range check), and the +0 terms they
-    // add after the row's last term leave the sum of squares unchanged.
+    // add after the row's last term leave the sum of squares unchanged.  The
+    // gamma loads go out with the row's, ahead of the reduction.
     const __amdgpu_buffer_rsrc_t xs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xr), (short)0, H * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t gs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(gamma), (short)0, H * 4, 0x00020000);
     uint16_t xb[32];
+    float gv[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) xb[j] = __builtin_amdgcn_raw_buffer_load_b16(xs, tid * 2, j * 512, 0);
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+        gv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gs, tid * 4, j * 1024, 0));
     double s = 0.0;
     int bad = 0;
 #pragma unroll
@@ -121,10 +126,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
     uint32_t b[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        const float g = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gs, tid * 4, j * 1024, 0));
-        b[j] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xb[j]), inv), g));
-    }
+    for (int j = 0; j < 32; ++j) b[j] = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(xb[j]), inv), gv[j]));
 #pragma unroll
     for (int j = 0; j < 32; ++j)
         if (tid + 256u * j < H) out[tid + 256 * j] = (uint16_t)b[j];
