@@ -229,16 +229,42 @@ __global__ void round_bf16_kernel(const float* __restrict__ in, size_t n,
 
 // out = bf16(bf16(prefix) + bf16(bf16(routed) + bf16(shared)))
 // (runtime/src/official_moe.cpp:336-340; no shared FFN: shared = 0).
+// Four elements per thread (16-byte loads, 8-byte store) when n % 4 == 0 and
+// the rows are 16-byte aligned, else one.
+template <int V>
 __global__ void official_out_kernel(const float* __restrict__ prefix,
                                     const float* __restrict__ routed,
                                     const float* __restrict__ shared, size_t n,
                                     uint16_t* __restrict__ out, const uint32_t* status) {
     if (*(volatile const uint32_t*)status) return;
-    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    const size_t i = ((size_t)blockIdx.x * kThreads + threadIdx.x) * V;
     if (i >= n) return;
-    const float sh = shared ? bf16_round(shared[i]) : 0.0f;
-    const float combined = bf16_round(__fadd_rn(bf16_round(routed[i]), sh));
-    out[i] = f32_to_bf16(__fadd_rn(bf16_round(prefix[i]), combined));
+    float pv[V], rv[V], sv[V];
+    if constexpr (V == 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(prefix + i);
+        const float4 r4 = *reinterpret_cast<const float4*>(routed + i);
+        const float4 s4 = shared ? *reinterpret_cast<const float4*>(shared + i) : make_float4(0, 0, 0, 0);
+        pv[0] = p4.x; pv[1] = p4.y; pv[2] = p4.z; pv[3] = p4.w;
+        rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+        sv[0] = s4.x; sv[1] = s4.y; sv[2] = s4.z; sv[3] = s4.w;
+    } else {
+        pv[0] = prefix[i];
+        rv[0] = routed[i];
+        sv[0] = shared ? shared[i] : 0.0f;
+    }
+    uint16_t o[V];
+#pragma unroll
+    for (int c = 0; c < V; ++c) {
+        const float sh = shared ? bf16_round(sv[c]) : 0.0f;
+        const float combined = bf16_round(__fadd_rn(bf16_round(rv[c]), sh));
+        o[c] = f32_to_bf16(__fadd_rn(bf16_round(pv[c]), combined));
+    }
+    if constexpr (V == 4) {
+        *reinterpret_cast<uint2*>(out + i) =
+            make_uint2(o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16);
+    } else {
+        out[i] = o[0];
+    }
 }
 
 // bf16 words -> fp32 on the host (exact).
@@ -689,9 +715,16 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
         if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
         st = st ? st : joiner.join();
         if (st) return st;
-        hipLaunchKernelGGL(official_out_kernel, dim3(blocks_for(n)), dim3(kThreads), 0,
-                           ctx->stream, prefix, b.routed, o->I_s ? b.shared : nullptr, n, out,
-                           ctx->status);
+        const bool vec = n % 4 == 0 && reinterpret_cast<uintptr_t>(prefix) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % 8 == 0;
+        if (vec)
+            hipLaunchKernelGGL(official_out_kernel<4>, dim3(blocks_for(n / 4)), dim3(kThreads), 0,
+                               ctx->stream, prefix, b.routed, o->I_s ? b.shared : nullptr, n, out,
+                               ctx->status);
+        else
+            hipLaunchKernelGGL(official_out_kernel<1>, dim3(blocks_for(n)), dim3(kThreads), 0,
+                               ctx->stream, prefix, b.routed, o->I_s ? b.shared : nullptr, n, out,
+                               ctx->status);
         if ((st = launched(ctx, 1))) return st;
     }
     if (taps) {
