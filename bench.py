@@ -70,6 +70,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-official", action="store_true")
     ap.add_argument("--no-storage", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the GPU legs of configs 1, 2 and 4")
+    ap.add_argument("--cpu-all", action="store_true",
+                    help="CPU baseline also on config 4 (full, N threads; one thread on a "
+                         "1/16 token sample) and a 1/16 token sample of config 5 (several "
+                         "minutes of CPU work)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
                          "(counter calibration), then decode layer calls")
@@ -241,6 +247,8 @@ def main() -> int:
 
     if not args.no_prefill:
         result["prefill"] = prefill(args, ctx, banks[0], k3x_amd, torch)
+    if not args.no_configs:
+        result["configs"] = config_legs(ctx, banks[0], k3x_amd, torch)
     for b in banks:
         b.close()
     if not args.no_official:
@@ -248,7 +256,7 @@ def main() -> int:
     if not args.no_storage:
         result["storage"] = storage(ctx, k3x_amd, torch, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"], result["cpu_configs"] = cpu_baseline(args.cpu_all)
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0
@@ -289,6 +297,88 @@ def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
             "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_floor_us": round(floor_us, 1),
             "frac_of_floor": round(floor_us / us, 4)}
+
+
+def time_calls(torch, fn, n: int, warmup: int = 3) -> float:
+    """Microseconds per call of fn(i) over n calls after `warmup` untimed ones,
+    bracketed by device synchronisation."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / n * 1e6
+
+
+def config_legs(ctx, bank_c3, k3x_amd, torch) -> dict:
+    """The other benchmark configurations through the same entry point
+    (k3x_hip_moe_forward, device routing), each timed over whole layer calls
+    with inputs resident in HBM:
+    c1  the tiny layer (T=1, H=256, E=16, I=512, Top-4), 8 banks cycled;
+    c2  one K3-shaped expert (T=1, H=7168, I=2048, E=1, Top-1, no shared
+        expert), 32 banks cycled so no cache holds the 23.4 MB expert;
+    c4  the verification window (T=64, Zipf-skewed bias over the c3 bank,
+        0..~40 rows per expert; the general path's narrow GEMMs)."""
+    sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
+    from oracle import Oracle
+    from synth import CONFIGS, SynthLayer
+    dev = "cuda:0"
+    out = {}
+    na = torch.empty(1, dtype=torch.int32, device=dev)
+    for cid, nbanks, steps in ((1, 8, 400), (2, 32, 400), (4, 1, 20)):
+        cfg = CONFIGS[cid]
+        T, Hc, Ic, Ec, Kc, Sc = (cfg.tokens, cfg.hidden, cfg.inter, cfg.experts, cfg.top_k,
+                                 cfg.shared_inter)
+        if cid == 4:
+            layer = SynthLayer(Oracle(), cfg)
+            k3x_amd.check(bank_c3.upload_router(layer.router, layer.bias, layer.gamma),
+                          "c4 router")
+            banks = [bank_c3]
+        else:
+            banks = []
+            for i in range(nbanks):
+                b = k3x_amd.Bank(ctx, k3x_amd.LayerShape(Hc, Ic, Ec, Sc))
+                b.fill_synthetic(cfg.seed + i, cfg.scale_lo, cfg.scale_hi, cfg.router_sigma,
+                                 cfg.bias_sigma, cfg.shared_sigma, 1.0)
+                banks.append(b)
+        x = torch.empty((T, Hc), dtype=torch.int16, device=dev)
+        k3x_amd.synth_normal_bf16(ctx, cfg.x_seed, k3x_amd.stream_id(k3x_amd.STREAM_INPUT), 1.0,
+                                  x)
+        y = torch.empty((T, Hc), dtype=torch.int16, device=dev)
+        params = k3x_amd.make_params(T, Kc, cfg.routed_scale, cfg.eps, cfg.glu, cfg.beta,
+                                     cfg.linear, cfg.renorm)
+        k3x_amd.check(k3x_amd.moe_forward(ctx, banks[0], params, x, y, {"n_active": na}),
+                      f"c{cid}")
+        k3x_amd.check(ctx.synchronize(), f"c{cid}")
+        d = int(na.item())
+
+        def call(i):
+            st = k3x_amd.moe_forward(ctx, banks[i % len(banks)], params, x, y)
+            if st:
+                raise k3x_amd.K3xError(st, f"c{cid}")
+
+        us = time_calls(torch, call, steps)
+        k3x_amd.check(ctx.synchronize(), f"c{cid}")
+        expert_bytes = 3 * (Hc * Ic // 2 + Hc * Ic // 32)
+        routed = d * expert_bytes
+        all_b = routed + 3 * Sc * Hc * 2 + Ec * Hc * 4 + Ec * 4 + Hc * 4 + 2 * T * Hc * 2
+        flops = T * Kc * 2 * 3 * Hc * Ic + T * 2 * 3 * Hc * Sc
+        out[f"c{cid}"] = {
+            "workload": cfg.name, "tokens": T, "hidden": Hc, "inter": Ic, "experts": Ec,
+            "top_k": Kc, "shared_inter": Sc, "banks_cycled": len(banks), "steps": steps,
+            "us_per_layer": round(us, 2), "tokens_per_s": round(T / (us * 1e-6), 1),
+            "experts_touched": d, "routed_bytes": routed,
+            "hbm_gbps_routed": round(routed / (us * 1e-6) / 1e9, 1),
+            "hbm_frac_routed": round(routed / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_gbps_all": round(all_b / (us * 1e-6) / 1e9, 1),
+            "tflops": round(flops / (us * 1e-6) / 1e12, 3)}
+        log(f"c{cid}: {us:.1f} us/layer, {d} experts touched")
+        if cid != 4:
+            for b in banks:
+                b.close()
+    return out
 
 
 # The official K3 MoE FFN (Stable LatentMoE): hidden 7168, latent 3584, 896
@@ -417,18 +507,20 @@ def storage(ctx, k3x_amd, torch, cpu: bool) -> dict:
                           "gbps": round(nbytes / per / 1e9, 2),
                           "source": "K3X file in the page cache"}
     if cpu:
-        # The reference's own crc32c.cpp (compiled in place into oracle/_ref),
-        # single thread, on 64 MiB of the same kind of data.
+        # The reference's byte-table CRC32C (runtime/src/crc32c.cpp), restated
+        # by the oracle and pinned to it (tests/test_oracle_vs_ref.py), single
+        # thread, on 64 MiB of the same kind of data.
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        from oracle import RefLib
+        from oracle import Oracle
         data = torch.randint(0, 256, (64 << 20,), dtype=torch.uint8, generator=rng).numpy()
-        ref = RefLib()
+        o = Oracle()
         t0 = time.perf_counter()
-        ref.crc32c(data.tobytes())
+        o.crc32c_table(data)
         cpu_s = time.perf_counter() - t0
         out["crc32c"]["cpu_baseline"] = {"value": round(data.size / cpu_s / 1e9, 3),
-                                         "unit": "GB/s", "cores": 1, "kind": "reference",
-                                         "sample": "64 MiB, runtime/src/crc32c.cpp"}
+                                         "unit": "GB/s", "cores": 1, "kind": "port",
+                                         "sample": "64 MiB, k3xo_crc32c_table (the byte-table "
+                                                   "method of runtime/src/crc32c.cpp)"}
     log(f"storage: crc32c {out['crc32c']['gbps']} GB/s, expert load "
         f"{out['expert_load']['us_per_expert']} us")
     return out
@@ -486,48 +578,85 @@ def traffic_from(fetch_dir: str, write_dir: str) -> dict:
     return out
 
 
-def cpu_baseline() -> dict:
-    """The reference's own CPU path (oracle/_ref, built from its sources):
-    one T=2 decode layer call of layer 0, token by token through rms_norm ->
-    router dense_matvec -> sigmoid -> select_routing -> mxfp4_situ_moe +
-    dense_situ_mlp shared expert, single thread, as the reference runs it."""
+def cpu_threads() -> int:
+    """Threads for the N-thread CPU baseline: the CPU share this process may
+    use (OMP_NUM_THREADS when the host sets it, else the affinity mask)."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    n = len(os.sched_getaffinity(0))
+    return max(1, min(int(env), n)) if env and env.isdigit() else n
+
+
+def cpu_baseline(all_configs: bool) -> tuple[dict, dict]:
+    """The reference's CPU expert path, restated by the oracle (k3x_oracle.c,
+    k3xo_moe_layer: pinned bit for bit to the reference's own CPU composition
+    by tests/test_oracle_vs_ref.py), timed on this host: rms_norm -> router
+    (double sums) -> libm sigmoid + bias Top-K -> per (token, slot) pair the
+    MXFP4 expert (decode to fp32, double GEMVs, GLU) -> slot-ordered mix +
+    bf16 shared expert.  One thread (the reference backend is
+    single-threaded) and N threads over tokens and pairs.  Returns the
+    headline entry (config 3 at N threads) and the per-config table."""
     import numpy as np
     sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
-    from oracle import ORDER_SEQ, REF_SO, SIGMOID_REF, Oracle, RefLib, bf16_to_f32
+    from oracle import ORDER_SEQ, SIGMOID_REF, Oracle, bf16_to_f32
     from synth import CONFIGS, SynthLayer
 
-    kind = "reference" if os.path.exists(REF_SO) else "port"
     o = Oracle()
-    cfg = CONFIGS[3]
-    layer = SynthLayer(o, cfg)
-    x = bf16_to_f32(layer.x_bits())
-    # Which experts the reference will select (same sequential-double router
-    # and libm sigmoid), so only those are generated on the host.
-    xn = [o.rms_norm(x[t], layer.gamma, cfg.eps) for t in range(cfg.tokens)]
-    ids = [o.route(o.router_logits(layer.router, xn[t], ORDER_SEQ), layer.bias, cfg.top_k,
-                   cfg.renorm, cfg.routed_scale, SIGMOID_REF)[1] for t in range(cfg.tokens)]
-    experts = [None] * cfg.experts
-    for e in sorted({int(e) for row in ids for e in row}):
-        experts[e] = layer.expert(e)
-    shared = tuple(bf16_to_f32(a) for a in layer.shared)
-    t0 = time.perf_counter()
-    if kind == "reference":
-        ref = RefLib()
-        for t in range(cfg.tokens):
-            st, _, _ = ref.moe_layer_token(x[t], layer.gamma, cfg.eps, layer.router, layer.bias,
-                                           experts, cfg.hidden, cfg.inter, cfg.top_k,
-                                           cfg.routed_scale, shared, beta=4.0)
+    n_thr = cpu_threads()
+    table = {"threads_n": n_thr, "nproc": os.cpu_count(), "kind": "port",
+             "source": "oracle/k3x_oracle.c k3xo_moe_layer"}
+
+    def run(cid, tokens=None, threads=(1, n_thr)):
+        cfg = CONFIGS[cid]
+        layer = SynthLayer(o, cfg)
+        x = bf16_to_f32(layer.x_bits())
+        if tokens is not None:
+            x = x[tokens]
+        T = x.shape[0]
+        # The experts the routes reach (the same double-sum router and libm
+        # sigmoid as the timed call), generated on the host.
+        need = set()
+        for t in range(T):
+            xn = o.rms_norm(x[t], layer.gamma, cfg.eps)
+            st, ids, _, _ = o.route(o.router_logits(layer.router, xn, ORDER_SEQ), layer.bias,
+                                    cfg.top_k, cfg.renorm, cfg.routed_scale, SIGMOID_REF)
+            need |= {int(e) for e in ids}
+        experts = [layer.expert(e) if e in need else None for e in range(cfg.experts)]
+        row = {"tokens": T, "pairs": T * cfg.top_k, "experts_touched": len(need)}
+        for n in threads:
+            t0 = time.perf_counter()
+            st, _, _, _ = o.moe_layer(x, layer.gamma, cfg.eps, layer.router, layer.bias,
+                                      experts, cfg.hidden, cfg.inter, cfg.top_k,
+                                      cfg.routed_scale, cfg.renorm, layer.shared, cfg.glu,
+                                      cfg.beta, cfg.linear, threads=n)
+            sec = time.perf_counter() - t0
             if st:
-                raise RuntimeError(f"reference CPU layer failed: {st}")
-    else:
-        for t in range(cfg.tokens):
-            for s in range(cfg.top_k):
-                o.expert_ffn(xn[t], experts[int(ids[t][s])], cfg.hidden, cfg.inter)
-    sec = time.perf_counter() - t0
-    log(f"cpu baseline ({kind}): {sec:.2f} s per T=2 layer call")
-    return {"value": round(sec * 1e6, 1), "unit": "us/layer", "cores": 1, "kind": kind,
-            "sample": "one c3 decode layer call (T=2, 32 routed pairs + shared expert), "
-                      "reference CPU composition, single thread"}
+                raise RuntimeError(f"CPU layer c{cid} failed: {st}")
+            row[f"us_{n}thr"] = round(sec * 1e6, 1)
+        log(f"cpu c{cid} ({T} tokens): " + ", ".join(f"{k} {v}" for k, v in row.items()))
+        return row
+
+    for cid in (1, 2, 3):
+        table[f"c{cid}"] = run(cid)
+        table[f"c{cid}"]["sample"] = "full layer call"
+    if all_configs:
+        table["c4"] = run(4, threads=(n_thr,))
+        table["c4"]["sample"] = "full layer call, N threads"
+        sub = run(4, tokens=list(range(0, 64, 16)), threads=(1,))
+        table["c4"]["us_1thr"] = round(sub["us_1thr"] * 16, 1)
+        table["c4"]["us_1thr_derived_from"] = "4 of 64 tokens (every 16th), x16"
+        c5 = run(5, tokens=list(range(0, 2048, 16)), threads=(n_thr,))
+        table["c5"] = {"tokens": 2048, "derived": True,
+                       f"us_{n_thr}thr": round(c5[f"us_{n_thr}thr"] * 16, 1),
+                       "sample": "128 of 2048 tokens (every 16th), N threads, x16",
+                       "sample_experts_touched": c5["experts_touched"]}
+    c3 = table["c3"]
+    head = {"value": c3[f"us_{n_thr}thr"], "unit": "us/layer", "cores": n_thr, "kind": "port",
+            "value_1thr": c3["us_1thr"],
+            "sample": "one full config-3 layer call (T=2: RMSNorm, router, Top-16, 32 routed "
+                      "pairs, shared expert) through k3xo_moe_layer, the oracle's pinned "
+                      f"restatement of the reference CPU path, {n_thr} threads; value_1thr "
+                      "is the same call on one thread"}
+    return head, table
 
 
 if __name__ == "__main__":

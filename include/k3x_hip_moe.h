@@ -298,9 +298,11 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
  * bf16 input [T][hidden], ids/weights device [T][K] in router order.  Routes
  * must not repeat an expert within a token and weights must be finite
  * (checked on the host copy passed in host_ids/host_weights, which may be
- * NULL to skip the check).  With host_ids, only the routed slots must hold
- * admitted experts (K3X_ERR_INVALID_STATE otherwise); without, every slot of
- * the bank must.  Replaces ComputeBackend::mxfp4_situ_moe
+ * NULL to skip the host check).  Only the routed slots must hold admitted
+ * experts: with host_ids the call returns K3X_ERR_INVALID_STATE otherwise;
+ * without, the grouping latches K3X_ERR_INVALID_STATE for a route to an
+ * empty slot, an expert id out of range or an expert repeated within a
+ * token.  Replaces ComputeBackend::mxfp4_situ_moe
  * (backend.hpp:364-368) batched over tokens.  Asynchronous. */
 int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                                const k3x_hip_moe_params* params,
@@ -398,7 +400,8 @@ int k3x_hip_official_prepare(k3x_hip_ctx* ctx, k3x_hip_official* official, uint3
  * the route as device ids [T][K] + contributions [T][K], or ids ==
  * contributions == NULL to route on the device (router logits over hidden,
  * sigmoid + correction, natural Top-K, contributions s / sum s in double:
- * official_moe.cpp:211-245).  out bf16 [T][H] = bf16(bf16(prefix) +
+ * official_moe.cpp:211-245; every slot of the bank must then hold an
+ * admitted expert, while a given route needs only its own slots).  out bf16 [T][H] = bf16(bf16(prefix) +
  * bf16(routed + shared)).  params: tokens, top_k, rms_epsilon and the GLU
  * (SiTU for the reference's layer); routed_scale, renorm and flags are not
  * used.  Replaces ComputeBackend::official_mxfp4_moe_ffn

@@ -717,8 +717,10 @@ static uint64_t word_at(uint64_t key, uint64_t index) {
 /* Packed E2M1 bytes: byte p is byte (p % 8) of word p / 8, so both nibbles
  * are uniform over the 16 codes. */
 void k3xo_synth_codes(uint64_t key, size_t nbytes, uint8_t* out) {
-    for (size_t p = 0; p < nbytes; ++p)
-        out[p] = (uint8_t)(word_at(key, p >> 3) >> ((p & 7) * 8));
+    for (size_t p = 0; p < nbytes; p += 8) {
+        const uint64_t w = word_at(key, p >> 3);  /* byte p + b is byte b of word p / 8 */
+        for (size_t b = 0; b < 8 && p + b < nbytes; ++b) out[p + b] = (uint8_t)(w >> (8 * b));
+    }
 }
 
 /* E8M0 scale bytes uniform over [lo, hi]. */
@@ -763,6 +765,26 @@ uint32_t k3xo_crc32c(const uint8_t* data, size_t n) {
     return ~crc;
 }
 
+/* The same value by the reference's own method, one 256-entry byte table
+ * built from the reflected polynomial and one lookup per byte
+ * (runtime/src/crc32c.cpp:7-28); the bench times it as the CPU baseline of
+ * the device CRC32C. */
+uint32_t k3xo_crc32c_table(const uint8_t* data, size_t n) {
+    static uint32_t table[256];
+    static int ready;
+    if (!ready) {
+        for (uint32_t v = 0; v < 256; ++v) {
+            uint32_t c = v;
+            for (int b = 0; b < 8; ++b) c = (c >> 1) ^ (0x82f63b78u & (0u - (c & 1u)));
+            table[v] = c;
+        }
+        ready = 1;
+    }
+    uint32_t crc = 0xffffffffu;
+    for (size_t i = 0; i < n; ++i) crc = table[(crc ^ data[i]) & 0xffu] ^ (crc >> 8);
+    return ~crc;
+}
+
 /* runtime/src/reader.cpp:405-412. */
 uint64_t k3xo_fnv1a64(const char* name) {
     uint64_t h = 0xcbf29ce484222325ull;
@@ -771,4 +793,128 @@ uint64_t k3xo_fnv1a64(const char* name) {
         h *= 0x100000001b3ull;
     }
     return h;
+}
+
+/* ---- the whole layer, threaded (the CPU baseline of the benchmark) ------- */
+/* One layer over T tokens as the reference CPU backend composes it, token by
+ * token: rms_norm (runtime/src/ops.cpp:10-18), the router's double-sum
+ * logits and libm sigmoid + bias Top-K (runtime/src/model.cpp:917-1010,
+ * runtime/src/routing_policy.cpp:31-160), one expert FFN per (token, slot)
+ * pair (decode to fp32, double GEMVs, GLU: runtime/src/backend_cpu.cpp:
+ * 124-189, runtime/src/ops.cpp:57-76), the slot-ordered mix
+ * (backend_cpu.cpp:295-301) and the shared expert (bf16 weights, double
+ * sums).  The reference runs this on one thread; here the tokens and the
+ * pairs are spread over `nthreads` POSIX threads that take work items from a
+ * shared counter, so every item computes exactly what the one-thread run
+ * computes. */
+#include <pthread.h>
+#include <stdatomic.h>
+
+typedef struct {
+    const k3xo_layer_args* a;
+    int phase;                 /* 0 route, 1 pairs, 2 mix + shared */
+    atomic_size_t next;
+    atomic_int status;
+    float* xn;                 /* [T][H] */
+    uint32_t* ids;             /* [T][K] */
+    float* w;                  /* [T][K] */
+    float* y;                  /* [T][K][H] */
+    float* out;                /* [T][H] */
+} layer_job;
+
+static void layer_item(layer_job* j, size_t i) {
+    const k3xo_layer_args* a = j->a;
+    const size_t H = a->hidden, K = a->top_k, E = a->experts;
+    int st = K3XO_OK;
+    if (j->phase == 0) {
+        float* xn = j->xn + i * H;
+        float* logits = (float*)malloc(E * sizeof(float));
+        float* scores = (float*)malloc(E * sizeof(float));
+        if (!logits || !scores) {
+            st = K3XO_INVALID_STATE;
+        } else {
+            k3xo_rms_norm(xn, a->x + i * H, a->gamma, H, a->epsilon);
+            k3xo_router_logits(a->router, xn, E, H, K3XO_ORDER_SEQ, logits);
+            st = k3xo_route(logits, a->bias, E, K, a->renorm, a->routed_scale, K3XO_SIGMOID_REF,
+                            j->ids + i * K, j->w + i * K, scores);
+        }
+        free(logits);
+        free(scores);
+    } else if (j->phase == 1) {
+        const size_t t = i / K;
+        const uint32_t e = j->ids[i];
+        const uint8_t* const* ex = a->expert_bytes + (size_t)e * 6;
+        if (e >= E || !ex[0])
+            st = K3XO_INVALID_STATE;
+        else
+            st = k3xo_expert_ffn(j->xn + t * H, H, a->inter, ex[0], ex[1], ex[2], ex[3], ex[4],
+                                 ex[5], a->glu, a->beta, a->has_linear, a->linear_beta,
+                                 a->round_act, NULL, j->y + i * H);
+    } else {
+        float* o = j->out + i * H;
+        k3xo_ordered_mix(j->y + i * K * H, j->w + i * K, K, H, o);
+        if (a->shared_inter) {
+            float* s = (float*)malloc(H * sizeof(float));
+            if (!s) {
+                st = K3XO_INVALID_STATE;
+            } else {
+                k3xo_shared_ffn(j->xn + i * H, H, a->shared_inter, a->shared_gate, a->shared_up,
+                                a->shared_down, a->glu, a->beta, a->has_linear, a->linear_beta,
+                                a->round_act, s);
+                for (size_t h = 0; h < H; ++h) o[h] += s[h];
+                free(s);
+            }
+        }
+    }
+    if (st) {
+        int zero = 0;
+        atomic_compare_exchange_strong(&j->status, &zero, st);
+    }
+}
+
+static void* layer_worker(void* p) {
+    layer_job* j = (layer_job*)p;
+    const size_t n = j->phase == 1 ? j->a->tokens * j->a->top_k : j->a->tokens;
+    for (;;) {
+        const size_t i = atomic_fetch_add(&j->next, 1);
+        if (i >= n || atomic_load(&j->status)) break;
+        layer_item(j, i);
+    }
+    return NULL;
+}
+
+int k3xo_moe_layer(const k3xo_layer_args* a, int nthreads, uint32_t* ids_out,
+                   float* weights_out, float* out) {
+    const size_t T = a->tokens, K = a->top_k, H = a->hidden;
+    if (!T || !K || K > a->experts || nthreads < 1) return K3XO_INVALID_EXTENT;
+    layer_job j;
+    memset(&j, 0, sizeof j);
+    j.a = a;
+    j.xn = (float*)malloc(T * H * sizeof(float));
+    j.ids = ids_out;
+    j.w = weights_out;
+    j.y = (float*)malloc(T * K * H * sizeof(float));
+    j.out = out;
+    atomic_init(&j.status, 0);
+    if (!j.xn || !j.y) {
+        free(j.xn);
+        free(j.y);
+        return K3XO_INVALID_STATE;
+    }
+    pthread_t* th = (pthread_t*)malloc((size_t)nthreads * sizeof(pthread_t));
+    int st = th ? K3XO_OK : K3XO_INVALID_STATE;
+    for (int phase = 0; phase < 3 && !st; ++phase) {
+        j.phase = phase;
+        atomic_init(&j.next, 0);
+        int started = 0;
+        for (; started < nthreads - 1; ++started)
+            if (pthread_create(&th[started], NULL, layer_worker, &j)) break;
+        layer_worker(&j);
+        for (int q = 0; q < started; ++q) pthread_join(th[q], NULL);
+        st = atomic_load(&j.status);
+    }
+    free(th);
+    free(j.xn);
+    free(j.y);
+    return st;
 }

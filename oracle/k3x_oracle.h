@@ -139,6 +139,34 @@ int k3xo_official_ffn(const float* hidden, const float* prefix, size_t width,
                       float* expert_out, float* mixed_out, float* routed_out,
                       float* shared_out, float* out);
 
+/* ---- the whole layer, threaded (CPU baseline) ---------------------------*/
+/* expert_bytes: [experts][6] pointers (gate packed, gate scales, up packed,
+ * up scales, down packed, down scales); experts no route reaches may be
+ * NULL.  x: [tokens][hidden] input; shared_*: bf16 words (shared_inter 0:
+ * none). */
+typedef struct k3xo_layer_args {
+    const float* x;
+    const float* gamma;
+    float epsilon;
+    const float* router;
+    const float* bias;
+    size_t tokens, hidden, inter, experts, top_k, shared_inter;
+    float routed_scale;
+    int renorm;
+    const uint8_t* const* expert_bytes;
+    const uint16_t* shared_gate;
+    const uint16_t* shared_up;
+    const uint16_t* shared_down;
+    int glu;
+    float beta;
+    int has_linear;
+    float linear_beta;
+    int round_act;
+} k3xo_layer_args;
+/* ids_out, weights_out [tokens][top_k]; out [tokens][hidden]. */
+int k3xo_moe_layer(const k3xo_layer_args* a, int nthreads, uint32_t* ids_out,
+                   float* weights_out, float* out);
+
 /* ---- portable synthetic inputs (no reference counterpart) ---------------*/
 uint64_t k3xo_mix64(uint64_t z);
 uint64_t k3xo_stream_key(uint64_t seed, uint64_t stream);
@@ -153,6 +181,8 @@ void k3xo_synth_normal_bf16(uint64_t key, size_t n, float sigma,
 /* CRC32C (Castagnoli, reflected polynomial 0x82F63B78, register preset and
  * final inversion 0xFFFFFFFF), bit at a time: runtime/src/crc32c.cpp:6-28. */
 uint32_t k3xo_crc32c(const uint8_t* data, size_t n);
+/* The same value with the byte table of runtime/src/crc32c.cpp:7-28. */
+uint32_t k3xo_crc32c_table(const uint8_t* data, size_t n);
 /* FNV-1a 64 of a NUL-terminated name: runtime/src/reader.cpp:405-412. */
 uint64_t k3xo_fnv1a64(const char* name);
 

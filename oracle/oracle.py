@@ -66,6 +66,8 @@ class Oracle:
         L = self.lib = C.CDLL(path)
         L.k3xo_crc32c.restype = C.c_uint32
         L.k3xo_crc32c.argtypes = [_u8p, _sz]
+        L.k3xo_crc32c_table.restype = C.c_uint32
+        L.k3xo_crc32c_table.argtypes = [_u8p, _sz]
         L.k3xo_fnv1a64.restype = C.c_uint64
         L.k3xo_fnv1a64.argtypes = [C.c_char_p]
         L.k3xo_round_bf16.restype = C.c_float
@@ -77,6 +79,7 @@ class Oracle:
         L.k3xo_canon_dot.restype = C.c_double
         L.k3xo_canon_dot.argtypes = [_f32p, _f32p, _sz]
         L.k3xo_decode_mxfp4.argtypes = [_u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
+        L.k3xo_moe_layer.argtypes = [C.c_void_p, C.c_int, _u32p, _f32p, _f32p]
         L.k3xo_mxfp4_matvec.argtypes = [_f32p, _sz, _u8p, _sz, _u8p, _sz, _sz, _sz, _sz, _f32p]
         L.k3xo_rms_norm.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
         L.k3xo_rms_norm_canon.argtypes = [_f32p, _f32p, _f32p, _sz, C.c_float]
@@ -310,6 +313,10 @@ class Oracle:
         a = np.frombuffer(bytes(data), dtype=np.uint8)
         return int(self.lib.k3xo_crc32c(_p(np.ascontiguousarray(a), _u8p), a.size))
 
+    def crc32c_table(self, data) -> int:
+        a = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+        return int(self.lib.k3xo_crc32c_table(_p(a, _u8p), a.size))
+
     def fnv1a64(self, name: str) -> int:
         return int(self.lib.k3xo_fnv1a64(name.encode()))
 
@@ -348,6 +355,49 @@ class Oracle:
         return st, out
 
     # -- synthetic inputs -----------------------------------------------------
+    def moe_layer(self, x, gamma, eps, router, bias, experts, hidden, inter, top_k,
+                  routed_scale=1.0, renorm=RENORM_FLOAT, shared=None, glu=GLU_SWIGLU, beta=4.0,
+                  linear=None, round_act=False, threads=1):
+        """The whole layer over T tokens as the reference CPU backend composes
+        it (k3xo_moe_layer), on `threads` threads.  experts: sequence over all
+        expert ids of dicts of the six MXFP4 arrays, or None for experts no
+        route reaches; shared: (gate, up, down) bf16-word arrays or None.
+        Returns status, ids [T][K], weights [T][K], out [T][H]."""
+        x = f32(x)
+        T = x.shape[0]
+        E = len(experts)
+        keep = []
+        table = (_u8p * (6 * E))()
+        for e, ex in enumerate(experts):
+            if ex is None:
+                continue
+            for k, name in enumerate(("gate_packed", "gate_scales", "up_packed", "up_scales",
+                                      "down_packed", "down_scales")):
+                a = np.ascontiguousarray(ex[name], dtype=np.uint8)
+                keep.append(a)
+                table[6 * e + k] = _p(a, _u8p)
+        g, r, b = f32(gamma), f32(router), f32(bias)
+        sh = [np.ascontiguousarray(m, dtype=np.uint16) for m in shared] if shared else []
+        args = _LayerArgs()
+        args.x, args.gamma, args.epsilon = _p(x, _f32p), _p(g, _f32p), eps
+        args.router, args.bias = _p(r, _f32p), _p(b, _f32p)
+        args.tokens, args.hidden, args.inter, args.experts = T, hidden, inter, E
+        args.top_k = top_k
+        args.shared_inter = sh[0].shape[0] if sh else 0
+        args.routed_scale, args.renorm = routed_scale, renorm
+        args.expert_bytes = C.cast(table, C.POINTER(_u8p))
+        if sh:
+            args.shared_gate, args.shared_up, args.shared_down = (_p(m, _u16p) for m in sh)
+        args.glu, args.beta = glu, beta
+        args.has_linear, args.linear_beta = int(linear is not None), linear or 0.0
+        args.round_act = int(round_act)
+        ids = np.zeros((T, top_k), np.uint32)
+        w = np.zeros((T, top_k), np.float32)
+        out = np.zeros((T, hidden), np.float32)
+        st = self.lib.k3xo_moe_layer(C.byref(args), threads, _p(ids, _u32p), _p(w, _f32p),
+                                     _p(out, _f32p))
+        return st, ids, w, out
+
     def stream_key(self, seed: int, stream: int) -> int:
         return self.lib.k3xo_stream_key(seed, stream)
 
@@ -370,6 +420,17 @@ class Oracle:
         out = np.zeros(n, np.uint16)
         self.lib.k3xo_synth_normal_bf16(key, n, sigma, _p(out, _u16p))
         return out
+
+
+class _LayerArgs(C.Structure):
+    _fields_ = [("x", _f32p), ("gamma", _f32p), ("epsilon", C.c_float), ("router", _f32p),
+                ("bias", _f32p), ("tokens", _sz), ("hidden", _sz), ("inter", _sz),
+                ("experts", _sz), ("top_k", _sz), ("shared_inter", _sz),
+                ("routed_scale", C.c_float), ("renorm", C.c_int),
+                ("expert_bytes", C.POINTER(_u8p)), ("shared_gate", _u16p),
+                ("shared_up", _u16p), ("shared_down", _u16p), ("glu", C.c_int),
+                ("beta", C.c_float), ("has_linear", C.c_int), ("linear_beta", C.c_float),
+                ("round_act", C.c_int)]
 
 
 class _ExpertBytes(C.Structure):

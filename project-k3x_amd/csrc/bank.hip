@@ -160,7 +160,8 @@ int check_launch(k3x_hip_ctx* ctx, unsigned launches = 1) {
 void free_bank_memory(k3x_hip_bank* b) {
     for (void* p : {(void*)b->gu_codes, (void*)b->gu_scales, (void*)b->dn_codes,
                     (void*)b->dn_scales, (void*)b->sh_gu, (void*)b->sh_dn, (void*)b->router_w,
-                    (void*)b->router_wp, (void*)b->router_bias, (void*)b->gamma})
+                    (void*)b->router_wp, (void*)b->router_bias, (void*)b->gamma,
+                    (void*)b->ready_dev})
         if (p) (void)hipFree(p);
 }
 
@@ -234,6 +235,14 @@ int retile_shared(k3x_hip_bank* b, const uint16_t* src[3], uint64_t seed, float 
 }  // namespace
 
 namespace k3x_hip {
+
+int set_expert_ready(k3x_hip_bank* b, uint32_t e, bool ready) {
+    b->expert_ready[e] = ready ? 1 : 0;
+    return hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(b->ready_dev + e), ready ? 1 : 0, 1,
+                             b->ctx->stream) == hipSuccess
+               ? K3X_OK
+               : K3X_ERR_BACKEND_UNAVAILABLE;
+}
 
 int retile_expert_device(k3x_hip_bank* b, uint32_t e, const uint8_t* const src[6]) {
     const uint8_t* s[6];
@@ -514,6 +523,9 @@ int k3x_hip_bank_create(k3x_hip_ctx* ctx, const k3x_hip_layer_desc* desc, k3x_hi
                              &b->device_bytes);
     st = st ? st : alloc(&b->router_bias, E * sizeof(float), &b->device_bytes);
     st = st ? st : alloc(&b->gamma, (size_t)d.hidden * sizeof(float), &b->device_bytes);
+    st = st ? st : alloc(&b->ready_dev, E * sizeof(uint32_t), &b->device_bytes);
+    if (!st && hipMemset(b->ready_dev, 0, E * sizeof(uint32_t)) != hipSuccess)
+        st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (d.shared_inter) {
         b->sgate = geom(d.shared_inter, d.hidden);
         b->sdown = geom(d.hidden, d.shared_inter);
@@ -571,7 +583,7 @@ int k3x_hip_bank_upload_expert(k3x_hip_bank* bank, uint32_t expert, const uint64
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     // The slot is about to be overwritten: whatever it held is no longer
     // resident (its ids stop resolving to it, even if the upload fails).
-    bank->expert_ready[expert] = 0;
+    if (int st = k3x_hip::set_expert_ready(bank, expert, false)) return st;
     for (auto it = bank->tensor_ids.begin(); it != bank->tensor_ids.end();)
         it = it->second / 4 == expert ? bank->tensor_ids.erase(it) : std::next(it);
     // Staging buffer holding the six source arrays, each 256-byte aligned so
@@ -602,7 +614,7 @@ int k3x_hip_bank_upload_expert(k3x_hip_bank* bank, uint32_t expert, const uint64
     if (staging) (void)hipFree(staging);
     if (st) return st;
     for (int m = 0; m < 3; ++m) bank->tensor_ids[tensor_ids[m]] = expert * 4 + (uint32_t)m;
-    bank->expert_ready[expert] = 1;
+    if ((st = k3x_hip::set_expert_ready(bank, expert, true))) return st;
     ctx->weight_h2d_bytes += 3 * (pbytes + sbytes);
     return K3X_OK;
 }
@@ -641,15 +653,15 @@ int k3x_hip_bank_upload_expert_device(k3x_hip_bank* bank, uint32_t expert,
             if (ff) return K3X_ERR_INVALID_MXFP4;
         }
     }
-    bank->expert_ready[expert] = 0;
+    int st = k3x_hip::set_expert_ready(bank, expert, false);
+    if (st) return st;
     for (auto it = bank->tensor_ids.begin(); it != bank->tensor_ids.end();)
         it = it->second / 4 == expert ? bank->tensor_ids.erase(it) : std::next(it);
-    int st = k3x_hip::retile_expert_device(bank, expert, extents);
+    st = k3x_hip::retile_expert_device(bank, expert, extents);
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (st) return st;
     for (int m = 0; m < 3; ++m) bank->tensor_ids[tensor_ids[m]] = expert * 4 + (uint32_t)m;
-    bank->expert_ready[expert] = 1;
-    return K3X_OK;
+    return k3x_hip::set_expert_ready(bank, expert, true);
 }
 
 int k3x_hip_bank_find(k3x_hip_bank* bank, uint64_t tensor_id, uint32_t* expert, uint32_t* matrix) {
@@ -762,6 +774,9 @@ int k3x_hip_bank_fill_synthetic(k3x_hip_bank* bank, const k3x_hip_synth_desc* s)
         const uint16_t* none3[3] = {nullptr, nullptr, nullptr};
         st = retile_shared(bank, none3, s->seed, s->shared_sigma);
     }
+    if (!st && hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(bank->ready_dev), 1,
+                                 d.experts, ctx->stream) != hipSuccess)
+        st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (st) return st;
     std::fill(bank->expert_ready.begin(), bank->expert_ready.end(), 1);

@@ -85,6 +85,10 @@ struct k3x_hip_bank {
     bool router_ready = false;
     bool shared_ready = false;
     std::vector<uint8_t> expert_ready;
+    // Device copy of expert_ready ([E] words, 1 = admitted), kept in step on
+    // the context stream: the grouping rejects a device-given route to a slot
+    // that holds no admitted expert.
+    uint32_t* ready_dev = nullptr;
     std::unordered_map<uint64_t, uint32_t> tensor_ids;  // id -> expert*4+matrix
     uint64_t device_bytes = 0;
 };
@@ -178,6 +182,9 @@ int crc32c_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* cr
 int any_ff_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, bool* found);
 void free_crc(k3x_hip_ctx* ctx);
 int retile_expert_device(k3x_hip_bank* b, uint32_t e, const uint8_t* const src[6]);
+// Marks slot e admitted (1) or not (0) on the host and, in stream order, on
+// the device.
+int set_expert_ready(k3x_hip_bank* b, uint32_t e, bool ready);
 
 // Whether a bank of this hidden size keeps the residue-major router copy,
 // and that copy's size in floats (experts padded to 16).

@@ -619,6 +619,11 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     if (!T || !K || K > 64 || K > o->E) return K3X_ERR_INVALID_EXTENT;
     if (!std::isfinite(p->rms_epsilon) || !(p->rms_epsilon > 0.0f)) return K3X_ERR_INVALID_EXTENT;
     if (!o->ffn_ready || (!ids && !o->route_ready)) return K3X_ERR_INVALID_STATE;
+    // A route found on the device may pick any expert of the bank; a given
+    // route needs only its own slots admitted (checked by the grouping).
+    if (!ids)
+        for (uint8_t r : o->bank->expert_ready)
+            if (!r) return K3X_ERR_INVALID_STATE;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     FfnBuffers b;
     int st = ensure(o, carve(nullptr, o, T, K, &b));

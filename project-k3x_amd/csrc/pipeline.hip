@@ -680,12 +680,13 @@ __global__ __launch_bounds__(64) void topk_reg_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t group_tps(uint32_t K) { return min(64u, 1024u / K); }
 
+// ready (may be null): [E] words, 0 for a slot that holds no admitted expert.
 __device__ inline bool group_count_body(uint32_t c, const uint32_t* __restrict__ ids,
-                                                           uint32_t T, uint32_t K, uint32_t E,
-                                                           uint32_t* __restrict__ chunk_cnt,
-                                                           uint32_t* __restrict__ chunk_fu,
-                                                           uint8_t* __restrict__ rank,
-                                                           uint32_t* status) {
+                                        uint32_t T, uint32_t K, uint32_t E,
+                                        const uint32_t* __restrict__ ready,
+                                        uint32_t* __restrict__ chunk_cnt,
+                                        uint32_t* __restrict__ chunk_fu,
+                                        uint8_t* __restrict__ rank, uint32_t* status) {
     extern __shared__ uint32_t smem[];
     uint32_t* s_ids = smem;          // [1024] the chunk's ids
     uint32_t* mask = s_ids + 1024;   // [E][2] token bitmap per expert
@@ -703,7 +704,7 @@ __device__ inline bool group_count_body(uint32_t c, const uint32_t* __restrict__
     const uint32_t e = valid ? ids[p] : 0u;
     s_ids[tid] = e;
     __syncthreads();
-    int bad = valid && e >= E;
+    int bad = valid && (e >= E || (ready && !ready[e]));
     if (valid)
         for (uint32_t q = 0; q < s; ++q) bad |= s_ids[tl * K + q] == e;
     if (__syncthreads_or(bad)) {
@@ -729,9 +730,9 @@ __device__ inline bool group_count_body(uint32_t c, const uint32_t* __restrict__
 
 __global__ __launch_bounds__(1024) void group_count_kernel(
     const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
-    uint32_t* __restrict__ chunk_cnt, uint32_t* __restrict__ chunk_fu,
-    uint8_t* __restrict__ rank, uint32_t* status) {
-    (void)group_count_body(blockIdx.x, ids, T, K, E, chunk_cnt, chunk_fu, rank, status);
+    const uint32_t* __restrict__ ready, uint32_t* __restrict__ chunk_cnt,
+    uint32_t* __restrict__ chunk_fu, uint8_t* __restrict__ rank, uint32_t* status) {
+    (void)group_count_body(blockIdx.x, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, status);
 }
 
 // Exclusive scan of one 64-bit value per thread over a 1024-thread block;
@@ -935,13 +936,13 @@ __global__ __launch_bounds__(1024) void group_scatter_kernel(
 // memory written and read by this workgroup only).
 __global__ __launch_bounds__(1024) void group_single_kernel(
     const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
-    uint32_t* __restrict__ chunk_cnt, uint32_t* __restrict__ chunk_fu, uint8_t* __restrict__ rank,
+    const uint32_t* __restrict__ ready, uint32_t* __restrict__ chunk_cnt, uint32_t* __restrict__ chunk_fu, uint8_t* __restrict__ rank,
     uint32_t* __restrict__ counts, uint32_t* __restrict__ offsets,
     uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
     uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu,
     uint32_t* __restrict__ witems, uint32_t* __restrict__ n_witems, uint32_t chunk_rows,
     uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot, uint32_t* status) {
-    if (!group_count_body(0, ids, T, K, E, chunk_cnt, chunk_fu, rank, status)) return;
+    if (!group_count_body(0, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, status)) return;
     __syncthreads();
     if (!group_scan_body(T, K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active,
                          active_asc, active_fu, witems, n_witems, chunk_rows, status))
@@ -1351,7 +1352,8 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
 bool finite_pos(float v) { return std::isfinite(v) && v > 0.0f; }
 
 // all_experts: every bank slot must be admitted (routes decided on the
-// device may pick any); host routes check their own slots instead.
+// device may pick any); routes given by the caller check their own slots
+// instead (on the host copy when there is one, else in the grouping).
 int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                     bool all_experts = true) {
     const auto& d = bank->desc;
@@ -1378,24 +1380,27 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 }
 
 
+// ready (may be null): the bank's admitted-slot words; a route to another
+// slot is latched as K3X_ERR_INVALID_STATE.
 int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
-                 uint32_t* counts, uint32_t* offsets, uint32_t* pair_token, uint32_t* pair_slot,
-                 uint32_t* first_use, uint32_t* n_active, uint32_t* active_asc,
-                 uint32_t* active_fu, uint8_t* gscratch, uint32_t* witems = nullptr,
-                 uint32_t* n_witems = nullptr) {
+                 const uint32_t* ready, uint32_t* counts, uint32_t* offsets,
+                 uint32_t* pair_token, uint32_t* pair_slot, uint32_t* first_use,
+                 uint32_t* n_active, uint32_t* active_asc, uint32_t* active_fu,
+                 uint8_t* gscratch, uint32_t* witems = nullptr, uint32_t* n_witems = nullptr) {
     const uint32_t tps = std::min(64u, 1024u / K), nch = (T + tps - 1) / tps;
     uint32_t* chunk_cnt = reinterpret_cast<uint32_t*>(gscratch);
     uint32_t* chunk_fu = chunk_cnt + (size_t)nch * E;
     uint8_t* rank = reinterpret_cast<uint8_t*>(chunk_fu + (size_t)nch * E);
     if (nch == 1) {
         hipLaunchKernelGGL(group_single_kernel, dim3(1), dim3(1024), (size_t)(1024 + 3 * E) * 4,
-                           ctx->stream, ids, T, K, E, chunk_cnt, chunk_fu, rank, counts, offsets,
+                           ctx->stream, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, counts,
+                           offsets,
                            first_use, n_active, active_asc, active_fu, witems, n_witems,
                            k3x_hip::kWideRows, pair_token, pair_slot, ctx->status);
         return launched(ctx, 1);
     }
     hipLaunchKernelGGL(group_count_kernel, dim3(nch), dim3(1024), (size_t)(1024 + 3 * E) * 4,
-                       ctx->stream, ids, T, K, E, chunk_cnt, chunk_fu, rank, ctx->status);
+                       ctx->stream, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, ctx->status);
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(1024), (size_t)3 * E * 4, ctx->stream, T,
                        K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active, active_asc,
                        active_fu, witems, n_witems, k3x_hip::kWideRows, ctx->status);
@@ -1588,9 +1593,9 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         if (sst) return sst;
     }
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
-    int st = launch_group(ctx, ids, T, K, d.experts, s.counts, s.offsets, s.pair_token,
-                          s.pair_slot, s.first_use, s.n_active, s.active_asc, s.active_fu,
-                          s.gscratch, s.witems, s.n_witems);
+    int st = launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts, s.offsets,
+                          s.pair_token, s.pair_slot, s.first_use, s.n_active, s.active_asc,
+                          s.active_fu, s.gscratch, s.witems, s.n_witems);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -2015,7 +2020,7 @@ int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                                uint16_t* out, const k3x_hip_moe_taps* taps) {
     if (!ctx || !bank || !p || !xn || !ids || !weights || !out || bank->ctx != ctx)
         return K3X_ERR_INVALID_EXTENT;
-    int st = validate_params(bank, p, host_ids == nullptr);
+    int st = validate_params(bank, p, false);
     if (st) return st;
     const uint32_t T = p->tokens, K = p->top_k, E = bank->desc.experts;
     // Route contract of build_expert_major_plan (expert_major.cpp:21-36);
@@ -2053,7 +2058,8 @@ int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t to
     int st = k3x_hip::ensure_scratch(ctx, asc + group_scratch_bytes(tokens, top_k, experts));
     if (st) return st;
     uint8_t* base = static_cast<uint8_t*>(ctx->scratch);
-    return launch_group(ctx, ids, tokens, top_k, experts, t->counts, t->offsets, t->pair_token,
+    return launch_group(ctx, ids, tokens, top_k, experts, nullptr, t->counts, t->offsets,
+                        t->pair_token,
                         t->pair_slot, t->first_use, t->n_active, reinterpret_cast<uint32_t*>(base),
                         t->active_first_use, base + asc);
 }

@@ -481,6 +481,7 @@ int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32
         at[i] = total;
         total += (len[i] + 255) & ~(uint64_t)255;
     }
+    if (expert >= bank->desc.experts) return K3X_ERR_INVALID_MXFP4;
     k3x_hip_ctx* ctx = bank->ctx;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     if (total > s->pinned_bytes) {
@@ -517,6 +518,10 @@ int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32
     for (int i = 0; i < 6; ++i) ext[i] = s->staging + at[i];
     const uint64_t ids[3] = {rec[0]->id, rec[1]->id, rec[2]->id};
     const int st = k3x_hip_bank_upload_expert_device(bank, expert, ids, ext, crc);
+    // A rejection may return before the copy above has been waited for:
+    // drain it, so that no later call refills the pinned or staging buffer
+    // while this copy still reads or writes it.
+    if (st && hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     if (!st && bytes_read) *bytes_read = len[0] + len[1] + len[2] + len[3] + len[4] + len[5];
     return st;
 }

@@ -523,6 +523,16 @@ int main() {
         return 85;
 
     if (int rc = official_checks(*backend)) return rc;
+    // More slots than routed experts (the normal configuration): the official
+    // FFN admits only the called experts and leaves the other slots empty,
+    // which must not make the call fail.
+    {
+        auto roomy = k3x_amd::make_hip_backend({0, 8});
+        if (!roomy) return 3;
+        if (int rc = official_checks(*roomy.value())) return 200 + rc % 100;
+        if (roomy.value()->runtime_stats().experts_admitted >= 8) return 118;
+        std::printf("official with 8 slots, fewer admitted: ok\n");
+    }
 
     const auto s = backend->runtime_stats();
     std::printf("ok: %llu calls, %llu layer calls, %llu kernel launches, %llu admitted, %llu hits\n",

@@ -87,13 +87,20 @@ SHAPES = {"small": (256, 128, 128, 128, 8), "wide": (1024, 512, 512, 512, 16),
           "no_shared": (512, 256, 256, 0, 12), "many": (256, 128, 128, 128, 600)}
 
 
-@pytest.mark.parametrize("name,T,K", [("small", 1, 4), ("small", 5, 3), ("wide", 2, 8),
-                                      ("wide", 160, 8), ("no_shared", 33, 4), ("many", 2, 8),
-                                      ("small", 300, 4)])
-def test_official_layer(hip, oracle, name, T, K):
+# Cases: (shape, T, K, prefix offset in floats).  A prefix view 4 bytes off
+# 16-byte alignment runs the scalar output kernel (many rows); no_shared at
+# T=2 runs the few-row output epilogue without a shared FFN.
+@pytest.mark.parametrize("name,T,K,poff", [("small", 1, 4, 0), ("small", 5, 3, 0),
+                                           ("wide", 2, 8, 0), ("wide", 160, 8, 0),
+                                           ("no_shared", 33, 4, 0), ("no_shared", 2, 4, 0),
+                                           ("many", 2, 8, 0), ("small", 300, 4, 0),
+                                           ("wide", 40, 4, 1)],
+                         ids=["small_t1", "small_t5", "wide_t2", "wide_t160", "no_shared_t33",
+                              "no_shared_t2", "many_t2", "small_t300", "wide_t40_offset_prefix"])
+def test_official_layer(hip, oracle, name, T, K, poff, parity_report):
     k3x_amd, ctx = hip
     H, L, I, Is, E = SHAPES[name]
-    say(f"official layer {name} T={T} K={K}")
+    say(f"official layer {name} T={T} K={K} prefix offset {poff}")
     w, experts, bank, off = build(k3x_amd, ctx, oracle, SHAPES[name], 11 + T)
     dev = "cuda:0"
     params = k3x_amd.make_params(T, K, 1.0, EPS, k3x_amd.GLU_SITU, BETA, LINEAR,
@@ -110,7 +117,13 @@ def test_official_layer(hip, oracle, name, T, K):
     rng = np.random.default_rng(T)
     prefix = rng.standard_normal((T, H)).astype(np.float32)
     residual = rng.standard_normal((T, H)).astype(np.float32)
-    prefix_d = torch.from_numpy(prefix).to(dev)
+    if poff:
+        pbuf = torch.zeros(T * H + poff, dtype=torch.float32, device=dev)
+        pbuf[poff:] = torch.from_numpy(prefix.reshape(-1)).to(dev)
+        prefix_d = pbuf[poff:].view(T, H)
+        assert prefix_d.data_ptr() % 16 != 0
+    else:
+        prefix_d = torch.from_numpy(prefix).to(dev)
     residual_d = torch.from_numpy(residual).to(dev)
     logits = torch.empty((T, E), dtype=torch.float32, device=dev)
     assert off.prepare(T, EPS, prefix_d, residual_d, hidden, logits) == 0
@@ -137,43 +150,12 @@ def test_official_layer(hip, oracle, name, T, K):
     assert off.ffn(params, hidden, prefix_d, out, taps=taps) == 0
     assert ctx.synchronize() == 0
     got = {k: to_np(v) for k, v in taps.items()}
-    ids = got["ids"].view(np.uint32)
-    contrib = got["contributions"]
-    o = to_np(out).view(np.uint16)
-    exact = total = 0
-    num = den = 0.0
-    for t in range(T):
-        st, rid, rc, _ = oracle.route(got["logits"][t], w["correction"], K, RENORM_DOUBLE, 1.0,
-                                      SIGMOID_CR)
-        assert st == 0 and list(rid) == list(ids[t]), f"token {t} ids"
-        assert np.array_equal(rc.view(np.uint32), contrib[t].view(np.uint32))
-        ow = {k: w[k] for k in ("routed_down", "routed_norm", "routed_up")}
-        if Is:
-            ow.update(sh)
-        st, ref = oracle.official_ffn(hid_f[t], prefix[t], ow, [experts[i] for i in ids[t]],
-                                      contrib[t], EPS, GLU_SITU, BETA, LINEAR)
-        assert st == 0
-        # Intermediates: within 2e-2 of their own scale (their magnitudes
-        # follow the synthetic weights; the RMSNorm rescales the mix).
-        for key, g in (("latent", bf16_to_f32(got["latent"][t].view(np.uint16))),
-                       ("mixed", bf16_to_f32(got["mixed"][t].view(np.uint16))),
-                       ("routed", got["routed"][t]), ("shared", got["shared"][t])):
-            scale = max(float(np.abs(ref[key]).max()), 1e-30)
-            assert float(np.abs(g - ref[key]).max()) <= TOL * scale, f"token {t} {key}"
-        ref_bits = (ref["out"].view(np.uint32) >> 16).astype(np.uint16)
-        of = bf16_to_f32(o[t])
-        assert np.allclose(of, ref["out"], rtol=TOL, atol=TOL), f"token {t} out"
-        # Bulk: the differences are rounding-sized (the activation is bf16 on
-        # the MFMA path), far below the tolerance.
-        num += float(np.sum((of.astype(np.float64) - ref["out"]) ** 2))
-        den += float(np.sum(ref["out"].astype(np.float64) ** 2))
-        d = ulps_bf16(o[t], ref_bits)
-        exact += int((d <= 1).sum())
-        total += d.size
-    rel = (num / den) ** 0.5
-    say(f"ffn: ids/contributions bit-exact; out within {TOL}; relative error norm {rel:.2e}; "
-        f"{exact / total:.4f} of outputs within 1 bf16 ulp")
-    assert rel <= 2.0 ** -7
+    got["out"] = to_np(out).view(np.uint16)
+    ow = {k: w[k] for k in ("routed_down", "routed_norm", "routed_up")}
+    if Is:
+        ow.update(sh)
+    verify_ffn(oracle, ow, w["correction"], experts, got, hid_f, prefix, K, range(T),
+               parity_report)
     # The same route given by the caller gives the same output.
     out2 = torch.empty_like(out)
     assert off.ffn(params, hidden, prefix_d, out2, ids=taps["ids"],
@@ -185,6 +167,166 @@ def test_official_layer(hip, oracle, name, T, K):
     assert off.ffn(params, hidden, prefix_d, out2, ids=taps["ids"]) == k3x_amd.ERR_INVALID_EXTENT
     off.close()
     bank.close()
+
+
+def verify_ffn(oracle, ow, correction, experts, got, hid_f, prefix, K, tokens, report=None):
+    """The FFN taps and output of the given tokens against the oracle's layer
+    on the GPU's own hidden: ids and contributions bit-exact (the oracle's
+    route over the GPU's logits); intermediates within 2e-2 of their scale;
+    out within atol = rtol = 2e-2 and 2^-7 in relative error norm.
+    experts[i] gives expert i's six MXFP4 arrays."""
+    ids = got["ids"].view(np.uint32)
+    contrib = got["contributions"]
+    o = got["out"]
+    exact = total = 0
+    num = den = 0.0
+    for t in tokens:
+        st, rid, rc, _ = oracle.route(got["logits"][t], correction, K, RENORM_DOUBLE, 1.0,
+                                      SIGMOID_CR)
+        assert st == 0 and list(rid) == list(ids[t]), f"token {t} ids"
+        assert np.array_equal(rc.view(np.uint32), contrib[t].view(np.uint32))
+        st, ref = oracle.official_ffn(hid_f[t], prefix[t], ow, [experts[i] for i in ids[t]],
+                                      contrib[t], EPS, GLU_SITU, BETA, LINEAR)
+        assert st == 0
+        # Intermediates: within 2e-2 of their own scale (their magnitudes
+        # follow the synthetic weights; the RMSNorm rescales the mix).  The
+        # routed tap is the routed_up sum before its bf16 rounding.
+        for key, g in (("latent", bf16_to_f32(got["latent"][t].view(np.uint16))),
+                       ("mixed", bf16_to_f32(got["mixed"][t].view(np.uint16))),
+                       ("routed", got["routed"][t]), ("shared", got["shared"][t])):
+            scale = max(float(np.abs(ref[key]).max()), 1e-30)
+            assert float(np.abs(g - ref[key]).max()) <= TOL * scale, f"token {t} {key}"
+        ref_bits = (ref["out"].view(np.uint32) >> 16).astype(np.uint16)
+        of = bf16_to_f32(o[t])
+        ok = np.abs(of - ref["out"]) <= TOL + TOL * np.abs(ref["out"])
+        if not ok.all():
+            for key, g in (("latent", bf16_to_f32(got["latent"][t].view(np.uint16))),
+                           ("mixed", bf16_to_f32(got["mixed"][t].view(np.uint16))),
+                           ("routed", got["routed"][t]), ("shared", got["shared"][t])):
+                d = (g - ref[key]).astype(np.float64)
+                say(f"token {t} {key}: rel err norm {np.linalg.norm(d) / np.linalg.norm(ref[key]):.3e}, "
+                    f"max |d| {np.abs(d).max():.4g} at {int(np.abs(d).argmax())}, "
+                    f"scale {np.abs(ref[key]).max():.4g}")
+            bad = np.flatnonzero(~ok)
+            for i in bad[:8]:
+                say(f"token {t} out[{i}]: gpu {of[i]:.6g} ref {ref['out'][i]:.6g} prefix "
+                    f"{prefix[t][i]:.6g} routed gpu {got['routed'][t][i]:.6g} ref "
+                    f"{ref['routed'][i]:.6g} shared gpu {got['shared'][t][i]:.6g} ref "
+                    f"{ref['shared'][i]:.6g}")
+        assert ok.all(), f"token {t} out: {int((~ok).sum())} elements beyond atol = rtol = {TOL}"
+        # Bulk: the differences are rounding-sized (the activation is bf16 on
+        # the MFMA path), far below the tolerance.
+        num += float(np.sum((of.astype(np.float64) - ref["out"]) ** 2))
+        den += float(np.sum(ref["out"].astype(np.float64) ** 2))
+        d = ulps_bf16(o[t], ref_bits)
+        exact += int((d <= 1).sum())
+        total += d.size
+    rel = (num / den) ** 0.5
+    say(f"ffn: ids/contributions bit-exact; out within {TOL}; relative error norm {rel:.2e}; "
+        f"{exact / total:.4f} of outputs within 1 bf16 ulp")
+    if report:
+        report(f"{len(tokens)} tokens: ids/contributions bit-exact, out within {TOL}, "
+               f"relative error norm {rel:.2e}, {exact}/{total} = {exact / total:.4f} "
+               f"of outputs within 1 bf16 ulp")
+    assert rel <= 2.0 ** -7
+
+
+class SynthExperts:
+    """Experts of a bank filled by k3x_hip_bank_fill_synthetic, regenerated
+    on the CPU on demand (the bank's seeded streams)."""
+
+    def __init__(self, oracle, seed, hidden, inter, lo, hi):
+        from synth import Config, SynthLayer
+        self.layer = SynthLayer.__new__(SynthLayer)
+        self.layer.o = oracle
+        self.layer.cfg = Config("official_bank", 1, hidden, inter, 1, 1, 0, lo, hi, seed=seed)
+        self.layer._experts = {}
+
+    def __getitem__(self, e):
+        return self.layer.expert(int(e))
+
+
+def synth_official_weights(oracle, seed, H, L, Is, E, sigma, router_sigma, proj_sigma,
+                           corr_sigma):
+    """The weights k3x_hip_official_fill_synthetic writes, on the CPU (its
+    streams 1..9 of stream_key(seed, stream << 32))."""
+    key = lambda s: oracle.stream_key(seed, s << 32)
+    one = np.full(H, 0x3F80, np.uint16)
+    w = dict(routed_down=oracle.synth_normal_bf16(key(1), L * H, sigma).reshape(L, H),
+             routed_up=oracle.synth_normal_bf16(key(2), H * L, sigma).reshape(H, L),
+             routed_norm=np.full(L, 0x3F80, np.uint16),
+             residual_norm=one, post_norm=one,
+             residual_proj=oracle.synth_normal_bf16(key(6), H, proj_sigma),
+             router=oracle.synth_normal_bf16(key(8), E * H, router_sigma).reshape(E, H),
+             correction=oracle.synth_normal(key(9), E, corr_sigma))
+    if Is:
+        w.update(shared_gate=oracle.synth_normal_bf16(key(3), Is * H, sigma).reshape(Is, H),
+                 shared_up=oracle.synth_normal_bf16(key(4), Is * H, sigma).reshape(Is, H),
+                 shared_down=oracle.synth_normal_bf16(key(5), H * Is, sigma).reshape(H, Is))
+    return w
+
+
+# The official K3 layer at the shapes the bench runs it (hidden 7168, latent
+# 3584, 896 MXFP4 experts of 3072, Top-16, shared FFN 6144), on the bench's
+# synthetic weights: T=2 (decode kernels and split-K GEMVs) and T=2048 (wide
+# grouped GEMMs, matrix-core router) on sampled tokens.
+@pytest.mark.xfail(strict=True, reason=(
+    "the expert and shared GLU activations enter the bf16 MFMA down projection rounded to "
+    "bf16, where official_moe.cpp:82-117 keeps them in fp32 (and rounds the shared gate/up "
+    "to bf16 first); at this shape that puts ~3e-3 relative error on routed and shared and "
+    "8 of 7168 outputs per token past atol = rtol = 2e-2"))
+@pytest.mark.parametrize("T,tokens", [(2, (0, 1)), (2048, (0, 1031, 2047))],
+                         ids=["t2", "t2048"])
+def test_official_layer_benched_shape(hip, oracle, T, tokens, parity_report):
+    k3x_amd, ctx = hip
+    H, L, I, E, K, Is = 7168, 3584, 3072, 896, 16, 6144
+    seed_bank, seed_ffn = 0x4B3358 + 100, 0x4B3358 + 101
+    say(f"official layer at the benched shape T={T}")
+    bank = k3x_amd.Bank(ctx, k3x_amd.LayerShape(L, I, E, 0))
+    bank.fill_synthetic(seed_bank, 119, 123, 0.02, 0.1, 0.02, 1.0)
+    off = k3x_amd.Official(ctx, bank, H, Is)
+    off.fill_synthetic(seed_ffn, 0.02, 0.02, 0.05, 0.1)
+    dev = "cuda:0"
+    rng = np.random.default_rng(T)
+    prefix = rng.standard_normal((T, H)).astype(np.float32)
+    residual = rng.standard_normal((T, H)).astype(np.float32)
+    prefix_d = torch.from_numpy(prefix).to(dev)
+    residual_d = torch.from_numpy(residual).to(dev)
+    hidden = torch.empty((T, H), dtype=torch.int16, device=dev)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    params = k3x_amd.make_params(T, K, 1.0, EPS, k3x_amd.GLU_SITU, BETA, LINEAR,
+                                 k3x_amd.RENORM_DOUBLE)
+    z = lambda shape, dt: torch.empty(shape, dtype=dt, device=dev)
+    taps = dict(ids=z((T, K), torch.int32), contributions=z((T, K), torch.float32),
+                latent=z((T, L), torch.int16), mixed=z((T, L), torch.int16),
+                routed=z((T, H), torch.float32), shared=z((T, H), torch.float32),
+                logits=z((T, E), torch.float32))
+    assert off.prepare(T, EPS, prefix_d, residual_d, hidden) == 0
+    assert off.ffn(params, hidden, prefix_d, out, taps=taps) == 0
+    assert ctx.synchronize() == 0
+    got = {k: to_np(v) for k, v in taps.items()}
+    got["out"] = to_np(out).view(np.uint16)
+    hid = to_np(hidden).view(np.uint16)
+    off.close()
+    bank.close()
+    w = synth_official_weights(oracle, seed_ffn, H, L, Is, E, 0.02, 0.02, 0.05, 0.1)
+    W = bf16_to_f32(w["router"])
+    hid_f = bf16_to_f32(hid)
+    worst = 0
+    for t in tokens:
+        st, ref = oracle.official_prepare(prefix[t], residual[t], w["residual_norm"],
+                                          w["residual_proj"], w["post_norm"], EPS)
+        assert st == 0
+        worst = max(worst, int(ulps_bf16(hid[t], (ref.view(np.uint32) >> 16).astype(np.uint16)).max()))
+        assert np.array_equal(got["logits"][t].view(np.uint32),
+                              oracle.router_logits(W, hid_f[t], ORDER_CANON).view(np.uint32))
+    assert worst <= 1, f"prepared hidden {worst} bf16 ulps off"
+    say(f"prepare: hidden within {worst} ulp, logits bit-exact on tokens {tokens}")
+    experts = SynthExperts(oracle, seed_bank, L, I, 119, 123)
+    ow = {k: w[k] for k in ("routed_down", "routed_norm", "routed_up", "shared_gate",
+                            "shared_up", "shared_down")}
+    verify_ffn(oracle, ow, w["correction"], experts, got, hid_f, prefix, K, tokens,
+               parity_report)
 
 
 def test_route_only_object(hip, oracle):

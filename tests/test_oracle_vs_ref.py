@@ -174,3 +174,31 @@ def test_layer_token_bitexact(oracle, reflib):
                                round_act=False)
         out = (mixed + sh).astype(np.float32)
         assert np.array_equal(bits(out), bits(out_ref))
+
+
+@pytest.mark.parametrize("threads", [1, 3])
+def test_threaded_layer_bitexact(oracle, reflib, threads):
+    """k3xo_moe_layer (the bench's CPU baseline: tokens and pairs spread over
+    threads) equals the reference's own one-token composition, token by
+    token, at any thread count."""
+    rng = np.random.default_rng(31)
+    H, I, E, K, S, T = 256, 512, 16, 4, 256, 5
+    experts = [rand_expert(rng, H, I, 121, 125) for _ in range(E)]
+    router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    gamma = np.ones(H, np.float32)
+    words = lambda r, c: ((rng.standard_normal((r, c)) * 0.02).astype(np.float32)
+                          .view(np.uint32) >> 16).astype(np.uint16)
+    shared_bits = (words(S, H), words(S, H), words(H, S))
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    st, ids, _, out = oracle.moe_layer(x, gamma, 1e-6, router, bias, experts, H, I, K, 2.5,
+                                       RENORM_FLOAT, shared_bits, GLU_SITU, 4.0,
+                                       threads=threads)
+    assert st == OK
+    for t in range(T):
+        st, ids_ref, out_ref = reflib.moe_layer_token(
+            x[t], gamma, 1e-6, router, bias, experts, H, I, K, 2.5,
+            tuple(bf16_to_f32(m) for m in shared_bits), beta=4.0)
+        assert st == OK
+        assert np.array_equal(ids[t], ids_ref)
+        assert np.array_equal(bits(out[t]), bits(out_ref))

@@ -30,6 +30,19 @@ def test_crc32c_vs_reference(oracle, reflib):
         assert oracle.crc32c(data) == reflib.crc32c(data)
 
 
+def test_crc32c_table_method(oracle):
+    """The byte-table restatement the bench times (k3xo_crc32c_table, the
+    method of runtime/src/crc32c.cpp) gives the bit-at-a-time value, the
+    RFC 3720 check values included."""
+    assert oracle.crc32c_table(b"123456789") == 0xE3069283
+    assert oracle.crc32c_table(b"") == 0
+    assert oracle.crc32c_table(bytes(32)) == 0x8A9136AA
+    rng = np.random.default_rng(4)
+    for n in (1, 2, 255, 4096, 65_537):
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert oracle.crc32c_table(data) == oracle.crc32c(data)
+
+
 def test_fnv1a64_known_answers(oracle):
     # Published FNV-1a 64 values (Fowler/Noll/Vo test suite).
     assert oracle.fnv1a64("") == 0xCBF29CE484222325
