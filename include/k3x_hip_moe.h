@@ -293,6 +293,28 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                         const k3x_hip_moe_params* params, const uint16_t* x,
                         uint16_t* out, const k3x_hip_moe_taps* taps);
 
+/* Bytes of the fixed device scratch behind k3x_hip_moe_forward_noalloc. */
+#define K3X_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* k3x_hip_moe_forward that allocates nothing: no reference counterpart.  It
+ * is for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The
+ * per-call buffers (normalised input, logits, routes, grouping, activations,
+ * per-pair outputs, shared expert) come from a fixed device array of
+ * K3X_HIP_NOALLOC_SCRATCH_BYTES per device (32 MiB, held until the process
+ * ends) instead of the context's grow-only scratch; a call whose buffers do
+ * not fit returns K3X_ERR_INVALID_EXTENT before anything is enqueued (the
+ * config-3 decode layer needs about 1.1 MiB, T=16 of it about 9 MiB).  The
+ * array is shared by every call on the device, whatever the context or
+ * stream: calls that overlap on one GPU race, so a caller serialises them
+ * (one stream, or events).  Nothing in it needs to start at zero; every
+ * buffer a call reads was written earlier in the same call.  Stage timing
+ * (k3x_hip_ctx_set_profiling) is not recorded for these calls.  Results are
+ * bit-identical to k3x_hip_moe_forward's.  Asynchronous. */
+int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                                const k3x_hip_moe_params* params, const uint16_t* x,
+                                uint16_t* out, const k3x_hip_moe_taps* taps);
+
 /* The same layer with host-decided routes (the reference's own contract:
  * routing on the host, model.cpp:917-1010): xn is the already-normalised
  * bf16 input [T][hidden], ids/weights device [T][K] in router order.  Routes

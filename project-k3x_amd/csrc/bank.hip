@@ -404,6 +404,11 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
     ctx->max_lds_per_block = (size_t)lds;
     ctx->cu_count = (uint32_t)cus;
     ctx->stream = ctx->own_stream;
+    // The no-allocation entry point's fixed scratch on this device (device
+    // current); without it that entry point reports backend_unavailable and
+    // the rest of the library is unaffected.
+    if (k3x_hip::noalloc_scratch(device, &ctx->noalloc_scratch) != K3X_OK)
+        ctx->noalloc_scratch = nullptr;
     *out = ctx;
     return K3X_OK;
 }

@@ -32,6 +32,9 @@ struct k3x_hip_ctx {
     // Grow-only scratch (replaces runtime/cuda/device_memory.cuh:44-61).
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Device address of the fixed scratch of k3x_hip_moe_forward_noalloc on
+    // this context's device (null when it could not be taken).
+    void* noalloc_scratch = nullptr;
     uint64_t forward_calls = 0;
     uint64_t kernel_launches = 0;
     uint64_t weight_h2d_bytes = 0;
@@ -127,6 +130,10 @@ inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BA
 
 // Makes sure ctx->scratch holds at least `bytes`; grow-only.
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
+
+// Device address of the fixed no-allocation scratch on `device`, which must
+// be current; taken once per device and kept.
+int noalloc_scratch(int device, void** out);
 
 // Refreshes bank->router_wp from bank->router_w on the context stream (a
 // no-op when the hidden size has no residue-major copy).

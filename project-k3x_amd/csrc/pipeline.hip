@@ -10,6 +10,9 @@
 //   combine_kernel   slot-ordered weighted sum + shared expert, bf16 cast
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <vector>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -1977,14 +1980,16 @@ int launch_combine(k3x_hip_ctx* ctx, const float* y, const float* weights, const
 
 extern "C" {
 
-int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
-                        const uint16_t* x, uint16_t* out, const k3x_hip_moe_taps* taps) {
-    if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
-    int st = validate_params(bank, p);
-    if (st) return st;
-    if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
-    Scratch s;
-    if ((st = prepare(ctx, bank, p, &s))) return st;
+}  // extern "C"
+
+namespace {
+
+// The layer with device routing over the per-call buffers `s` (already laid
+// out): the decode path when it applies, else the general path.
+int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                          const Scratch& s, const uint16_t* x, uint16_t* out,
+                          const k3x_hip_moe_taps* taps) {
+    int st = K3X_OK;
     if (!(p->flags & (K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)) &&
         k3x_hip::decode_eligible(ctx, bank, p, x)) {
         if ((st = k3x_hip::decode_forward(ctx, bank, p, s, x, out,
@@ -2011,6 +2016,74 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
         return st;
     ++ctx->forward_calls;
     return copy_taps(ctx, bank, p, s, s.xn, s.ids, s.weights, taps);
+}
+
+}  // namespace
+
+// Scratch of k3x_hip_moe_forward_noalloc: the per-call buffers live in this
+// fixed array instead of the context's grow-only allocation.  In host code
+// `scratch` names a host-side stand-in, never the device memory: the device
+// address comes from hipGetSymbolAddress, taken once per device
+// (k3x_hip::noalloc_scratch) and kept in the context; only that address is
+// passed to kernels.  Each device holds its own copy for the life of the
+// process, shared by every no-allocation call on that device.
+static __device__ __align__(256) uint8_t scratch[K3X_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace k3x_hip {
+
+int noalloc_scratch(int device, void** out) {
+    static std::mutex mu;
+    static std::vector<void*> by_device;
+    std::lock_guard<std::mutex> lock(mu);
+    if (device < 0) return K3X_ERR_INVALID_EXTENT;
+    if ((size_t)device >= by_device.size()) by_device.resize((size_t)device + 1, nullptr);
+    if (!by_device[device]) {
+        void* ptr = nullptr;  // with `device` current (the caller's hipSetDevice)
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+            (void)hipGetLastError();
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        by_device[device] = ptr;
+    }
+    *out = by_device[device];
+    return K3X_OK;
+}
+
+}  // namespace k3x_hip
+
+extern "C" {
+
+int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                        const uint16_t* x, uint16_t* out, const k3x_hip_moe_taps* taps) {
+    if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    int st = validate_params(bank, p);
+    if (st) return st;
+    if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
+    Scratch s;
+    if ((st = prepare(ctx, bank, p, &s))) return st;
+    return forward_device_routed(ctx, bank, p, s, x, out, taps);
+}
+
+int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                                const k3x_hip_moe_params* p, const uint16_t* x, uint16_t* out,
+                                const k3x_hip_moe_taps* taps) {
+    if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    int st = validate_params(bank, p);
+    if (st) return st;
+    if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
+    if (!ctx->noalloc_scratch) return K3X_ERR_BACKEND_UNAVAILABLE;
+    Scratch s;
+    if (carve(nullptr, bank->desc, p->tokens, p->top_k, &s) > K3X_HIP_NOALLOC_SCRATCH_BYTES)
+        return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    carve(static_cast<uint8_t*>(ctx->noalloc_scratch), bank->desc, p->tokens, p->top_k, &s);
+    // Stage timing takes events from a pool that may have to create them:
+    // not on this path.
+    const bool profiling = ctx->profiling;
+    ctx->profiling = false;
+    st = forward_device_routed(ctx, bank, p, s, x, out, taps);
+    ctx->profiling = profiling;
+    return st;
 }
 
 int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,

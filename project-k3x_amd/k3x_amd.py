@@ -145,6 +145,8 @@ _SIGS = {
     "k3x_hip_bank_bytes": (C.c_uint64, [_vp]),
     "k3x_hip_moe_forward": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp,
                                       C.POINTER(MoeTaps)]),
+    "k3x_hip_moe_forward_noalloc": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp,
+                                              C.POINTER(MoeTaps)]),
     "k3x_hip_moe_forward_routed": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp, _vp, _vp,
                                              _vp, _vp, C.POINTER(MoeTaps)]),
     "k3x_hip_expert_major_plan": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
@@ -460,6 +462,14 @@ def moe_forward(ctx: Context, bank: Bank, params: MoeParams, x, out, taps=None) 
     t = make_taps(taps)
     return ctx.lib.k3x_hip_moe_forward(ctx.handle, bank.handle, C.byref(params), ptr(x),
                                        ptr(out), C.byref(t) if t is not None else None)
+
+
+def moe_forward_noalloc(ctx: Context, bank: Bank, params: MoeParams, x, out, taps=None) -> int:
+    """k3x_hip_moe_forward over the library's fixed device scratch (no device
+    allocation in the call)."""
+    t = make_taps(taps)
+    return ctx.lib.k3x_hip_moe_forward_noalloc(ctx.handle, bank.handle, C.byref(params), ptr(x),
+                                               ptr(out), C.byref(t) if t is not None else None)
 
 
 def moe_forward_routed(ctx: Context, bank: Bank, params: MoeParams, xn, ids, weights, out,
