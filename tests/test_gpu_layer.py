@@ -478,7 +478,8 @@ def test_repeated_decode_calls(hip, oracle, c3):
     k3x_amd, ctx = hip
     cfg, layer, bank = c3
     import dataclasses
-    for i, T in enumerate((2, 2, 1, 2, 1)):
+    # Every decode-path token count, 1 to 4 (16 to 64 pairs).
+    for i, T in enumerate((2, 2, 1, 2, 1, 4, 3)):
         x = oracle.synth_normal_bf16(oracle.stream_key(cfg.x_seed + 100 + i, sid(STREAM_INPUT)),
                                      T * cfg.hidden, 1.0).reshape(T, cfg.hidden)
         c = dataclasses.replace(cfg, tokens=T)
