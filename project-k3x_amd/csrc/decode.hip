@@ -63,29 +63,6 @@ __device__ inline double canon_reduce(const double p[4]) {
     return v;
 }
 
-// Block-wide exclusive scan of one value per thread (512 threads).  Returns
-// the exclusive prefix; *total receives the sum.
-__device__ inline uint32_t block_scan_excl(uint32_t v, uint32_t* wave_sums, uint32_t* total) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-    }
-    if (lane == 63) wave_sums[wave] = incl;
-    __syncthreads();
-    uint32_t base = 0, all = 0;
-    for (int w = 0; w < kFrontWaves; ++w) {
-        const uint32_t s = wave_sums[w];
-        if (w < wave) base += s;
-        all += s;
-    }
-    __syncthreads();
-    *total = all;
-    return base + incl - v;
-}
-
 // ---------------------------------------------------------------------------
 // MXFP4 step helpers: one 128-K tile of S 16-row blocks (codes [S][64] x
 // 16 B, one E8M0 byte per lane per block), dequantised in registers and
@@ -373,14 +350,16 @@ __device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[w][j] = tiles[(((size_t)k * 2 + w) * 4 + j) * 64];
     };
-    auto prefetch = [&]() {
-#pragma unroll
-        for (int d = 0; d < PD; ++d) load(bn[d], min(k0 + d, kt - 1));
-    };
-    // A non-finite x is reported by the router blocks.
+    // The weights are requested only once xn is built: requested with the
+    // x / gamma loads, the 59 MB of shared gate/up tiles would queue ahead
+    // of the router blocks' x / gamma and router rows, which are on the
+    // layer's critical path.  A non-finite x is reported by the router
+    // blocks.
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr,
-                                 a.status, prefetch))
+                                 a.status, [] {}))
         return;
+#pragma unroll
+    for (int d = 0; d < PD; ++d) load(bn[d], min(k0 + d, kt - 1));
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
     const uint16_t* xrow = s_x + (size_t)(n < T ? n : 0) * H + 32 * g;  // unused rows: row 0
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -459,117 +438,291 @@ struct SelectArgs {
     uint32_t* active_asc;
     uint32_t* active_fu;
     uint4* arec;         // [E] per active slot: {expert, rows, offset, row tokens}
-    const uint4* sh_dn;  // shared down tiles [H/16][S/128][4][64] x 16 B
-    const uint16_t* sact;  // [T][S]
-    uint32_t H, S;
-    float* sy;           // [T][H] shared expert output, fp32
+    uint32_t group_taps; // nonzero: also counts, offsets, first_use, active_asc, active_fu
     uint32_t* status;
 };
 
-struct SelectShared {
-    int bad;
-    uint32_t wave_sums[kFrontWaves];
-    uint32_t ids[kMaxDecodeTokens * 64];
-    uint32_t cnt[kKeysPerLane * 64];
-    uint32_t fu[kKeysPerLane * 64];
-    uint32_t off[kKeysPerLane * 64];
-    uint32_t active[kMaxDecodeTokens * 64];
-    uint32_t ptok[kMaxDecodeTokens * 64];
+// The shared expert's down projection: the select launch's other workgroups.
+struct SharedDownArgs {
+    const uint4* sh_dn;    // shared down tiles [H/16][S/128][4][64] x 16 B
+    const uint16_t* sact;  // [T][S] bf16 shared activation
+    uint32_t T, H, S;
+    float* sy;             // [T][H] shared expert output, fp32
+    const uint32_t* status;
 };
 
-// Top-K of one token by one wave (topk_wave, 8 keys per lane); the ids and
-// weights go to the outputs and to the block's grouping.
-// lg / bv: the token's logits and the bias of experts lane + 64 i (loaded
-// by the caller, before its status check).
-__device__ void topk_token(const SelectArgs& a, uint32_t t, const float (&lgv)[kKeysPerLane],
-                           const float (&bv)[kKeysPerLane], SelectShared& sh) {
-    const int lane = threadIdx.x & 63;
-    uint32_t selid;
-    float w;
-    const uint32_t err = topk_wave<kKeysPerLane>(lgv, bv, a.E, a.K, a.renorm == K3X_RENORM_DOUBLE,
-                                                 a.routed_scale, &selid, &w);
-    if (err) {
-        if (lane == 0) {
-            latch(a.status, err);
-            sh.bad = 1;
+// Block 0 of the select kernel: natural Top-K of every token and the
+// expert-major grouping, by all eight waves.  Thread e owns expert e of every
+// token (E <= kSelExperts).
+//   keys       sigmoid + bias, the validation and the sort key of topk_wave
+//              (score order, then the lower expert index);
+//   threshold  the maximum score half of each 16-expert group (DPP row
+//              rotates); with G groups and K <= G, the K-th largest group
+//              maximum tau has at least K keys at or above it (one per group
+//              at or above tau), so no key with score half below tau can be
+//              selected;
+//   survivors  the keys at or above tau (every key when K > G) are compacted
+//              per token and ranked exactly among themselves by the full
+//              64-bit key (keys are distinct: the low half holds the
+//              expert); rank r < K is router slot r;
+//   renorm     one wave per token, sequential sums in slot order, as
+//              topk_wave;
+//   grouping   per pair p = token * K + slot, counts of equal and smaller
+//              expert ids among the P = T * K pairs give the CSR row, the
+//              active index and the first-use rank directly
+//              (runtime/src/expert_major.cpp:10-54), with no atomics.
+constexpr uint32_t kSelExperts = kKeysPerLane * 64;  // experts per token: E <= 512
+constexpr uint32_t kSelGroups = kSelExperts / 16;    // 16-expert groups
+constexpr uint32_t kSelMaxPairs = kMaxDecodeTokens * 64;
+constexpr uint32_t kRankThreads = kFrontThreads / kMaxDecodeTokens;  // per token
+static_assert(kSelGroups <= 32, "one lane per group in half a wave");
+static_assert(kFrontWaves >= 2 * kMaxDecodeTokens, "renormalisation waves apart from the pairs'");
+
+struct SelectShared {
+    uint64_t ckey[kMaxDecodeTokens][kSelExperts];  // survivors' keys, compacted, 0 past them
+    uint32_t cid[kMaxDecodeTokens][kSelExperts];   // survivors' experts
+    float csc[kMaxDecodeTokens][kSelExperts];      // survivors' sigmoid scores
+    uint32_t gmax[kMaxDecodeTokens][kSelGroups];   // group maxima of the score half
+    uint32_t thr[kMaxDecodeTokens];                // survivor threshold tau
+    uint32_t ncand[kMaxDecodeTokens];
+    uint32_t sel[kSelMaxPairs];      // expert of pair t * K + s
+    float selsc[kSelMaxPairs];       // its sigmoid score
+    float selw[kSelMaxPairs];        // its contribution
+    uint32_t first[kSelMaxPairs];    // 1: the pair is its expert's first use
+    uint32_t rowtok[kSelMaxPairs];   // token of CSR row r
+    uint32_t bad;
+};
+
+// Top-K of the T tokens into sh.sel / sh.selsc (router order); false (error
+// latched) when a score fails its check.  lg[t]: logit of expert tid for
+// token t; b: bias of expert tid.
+__device__ bool select_topk(const SelectArgs& a, SelectShared& sh,
+                            const float (&lg)[kMaxDecodeTokens], float b) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t T = a.T, K = a.K, e = tid;
+    const bool dbl = a.renorm == K3X_RENORM_DOUBLE;
+    const bool valid = e < a.E;
+    constexpr uint32_t kErrExtent = K3X_ERR_INVALID_EXTENT, kErrState = K3X_ERR_INVALID_STATE;
+    if (tid < kMaxDecodeTokens) sh.ncand[tid] = 0;
+    if (tid == 0) sh.bad = 0;
+    // Candidate keys past the survivors stay 0, below every real key, and
+    // pairs past T * K hold expert 0xffffffff, above every real one (the
+    // loops read whole batches of eight).
+#pragma unroll
+    for (int t = 0; t < kMaxDecodeTokens; ++t) sh.ckey[t][tid] = 0;
+    if (tid < kSelMaxPairs) {
+        sh.sel[tid] = 0xffffffffu;
+        sh.first[tid] = 0;
+    }
+    // Keys and validation (runtime/src/routing_policy.cpp:40-95,
+    // runtime/src/official_moe.cpp:214-232), as topk_wave; experts past E
+    // hold key 0, below every real key.  Group maxima over rows of 16 lanes
+    // (all lanes active for the DPP moves).
+    uint64_t key[kMaxDecodeTokens];
+    float sc[kMaxDecodeTokens];
+    uint32_t err = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxDecodeTokens; ++t) {
+        key[t] = 0;
+        sc[t] = 0.0f;
+        if ((uint32_t)t >= T) continue;
+        if (valid) {
+            if (dbl && (!__builtin_isfinite(lg[t]) || !__builtin_isfinite(b))) err = kErrExtent;
+            const float s = sigmoid_cr(lg[t]);
+            const float adj = __fadd_rn(s, b);
+            if (!dbl && (!__builtin_isfinite(s) || s < 0.0f || s > 1.0f || !__builtin_isfinite(b) ||
+                         !__builtin_isfinite(adj)))
+                err = kErrState;
+            sc[t] = s;
+            key[t] = topk_key(adj, e);
         }
-        return;
+        uint32_t m = (uint32_t)(key[t] >> 32);
+        m = dpp_max_step<0x128, 0xf>(m);  // row_ror:8
+        m = dpp_max_step<0x124, 0xf>(m);  // row_ror:4
+        m = dpp_max_step<0x122, 0xf>(m);  // row_ror:2
+        m = dpp_max_step<0x121, 0xf>(m);  // row_ror:1
+        if ((lane & 15) == 0) sh.gmax[t][tid >> 4] = m;
     }
-    if ((uint32_t)lane < a.K) {
-        a.ids[(size_t)t * a.K + lane] = selid;
-        a.weights[(size_t)t * a.K + lane] = w;
-        sh.ids[t * a.K + lane] = selid;
+    __syncthreads();
+    if (err) atomicMax(&sh.bad, err);
+    // tau of token t by wave t: the group maximum m with fewer than K larger
+    // maxima and at least K at or above it (lanes 32..63 repeat 0..31).
+    const uint32_t G = (a.E + 15) / 16;
+    if (wave < T) {
+        const uint32_t t = wave, g = lane & 31;
+        uint32_t th = 0;
+        if (K <= G) {
+            const uint32_t m = sh.gmax[t][g];
+            uint32_t gt = 0, ge = 0;
+            const uint4* gm = reinterpret_cast<const uint4*>(sh.gmax[t]);
+            for (uint32_t g4 = 0; g4 < (G + 3) / 4; ++g4) {  // groups past G hold 0
+                const uint4 v = gm[g4];
+                gt += (v.x > m) + (v.y > m) + (v.z > m) + (v.w > m);
+                ge += (v.x >= m) + (v.y >= m) + (v.z >= m) + (v.w >= m);
+            }
+            const uint64_t q = __ballot(g < G && gt < K && K <= ge);
+            if (q) th = (uint32_t)__builtin_amdgcn_readlane((int)m, (int)__builtin_ctzll(q));
+        }
+        if (lane == 0) sh.thr[t] = th;
     }
+    __syncthreads();
+    if (sh.bad) {
+        if (tid == 0) latch(a.status, sh.bad);
+        return false;
+    }
+    // Compact the survivors (their order in the list does not matter: the
+    // ranking is exact).
+#pragma unroll
+    for (int t = 0; t < kMaxDecodeTokens; ++t) {
+        if ((uint32_t)t >= T) continue;
+        const bool surv = valid && (uint32_t)(key[t] >> 32) >= sh.thr[t];
+        const uint64_t m = __ballot(surv);
+        if (!m) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&sh.ncand[t], (uint32_t)__popcll(m));
+        base = __builtin_amdgcn_readfirstlane(base);
+        if (surv) {
+            const uint32_t c = base + (uint32_t)__popcll(m & ((1ull << lane) - 1));
+            sh.ckey[t][c] = key[t];
+            sh.cid[t][c] = e;
+            sh.csc[t][c] = sc[t];
+        }
+    }
+    __syncthreads();
+    // Exact rank among the survivors, kRankThreads threads per token; rank
+    // r < K is slot r.
+    const uint32_t rt = tid / kRankThreads;
+    if (rt < T) {
+        const uint32_t n = sh.ncand[rt];
+        const ulonglong2* ck = reinterpret_cast<const ulonglong2*>(&sh.ckey[rt][0]);
+        for (uint32_t c = tid % kRankThreads; c < n; c += kRankThreads) {
+            const uint64_t k = sh.ckey[rt][c];
+            uint32_t r = 0;
+            for (uint32_t c2 = 0; c2 < n; c2 += 8) {  // zero-padded past n
+                ulonglong2 kk[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) kk[q] = ck[c2 / 2 + q];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) r += (kk[q].x > k) + (kk[q].y > k);
+            }
+            if (r < K) {
+                sh.sel[rt * K + r] = sh.cid[rt][c];
+                sh.selsc[rt * K + r] = sh.csc[rt][c];
+            }
+        }
+    }
+    __syncthreads();
+    return true;
 }
 
-// Expert-major grouping of the T*K selected pairs by the whole block:
-// ascending-expert CSR, rows of one expert in (token, slot) order, plus
-// first-use keys and the first-use order of the active experts
-// (runtime/src/expert_major.cpp:10-54).
-__device__ void group_pairs(const SelectArgs& a, SelectShared& sh) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t P = a.T * a.K, E = a.E;
-    for (uint32_t e = tid; e < E; e += kFrontThreads) {
-        sh.cnt[e] = 0;
-        sh.fu[e] = 0xffffffffu;
+// Renormalisation of the Top-K and the expert-major grouping of the P = T *
+// K selected pairs (pair p = token * K + slot): ascending-expert CSR with the
+// rows of one expert in pair order and the active-slot records of the
+// decode kernels; with group_taps also the per-expert counts, offsets and
+// first-use keys and both orders of the active experts
+// (runtime/src/expert_major.cpp:10-54).  Every quantity is a count over the
+// P pairs.
+__device__ void select_group(const SelectArgs& a, SelectShared& sh) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t K = a.K, P = a.T * K, E = a.E;
+    const bool dbl = a.renorm == K3X_RENORM_DOUBLE;
+    // Pairs are read eight at a time (two 16-byte LDS reads per wait); the
+    // padding past P matches no expert and is below no expert.
+    const uint4* sel4 = reinterpret_cast<const uint4*>(sh.sel);
+    const uint4* first4 = reinterpret_cast<const uint4*>(sh.first);
+#define SEL_BATCH(q0, body)                                                                     \
+    {                                                                                           \
+        const uint4 u0_ = sel4[(q0) / 4], u1_ = sel4[(q0) / 4 + 1];                             \
+        const uint32_t fv_[8] = {u0_.x, u0_.y, u0_.z, u0_.w, u1_.x, u1_.y, u1_.z, u1_.w};      \
+        _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) {                                      \
+            const uint32_t q = (q0) + i_, f = fv_[i_];                                          \
+            body                                                                                \
+        }                                                                                       \
     }
-    __syncthreads();
+    uint32_t e = 0, rin = 0, below = 0, cnt = 0;
     if (tid < P) {
-        const uint32_t e = sh.ids[tid];
-        atomicAdd(&sh.cnt[e], 1u);
-        atomicMin(&sh.fu[e], tid);
+        e = sh.sel[tid];
+        for (uint32_t q0 = 0; q0 < P; q0 += 8)
+            SEL_BATCH(q0, rin += q < tid && f == e; cnt += f == e; below += f < e;)
+        sh.first[tid] = rin == 0;
+        sh.rowtok[below + rin] = tid / K;
     }
-    __syncthreads();
-    // E <= 512: one expert per thread.
-    const uint32_t c = tid < E ? sh.cnt[tid] : 0u;
-    uint32_t total = 0, na = 0;
-    const uint32_t excl = block_scan_excl(c, sh.wave_sums, &total);
-    const uint32_t aidx = block_scan_excl(c ? 1u : 0u, sh.wave_sums, &na);
-    if (tid < E) {
-        sh.off[tid] = excl;
-        a.offsets[tid] = excl;
-        a.counts[tid] = c;
-        a.first_use[tid] = sh.fu[tid];
-        if (c) {
-            a.active_asc[aidx] = tid;
-            sh.active[aidx] = tid;
+    // Renormalise in slot order (sequential sums as the reference), then
+    // * routed_scale (runtime/src/routing_policy.cpp:146-157,
+    // runtime/src/official_moe.cpp:235-242, runtime/src/model.cpp:1004-1009),
+    // on waves kMaxDecodeTokens.. (the pairs' own waves are 0..).
+    if (wave >= kMaxDecodeTokens && wave - kMaxDecodeTokens < a.T) {
+        const uint32_t t = wave - kMaxDecodeTokens;
+        const float v = lane < K ? sh.selsc[t * K + lane] : 0.0f;
+        float den_f = 0.0f;
+        double den_d = 0.0;
+        for (uint32_t s = 0; s < K; ++s) {
+            const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s));
+            den_f = __fadd_rn(den_f, x);
+            den_d = __dadd_rn(den_d, (double)x);
+        }
+        const bool ok = dbl ? (__builtin_isfinite(den_d) && den_d > 0.0)
+                            : (__builtin_isfinite(den_f) && den_f > 0.0f);
+        if (!ok) {
+            if (lane == 0) {
+                latch(a.status, dbl ? K3X_ERR_INVALID_EXTENT : K3X_ERR_INVALID_STATE);
+                atomicMax(&sh.bad, 1u);
+            }
+        } else if (lane < K) {
+            sh.selw[t * K + lane] = dbl ? __fmul_rn((float)__ddiv_rn((double)v, den_d),
+                                                    a.routed_scale)
+                                        : __fmul_rn(__fdiv_rn(v, den_f), a.routed_scale);
         }
     }
-    if (tid == 0) {
-        a.offsets[E] = total;
-        *a.n_active = na;
-    }
+    // The last barrier: every global store of the block comes after it, so
+    // no barrier waits for stores to drain.
     __syncthreads();
+    if (sh.bad) return;
     if (tid < P) {
-        const uint32_t e = sh.ids[tid];
-        uint32_t rank = 0;
-        for (uint32_t q = 0; q < tid; ++q) rank += sh.ids[q] == e;
-        const uint32_t r = sh.off[e] + rank;
-        a.pair_token[r] = tid / a.K;
-        a.pair_slot[r] = tid % a.K;
-        sh.ptok[r] = tid / a.K;
+        const uint32_t r = below + rin;  // CSR row
+        a.pair_token[r] = tid / K;
+        a.pair_slot[r] = tid % K;
+        a.ids[tid] = e;
+        a.weights[tid] = sh.selw[tid];
     }
-    __syncthreads();
-    if (tid < na) {  // record of active slot tid: rows' tokens packed 8 bits each
-        const uint32_t e = sh.active[tid], c = sh.cnt[e], o = sh.off[e];
-        uint32_t toks = 0;
-        for (uint32_t q = 0; q < c && q < 4; ++q) toks |= sh.ptok[o + q] << (8 * q);
-        a.arec[tid] = make_uint4(e, c, o, toks);
+    if (tid < P && sh.first[tid]) {
+        uint32_t ai = 0, fr = 0, na = 0;
+        for (uint32_t q0 = 0; q0 < P; q0 += 8) {
+            const uint4 g0 = first4[q0 / 4], g1 = first4[q0 / 4 + 1];
+            const uint32_t fq_[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            SEL_BATCH(q0, const bool fq = fq_[i_] != 0;
+                      ai += fq && f < e;    /* active experts below e: ascending index */
+                      fr += fq && q < tid;  /* first uses before e's: first-use rank */
+                      na += fq;)
+        }
+        uint32_t toks = 0;  // tokens of e's first four rows, 8 bits each
+        for (uint32_t j = 0; j < min(cnt, 4u); ++j) toks |= sh.rowtok[below + j] << (8 * j);
+        a.arec[ai] = make_uint4(e, cnt, below, toks);
+        if (ai == 0) *a.n_active = na;
+        if (a.group_taps) {
+            a.active_asc[ai] = e;
+            a.active_fu[fr] = e;
+        }
     }
-    if (tid < na) {
-        const uint32_t e = sh.active[tid];
-        const uint32_t key = sh.fu[e];
-        uint32_t rank = 0;
-        for (uint32_t b = 0; b < na; ++b) rank += sh.fu[sh.active[b]] < key;
-        a.active_fu[rank] = e;
+    if (!a.group_taps) return;
+    // Per expert: count, CSR offset, first use (0xffffffff when unused).
+    for (uint32_t x = tid; x < E; x += kFrontThreads) {
+        uint32_t c = 0, o = 0, fu = 0xffffffffu;
+        for (uint32_t q0 = 0; q0 < P; q0 += 8)
+            SEL_BATCH(q0, c += f == x; o += f < x; if (f == x && fu == 0xffffffffu) fu = q;)
+        a.counts[x] = c;
+        a.offsets[x] = o;
+        a.first_use[x] = fu;
     }
+    if (tid == 0) a.offsets[E] = P;
+#undef SEL_BATCH
 }
 
 // Shared down block: one 16-row block rb of H, K = S split over the eight
 // waves (up to two tiles in flight per wave, refills clamped to the last
 // tile), partials added in a fixed tree in LDS (wave w += wave w + h for
 // h = 4, 2, 1).
-__device__ __forceinline__ void shared_down_block(const SelectArgs& a, uint32_t rb,
+__device__ __forceinline__ void shared_down_block(const SharedDownArgs& a, uint32_t rb,
                                                   f32x4 (&red)[kFrontWaves][64]) {
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
@@ -631,30 +784,26 @@ union SelectLds {
     f32x4 red[kFrontWaves][64];
 };
 
-__global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a) {
-    __shared__ SelectLds sh;
+// Block 0: the Top-K of every token and the grouping; blocks 1.. the shared
+// expert's down projection, which streams while block 0 works.
+__global__ __launch_bounds__(kFrontThreads) void decode_select_kernel(SelectArgs a,
+                                                                     SharedDownArgs sd) {
+    __shared__ SelectLds lds;
     if (blockIdx.x) {
-        shared_down_block(a, blockIdx.x - 1, sh.red);
+        shared_down_block(sd, blockIdx.x - 1, lds.red);
         return;
     }
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    // The token's logits and the bias (wave t < T takes token t), loaded
+    SelectShared& sh = lds.sel;
+    // Logits of expert tid for every token and its bias, loaded
     // unconditionally (indices clamped) before the status check.
-    float lgv[kKeysPerLane], bv[kKeysPerLane];
-    const uint32_t t = min(wave, a.T - 1);
+    const uint32_t e = min(threadIdx.x, a.E - 1);
+    float lg[kMaxDecodeTokens];
 #pragma unroll
-    for (int i = 0; i < kKeysPerLane; ++i) {
-        const uint32_t e = min(lane + 64u * i, a.E - 1);
-        lgv[i] = a.logits[(size_t)t * a.E + e];
-        bv[i] = a.bias[e];
-    }
+    for (int t = 0; t < kMaxDecodeTokens; ++t)
+        lg[t] = a.logits[(size_t)min((uint32_t)t, a.T - 1) * a.E + e];
+    const float b = a.bias[e];
     if (prior_status(a.status)) return;
-    if (tid == 0) sh.sel.bad = 0;
-    __syncthreads();
-    if (wave < a.T) topk_token(a, wave, lgv, bv, sh.sel);
-    __syncthreads();
-    if (sh.sel.bad) return;
-    group_pairs(a, sh.sel);
+    if (select_topk(a, sh, lg, b)) select_group(a, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -938,7 +1087,8 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
 // gate/up blocks beside the router blocks, its down blocks beside the Top-K
 // block, so its ~90 MB stream while those steps wait on latency.
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
-                   const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32) {
+                   const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32,
+                   bool group_taps) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k, S = d.shared_inter;
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
@@ -990,15 +1140,19 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     sa.active_asc = b.active_asc;
     sa.active_fu = b.active_fu;
     sa.arec = b.arec;
-    sa.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
-    sa.sact = b.sact;
-    sa.H = d.hidden;
-    sa.S = S;
-    sa.sy = b.sy;
+    sa.group_taps = group_taps;
     sa.status = ctx->status;
+    SharedDownArgs sd{};
+    sd.sh_dn = reinterpret_cast<const uint4*>(bank->sh_dn);
+    sd.sact = b.sact;
+    sd.T = T;
+    sd.H = d.hidden;
+    sd.S = S;
+    sd.sy = b.sy;
+    sd.status = ctx->status;
     mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT);
     hipLaunchKernelGGL(decode_select_kernel, dim3(1 + (S ? d.hidden / 16 : 0)),
-                       dim3(kFrontThreads), 0, main, sa);
+                       dim3(kFrontThreads), 0, main, sa, sd);
     end_stage(ctx, mark);
 
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);

@@ -7,14 +7,17 @@ namespace k3x_hip {
 
 constexpr int kMaxDecodeTokens = 4;
 
-// Whether the three-launch decode path handles this call.
+// Whether the five-launch decode path handles this call.
 bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
                      const k3x_hip_moe_params* p, const void* x);
 
 // RMSNorm, routing, grouping, experts, shared expert and combine of one
-// decode call; x is the raw bf16 input [T][H].  Asynchronous.
+// decode call; x is the raw bf16 input [T][H].  The per-expert grouping
+// arrays (counts, offsets, first_use, active_asc, active_fu), which no decode
+// kernel reads, are written only with group_taps.  Asynchronous.
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
-                   const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32);
+                   const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32,
+                   bool group_taps);
 
 // out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
 // + shared[t][h]) on the context stream (the combine of both paths).

@@ -1992,8 +1992,10 @@ int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_mo
     int st = K3X_OK;
     if (!(p->flags & (K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)) &&
         k3x_hip::decode_eligible(ctx, bank, p, x)) {
+        const bool group_taps = taps && (taps->counts || taps->offsets || taps->first_use ||
+                                         taps->active_first_use);
         if ((st = k3x_hip::decode_forward(ctx, bank, p, s, x, out,
-                                           taps ? taps->out_f32 : nullptr)))
+                                           taps ? taps->out_f32 : nullptr, group_taps)))
             return st;
         ++ctx->forward_calls;
         return copy_taps(ctx, bank, p, s, s.xn, s.ids, s.weights, taps);
