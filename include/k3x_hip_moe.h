@@ -119,6 +119,11 @@ enum k3x_flags {
      * official layer does (runtime/src/official_moe.cpp:99-101, :318-326);
      * runs the general path. */
     K3X_FLAG_ROUND_EXPERT_OUT = 2u,
+    /* Keep the routed GLU activation at fp32 precision into the down
+     * projection (stored as a bf16 hi + lo pair per element, the down
+     * projection run over both halves), as the official layer does
+     * (runtime/src/official_moe.cpp:82-101); runs the general path. */
+    K3X_FLAG_SPLIT_ACT = 4u,
 };
 
 /* Optional device buffers that receive intermediates of k3x_hip_moe_forward;

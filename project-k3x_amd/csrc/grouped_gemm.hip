@@ -87,7 +87,10 @@ __device__ inline void end_step(int d) {
     }
 }
 
-template <bool FP4, bool GATEUP, int NT>
+// SPLIT: gate/up stores each activation as bf16 hi and lo halves (act_lo
+// elements apart); down reads rows [hi | lo] of 2 kt tiles against the
+// weights repeated along K.
+template <bool FP4, bool GATEUP, int NT, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     __shared__ u32x4 s_a4[kWideStages * kTileChunks];  // 128 KiB ring
     __shared__ uint32_t s_yrow[kWideRows];              // down: output row of each chunk row
@@ -120,6 +123,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     }
     if (m0 >= cnt) return;
     const uint32_t kt = a.kt;  // multiple of kWideStages (checked on the host)
+    // Activation tiles: kt, or 2 kt for split [hi | lo] rows, whose tile k
+    // meets weight tile k mod kt (a multiple of four tiles: a block of four
+    // never straddles the two halves, nor its scale dword).
+    constexpr bool kSplitIn = SPLIT && !GATEUP;
+    const uint32_t kta = kSplitIn ? 2 * kt : kt;
+    auto wtile = [&](uint32_t k) {
+        if constexpr (kSplitIn) return k >= kt ? k - kt : k;
+        else return k;
+    };
     const uint32_t rows = min(cnt - m0, kWideRows);
     const uint32_t rb0 = (jb * kWaves + wave) * NT;
     // Weights of expert e through buffer resources: the per-lane offset is
@@ -208,18 +220,18 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         // activation and weight tile s + 3 (the scales of tiles 0..3 with
         // step -3's).
         WIDE_LOAD_A(0u, 0)
-        WIDE_LOAD_B(0, 0u)
-        WIDE_LOAD_SCALES(sc, 0u)
+        WIDE_LOAD_B(0, wtile(0u))
+        WIDE_LOAD_SCALES(sc, wtile(0u))
         WIDE_ORDER();
         WIDE_LOAD_A(1u, 1)
-        WIDE_LOAD_B(1, 1u)
+        WIDE_LOAD_B(1, wtile(1u))
         WIDE_ORDER();
         WIDE_LOAD_A(2u, 2)
-        WIDE_LOAD_B(2, 2u)
+        WIDE_LOAD_B(2, wtile(2u))
         // Steps -2 and -1 may stay in flight; tile 0 (step -3) has arrived.
         wait_and_barrier<2 * (kALoads + NT * S * U)>();
 
-        for (uint32_t kb = 0; kb < kt; kb += kWideStages) {
+        for (uint32_t kb = 0; kb < kta; kb += kWideStages) {
 #pragma unroll
             for (int d = 0; d < kWideStages; ++d) {
                 const uint32_t k = kb + d;
@@ -253,9 +265,9 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                 // after multiplying it); past the end they repeat the last
                 // tile (the loads stay unconditional, the count exact).  The
                 // next block's scales ride with the block's first step.
-                WIDE_LOAD_A(min(k + 3, kt - 1), (d + 3) % kWideStages)
-                WIDE_LOAD_B((d + 3) % kWideStages, min(k + 3, kt - 1))
-                if (d == 0) WIDE_LOAD_SCALES(scn, min(k + 4, kt - 1))
+                WIDE_LOAD_A(min(k + 3, kta - 1), (d + 3) % kWideStages)
+                WIDE_LOAD_B((d + 3) % kWideStages, wtile(min(k + 3, kta - 1)))
+                if (d == 0) WIDE_LOAD_SCALES(scn, wtile(min(k + 4, kta - 1)))
                 // Tile k + 1 (requested at step k - 2) is in LDS once only
                 // steps k - 1 and k are outstanding.
                 end_step<FP4, NT, S, U>(d);
@@ -280,7 +292,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         // the four row groups of a write land 16 banks apart.  Down tiles
         // larger than the ring go in passes of RP rows.
         constexpr uint32_t kCols = kWaves * NT * 16;
-        constexpr uint32_t kEs = GATEUP ? 2 : 4;                    // output element bytes
+        // Output element bytes (split gate/up: the hi row, then the lo row).
+        constexpr uint32_t kEs = GATEUP ? (SPLIT ? 4 : 2) : 4;
         constexpr uint32_t kChunks = kCols * kEs / 16;              // 16-byte chunks per row
         constexpr uint32_t kPitch = kCols * kEs + 16;               // staged row bytes
         constexpr uint32_t kRing = sizeof(s_a4);
@@ -306,8 +319,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                         const uint32_t col = (wave * NT + nt) * 16 + n;
                         if constexpr (GATEUP) {
                             const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
-                            *reinterpret_cast<uint16_t*>(stage + row * kPitch + col * 2) =
-                                f32_to_bf16(v);
+                            uint16_t* sp = reinterpret_cast<uint16_t*>(stage + row * kPitch) + col;
+                            const uint16_t hi = f32_to_bf16(v);
+                            sp[0] = hi;
+                            if constexpr (SPLIT) sp[kCols] = act_lo_bf16(v, hi);
                         } else {
                             *reinterpret_cast<float*>(stage + row * kPitch + col * 4) =
                                 acc[mt][nt][0][i];
@@ -320,8 +335,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                 const uint32_t row = c / kChunks, ch = c % kChunks;
                 const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * kPitch + ch * 16);
                 if constexpr (GATEUP) {
-                    uint16_t* dst = a.act + (size_t)(off + m0 + p0 + row) * a.act_stride + col0;
-                    *reinterpret_cast<u32x4*>(dst + ch * 8) = v;
+                    // Chunks past the hi row's kCols / 8 carry the lo row.
+                    constexpr uint32_t kHiChunks = kCols / 8;
+                    const uint32_t lo = SPLIT && ch >= kHiChunks;
+                    uint16_t* dst = a.act + (size_t)(off + m0 + p0 + row) * a.act_stride + col0 +
+                                    (lo ? a.act_lo : 0u);
+                    *reinterpret_cast<u32x4*>(dst + (ch - (lo ? kHiChunks : 0u)) * 8) = v;
                 } else {
                     float* dst = a.y + (size_t)s_yrow[p0 + row] * a.y_stride + col0;
                     *reinterpret_cast<u32x4*>(dst + ch * 4) = v;
@@ -372,27 +391,24 @@ int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uin
     if (a.nrb % per || a.kt % kWideStages || !a.kt || !max_items) return K3X_ERR_INVALID_EXTENT;
     // The epilogue stores 16-byte row pieces.
     const bool gu = kind == kWideRoutedGateUp || kind == kWideSharedGateUp;
-    if (gu ? ((uintptr_t)a.act % 16 || a.act_stride % 8) : ((uintptr_t)a.y % 16 || a.y_stride % 4))
+    if (gu ? ((uintptr_t)a.act % 16 || a.act_stride % 8 || a.act_lo % 8)
+           : ((uintptr_t)a.y % 16 || a.y_stride % 4))
         return K3X_ERR_INVALID_EXTENT;
+    if (a.kta && (a.kta != 2 * a.kt || gu)) return K3X_ERR_INVALID_EXTENT;
+    const bool split = gu ? a.act_lo != 0 : a.kta != 0;
     const dim3 grid(max_items * (a.nrb / per));
+#define K3X_WIDE(FP4, GU, NT)                                                                   \
+    if (split)                                                                                  \
+        hipLaunchKernelGGL((wide_gemm<FP4, GU, NT, true>), grid, dim3(kThreads), 0, stream, a); \
+    else                                                                                        \
+        hipLaunchKernelGGL((wide_gemm<FP4, GU, NT, false>), grid, dim3(kThreads), 0, stream, a);
     switch (kind) {
-        case kWideRoutedGateUp:
-            hipLaunchKernelGGL((wide_gemm<true, true, kNtRoutedGateUp>), grid, dim3(kThreads), 0,
-                               stream, a);
-            break;
-        case kWideRoutedDown:
-            hipLaunchKernelGGL((wide_gemm<true, false, kNtRoutedDown>), grid, dim3(kThreads), 0,
-                               stream, a);
-            break;
-        case kWideSharedGateUp:
-            hipLaunchKernelGGL((wide_gemm<false, true, kNtSharedGateUp>), grid, dim3(kThreads), 0,
-                               stream, a);
-            break;
-        default:
-            hipLaunchKernelGGL((wide_gemm<false, false, kNtSharedDown>), grid, dim3(kThreads), 0,
-                               stream, a);
-            break;
+        case kWideRoutedGateUp: K3X_WIDE(true, true, kNtRoutedGateUp) break;
+        case kWideRoutedDown: K3X_WIDE(true, false, kNtRoutedDown) break;
+        case kWideSharedGateUp: K3X_WIDE(false, true, kNtSharedGateUp) break;
+        default: K3X_WIDE(false, false, kNtSharedDown) break;
     }
+#undef K3X_WIDE
     ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }

@@ -241,6 +241,7 @@ struct GluParams {
     float beta;
     int has_linear;
     float linear_beta;
+    int round_in;    // 1: gate and up rounded to bf16 first (a bf16 projection's output)
 };
 
 // SiTU-GLU (runtime/src/ops.cpp:20-30) or SwiGLU (silu(g) * u).  The gate
@@ -250,6 +251,10 @@ struct GluParams {
 // divide made the epilogue a sizeable share of the kernel.  g -> -inf gives
 // exp2 = inf and a sigmoid of 0; NaN propagates.
 __device__ inline float glu(float g, float u, const GluParams& p) {
+    if (p.round_in) {
+        g = __uint_as_float((uint32_t)f32_to_bf16(g) << 16);
+        u = __uint_as_float((uint32_t)f32_to_bf16(u) << 16);
+    }
     const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f));
     if (p.kind == 1) {
         const float bg = p.beta * tanhf(g / p.beta) * sig;
@@ -257,6 +262,14 @@ __device__ inline float glu(float g, float u, const GluParams& p) {
         return bg * bu;
     }
     return (g * sig) * u;
+}
+
+// A GLU activation v as two bf16 words, hi = bf16(v) and lo = bf16(v - hi):
+// hi + lo carries v to about 2^-17 relative, so a bf16 MFMA over both
+// halves (the activation as a row [hi | lo] against the weights repeated
+// along K) multiplies by an fp32 activation.
+__device__ inline uint16_t act_lo_bf16(float v, uint16_t hi) {
+    return f32_to_bf16(__fsub_rn(v, __uint_as_float((uint32_t)hi << 16)));
 }
 
 // SplitMix64 output function (Steele, Lea & Flood, OOPSLA 2014) and the

@@ -24,6 +24,8 @@ struct WideGemmArgs {
     const uint16_t* a;           // activation rows, bf16
     uint32_t a_stride;           // elements per activation row
     uint32_t a_bytes;            // bytes readable from a (loads past it read 0)
+    uint32_t kta;                // activation K tiles (0: kt); 2 kt for split [hi | lo]
+                                 // rows against the weights repeated along K
     uint32_t gather;             // A row = pair_token[off + m] (1) or off + m (0)
     const uint32_t* items;       // routed: (expert << 16 | chunk) work items
     const uint32_t* n_items;
@@ -35,6 +37,7 @@ struct WideGemmArgs {
     uint32_t top_k;
     uint16_t* act;               // gate/up output [row][act_stride] bf16
     uint32_t act_stride;
+    uint32_t act_lo;             // gate/up: element offset of the lo half in a row (0: none)
     float* y;                    // down output [row][y_stride] fp32
     uint32_t y_stride;
     uint32_t scatter;            // y row = token * top_k + slot (1) or off + m (0)

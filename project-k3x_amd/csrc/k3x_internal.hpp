@@ -167,15 +167,20 @@ bool router_uses_mfma(uint32_t H, uint32_t T);
 size_t router_xp_bytes(uint32_t T);
 int launch_topk(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E, uint32_t K,
                 uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids, float* weights);
+// split: activations stored as rows [hi | lo] of 2 I (dense_gate_up) and read
+// as such (dense_down, K = the activation width I), the down projection
+// running over both halves: an fp32 activation into the bf16 MFMA.
 int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
-                  uint32_t T, const k3x_dev::GluParams& glu, uint16_t* act, hipStream_t stream);
+                  uint32_t T, const k3x_dev::GluParams& glu, uint16_t* act, hipStream_t stream,
+                  bool split = false);
 // Up to kDenseDirectTokens rows the projections run as a split-K GEMV on
 // any stream, and dense_down can round its output to bf16 itself (y_bf16;
 // y is then unused); above, y_bf16 must be null and the narrow GEMM runs on
 // the context stream only.
 constexpr uint32_t kDenseDirectTokens = 16;
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
-               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr);
+               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr,
+               bool split = false);
 // Up to kDenseDirectTokens rows on the context stream: y = tiles . a with the
 // official layer's output in the epilogue: routed = y (fp32) and out =
 // bf16(bf16(prefix) + bf16(bf16(y) + bf16(shared))) (shared may be null).

@@ -375,7 +375,7 @@ struct FfnBuffers {
     uint16_t* mixed;      // [T][L]
     uint16_t* normed;     // [T][L]
     float* routed;        // [T][H]
-    uint16_t* sact;       // [T][Is]
+    uint16_t* sact;       // [T][2 Is] split [hi | lo] rows
     float* shared;        // [T][H]
 };
 
@@ -394,7 +394,7 @@ size_t carve(uint8_t* base, const k3x_hip_official* o, uint32_t T, uint32_t K, F
     b->mixed = (uint16_t*)take((size_t)T * o->L * 2);
     b->normed = (uint16_t*)take((size_t)T * o->L * 2);
     b->routed = (float*)take((size_t)T * o->H * 4);
-    b->sact = (uint16_t*)take((size_t)T * std::max(o->I_s, 1u) * 2);
+    b->sact = (uint16_t*)take((size_t)T * std::max(o->I_s, 1u) * 4);
     b->shared = (float*)take((size_t)T * o->H * 4);
     return at;
 }
@@ -648,11 +648,16 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
         }
         ~Join() { (void)join(); }
     } joiner{o};
+    // The shared gate and up are bf16 projections (rounded before the GLU)
+    // and the activation enters the down projection at fp32 precision, as a
+    // split [hi | lo] row.
+    GluParams sglu = glu;
+    sglu.round_in = 1;
     auto shared_ffn = [&](hipStream_t stream) {
-        int r = k3x_hip::dense_gate_up(ctx, o->shared_gu, o->I_s, o->H, hidden, T, glu, b.sact,
-                                       stream);
+        int r = k3x_hip::dense_gate_up(ctx, o->shared_gu, o->I_s, o->H, hidden, T, sglu, b.sact,
+                                       stream, true);
         return r ? r : k3x_hip::dense_down(ctx, o->shared_dn, o->H, o->I_s, b.sact, T, b.shared,
-                                           stream);
+                                           stream, nullptr, true);
     };
     if (side) {
         if (hipEventRecord(o->fork_ev, ctx->stream) != hipSuccess ||
@@ -690,13 +695,13 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
                            0, ctx->stream, b.latent_f32, (size_t)T * o->L, b.latent);
         if ((st = launched(ctx, 1))) return st;
     }
-    // Experts on the latent: the bank's grouped path, each expert output
-    // rounded to bf16 before the slot-ordered mix, the mix rounded
-    // (official_moe.cpp:82-103, :313-326).
+    // Experts on the latent: the bank's grouped path with fp32 activations
+    // into the down projection, each expert output rounded to bf16 before the
+    // slot-ordered mix, the mix rounded (official_moe.cpp:82-103, :313-326).
     k3x_hip_moe_params ep = *p;
     ep.routed_scale = 1.0f;
     ep.renorm = K3X_RENORM_DOUBLE;
-    ep.flags = K3X_FLAG_ROUND_EXPERT_OUT;
+    ep.flags = K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT;
     k3x_hip_moe_taps et{};
     if (taps) et.expert_out = taps->expert_out;
     st = k3x_hip_moe_forward_routed(ctx, o->bank, &ep, b.latent, ids, contributions, nullptr,

@@ -977,6 +977,8 @@ struct GemmArgs {
     uint32_t blocks_per_expert; // workgroups per expert
     const uint16_t* a;          // activation rows (bf16)
     uint32_t a_stride;          // elements per activation row
+    uint32_t kta;               // activation K tiles (0: kt); 2 kt for a split [hi | lo]
+                                // row, the weights repeated along K
     uint32_t gather;            // A row = pair_token[off+m] (1) or off+m (0)
     const uint32_t* n_active;   // grouping (nullptr = single block of `tokens` rows)
     const uint32_t* active;
@@ -988,6 +990,7 @@ struct GemmArgs {
     uint32_t top_k;
     uint16_t* act;              // GATEUP output [row][act_stride] bf16
     uint32_t act_stride;
+    uint32_t act_lo;            // GATEUP: element offset of the lo half in a row (0: none)
     float* y;                   // down output [row][y_stride] fp32
     uint32_t y_stride;
     uint32_t scatter;           // y row = token*top_k + slot (1) or off+m (0)
@@ -1016,6 +1019,7 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
     const uint32_t rb0 = (jb * 4 + wave) * NT;
     const uint4* codes = reinterpret_cast<const uint4*>(a.codes + e * a.codes_per_expert);
     const uint32_t* scales = FP4 ? a.scales + e * a.scales_per_expert : nullptr;
+    const uint32_t kta = a.kta ? a.kta : a.kt;
 
     for (uint32_t m0 = 0; m0 < cnt; m0 += 16 * MT) {
         const uint16_t* arow[MT];
@@ -1038,15 +1042,17 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 
         // One row tile: D K steps of loads issued together (steps past the
         // last tile clamped, their activations zeroed), since a lone step's
-        // round trip would bound the wave.
+        // round trip would bound the wave.  Activation tile ka meets weight
+        // tile ka mod kt.
         constexpr int D = MT == 1 ? kGemmDepth : 1;
-        for (uint32_t k0 = 0; k0 < a.kt; k0 += D) {
+        for (uint32_t k0 = 0; k0 < kta; k0 += D) {
             uint4 bt[D][NT][S][U];
             float sc[D][NT][S];
             bf16x8 af[D][MT][4];
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                const uint32_t k = min(k0 + d, a.kt - 1);
+                const uint32_t ka = min(k0 + d, kta - 1);
+                const uint32_t k = ka >= a.kt ? ka - a.kt : ka;
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -1062,8 +1068,8 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                     }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    if (arow[mt] && k0 + d < a.kt) {
-                        const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)k * 128);
+                    if (arow[mt] && k0 + d < kta) {
+                        const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)ka * 128);
 #pragma unroll
                         for (int j = 0; j < 4; ++j) af[d][mt][j] = as_bf16x8(p[j]);
                     } else {
@@ -1106,7 +1112,10 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                     const uint32_t col = (rb0 + nt) * 16 + n;
                     if constexpr (GATEUP) {
                         const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
-                        a.act[(size_t)(off + row) * a.act_stride + col] = f32_to_bf16(v);
+                        uint16_t* dst = a.act + (size_t)(off + row) * a.act_stride + col;
+                        const uint16_t hi = f32_to_bf16(v);
+                        *dst = hi;
+                        if (a.act_lo) dst[a.act_lo] = act_lo_bf16(v, hi);
                     } else {
                         const uint32_t r = off + row;
                         const size_t yrow = a.scatter
@@ -1148,6 +1157,11 @@ struct GemvArgs {
     const float* prefix;
     const float* shared;
     float* routed;
+    // Split activations: x rows [hi | lo] of kta = 2 kt tiles against the
+    // weights repeated along K (0: kt); OUT 2 also stores lo = bf16(v -
+    // hi) out_lo elements after hi (0: none).
+    uint32_t kta;
+    uint32_t out_lo;
 };
 
 template <int S, int D, int OUT, int W = kGemvWaves>
@@ -1165,21 +1179,23 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     f32x4 acc[S];
 #pragma unroll
     for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k0 = wave; k0 < a.kt; k0 += W * D) {
+    const uint32_t kta = a.kta ? a.kta : a.kt;
+    for (uint32_t k0 = wave; k0 < kta; k0 += W * D) {
         uint4 b[D][S][4], xa[D][4];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const uint32_t k = min(k0 + d * W, a.kt - 1);
+            const uint32_t ka = min(k0 + d * W, kta - 1);
+            const uint32_t k = ka >= a.kt ? ka - a.kt : ka;  // weight tile
 #pragma unroll
             for (int w = 0; w < S; ++w)
 #pragma unroll
                 for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[d][j] = xr[(size_t)k * 16 + j];
+            for (int j = 0; j < 4; ++j) xa[d][j] = xr[(size_t)ka * 16 + j];
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const bool live = live_row && k0 + d * W < a.kt;
+            const bool live = live_row && k0 + d * W < kta;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint4 xv = live ? xa[d][j] : make_uint4(0, 0, 0, 0);
@@ -1207,7 +1223,12 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     const size_t at = (size_t)t * a.out_stride + (size_t)rb * 16 + c;
     if constexpr (OUT == 0) static_cast<float*>(a.out)[at] = v[0];
     else if constexpr (OUT == 1) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(v[0]);
-    else if constexpr (OUT == 2) static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(glu(v[0], v[S - 1], a.glu));
+    else if constexpr (OUT == 2) {
+        const float g = glu(v[0], v[S - 1], a.glu);
+        const uint16_t hi = f32_to_bf16(g);
+        static_cast<uint16_t*>(a.out)[at] = hi;
+        if (a.out_lo) static_cast<uint16_t*>(a.out)[at + a.out_lo] = act_lo_bf16(g, hi);
+    }
     else {
         auto r16 = [](float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); };
         a.routed[at] = v[0];
@@ -1317,7 +1338,9 @@ size_t group_scratch_bytes(uint32_t T, uint32_t K, uint32_t E) {
     return 2 * nch * E * 4 + (((size_t)T * K + 255) & ~(size_t)255);
 }
 
-size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, Scratch* s) {
+// split: the routed activation rows hold [hi | lo] halves (K3X_FLAG_SPLIT_ACT).
+size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, bool split,
+             Scratch* s) {
     size_t at = 0;
     auto take = [&](size_t bytes) {
         uint8_t* p = base ? base + at : nullptr;
@@ -1337,7 +1360,7 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->n_active = (uint32_t*)take(4);
     s->active_asc = (uint32_t*)take((size_t)d.experts * 4);
     s->active_fu = (uint32_t*)take((size_t)d.experts * 4);
-    s->act = (uint16_t*)take(P * d.inter * 2);
+    s->act = (uint16_t*)take(P * d.inter * (split ? 4 : 2));
     // y is first written by the down projection, after the router: the
     // residue-major xn copy of router_mfma_kernel lives in the same bytes.
     const size_t xp_bytes = (size_t)(T + 15) / 16 * kRouterRes * kRouterTileRes * 2;
@@ -1365,7 +1388,8 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         return K3X_ERR_INVALID_EXTENT;
     if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
         p->renorm > 1 ||
-        (p->flags & ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)))
+        (p->flags &
+         ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT)))
         return K3X_ERR_INVALID_MXFP4;
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
@@ -1423,7 +1447,7 @@ void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32
 // staged in LDS) for the routed and the shared expert.  Shapes it needs: K
 // tile counts even, output rows a multiple of the workgroup's row blocks,
 // element offsets of the activation rows below 2^32.
-bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
+bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, bool split) {
     using k3x_hip::wide_rb_per_block;
     constexpr uint32_t kq = 128 * k3x_hip::kWideStages;  // K extents: whole pipeline blocks
     const uint64_t rows = (uint64_t)T * K;
@@ -1435,7 +1459,8 @@ bool use_wide_gemm(const k3x_hip_layer_desc& d, uint32_t T, uint32_t K) {
             (d.shared_inter % kq == 0 &&
              (d.shared_inter / 16) % wide_rb_per_block(k3x_hip::kWideSharedGateUp) == 0 &&
              (d.hidden / 16) % wide_rb_per_block(k3x_hip::kWideSharedDown) == 0)) &&
-           rows * std::max(d.hidden, std::max(d.inter, d.shared_inter)) * 2 < (1ull << 32) &&
+           rows * std::max(d.hidden, std::max(d.inter * (split ? 2 : 1), d.shared_inter)) * 2 <
+               (1ull << 32) &&
            // weight byte offsets within one matrix pair are 32-bit as well
            (uint64_t)std::max(d.inter, d.shared_inter) * d.hidden * 4 < (1ull << 32);
 }
@@ -1468,7 +1493,9 @@ k3x_hip::WideGemmArgs wide_gate_up_args(k3x_hip_ctx* ctx, const k3x_hip_bank* ba
     g.a_bytes = T * d.hidden * 2;
     g.gather = 1;
     g.act = s.act;
-    g.act_stride = d.inter;
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    g.act_stride = split ? 2 * d.inter : d.inter;
+    g.act_lo = split ? d.inter : 0;
     return g;
 }
 
@@ -1493,6 +1520,7 @@ int run_shared_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_para
     sg.tokens = T;
     sg.act = s.sact;
     sg.act_stride = d.shared_inter;
+    sg.act_lo = 0;  // the bank's shared expert keeps bf16 activations
     int mark = marks ? begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP) : -1;
     int st = launch_wide_gemm(ctx, kWideSharedGateUp, sg, all_chunks, stream);
     end_stage(ctx, mark);
@@ -1541,8 +1569,9 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.ks = bank->down.ks;
     dn.nrb = d.hidden / 16;
     dn.a = s.act;
-    dn.a_stride = d.inter;
-    dn.a_bytes = T * K * d.inter * 2;
+    dn.a_stride = g.act_stride;
+    dn.a_bytes = T * K * g.act_stride * 2;
+    dn.kta = g.act_lo ? 2 * dn.kt : 0;
     dn.gather = 0;
     dn.act = nullptr;
     dn.y = s.y;
@@ -1568,7 +1597,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     // tails); the context stream waits for them before the combine, and on
     // every early return (they read and write this call's scratch).  With
     // stage profiling on, everything stays on the context stream.
-    const bool wide_path = use_wide_gemm(d, T, K);
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    const bool wide_path = use_wide_gemm(d, T, K, split);
     const bool side = wide_path && d.shared_inter && !ctx->profiling && ctx->side_stream;
     struct Join {
         k3x_hip_ctx* ctx;
@@ -1632,7 +1662,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.pair_token = s.pair_token;
     g.pair_slot = s.pair_slot;
     g.act = s.act;
-    g.act_stride = d.inter;
+    g.act_stride = split ? 2 * d.inter : d.inter;
+    g.act_lo = split ? d.inter : 0;
     mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
     if (wide) launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
     else launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
@@ -1650,6 +1681,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sg.tokens = T;
         sg.act = s.sact;
         sg.act_stride = d.shared_inter;
+        sg.act_lo = 0;  // the bank's shared expert keeps bf16 activations
         mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP);
         if (wide) launch_gemm<false, true, 4, 1>(ctx, sg, 1, d.shared_inter);
         else launch_gemm<false, true, 1, 1>(ctx, sg, 1, d.shared_inter);
@@ -1664,7 +1696,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.kt = bank->down.kt;
     dn.ks = bank->down.ks;
     dn.a = s.act;
-    dn.a_stride = d.inter;
+    dn.a_stride = g.act_stride;
+    dn.kta = split ? 2 * dn.kt : 0;
     dn.gather = 0;
     dn.y = s.y;
     dn.y_stride = d.hidden;
@@ -1679,6 +1712,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sd.scales = nullptr;
         sd.codes_per_expert = 0;
         sd.kt = bank->sdown.kt;
+        sd.kta = 0;
         sd.a = s.sact;
         sd.a_stride = d.shared_inter;
         sd.n_active = nullptr;
@@ -1703,6 +1737,12 @@ int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_para
     if (!taps) return K3X_OK;
     const auto& d = bank->desc;
     const size_t T = p->tokens, K = p->top_k, P = T * K, E = d.experts;
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    // Split activation rows [hi | lo]: the tap receives the hi halves.
+    if (split && taps->act &&
+        hipMemcpy2DAsync(taps->act, d.inter * 2, s.act, d.inter * 4, d.inter * 2, P,
+                         hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
     struct Item { void* dst; const void* src; size_t bytes; };
     const Item items[] = {
         {taps->normed_x, xn, T * d.hidden * 2},
@@ -1716,7 +1756,7 @@ int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_para
         {taps->first_use, s.first_use, E * 4},
         {taps->n_active, s.n_active, 4},
         {taps->active_first_use, s.active_fu, E * 4},
-        {taps->act, s.act, P * d.inter * 2},
+        {taps->act, split ? nullptr : s.act, P * d.inter * 2},
         {taps->expert_out, s.y, P * d.hidden * 4},
         {taps->shared_out, d.shared_inter ? s.sy : nullptr, T * d.hidden * 4},
         {taps->shared_act, d.shared_inter ? s.sact : nullptr, T * d.shared_inter * 2},
@@ -1798,10 +1838,11 @@ int launch_topk_any(k3x_hip_ctx* ctx, const float* logits, const float* bias, ui
 
 int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, Scratch* s) {
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, s);
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, split, s);
     int st = k3x_hip::ensure_scratch(ctx, need);
     if (st) return st;
-    carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, s);
+    carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, split, s);
     return K3X_OK;
 }
 
@@ -1869,8 +1910,10 @@ bool dense_wide_ok(WideKind kind, uint32_t N, uint32_t K, uint32_t T) {
 }
 
 int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
-                  uint32_t T, const GluParams& glu, uint16_t* act, hipStream_t stream) {
+                  uint32_t T, const GluParams& glu, uint16_t* act, hipStream_t stream,
+                  bool split) {
     if (!T || I % 64 || H % 128) return K3X_ERR_INVALID_EXTENT;
+    const uint32_t act_stride = split ? 2 * I : I, act_lo = split ? I : 0;
     if (dense_wide_ok(kWideSharedGateUp, I, H, T)) {
         WideGemmArgs g{};
         g.codes = reinterpret_cast<const uint8_t*>(tiles);
@@ -1881,13 +1924,15 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
         g.a_bytes = T * H * 2;
         g.tokens = T;
         g.act = act;
-        g.act_stride = I;
+        g.act_stride = act_stride;
+        g.act_lo = act_lo;
         g.glu = glu;
         g.status = ctx->status;
         return launch_wide_gemm(ctx, kWideSharedGateUp, g, (T + kWideRows - 1) / kWideRows, stream);
     }
     if (T <= kGemvMaxTokens) {
-        GemvArgs g{tiles, H / 128, x, H, T, act, I, glu, ctx->status};
+        GemvArgs g{tiles, H / 128, x, H, T, act, act_stride, glu, ctx->status};
+        g.out_lo = act_lo;
         // Beside the context stream: half-size workgroups, so that the
         // other stream's launches find room on every compute unit.
         if (stream == ctx->stream)
@@ -1906,7 +1951,8 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
     g.a_stride = H;
     g.tokens = T;
     g.act = act;
-    g.act_stride = I;
+    g.act_stride = act_stride;
+    g.act_lo = act_lo;
     g.glu = glu;
     g.status = ctx->status;
     if (T > 16) launch_gemm<false, true, 4, 1>(ctx, g, 1, I);
@@ -1915,10 +1961,14 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
 }
 
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
-               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16) {
+               uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16, bool split) {
     if (!T || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
+    // Split rows [hi | lo]: 2 K activation columns against the weights twice.
+    const uint32_t a_stride = split ? 2 * K : K, kta = split ? 2 * (K / 128) : 0;
     if (T <= kGemvMaxTokens) {
-        GemvArgs g{tiles, K / 128, a, K, T, y_bf16 ? (void*)y_bf16 : (void*)y, N, {}, ctx->status};
+        GemvArgs g{tiles, K / 128, a, a_stride, T, y_bf16 ? (void*)y_bf16 : (void*)y, N, {},
+                   ctx->status};
+        g.kta = kta;
         const dim3 grid(N / 16);
         if (y_bf16)
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), grid, dim3(64 * kGemvWaves), 0, stream,
@@ -1936,10 +1986,11 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
         WideGemmArgs g{};
         g.codes = reinterpret_cast<const uint8_t*>(tiles);
         g.kt = K / 128;
+        g.kta = kta;
         g.nrb = N / 16;
         g.a = a;
-        g.a_stride = K;
-        g.a_bytes = T * K * 2;
+        g.a_stride = a_stride;
+        g.a_bytes = T * a_stride * 2;
         g.tokens = T;
         g.y = y;
         g.y_stride = N;
@@ -1950,8 +2001,9 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
     GemmArgs g{};
     g.codes = reinterpret_cast<const uint8_t*>(tiles);
     g.kt = K / 128;
+    g.kta = kta;
     g.a = a;
-    g.a_stride = K;
+    g.a_stride = a_stride;
     g.tokens = T;
     g.y = y;
     g.y_stride = N;
@@ -1990,7 +2042,8 @@ int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_mo
                           const Scratch& s, const uint16_t* x, uint16_t* out,
                           const k3x_hip_moe_taps* taps) {
     int st = K3X_OK;
-    if (!(p->flags & (K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT)) &&
+    if (!(p->flags &
+          (K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT)) &&
         k3x_hip::decode_eligible(ctx, bank, p, x)) {
         const bool group_taps = taps && (taps->counts || taps->offsets || taps->first_use ||
                                          taps->active_first_use);
@@ -2075,10 +2128,13 @@ int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     if (!ctx->noalloc_scratch) return K3X_ERR_BACKEND_UNAVAILABLE;
     Scratch s;
-    if (carve(nullptr, bank->desc, p->tokens, p->top_k, &s) > K3X_HIP_NOALLOC_SCRATCH_BYTES)
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    if (carve(nullptr, bank->desc, p->tokens, p->top_k, split, &s) >
+        K3X_HIP_NOALLOC_SCRATCH_BYTES)
         return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    carve(static_cast<uint8_t*>(ctx->noalloc_scratch), bank->desc, p->tokens, p->top_k, &s);
+    carve(static_cast<uint8_t*>(ctx->noalloc_scratch), bank->desc, p->tokens, p->top_k, split,
+          &s);
     // Stage timing takes events from a pool that may have to create them:
     // not on this path.
     const bool profiling = ctx->profiling;

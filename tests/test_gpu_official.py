@@ -270,11 +270,6 @@ def synth_official_weights(oracle, seed, H, L, Is, E, sigma, router_sigma, proj_
 # 3584, 896 MXFP4 experts of 3072, Top-16, shared FFN 6144), on the bench's
 # synthetic weights: T=2 (decode kernels and split-K GEMVs) and T=2048 (wide
 # grouped GEMMs, matrix-core router) on sampled tokens.
-@pytest.mark.xfail(strict=True, reason=(
-    "the expert and shared GLU activations enter the bf16 MFMA down projection rounded to "
-    "bf16, where official_moe.cpp:82-117 keeps them in fp32 (and rounds the shared gate/up "
-    "to bf16 first); at this shape that puts ~3e-3 relative error on routed and shared and "
-    "8 of 7168 outputs per token past atol = rtol = 2e-2"))
 @pytest.mark.parametrize("T,tokens", [(2, (0, 1)), (2048, (0, 1031, 2047))],
                          ids=["t2", "t2048"])
 def test_official_layer_benched_shape(hip, oracle, T, tokens, parity_report):
