@@ -124,6 +124,12 @@ enum k3x_flags {
      * projection run over both halves), as the official layer does
      * (runtime/src/official_moe.cpp:82-101); runs the general path. */
     K3X_FLAG_SPLIT_ACT = 4u,
+    /* k3x_hip_moe_forward_routed only: the input rows are fp32 values held
+     * as bf16 hi + lo halves, [T][2 H] (hi = bf16(v), lo = bf16(v - hi)),
+     * and the gate/up projections run over both halves; the latent layer's
+     * fp32 experts (runtime/src/backend_cpu.cpp:317-318).  Runs the
+     * general path's narrow GEMMs. */
+    K3X_FLAG_SPLIT_INPUT = 8u,
 };
 
 /* Optional device buffers that receive intermediates of k3x_hip_moe_forward;
@@ -438,6 +444,69 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* official,
                          const float* prefix, const uint32_t* ids,
                          const float* contributions, uint16_t* out,
                          const k3x_hip_official_taps* taps);
+
+/* ---- fp32 products and the resident latent layer ------------------------ */
+
+/* The fp32 operations of ComputeBackend: each product is formed exactly in
+ * double and summed in double, one rounding to fp32 at the end (the
+ * reference sums sequentially; only the order differs).  All pointers are
+ * device memory; every call is asynchronous on the context stream.  Inputs
+ * x are [tokens][cols] fp32, outputs [tokens][rows] fp32. */
+
+/* y = W x, W fp32 [rows][cols] row-major.  Replaces
+ * ComputeBackend::dense_matvec (runtime/include/k3x/backend.hpp:333-335;
+ * runtime/src/backend_cpu.cpp:22-45). */
+int k3x_hip_dense_f32_matvec(k3x_hip_ctx* ctx, const float* W, uint32_t rows, uint32_t cols,
+                             const float* x, uint32_t tokens, float* y);
+
+/* y = W x for an MXFP4 matrix in the K3X layout: packed [rows][cols / 2]
+ * (low nibble = even column, 16-byte aligned), E8M0 scales
+ * [rows][cols / 32], group size 32.  Replaces ComputeBackend::mxfp4_matvec
+ * (backend.hpp:336-338; backend_cpu.cpp:47-59, runtime/src/ops.cpp:57-76);
+ * scale bytes must be checked for 0xFF by the caller (the reference's
+ * decode_mxfp4 rejects them). */
+int k3x_hip_mxfp4_matvec(k3x_hip_ctx* ctx, const uint8_t* packed, const uint8_t* scales,
+                         uint32_t rows, uint32_t cols, const float* x, uint32_t tokens, float* y);
+
+/* The fp32 SiTU MLP: act [tokens][inter] = situ_glu(gate x, up x) (gate and
+ * up [inter][hidden]), y [tokens][out_rows] = down act (down
+ * [out_rows][inter]).  Replaces ComputeBackend::dense_situ_mlp
+ * (backend.hpp:345-348; backend_cpu.cpp:108-122). */
+int k3x_hip_dense_situ_mlp(k3x_hip_ctx* ctx, const float* gate, const float* up,
+                           const float* down, uint32_t hidden, uint32_t inter, uint32_t out_rows,
+                           float situ_beta, int has_situ_linear, float situ_linear_beta,
+                           const float* x, uint32_t tokens, float* act, float* y);
+
+/* fp32 dense weights of the resident latent MoE layer, device row-major
+ * (ResidentMoeLayerView, backend.hpp:302-307). */
+typedef struct k3x_hip_latent_weights {
+    const float* routed_down;  /* [latent][hidden] */
+    const float* routed_norm;  /* [latent] */
+    const float* routed_up;    /* [hidden][latent] */
+    const float* shared_gate;  /* [shared_inter][hidden] */
+    const float* shared_up;    /* [shared_inter][hidden] */
+    const float* shared_down;  /* [hidden][shared_inter] */
+    uint32_t hidden, latent, shared_inter;
+} k3x_hip_latent_weights;
+
+/* The resident latent MoE layer for T tokens: latent = routed_down x; the
+ * routed experts of `bank` (hidden = latent, no shared expert) on the fp32
+ * latent, slots ids [T][K] (device) mixed in slot order with contributions
+ * [T][K] in fp32; normalized = RMSNorm(mixed, routed_norm); out [T][hidden]
+ * = routed_up normalized + the fp32 SiTU MLP of x.  x, out device fp32;
+ * mixed_out (optional) receives the mix [T][latent].  params: tokens,
+ * top_k, rms_epsilon, glu = SiTU and its betas; flags must be 0 (the call
+ * sets its own).  host_ids / host_contributions as
+ * k3x_hip_moe_forward_routed.  Replaces
+ * ComputeBackend::resident_mxfp4_moe_layer (backend.hpp:369-375;
+ * runtime/src/backend_cpu.cpp:305-339, runtime/cuda/backend_cuda.cu:
+ * 1789-2545). */
+int k3x_hip_resident_moe_layer(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
+                               const k3x_hip_latent_weights* weights,
+                               const k3x_hip_moe_params* params, const float* x,
+                               const uint32_t* ids, const float* contributions,
+                               const uint32_t* host_ids, const float* host_contributions,
+                               float* out, float* mixed_out);
 
 /* ---- K3X storage records -------------------------------------------------- */
 

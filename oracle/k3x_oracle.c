@@ -543,6 +543,92 @@ void k3xo_ordered_mix(const float* expert_out, const float* weights,
 }
 
 /* ------------------------------------------------------------------------ */
+/* fp32 backend operations and the resident latent layer:                   */
+/* runtime/src/backend_cpu.cpp                                              */
+/* ------------------------------------------------------------------------ */
+
+/* backend_cpu.cpp:22-45 (dense_matvec): double sum in column order of
+ * double(weight) * input, one rounding to float. */
+void k3xo_dense_matvec(const float* x, const float* weight, size_t rows,
+                       size_t cols, float* out) {
+    for (size_t r = 0; r < rows; ++r) {
+        double sum = 0.0;
+        const float* row = weight + r * cols;
+        for (size_t c = 0; c < cols; ++c) sum += (double)row[c] * x[c];
+        out[r] = (float)sum;
+    }
+}
+
+/* backend_cpu.cpp:108-122 (dense_situ_mlp): gate and up dense_matvec, SiTU
+ * (runtime/src/ops.cpp:20-30), down dense_matvec. */
+void k3xo_dense_situ_mlp(const float* x, size_t hidden, size_t inter,
+                         size_t out_rows, const float* gate, const float* up,
+                         const float* down, float beta, int has_linear,
+                         float linear_beta, float* act, float* out) {
+    float* g = (float*)malloc(inter * sizeof(float));
+    float* u = (float*)malloc(inter * sizeof(float));
+    float* a = (float*)malloc(inter * sizeof(float));
+    if (g && u && a) {
+        k3xo_dense_matvec(x, gate, inter, hidden, g);
+        k3xo_dense_matvec(x, up, inter, hidden, u);
+        k3xo_glu(a, g, u, inter, K3XO_GLU_SITU, beta, has_linear, linear_beta);
+        if (act) memcpy(act, a, inter * sizeof(float));
+        k3xo_dense_matvec(a, down, out_rows, inter, out);
+    }
+    free(g);
+    free(u);
+    free(a);
+}
+
+/* backend_cpu.cpp:305-339 (resident_mxfp4_moe_layer, executed path):
+ * latent = routed_down . input; each expert on the latent
+ * (mxfp4_situ_mlp_group, :124-154); mixed[row] += contribution * output in
+ * slot order from 0; rms_norm (runtime/src/ops.cpp:10-18) with routed_norm;
+ * routed = routed_up . normalized; out = routed + dense_situ_mlp(input). */
+int k3xo_resident_layer(const float* input, size_t hidden, size_t latent,
+                        size_t inter, size_t shared_inter,
+                        const float* routed_down, const float* routed_norm,
+                        const float* routed_up, const float* shared_gate,
+                        const float* shared_up, const float* shared_down,
+                        const uint8_t* const* experts, const float* contributions,
+                        size_t n_experts, float epsilon, float beta,
+                        int has_linear, float linear_beta, float* mixed_out,
+                        float* out) {
+    int status = K3XO_INVALID_MXFP4;
+    float* lat = (float*)malloc(latent * sizeof(float));
+    float* y = (float*)malloc(n_experts * latent * sizeof(float));
+    float* mixed = (float*)malloc(latent * sizeof(float));
+    float* normed = (float*)malloc(latent * sizeof(float));
+    float* routed = (float*)malloc(hidden * sizeof(float));
+    float* shared = (float*)malloc(hidden * sizeof(float));
+    if (!lat || !y || !mixed || !normed || !routed || !shared) goto done;
+    k3xo_dense_matvec(input, routed_down, latent, hidden, lat);
+    for (size_t k = 0; k < n_experts; ++k) {
+        const uint8_t* const* e = experts + 6 * k;
+        status = k3xo_expert_ffn(lat, latent, inter, e[0], e[1], e[2], e[3], e[4], e[5],
+                                 K3XO_GLU_SITU, beta, has_linear, linear_beta, 0, NULL,
+                                 y + k * latent);
+        if (status) goto done;
+    }
+    k3xo_ordered_mix(y, contributions, n_experts, latent, mixed);
+    if (mixed_out) memcpy(mixed_out, mixed, latent * sizeof(float));
+    k3xo_rms_norm(normed, mixed, routed_norm, latent, epsilon);
+    k3xo_dense_matvec(normed, routed_up, hidden, latent, routed);
+    k3xo_dense_situ_mlp(input, hidden, shared_inter, hidden, shared_gate, shared_up,
+                        shared_down, beta, has_linear, linear_beta, NULL, shared);
+    for (size_t h = 0; h < hidden; ++h) out[h] = routed[h] + shared[h];
+    status = K3XO_OK;
+done:
+    free(lat);
+    free(y);
+    free(mixed);
+    free(normed);
+    free(routed);
+    free(shared);
+    return status;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Official K3 MoE FFN (Stable LatentMoE): runtime/src/official_moe.cpp     */
 /* ------------------------------------------------------------------------ */
 

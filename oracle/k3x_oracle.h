@@ -139,6 +139,29 @@ int k3xo_official_ffn(const float* hidden, const float* prefix, size_t width,
                       float* expert_out, float* mixed_out, float* routed_out,
                       float* shared_out, float* out);
 
+/* ---- fp32 backend operations and the resident latent layer --------------*/
+/* y = W x, W fp32 [rows][cols], sequential double sum per row. */
+void k3xo_dense_matvec(const float* x, const float* weight, size_t rows,
+                       size_t cols, float* out);
+/* act = situ_glu(gate x, up x) [inter], out = down act [out_rows]; act may
+ * be NULL. */
+void k3xo_dense_situ_mlp(const float* x, size_t hidden, size_t inter,
+                         size_t out_rows, const float* gate, const float* up,
+                         const float* down, float beta, int has_linear,
+                         float linear_beta, float* act, float* out);
+/* The executed path of the resident latent MoE layer for one token.
+ * experts: per slot, the six pointers of k3xo_official_ffn (an expert of
+ * hidden `latent`, down rows `latent`).  mixed_out [latent] may be NULL. */
+int k3xo_resident_layer(const float* input, size_t hidden, size_t latent,
+                        size_t inter, size_t shared_inter,
+                        const float* routed_down, const float* routed_norm,
+                        const float* routed_up, const float* shared_gate,
+                        const float* shared_up, const float* shared_down,
+                        const uint8_t* const* experts, const float* contributions,
+                        size_t n_experts, float epsilon, float beta,
+                        int has_linear, float linear_beta, float* mixed_out,
+                        float* out);
+
 /* ---- the whole layer, threaded (CPU baseline) ---------------------------*/
 /* expert_bytes: [experts][6] pointers (gate packed, gate scales, up packed,
  * up scales, down packed, down scales); experts no route reaches may be

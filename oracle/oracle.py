@@ -108,6 +108,12 @@ class Oracle:
         L.k3xo_official_ffn.argtypes = ([_f32p, _f32p, _sz, _sz, _sz, _sz] + [_u16p] * 6 +
                                         [C.POINTER(_u8p), _f32p, _sz, C.c_float, C.c_int,
                                          C.c_float, C.c_int, C.c_float] + [_f32p] * 6)
+        L.k3xo_dense_matvec.argtypes = [_f32p, _f32p, _sz, _sz, _f32p]
+        L.k3xo_dense_situ_mlp.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float,
+                                          C.c_int, C.c_float, _f32p, _f32p]
+        L.k3xo_resident_layer.argtypes = ([_f32p, _sz, _sz, _sz, _sz] + [_f32p] * 6 +
+                                          [C.POINTER(_u8p), _f32p, _sz, C.c_float, C.c_float,
+                                           C.c_int, C.c_float, _f32p, _f32p])
         L.k3xo_mix64.restype = C.c_uint64
         L.k3xo_mix64.argtypes = [C.c_uint64]
         L.k3xo_stream_key.restype = C.c_uint64
@@ -354,6 +360,52 @@ class Oracle:
         out["expert_out"] = out["expert_out"].reshape(K, L)
         return st, out
 
+    # -- fp32 backend operations and the resident latent layer ----------------
+    def dense_matvec(self, x, W):
+        """y = W x (fp32 W [rows][cols]), sequential double sums."""
+        x, W = f32(x), f32(W)
+        rows, cols = W.shape
+        out = np.zeros(rows, np.float32)
+        self.lib.k3xo_dense_matvec(_p(x, _f32p), _p(W, _f32p), rows, cols, _p(out, _f32p))
+        return out
+
+    def dense_situ_mlp(self, x, gate, up, down, beta, linear=None):
+        """(act, out) of the fp32 SiTU MLP; gate/up [I][H], down [O][I]."""
+        x, gate, up, down = f32(x), f32(gate), f32(up), f32(down)
+        I, H = gate.shape
+        O = down.shape[0]
+        act = np.zeros(I, np.float32)
+        out = np.zeros(O, np.float32)
+        self.lib.k3xo_dense_situ_mlp(_p(x, _f32p), H, I, O, _p(gate, _f32p), _p(up, _f32p),
+                                     _p(down, _f32p), beta, int(linear is not None),
+                                     linear or 0.0, _p(act, _f32p), _p(out, _f32p))
+        return act, out
+
+    def resident_layer(self, x, weights, experts, contributions, eps, beta, linear=None):
+        """One token of the resident latent layer.  weights: dict of fp32
+        routed_down [L][H], routed_norm [L], routed_up [H][L], shared_gate /
+        shared_up [S][H], shared_down [H][S]; experts: dicts of the six MXFP4
+        arrays at hidden L, in slot order.  Returns status, mixed [L], out [H]."""
+        x = f32(x)
+        w = {k: f32(v) for k, v in weights.items()}
+        L, H = w["routed_down"].shape
+        S = w["shared_gate"].shape[0]
+        keep = [np.ascontiguousarray(e[k], dtype=np.uint8) for e in experts for k in
+                ("gate_packed", "gate_scales", "up_packed", "up_scales", "down_packed",
+                 "down_scales")]
+        I = experts[0]["gate_packed"].size * 2 // L
+        ptrs = (_u8p * len(keep))(*[_p(a, _u8p) for a in keep])
+        c = f32(contributions)
+        mixed = np.zeros(L, np.float32)
+        out = np.zeros(H, np.float32)
+        st = self.lib.k3xo_resident_layer(
+            _p(x, _f32p), H, L, I, S,
+            *[_p(w[k], _f32p) for k in ("routed_down", "routed_norm", "routed_up",
+                                         "shared_gate", "shared_up", "shared_down")],
+            ptrs, _p(c, _f32p), c.size, eps, beta, int(linear is not None), linear or 0.0,
+            _p(mixed, _f32p), _p(out, _f32p))
+        return st, mixed, out
+
     # -- synthetic inputs -----------------------------------------------------
     def moe_layer(self, x, gamma, eps, router, bias, experts, hidden, inter, top_k,
                   routed_scale=1.0, renorm=RENORM_FLOAT, shared=None, glu=GLU_SWIGLU, beta=4.0,
@@ -476,6 +528,11 @@ class RefLib:
         L.k3xr_moe_layer_token.argtypes = [_f32p, _f32p, C.c_float, _f32p, _f32p, _sz, _sz, _sz,
                                            _sz, C.c_float, EB, _f32p, _f32p, _f32p, _sz,
                                            C.c_float, C.c_int, C.c_float, _u32p, _f32p]
+        L.k3xr_dense_situ_mlp.argtypes = [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float,
+                                          C.c_int, C.c_float, _f32p]
+        L.k3xr_resident_layer.argtypes = ([_f32p, _sz, _sz, _sz, _sz] + [_f32p] * 6 +
+                                          [EB, _f32p, _sz, C.c_float, C.c_float, C.c_int,
+                                           C.c_float, C.POINTER(C.c_int), _f32p])
 
     def decode_mxfp4(self, packed, scales, rows, cols, group=32):
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
@@ -552,6 +609,38 @@ class RefLib:
         out = np.zeros(rows, np.float32)
         st = self.lib.k3xr_dense_matvec(_p(x, _f32p), _p(W, _f32p), rows, cols, _p(out, _f32p))
         return st, out
+
+    def dense_situ_mlp(self, x, gate, up, down, beta, linear=None):
+        x, gate, up, down = f32(x), f32(gate), f32(up), f32(down)
+        I, H = gate.shape
+        O = down.shape[0]
+        out = np.zeros(O, np.float32)
+        st = self.lib.k3xr_dense_situ_mlp(_p(x, _f32p), H, I, O, _p(gate, _f32p), _p(up, _f32p),
+                                          _p(down, _f32p), beta, int(linear is not None),
+                                          linear or 0.0, _p(out, _f32p))
+        return st, out
+
+    def resident_layer(self, x, weights, experts, contributions, eps, beta, linear=None):
+        """CpuBackend::resident_mxfp4_moe_layer for one token: status,
+        executed, out [H]."""
+        x = f32(x)
+        w = {k: f32(v) for k, v in weights.items()}
+        L, H = w["routed_down"].shape
+        S = w["shared_gate"].shape[0]
+        I = experts[0]["gate_packed"].size * 2 // L
+        structs, keep = zip(*[expert_struct(e) for e in experts])
+        arr = (_ExpertBytes * len(structs))(*structs)
+        c = f32(contributions)
+        executed = C.c_int(0)
+        out = np.zeros(H, np.float32)
+        st = self.lib.k3xr_resident_layer(
+            _p(x, _f32p), H, L, I, S,
+            *[_p(w[k], _f32p) for k in ("routed_down", "routed_norm", "routed_up",
+                                         "shared_gate", "shared_up", "shared_down")],
+            arr, _p(c, _f32p), c.size, eps, beta, int(linear is not None), linear or 0.0,
+            C.byref(executed), _p(out, _f32p))
+        del keep
+        return st, bool(executed.value), out
 
     def mxfp4_situ_mlp_group(self, x, experts, hidden, inter, beta, linear=None):
         x = f32(x)

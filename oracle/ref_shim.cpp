@@ -387,4 +387,50 @@ int k3xr_official_moe(const float* prefix, const float* block_residual, std::siz
     return 0;
 }
 
+// CpuBackend::dense_situ_mlp (runtime/src/backend_cpu.cpp:108-122).
+int k3xr_dense_situ_mlp(const float* input, std::size_t hidden, std::size_t inter,
+                        std::size_t out_rows, const float* gate, const float* up,
+                        const float* down, float beta, int has_linear, float linear_beta,
+                        float* out) {
+    const k3x::DenseMlpView mlp{{21, {gate, inter * hidden}, inter, hidden},
+                                {22, {up, inter * hidden}, inter, hidden},
+                                {23, {down, out_rows * inter}, out_rows, inter}};
+    auto r = cpu_backend().dense_situ_mlp({input, hidden}, mlp, beta,
+                                          linear_of(has_linear, linear_beta), 0,
+                                          k3x::ProfilePhase::decode);
+    if (!r) return static_cast<int>(r.error());
+    std::memcpy(out, r.value().data(), out_rows * sizeof(float));
+    return 0;
+}
+
+// CpuBackend::resident_mxfp4_moe_layer (runtime/src/backend_cpu.cpp:
+// 305-339) for one token; experts in the K3X layout at the latent width.
+// Returns the error code, or 0 with out [hidden] and *executed.
+int k3xr_resident_layer(const float* input, std::size_t hidden, std::size_t latent,
+                        std::size_t inter, std::size_t shared_inter, const float* routed_down,
+                        const float* routed_norm, const float* routed_up,
+                        const float* shared_gate, const float* shared_up,
+                        const float* shared_down, const ExpertBytes* experts,
+                        const float* contributions, std::size_t n_experts, float epsilon,
+                        float beta, int has_linear, float linear_beta, int* executed,
+                        float* out) {
+    const k3x::ResidentMoeLayerView view{
+        {31, {routed_down, latent * hidden}, latent, hidden},
+        {32, {routed_norm, latent}},
+        {33, {routed_up, hidden * latent}, hidden, latent},
+        {{34, {shared_gate, shared_inter * hidden}, shared_inter, hidden},
+         {35, {shared_up, shared_inter * hidden}, shared_inter, hidden},
+         {36, {shared_down, hidden * shared_inter}, hidden, shared_inter}}};
+    std::vector<k3x::Mxfp4MlpView> views;
+    for (std::size_t e = 0; e < n_experts; ++e)
+        views.push_back(expert_view(experts[e], latent, inter, 64 * (e + 1)));
+    auto r = cpu_backend().resident_mxfp4_moe_layer(
+        {input, hidden}, view, views, {contributions, n_experts}, epsilon, beta,
+        linear_of(has_linear, linear_beta), 0, k3x::ProfilePhase::decode);
+    if (!r) return static_cast<int>(r.error());
+    *executed = r.value().executed ? 1 : 0;
+    std::memcpy(out, r.value().output.data(), r.value().output.size() * sizeof(float));
+    return 0;
+}
+
 }  // extern "C"

@@ -420,6 +420,7 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamSynchronize(ctx->side_stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->latent_scratch) (void)hipFree(ctx->latent_scratch);
     if (ctx->status) (void)hipFree(ctx->status);
     k3x_hip::free_crc(ctx);
     for (const StageMark& m : ctx->pending) {

@@ -32,6 +32,9 @@ struct k3x_hip_ctx {
     // Grow-only scratch (replaces runtime/cuda/device_memory.cuh:44-61).
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Grow-only scratch of the latent layer (k3x_hip_resident_moe_layer).
+    void* latent_scratch = nullptr;
+    size_t latent_bytes = 0;
     // Device address of the fixed scratch of k3x_hip_moe_forward_noalloc on
     // this context's device (null when it could not be taken).
     void* noalloc_scratch = nullptr;

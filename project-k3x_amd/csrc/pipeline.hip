@@ -1388,8 +1388,8 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         return K3X_ERR_INVALID_EXTENT;
     if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
         p->renorm > 1 ||
-        (p->flags &
-         ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT)))
+        (p->flags & ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT |
+                                K3X_FLAG_SPLIT_ACT | K3X_FLAG_SPLIT_INPUT)))
         return K3X_ERR_INVALID_MXFP4;
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
@@ -1598,7 +1598,10 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     // every early return (they read and write this call's scratch).  With
     // stage profiling on, everything stays on the context stream.
     const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
-    const bool wide_path = use_wide_gemm(d, T, K, split);
+    // Split input rows [hi | lo] (2 H): the narrow GEMMs, gate/up over both
+    // halves.
+    const bool split_in = (p->flags & K3X_FLAG_SPLIT_INPUT) != 0;
+    const bool wide_path = !split_in && use_wide_gemm(d, T, K, split);
     const bool side = wide_path && d.shared_inter && !ctx->profiling && ctx->side_stream;
     struct Join {
         k3x_hip_ctx* ctx;
@@ -1653,7 +1656,8 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.kt = bank->gate.kt;
     g.ks = bank->gate.ks;
     g.a = xn;
-    g.a_stride = d.hidden;
+    g.a_stride = split_in ? 2 * d.hidden : d.hidden;
+    g.kta = split_in ? 2 * g.kt : 0;
     g.gather = 1;
     g.n_active = s.n_active;
     g.active = s.active_asc;
@@ -1675,6 +1679,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sg.scales = nullptr;
         sg.codes_per_expert = 0;
         sg.kt = bank->sgate.kt;
+        sg.kta = split_in ? 2 * sg.kt : 0;
         sg.gather = 0;
         sg.n_active = nullptr;
         sg.active = nullptr;
@@ -1738,14 +1743,18 @@ int copy_taps(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_para
     const auto& d = bank->desc;
     const size_t T = p->tokens, K = p->top_k, P = T * K, E = d.experts;
     const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
-    // Split activation rows [hi | lo]: the tap receives the hi halves.
+    // Split rows [hi | lo]: the taps receive the hi halves.
+    if ((p->flags & K3X_FLAG_SPLIT_INPUT) && taps->normed_x && taps->normed_x != xn &&
+        hipMemcpy2DAsync(taps->normed_x, d.hidden * 2, xn, d.hidden * 4, d.hidden * 2, T,
+                         hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
     if (split && taps->act &&
         hipMemcpy2DAsync(taps->act, d.inter * 2, s.act, d.inter * 4, d.inter * 2, P,
                          hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
         return K3X_ERR_BACKEND_UNAVAILABLE;
     struct Item { void* dst; const void* src; size_t bytes; };
     const Item items[] = {
-        {taps->normed_x, xn, T * d.hidden * 2},
+        {taps->normed_x, (p->flags & K3X_FLAG_SPLIT_INPUT) ? nullptr : xn, T * d.hidden * 2},
         {taps->logits, s.logits, T * E * 4},
         {taps->ids, ids, P * 4},
         {taps->weights, weights, P * 4},
@@ -2113,6 +2122,7 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_
     if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
     int st = validate_params(bank, p);
     if (st) return st;
+    if (p->flags & K3X_FLAG_SPLIT_INPUT) return K3X_ERR_INVALID_MXFP4;  // x is raw bf16 here
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     Scratch s;
     if ((st = prepare(ctx, bank, p, &s))) return st;
@@ -2125,6 +2135,7 @@ int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
     if (!ctx || !bank || !p || !x || !out || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
     int st = validate_params(bank, p);
     if (st) return st;
+    if (p->flags & K3X_FLAG_SPLIT_INPUT) return K3X_ERR_INVALID_MXFP4;  // x is raw bf16 here
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     if (!ctx->noalloc_scratch) return K3X_ERR_BACKEND_UNAVAILABLE;
     Scratch s;

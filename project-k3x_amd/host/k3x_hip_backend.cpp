@@ -98,6 +98,23 @@ struct HipMoeBackend::Impl {
     };
     Dev xn, ids, w, out, out_f32, pairs;
 
+    // Resident single matrices (fp32 dense weights, row-major MXFP4
+    // matrices), keyed by tensor id; identity = host data, bytes and shape,
+    // and a changed identity is uploaded again.  Least recently used first
+    // out within opt.resident_dense_bytes; entries used by the current call
+    // (last_use == dense_tick) stay.
+    struct Resident {
+        void* p = nullptr;
+        std::size_t bytes = 0;
+        const void* host = nullptr;
+        std::size_t host_bytes = 0, rows = 0, cols = 0;
+        std::uint64_t last_use = 0;
+    };
+    std::map<std::uint64_t, Resident> resident;
+    std::uint64_t resident_total = 0;
+    std::uint64_t dense_tick = 0;
+    Dev transient[3], vin, vout, vact, vids, vc;
+
     // Official layer: per layer, a route-only object for the preparation;
     // per (layer, H, L, I, Is), the FFN object over a bank of latent experts.
     // Dense weights are uploaded again when a tensor id or its host data
@@ -138,8 +155,10 @@ struct HipMoeBackend::Impl {
         for (auto& kv : banks) k3x_hip_bank_destroy(kv.second.bank);
         for (Dev* d : {&xn, &ids, &w, &out, &out_f32, &pairs, &prep_prefix, &prep_block,
                        &prep_hidden, &prep_logits, &o_hidden, &o_prefix, &o_ids, &o_contrib,
-                       &o_out})
+                       &o_out, &transient[0], &transient[1], &transient[2], &vin, &vout, &vact,
+                       &vids, &vc})
             if (d->p) (void)hipFree(d->p);
+        for (auto& kv : resident) (void)hipFree(kv.second.p);
         if (ctx) k3x_hip_ctx_destroy(ctx);
     }
 
@@ -156,6 +175,101 @@ struct HipMoeBackend::Impl {
         }
         d.bytes = n;
         return ErrorCode::ok;
+    }
+
+    // One matrix as device bytes: its host segments (data, bytes) placed
+    // 256-byte aligned one after the other.  `check` (may be null) runs on
+    // the host data before any upload and rejects it with its error code.
+    // Returns the device base, or nullptr with ok when the resident budget
+    // cannot hold it (then `fallback`, if given, receives a transient copy).
+    struct Segment {
+        const void* data;
+        std::size_t bytes;
+    };
+    template <typename Check>
+    ErrorCode acquire(std::uint64_t id, std::initializer_list<Segment> segs, std::size_t rows,
+                      std::size_t cols, Check check, Dev* fallback, const void** out) {
+        *out = nullptr;
+        std::size_t total = 0;
+        for (const Segment& g : segs) total += (g.bytes + 255) & ~(std::size_t)255;
+        const Segment first = *segs.begin();
+        // Tensor id 0 names no tensor (the reference's convenience overloads
+        // pass it): always a transient copy.
+        auto it = id ? resident.find(id) : resident.end();
+        if (it != resident.end() && it->second.host == first.data &&
+            it->second.host_bytes == total && it->second.rows == rows && it->second.cols == cols) {
+            it->second.last_use = dense_tick;
+            *out = it->second.p;
+            return ErrorCode::ok;
+        }
+        if (ErrorCode c = check(); c != ErrorCode::ok) return c;
+        if (it != resident.end()) {  // same id, other data: replaced
+            (void)hipFree(it->second.p);
+            resident_total -= it->second.bytes;
+            resident.erase(it);
+        }
+        void* dst = nullptr;
+        const bool fits_budget = id != 0 && total <= opt.resident_dense_bytes;
+        while (fits_budget && resident_total + total > opt.resident_dense_bytes) {
+            auto victim = resident.end();
+            for (auto r = resident.begin(); r != resident.end(); ++r)
+                if (r->second.last_use != dense_tick &&
+                    (victim == resident.end() || r->second.last_use < victim->second.last_use))
+                    victim = r;
+            if (victim == resident.end()) break;
+            (void)hipFree(victim->second.p);
+            resident_total -= victim->second.bytes;
+            resident.erase(victim);
+        }
+        if (fits_budget && resident_total + total <= opt.resident_dense_bytes) {
+            if (hipMalloc(&dst, total) != hipSuccess) {
+                (void)hipGetLastError();
+                dst = nullptr;
+            }
+        }
+        if (!dst) {
+            if (!fallback) return ErrorCode::ok;  // not resident: the caller bypasses
+            if (ErrorCode c = ensure(*fallback, total); c != ErrorCode::ok) return c;
+            dst = fallback->p;
+        }
+        std::size_t at = 0;
+        for (const Segment& g : segs) {
+            if (g.bytes && hipMemcpy(static_cast<std::uint8_t*>(dst) + at, g.data, g.bytes,
+                                     hipMemcpyHostToDevice) != hipSuccess)
+                return ErrorCode::backend_unavailable;
+            at += (g.bytes + 255) & ~(std::size_t)255;
+        }
+        stats.weight_h2d_bytes += total;
+        ++stats.dense_uploads;
+        if (!fallback || dst != fallback->p) {
+            Resident r;
+            r.p = dst;
+            r.bytes = total;
+            r.host = first.data;
+            r.host_bytes = total;
+            r.rows = rows;
+            r.cols = cols;
+            r.last_use = dense_tick;
+            resident[id] = r;
+            resident_total += total;
+        }
+        *out = dst;
+        return ErrorCode::ok;
+    }
+
+    ErrorCode upload(Dev& d, const void* host, std::size_t bytes) {
+        if (ErrorCode c = ensure(d, std::max<std::size_t>(bytes, 16)); c != ErrorCode::ok) return c;
+        return hipMemcpy(d.p, host, bytes, hipMemcpyHostToDevice) == hipSuccess
+                   ? ErrorCode::ok
+                   : ErrorCode::backend_unavailable;
+    }
+
+    ErrorCode finish(const Dev& d, std::vector<float>& out, std::size_t n) {
+        if (int st = k3x_hip_ctx_synchronize(ctx)) return code_of(st);
+        out.resize(n);
+        return hipMemcpy(out.data(), d.p, n * 4, hipMemcpyDeviceToHost) == hipSuccess
+                   ? ErrorCode::ok
+                   : ErrorCode::backend_unavailable;
     }
 
     // The layer's shapes this library runs: group size 32 (as the CUDA
@@ -924,6 +1038,290 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
     ++m.stats.calls;
     ++m.stats.layer_calls;
     return R::success(std::move(r));
+}
+
+namespace {
+
+// backend_cpu.cpp:365-374 (valid_dense).
+bool valid_dense(std::size_t input_size, const DenseWeightView& w) {
+    if (input_size != w.cols || w.rows > w.values.size() ||
+        (w.cols != 0 && w.rows > w.values.size() / w.cols))
+        return false;
+    return w.values.size() == w.rows * w.cols;
+}
+
+// backend_cpu.cpp:410-420 (valid_dense_size: non-empty as well).
+bool valid_dense_size(std::size_t input_size, const DenseWeightView& w) {
+    return w.rows && w.cols && valid_dense(input_size, w);
+}
+
+// backend_cpu.cpp:403-408 (valid_dense_mlp).
+bool valid_dense_mlp(std::size_t input_size, const DenseMlpView& m) {
+    return valid_dense(input_size, m.gate) && valid_dense(input_size, m.up) && m.gate.rows != 0 &&
+           m.gate.rows == m.up.rows && valid_dense_size(m.gate.rows, m.down);
+}
+
+bool all_finite(std::span<const float> v) {
+    for (float x : v)
+        if (!std::isfinite(x)) return false;
+    return true;
+}
+
+std::span<const float> as_span(const float* p, std::size_t n) { return {p, n}; }
+
+}  // namespace
+
+Result<std::vector<float>> HipMoeBackend::dense_matvec(std::span<const float> input,
+                                                       DenseWeightView weight, std::uint32_t,
+                                                       ProfilePhase) {
+    using R = Result<std::vector<float>>;
+    if (!valid_dense(input.size(), weight)) return R::failure(ErrorCode::invalid_extent);
+    if (!weight.rows || !weight.cols) return R::success(std::vector<float>(weight.rows, 0.0f));
+    if (weight.rows > (1u << 24) || weight.cols > (1u << 24))
+        return R::failure(ErrorCode::backend_unavailable);
+    Impl& m = *impl_;
+    ++m.dense_tick;
+    const void* W = nullptr;
+    auto none = [] { return ErrorCode::ok; };
+    if (ErrorCode c = m.acquire(weight.tensor_id, {{weight.values.data(), weight.values.size_bytes()}},
+                                weight.rows, weight.cols, none, &m.transient[0], &W);
+        c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.ensure(m.vout, weight.rows * 4); c != ErrorCode::ok) return R::failure(c);
+    if (int st = k3x_hip_dense_f32_matvec(m.ctx, static_cast<const float*>(W),
+                                          (std::uint32_t)weight.rows, (std::uint32_t)weight.cols,
+                                          static_cast<const float*>(m.vin.p), 1,
+                                          static_cast<float*>(m.vout.p)))
+        return R::failure(code_of(st));
+    std::vector<float> out;
+    if (ErrorCode c = m.finish(m.vout, out, weight.rows); c != ErrorCode::ok) return R::failure(c);
+    ++m.stats.calls;
+    return R::success(std::move(out));
+}
+
+Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> input,
+                                                       Mxfp4WeightView weight, std::uint32_t,
+                                                       ProfilePhase) {
+    using R = Result<std::vector<float>>;
+    // mxfp4_matmul and decode_mxfp4 (runtime/src/ops.cpp:32-76): extents
+    // first, then the scale bytes (at upload; a resident copy was checked).
+    if (input.size() != weight.cols || !weight.rows || !weight.cols || !weight.group_size ||
+        weight.cols % weight.group_size || weight.cols % 2 || !mul_fits(weight.rows, weight.cols) ||
+        weight.packed.size() != weight.rows * weight.cols / 2 ||
+        weight.scales.size() != weight.rows * weight.cols / weight.group_size)
+        return R::failure(ErrorCode::invalid_mxfp4);
+    if (weight.group_size != 32 || weight.rows > (1u << 24) || weight.cols > (1u << 24))
+        return R::failure(ErrorCode::backend_unavailable, "group size 32 only");
+    Impl& m = *impl_;
+    ++m.dense_tick;
+    auto scales_ok = [&] {
+        for (const std::byte b : weight.scales)
+            if (b == std::byte{0xff}) return ErrorCode::invalid_mxfp4;
+        return ErrorCode::ok;
+    };
+    const void* W = nullptr;
+    if (ErrorCode c = m.acquire(weight.tensor_id,
+                                {{weight.packed.data(), weight.packed.size()},
+                                 {weight.scales.data(), weight.scales.size()}},
+                                weight.rows, weight.cols, scales_ok, &m.transient[0], &W);
+        c != ErrorCode::ok)
+        return R::failure(c);
+    const std::uint8_t* packed = static_cast<const std::uint8_t*>(W);
+    const std::uint8_t* scales = packed + ((weight.packed.size() + 255) & ~(std::size_t)255);
+    if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.ensure(m.vout, weight.rows * 4); c != ErrorCode::ok) return R::failure(c);
+    if (int st = k3x_hip_mxfp4_matvec(m.ctx, packed, scales, (std::uint32_t)weight.rows,
+                                      (std::uint32_t)weight.cols,
+                                      static_cast<const float*>(m.vin.p), 1,
+                                      static_cast<float*>(m.vout.p)))
+        return R::failure(code_of(st));
+    std::vector<float> out;
+    if (ErrorCode c = m.finish(m.vout, out, weight.rows); c != ErrorCode::ok) return R::failure(c);
+    ++m.stats.calls;
+    return R::success(std::move(out));
+}
+
+Result<Outputs> HipMoeBackend::dense_matvec_group(std::span<const float> input,
+                                                  std::span<const DenseWeightView> weights,
+                                                  std::uint32_t layer, ProfilePhase phase) {
+    for (const auto& w : weights)
+        if (!valid_dense(input.size(), w)) return Result<Outputs>::failure(ErrorCode::invalid_extent);
+    Outputs out;
+    out.reserve(weights.size());
+    for (const auto& w : weights) {
+        auto r = dense_matvec(input, w, layer, phase);
+        if (!r) return Result<Outputs>::failure(r.error(), r.message());
+        out.push_back(std::move(r.value()));
+    }
+    return Result<Outputs>::success(std::move(out));
+}
+
+Result<Outputs> HipMoeBackend::mxfp4_matvec_group(std::span<const float> input,
+                                                  std::span<const Mxfp4WeightView> weights,
+                                                  std::uint32_t layer, ProfilePhase phase) {
+    for (const auto& w : weights)
+        if (!valid_mxfp4(input.size(), w)) return Result<Outputs>::failure(ErrorCode::invalid_mxfp4);
+    Outputs out;
+    out.reserve(weights.size());
+    for (const auto& w : weights) {
+        auto r = mxfp4_matvec(input, w, layer, phase);
+        if (!r) return Result<Outputs>::failure(r.error(), r.message());
+        out.push_back(std::move(r.value()));
+    }
+    return Result<Outputs>::success(std::move(out));
+}
+
+Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> input,
+                                                         DenseMlpView weights, float situ_beta,
+                                                         std::optional<float> situ_linear,
+                                                         std::uint32_t, ProfilePhase) {
+    using R = Result<std::vector<float>>;
+    if (!valid_dense_mlp(input.size(), weights)) return R::failure(ErrorCode::invalid_extent);
+    const std::size_t H = input.size(), I = weights.gate.rows, O = weights.down.rows;
+    if (!H || H > (1u << 24) || I > (1u << 24) || O > (1u << 24))
+        return R::failure(ErrorCode::backend_unavailable);
+    Impl& m = *impl_;
+    ++m.dense_tick;
+    auto none = [] { return ErrorCode::ok; };
+    const void* W[3] = {};
+    const DenseWeightView* v[3] = {&weights.gate, &weights.up, &weights.down};
+    for (int i = 0; i < 3; ++i)
+        if (ErrorCode c = m.acquire(v[i]->tensor_id, {{v[i]->values.data(), v[i]->values.size_bytes()}},
+                                    v[i]->rows, v[i]->cols, none, &m.transient[i], &W[i]);
+            c != ErrorCode::ok)
+            return R::failure(c);
+    if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.ensure(m.vact, I * 4); c != ErrorCode::ok) return R::failure(c);
+    if (ErrorCode c = m.ensure(m.vout, O * 4); c != ErrorCode::ok) return R::failure(c);
+    if (int st = k3x_hip_dense_situ_mlp(
+            m.ctx, static_cast<const float*>(W[0]), static_cast<const float*>(W[1]),
+            static_cast<const float*>(W[2]), (std::uint32_t)H, (std::uint32_t)I, (std::uint32_t)O,
+            situ_beta, situ_linear.has_value(), situ_linear.value_or(0.0f),
+            static_cast<const float*>(m.vin.p), 1, static_cast<float*>(m.vact.p),
+            static_cast<float*>(m.vout.p)))
+        return R::failure(code_of(st));
+    std::vector<float> out;
+    if (ErrorCode c = m.finish(m.vout, out, O); c != ErrorCode::ok) return R::failure(c);
+    ++m.stats.calls;
+    return R::success(std::move(out));
+}
+
+Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
+    std::span<const float> input, ResidentMoeLayerView weights,
+    std::span<const Mxfp4MlpView> experts, std::span<const float> contributions, float epsilon,
+    float situ_beta, std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    using R = Result<ResidentMoeLayerResult>;
+    const auto bad = [] { return R::failure(ErrorCode::invalid_mxfp4); };
+    // valid_resident_moe_layer (backend_cpu.cpp:441-497); the finiteness of
+    // the dense weights is checked when they are uploaded (a resident copy
+    // was checked then).
+    if (input.empty() || experts.empty() || experts.size() != contributions.size() ||
+        !std::isfinite(epsilon) || epsilon <= 0.0f || !valid_situ(situ_beta, situ_linear) ||
+        !all_finite(input) || !all_finite(contributions) ||
+        !valid_dense(input.size(), weights.routed_down) ||
+        !valid_dense_mlp(input.size(), weights.shared))
+        return bad();
+    const std::size_t H = input.size(), L = weights.routed_down.rows,
+                      W = experts.front().down.rows;
+    if (L == 0 || W == 0 || weights.routed_norm.values.size() != W ||
+        !valid_dense_size(W, weights.routed_up) || weights.routed_up.rows != H ||
+        weights.shared.down.rows != H)
+        return bad();
+    std::vector<std::uint64_t> ids;
+    auto insert_id = [&](std::uint64_t id) {
+        if (id == 0 || std::find(ids.begin(), ids.end(), id) != ids.end()) return false;
+        ids.push_back(id);
+        return true;
+    };
+    if (!insert_id(weights.routed_down.tensor_id) || !insert_id(weights.routed_norm.tensor_id) ||
+        !insert_id(weights.routed_up.tensor_id) || !insert_id(weights.shared.gate.tensor_id) ||
+        !insert_id(weights.shared.up.tensor_id) || !insert_id(weights.shared.down.tensor_id))
+        return bad();
+    const std::size_t I = experts.front().gate.rows;
+    for (const auto& e : experts)
+        if (!valid_mxfp4_mlp(L, e) || e.gate.rows != I || e.down.rows != W ||
+            e.gate.group_size != 32 || e.up.group_size != 32 || e.down.group_size != 32 ||
+            !insert_id(e.gate.tensor_id) || !insert_id(e.up.tensor_id) ||
+            !insert_id(e.down.tensor_id))
+            return bad();
+    // Shapes the device path runs: routed width = latent (a square expert
+    // bank), widths multiples of 128, one layer call of at most 64 slots.
+    if (W != L || experts.size() > kMaxSlotsPerToken || H > (1u << 24) ||
+        weights.shared.gate.rows > (1u << 24))
+        return R::failure(ErrorCode::backend_unavailable);
+    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok) return R::failure(c);
+    Impl& m = *impl_;
+    auto bypass = [&] {
+        ++m.stats.resident_layer_fallbacks;
+        return R::success(ResidentMoeLayerResult{false, {}});
+    };
+    // Experts into the bank's slots: more distinct experts than slots is the
+    // capacity bypass.
+    auto bank = m.bank_for(layer, L, I);
+    if (!bank) return R::failure(bank.error(), bank.message());
+    if (experts.size() > bank.value()->slots.size()) return bypass();
+    std::vector<std::uint32_t> slot;
+    if (ErrorCode c = m.admit(*bank.value(), experts, slot); c != ErrorCode::ok) return R::failure(c);
+    // The six dense weights resident, or the bypass.
+    ++m.dense_tick;
+    const DenseWeightView norm_view{weights.routed_norm.tensor_id, weights.routed_norm.values, 1,
+                                    W};
+    const DenseWeightView* dv[6] = {&weights.routed_down, &norm_view,          &weights.routed_up,
+                                    &weights.shared.gate, &weights.shared.up, &weights.shared.down};
+    const void* dp[6] = {};
+    for (int i = 0; i < 6; ++i) {
+        const DenseWeightView& v = *dv[i];
+        auto finite = [&] {
+            return all_finite(as_span(v.values.data(), v.values.size())) ? ErrorCode::ok
+                                                                          : ErrorCode::invalid_mxfp4;
+        };
+        if (ErrorCode c = m.acquire(v.tensor_id, {{v.values.data(), v.values.size_bytes()}}, v.rows,
+                                    v.cols, finite, nullptr, &dp[i]);
+            c != ErrorCode::ok)
+            return R::failure(c);
+        if (!dp[i]) return bypass();
+    }
+    const std::size_t K = experts.size();
+    if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.upload(m.vids, slot.data(), K * 4); c != ErrorCode::ok) return R::failure(c);
+    if (ErrorCode c = m.upload(m.vc, contributions.data(), K * 4); c != ErrorCode::ok)
+        return R::failure(c);
+    if (ErrorCode c = m.ensure(m.vout, H * 4); c != ErrorCode::ok) return R::failure(c);
+    k3x_hip_latent_weights lw{};
+    lw.routed_down = static_cast<const float*>(dp[0]);
+    lw.routed_norm = static_cast<const float*>(dp[1]);
+    lw.routed_up = static_cast<const float*>(dp[2]);
+    lw.shared_gate = static_cast<const float*>(dp[3]);
+    lw.shared_up = static_cast<const float*>(dp[4]);
+    lw.shared_down = static_cast<const float*>(dp[5]);
+    lw.hidden = (std::uint32_t)H;
+    lw.latent = (std::uint32_t)L;
+    lw.shared_inter = (std::uint32_t)weights.shared.gate.rows;
+    k3x_hip_moe_params p{};
+    p.tokens = 1;
+    p.top_k = (std::uint32_t)K;
+    p.routed_scale = 1.0f;
+    p.rms_epsilon = epsilon;
+    p.glu = K3X_GLU_SITU;
+    p.situ_beta = situ_beta;
+    p.has_situ_linear = situ_linear.has_value();
+    p.situ_linear_beta = situ_linear.value_or(0.0f);
+    p.renorm = K3X_RENORM_FLOAT;
+    if (int st = k3x_hip_resident_moe_layer(
+            m.ctx, bank.value()->bank, &lw, &p, static_cast<const float*>(m.vin.p),
+            static_cast<const std::uint32_t*>(m.vids.p), static_cast<const float*>(m.vc.p),
+            slot.data(), contributions.data(), static_cast<float*>(m.vout.p), nullptr))
+        return R::failure(code_of(st));
+    ResidentMoeLayerResult res{true, {}};
+    if (ErrorCode c = m.finish(m.vout, res.output, H); c != ErrorCode::ok) return R::failure(c);
+    ++m.stats.calls;
+    ++m.stats.layer_calls;
+    return R::success(std::move(res));
 }
 
 HipBackendStats HipMoeBackend::runtime_stats() const noexcept {

@@ -99,6 +99,40 @@ struct Mxfp4WeightView {
     std::size_t group_size;
 };
 
+// fp32 dense views (backend.hpp:131-136, :204-207, :165-169): values
+// row-major [rows][cols].
+struct DenseWeightView {
+    std::uint64_t tensor_id;
+    std::span<const float> values;
+    std::size_t rows;
+    std::size_t cols;
+};
+
+struct DenseVectorView {
+    std::uint64_t tensor_id;
+    std::span<const float> values;
+};
+
+struct DenseMlpView {
+    DenseWeightView gate;
+    DenseWeightView up;
+    DenseWeightView down;
+};
+
+// The resident latent layer's dense weights and result (backend.hpp:
+// 302-312).
+struct ResidentMoeLayerView {
+    DenseWeightView routed_down;
+    DenseVectorView routed_norm;
+    DenseWeightView routed_up;
+    DenseMlpView shared;
+};
+
+struct ResidentMoeLayerResult {
+    bool executed{};
+    std::vector<float> output;
+};
+
 // gate [I x H], up [I x H], down [out x I] (backend.hpp:315-319).
 struct Mxfp4MlpView {
     Mxfp4WeightView gate;
@@ -177,6 +211,11 @@ struct HipBackendOptions {
     // one expert (hidden * intermediate * 3 * 17 / 32 bytes, 23.4 MB at
     // 7168 x 2048).
     std::uint32_t resident_experts = 64;
+    // Device bytes for resident fp32 dense weights and single MXFP4
+    // matrices (the matvec methods and the latent layer's dense weights),
+    // least recently used first out; a matrix that does not fit runs from a
+    // transient upload (matvec methods) or bypasses the latent layer.
+    std::uint64_t resident_dense_bytes = 8ull << 30;
 };
 
 struct HipBackendStats {
@@ -186,6 +225,8 @@ struct HipBackendStats {
     std::uint64_t experts_admitted = 0;  // slot uploads
     std::uint64_t residency_hits = 0;    // experts found resident
     std::uint64_t weight_h2d_bytes = 0;
+    std::uint64_t dense_uploads = 0;             // dense / single-matrix uploads
+    std::uint64_t resident_layer_fallbacks = 0;  // latent layer calls returned executed=false
 };
 
 class HipMoeBackend {
@@ -278,6 +319,43 @@ public:
         std::span<const float> latents, std::size_t positions,
         std::span<const ExpertMajorTokenRoute> routes, std::span<const Mxfp4MlpView> experts,
         float situ_beta, std::optional<float> situ_linear, std::uint32_t layer,
+        ProfilePhase phase);
+
+    // y = W x in fp32 with double sums (backend.hpp:333-335,
+    // backend_cpu.cpp:22-45); invalid_extent when the extents disagree.
+    Result<std::vector<float>> dense_matvec(std::span<const float> input, DenseWeightView weight,
+                                            std::uint32_t layer, ProfilePhase phase);
+    // y = W x for one MXFP4 matrix (backend.hpp:336-338, backend_cpu.cpp:
+    // 47-59); invalid_mxfp4 for a malformed matrix (a 0xFF scale included),
+    // backend_unavailable for a group size other than 32.
+    Result<std::vector<float>> mxfp4_matvec(std::span<const float> input, Mxfp4WeightView weight,
+                                            std::uint32_t layer, ProfilePhase phase);
+    // Every weight checked first, then one product each (backend.hpp:339-344,
+    // backend_cpu.cpp:61-106).
+    Result<std::vector<std::vector<float>>> dense_matvec_group(
+        std::span<const float> input, std::span<const DenseWeightView> weights,
+        std::uint32_t layer, ProfilePhase phase);
+    Result<std::vector<std::vector<float>>> mxfp4_matvec_group(
+        std::span<const float> input, std::span<const Mxfp4WeightView> weights,
+        std::uint32_t layer, ProfilePhase phase);
+    // down(situ(gate x, up x)) in fp32 (backend.hpp:345-348, backend_cpu.cpp:
+    // 108-122).
+    Result<std::vector<float>> dense_situ_mlp(std::span<const float> input, DenseMlpView weights,
+                                              float situ_beta, std::optional<float> situ_linear,
+                                              std::uint32_t layer, ProfilePhase phase);
+    // The resident latent MoE layer for one token (backend.hpp:369-375):
+    // latent = routed_down x, the experts on the fp32 latent mixed in slot
+    // order, RMSNorm with routed_norm, routed_up, plus the fp32 SiTU shared
+    // MLP of x (backend_cpu.cpp:305-339).  Arguments are checked as
+    // valid_resident_moe_layer (backend_cpu.cpp:441-497, invalid_mxfp4).
+    // When the experts or the dense weights cannot all be resident (more
+    // experts than bank slots, dense weights over resident_dense_bytes) the
+    // call succeeds with executed = false and no output, for the caller's
+    // split path (backend_cuda.cu:1995-2003).
+    Result<ResidentMoeLayerResult> resident_mxfp4_moe_layer(
+        std::span<const float> input, ResidentMoeLayerView weights,
+        std::span<const Mxfp4MlpView> experts, std::span<const float> contributions,
+        float epsilon, float situ_beta, std::optional<float> situ_linear, std::uint32_t layer,
         ProfilePhase phase);
 
     HipBackendStats runtime_stats() const noexcept;

@@ -69,6 +69,14 @@ class MoeParams(C.Structure):
 
 FLAG_GENERAL_PATH = 1
 FLAG_ROUND_EXPERT_OUT = 2
+FLAG_SPLIT_ACT = 4
+FLAG_SPLIT_INPUT = 8
+
+
+class LatentWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("routed_down", "routed_norm", "routed_up",
+                                         "shared_gate", "shared_up", "shared_down")] + \
+               [("hidden", C.c_uint32), ("latent", C.c_uint32), ("shared_inter", C.c_uint32)]
 
 
 TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair_token",
@@ -160,6 +168,16 @@ _SIGS = {
     "k3x_hip_official_prepare": (C.c_int, [_vp, _vp, C.c_uint32, C.c_float, _vp, _vp, _vp, _vp]),
     "k3x_hip_official_ffn": (C.c_int, [_vp, _vp, C.POINTER(MoeParams), _vp, _vp, _vp, _vp, _vp,
                                        C.POINTER(OfficialTaps)]),
+    "k3x_hip_dense_f32_matvec": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, _vp, C.c_uint32,
+                                           _vp]),
+    "k3x_hip_mxfp4_matvec": (C.c_int, [_vp, _vp, _vp, C.c_uint32, C.c_uint32, _vp, C.c_uint32,
+                                       _vp]),
+    "k3x_hip_dense_situ_mlp": (C.c_int, [_vp, _vp, _vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
+                                         C.c_float, C.c_int, C.c_float, _vp, C.c_uint32, _vp,
+                                         _vp]),
+    "k3x_hip_resident_moe_layer": (C.c_int, [_vp, _vp, C.POINTER(LatentWeights),
+                                             C.POINTER(MoeParams), _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _vp]),
 }
 
 EXPORTED = sorted(_SIGS)
@@ -479,6 +497,46 @@ def moe_forward_routed(ctx: Context, bank: Bank, params: MoeParams, xn, ids, wei
         ctx.handle, bank.handle, C.byref(params), ptr(xn), ptr(ids), ptr(weights),
         host_ptr(host_ids), host_ptr(host_weights), ptr(out),
         C.byref(t) if t is not None else None)
+
+
+def dense_f32_matvec(ctx: Context, W, x, y) -> int:
+    """y [T][rows] = W [rows][cols] x [T][cols] (fp32 device tensors)."""
+    rows, cols = W.shape
+    T = x.numel() // cols
+    return load().k3x_hip_dense_f32_matvec(ctx.handle, ptr(W), rows, cols, ptr(x), T, ptr(y))
+
+
+def mxfp4_matvec(ctx: Context, packed, scales, rows: int, cols: int, x, y) -> int:
+    """y [T][rows] = an MXFP4 matrix (K3X layout, device uint8 tensors) x."""
+    T = x.numel() // cols
+    return load().k3x_hip_mxfp4_matvec(ctx.handle, ptr(packed), ptr(scales), rows, cols, ptr(x),
+                                       T, ptr(y))
+
+
+def dense_situ_mlp(ctx: Context, gate, up, down, x, act, y, beta=4.0, linear=None) -> int:
+    inter, hidden = gate.shape
+    out_rows = down.shape[0]
+    T = x.numel() // hidden
+    return load().k3x_hip_dense_situ_mlp(ctx.handle, ptr(gate), ptr(up), ptr(down), hidden,
+                                         inter, out_rows, beta, int(linear is not None),
+                                         linear or 0.0, ptr(x), T, ptr(act), ptr(y))
+
+
+def resident_moe_layer(ctx: Context, bank: "Bank", weights: dict, params: MoeParams, x, ids,
+                       contributions, out, mixed=None, host_ids=None,
+                       host_contributions=None) -> int:
+    """The resident latent layer: weights is a dict of fp32 device tensors
+    (routed_down [L][H], routed_norm [L], routed_up [H][L], shared_gate /
+    shared_up [S][H], shared_down [H][S])."""
+    L, H = weights["routed_down"].shape
+    S = weights["shared_gate"].shape[0]
+    w = LatentWeights(*[ptr(weights[k]) for k in ("routed_down", "routed_norm", "routed_up",
+                                                  "shared_gate", "shared_up", "shared_down")],
+                      H, L, S)
+    return load().k3x_hip_resident_moe_layer(
+        ctx.handle, bank.handle, C.byref(w), C.byref(params), ptr(x), ptr(ids),
+        ptr(contributions), host_ptr(host_ids), host_ptr(host_contributions), ptr(out),
+        ptr(mixed))
 
 
 def expert_major_plan(ctx: Context, ids, tokens, top_k, experts, taps: dict) -> int:

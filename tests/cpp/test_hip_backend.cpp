@@ -108,6 +108,229 @@ bool identical(const std::vector<float>& a, const std::vector<float>& b) {
     return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * 4) == 0;
 }
 
+// ---- fp32 operations and the resident latent layer ---------------------------
+// dense_matvec, mxfp4_matvec (+ groups) and dense_situ_mlp against the
+// oracle's restatement of backend_cpu.cpp:22-122 (double sums on both sides,
+// only the order differs: within 2 ulps, |d| <= 2.5e-7 |ref| + 1e-30), the
+// fp32 MLP within 1e-5 of its output scale (the device's expf / tanhf); the
+// resident latent layer (backend_cpu.cpp:305-339) within 1e-3 of its output
+// scale; then the reference's rejections and the capacity bypass
+// (executed = false).
+constexpr std::size_t LH = 384, LL = 128, LI = 256, LS = 192;
+constexpr float kLatentEps = 1e-6f;
+
+std::vector<float> rand_f32(std::size_t n, float scale) {
+    std::vector<float> v(n);
+    for (auto& f : v) f = scale * (float)((int)(next_u32() % 20001) - 10000) / 10000.0f;
+    return v;
+}
+
+struct ResidentExpert {
+    std::vector<std::byte> gp, gs, up, us, dp, ds;
+    std::uint64_t id;
+    Mxfp4MlpView view() const {
+        return {{id, gp, gs, LI, LL, G}, {id + 1, up, us, LI, LL, G}, {id + 2, dp, ds, LL, LI, G}};
+    }
+    const std::uint8_t* const* ptrs(const std::uint8_t* (&p)[6]) const {
+        const std::vector<std::byte>* v[6] = {&gp, &gs, &up, &us, &dp, &ds};
+        for (int i = 0; i < 6; ++i) p[i] = reinterpret_cast<const std::uint8_t*>(v[i]->data());
+        return p;
+    }
+};
+
+ResidentExpert make_resident_expert(std::uint64_t id) {
+    ResidentExpert e;
+    e.id = id;
+    auto codes = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& b : v) b = std::byte(next_u32() & 0xff);
+        return v;
+    };
+    auto scales = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& b : v) b = std::byte(121 + next_u32() % 5);
+        return v;
+    };
+    e.gp = codes(LI * LL / 2);
+    e.gs = scales(LI * LL / G);
+    e.up = codes(LI * LL / 2);
+    e.us = scales(LI * LL / G);
+    e.dp = codes(LL * LI / 2);
+    e.ds = scales(LL * LI / G);
+    return e;
+}
+
+bool near(const std::vector<float>& got, const std::vector<float>& ref, float rel, float abs_of_scale,
+            const char* what) {
+    if (got.size() != ref.size()) {
+        std::printf("%s: size %zu, want %zu\n", what, got.size(), ref.size());
+        return false;
+    }
+    float scale = 0.0f;
+    for (float r : ref) scale = std::fmax(scale, std::fabs(r));
+    for (std::size_t i = 0; i < ref.size(); ++i)
+        if (!(std::fabs(got[i] - ref[i]) <= rel * std::fabs(ref[i]) + abs_of_scale * scale + 1e-30f)) {
+            std::printf("%s: [%zu] %.9g, oracle %.9g (scale %.6g)\n", what, i, got[i], ref[i],
+                        scale);
+            return false;
+        }
+    return true;
+}
+
+int latent_checks(k3x_amd::HipMoeBackend& b) {
+    using k3x_amd::DenseMlpView;
+    using k3x_amd::DenseWeightView;
+    // dense_matvec and its group.
+    const auto W0 = rand_f32(LL * LH, 0.05f), W1 = rand_f32(LS * LH, 0.05f);
+    const auto xin = rand_f32(LH, 1.0f);
+    std::vector<float> want0(LL), want1(LS);
+    k3xo_dense_matvec(xin.data(), W0.data(), LL, LH, want0.data());
+    k3xo_dense_matvec(xin.data(), W1.data(), LS, LH, want1.data());
+    const DenseWeightView dv[2] = {{701, W0, LL, LH}, {702, W1, LS, LH}};
+    auto d0 = b.dense_matvec(xin, dv[0], 3, ProfilePhase::decode);
+    if (!d0 || !near(d0.value(), want0, 2.5e-7f, 1e-7f, "dense_matvec")) return 130;
+    auto dg = b.dense_matvec_group(xin, dv, 3, ProfilePhase::decode);
+    if (!dg || dg.value().size() != 2 || !identical(dg.value()[0], d0.value()) ||
+        !near(dg.value()[1], want1, 2.5e-7f, 1e-7f, "dense_matvec_group"))
+        return 131;
+    const DenseWeightView anon{0, W0, LL, LH};  // tensor id 0: a transient copy
+    auto d0b = b.dense_matvec(xin, anon, 3, ProfilePhase::decode);
+    if (!d0b || !identical(d0b.value(), d0.value())) return 132;
+    if (b.dense_matvec(std::span<const float>(xin.data(), LH - 1), dv[0], 3, ProfilePhase::decode)
+            .error() != ErrorCode::invalid_extent)
+        return 133;
+    std::printf("dense_matvec (+group, transient): ok\n");
+
+    // mxfp4_matvec and its group.
+    const ResidentExpert le = make_resident_expert(801);
+    const auto xl = rand_f32(LL, 1.0f);
+    std::vector<float> wantg(LI);
+    k3xo_mxfp4_matvec(xl.data(), LL, reinterpret_cast<const std::uint8_t*>(le.gp.data()),
+                      le.gp.size(), reinterpret_cast<const std::uint8_t*>(le.gs.data()),
+                      le.gs.size(), LI, LL, G, wantg.data());
+    const k3x_amd::Mxfp4WeightView mv[2] = {le.view().gate, le.view().up};
+    auto m0 = b.mxfp4_matvec(xl, mv[0], 3, ProfilePhase::decode);
+    if (!m0 || !near(m0.value(), wantg, 2.5e-7f, 1e-7f, "mxfp4_matvec")) return 134;
+    auto mg = b.mxfp4_matvec_group(xl, mv, 3, ProfilePhase::decode);
+    if (!mg || mg.value().size() != 2 || !identical(mg.value()[0], m0.value())) return 135;
+    auto bad_scales = le.gs;
+    bad_scales[5] = std::byte{0xff};
+    const k3x_amd::Mxfp4WeightView badv{899, le.gp, bad_scales, LI, LL, G};
+    if (b.mxfp4_matvec(xl, badv, 3, ProfilePhase::decode).error() != ErrorCode::invalid_mxfp4)
+        return 136;
+    std::vector<std::byte> s16(LI * LL / 16, std::byte{127});
+    const k3x_amd::Mxfp4WeightView g16{898, le.gp, s16, LI, LL, 16};
+    if (b.mxfp4_matvec(xl, g16, 3, ProfilePhase::decode).error() != ErrorCode::backend_unavailable)
+        return 137;
+    std::printf("mxfp4_matvec (+group, rejections): ok\n");
+
+    // dense_situ_mlp.
+    const auto Sg = rand_f32(LS * LH, 0.05f), Su = rand_f32(LS * LH, 0.05f),
+               Sd = rand_f32(LH * LS, 0.05f);
+    const DenseMlpView mlp{{711, Sg, LS, LH}, {712, Su, LS, LH}, {713, Sd, LH, LS}};
+    std::vector<float> want_mlp(LH);
+    k3xo_dense_situ_mlp(xin.data(), LH, LS, LH, Sg.data(), Su.data(), Sd.data(), kBeta, 1,
+                        kLinear, nullptr, want_mlp.data());
+    auto sm = b.dense_situ_mlp(xin, mlp, kBeta, kLinear, 3, ProfilePhase::decode);
+    if (!sm || !near(sm.value(), want_mlp, 0.0f, 1e-5f, "dense_situ_mlp")) return 138;
+    std::printf("dense_situ_mlp: ok\n");
+
+    // The resident latent layer on three experts.
+    const ResidentExpert ex[3] = {make_resident_expert(821), make_resident_expert(824),
+                                make_resident_expert(827)};
+    const Mxfp4MlpView ev[3] = {ex[0].view(), ex[1].view(), ex[2].view()};
+    const auto Rd = rand_f32(LL * LH, 0.05f), Ru = rand_f32(LH * LL, 0.05f);
+    std::vector<float> Rn(LL);
+    for (auto& v : Rn) v = 0.5f + (float)(next_u32() % 1000) / 1000.0f;
+    const float contrib[3] = {0.5f, 0.3f, 0.2f};
+    const k3x_amd::ResidentMoeLayerView lv{{731, Rd, LL, LH},
+                                           {732, Rn},
+                                           {733, Ru, LH, LL},
+                                           {{734, Sg, LS, LH}, {735, Su, LS, LH}, {736, Sd, LH, LS}}};
+    std::vector<const std::uint8_t*> eptrs;
+    for (const auto& e : ex) {
+        const std::uint8_t* p[6];
+        e.ptrs(p);
+        eptrs.insert(eptrs.end(), p, p + 6);
+    }
+    std::vector<float> want_layer(LH), want_mixed(LL);
+    if (k3xo_resident_layer(xin.data(), LH, LL, LI, LS, Rd.data(), Rn.data(), Ru.data(),
+                            Sg.data(), Su.data(), Sd.data(), eptrs.data(), contrib, 3, kLatentEps,
+                            kBeta, 1, kLinear, want_mixed.data(), want_layer.data()) != 0)
+        return 139;
+    auto rl = b.resident_mxfp4_moe_layer(xin, lv, ev, contrib, kLatentEps, kBeta, kLinear, 5,
+                                         ProfilePhase::decode);
+    if (!rl || !rl.value().executed ||
+        !near(rl.value().output, want_layer, 1e-3f, 1e-3f, "resident layer"))
+        return 140;
+    auto rl2 = b.resident_mxfp4_moe_layer(xin, lv, ev, contrib, kLatentEps, kBeta, kLinear, 5,
+                                          ProfilePhase::decode);
+    if (!rl2 || !identical(rl2.value().output, rl.value().output)) return 141;
+    // Rejections as valid_resident_moe_layer: epsilon, a shared tensor id, a
+    // non-finite dense weight.
+    if (b.resident_mxfp4_moe_layer(xin, lv, ev, contrib, 0.0f, kBeta, kLinear, 5,
+                                   ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4)
+        return 142;
+    auto dup = lv;
+    dup.routed_up.tensor_id = 731;
+    if (b.resident_mxfp4_moe_layer(xin, dup, ev, contrib, kLatentEps, kBeta, kLinear, 5,
+                                   ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4)
+        return 143;
+    auto Ru_nan = Ru;
+    Ru_nan[17] = std::numeric_limits<float>::quiet_NaN();
+    auto nanv = lv;
+    nanv.routed_up = {737, Ru_nan, LH, LL};
+    if (b.resident_mxfp4_moe_layer(xin, nanv, ev, contrib, kLatentEps, kBeta, kLinear, 5,
+                                   ProfilePhase::decode)
+            .error() != ErrorCode::invalid_mxfp4)
+        return 144;
+    std::printf("resident latent layer (+rejections): ok\n");
+    return 0;
+}
+
+int latent_bypass_checks() {
+    // Two slots for three experts, and a dense budget below the weights:
+    // both succeed with executed = false.
+    const auto xin = rand_f32(LH, 1.0f);
+    const auto Rd = rand_f32(LL * LH, 0.05f), Ru = rand_f32(LH * LL, 0.05f);
+    const auto Sg = rand_f32(LS * LH, 0.05f), Su = rand_f32(LS * LH, 0.05f),
+               Sd = rand_f32(LH * LS, 0.05f);
+    const std::vector<float> Rn(LL, 1.0f);
+    const k3x_amd::ResidentMoeLayerView lv{{741, Rd, LL, LH},
+                                           {742, Rn},
+                                           {743, Ru, LH, LL},
+                                           {{744, Sg, LS, LH}, {745, Su, LS, LH}, {746, Sd, LH, LS}}};
+    const ResidentExpert ex[3] = {make_resident_expert(851), make_resident_expert(854),
+                                make_resident_expert(857)};
+    const Mxfp4MlpView ev[3] = {ex[0].view(), ex[1].view(), ex[2].view()};
+    const float contrib[3] = {0.4f, 0.4f, 0.2f};
+    k3x_amd::HipBackendOptions few;
+    few.resident_experts = 2;
+    auto small = k3x_amd::make_hip_backend(few);
+    if (!small) return 150;
+    auto r = small.value()->resident_mxfp4_moe_layer(xin, lv, ev, contrib, kLatentEps, kBeta, kLinear,
+                                                     0, ProfilePhase::decode);
+    if (!r || r.value().executed || !r.value().output.empty() ||
+        small.value()->runtime_stats().resident_layer_fallbacks != 1)
+        return 151;
+    k3x_amd::HipBackendOptions tight;
+    tight.resident_dense_bytes = 64 << 10;
+    auto starved = k3x_amd::make_hip_backend(tight);
+    if (!starved) return 152;
+    r = starved.value()->resident_mxfp4_moe_layer(xin, lv, ev, contrib, kLatentEps, kBeta, kLinear, 0,
+                                                  ProfilePhase::decode);
+    if (!r || r.value().executed) return 153;
+    // The matvec methods run over budget from a transient copy.
+    auto d = starved.value()->dense_matvec(xin, {747, Rd, LL, LH}, 0, ProfilePhase::decode);
+    std::vector<float> want(LL);
+    k3xo_dense_matvec(xin.data(), Rd.data(), LL, LH, want.data());
+    if (!d || !near(d.value(), want, 2.5e-7f, 1e-7f, "transient dense_matvec")) return 154;
+    std::printf("latent layer bypass (slots, dense budget) and transient matvec: ok\n");
+    return 0;
+}
+
 // ---- official K3 MoE FFN -----------------------------------------------------
 // A small official layer (hidden 256, latent 128, experts of 128, shared FFN
 // of 128, 8 router rows, Top-4) through prepare_official_moe_route and both
@@ -523,6 +746,8 @@ int main() {
         return 85;
 
     if (int rc = official_checks(*backend)) return rc;
+    if (int rc = latent_checks(*backend)) return rc;
+    if (int rc = latent_bypass_checks()) return rc;
     // More slots than routed experts (the normal configuration): the official
     // FFN admits only the called experts and leaves the other slots empty,
     // which must not make the call fail.

@@ -202,3 +202,45 @@ def test_threaded_layer_bitexact(oracle, reflib, threads):
         assert st == OK
         assert np.array_equal(ids[t], ids_ref)
         assert np.array_equal(bits(out[t]), bits(out_ref))
+
+
+def rand_latent_weights(rng, H, L, S):
+    """fp32 dense weights of a resident latent layer (routed_norm near 1)."""
+    g = lambda *shape: (rng.standard_normal(shape) * 0.05).astype(np.float32)
+    return dict(routed_down=g(L, H), routed_norm=rng.uniform(0.5, 1.5, L).astype(np.float32),
+                routed_up=g(H, L), shared_gate=g(S, H), shared_up=g(S, H), shared_down=g(H, S))
+
+
+@pytest.mark.parametrize("linear", [None, 25.0])
+def test_dense_situ_mlp_bitexact(oracle, reflib, linear):
+    """k3xo_dense_situ_mlp == CpuBackend::dense_situ_mlp."""
+    rng = np.random.default_rng(31)
+    H, I, O = 384, 256, 320
+    x = rng.standard_normal(H).astype(np.float32)
+    gate, up = (rng.standard_normal((I, H)) * 0.1).astype(np.float32), \
+        (rng.standard_normal((I, H)) * 0.1).astype(np.float32)
+    down = (rng.standard_normal((O, I)) * 0.1).astype(np.float32)
+    st, want = reflib.dense_situ_mlp(x, gate, up, down, 4.0, linear)
+    assert st == OK
+    _, got = oracle.dense_situ_mlp(x, gate, up, down, 4.0, linear)
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(oracle.dense_matvec(x, gate)), bits(reflib.dense_matvec(x, gate)[1]))
+
+
+@pytest.mark.parametrize("linear", [None, 25.0])
+def test_resident_layer_bitexact(oracle, reflib, linear):
+    """k3xo_resident_layer == CpuBackend::resident_mxfp4_moe_layer (executed
+    path) on one token: dense fp32 latent, MXFP4 experts, ordered mix,
+    RMSNorm, routed_up and the fp32 shared MLP."""
+    rng = np.random.default_rng(32)
+    H, L, I, S, K = 512, 256, 256, 384, 3
+    w = rand_latent_weights(rng, H, L, S)
+    experts = [rand_expert(rng, L, I) for _ in range(K)]
+    c = np.array([0.5, 0.3, 0.2], np.float32)
+    x = rng.standard_normal(H).astype(np.float32)
+    st, executed, want = reflib.resident_layer(x, w, experts, c, 1e-6, 4.0, linear)
+    assert st == OK and executed
+    st, mixed, got = oracle.resident_layer(x, w, experts, c, 1e-6, 4.0, linear)
+    assert st == OK
+    assert np.array_equal(bits(got), bits(want))
+    assert np.abs(mixed).max() > 0
