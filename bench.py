@@ -79,6 +79,13 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
                          "(counter calibration), then decode layer calls")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="short workload for a rocprofv3 --pmc pass over the T=2048 prefill "
+                         "chunk: the calibration copy, then --steps prefill layer calls")
+    ap.add_argument("--counters-from", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc passes over --pmc-prefill (per-kernel "
+                         "medians, HBM bytes from FETCH_SIZE / WRITE_SIZE against the "
+                         "calibration copy) into " + "profiles/prefill_c5_counters.json")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the FETCH_SIZE and WRITE_SIZE pass outputs into " + TRAFFIC_JSON_REL)
     return ap.parse_args()
@@ -88,6 +95,9 @@ def main() -> int:
     args = parse()
     if args.traffic_from:
         print(json.dumps(traffic_from(*args.traffic_from)))
+        return 0
+    if args.counters_from:
+        print(json.dumps(counters_from(args.counters_from)))
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the layer and its resident "
@@ -120,6 +130,28 @@ def main() -> int:
     params = k3x_amd.make_params(T, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
                                  k3x_amd.RENORM_FLOAT)
     combos = np.lcm(args.layers, args.inputs)
+    if args.pmc_prefill:
+        src = torch.empty(CALIB_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # the calibration copy: reads and writes CALIB_BYTES
+        torch.cuda.synchronize()
+        Tp = 2048
+        xp = torch.empty((Tp, H), dtype=torch.int16, device=dev)
+        k3x_amd.synth_normal_bf16(ctx, X_SEED + 1000, k3x_amd.stream_id(k3x_amd.STREAM_INPUT),
+                                  1.0, xp)
+        outp = torch.empty((Tp, H), dtype=torch.int16, device=dev)
+        pp = k3x_amd.make_params(Tp, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
+                                 k3x_amd.RENORM_FLOAT)
+        ctx.set_profiling(True)  # one stream: every kernel in stream order, no overlap
+        for i in range(max(args.steps, 1)):
+            k3x_amd.check(k3x_amd.moe_forward(ctx, banks[0], pp, xp, outp), "prefill")
+            k3x_amd.check(ctx.synchronize(), "pmc prefill")
+        for b in banks:
+            b.close()
+        ctx.close()
+        log("pmc prefill pass done")
+        return 0
     if args.pmc_pass:
         src = torch.empty(CALIB_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -573,6 +605,61 @@ def traffic_from(fetch_dir: str, write_dir: str) -> dict:
                            "fetch_scale": round(kf, 4), "write_scale": round(kw, 4)},
            "kernels": kernels}
     with open(os.path.join(ROOT, TRAFFIC_JSON_REL), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    return out
+
+
+COUNTERS_JSON_REL = os.path.join("profiles", "prefill_c5_counters.json")
+
+
+def counters_from(dirs: list[str]) -> dict:
+    """Per-kernel medians of every counter in rocprofv3 --pmc passes over
+    `bench.py --pmc-prefill` (one directory per pass), with HBM bytes per
+    dispatch from FETCH_SIZE / WRITE_SIZE scaled by the calibration copy, and
+    for the MFMA kernels the MFMA-busy share of the busy cycles.  Writes
+    COUNTERS_JSON_REL."""
+    import csv
+    import glob
+    import re
+    import statistics
+
+    per: dict = {}
+    calib: dict = {}
+    for d in dirs:
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        for fn in files:
+            with open(fn) as f:
+                for r in csv.DictReader(f):
+                    name, c, v = r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])
+                    if "copyBuffer" in name:
+                        calib[c] = max(calib.get(c, 0.0), v)
+                        continue
+                    m = re.search(r"(\w+)(<[^()]*>)?\(", name.replace("(anonymous namespace)::", ""))
+                    key = (m.group(1) + (m.group(2) or "")) if m else name
+                    per.setdefault(key, {}).setdefault(c, []).append(v)
+    kf = CALIB_BYTES / (calib["FETCH_SIZE"] * 1024) if "FETCH_SIZE" in calib else None
+    kw = CALIB_BYTES / (calib["WRITE_SIZE"] * 1024) if "WRITE_SIZE" in calib else None
+    kernels = {}
+    for k, cs in sorted(per.items()):
+        row = {"dispatches": max(len(v) for v in cs.values())}
+        for c, vals in sorted(cs.items()):
+            row[c] = round(statistics.median(vals), 1)
+        if kf and kw and "FETCH_SIZE" in cs and "WRITE_SIZE" in cs:
+            row["hbm_bytes_per_dispatch"] = round(row["FETCH_SIZE"] * 1024 * kf +
+                                                  row["WRITE_SIZE"] * 1024 * kw)
+        if cs.get("SQ_BUSY_CYCLES") and cs.get("SQ_VALU_MFMA_BUSY_CYCLES"):
+            row["mfma_busy_over_sq_busy"] = round(row["SQ_VALU_MFMA_BUSY_CYCLES"] /
+                                                  max(row["SQ_BUSY_CYCLES"], 1.0), 4)
+        kernels[k] = row
+    out = {"workload": "bench.py --pmc-prefill (c5 prefill chunk, T=2048, one stream)",
+           "calibration": {"copy_bytes": CALIB_BYTES, **calib,
+                           "fetch_scale": round(kf, 4) if kf else None,
+                           "write_scale": round(kw, 4) if kw else None},
+           "kernels": kernels}
+    with open(os.path.join(ROOT, COUNTERS_JSON_REL), "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
     return out

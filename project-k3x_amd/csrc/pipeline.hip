@@ -977,8 +977,7 @@ struct GemmArgs {
     uint32_t blocks_per_expert; // workgroups per expert
     const uint16_t* a;          // activation rows (bf16)
     uint32_t a_stride;          // elements per activation row
-    uint32_t kta;               // activation K tiles (0: kt); 2 kt for a split [hi | lo]
-                                // row, the weights repeated along K
+    uint32_t a_lo;              // split rows [hi | lo]: element offset of the lo half (0: none)
     uint32_t gather;            // A row = pair_token[off+m] (1) or off+m (0)
     const uint32_t* n_active;   // grouping (nullptr = single block of `tokens` rows)
     const uint32_t* active;
@@ -1000,7 +999,10 @@ struct GemmArgs {
 
 constexpr int kGemmDepth = 4;  // K steps in flight per wave of a one-row-tile GEMM
 
-template <bool FP4, bool GATEUP, int MT, int NT>
+// SPLIT: activation rows [hi | lo] (a_lo elements apart), an fp32 value in
+// two bf16 halves; each weight fragment meets both (two MFMAs, the weights
+// read once).
+template <bool FP4, bool GATEUP, int MT, int NT, bool SPLIT>
 __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
     if (*(volatile const uint32_t*)a.status) return;
     const uint32_t eb = blockIdx.x / a.blocks_per_expert;
@@ -1019,7 +1021,7 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
     const uint32_t rb0 = (jb * 4 + wave) * NT;
     const uint4* codes = reinterpret_cast<const uint4*>(a.codes + e * a.codes_per_expert);
     const uint32_t* scales = FP4 ? a.scales + e * a.scales_per_expert : nullptr;
-    const uint32_t kta = a.kta ? a.kta : a.kt;
+    constexpr int H2 = SPLIT ? 2 : 1;  // activation halves
 
     for (uint32_t m0 = 0; m0 < cnt; m0 += 16 * MT) {
         const uint16_t* arow[MT];
@@ -1042,17 +1044,15 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 
         // One row tile: D K steps of loads issued together (steps past the
         // last tile clamped, their activations zeroed), since a lone step's
-        // round trip would bound the wave.  Activation tile ka meets weight
-        // tile ka mod kt.
+        // round trip would bound the wave.
         constexpr int D = MT == 1 ? kGemmDepth : 1;
-        for (uint32_t k0 = 0; k0 < kta; k0 += D) {
+        for (uint32_t k0 = 0; k0 < a.kt; k0 += D) {
             uint4 bt[D][NT][S][U];
             float sc[D][NT][S];
-            bf16x8 af[D][MT][4];
+            bf16x8 af[D][MT][H2][4];
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                const uint32_t ka = min(k0 + d, kta - 1);
-                const uint32_t k = ka >= a.kt ? ka - a.kt : ka;
+                const uint32_t k = min(k0 + d, a.kt - 1);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -1067,16 +1067,20 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                         }
                     }
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    if (arow[mt] && k0 + d < kta) {
-                        const uint4* p = reinterpret_cast<const uint4*>(arow[mt] + (size_t)ka * 128);
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) af[d][mt][j] = as_bf16x8(p[j]);
-                    } else {
+                    for (int h = 0; h < H2; ++h) {
+                        if (arow[mt] && k0 + d < a.kt) {
+                            const uint4* p = reinterpret_cast<const uint4*>(
+                                arow[mt] + (h ? a.a_lo : 0u) + (size_t)k * 128);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) af[d][mt][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
+                            for (int j = 0; j < 4; ++j) af[d][mt][h][j] = as_bf16x8(p[j]);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                af[d][mt][h][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
+                        }
                     }
-                }
             }
 #pragma unroll
             for (int d = 0; d < D; ++d)
@@ -1096,7 +1100,9 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                             }
 #pragma unroll
                             for (int mt = 0; mt < MT; ++mt)
-                                acc[mt][nt][w] = mfma16x16x32(af[d][mt][j], b, acc[mt][nt][w]);
+#pragma unroll
+                                for (int h = 0; h < H2; ++h)
+                                    acc[mt][nt][w] = mfma16x16x32(af[d][mt][h][j], b, acc[mt][nt][w]);
                         }
                 }
         }
@@ -1157,14 +1163,14 @@ struct GemvArgs {
     const float* prefix;
     const float* shared;
     float* routed;
-    // Split activations: x rows [hi | lo] of kta = 2 kt tiles against the
-    // weights repeated along K (0: kt); OUT 2 also stores lo = bf16(v -
-    // hi) out_lo elements after hi (0: none).
-    uint32_t kta;
+    // Split activations: x rows [hi | lo], the lo half x_lo elements after
+    // hi (SPLIT kernels; each weight tile meets both halves); OUT 2 also
+    // stores lo = bf16(v - hi) out_lo elements after hi (0: none).
+    uint32_t x_lo;
     uint32_t out_lo;
 };
 
-template <int S, int D, int OUT, int W = kGemvWaves>
+template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false>
 __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     __shared__ f32x4 part[W][S][64];
     if (*(volatile const uint32_t*)a.status) return;
@@ -1179,30 +1185,36 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     f32x4 acc[S];
 #pragma unroll
     for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t kta = a.kta ? a.kta : a.kt;
-    for (uint32_t k0 = wave; k0 < kta; k0 += W * D) {
-        uint4 b[D][S][4], xa[D][4];
+    constexpr int H2 = SPLIT ? 2 : 1;  // activation halves
+    const uint4* xl = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + a.x_lo +
+                                                     32 * g);
+    for (uint32_t k0 = wave; k0 < a.kt; k0 += W * D) {
+        uint4 b[D][S][4], xa[D][H2][4];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const uint32_t ka = min(k0 + d * W, kta - 1);
-            const uint32_t k = ka >= a.kt ? ka - a.kt : ka;  // weight tile
+            const uint32_t k = min(k0 + d * W, a.kt - 1);
 #pragma unroll
             for (int w = 0; w < S; ++w)
 #pragma unroll
                 for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[d][j] = xr[(size_t)ka * 16 + j];
+            for (int j = 0; j < 4; ++j) {
+                xa[d][0][j] = xr[(size_t)k * 16 + j];
+                if constexpr (SPLIT) xa[d][H2 - 1][j] = xl[(size_t)k * 16 + j];
+            }
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const bool live = live_row && k0 + d * W < kta;
+            const bool live = live_row && k0 + d * W < a.kt;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint4 xv = live ? xa[d][j] : make_uint4(0, 0, 0, 0);
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int w = 0; w < S; ++w)
-                    acc[w] = mfma16x16x32(as_bf16x8(xv), as_bf16x8(b[d][w][j]), acc[w]);
-            }
+                for (int h = 0; h < H2; ++h) {
+                    const uint4 xv = live ? xa[d][h][j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                    for (int w = 0; w < S; ++w)
+                        acc[w] = mfma16x16x32(as_bf16x8(xv), as_bf16x8(b[d][w][j]), acc[w]);
+                }
         }
     }
 #pragma unroll
@@ -1439,8 +1451,13 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
 template <bool FP4, bool GATEUP, int MT, int NT>
 void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32_t rows) {
     g.blocks_per_expert = rows / 16 / (4 * NT);
-    hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT>), dim3(experts_in_grid * g.blocks_per_expert),
-                       dim3(256), 0, ctx->stream, g);
+    const dim3 grid(experts_in_grid * g.blocks_per_expert);
+    if (g.a_lo)
+        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, true>), grid, dim3(256), 0,
+                           ctx->stream, g);
+    else
+        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, false>), grid, dim3(256), 0,
+                           ctx->stream, g);
 }
 
 // Many rows per expert: the wide grouped GEMM (128-row chunks, activations
@@ -1657,7 +1674,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.ks = bank->gate.ks;
     g.a = xn;
     g.a_stride = split_in ? 2 * d.hidden : d.hidden;
-    g.kta = split_in ? 2 * g.kt : 0;
+    g.a_lo = split_in ? d.hidden : 0;
     g.gather = 1;
     g.n_active = s.n_active;
     g.active = s.active_asc;
@@ -1679,7 +1696,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sg.scales = nullptr;
         sg.codes_per_expert = 0;
         sg.kt = bank->sgate.kt;
-        sg.kta = split_in ? 2 * sg.kt : 0;
+        sg.a_lo = split_in ? d.hidden : 0;
         sg.gather = 0;
         sg.n_active = nullptr;
         sg.active = nullptr;
@@ -1702,7 +1719,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.ks = bank->down.ks;
     dn.a = s.act;
     dn.a_stride = g.act_stride;
-    dn.kta = split ? 2 * dn.kt : 0;
+    dn.a_lo = split ? d.inter : 0;
     dn.gather = 0;
     dn.y = s.y;
     dn.y_stride = d.hidden;
@@ -1717,7 +1734,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         sd.scales = nullptr;
         sd.codes_per_expert = 0;
         sd.kt = bank->sdown.kt;
-        sd.kta = 0;
+        sd.a_lo = 0;
         sd.a = s.sact;
         sd.a_stride = d.shared_inter;
         sd.n_active = nullptr;
@@ -1972,19 +1989,26 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
                uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16, bool split) {
     if (!T || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
-    // Split rows [hi | lo]: 2 K activation columns against the weights twice.
-    const uint32_t a_stride = split ? 2 * K : K, kta = split ? 2 * (K / 128) : 0;
+    // Split rows [hi | lo] of 2 K: each weight tile meets both halves.
+    const uint32_t a_stride = split ? 2 * K : K;
     if (T <= kGemvMaxTokens) {
         GemvArgs g{tiles, K / 128, a, a_stride, T, y_bf16 ? (void*)y_bf16 : (void*)y, N, {},
                    ctx->status};
-        g.kta = kta;
+        g.x_lo = split ? K : 0;
         const dim3 grid(N / 16);
+        if (y_bf16 && split) return K3X_ERR_INVALID_EXTENT;
         if (y_bf16)
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 1>), grid, dim3(64 * kGemvWaves), 0, stream,
                                g);
+        else if (stream == ctx->stream && split)
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 2, 0, kGemvWaves, true>), grid,
+                               dim3(64 * kGemvWaves), 0, stream, g);
         else if (stream == ctx->stream)
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0>), grid, dim3(64 * kGemvWaves), 0, stream,
                                g);
+        else if (split)
+            hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0, kGemvWaves / 2, true>), grid,
+                               dim3(32 * kGemvWaves), 0, stream, g);
         else
             hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 0, kGemvWaves / 2>), grid,
                                dim3(32 * kGemvWaves), 0, stream, g);
@@ -1995,7 +2019,7 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
         WideGemmArgs g{};
         g.codes = reinterpret_cast<const uint8_t*>(tiles);
         g.kt = K / 128;
-        g.kta = kta;
+        g.kta = split ? 2 * g.kt : 0;  // the weights repeated along K
         g.nrb = N / 16;
         g.a = a;
         g.a_stride = a_stride;
@@ -2010,7 +2034,7 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
     GemmArgs g{};
     g.codes = reinterpret_cast<const uint8_t*>(tiles);
     g.kt = K / 128;
-    g.kta = kta;
+    g.a_lo = split ? K : 0;
     g.a = a;
     g.a_stride = a_stride;
     g.tokens = T;
