@@ -22,6 +22,7 @@
 
 #include "k3x_device.hpp"
 #include "k3x_internal.hpp"
+#include "k3x_reader.hpp"
 
 using namespace k3x_dev;
 
@@ -244,32 +245,15 @@ extern "C" int k3x_hip_crc32c(k3x_hip_ctx* ctx, const void* data, size_t bytes, 
 }
 
 // ---------------------------------------------------------------------------
-// K3X reader (host): the structural checks of Reader::open and the expert
-// load of load_storage_expert, feeding the bank through one pinned staging
-// buffer and one device staging buffer per storage object.
+// K3X storage objects: the reader's checked directory (k3x_reader.cpp) and
+// the expert load of load_storage_expert, feeding the bank through one pinned
+// staging buffer and one device staging buffer per storage object.
 // ---------------------------------------------------------------------------
-#include <fcntl.h>
-#include <sys/stat.h>
-#include <unistd.h>
-
 #include <string>
-#include <unordered_set>
 
 struct k3x_hip_storage {
-    int fd = -1;
-    uint64_t file_length = 0;
-    uint64_t optional_features = 0;
-    struct Tensor {
-        uint64_t id;
-        uint16_t dtype, quant;
-        uint8_t rank;
-        int32_t layer, expert;
-        uint64_t dims[4];
-        uint64_t data_offset, data_length, aux_offset, aux_length;
-        uint32_t data_crc, aux_crc;
-    };
-    std::vector<Tensor> tensors;
-    uint8_t* pinned = nullptr;  // hipHostMalloc
+    k3x_reader::Directory dir;   // the checked directory (k3x_reader.cpp)
+    uint8_t* pinned = nullptr;   // hipHostMalloc
     size_t pinned_bytes = 0;
     uint8_t* staging = nullptr;  // device
     size_t staging_bytes = 0;
@@ -278,136 +262,8 @@ struct k3x_hip_storage {
 
 namespace {
 
-template <typename T>
-T le(const uint8_t* p, size_t at) {
-    T v;
-    std::memcpy(&v, p + at, sizeof(T));
-    return v;
-}
-
-uint32_t crc32c_host(const uint8_t* p, size_t n) {
-    const CrcTables& h = host_tables();
-    uint32_t r = 0xffffffffu;
-    for (size_t i = 0; i < n; ++i) r = h.slice[0][(r ^ p[i]) & 255] ^ (r >> 8);
-    return ~r;
-}
-
-uint64_t fnv1a64(const std::string& s) {  // runtime/src/reader.cpp:405-412
-    uint64_t h = 0xcbf29ce484222325ull;
-    for (unsigned char c : s) {
-        h ^= c;
-        h *= 0x100000001b3ull;
-    }
-    return h;
-}
-
-bool read_at(int fd, uint64_t off, size_t n, uint8_t* dst) {
-    while (n) {
-        const ssize_t r = pread(fd, dst, n, (off_t)off);
-        if (r <= 0) return false;
-        dst += r;
-        off += (uint64_t)r;
-        n -= (size_t)r;
-    }
-    return true;
-}
-
-bool range_ok(uint64_t off, uint64_t len, uint64_t file) {
-    return off <= file && len <= file - off;
-}
-
-bool zero(const uint8_t* p, size_t n) {
-    for (size_t i = 0; i < n; ++i)
-        if (p[i]) return false;
-    return true;
-}
-
-// Directory header: tag, record size, count (reader.cpp:54-65).
-bool directory_count(const std::vector<uint8_t>& d, const char* tag, uint32_t rec, uint64_t* n) {
-    if (d.size() < 16 || std::memcmp(d.data(), tag, 4) || le<uint32_t>(d.data(), 4) != rec)
-        return false;
-    const uint64_t c = le<uint64_t>(d.data(), 8);
-    if (c > (d.size() - 16) / rec || d.size() != 16 + c * rec) return false;
-    *n = c;
-    return true;
-}
-
-int open_checked(k3x_hip_storage* s, const char* path) {
-    s->fd = ::open(path, O_RDONLY | O_CLOEXEC);
-    if (s->fd < 0) return K3X_ERR_IO;
-    struct stat st {};
-    if (fstat(s->fd, &st)) return K3X_ERR_IO;
-    const uint64_t file = (uint64_t)st.st_size;
-    if (file < 4096) return K3X_ERR_TRUNCATED_FILE;
-    std::vector<uint8_t> sb(4096);
-    if (!read_at(s->fd, 0, 4096, sb.data())) return K3X_ERR_TRUNCATED_FILE;
-    const uint8_t* b = sb.data();
-    if (std::memcmp(b, "K3XCHKPT", 8)) return K3X_ERR_BAD_MAGIC;
-    if (le<uint16_t>(b, 8) != 1 || le<uint16_t>(b, 10) != 0 || le<uint32_t>(b, 12) != 4096 ||
-        le<uint32_t>(b, 16) != 4096)
-        return K3X_ERR_UNSUPPORTED_VERSION;
-    if (crc32c_host(b, 4092) != le<uint32_t>(b, 4092)) return K3X_ERR_SUPERBLOCK_CRC_MISMATCH;
-    if (le<uint64_t>(b, 24)) return K3X_ERR_UNSUPPORTED_REQUIRED_FEATURE;  // none supported
-    if (!zero(b + 232, 4092 - 232)) return K3X_ERR_INVALID_DIRECTORY;
-    s->optional_features = le<uint64_t>(b, 32);
-    uint64_t v[10];
-    for (int i = 0; i < 10; ++i) v[i] = le<uint64_t>(b, 88 + 8 * i);
-    if (le<uint32_t>(b, 20) != 1 || v[9] != file) return K3X_ERR_TRUNCATED_FILE;
-    s->file_length = file;
-    std::vector<uint8_t> dir[4];
-    for (int i = 0; i < 4; ++i) {
-        const uint64_t off = v[2 * i], len = v[2 * i + 1];
-        if (off % 4096 || !range_ok(off, len, file)) return K3X_ERR_INVALID_EXTENT;
-        dir[i].resize(len);
-        if (!read_at(s->fd, off, len, dir[i].data())) return K3X_ERR_INVALID_DIRECTORY;
-    }
-    uint64_t nt = 0, nl = 0, ne = 0;
-    const std::vector<uint8_t>& cfg = dir[3];
-    if (cfg.size() != 256 || !directory_count(dir[0], "TENS", 128, &nt) ||
-        !directory_count(dir[1], "LAYR", 64, &nl) || !directory_count(dir[2], "EXPT", 64, &ne) ||
-        le<uint32_t>(cfg.data(), 8) != nl || !zero(cfg.data() + 112, 144) ||
-        (le<uint32_t>(cfg.data(), 108) & ~3u))
-        return K3X_ERR_INVALID_DIRECTORY;
-    std::vector<std::pair<uint64_t, uint64_t>> ranges{{0, 4096}};
-    for (int i = 0; i < 4; ++i) ranges.push_back({v[2 * i], v[2 * i] + v[2 * i + 1]});
-    std::unordered_set<uint64_t> ids;
-    for (uint64_t i = 0; i < nt; ++i) {
-        const uint8_t* r = dir[0].data() + 16 + i * 128;
-        k3x_hip_storage::Tensor t{};
-        t.id = le<uint64_t>(r, 0);
-        t.dtype = le<uint16_t>(r, 12);
-        t.quant = le<uint16_t>(r, 14);
-        t.rank = r[16];
-        t.layer = (int32_t)le<uint32_t>(r, 20);
-        t.expert = (int32_t)le<uint32_t>(r, 24);
-        for (int d = 0; d < 4; ++d) t.dims[d] = le<uint64_t>(r, 32 + 8 * d);
-        t.data_offset = le<uint64_t>(r, 64);
-        t.data_length = le<uint64_t>(r, 72);
-        t.aux_offset = le<uint64_t>(r, 88);
-        t.aux_length = le<uint64_t>(r, 96);
-        t.data_crc = le<uint32_t>(r, 104);
-        t.aux_crc = le<uint32_t>(r, 108);
-        if (t.rank > 4 || (t.dtype < 1 || t.dtype > 3) || t.quant > 1 || le<uint32_t>(r, 8) ||
-            r[17] || le<uint16_t>(r, 18) || le<uint32_t>(r, 28) || !zero(r + 112, 16) ||
-            !ids.insert(t.id).second)
-            return K3X_ERR_INVALID_DIRECTORY;
-        for (int d = t.rank; d < 4; ++d)
-            if (t.dims[d]) return K3X_ERR_INVALID_DIRECTORY;
-        if (t.data_offset % 4096 || !range_ok(t.data_offset, t.data_length, file) ||
-            (t.aux_length && (t.aux_offset % 4096 || !range_ok(t.aux_offset, t.aux_length, file))))
-            return K3X_ERR_INVALID_EXTENT;
-        if (t.data_length) ranges.push_back({t.data_offset, t.data_offset + t.data_length});
-        if (t.aux_length) ranges.push_back({t.aux_offset, t.aux_offset + t.aux_length});
-        s->tensors.push_back(t);
-    }
-    std::sort(ranges.begin(), ranges.end());
-    for (size_t i = 1; i < ranges.size(); ++i)
-        if (ranges[i].first < ranges[i - 1].second) return K3X_ERR_INVALID_EXTENT;
-    return K3X_OK;
-}
-
 void close_storage(k3x_hip_storage* s) {
-    if (s->fd >= 0) ::close(s->fd);
+    k3x_reader::close(&s->dir);
     if (s->pinned) (void)hipHostFree(s->pinned);
     if (s->staging) {
         (void)hipSetDevice(s->staging_device);
@@ -424,7 +280,7 @@ int k3x_hip_storage_open(const char* path, k3x_hip_storage** out) {
     *out = nullptr;
     auto* s = new (std::nothrow) k3x_hip_storage();
     if (!s) return K3X_ERR_BACKEND_UNAVAILABLE;
-    const int st = open_checked(s, path);
+    const int st = k3x_reader::open_checked(&s->dir, path);
     if (st) {
         close_storage(s);
         delete s;
@@ -444,17 +300,17 @@ int k3x_hip_storage_close(k3x_hip_storage* s) {
 int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32_t expert,
                                   uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read) {
     if (!s || !bank) return K3X_ERR_INVALID_EXTENT;
-    if (!(s->optional_features & 1u)) return K3X_ERR_INVALID_EXTENT;  // not a storage fixture
+    if (!(s->dir.optional_features & 1u)) return K3X_ERR_INVALID_EXTENT;  // not a storage fixture
     const auto& d = bank->desc;
     const std::string base = "model.layers." + std::to_string(layer_id) +
                              ".feed_forward.experts." + std::to_string(expert_id) + ".";
     const char* roles[3] = {"gate", "up", "down"};
     const uint64_t shape[3][2] = {{d.inter, d.hidden}, {d.inter, d.hidden}, {d.hidden, d.inter}};
-    const k3x_hip_storage::Tensor* rec[3];
+    const k3x_reader::TensorRecord* rec[3];
     for (int m = 0; m < 3; ++m) {
-        const uint64_t id = fnv1a64(base + roles[m]);
+        const uint64_t id = k3x_reader::fnv1a64(base + roles[m]);
         rec[m] = nullptr;
-        for (const auto& t : s->tensors)
+        for (const auto& t : s->dir.tensors)
             if (t.id == id) rec[m] = &t;
         if (!rec[m]) return K3X_ERR_TENSOR_NOT_FOUND;
         const auto& t = *rec[m];
@@ -510,7 +366,8 @@ int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32
         s->staging_device = ctx->device;
     }
     for (int i = 0; i < 6; ++i)
-        if (!read_at(s->fd, off[i], len[i], s->pinned + at[i])) return K3X_ERR_TRUNCATED_FILE;
+        if (!k3x_reader::read_at(s->dir.fd, off[i], len[i], s->pinned + at[i]))
+            return K3X_ERR_TRUNCATED_FILE;
     if (hipMemcpyAsync(s->staging, s->pinned, total, hipMemcpyHostToDevice, ctx->stream) !=
         hipSuccess)
         return K3X_ERR_BACKEND_UNAVAILABLE;

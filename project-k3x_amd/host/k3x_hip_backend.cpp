@@ -14,6 +14,7 @@
 #include <map>
 #include <tuple>
 
+#include "k3x_hip_checks.hpp"
 #include "k3x_hip_moe.h"
 
 namespace k3x_amd {
@@ -29,33 +30,14 @@ constexpr std::size_t kTokensPerCall = 4096;   // bounds the per-pair output buf
 
 ErrorCode code_of(int status) { return static_cast<ErrorCode>(status); }
 
-bool mul_fits(std::size_t a, std::size_t b) {
-    return b == 0 || a <= std::numeric_limits<std::size_t>::max() / b;
-}
-
-// backend_cpu.cpp:384-402.
-bool valid_mxfp4(std::size_t input_size, const Mxfp4WeightView& w) {
-    if (input_size != w.cols || !w.rows || !w.cols || !w.group_size || w.cols % w.group_size ||
-        w.cols % 2 || !mul_fits(w.rows, w.cols))
-        return false;
-    const std::size_t elements = w.rows * w.cols;
-    if (w.packed.size() != elements / 2 || w.scales.size() != elements / w.group_size)
-        return false;
-    for (const std::byte s : w.scales)
-        if (s == std::byte{0xff}) return false;
-    return true;
-}
-
-// backend_cpu.cpp:427-433.
-bool valid_mxfp4_mlp(std::size_t input_size, const Mxfp4MlpView& e) {
-    return valid_mxfp4(input_size, e.gate) && valid_mxfp4(input_size, e.up) &&
-           e.gate.rows == e.up.rows && valid_mxfp4(e.gate.rows, e.down);
-}
-
-bool valid_situ(float beta, std::optional<float> linear) {
-    return std::isfinite(beta) && beta > 0.0f &&
-           (!linear || (std::isfinite(*linear) && *linear > 0.0f));
-}
+using checks::mul_fits;
+using checks::valid_dense;
+using checks::valid_dense_mlp;
+using checks::valid_dense_size;
+using checks::valid_mxfp4;
+using checks::valid_mxfp4_mlp;
+using checks::valid_situ;
+using checks::all_finite;
 
 bool same_expert(const Mxfp4MlpView& a, const Mxfp4MlpView& b) {
     return a.gate.tensor_id == b.gate.tensor_id && a.up.tensor_id == b.up.tensor_id &&
@@ -443,15 +425,18 @@ struct HipMoeBackend::Impl {
     }
 
     // Per-expert outputs of T tokens through every expert of `experts`
-    // (distinct), in chunks of at most 64 experts and kTokensPerCall tokens:
+    // (distinct), in chunks of at most 64 experts (and at most the layer's
+    // bank slots, so that more experts than slots run chunk after chunk,
+    // each admitted over the last) and kTokensPerCall tokens:
     // out[e][t * H + h].
     ErrorCode grid(std::uint32_t layer, std::span<const float> inputs, std::size_t T,
                    std::span<const Mxfp4MlpView> experts, float beta,
                    std::optional<float> linear, Outputs& out) {
         const std::size_t H = experts.front().gate.cols;
         out.assign(experts.size(), std::vector<float>(T * H));
-        for (std::size_t e0 = 0; e0 < experts.size(); e0 += kMaxSlotsPerToken) {
-            const std::size_t K = std::min(kMaxSlotsPerToken, experts.size() - e0);
+        const std::size_t chunk = std::min<std::size_t>(kMaxSlotsPerToken, opt.resident_experts);
+        for (std::size_t e0 = 0; e0 < experts.size(); e0 += chunk) {
+            const std::size_t K = std::min(chunk, experts.size() - e0);
             const auto chunk = experts.subspan(e0, K);
             for (std::size_t t0 = 0; t0 < T; t0 += kTokensPerCall) {
                 const std::size_t Tc = std::min(kTokensPerCall, T - t0);
@@ -599,13 +584,17 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe(std::span<const float> 
     for (const auto& e : experts)
         if (!valid_mxfp4_mlp(input.size(), e) || e.down.rows != out_rows)
             return R::failure(ErrorCode::invalid_mxfp4);
-    bool distinct = experts.size() <= kMaxSlotsPerToken;
+    // One layer call takes each expert once, at most 64 slots and at most the
+    // bank's slots; otherwise the per-expert outputs (run chunk by chunk) are
+    // mixed here.
+    bool distinct = experts.size() <= std::min<std::size_t>(kMaxSlotsPerToken,
+                                                            impl_->opt.resident_experts);
     for (std::size_t i = 0; i < experts.size() && distinct; ++i)
         for (std::size_t j = 0; j < i && distinct; ++j) distinct = !same_expert(experts[i], experts[j]);
     if (!distinct) {
-        // An expert twice (or more slots than one layer call takes): the
-        // per-expert outputs, mixed here in slot order as backend_cpu.cpp
-        // :294-301 does.
+        // An expert twice, or more experts than one layer call or the bank
+        // takes: the per-expert outputs, mixed here in slot order as
+        // backend_cpu.cpp:294-301 does.
         auto outs = mxfp4_situ_mlp_group(input, experts, situ_beta, situ_linear, layer, phase);
         if (!outs) return R::failure(outs.error(), outs.message());
         std::vector<float> mixed(out_rows, 0.0f);
@@ -1042,31 +1031,6 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
 
 namespace {
 
-// backend_cpu.cpp:365-374 (valid_dense).
-bool valid_dense(std::size_t input_size, const DenseWeightView& w) {
-    if (input_size != w.cols || w.rows > w.values.size() ||
-        (w.cols != 0 && w.rows > w.values.size() / w.cols))
-        return false;
-    return w.values.size() == w.rows * w.cols;
-}
-
-// backend_cpu.cpp:410-420 (valid_dense_size: non-empty as well).
-bool valid_dense_size(std::size_t input_size, const DenseWeightView& w) {
-    return w.rows && w.cols && valid_dense(input_size, w);
-}
-
-// backend_cpu.cpp:403-408 (valid_dense_mlp).
-bool valid_dense_mlp(std::size_t input_size, const DenseMlpView& m) {
-    return valid_dense(input_size, m.gate) && valid_dense(input_size, m.up) && m.gate.rows != 0 &&
-           m.gate.rows == m.up.rows && valid_dense_size(m.gate.rows, m.down);
-}
-
-bool all_finite(std::span<const float> v) {
-    for (float x : v)
-        if (!std::isfinite(x)) return false;
-    return true;
-}
-
 std::span<const float> as_span(const float* p, std::size_t n) { return {p, n}; }
 
 }  // namespace
@@ -1219,35 +1183,11 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     // valid_resident_moe_layer (backend_cpu.cpp:441-497); the finiteness of
     // the dense weights is checked when they are uploaded (a resident copy
     // was checked then).
-    if (input.empty() || experts.empty() || experts.size() != contributions.size() ||
-        !std::isfinite(epsilon) || epsilon <= 0.0f || !valid_situ(situ_beta, situ_linear) ||
-        !all_finite(input) || !all_finite(contributions) ||
-        !valid_dense(input.size(), weights.routed_down) ||
-        !valid_dense_mlp(input.size(), weights.shared))
+    if (!checks::valid_resident_layer(input, weights, experts, contributions, epsilon, situ_beta,
+                                      situ_linear))
         return bad();
     const std::size_t H = input.size(), L = weights.routed_down.rows,
-                      W = experts.front().down.rows;
-    if (L == 0 || W == 0 || weights.routed_norm.values.size() != W ||
-        !valid_dense_size(W, weights.routed_up) || weights.routed_up.rows != H ||
-        weights.shared.down.rows != H)
-        return bad();
-    std::vector<std::uint64_t> ids;
-    auto insert_id = [&](std::uint64_t id) {
-        if (id == 0 || std::find(ids.begin(), ids.end(), id) != ids.end()) return false;
-        ids.push_back(id);
-        return true;
-    };
-    if (!insert_id(weights.routed_down.tensor_id) || !insert_id(weights.routed_norm.tensor_id) ||
-        !insert_id(weights.routed_up.tensor_id) || !insert_id(weights.shared.gate.tensor_id) ||
-        !insert_id(weights.shared.up.tensor_id) || !insert_id(weights.shared.down.tensor_id))
-        return bad();
-    const std::size_t I = experts.front().gate.rows;
-    for (const auto& e : experts)
-        if (!valid_mxfp4_mlp(L, e) || e.gate.rows != I || e.down.rows != W ||
-            e.gate.group_size != 32 || e.up.group_size != 32 || e.down.group_size != 32 ||
-            !insert_id(e.gate.tensor_id) || !insert_id(e.up.tensor_id) ||
-            !insert_id(e.down.tensor_id))
-            return bad();
+                      W = experts.front().down.rows, I = experts.front().gate.rows;
     // Shapes the device path runs: routed width = latent (a square expert
     // bank), widths multiples of 128, one layer call of at most 64 slots.
     if (W != L || experts.size() > kMaxSlotsPerToken || H > (1u << 24) ||

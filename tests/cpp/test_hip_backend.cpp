@@ -735,6 +735,29 @@ int main() {
         !identical(again.value()[1], blocks.value()[1]))
         return 84;
 
+    // More experts than the bank's 4 slots: the group runs in chunks that fit
+    // (each admitted over the last), and the mix of six is formed from the
+    // per-expert outputs in slot order (the reference's transient path runs
+    // such calls too, backend_cuda.cu:1570-1615).
+    {
+        const Expert e5 = make_expert(416);
+        const Mxfp4MlpView six[6] = {e0.view(), e1.view(), e2.view(), e3.view(), e4.view(),
+                                     e5.view()};
+        const Expert* sixe[6] = {&e0, &e1, &e2, &e3, &e4, &e5};
+        auto g6 = backend->mxfp4_situ_mlp_group(x1, six, kBeta, kLinear, 14, ProfilePhase::decode);
+        if (!g6 || g6.value().size() != 6) return 120;
+        for (int i = 0; i < 6; ++i)
+            if (!close_to(g6.value()[i], oracle_out(*sixe[i], x1.data()), "six experts")) return 121;
+        const float c6[6] = {0.3f, 0.2f, 0.15f, 0.15f, 0.1f, 0.1f};
+        auto m6 = backend->mxfp4_situ_moe(x1, six, c6, kBeta, kLinear, 14, ProfilePhase::decode);
+        if (!m6) return 122;
+        std::vector<float> want(H, 0.0f);
+        for (int i = 0; i < 6; ++i)
+            for (std::size_t h = 0; h < H; ++h) want[h] += c6[i] * g6.value()[i][h];
+        if (!identical(m6.value(), want)) return 123;
+        std::printf("more experts than slots (group of 6, mix of 6 over 4 slots): ok\n");
+    }
+
     // Shapes the kernels do not run: backend_unavailable, not a wrong answer.
     std::vector<std::byte> p32(32 * 32 / 2), s32(32);
     std::vector<std::byte> pd(32 / 2), sd(1);

@@ -1,0 +1,90 @@
+"""Host code that parses untrusted input, built with AddressSanitizer and
+UndefinedBehaviorSanitizer and run on the CPU (tests/cpp/sanitize_driver.cpp):
+
+* the K3X reader's open-time checks (project-k3x_amd/csrc/k3x_reader.cpp) over
+  the corrupted files of tests/test_storage.py and 300 seeded mutants of a
+  good file (byte changes in the superblock, the directories and the payload,
+  and truncations); every status must equal the library's own open;
+* HipMoeBackend's argument checks (project-k3x_amd/host/k3x_hip_checks.hpp)
+  over 20,000 randomised views: extents that disagree with their spans,
+  products past SIZE_MAX, zero and odd sizes, 0xFF scales, non-finite values.
+
+Any sanitizer report fails the test.  Skipped where g++ cannot build with the
+sanitizers."""
+from __future__ import annotations
+
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from test_storage import open_status, reader_cases
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRIVER_SRC = os.path.join(ROOT, "tests", "cpp", "sanitize_driver.cpp")
+READER_SRC = os.path.join(ROOT, "project-k3x_amd", "csrc", "k3x_reader.cpp")
+FLAGS = ["-std=c++20", "-O1", "-g", "-fsanitize=address,undefined",
+         "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-Wall", "-Wextra",
+         "-Werror", f"-I{os.path.join(ROOT, 'project-k3x_amd', 'host')}",
+         f"-I{os.path.join(ROOT, 'project-k3x_amd', 'csrc')}", f"-I{os.path.join(ROOT, 'include')}"]
+ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:halt_on_error=1",
+           UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+
+
+@pytest.fixture(scope="module")
+def driver(tmp_path_factory):
+    exe = str(tmp_path_factory.mktemp("sanitize") / "sanitize_driver")
+    r = subprocess.run(["g++", *FLAGS, DRIVER_SRC, READER_SRC, "-o", exe], capture_output=True,
+                       text=True, timeout=300)
+    if r.returncode != 0 and "sanitize" in r.stderr:
+        pytest.skip("g++ without the sanitizer runtimes")
+    assert r.returncode == 0, r.stderr[-4000:]
+    return exe
+
+
+def run(exe, *args):
+    r = subprocess.run([exe, *args], capture_output=True, text=True, timeout=600, env=ENV)
+    report = [m for m in ("AddressSanitizer", "LeakSanitizer", "runtime error:")
+              if m in r.stderr]
+    assert r.returncode == 0 and not report, r.stderr[-4000:]
+    return r.stdout
+
+
+def mutants(good: str, out_dir, n: int):
+    data = open(good, "rb").read()
+    rng = np.random.default_rng(11)
+    paths = []
+    for i in range(n):
+        b = bytearray(data)
+        kind = i % 4
+        if kind == 0:  # superblock fields (the CRC then usually fails first)
+            for _ in range(1 + i % 3):
+                b[int(rng.integers(0, 4096))] = int(rng.integers(0, 256))
+        elif kind == 1:  # directory bytes behind a valid superblock CRC
+            at = int(rng.integers(4096, min(len(b), 4 * 4096)))
+            b[at:at + 8] = struct.pack("<Q", int(rng.integers(0, 2**63)))
+        elif kind == 2:  # truncation
+            b = b[:int(rng.integers(0, len(b)))]
+        else:  # payload bytes
+            b[int(rng.integers(0, len(b)))] ^= 0xFF
+        p = str(out_dir / f"mutant{i}.k3x")
+        open(p, "wb").write(bytes(b))
+        paths.append(p)
+    return paths
+
+
+def test_reader_under_sanitizers(driver, oracle, tmp_path):
+    cases = reader_cases(oracle, tmp_path)
+    paths = [p for p, _ in cases] + mutants(cases[0][0], tmp_path, 300)
+    got = [int(v) for v in run(driver, "reader", *paths).split()]
+    assert got[:len(cases)] == [want for _, want in cases]
+    lib = [open_status(p) for p in paths]
+    assert got == lib
+    assert len(set(got)) >= 5  # the mutants reach several distinct checks
+
+
+def test_backend_checks_under_sanitizers(driver):
+    out = run(driver, "checks", "1", "20000")
+    assert out.startswith("checks: 20000 views")

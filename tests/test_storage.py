@@ -78,12 +78,15 @@ def rewrite(path, at, data, fix_crc, oracle):
     open(path, "wb").write(bytes(b))
 
 
-def test_reader_open_checks(oracle, tmp_path):
-    import k3x_amd
+def reader_cases(oracle, tmp_path):
+    """K3X files and the status reader.cpp gives each: a good file, the
+    superblock field cases, a truncated file, overlapping and unaligned
+    extents, a duplicate tensor id and a missing file."""
     crc = oracle.crc32c
+    out = []
     good = str(tmp_path / "good.k3x")
     write_k3x(good, small_tensors(oracle), crc)
-    assert open_status(good) == 0
+    out.append((good, 0))
     cases = {  # (offset, bytes, recompute the superblock CRC) -> reader.cpp status
         "magic": (0, b"K3XCHKPX", True, 2),
         "version": (8, struct.pack("<H", 2), True, 3),
@@ -96,13 +99,13 @@ def test_reader_open_checks(oracle, tmp_path):
         p = str(tmp_path / f"{name}.k3x")
         write_k3x(p, small_tensors(oracle), crc)
         rewrite(p, at, data, fix, oracle)
-        assert open_status(p) == want, name
+        out.append((p, want))
     # Truncated: the declared length no longer matches.
     p = str(tmp_path / "short.k3x")
     write_k3x(p, small_tensors(oracle), crc)
     b = open(p, "rb").read()
     open(p, "wb").write(b[:-4096])
-    assert open_status(p) == 7
+    out.append((p, 7))
     # Overlapping and unaligned extents; a duplicate tensor id.
     t = small_tensors(oracle)
     layout = write_k3x(str(tmp_path / "probe.k3x"), t, crc)
@@ -110,15 +113,22 @@ def test_reader_open_checks(oracle, tmp_path):
     p = str(tmp_path / "overlap.k3x")
     write_k3x(p, t, crc)
     rewrite(p, tens + 16 + 128 + 64, struct.pack("<Q", layout["payload"][0]), False, oracle)
-    assert open_status(p) == 9
+    out.append((p, 9))
     p = str(tmp_path / "unaligned.k3x")
     write_k3x(p, t, crc)
     rewrite(p, tens + 16 + 64, struct.pack("<Q", layout["payload"][0] + 16), False, oracle)
-    assert open_status(p) == 9
+    out.append((p, 9))
     p = str(tmp_path / "dup.k3x")
     t2 = small_tensors(oracle)
     t2[1]["id"] = fnv1a64(t2[0]["name"])
     write_k3x(p, t2, crc)
-    assert open_status(p) == 8
-    assert open_status(str(tmp_path / "absent.k3x")) == 1
+    out.append((p, 8))
+    out.append((str(tmp_path / "absent.k3x"), 1))
+    return out
+
+
+def test_reader_open_checks(oracle, tmp_path):
+    import k3x_amd
+    for path, want in reader_cases(oracle, tmp_path):
+        assert open_status(path) == want, os.path.basename(path)
     del k3x_amd
