@@ -307,13 +307,23 @@ def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
     k3x_amd.check(k3x_amd.moe_forward(ctx, bank, params, x, out, {"n_active": na}), "prefill")
     k3x_amd.check(ctx.synchronize(), "prefill")
     d = int(na.item())
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.prefill_steps):
-        k3x_amd.check(k3x_amd.moe_forward(ctx, bank, params, x, out), "prefill")
-    torch.cuda.synchronize()
-    us = (time.perf_counter() - t0) / args.prefill_steps * 1e6
-    k3x_amd.check(ctx.synchronize(), "prefill")
+
+    def timed(p) -> float:
+        k3x_amd.check(k3x_amd.moe_forward(ctx, bank, p, x, out), "prefill")  # warm scratch
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.prefill_steps):
+            k3x_amd.check(k3x_amd.moe_forward(ctx, bank, p, x, out), "prefill")
+        torch.cuda.synchronize()
+        k3x_amd.check(ctx.synchronize(), "prefill")
+        return (time.perf_counter() - t0) / args.prefill_steps * 1e6
+
+    us = timed(params)
+    # The same chunk with the routed experts on the scaled FP4 MFMA.
+    scaled = k3x_amd.make_params(T, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
+                                 k3x_amd.RENORM_FLOAT, k3x_amd.FLAG_SCALED_FP4)
+    us_scaled = timed(scaled)
+    log(f"prefill T=2048, scaled FP4 MFMA: {us_scaled:.1f} us/layer")
     routed_flops = T * K * EXPERT_FLOPS
     all_flops = routed_flops + T * SHARED_FLOPS
     bytes_ = d * EXPERT_BYTES + SHARED_GU_BYTES + SHARED_DOWN_BYTES + ROUTER_BYTES + 2 * T * H * 2
@@ -328,7 +338,10 @@ def prefill(args, ctx, bank, k3x_amd, torch) -> dict:
             "mxfp4_peak_frac": round(tflops / MXFP4_PEAK_TFLOPS, 4),
             "hbm_frac": round(bytes_ / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_floor_us": round(floor_us, 1),
-            "frac_of_floor": round(floor_us / us, 4)}
+            "frac_of_floor": round(floor_us / us, 4),
+            "scaled_fp4": {"flags": "K3X_FLAG_SCALED_FP4", "us_per_layer": round(us_scaled, 1),
+                           "tokens_per_s": round(T / (us_scaled * 1e-6), 1),
+                           "routed_tflops": round(routed_flops / (us_scaled * 1e-6) / 1e12, 2)}}
 
 
 def time_calls(torch, fn, n: int, warmup: int = 3) -> float:

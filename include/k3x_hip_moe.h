@@ -130,6 +130,14 @@ enum k3x_flags {
      * fp32 experts (runtime/src/backend_cpu.cpp:317-318).  Runs the
      * general path's narrow GEMMs. */
     K3X_FLAG_SPLIT_INPUT = 8u,
+    /* Multiply the routed experts of the wide GEMM (prefill chunks, many
+     * rows per expert) on the scaled FP4 MFMA: the bf16 activation rows are
+     * re-encoded as two FP8 E4M3 terms with one power-of-two scale per 32
+     * values each (exact for bf16 values down to 2^-13 of their block's
+     * largest, within 2^-21 of it below), the MXFP4 weights go in as they
+     * are stored.  Ignored with K3X_FLAG_SPLIT_ACT and on the decode and
+     * narrow paths. */
+    K3X_FLAG_SCALED_FP4 = 16u,
 };
 
 /* Optional device buffers that receive intermediates of k3x_hip_moe_forward;

@@ -57,12 +57,21 @@ __device__ inline uint32_t wave_index() {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Vector-memory requests one wave issues at pipeline step k (activation tile
-// + weight tile; the MXFP4 scale dwords cover four K tiles and are requested
-// at steps with k % 4 == 0).
-template <bool FP4, int NT, int S, int U>
+// Step (k % 4) of a block of four K tiles at which the MXFP4 weight scale
+// dwords of the next block are requested: with the block's first step, or
+// (q8 rows, which leave fewer registers) first thing at its third, so that
+// they occupy registers for two steps instead of four.
+template <bool Q>
+constexpr int scale_step() {
+    return Q ? 2 : 0;
+}
+
+// Vector-memory requests one wave issues at pipeline step k (activation tile,
+// q8 scale dwords, weight tile; the MXFP4 scale dwords cover four K tiles and
+// are requested at steps with k % 4 == scale_step).
+template <bool FP4, int NT, int S, int U, bool Q>
 constexpr int step_loads(int d) {
-    return kALoads + NT * S * U + ((FP4 && d == 0) ? NT * S : 0);
+    return kALoads + (Q ? 1 : 0) + NT * S * U + ((FP4 && d == scale_step<Q>()) ? NT * S : 0);
 }
 
 // Waits until at most N of this wave's vector-memory requests are
@@ -77,23 +86,33 @@ __device__ inline void wait_and_barrier() {
 
 // End of pipeline step d (= k % 4): only the requests of steps k - 1 and k
 // may stay outstanding.  d is a constant once the step loop is unrolled.
-template <bool FP4, int NT, int S, int U>
+template <bool FP4, int NT, int S, int U, bool Q>
 __device__ inline void end_step(int d) {
+#define K3X_SL(i) step_loads<FP4, NT, S, U, Q>(i)
     switch (d) {
-        case 0: wait_and_barrier<step_loads<FP4, NT, S, U>(3) + step_loads<FP4, NT, S, U>(0)>(); break;
-        case 1: wait_and_barrier<step_loads<FP4, NT, S, U>(0) + step_loads<FP4, NT, S, U>(1)>(); break;
-        case 2: wait_and_barrier<step_loads<FP4, NT, S, U>(1) + step_loads<FP4, NT, S, U>(2)>(); break;
-        default: wait_and_barrier<step_loads<FP4, NT, S, U>(2) + step_loads<FP4, NT, S, U>(3)>(); break;
+        case 0: wait_and_barrier<K3X_SL(3) + K3X_SL(0)>(); break;
+        case 1: wait_and_barrier<K3X_SL(0) + K3X_SL(1)>(); break;
+        case 2: wait_and_barrier<K3X_SL(1) + K3X_SL(2)>(); break;
+        default: wait_and_barrier<K3X_SL(2) + K3X_SL(3)>(); break;
     }
+#undef K3X_SL
 }
 
 // SPLIT: gate/up stores each activation as bf16 hi and lo halves (act_lo
 // elements apart); down reads rows [hi | lo] of 2 kt tiles against the
 // weights repeated along K.
-template <bool FP4, bool GATEUP, int NT, bool SPLIT>
+// Q (MXFP4 only): the activation rows are q8 rows (hi and lo E4M3 codes of
+// each K tile, 256 bytes like a bf16 tile row) with E8M0 scale dwords; each
+// (row tile, weight block) pair takes two v_mfma_scale_f32_16x16x128_f8f6f4
+// per K tile (hi, lo) on the weight codes as stored, in place of four bf16
+// MFMAs on dequantised weights.
+template <bool FP4, bool GATEUP, int NT, bool SPLIT, bool Q>
 __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
+    static_assert(!Q || (FP4 && !SPLIT), "q8 rows meet MXFP4 weights, one term pair per tile");
     __shared__ u32x4 s_a4[kWideStages * kTileChunks];  // 128 KiB ring
     __shared__ uint32_t s_yrow[kWideRows];              // down: output row of each chunk row
+    // Q: scale dwords {hi, lo} of the chunk's rows per ring stage.
+    __shared__ uint32_t s_qs[Q ? kWideStages * kWideRows * 2 : 1];
     constexpr int S = GATEUP ? 2 : 1;  // matrices per output row block (gate, up)
     constexpr int U = FP4 ? 1 : 4;     // 16-byte words per lane per tile
     static_assert(kWideStages == 4, "the step schedule below is written for four stages");
@@ -160,9 +179,23 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         const uint32_t src = a.gather ? a.pair_token[rr] : rr;
         aoff[q] = (src * a.a_stride + ((lane >> 2) ^ q) * 8) * 2;
     }
+    // Q: scale loads also write LDS directly, one dword per lane: waves w
+    // and w + 4 both fill quarter w % 4 of a stage (rows 32 (w % 4) ..
+    // + 31, {hi, lo} each; the same values), so every wave issues the same
+    // number of requests per step.
+    const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        Q ? const_cast<uint32_t*>(a.qs) : nullptr, (short)0, Q ? a.qs_bytes : 0u, 0x00020000);
+    uint32_t qoff = 0;
+    if constexpr (Q) {
+        const uint32_t r = (wave & 3) * 32 + (lane >> 1);
+        const uint32_t rr = off + m0 + min(r, rows - 1);
+        const uint32_t src = a.gather ? a.pair_token[rr] : rr;
+        qoff = (src * kt * 2 + (lane & 1)) * 4;
+    }
     // Down: the output row of chunk row tid % 128 (the pair's token * top_k
-    // + slot, or the row itself), requested now so that it has arrived by
-    // the epilogue; it goes through LDS to the lanes that store the row.
+    // + slot, or the row itself), requested first; it goes through LDS to
+    // the lanes that store the row, stored there once the prologue's
+    // requests are out (no register holds it through the step loop).
     uint32_t yv = 0;
     if constexpr (!GATEUP) {
         const uint32_t r = off + m0 + min(tid % kWideRows, rows - 1);
@@ -170,9 +203,17 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     }
     // MFMA operand of lane (n, g), 8-column group j: row n (+ 16 per row
     // tile, 4 KiB), chunk 4 g + j; in 16-byte units.
+    // Q: the E4M3 operand of lane (n, g) is K 16 g .. + 15 and 64 + 16 g ..
+    // + 15 of row n (the scaled MFMA's 8-bit lane layout): chunks g and
+    // g + 4 of the hi codes, 8 + g and 12 + g of the lo codes.  The swizzle
+    // only touches c % 4, so they sit 0, 4, 8 and 12 chunk positions (16
+    // units each) past chunk g: apos[0] serves all four.
     uint32_t apos[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) apos[j] = (n >> 2) * 64 + (4 * g + (j ^ (n >> 2))) * 4 + (n & 3);
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = Q ? g : 4 * g + j;
+        apos[j] = (n >> 2) * 64 + (c ^ (n >> 2)) * 4 + (n & 3);
+    }
 
     // Weight stages: codes bc[d][nt][w][u] of K tile k in stage d = k % 4
     // (three are live at a time: tiles k .. k + 2 while tile k is
@@ -198,6 +239,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                 __builtin_amdgcn_raw_buffer_load_b32(                                        \
                     srsrc, lane4, (((rb0 + nt) * a.ks + (k) / 4) * S + w) * 256, 0);          \
     }
+#define WIDE_LOAD_Q(k, buf)                                                                  \
+    if constexpr (Q)                                                                         \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                            \
+            qrsrc, (lds_ptr_t)&s_qs[(buf) * (kWideRows * 2) + (wave & 3) * 64], 4, qoff,     \
+            (k) * 8, 0, 0);
 #define WIDE_ORDER() asm volatile("" ::: "memory")
 
     // MT = row tiles multiplied: the chunk's rows rounded up to 64, 96 or
@@ -220,57 +266,115 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         // activation and weight tile s + 3 (the scales of tiles 0..3 with
         // step -3's).
         WIDE_LOAD_A(0u, 0)
+        WIDE_LOAD_Q(0u, 0)
         WIDE_LOAD_B(0, wtile(0u))
         WIDE_LOAD_SCALES(sc, wtile(0u))
         WIDE_ORDER();
         WIDE_LOAD_A(1u, 1)
+        WIDE_LOAD_Q(1u, 1)
         WIDE_LOAD_B(1, wtile(1u))
         WIDE_ORDER();
         WIDE_LOAD_A(2u, 2)
+        WIDE_LOAD_Q(2u, 2)
         WIDE_LOAD_B(2, wtile(2u))
+        if constexpr (!GATEUP) {
+            if (tid < kWideRows) s_yrow[tid] = yv;
+        }
         // Steps -2 and -1 may stay in flight; tile 0 (step -3) has arrived.
-        wait_and_barrier<2 * (kALoads + NT * S * U)>();
+        wait_and_barrier<2 * (kALoads + (Q ? 1 : 0) + NT * S * U)>();
 
         for (uint32_t kb = 0; kb < kta; kb += kWideStages) {
 #pragma unroll
             for (int d = 0; d < kWideStages; ++d) {
                 const uint32_t k = kb + d;
                 const u32x4* sa = s_a4 + d * kTileChunks;
+                if constexpr (Q) {
+                    // Scale bytes: the weights' byte d of each block dword
+                    // (selected by the MFMA's op_sel), the rows' byte g of
+                    // their {hi, lo} dwords (read as a byte from LDS).
+                    const uint8_t* sq =
+                        reinterpret_cast<const uint8_t*>(s_qs + d * (kWideRows * 2));
+                    // All row tiles' hi terms, then their lo terms (an
+                    // accumulator's two updates MT * NT * S MFMAs apart).
+                    // The operand of the next row tile is read from LDS
+                    // before the MFMAs of this one; the scheduling barrier
+                    // keeps the compiler from hoisting more reads (their
+                    // registers would spill).
+                    auto operand = [&](int i) {
+                        const int t = i / MT, mt = i % MT;
+                        return q8_operand(sa[mt * 256 + t * 32 + apos[0]],
+                                          sa[mt * 256 + t * 32 + 16 + apos[0]]);
+                    };
+                    auto exponent = [&](int i) {
+                        const int t = i / MT, mt = i % MT;
+                        return (uint32_t)sq[(mt * 16 + n) * 8 + t * 4 + g];
+                    };
+                    i32x8 av = operand(0);
+                    uint32_t ea = exponent(0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    bf16x8 bw[NT][S];
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                        for (int w = 0; w < S; ++w) {
-                            if constexpr (FP4) {
-                                const uint32_t word = bc[d][nt][w][0][j];
-                                bw[nt][w] = dequant8(word, e8m0_to_f32((sc[nt][w] >> (8 * d)) & 0xffu));
-                            } else {
-                                bw[nt][w] = as_bf16x8(bc[d][nt][w][j]);
-                            }
+                    for (int i = 0; i < 2 * MT; ++i) {
+                        i32x8 an = av;
+                        uint32_t en = ea;
+                        if (i + 1 < 2 * MT) {
+                            an = operand(i + 1);
+                            en = exponent(i + 1);
                         }
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const bf16x8 af = as_bf16x8(sa[mt * 256 + apos[j]]);
+                        const int mt = i % MT;
 #pragma unroll
                         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                             for (int w = 0; w < S; ++w)
-                                acc[mt][nt][w] = mfma16x16x32(af, bw[nt][w], acc[mt][nt][w]);
+                                acc[mt][nt][w] = mfma_q8_fp4_sel(d, av, bc[d][nt][w][0],
+                                                                 acc[mt][nt][w], ea, sc[nt][w]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        av = an;
+                        ea = en;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        bf16x8 bw[NT][S];
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                            for (int w = 0; w < S; ++w) {
+                                if constexpr (FP4) {
+                                    const uint32_t word = bc[d][nt][w][0][j];
+                                    bw[nt][w] = dequant8(
+                                        word, e8m0_to_f32((sc[nt][w] >> (8 * d)) & 0xffu));
+                                } else {
+                                    bw[nt][w] = as_bf16x8(bc[d][nt][w][j]);
+                                }
+                            }
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            const bf16x8 af = as_bf16x8(sa[mt * 256 + apos[j]]);
+#pragma unroll
+                            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                                for (int w = 0; w < S; ++w)
+                                    acc[mt][nt][w] = mfma16x16x32(af, bw[nt][w], acc[mt][nt][w]);
+                        }
                     }
                 }
                 // Step k's requests: tile k + 3 into the LDS buffer and
                 // weight stage tile k - 1 used (all waves passed the barrier
                 // after multiplying it); past the end they repeat the last
                 // tile (the loads stay unconditional, the count exact).  The
-                // next block's scales ride with the block's first step.
+                // next block's scales ride with step scale_step of the block
+                // (with q8 rows requested first, so that waiting for them at
+                // the next block does not wait for this step's tiles).
+                constexpr bool kScalesFirst = Q;
+                if (kScalesFirst && d == scale_step<Q>())
+                    WIDE_LOAD_SCALES(scn, wtile(min(kb + 4, kta - 1)))
                 WIDE_LOAD_A(min(k + 3, kta - 1), (d + 3) % kWideStages)
+                WIDE_LOAD_Q(min(k + 3, kta - 1), (d + 3) % kWideStages)
                 WIDE_LOAD_B((d + 3) % kWideStages, wtile(min(k + 3, kta - 1)))
-                if (d == 0) WIDE_LOAD_SCALES(scn, wtile(min(k + 4, kta - 1)))
+                if (!kScalesFirst && d == scale_step<Q>())
+                    WIDE_LOAD_SCALES(scn, wtile(min(kb + 4, kta - 1)))
                 // Tile k + 1 (requested at step k - 2) is in LDS once only
                 // steps k - 1 and k are outstanding.
-                end_step<FP4, NT, S, U>(d);
+                end_step<FP4, NT, S, U, Q>(d);
             }
             if constexpr (FP4) {
 #pragma unroll
@@ -301,9 +405,6 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         constexpr uint32_t RP = RP0 < MT * 16 ? RP0 : MT * 16;     // rows per pass
         static_assert(RP >= 16, "one row tile per pass at least");
         uint8_t* stage = reinterpret_cast<uint8_t*>(s_a4);
-        if constexpr (!GATEUP) {
-            if (tid < kWideRows) s_yrow[tid] = yv;
-        }
         const uint32_t col0 = jb * kCols;
 #pragma unroll
         for (uint32_t p0 = 0; p0 < MT * 16; p0 += RP) {
@@ -364,12 +465,56 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
 #undef WIDE_LOAD_A
 #undef WIDE_LOAD_B
 #undef WIDE_LOAD_SCALES
+#undef WIDE_LOAD_Q
 #undef WIDE_ORDER
 
 // Output 16-row blocks per wave (kWaves * NT per workgroup): the more output
 // rows a workgroup covers, the fewer times the chunk's activation rows are
 // streamed from L2.
 constexpr int kNtRoutedGateUp = 2, kNtRoutedDown = 4, kNtSharedGateUp = 1, kNtSharedDown = 2;
+
+// bf16 rows -> q8 rows: one thread per 32-element block; the four threads of
+// one K tile (consecutive lanes) merge their exponents into the tile's two
+// scale dwords.
+__global__ __launch_bounds__(256) void q8_rows_kernel(const uint16_t* __restrict__ src,
+                                                      uint32_t rows, uint32_t cols,
+                                                      uint32_t stride, uint16_t* __restrict__ q,
+                                                      uint32_t* __restrict__ qs,
+                                                      const uint32_t* status) {
+    if (prior_status(status)) return;
+    const uint32_t nb = cols / 32;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    // rows * nb is a multiple of 4: a tile's four threads are all in or out.
+    if (i >= rows * nb) return;
+    const uint32_t row = i / nb, b = i % nb, t = b / 4, bb = b % 4;
+    const u32x4* in = reinterpret_cast<const u32x4*>(src + (size_t)row * stride + b * 32);
+    float x[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 v = in[c];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[8 * c + 2 * j] = __uint_as_float(v[j] << 16);
+            x[8 * c + 2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
+        }
+    }
+    uint32_t hi[8], lo[8], eh, el;
+    q8_block(x, hi, lo, eh, el);
+    u32x4* out = reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(q) + (size_t)row * cols * 2 +
+                                          t * 256 + bb * 32);
+    out[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    out[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    out[8] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    out[9] = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    eh <<= 8 * bb;
+    el <<= 8 * bb;
+    eh |= __shfl_xor(eh, 1);
+    el |= __shfl_xor(el, 1);
+    eh |= __shfl_xor(eh, 2);
+    el |= __shfl_xor(el, 2);
+    if (bb == 0)
+        *reinterpret_cast<uint2*>(qs + ((size_t)row * (cols / 128) + t) * 2) = make_uint2(eh, el);
+}
 
 }  // namespace
 
@@ -396,19 +541,49 @@ int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uin
         return K3X_ERR_INVALID_EXTENT;
     if (a.kta && (a.kta != 2 * a.kt || gu)) return K3X_ERR_INVALID_EXTENT;
     const bool split = gu ? a.act_lo != 0 : a.kta != 0;
+    // q8 rows: routed kinds only, no split halves, a scale dword pair per
+    // row and K tile.
+    const bool q8 = a.qs != nullptr;
+    if (q8 && (split || (kind != kWideRoutedGateUp && kind != kWideRoutedDown) ||
+               (uintptr_t)a.qs % 8 || a.a_stride != a.kt * 128))
+        return K3X_ERR_INVALID_EXTENT;
     const dim3 grid(max_items * (a.nrb / per));
-#define K3X_WIDE(FP4, GU, NT)                                                                   \
-    if (split)                                                                                  \
-        hipLaunchKernelGGL((wide_gemm<FP4, GU, NT, true>), grid, dim3(kThreads), 0, stream, a); \
-    else                                                                                        \
-        hipLaunchKernelGGL((wide_gemm<FP4, GU, NT, false>), grid, dim3(kThreads), 0, stream, a);
+#define K3X_GO(...) hipLaunchKernelGGL((__VA_ARGS__), grid, dim3(kThreads), 0, stream, a)
     switch (kind) {
-        case kWideRoutedGateUp: K3X_WIDE(true, true, kNtRoutedGateUp) break;
-        case kWideRoutedDown: K3X_WIDE(true, false, kNtRoutedDown) break;
-        case kWideSharedGateUp: K3X_WIDE(false, true, kNtSharedGateUp) break;
-        default: K3X_WIDE(false, false, kNtSharedDown) break;
+        case kWideRoutedGateUp:
+            if (q8) K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, false, true>);
+            else if (split) K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, true, false>);
+            else K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, false, false>);
+            break;
+        case kWideRoutedDown:
+            if (q8) K3X_GO(wide_gemm<true, false, kNtRoutedDown, false, true>);
+            else if (split) K3X_GO(wide_gemm<true, false, kNtRoutedDown, true, false>);
+            else K3X_GO(wide_gemm<true, false, kNtRoutedDown, false, false>);
+            break;
+        case kWideSharedGateUp:
+            if (split) K3X_GO(wide_gemm<false, true, kNtSharedGateUp, true, false>);
+            else K3X_GO(wide_gemm<false, true, kNtSharedGateUp, false, false>);
+            break;
+        default:
+            if (split) K3X_GO(wide_gemm<false, false, kNtSharedDown, true, false>);
+            else K3X_GO(wide_gemm<false, false, kNtSharedDown, false, false>);
+            break;
     }
-#undef K3X_WIDE
+#undef K3X_GO
+    ctx->kernel_launches += 1;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+int launch_q8_rows(k3x_hip_ctx* ctx, const uint16_t* src, uint32_t rows, uint32_t cols,
+                   uint32_t stride, uint16_t* q, uint32_t* qs, hipStream_t stream) {
+    if (!stream) stream = ctx->stream;
+    if (!rows) return K3X_OK;
+    if (cols % 128 || stride < cols || stride % 8 || (uintptr_t)src % 16 || (uintptr_t)q % 16 ||
+        (uintptr_t)qs % 8 || (uint64_t)rows * (cols / 32) >= (1ull << 32))
+        return K3X_ERR_INVALID_EXTENT;
+    const uint32_t n = rows * (cols / 32);
+    hipLaunchKernelGGL(q8_rows_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, src, rows,
+                       cols, stride, q, qs, ctx->status);
     ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }

@@ -66,6 +66,38 @@ __device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+// 32 E4M3 codes of one lane (two 16-byte pieces, element i in byte i) as the
+// A operand of the scaled MFMA.
+__device__ inline i32x8 q8_operand(u32x4 p0, u32x4 p1) {
+    return i32x8{(int)p0[0], (int)p0[1], (int)p0[2], (int)p0[3],
+                 (int)p1[0], (int)p1[1], (int)p1[2], (int)p1[3]};
+}
+
+// C += (A * 2^(sa-127)) (B * 2^(sb-127)) over K = 128: A = E4M3 codes
+// (lane (n, g): row n, K 32 g .. 32 g + 31), B = the lane's 32 E2M1 codes
+// of the bank tile (one 16-byte word, low nibble first); sa = E8M0 byte in
+// bits 0..7.  Output in the 16x16 accumulator layout of mfma16x16x32.
+// sb's byte OPB is the weights' scale (op_sel of the scale operand).
+template <int OPB>
+__device__ inline f32x4 mfma_q8_fp4(i32x8 a, u32x4 b, f32x4 c, uint32_t sa, uint32_t sb) {
+    const i32x8 b8 = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b8, c, 0, 4, 0, (int)sa, OPB,
+                                                            (int)sb);
+}
+
+// The same with the byte chosen by opb = 0..3, a constant once unrolled.
+__device__ inline f32x4 mfma_q8_fp4_sel(int opb, i32x8 a, u32x4 b, f32x4 c, uint32_t sa,
+                                        uint32_t sb) {
+    switch (opb) {
+        case 0: return mfma_q8_fp4<0>(a, b, c, sa, sb);
+        case 1: return mfma_q8_fp4<1>(a, b, c, sa, sb);
+        case 2: return mfma_q8_fp4<2>(a, b, c, sa, sb);
+        default: return mfma_q8_fp4<3>(a, b, c, sa, sb);
+    }
+}
+
 // Correctly rounded expf evaluated in double (x = k ln2 + r, degree-13
 // Taylor polynomial on |r| <= ln2/2, one final rounding).  The operation
 // sequence is fixed with explicit fma so the CPU checker reproduces it bit
@@ -270,6 +302,83 @@ __device__ inline float glu(float g, float u, const GluParams& p) {
 // along K) multiplies by an fp32 activation.
 __device__ inline uint16_t act_lo_bf16(float v, uint16_t hi) {
     return f32_to_bf16(__fsub_rn(v, __uint_as_float((uint32_t)hi << 16)));
+}
+
+// ---------------------------------------------------------------------------
+// Two-term FP8 activation blocks ("q8 rows") for the scaled FP4 MFMA
+// (v_mfma_scale_f32_16x16x128_f8f6f4: OCP E4M3 activations x E2M1 weights,
+// one E8M0 scale per 32-element block of each operand).
+//
+// A block of 32 values x is stored as hi + lo with
+//   s_hi = 2^(floor(log2 max|x|) - 7)       (max|x| / s_hi in [128, 256))
+//   hi   = E4M3(x / s_hi)                   (round to nearest even)
+//   r    = x - hi * s_hi                    (exact in fp32)
+//   s_lo = 2^(floor(log2 max|r|) - 7),  lo = E4M3(r / s_lo).
+// For bf16 x the residual r of every element within 2^-13 of max|x| has at
+// most four significant bits, so lo holds it exactly; smaller elements are
+// off by at most 2^-21 max|x|.  hi * s_hi + lo * s_lo is thus the bf16 value
+// (to that bound), and two scaled MFMAs (hi, lo) reproduce the bf16 product.
+//
+// Row layout, per 128-element K tile: 128 hi codes then 128 lo codes (256
+// bytes, as many as the bf16 row); scales [row][tile] = {hi, lo} dwords, byte
+// b = 32-element block b of the tile.
+// ---------------------------------------------------------------------------
+
+// Biased E8M0 exponent e with m / 2^(e-127) in [128, 256) for m = max|x| (at
+// least 1: the scale stays a normal fp32).
+__device__ inline uint32_t q8_exponent(float m) {
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 7;
+    return (uint32_t)(e < 1 ? 1 : e);
+}
+
+// Four values -> four E4M3 codes (byte i = v[i] * inv), rounded to nearest
+// even; inv is an exact power of two, so the scaling adds no rounding.
+__device__ inline uint32_t q8_pack4(float a, float b, float c, float d, float inv) {
+    typedef __attribute__((ext_vector_type(2))) short i16x2;
+    i16x2 o = {0, 0};
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a * inv, b * inv, 1.0f, false);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, c * inv, d * inv, 1.0f, true);
+    return __builtin_bit_cast(uint32_t, o);
+}
+
+// Four E4M3 codes -> their values times s.
+__device__ inline void q8_unpack4(uint32_t q, float s, float* out) {
+    typedef __attribute__((ext_vector_type(2))) float f32x2;
+    const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)q, 1.0f, false);
+    const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((int)q, 1.0f, true);
+    out[0] = lo[0] * s;
+    out[1] = lo[1] * s;
+    out[2] = hi[0] * s;
+    out[3] = hi[1] * s;
+}
+
+// One 32-element block: hi and lo codes (eight dwords each, element i in
+// byte i % 4 of dword i / 4) and the two E8M0 exponents.
+__device__ inline void q8_block(const float (&x)[32], uint32_t (&hi)[8], uint32_t (&lo)[8],
+                                uint32_t& ehi, uint32_t& elo) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(x[i]));
+    ehi = q8_exponent(m);
+    const float inv_hi = __uint_as_float((254u - ehi) << 23), s_hi = __uint_as_float(ehi << 23);
+    float r[32];
+    float rm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = q8_pack4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3], inv_hi);
+        float b[4];
+        q8_unpack4(hi[i], s_hi, b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r[4 * i + j] = __fsub_rn(x[4 * i + j], b[j]);
+            rm = fmaxf(rm, fabsf(r[4 * i + j]));
+        }
+    }
+    elo = q8_exponent(rm);
+    const float inv_lo = __uint_as_float((254u - elo) << 23);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        lo[i] = q8_pack4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3], inv_lo);
 }
 
 // SplitMix64 output function (Steele, Lea & Flood, OOPSLA 2014) and the

@@ -38,6 +38,12 @@ struct WideGemmArgs {
     uint16_t* act;               // gate/up output [row][act_stride] bf16
     uint32_t act_stride;
     uint32_t act_lo;             // gate/up: element offset of the lo half in a row (0: none)
+    // Routed kinds on the scaled FP4 MFMA: `a` holds q8 rows (two E4M3
+    // terms per element, the bf16 row's bytes; k3x_device.hpp) and qs their
+    // scales [row][kt] {hi, lo} dwords.  Null: bf16 rows, weights
+    // dequantised to bf16.
+    const uint32_t* qs;
+    uint32_t qs_bytes;           // bytes readable from qs
     float* y;                    // down output [row][y_stride] fp32
     uint32_t y_stride;
     uint32_t scatter;            // y row = token * top_k + slot (1) or off + m (0)
@@ -67,5 +73,12 @@ uint32_t wide_rb_per_block(WideKind kind);
 // the output row blocks, one workgroup each.
 int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items,
                      hipStream_t stream = nullptr);
+
+// bf16 rows [rows][cols] (row stride `stride` elements) -> q8 rows q
+// ([rows][cols] 16-bit units: 2 cols bytes a row) and their scale dwords qs
+// [rows][cols / 128][2] (k3x_device.hpp), on `stream` (the context stream
+// when null).  cols a multiple of 128.
+int launch_q8_rows(k3x_hip_ctx* ctx, const uint16_t* src, uint32_t rows, uint32_t cols,
+                   uint32_t stride, uint16_t* q, uint32_t* qs, hipStream_t stream = nullptr);
 
 }  // namespace k3x_hip

@@ -127,6 +127,12 @@ struct LayerBuffers {
     uint32_t* n_witems;    // [1]
     uint8_t* gscratch;     // grouping: per-chunk counts and first uses, pair ranks
     uint16_t* xp;          // [T/16][256][16][4][8] bf16 tile/residue-major xn (in y's bytes)
+    // K3X_FLAG_SCALED_FP4 only (else null): q8 rows of xn and act, and their
+    // scale dword pairs per 128-element tile.
+    uint16_t* qx;          // [T][H] 16-bit units
+    uint32_t* qxs;         // [T][H/128][2]
+    uint16_t* qact;        // [P][I] 16-bit units
+    uint32_t* qacts;       // [P][I/128][2]
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }

@@ -1350,9 +1350,16 @@ size_t group_scratch_bytes(uint32_t T, uint32_t K, uint32_t E) {
     return 2 * nch * E * 4 + (((size_t)T * K + 255) & ~(size_t)255);
 }
 
-// split: the routed activation rows hold [hi | lo] halves (K3X_FLAG_SPLIT_ACT).
+// K3X_FLAG_SCALED_FP4 in effect: not with split activations or inputs.
+bool scaled_fp4(const k3x_hip_moe_params* p) {
+    return (p->flags & K3X_FLAG_SCALED_FP4) &&
+           !(p->flags & (K3X_FLAG_SPLIT_ACT | K3X_FLAG_SPLIT_INPUT));
+}
+
+// split: the routed activation rows hold [hi | lo] halves (K3X_FLAG_SPLIT_ACT);
+// q8: room for the q8 rows of the scaled FP4 wide GEMM.
 size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K, bool split,
-             Scratch* s) {
+             bool q8, Scratch* s) {
     size_t at = 0;
     auto take = [&](size_t bytes) {
         uint8_t* p = base ? base + at : nullptr;
@@ -1384,6 +1391,10 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->witems = (uint32_t*)take((size_t)wide_max_items(d, T, K) * 4);
     s->n_witems = (uint32_t*)take(4);
     s->gscratch = take(group_scratch_bytes(T, K, d.experts));
+    s->qx = q8 ? (uint16_t*)take((size_t)T * d.hidden * 2) : nullptr;
+    s->qxs = q8 ? (uint32_t*)take((size_t)T * (d.hidden / 128) * 8) : nullptr;
+    s->qact = q8 ? (uint16_t*)take(P * d.inter * 2) : nullptr;
+    s->qacts = q8 ? (uint32_t*)take(P * (d.inter / 128) * 8) : nullptr;
     return at;
 }
 
@@ -1401,7 +1412,8 @@ int validate_params(const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     if (!finite_pos(p->rms_epsilon) || !std::isfinite(p->routed_scale) || p->glu > 1 ||
         p->renorm > 1 ||
         (p->flags & ~(uint32_t)(K3X_FLAG_GENERAL_PATH | K3X_FLAG_ROUND_EXPERT_OUT |
-                                K3X_FLAG_SPLIT_ACT | K3X_FLAG_SPLIT_INPUT)))
+                                K3X_FLAG_SPLIT_ACT | K3X_FLAG_SPLIT_INPUT |
+                                K3X_FLAG_SCALED_FP4)))
         return K3X_ERR_INVALID_MXFP4;
     if (p->glu == K3X_GLU_SITU &&
         (!finite_pos(p->situ_beta) || (p->has_situ_linear && !finite_pos(p->situ_linear_beta))))
@@ -1570,8 +1582,18 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     // grouping listed (up to wide_max_items).
     const uint32_t routed_chunks = wide_max_items(d, T, K);
     WideGemmArgs g = wide_gate_up_args(ctx, bank, p, s, xn, glu);
+    // Scaled FP4: the experts read q8 rows of xn, then of act (quantised
+    // in the stage that consumes them).
+    const bool q8 = s.qx != nullptr;
     int mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
-    int st = launch_wide_gemm(ctx, kWideRoutedGateUp, g, routed_chunks);
+    int st = K3X_OK;
+    if (q8) {
+        st = launch_q8_rows(ctx, xn, T, d.hidden, d.hidden, s.qx, s.qxs);
+        g.a = s.qx;
+        g.qs = s.qxs;
+        g.qs_bytes = T * (d.hidden / 128) * 8;
+    }
+    if (!st) st = launch_wide_gemm(ctx, kWideRoutedGateUp, g, routed_chunks);
     end_stage(ctx, mark);
     if (st) return st;
     if (shared_inline && d.shared_inter &&
@@ -1594,8 +1616,15 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.y = s.y;
     dn.y_stride = d.hidden;
     dn.scatter = 1;
+    dn.qs = nullptr;
     mark = begin_stage(ctx, K3X_STAGE_DOWN);
-    st = launch_wide_gemm(ctx, kWideRoutedDown, dn, routed_chunks);
+    if (q8) {
+        st = launch_q8_rows(ctx, s.act, T * K, d.inter, d.inter, s.qact, s.qacts);
+        dn.a = s.qact;
+        dn.qs = s.qacts;
+        dn.qs_bytes = T * K * (d.inter / 128) * 8;
+    }
+    if (!st) st = launch_wide_gemm(ctx, kWideRoutedDown, dn, routed_chunks);
     end_stage(ctx, mark);
     return st;
 }
@@ -1865,10 +1894,11 @@ int launch_topk_any(k3x_hip_ctx* ctx, const float* logits, const float* bias, ui
 int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, Scratch* s) {
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
-    const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, split, s);
+    const bool q8 = scaled_fp4(p);
+    const size_t need = carve(nullptr, bank->desc, p->tokens, p->top_k, split, q8, s);
     int st = k3x_hip::ensure_scratch(ctx, need);
     if (st) return st;
-    carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, split, s);
+    carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, split, q8, s);
     return K3X_OK;
 }
 
@@ -2163,13 +2193,13 @@ int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
     if (!bank->router_ready) return K3X_ERR_INVALID_STATE;
     if (!ctx->noalloc_scratch) return K3X_ERR_BACKEND_UNAVAILABLE;
     Scratch s;
-    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
-    if (carve(nullptr, bank->desc, p->tokens, p->top_k, split, &s) >
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0, q8 = scaled_fp4(p);
+    if (carve(nullptr, bank->desc, p->tokens, p->top_k, split, q8, &s) >
         K3X_HIP_NOALLOC_SCRATCH_BYTES)
         return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     carve(static_cast<uint8_t*>(ctx->noalloc_scratch), bank->desc, p->tokens, p->top_k, split,
-          &s);
+          q8, &s);
     // Stage timing takes events from a pool that may have to create them:
     // not on this path.
     const bool profiling = ctx->profiling;

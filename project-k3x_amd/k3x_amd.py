@@ -71,6 +71,7 @@ FLAG_GENERAL_PATH = 1
 FLAG_ROUND_EXPERT_OUT = 2
 FLAG_SPLIT_ACT = 4
 FLAG_SPLIT_INPUT = 8
+FLAG_SCALED_FP4 = 16
 
 
 class LatentWeights(C.Structure):

@@ -607,3 +607,57 @@ def test_c5_prefill_chunk(hip, oracle, parity_report):
     assert np.array_equal(gp["out_f32"].view(np.uint32), got["out_f32"][perm].view(np.uint32))
     say("c5 token permutation equivariance bit-exact")
     bank.close()
+
+
+def test_c5_prefill_scaled_fp4(hip, oracle, parity_report):
+    """Config 5 on the scaled FP4 MFMA (K3X_FLAG_SCALED_FP4): the routed
+    experts take xn and act as two-term E4M3 rows against the MXFP4 codes as
+    stored.  Routing and grouping bit-exact and permutation equivariance
+    bit-exact as on the bf16 path; outputs of tokens in every work-item class
+    against the oracle, with the fractions within rtol 2e-3 / atol 1e-3 and
+    within 1e-2 / 5e-3 reported.  The MFMA sums each 32-element block's
+    products in a window of about 2^-13 of the block's largest product (not
+    in fp32), so this path does not meet the fp32-accumulation standard the
+    bf16 path meets; the bounds asserted here are the measured ones."""
+    from synth import CONFIGS, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = CONFIGS[5]
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    x = layer.x_bits()
+    got = run_layer(k3x_amd, ctx, cfg, bank, x, flags=k3x_amd.FLAG_SCALED_FP4, per_pair=False)
+    xn, ids, w, csr = check_routing(oracle, layer, got, x)
+    ch = 128
+    picked = tokens_by_row_class(got, cfg.top_k, {
+        "full_128": (ch, lambda r, last: r == ch),
+        "partial_97_127": (ch, lambda r, last: 96 < r < ch),
+        "partial_65_96": (ch, lambda r, last: 64 < r <= 96),
+        "partial_le_64": (ch, lambda r, last: r <= 64 and last)})
+    tokens = sorted(set(picked.values()) | {0, cfg.tokens - 1})
+    assert len(picked) == 4
+    act_ref, y_ref = layer.pair_outputs(xn, ids, tokens)
+    shared = layer.shared_out(xn, tokens)
+    out_ref = layer.combine(y_ref, w, shared, tokens)
+    ref = np.stack([out_ref[t] for t in tokens]).astype(np.float64)
+    gpu = np.stack([got["out_f32"][t] for t in tokens]).astype(np.float64)
+    err = np.abs(gpu - ref)
+    f_tight = float(np.mean(err <= ATOL + RTOL * np.abs(ref)))
+    f_loose = float(np.mean(err <= 5e-3 + 1e-2 * np.abs(ref)))
+    scale = np.abs(ref).max(axis=1, keepdims=True)
+    worst = float((err / scale).max())
+    # Activations against the bf16-dequant path's (same grouping, CSR rows).
+    base = run_layer(k3x_amd, ctx, cfg, bank, x, per_pair=False)
+    d_act = ulp_diff_bf16(got["act"], base["act"])
+    msg = (f"c5 scaled FP4: {len(tokens)} tokens; {f_tight:.4f} of outputs within rtol {RTOL} / "
+           f"atol {ATOL}, {f_loose:.4f} within 1e-2 / 5e-3, max |err| / row max {worst:.2e}; "
+           f"activations vs bf16 path: {np.count_nonzero(d_act) / d_act.size:.4f} differ, "
+           f"max {int(d_act.max())} bf16 ulp")
+    say(msg)
+    parity_report(msg)
+    assert f_tight >= 0.9 and f_loose >= 0.99 and worst < 1e-2
+    perm = np.random.default_rng(5).permutation(cfg.tokens)
+    gp = run_layer(k3x_amd, ctx, cfg, bank, x[perm], flags=k3x_amd.FLAG_SCALED_FP4,
+                   per_pair=False)
+    assert np.array_equal(gp["out_f32"].view(np.uint32), got["out_f32"][perm].view(np.uint32))
+    say("c5 scaled: token permutation equivariance bit-exact")
+    bank.close()
