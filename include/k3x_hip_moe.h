@@ -185,11 +185,11 @@ enum k3x_stage {
     K3X_STAGE_DOWN = 4,         /* routed MXFP4 down projection */
     K3X_STAGE_SHARED_DOWN = 5,
     K3X_STAGE_COMBINE = 6,      /* slot-ordered mix + shared add + bf16 cast */
-    /* Decode path (T <= 4); its combine is K3X_STAGE_COMBINE. */
+    /* Decode path (T <= 4); its combine is part of K3X_STAGE_DECODE_DOWN. */
     K3X_STAGE_DECODE_FRONT = 7,   /* RMSNorm, router logits, shared gate/up */
     K3X_STAGE_DECODE_SELECT = 8,  /* Top-K, grouping, shared down */
     K3X_STAGE_DECODE_GATE_UP = 9, /* routed gate/up + GLU */
-    K3X_STAGE_DECODE_DOWN = 10,   /* routed down */
+    K3X_STAGE_DECODE_DOWN = 10,   /* routed down, then the slot-ordered mix */
     K3X_STAGE_COUNT = 11,
 };
 
@@ -322,12 +322,15 @@ int k3x_hip_moe_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
  * per-pair outputs, shared expert) come from a fixed device array of
  * K3X_HIP_NOALLOC_SCRATCH_BYTES per device (32 MiB, held until the process
  * ends) instead of the context's grow-only scratch; a call whose buffers do
- * not fit returns K3X_ERR_INVALID_EXTENT before anything is enqueued (the
- * config-3 decode layer needs about 1.1 MiB, T=16 of it about 9 MiB).  The
- * array is shared by every call on the device, whatever the context or
- * stream: calls that overlap on one GPU race, so a caller serialises them
- * (one stream, or events).  Nothing in it needs to start at zero; every
- * buffer a call reads was written earlier in the same call.  Stage timing
+ * not fit in it less its last 16 KiB returns K3X_ERR_INVALID_EXTENT before
+ * anything is enqueued (the config-3 decode layer needs about 1.1 MiB, T=16
+ * of it about 9 MiB).  The array is shared by every call on the device,
+ * whatever the context or stream: calls that overlap on one GPU race, so a
+ * caller serialises them (one stream, or events).  Its last 16 KiB hold the
+ * decode path's combine counters, zero when the process loads the library
+ * and left zero by every call that completes; nothing else in it needs to
+ * start at zero (every other buffer a call reads was written earlier in the
+ * same call).  Stage timing
  * (k3x_hip_ctx_set_profiling) is not recorded for these calls.  Results are
  * bit-identical to k3x_hip_moe_forward's.  Asynchronous. */
 int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,

@@ -7,6 +7,7 @@
 #include <iterator>
 #include <new>
 
+#include "k3x_decode.hpp"
 #include "k3x_device.hpp"
 #include "k3x_internal.hpp"
 
@@ -389,6 +390,8 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
         hipMemset(ctx->status, 0, 256) != hipSuccess ||
+        hipMalloc((void**)&ctx->mix_counts, k3x_hip::kDecodeMixBytes) != hipSuccess ||
+        hipMemset(ctx->mix_counts, 0, k3x_hip::kDecodeMixBytes) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
             hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
@@ -398,6 +401,7 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
         if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
         if (ctx->status) (void)hipFree(ctx->status);
+        if (ctx->mix_counts) (void)hipFree(ctx->mix_counts);
         delete ctx;
         return K3X_ERR_BACKEND_UNAVAILABLE;
     }
@@ -422,6 +426,7 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->latent_scratch) (void)hipFree(ctx->latent_scratch);
     if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->mix_counts) (void)hipFree(ctx->mix_counts);
     k3x_hip::free_crc(ctx);
     for (const StageMark& m : ctx->pending) {
         (void)hipEventDestroy(m.start);

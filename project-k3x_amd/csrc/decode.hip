@@ -1,5 +1,6 @@
-// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): five
-// launches, no cross-workgroup synchronisation inside any of them.
+// decode.hip -- the decode path of the MoE layer (T <= 4 tokens): four
+// launches; no workgroup ever waits for another (the fused combine is done
+// by whichever workgroup completes a counter).
 //
 //   decode_front_kernel   router blocks rebuild xn = bf16(RMSNorm(x) * gamma)
 //                         in LDS and stream the fp32 router, one wave per
@@ -14,8 +15,10 @@
 //                         expert, 16-row block), weights dequantised in
 //                         registers.
 //   decode_down_kernel    routed MXFP4 down projection: one wave per (active
-//                         expert, 16-row block) -> per-pair rows y.
-//   decode_combine_kernel out = bf16(sum over slots in router order of w * y
+//                         expert, 16-row block) -> per-pair rows y; the
+//                         workgroup that stores the last of a token's K rows
+//                         of a 64-column group writes that group of
+//                         out = bf16(sum over slots in router order of w * y
 //                         + shared).
 // The shared expert needs only xn, so it rides along as extra workgroups of
 // the two latency-bound launches (router, Top-K), whose own blocks leave
@@ -114,11 +117,14 @@ struct NormShared {
 // prefetch goes there: vector loads complete in order, so loads issued
 // before x / gamma would delay the prologue); then the latched error word of
 // earlier launches is checked (false, for the whole block, when it is set).
-template <int kThreads, typename Mid>
+// late() runs once this wave's x / gamma loads have arrived, before the sum
+// of squares and the xn pass (loads issued there overlap them without
+// queueing ahead of any block's x / gamma).
+template <int kThreads, typename Mid, typename Late>
 __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, uint32_t T,
                                          uint32_t H, float eps, uint4* s_x4, NormShared& ns,
                                          uint16_t* xn_out, uint32_t* status,
-                                         const uint32_t* prior, Mid&& mid) {
+                                         const uint32_t* prior, Mid&& mid, Late&& late) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
     const uint32_t chunks = T * H / 8;          // x chunks; gamma chunks follow
@@ -149,6 +155,9 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         for (int it = 0; it < kLoads; ++it)
             s_x4[(min(c0 + tid + kThreads * it, all - 1) + rot) % all] = v[it];
     }
+    // x and gamma have arrived (this wave's, and the block's after the
+    // barrier): late() may now request what the block needs after xn.
+    late();
     __syncthreads();
     // Sum of squares per token in the canonical order -- partial q (of 256)
     // sums the elements 256 j + q over j in sequence, then the balanced
@@ -163,22 +172,42 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         const uint16_t* xr = s_x + (size_t)t * H;
         double v;
         int bad = 0;
+        // The values of eight steps j are read from LDS before their eight
+        // dependent FMAs (one LDS round trip per eight steps, not per step);
+        // reads past the row end repeat its last group and are not added.
+        constexpr uint32_t kB = 8;
+        const uint32_t J = H / 256;
         if (nw == 4) {
             double p = 0.0;
-            for (uint32_t j = 0; j < H / 256; ++j) {
-                const float f = bf16_to_f32(xr[256 * j + 64 * u + lane]);
-                bad |= !__builtin_isfinite(f);
-                p = __builtin_fma((double)f, (double)f, p);  // exact product
+            for (uint32_t j0 = 0; j0 < J; j0 += kB) {
+                float f[kB];
+#pragma unroll
+                for (uint32_t i = 0; i < kB; ++i)
+                    f[i] = bf16_to_f32(xr[256 * min(j0 + i, J - 1) + 64 * u + lane]);
+#pragma unroll
+                for (uint32_t i = 0; i < kB; ++i) {
+                    if (j0 + i >= J) break;
+                    bad |= !__builtin_isfinite(f[i]);
+                    p = __builtin_fma((double)f[i], (double)f[i], p);  // exact product
+                }
             }
             v = p;
         } else {
             double p0 = 0.0, p1 = 0.0;
-            for (uint32_t j = 0; j < H / 256; ++j) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(xr + 256 * j + 128 * u + 2 * lane);
-                const float f0 = lo_bf16(w), f1 = hi_bf16(w);
-                bad |= !__builtin_isfinite(f0) | !__builtin_isfinite(f1);
-                p0 = __builtin_fma((double)f0, (double)f0, p0);
-                p1 = __builtin_fma((double)f1, (double)f1, p1);
+            for (uint32_t j0 = 0; j0 < J; j0 += kB) {
+                uint32_t w[kB];
+#pragma unroll
+                for (uint32_t i = 0; i < kB; ++i)
+                    w[i] = *reinterpret_cast<const uint32_t*>(xr + 256 * min(j0 + i, J - 1) +
+                                                              128 * u + 2 * lane);
+#pragma unroll
+                for (uint32_t i = 0; i < kB; ++i) {
+                    if (j0 + i >= J) break;
+                    const float f0 = lo_bf16(w[i]), f1 = hi_bf16(w[i]);
+                    bad |= !__builtin_isfinite(f0) | !__builtin_isfinite(f1);
+                    p0 = __builtin_fma((double)f0, (double)f0, p0);
+                    p1 = __builtin_fma((double)f1, (double)f1, p1);
+                }
             }
             v = p0 + p1;
         }
@@ -199,25 +228,38 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         if (status && tid == 0) latch(status, K3X_ERR_INVALID_MXFP4);
         return false;
     }
-    for (uint32_t c = tid; c < chunks; c += kThreads) {
-        const uint32_t t = (c * 8) / H, k = (c * 8) % H;
-        const uint4 w = s_x4[c];
-        const float4 g0 = *reinterpret_cast<const float4*>(s_g + k);
-        const float4 g1 = *reinterpret_cast<const float4*>(s_g + k + 4);
-        const float inv = ns.inv[t];
-        const uint32_t in[4] = {w.x, w.y, w.z, w.w};
-        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        uint32_t o[4];
+    // xn = bf16(x * inv * gamma) in place: thread per 8-element column chunk,
+    // its gamma read once for all tokens, all tokens' chunks read before any
+    // is written.
+    float inv[kMaxDecodeTokens];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = f32_to_bf16(__fmul_rn(__fmul_rn(lo_bf16(in[q]), inv), g[2 * q]));
-            const uint32_t hi =
-                f32_to_bf16(__fmul_rn(__fmul_rn(hi_bf16(in[q]), inv), g[2 * q + 1]));
-            o[q] = lo | (hi << 16);
+    for (uint32_t t2 = 0; t2 < (uint32_t)kMaxDecodeTokens; ++t2) inv[t2] = t2 < T ? ns.inv[t2] : 0.f;
+    const uint32_t rc = H / 8;  // chunks per row
+    for (uint32_t k8 = tid; k8 < rc; k8 += kThreads) {
+        const float4 g0 = *reinterpret_cast<const float4*>(s_g + 8 * k8);
+        const float4 g1 = *reinterpret_cast<const float4*>(s_g + 8 * k8 + 4);
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        uint4 w[kMaxDecodeTokens];
+#pragma unroll
+        for (uint32_t t2 = 0; t2 < (uint32_t)kMaxDecodeTokens; ++t2)
+            if (t2 < T) w[t2] = s_x4[t2 * rc + k8];
+#pragma unroll
+        for (uint32_t t2 = 0; t2 < (uint32_t)kMaxDecodeTokens; ++t2) {
+            if (t2 >= T) break;
+            const uint32_t in[4] = {w[t2].x, w[t2].y, w[t2].z, w[t2].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t lo =
+                    f32_to_bf16(__fmul_rn(__fmul_rn(lo_bf16(in[q]), inv[t2]), g[2 * q]));
+                const uint32_t hi =
+                    f32_to_bf16(__fmul_rn(__fmul_rn(hi_bf16(in[q]), inv[t2]), g[2 * q + 1]));
+                o[q] = lo | (hi << 16);
+            }
+            const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
+            s_x4[t2 * rc + k8] = ov;
+            if (xn_out) reinterpret_cast<uint4*>(xn_out)[t2 * rc + k8] = ov;
         }
-        const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
-        s_x4[c] = ov;
-        if (xn_out) reinterpret_cast<uint4*>(xn_out)[c] = ov;
     }
     __syncthreads();
     return true;
@@ -283,7 +325,7 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
                 }
     };
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, ns,
-                                 blk == 0 ? a.xn : nullptr, a.status, a.status, prefetch))
+                                 blk == 0 ? a.xn : nullptr, a.status, a.status, prefetch, [] {}))
         return;
     if (!row) return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
@@ -350,16 +392,18 @@ __device__ __forceinline__ void shared_gateup_block(const FrontArgs& a, uint32_t
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[w][j] = tiles[(((size_t)k * 2 + w) * 4 + j) * 64];
     };
-    // The weights are requested only once xn is built: requested with the
-    // x / gamma loads, the 59 MB of shared gate/up tiles would queue ahead
-    // of the router blocks' x / gamma and router rows, which are on the
-    // layer's critical path.  A non-finite x is reported by the router
-    // blocks.
-    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr,
-                                 a.status, [] {}))
-        return;
+    // The weights are requested once this block's x / gamma have arrived
+    // (and so, nearly, every block's): requested with the x / gamma loads,
+    // the 59 MB of shared gate/up tiles would queue ahead of the router
+    // blocks' x / gamma and router rows, which are on the layer's critical
+    // path.  A non-finite x is reported by the router blocks.
+    auto prefetch = [&]() {
 #pragma unroll
-    for (int d = 0; d < PD; ++d) load(bn[d], min(k0 + d, kt - 1));
+        for (int d = 0; d < PD; ++d) load(bn[d], min(k0 + d, kt - 1));
+    };
+    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr, nullptr,
+                                 a.status, [] {}, prefetch))
+        return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
     const uint16_t* xrow = s_x + (size_t)(n < T ? n : 0) * H + 32 * g;  // unused rows: row 0
     f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -937,8 +981,51 @@ struct DownArgs {
     const uint32_t* pair_token;
     const uint32_t* pair_slot;
     float* y;                  // [T][K][H] per-pair outputs
+    // Fused combine (decode_mix): router weights [T][K], shared expert
+    // output [T][H] or null, the layer output, and the arrival counters
+    // [T][H / 64] (zero between calls).
+    const float* weights;
+    const float* shared_y;
+    uint16_t* out;
+    float* out_f32;            // optional
+    uint32_t* mix;
     const uint32_t* status;
 };
+
+// out[t][h] = bf16(sum over slots s in router order of w[t][s] * y[t][s][h]
+// + shared[t][h]), float mul then float add per term
+// (runtime/src/backend_cpu.cpp:295-301, runtime/src/model.cpp:1145), for
+// the 64 columns h0 + lane of token t, by one wave.  The loads of a group of
+// 16 slots are issued together (indices clamped, so there is no branch
+// around them).
+constexpr int kCombineBatch = 16;
+
+__device__ inline void decode_mix(const float* y, const float* weights, const float* shared_y,
+                                  uint32_t K, uint32_t H, uint32_t t, uint32_t h, uint16_t* out,
+                                  float* out_f32) {
+    const float* yr = y + (size_t)t * K * H + h;
+    const float* wr = weights + (size_t)t * K;
+    const float sh = shared_y ? shared_y[(size_t)t * H + h] : 0.0f;
+    float mix = 0.0f;
+    for (uint32_t s0 = 0; s0 < K; s0 += kCombineBatch) {
+        float yv[kCombineBatch], wv[kCombineBatch];
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) {
+            const uint32_t s = min(s0 + u, K - 1);
+            // Rows of other workgroups, stored device-scope in this launch:
+            // device-scope loads (no stale cache line can answer them).
+            yv[u] = __hip_atomic_load(yr + (size_t)s * H, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            wv[u] = wr[s];
+        }
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u)
+            if (s0 + u < K) mix = __fadd_rn(mix, __fmul_rn(wv[u], yv[u]));
+    }
+    const float v = shared_y ? __fadd_rn(mix, sh) : mix;
+    out[(size_t)t * H + h] = f32_to_bf16(v);
+    if (out_f32) out_f32[(size_t)t * H + h] = v;
+}
 
 // Workgroup = kDownWaves waves of one active slot ai, wave w taking 16-row
 // block rb = (block % (H / 64)) * 4 + w.  The slot's activation rows (cnt
@@ -949,6 +1036,17 @@ struct DownArgs {
 // clamped; a clamped activation chunk is stored again with its own value),
 // so the compiler keeps them all in flight.  The rows of the slot's pairs
 // go to y.
+// Then the combine, fused: per (token, 64-column group) a counter counts the
+// workgroups that have stored their rows (one per router slot: an expert is
+// routed at most once per token).  Wave w of the workgroup whose increment
+// for the token of its row w completes the count (old value K - 1) mixes the
+// token's 64 columns in router-slot order -- the same arithmetic whichever
+// workgroup arrives last, so the result does not depend on the order -- and
+// resets the counter for the next call.  The rows of y are stored, and read
+// by the mixing wave, with device-scope atomic stores and loads, which are
+// coherent across the XCDs' L2s without any cache write-back or
+// invalidation; every store has completed before the workgroup's
+// increments.  No workgroup waits for another.
 constexpr int kDownWaves = 4;
 constexpr int kDownTiles = 16;      // K tiles of the down projection: I <= 2048
 constexpr int kDownActLoads = 4;    // 16-byte activation loads per thread
@@ -1008,49 +1106,27 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        if (4 * g + q < cnt) a.y[(size_t)yrow[q] * a.H + rb * 16 + n] = acc[q];
-}
-
-struct CombineArgs {
-    const float* y;         // [T][K][H]
-    const float* weights;   // [T][K]
-    const float* shared_y;  // [T][H] or null
-    uint32_t K, H;
-    uint16_t* out;          // [T][H] bf16
-    float* out_f32;         // optional
-    const uint32_t* status;
-};
-
-// out[t][h] = bf16(sum over slots s in router order of w[t][s] * y[t][s][h]
-// + shared[t][h]), float mul then float add per term
-// (runtime/src/backend_cpu.cpp:295-301, runtime/src/model.cpp:1145).  The
-// loads of a group of 16 slots are issued together (indices clamped, so
-// there is no branch around them).  Grid (H / 256, T).
-constexpr int kCombineBatch = 16;
-
-__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
-    if (prior_status(a.status)) return;
-    const uint32_t t = blockIdx.y, h = blockIdx.x * 256 + threadIdx.x;
-    if (h >= a.H) return;
-    const float* yr = a.y + (size_t)t * a.K * a.H + h;
-    const float* wr = a.weights + (size_t)t * a.K;
-    const float sh = a.shared_y ? a.shared_y[(size_t)t * a.H + h] : 0.0f;
-    float mix = 0.0f;
-    for (uint32_t s0 = 0; s0 < a.K; s0 += kCombineBatch) {
-        float yv[kCombineBatch], wv[kCombineBatch];
-#pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u) {
-            const uint32_t s = min(s0 + u, a.K - 1);
-            yv[u] = yr[(size_t)s * a.H];
-            wv[u] = wr[s];
+        if (4 * g + q < cnt)
+            __hip_atomic_store(a.y + (size_t)yrow[q] * a.H + rb * 16 + n, acc[q], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    // The device-scope stores above are complete (so visible to every XCD)
+    // once this wave's vector-memory counter is zero; the barrier extends
+    // that to the workgroup before any increment.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (wave < cnt) {  // wave-uniform; cnt <= T <= kDownWaves (checked on the host)
+        const uint32_t hg = blockIdx.x % per_expert, t = a.pair_token[off + wave];
+        uint32_t* ctr = a.mix + (size_t)t * per_expert + hg;
+        uint32_t old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0);
+        if (old == a.K - 1) {  // issued after the increment returned
+            decode_mix(a.y, a.weights, a.shared_y, a.K, a.H, t, hg * 64 + lane, a.out,
+                       a.out_f32);
+            if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-#pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u)
-            if (s0 + u < a.K) mix = __fadd_rn(mix, __fmul_rn(wv[u], yv[u]));
     }
-    const float v = a.shared_y ? __fadd_rn(mix, sh) : mix;
-    a.out[(size_t)t * a.H + h] = f32_to_bf16(v);
-    if (a.out_f32) a.out_f32[(size_t)t * a.H + h] = v;
 }
 
 }  // namespace
@@ -1077,7 +1153,8 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
            d.inter % 128 == 0 && d.inter <= 128 * kDownTiles &&
            d.hidden <= 128 * kGuWaves * kGuTiles &&
            (size_t)p->tokens * d.hidden / 8 <= (size_t)64 * kGuWaves * kGuActLoads &&
-           d.hidden % (16 * kDownWaves) == 0 &&
+           d.hidden % (16 * kDownWaves) == 0 && d.hidden / 64 <= kMixGroupsMax &&
+           p->tokens <= (uint32_t)kDownWaves &&  // a slot's rows: one per mixing wave
            (size_t)p->tokens * d.inter / 8 <= (size_t)64 * kDownWaves * kDownActLoads &&
            d.shared_inter % 256 == 0;
 }
@@ -1193,26 +1270,17 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.pair_token = b.pair_token;
     dn.pair_slot = b.pair_slot;
     dn.y = b.y;
+    dn.weights = b.weights;
+    dn.shared_y = S ? b.sy : nullptr;
+    dn.out = out;
+    dn.out_f32 = out_f32;
+    dn.mix = b.mix;
     dn.status = ctx->status;
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
     hipLaunchKernelGGL(decode_down_kernel, dim3(max_active * (d.hidden / (16 * kDownWaves))),
                        dim3(64 * kDownWaves), (size_t)T * d.inter * 2, main, dn);
     end_stage(ctx, mark);
-
-    CombineArgs cb{};
-    cb.y = b.y;
-    cb.weights = b.weights;
-    cb.shared_y = S ? b.sy : nullptr;
-    cb.K = K;
-    cb.H = d.hidden;
-    cb.out = out;
-    cb.out_f32 = out_f32;
-    cb.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_COMBINE);
-    hipLaunchKernelGGL(decode_combine_kernel, dim3((d.hidden + 255) / 256, T), dim3(256), 0, main,
-                       cb);
-    end_stage(ctx, mark);
-    ctx->kernel_launches += 5;
+    ctx->kernel_launches += 4;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 

@@ -6,6 +6,10 @@
 namespace k3x_hip {
 
 constexpr int kMaxDecodeTokens = 4;
+// Arrival counters of the decode down kernel's fused combine: one per
+// (token, 64-column group of H), H <= 64 * kMixGroupsMax.
+constexpr uint32_t kMixGroupsMax = 1024;
+constexpr size_t kDecodeMixBytes = (size_t)kMaxDecodeTokens * kMixGroupsMax * 4;
 
 // Whether the five-launch decode path handles this call.
 bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
@@ -14,7 +18,8 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
 // RMSNorm, routing, grouping, experts, shared expert and combine of one
 // decode call; x is the raw bf16 input [T][H].  The per-expert grouping
 // arrays (counts, offsets, first_use, active_asc, active_fu), which no decode
-// kernel reads, are written only with group_taps.  Asynchronous.
+// kernel reads, are written only with group_taps.  b.mix: kDecodeMixBytes
+// of counters, zero before the call and left zero by it.  Asynchronous.
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                    const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32,
                    bool group_taps);

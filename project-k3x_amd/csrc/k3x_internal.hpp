@@ -38,6 +38,9 @@ struct k3x_hip_ctx {
     // Device address of the fixed scratch of k3x_hip_moe_forward_noalloc on
     // this context's device (null when it could not be taken).
     void* noalloc_scratch = nullptr;
+    // Decode combine counters of k3x_hip_moe_forward (zeroed at creation,
+    // left zero by every call).
+    uint32_t* mix_counts = nullptr;
     uint64_t forward_calls = 0;
     uint64_t kernel_launches = 0;
     uint64_t weight_h2d_bytes = 0;
@@ -133,6 +136,9 @@ struct LayerBuffers {
     uint32_t* qxs;         // [T][H/128][2]
     uint16_t* qact;        // [P][I] 16-bit units
     uint32_t* qacts;       // [P][I/128][2]
+    // Decode path: arrival counters of the fused combine (kDecodeMixBytes,
+    // zero between calls); set by the entry point, not by the carve.
+    uint32_t* mix;
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }

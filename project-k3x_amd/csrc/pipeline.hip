@@ -1899,6 +1899,7 @@ int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, S
     int st = k3x_hip::ensure_scratch(ctx, need);
     if (st) return st;
     carve(static_cast<uint8_t*>(ctx->scratch), bank->desc, p->tokens, p->top_k, split, q8, s);
+    s->mix = ctx->mix_counts;
     return K3X_OK;
 }
 
@@ -2194,12 +2195,16 @@ int k3x_hip_moe_forward_noalloc(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
     if (!ctx->noalloc_scratch) return K3X_ERR_BACKEND_UNAVAILABLE;
     Scratch s;
     const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0, q8 = scaled_fp4(p);
-    if (carve(nullptr, bank->desc, p->tokens, p->top_k, split, q8, &s) >
-        K3X_HIP_NOALLOC_SCRATCH_BYTES)
+    // The fixed scratch's last kDecodeMixBytes hold the decode combine's
+    // counters (zero from load time, left zero by every call); the carve
+    // stays below them.
+    constexpr size_t kCarveMax = K3X_HIP_NOALLOC_SCRATCH_BYTES - k3x_hip::kDecodeMixBytes;
+    if (carve(nullptr, bank->desc, p->tokens, p->top_k, split, q8, &s) > kCarveMax)
         return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     carve(static_cast<uint8_t*>(ctx->noalloc_scratch), bank->desc, p->tokens, p->top_k, split,
           q8, &s);
+    s.mix = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ctx->noalloc_scratch) + kCarveMax);
     // Stage timing takes events from a pool that may have to create them:
     // not on this path.
     const bool profiling = ctx->profiling;
