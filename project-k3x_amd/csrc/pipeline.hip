@@ -660,6 +660,164 @@ __global__ __launch_bounds__(64) void topk_reg_kernel(const float* __restrict__ 
     }
 }
 
+// The same Top-K by one 256-thread workgroup per token, for few tokens (one
+// wave per token leaves the device idle while it works through K rounds of
+// wave maxima).  Thread tid owns experts tid + 256 i, i < EPT (E <= 256 EPT):
+//   keys       sigmoid + bias, the validation and the sort key of topk_wave;
+//   threshold  the maximum score half of each 16-expert group (DPP row
+//              rotates); with G groups and K <= G, the K-th largest group
+//              maximum tau has at least K keys at or above it, so no key with
+//              score half below tau is selected;
+//   survivors  the keys at or above tau (every key when K > G), compacted,
+//              ranked exactly by the full 64-bit key (keys are distinct: the
+//              low half holds the expert); rank r < K is router slot r;
+//   renorm     one wave, sequential sums in slot order, as topk_wave.
+// Same results as topk_reg_kernel, bit for bit.
+constexpr uint32_t kTopkThrThreads = 256;
+constexpr uint32_t kTopkThrMaxTokens = 256;  // tokens up to which launch_topk_any uses it
+
+template <int EPT>
+__global__ __launch_bounds__(kTopkThrThreads) void topk_thr_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, uint32_t E, uint32_t K,
+    float routed_scale, uint32_t renorm, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, uint32_t* status) {
+    constexpr uint32_t kN = kTopkThrThreads * EPT;
+    __shared__ __align__(16) uint64_t ckey[kN];  // survivors' keys, compacted, 0 past them
+    __shared__ uint32_t cid[kN];
+    __shared__ float csc[kN];
+    __shared__ __align__(16) uint32_t gmax[kN / 16];  // every group written (0 past E)
+    __shared__ uint32_t sel[64];
+    __shared__ float selsc[64];
+    __shared__ uint32_t ncand, thr, bad, prior;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool dbl = renorm == K3X_RENORM_DOUBLE;
+    constexpr uint32_t kErrExtent = K3X_ERR_INVALID_EXTENT, kErrState = K3X_ERR_INVALID_STATE;
+    float lv[EPT], bv[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const uint32_t e = min(tid + kTopkThrThreads * i, E - 1);
+        lv[i] = logits[(size_t)t * E + e];
+        bv[i] = bias[e];
+    }
+    if (tid == 0) {
+        ncand = 0;
+        bad = 0;
+        prior = *(volatile uint32_t*)status;  // one read: the block decides as one
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) ckey[tid + kTopkThrThreads * i] = 0;
+    __syncthreads();
+    if (prior) return;
+    uint64_t key[EPT];
+    float sc[EPT];
+    uint32_t err = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const uint32_t e = tid + kTopkThrThreads * i;
+        key[i] = 0;
+        sc[i] = 0.0f;
+        if (e < E) {
+            if (dbl && (!__builtin_isfinite(lv[i]) || !__builtin_isfinite(bv[i]))) err = kErrExtent;
+            const float sg = sigmoid_cr(lv[i]);
+            const float adj = __fadd_rn(sg, bv[i]);
+            if (!dbl && (!__builtin_isfinite(sg) || sg < 0.0f || sg > 1.0f ||
+                         !__builtin_isfinite(bv[i]) || !__builtin_isfinite(adj)))
+                err = kErrState;
+            sc[i] = sg;
+            key[i] = topk_key(adj, e);
+        }
+        uint32_t m = (uint32_t)(key[i] >> 32);
+        m = dpp_max_step<0x128, 0xf>(m);  // row_ror:8
+        m = dpp_max_step<0x124, 0xf>(m);  // row_ror:4
+        m = dpp_max_step<0x122, 0xf>(m);  // row_ror:2
+        m = dpp_max_step<0x121, 0xf>(m);  // row_ror:1
+        if ((lane & 15) == 0) gmax[(tid + kTopkThrThreads * i) >> 4] = m;
+    }
+    if (err) atomicMax(&bad, err);
+    __syncthreads();
+    if (bad) {
+        if (tid == 0) latch(status, bad);
+        return;
+    }
+    // tau by wave 0: the group maximum m with fewer than K larger maxima and
+    // at least K at or above it (groups past G hold 0).
+    const uint32_t G = (E + 15) / 16;
+    if (wave == 0) {
+        uint32_t th = 0;
+        if (K <= G) {
+            const uint32_t m = lane < G ? gmax[lane] : 0u;
+            uint32_t gt = 0, ge = 0;
+            const uint4* gm = reinterpret_cast<const uint4*>(gmax);
+            for (uint32_t g4 = 0; g4 < (G + 3) / 4; ++g4) {  // groups past G hold 0
+                const uint4 v = gm[g4];
+                gt += (v.x > m) + (v.y > m) + (v.z > m) + (v.w > m);
+                ge += (v.x >= m) + (v.y >= m) + (v.z >= m) + (v.w >= m);
+            }
+            const uint64_t q = __ballot(lane < G && gt < K && K <= ge);
+            if (q) th = (uint32_t)__builtin_amdgcn_readlane((int)m, (int)__builtin_ctzll(q));
+        }
+        if (lane == 0) thr = th;
+    }
+    __syncthreads();
+    const uint32_t tau = thr;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const uint32_t e = tid + kTopkThrThreads * i;
+        const bool surv = e < E && (uint32_t)(key[i] >> 32) >= tau;
+        const uint64_t m = __ballot(surv);
+        if (!m) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&ncand, (uint32_t)__popcll(m));
+        base = __builtin_amdgcn_readfirstlane(base);
+        if (surv) {
+            const uint32_t c = base + (uint32_t)__popcll(m & ((1ull << lane) - 1));
+            ckey[c] = key[i];
+            cid[c] = e;
+            csc[c] = sc[i];
+        }
+    }
+    __syncthreads();
+    const uint32_t n = ncand;
+    const ulonglong2* ck = reinterpret_cast<const ulonglong2*>(ckey);
+    for (uint32_t c = tid; c < n; c += kTopkThrThreads) {
+        const uint64_t k = ckey[c];
+        uint32_t r = 0;
+        for (uint32_t c2 = 0; c2 < n; c2 += 8) {  // zero-padded past n (kN is a multiple of 8)
+            ulonglong2 kk[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) kk[q] = ck[c2 / 2 + q];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) r += (kk[q].x > k) + (kk[q].y > k);
+        }
+        if (r < K) {
+            sel[r] = cid[c];
+            selsc[r] = csc[c];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // Renormalise in slot order (sequential sums as the reference).
+    const float v = lane < K ? selsc[lane] : 0.0f;
+    float den_f = 0.0f;
+    double den_d = 0.0;
+    for (uint32_t s2 = 0; s2 < K; ++s2) {
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s2));
+        den_f = __fadd_rn(den_f, x);
+        den_d = __dadd_rn(den_d, (double)x);
+    }
+    if (dbl ? !(__builtin_isfinite(den_d) && den_d > 0.0)
+            : !(__builtin_isfinite(den_f) && den_f > 0.0f)) {
+        if (lane == 0) latch(status, dbl ? kErrExtent : kErrState);
+        return;
+    }
+    if (lane < K) {
+        ids[(size_t)t * K + lane] = sel[lane];
+        weights[(size_t)t * K + lane] =
+            dbl ? __fmul_rn((float)__ddiv_rn((double)v, den_d), routed_scale)
+                : __fmul_rn(__fdiv_rn(v, den_f), routed_scale);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Expert-major grouping in three launches.  Produces the ascending-expert CSR
 // (counts, offsets, pair_token, pair_slot; rows of one expert in (token,
@@ -1433,6 +1591,96 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 
 // ready (may be null): the bank's admitted-slot words; a route to another
 // slot is latched as K3X_ERR_INVALID_STATE.
+// The grouping of a small route (P = T * K <= kGroupSmallPairs pairs, no
+// wide-GEMM work items) by one workgroup with the route in LDS: every output
+// is a count over the P pairs, no pass goes through global memory.  For pair
+// p = token * K + slot of expert e: rin = earlier pairs of e, below = pairs
+// of smaller experts; its CSR row is below + rin (rows of one expert in pair
+// order, as the count/scan/scatter kernels order them).  Per expert: counts,
+// offsets (pairs of smaller experts; offsets[E] = P), first_use (its first
+// pair, 0xffffffff unused).  The pair with rin = 0 places its expert in
+// active_asc (rank among the first uses of smaller experts) and active_fu
+// (rank among earlier first uses).  Validation as group_count_body: an id
+// past E, a slot that holds no admitted expert, or an expert twice in one
+// token latches K3X_ERR_INVALID_STATE.
+constexpr uint32_t kGroupSmallPairs = 256;
+
+__global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    const uint32_t* __restrict__ ready, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
+    uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
+    uint32_t* __restrict__ active_fu, uint32_t* __restrict__ pair_token,
+    uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    __shared__ __align__(16) uint32_t s_id[kGroupSmallPairs];   // 0xffffffff past P
+    __shared__ __align__(16) uint32_t s_first[kGroupSmallPairs];  // 1: pair is its expert's first use
+    __shared__ uint32_t prior;
+    const uint32_t tid = threadIdx.x, P = T * K;
+    if (tid == 0) prior = *(volatile uint32_t*)status;
+    const uint32_t e = tid < P ? ids[tid] : 0xffffffffu;
+    s_id[tid] = e;
+    __syncthreads();
+    if (prior) return;
+    const uint32_t tok = tid / K, slot = tid % K;
+    int bad = tid < P && (e >= E || (ready && !ready[e]));
+    if (tid < P)
+        for (uint32_t q = 0; q < slot; ++q) bad |= s_id[tok * K + q] == e;
+    if (__syncthreads_or(bad)) {
+        if (tid == 0) latch(status, K3X_ERR_INVALID_STATE);
+        return;
+    }
+    const uint4* id4 = reinterpret_cast<const uint4*>(s_id);
+    uint32_t rin = 0, below = 0;
+    if (tid < P) {
+        for (uint32_t q0 = 0; q0 < P; q0 += 4) {  // entries past P hold 0xffffffff
+            const uint4 v = id4[q0 / 4];
+            const uint32_t f[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                rin += q0 + i < tid && f[i] == e;
+                below += f[i] < e;
+            }
+        }
+        pair_token[below + rin] = tok;
+        pair_slot[below + rin] = slot;
+    }
+    s_first[tid] = tid < P && rin == 0;
+    __syncthreads();
+    if (tid < P && rin == 0) {
+        uint32_t asc = 0, fu = 0;
+        for (uint32_t q = 0; q < P; ++q) {
+            if (!s_first[q]) continue;
+            asc += s_id[q] < e;
+            fu += q < tid;
+        }
+        active_asc[asc] = e;
+        active_fu[fu] = e;
+    }
+    // Per expert: counts over the pairs (E * P / 256 comparisons a thread).
+    for (uint32_t x = tid; x < E; x += kGroupSmallPairs) {
+        uint32_t c = 0, b = 0, f = 0xffffffffu;
+        for (uint32_t q0 = 0; q0 < P; q0 += 4) {
+            const uint4 v = id4[q0 / 4];
+            const uint32_t g[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                c += g[i] == x;
+                b += g[i] < x;
+                if (g[i] == x) f = min(f, q0 + i);
+            }
+        }
+        counts[x] = c;
+        offsets[x] = b;
+        first_use[x] = f;
+    }
+    if (tid == 0) {
+        offsets[E] = P;
+        uint32_t na = 0;
+        for (uint32_t q = 0; q < P; ++q) na += s_first[q];
+        *n_active = na;
+    }
+}
+
 int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
                  const uint32_t* ready, uint32_t* counts, uint32_t* offsets,
                  uint32_t* pair_token, uint32_t* pair_slot, uint32_t* first_use,
@@ -1442,6 +1690,12 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
     uint32_t* chunk_cnt = reinterpret_cast<uint32_t*>(gscratch);
     uint32_t* chunk_fu = chunk_cnt + (size_t)nch * E;
     uint8_t* rank = reinterpret_cast<uint8_t*>(chunk_fu + (size_t)nch * E);
+    if (!witems && T * K <= kGroupSmallPairs) {
+        hipLaunchKernelGGL(group_small_kernel, dim3(1), dim3(kGroupSmallPairs), 0, ctx->stream,
+                           ids, T, K, E, ready, counts, offsets, first_use, n_active, active_asc,
+                           active_fu, pair_token, pair_slot, ctx->status);
+        return launched(ctx, 1);
+    }
     if (nch == 1) {
         hipLaunchKernelGGL(group_single_kernel, dim3(1), dim3(1024), (size_t)(1024 + 3 * E) * 4,
                            ctx->stream, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, counts,
@@ -1675,9 +1929,12 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         if (sst) return sst;
     }
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
+    // Work items of the wide GEMM only where it runs (without them a small
+    // route is grouped by one workgroup).
     int st = launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts, s.offsets,
                           s.pair_token, s.pair_slot, s.first_use, s.n_active, s.active_asc,
-                          s.active_fu, s.gscratch, s.witems, s.n_witems);
+                          s.active_fu, s.gscratch, wide_path ? s.witems : nullptr,
+                          wide_path ? s.n_witems : nullptr);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -1874,14 +2131,21 @@ int launch_router(k3x_hip_ctx* ctx, const float* W, const float* Wp, const uint1
     return launched(ctx, 1);
 }
 
-// Top-K of T rows of logits: the register kernel up to 1024 experts.
+// Top-K of T rows of logits: for few tokens the threshold kernel (257 to
+// 1024 experts), else the register kernel up to 1024 experts.
 int launch_topk_any(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E,
                     uint32_t K, uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids,
                     float* weights) {
 #define K3X_TOPK(kpl)                                                                          \
     hipLaunchKernelGGL(topk_reg_kernel<kpl>, dim3(T), dim3(64), 0, ctx->stream, logits, bias, E, \
                        K, routed_scale, renorm, ids, weights, ctx->status)
-    if (E <= 256) K3X_TOPK(4);
+#define K3X_TOPK_THR(ept)                                                                      \
+    hipLaunchKernelGGL(topk_thr_kernel<ept>, dim3(T), dim3(kTopkThrThreads), 0, ctx->stream,    \
+                       logits, bias, E, K, routed_scale, renorm, ids, weights, ctx->status)
+    if (T <= kTopkThrMaxTokens && E > 256 && E <= 512) K3X_TOPK_THR(2);
+    else if (T <= kTopkThrMaxTokens && E > 512 && E <= 1024) K3X_TOPK_THR(4);
+#undef K3X_TOPK_THR
+    else if (E <= 256) K3X_TOPK(4);
     else if (E <= 512) K3X_TOPK(8);
     else if (E <= 1024) K3X_TOPK(16);
 #undef K3X_TOPK

@@ -2,9 +2,10 @@
 
 * Top-K ties go to the lower expert index (runtime/src/official_moe.cpp:226-232,
   runtime/src/routing_policy.cpp:83-87), on every device Top-K: the decode
-  path's select kernel (up to 512 experts), the register Top-K of the general
-  path with 4, 8 and 16 keys per lane (up to 256, 512 and 1024 experts) and
-  the LDS Top-K past 1024 experts.  Two kinds of tie: every score equal (zero
+  path's select kernel (up to 512 experts), the general path's threshold
+  Top-K for few tokens (257 to 512 and 513 to 1024 experts), its register
+  Top-K with 4, 8 and 16 keys per lane (up to 256, 512 and 1024 experts; more
+  than 256 tokens past 256 experts) and the LDS Top-K past 1024 experts.  Two kinds of tie: every score equal (zero
   input, equal bias: ids 0..K-1, weights routed_scale / K), and planted groups
   of duplicated router rows with equal bias, within one lane and across
   lanes, straddling the K boundary (the lower ids are selected, in order).
@@ -82,8 +83,10 @@ def route_taps(k3x_amd, ctx, cfg, bank, x_bits, flags):
 TOPK_CASES = {
     "decode_select_e384": (2, 384, False),
     "reg4_e200": (3, 200, True),
-    "reg8_e384": (2, 384, True),
-    "reg16_e1000": (2, 1000, True),
+    "thr2_e384": (2, 384, True),
+    "thr4_e1000": (2, 1000, True),
+    "reg8_e384": (300, 384, True),
+    "reg16_e1000": (300, 1000, True),
     "lds_e1100": (2, 1100, True),
 }
 
