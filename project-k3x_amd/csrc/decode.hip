@@ -78,6 +78,20 @@ __device__ inline f32x4 mxfp4_tile(const uint4& c, float scale, const uint4 av[4
     return acc;
 }
 
+// The same tile against split activations hi + lo (each weight fragment
+// dequantised once, two MFMAs).
+__device__ inline f32x4 mxfp4_tile2(const uint4& c, float scale, const uint4 ah[4],
+                                    const uint4 al[4], f32x4 acc) {
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bf16x8 b = dequant8(cw[j], scale);
+        acc = mfma16x16x32(as_bf16x8(ah[j]), b, acc);
+        acc = mfma16x16x32(as_bf16x8(al[j]), b, acc);
+    }
+    return acc;
+}
+
 // Activation slice for K tile k, loaded only by the lanes whose MFMA row is
 // used: row m of an MFMA result depends only on row m of A, and unused rows
 // are never stored, so the other lanes' registers may hold anything.  Issued
@@ -863,7 +877,9 @@ struct GateUpArgs {
     const uint16_t* xn;        // [T][H]
     const uint32_t* n_active;
     const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
-    uint16_t* act;             // [pairs][I] bf16, CSR row order
+    uint16_t* act;             // [pairs][act_stride] bf16, CSR row order
+    uint32_t act_stride;       // elements per act row
+    uint32_t act_lo;           // element offset of the lo halves (split activations), 0: none
     GluParams glu;
     const uint32_t* status;
 };
@@ -880,13 +896,19 @@ constexpr int kGuWaves = 8;
 constexpr int kGuTiles = 8;       // K tiles per wave: H <= 128 * 8 * 8
 constexpr int kGuActLoads = 7;    // 16-byte xn loads per thread: T * H / 8 <= 7 * 512
 
+// RB > 1: the workgroup takes RB consecutive 16-row blocks, each over
+// kGuWaves / RB waves (the xn rows in LDS serve them all; for short K ranges,
+// where a one-block unit's fixed cost would dominate).
+template <int RB>
 __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs a) {
     extern __shared__ uint4 s_x4[];  // [cnt][H] bf16
     __shared__ f32x4 red[kGuWaves][2][64];
+    constexpr uint32_t kWpr = kGuWaves / RB;  // waves per row block
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t per_expert = a.I / 16;
-    const uint32_t ai = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
+    const uint32_t per_expert = a.I / (16 * RB);
+    const uint32_t ai = blockIdx.x / per_expert;
+    const uint32_t rb = (blockIdx.x % per_expert) * RB + wave / kWpr, wv = wave % kWpr;
     // Status, active count and this slot's record in one round trip (the
     // record of an inactive slot is not used).
     const uint32_t st = prior_status(a.status);
@@ -907,7 +929,7 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
     }
     // 2. This wave's K tiles [k0, k1) of the gate and up blocks, and the
     //    scale dwords of the (at most three) groups they touch.
-    const uint32_t k0 = wave * kt / kGuWaves, k1 = (wave + 1) * kt / kGuWaves;
+    const uint32_t k0 = wv * kt / kWpr, k1 = (wv + 1) * kt / kWpr;
     const uint32_t N = k1 - k0;
     const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
     const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
@@ -948,20 +970,25 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
     red[wave][0][lane] = acc[0];
     red[wave][1][lane] = acc[1];
 #pragma unroll
-    for (uint32_t h = kGuWaves / 2; h >= 1; h /= 2) {
+    for (uint32_t h = kWpr / 2; h >= 1; h /= 2) {
         __syncthreads();
-        if (wave < h) {
+        if (wv < h) {
             red[wave][0][lane] = red[wave][0][lane] + red[wave + h][0][lane];
             red[wave][1][lane] = red[wave][1][lane] + red[wave + h][1][lane];
         }
     }
-    if (wave != 0) return;
-    const f32x4 gs = red[0][0][lane], us = red[0][1][lane];
+    if (wv != 0) return;
+    const f32x4 gs = red[wave][0][lane], us = red[wave][1][lane];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = 4 * g + i;
-        if (row < cnt)
-            a.act[(size_t)(rec.z + row) * a.I + rb * 16 + n] = f32_to_bf16(glu(gs[i], us[i], a.glu));
+        if (row < cnt) {
+            const float v = glu(gs[i], us[i], a.glu);
+            uint16_t* dst = a.act + (size_t)(rec.z + row) * a.act_stride + rb * 16 + n;
+            const uint16_t hi = f32_to_bf16(v);
+            *dst = hi;
+            if (a.act_lo) dst[a.act_lo] = act_lo_bf16(v, hi);
+        }
     }
 }
 
@@ -975,7 +1002,8 @@ struct DownArgs {
     size_t scales_per_expert;
     uint32_t kt, ks;           // I/128, scale groups
     uint32_t I, H, K;
-    const uint16_t* act;       // [pairs][I] CSR order
+    const uint16_t* act;       // [pairs][a_stride] CSR order (SPLIT: [hi | lo], lo at I)
+    uint32_t a_stride;
     const uint32_t* n_active;
     const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
     const uint32_t* pair_token;
@@ -983,7 +1011,8 @@ struct DownArgs {
     float* y;                  // [T][K][H] per-pair outputs
     // Fused combine (decode_mix): router weights [T][K], shared expert
     // output [T][H] or null, the layer output, and the arrival counters
-    // [T][H / 64] (zero between calls).
+    // [T][H / 64] (zero between calls).  mix null: y only (the general
+    // path's combine follows).
     const float* weights;
     const float* shared_y;
     uint16_t* out;
@@ -1048,9 +1077,13 @@ __device__ inline void decode_mix(const float* y, const float* weights, const fl
 // invalidation; every store has completed before the workgroup's
 // increments.  No workgroup waits for another.
 constexpr int kDownWaves = 4;
-constexpr int kDownTiles = 16;      // K tiles of the down projection: I <= 2048
-constexpr int kDownActLoads = 4;    // 16-byte activation loads per thread
+// TILES: K tiles of the down projection held in registers (I <= 128 TILES);
+// ACT: 16-byte activation loads per thread (cnt * a_stride / 8 <= 256 ACT);
+// SPLIT: activation rows [hi | lo], two MFMAs per weight fragment.
+constexpr int kDownTilesDecode = 16, kDownActDecode = 4;  // the decode path: I <= 2048
+constexpr int kDownTilesFew = 24, kDownActFew = 12;       // general path: I <= 3072, split
 
+template <int TILES, int ACT, bool SPLIT>
 __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
     extern __shared__ uint4 s_act4[];  // [cnt][I] bf16
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -1064,22 +1097,22 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     if (st || ai >= na) return;
     const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
     const uint32_t kt = a.kt;
-    // 1. Activation rows: chunks c < cnt * I / 8 (at most kDownActLoads per
+    // 1. Activation rows: chunks c < cnt * a_stride / 8 (at most ACT per
     //    thread, checked by the host).
-    const uint32_t chunks = cnt * (a.I / 8);
-    const uint4* src = reinterpret_cast<const uint4*>(a.act + (size_t)off * a.I);
-    uint4 v[kDownActLoads];
+    const uint32_t chunks = cnt * (a.a_stride / 8);
+    const uint4* src = reinterpret_cast<const uint4*>(a.act + (size_t)off * a.a_stride);
+    uint4 v[ACT];
 #pragma unroll
-    for (int i = 0; i < kDownActLoads; ++i) v[i] = src[min(tid + 64 * kDownWaves * i, chunks - 1)];
+    for (int i = 0; i < ACT; ++i) v[i] = src[min(tid + 64 * kDownWaves * i, chunks - 1)];
     // 2. Code tiles and scale dwords of this wave's 16-row block.
     const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
     const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
-    uint4 c[kDownTiles];
-    uint32_t sw[kDownTiles / 4];
+    uint4 c[TILES];
+    uint32_t sw[TILES / 4];
 #pragma unroll
-    for (int i = 0; i < kDownTiles; ++i) c[i] = codes[(size_t)min((uint32_t)i, kt - 1) * 64];
+    for (int i = 0; i < TILES; ++i) c[i] = codes[(size_t)min((uint32_t)i, kt - 1) * 64];
 #pragma unroll
-    for (int i = 0; i < kDownTiles / 4; ++i) sw[i] = scales[(size_t)min((uint32_t)i, a.ks - 1) * 64];
+    for (int i = 0; i < TILES / 4; ++i) sw[i] = scales[(size_t)min((uint32_t)i, a.ks - 1) * 64];
     // 3. Pair rows of the outputs (needed at the end).
     uint32_t yrow[4];
 #pragma unroll
@@ -1088,20 +1121,29 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
         yrow[q] = a.pair_token[r] * a.K + a.pair_slot[r];
     }
 #pragma unroll
-    for (int i = 0; i < kDownActLoads; ++i) s_act4[min(tid + 64 * kDownWaves * i, chunks - 1)] = v[i];
+    for (int i = 0; i < ACT; ++i) s_act4[min(tid + 64 * kDownWaves * i, chunks - 1)] = v[i];
     __syncthreads();
     const uint16_t* s_act = reinterpret_cast<const uint16_t*>(s_act4);
-    const uint16_t* arow = s_act + (size_t)(n < cnt ? n : 0) * a.I + 32 * g;  // unused rows: row 0
+    const uint16_t* arow =
+        s_act + (size_t)(n < cnt ? n : 0) * a.a_stride + 32 * g;  // unused rows: row 0
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kDownTiles; ++i) {
+    for (int i = 0; i < TILES; ++i) {
         if ((uint32_t)i < kt) {
             uint4 av[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 av[j] = *reinterpret_cast<const uint4*>(arow + (size_t)i * 128 + 8 * j);
             const float sc = e8m0_to_f32((sw[i / 4] >> (8 * (i & 3))) & 0xffu);
-            acc = mxfp4_tile(c[i], sc, av, acc);
+            if constexpr (SPLIT) {
+                uint4 al[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    al[j] = *reinterpret_cast<const uint4*>(arow + a.I + (size_t)i * 128 + 8 * j);
+                acc = mxfp4_tile2(c[i], sc, av, al, acc);
+            } else {
+                acc = mxfp4_tile(c[i], sc, av, acc);
+            }
         }
     }
 #pragma unroll
@@ -1114,7 +1156,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     // that to the workgroup before any increment.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (wave < cnt) {  // wave-uniform; cnt <= T <= kDownWaves (checked on the host)
+    if (a.mix && wave < cnt) {  // wave-uniform; cnt <= T <= kDownWaves (checked on the host)
         const uint32_t hg = blockIdx.x % per_expert, t = a.pair_token[off + wave];
         uint32_t* ctr = a.mix + (size_t)t * per_expert + hg;
         uint32_t old = 0;
@@ -1150,12 +1192,12 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
     return p->tokens <= (uint32_t)kMaxDecodeTokens && lds <= ctx->max_lds_per_block &&
            d.hidden % 256 == 0 && d.experts <= (uint32_t)(kKeysPerLane * 64) &&
            p->top_k <= 64 && p->tokens * p->top_k <= (uint32_t)kMaxDecodePairs &&
-           d.inter % 128 == 0 && d.inter <= 128 * kDownTiles &&
+           d.inter % 128 == 0 && d.inter <= 128 * kDownTilesDecode &&
            d.hidden <= 128 * kGuWaves * kGuTiles &&
            (size_t)p->tokens * d.hidden / 8 <= (size_t)64 * kGuWaves * kGuActLoads &&
            d.hidden % (16 * kDownWaves) == 0 && d.hidden / 64 <= kMixGroupsMax &&
            p->tokens <= (uint32_t)kDownWaves &&  // a slot's rows: one per mixing wave
-           (size_t)p->tokens * d.inter / 8 <= (size_t)64 * kDownWaves * kDownActLoads &&
+           (size_t)p->tokens * d.inter / 8 <= (size_t)64 * kDownWaves * kDownActDecode &&
            d.shared_inter % 256 == 0;
 }
 
@@ -1246,11 +1288,13 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.n_active = b.n_active;
     gu.arec = b.arec;
     gu.act = b.act;
+    gu.act_stride = d.inter;
+    gu.act_lo = 0;
     gu.glu = glu;
     gu.status = ctx->status;
     const uint32_t gu_blocks = max_active * (d.inter / 16);
     mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
-    hipLaunchKernelGGL(decode_gateup_kernel, dim3(gu_blocks), dim3(64 * kGuWaves),
+    hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(gu_blocks), dim3(64 * kGuWaves),
                        (size_t)T * d.hidden * 2, main, gu);
     end_stage(ctx, mark);
 
@@ -1265,6 +1309,7 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.H = d.hidden;
     dn.K = K;
     dn.act = b.act;
+    dn.a_stride = d.inter;
     dn.n_active = b.n_active;
     dn.arec = b.arec;
     dn.pair_token = b.pair_token;
@@ -1277,10 +1322,93 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.mix = b.mix;
     dn.status = ctx->status;
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
-    hipLaunchKernelGGL(decode_down_kernel, dim3(max_active * (d.hidden / (16 * kDownWaves))),
-                       dim3(64 * kDownWaves), (size_t)T * d.inter * 2, main, dn);
+    hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false>),
+                       dim3(max_active * (d.hidden / (16 * kDownWaves))), dim3(64 * kDownWaves),
+                       (size_t)T * d.inter * 2, main, dn);
     end_stage(ctx, mark);
     ctx->kernel_launches += 4;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+bool few_row_experts_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T,
+                              bool split) {
+    const auto& d = bank->desc;
+    const uint32_t a_stride = split ? 2 * d.inter : d.inter;
+    return T <= (uint32_t)kMaxDecodeTokens && d.hidden % 256 == 0 &&
+           d.hidden <= 128 * kGuWaves * kGuTiles &&
+           (size_t)T * d.hidden / 8 <= (size_t)64 * kGuWaves * kGuActLoads &&
+           (size_t)T * d.hidden * 2 <= ctx->max_lds_per_block && d.inter % 128 == 0 &&
+           d.inter <= 128 * kDownTilesFew && d.hidden % (16 * kDownWaves) == 0 &&
+           (size_t)T * a_stride / 8 <= (size_t)64 * kDownWaves * kDownActFew &&
+           (size_t)T * a_stride * 2 <= ctx->max_lds_per_block;
+}
+
+int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
+                           const LayerBuffers& b, const uint16_t* xn, const GluParams& glu,
+                           bool split) {
+    const auto& d = bank->desc;
+    GateUpArgs gu{};
+    gu.gu_codes = reinterpret_cast<const uint4*>(bank->gu_codes);
+    gu.gu_scales = bank->gu_scales;
+    gu.codes_per_expert = bank->gu_codes_per_expert / 16;
+    gu.scales_per_expert = bank->gu_scales_per_expert;
+    gu.kt = bank->gate.kt;
+    gu.ks = bank->gate.ks;
+    gu.I = d.inter;
+    gu.H = d.hidden;
+    gu.xn = xn;
+    gu.n_active = b.n_active;
+    gu.arec = b.arec;
+    gu.act = b.act;
+    gu.act_stride = split ? 2 * d.inter : d.inter;
+    gu.act_lo = split ? d.inter : 0;
+    gu.glu = glu;
+    gu.status = ctx->status;
+    const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
+    // Two row blocks a workgroup when each one's K range fits half the waves.
+    const bool two = gu.kt <= (uint32_t)(kGuWaves / 2 * kGuTiles) && (d.inter / 16) % 2 == 0;
+    if (two)
+        hipLaunchKernelGGL(decode_gateup_kernel<2>, dim3(max_active * (d.inter / 32)),
+                           dim3(64 * kGuWaves), (size_t)T * d.hidden * 2, ctx->stream, gu);
+    else
+        hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(max_active * (d.inter / 16)),
+                           dim3(64 * kGuWaves), (size_t)T * d.hidden * 2, ctx->stream, gu);
+    ctx->kernel_launches += 1;
+    return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
+}
+
+int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
+                        const LayerBuffers& b, bool split) {
+    const auto& d = bank->desc;
+    DownArgs dn{};
+    dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
+    dn.dn_scales = bank->dn_scales;
+    dn.codes_per_expert = bank->dn_codes_per_expert / 16;
+    dn.scales_per_expert = bank->dn_scales_per_expert;
+    dn.kt = bank->down.kt;
+    dn.ks = bank->down.ks;
+    dn.I = d.inter;
+    dn.H = d.hidden;
+    dn.K = K;
+    dn.act = b.act;
+    dn.a_stride = split ? 2 * d.inter : d.inter;
+    dn.n_active = b.n_active;
+    dn.arec = b.arec;
+    dn.pair_token = b.pair_token;
+    dn.pair_slot = b.pair_slot;
+    dn.y = b.y;
+    dn.mix = nullptr;  // the general path's combine follows
+    dn.status = ctx->status;
+    const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
+    const dim3 grid(max_active * (d.hidden / (16 * kDownWaves)));
+    const size_t lds = (size_t)T * dn.a_stride * 2;
+    if (split)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true>), grid,
+                           dim3(64 * kDownWaves), lds, ctx->stream, dn);
+    else
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, false>), grid,
+                           dim3(64 * kDownWaves), lds, ctx->stream, dn);
+    ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 

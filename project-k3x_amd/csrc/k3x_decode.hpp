@@ -1,6 +1,7 @@
 // k3x_decode.hpp -- the decode path (T <= kMaxDecodeTokens) of the layer.
 #pragma once
 
+#include "k3x_device.hpp"
 #include "k3x_internal.hpp"
 
 namespace k3x_hip {
@@ -23,6 +24,19 @@ bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
 int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                    const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32,
                    bool group_taps);
+
+// The routed experts of a general-path call with few tokens (T <=
+// kMaxDecodeTokens) on the decode path's gate/up and down kernels: b.arec
+// holds the active slots' records (the small-route grouping writes them),
+// act rows [P][I] or, split, [P][2 I] as [hi | lo]; y receives the per-pair
+// rows.  Whether the bank's shapes fit those kernels:
+bool few_row_experts_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T,
+                              bool split);
+int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
+                           const LayerBuffers& b, const uint16_t* xn,
+                           const k3x_dev::GluParams& glu, bool split);
+int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
+                        const LayerBuffers& b, bool split);
 
 // out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
 // + shared[t][h]) on the context stream (the combine of both paths).

@@ -1602,7 +1602,9 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 // active_asc (rank among the first uses of smaller experts) and active_fu
 // (rank among earlier first uses).  Validation as group_count_body: an id
 // past E, a slot that holds no admitted expert, or an expert twice in one
-// token latches K3X_ERR_INVALID_STATE.
+// token latches K3X_ERR_INVALID_STATE.  arec (T <= 4): the active slot
+// records of the decode kernels, {expert, rows, CSR offset, tokens of the
+// rows (8 bits each)}, in active_asc order.
 constexpr uint32_t kGroupSmallPairs = 256;
 
 __global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
@@ -1611,7 +1613,7 @@ __global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
     uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
     uint32_t* __restrict__ active_fu, uint32_t* __restrict__ pair_token,
-    uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    uint32_t* __restrict__ pair_slot, uint4* __restrict__ arec, uint32_t* status) {
     __shared__ __align__(16) uint32_t s_id[kGroupSmallPairs];   // 0xffffffff past P
     __shared__ __align__(16) uint32_t s_first[kGroupSmallPairs];  // 1: pair is its expert's first use
     __shared__ uint32_t prior;
@@ -1647,14 +1649,19 @@ __global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
     s_first[tid] = tid < P && rin == 0;
     __syncthreads();
     if (tid < P && rin == 0) {
-        uint32_t asc = 0, fu = 0;
+        uint32_t asc = 0, fu = 0, rows = 0, toks = 0;
         for (uint32_t q = 0; q < P; ++q) {
+            if (s_id[q] == e) {  // the expert's rows in pair order (at most one per token)
+                if (rows < 4) toks |= (q / K) << (8 * rows);
+                ++rows;
+            }
             if (!s_first[q]) continue;
             asc += s_id[q] < e;
             fu += q < tid;
         }
         active_asc[asc] = e;
         active_fu[fu] = e;
+        if (arec) arec[asc] = make_uint4(e, rows, below, toks);
     }
     // Per expert: counts over the pairs (E * P / 256 comparisons a thread).
     for (uint32_t x = tid; x < E; x += kGroupSmallPairs) {
@@ -1685,7 +1692,8 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
                  const uint32_t* ready, uint32_t* counts, uint32_t* offsets,
                  uint32_t* pair_token, uint32_t* pair_slot, uint32_t* first_use,
                  uint32_t* n_active, uint32_t* active_asc, uint32_t* active_fu,
-                 uint8_t* gscratch, uint32_t* witems = nullptr, uint32_t* n_witems = nullptr) {
+                 uint8_t* gscratch, uint32_t* witems = nullptr, uint32_t* n_witems = nullptr,
+                 uint4* arec = nullptr) {
     const uint32_t tps = std::min(64u, 1024u / K), nch = (T + tps - 1) / tps;
     uint32_t* chunk_cnt = reinterpret_cast<uint32_t*>(gscratch);
     uint32_t* chunk_fu = chunk_cnt + (size_t)nch * E;
@@ -1693,7 +1701,8 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
     if (!witems && T * K <= kGroupSmallPairs) {
         hipLaunchKernelGGL(group_small_kernel, dim3(1), dim3(kGroupSmallPairs), 0, ctx->stream,
                            ids, T, K, E, ready, counts, offsets, first_use, n_active, active_asc,
-                           active_fu, pair_token, pair_slot, ctx->status);
+                           active_fu, pair_token, pair_slot, T <= 4 ? arec : nullptr,
+                           ctx->status);
         return launched(ctx, 1);
     }
     if (nch == 1) {
@@ -1931,10 +1940,14 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     // Work items of the wide GEMM only where it runs (without them a small
     // route is grouped by one workgroup).
+    // Few tokens: the routed experts on the decode path's kernels, fed by
+    // the active-slot records of the small-route grouping.
+    const bool few = !wide_path && !split_in && T * K <= kGroupSmallPairs &&
+                     k3x_hip::few_row_experts_eligible(ctx, bank, T, split);
     int st = launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts, s.offsets,
                           s.pair_token, s.pair_slot, s.first_use, s.n_active, s.active_asc,
                           s.active_fu, s.gscratch, wide_path ? s.witems : nullptr,
-                          wide_path ? s.n_witems : nullptr);
+                          wide_path ? s.n_witems : nullptr, few ? s.arec : nullptr);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -1972,8 +1985,13 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.act_stride = split ? 2 * d.inter : d.inter;
     g.act_lo = split ? d.inter : 0;
     mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
-    if (wide) launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
-    else launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
+    if (few) {
+        if ((st = k3x_hip::launch_few_row_gate_up(ctx, bank, T, K, s, xn, glu, split))) return st;
+    } else if (wide) {
+        launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
+    } else {
+        launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
+    }
     end_stage(ctx, mark);
     // Shared gate/up + GLU (single block of T rows).
     if (d.shared_inter) {
@@ -2011,8 +2029,13 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.y_stride = d.hidden;
     dn.scatter = 1;
     mark = begin_stage(ctx, K3X_STAGE_DOWN);
-    if (wide) launch_gemm<true, false, 4, 2>(ctx, dn, max_active, d.hidden);
-    else launch_gemm<true, false, 1, 2>(ctx, dn, max_active, d.hidden);
+    if (few) {
+        if ((st = k3x_hip::launch_few_row_down(ctx, bank, T, K, s, split))) return st;
+    } else if (wide) {
+        launch_gemm<true, false, 4, 2>(ctx, dn, max_active, d.hidden);
+    } else {
+        launch_gemm<true, false, 1, 2>(ctx, dn, max_active, d.hidden);
+    }
     end_stage(ctx, mark);
     if (d.shared_inter) {
         GemmArgs sd = dn;
@@ -2033,7 +2056,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden);
         end_stage(ctx, mark);
     }
-    if ((st = launched(ctx, d.shared_inter ? 4 : 2))) return st;
+    if ((st = launched(ctx, (few ? 0 : 2) + (d.shared_inter ? 2 : 0)))) return st;
     return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
                                    d.hidden, T, out, out_f32,
                                        (p->flags & K3X_FLAG_ROUND_EXPERT_OUT) != 0);
