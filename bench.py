@@ -47,7 +47,7 @@ CALIB_BYTES = 256 << 20   # plain device copy used to scale the PMC byte counter
 # Bench stage -> kernel it times (for the PMC traffic of the dominant stage).
 STAGE_KERNEL = {"decode_front": "decode_front_kernel", "decode_select": "decode_select_kernel",
                 "decode_gate_up": "decode_gateup_kernel", "decode_down": "decode_down_kernel",
-                "combine": "decode_combine_kernel", "gate_up": "expert_gemm",
+                "combine": "combine_kernel", "gate_up": "expert_gemm",
                 "down": "expert_gemm"}
 SCALE_LO, SCALE_HI = 119, 123
 
