@@ -12,7 +12,7 @@ constexpr int kMaxDecodeTokens = 4;
 constexpr uint32_t kMixGroupsMax = 1024;
 constexpr size_t kDecodeMixBytes = (size_t)kMaxDecodeTokens * kMixGroupsMax * 4;
 
-// Whether the five-launch decode path handles this call.
+// Whether the four-launch decode path handles this call.
 bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
                      const k3x_hip_moe_params* p, const void* x);
 

@@ -16,8 +16,8 @@ Standards:
   hidden and route -- the tolerance the reference's own checks hold this
   layer to (official_mxfp4_moe_ffn parity) -- and within 2^-7 in relative
   error norm (the differences are roundings: fp32 MFMA projections against
-  double sums, and the activation rounded to bf16 before each down
-  projection where the reference keeps it in fp32);
+  double sums; the fp32 GLU activations reach the down projections as bf16
+  hi + lo rows, within 2^-16 of the reference's fp32 values);
 * a host-given route gives the same output as the same route found on the
   device; missing uploads and bad arguments are rejected.
 """
@@ -214,8 +214,8 @@ def verify_ffn(oracle, ow, correction, experts, got, hid_f, prefix, K, tokens, r
                     f"{ref['routed'][i]:.6g} shared gpu {got['shared'][t][i]:.6g} ref "
                     f"{ref['shared'][i]:.6g}")
         assert ok.all(), f"token {t} out: {int((~ok).sum())} elements beyond atol = rtol = {TOL}"
-        # Bulk: the differences are rounding-sized (the activation is bf16 on
-        # the MFMA path), far below the tolerance.
+        # Bulk: the differences are rounding-sized (fp32 MFMA sums against
+        # double sums, the activation as bf16 hi + lo), far below the tolerance.
         num += float(np.sum((of.astype(np.float64) - ref["out"]) ** 2))
         den += float(np.sum(ref["out"].astype(np.float64) ** 2))
         d = ulps_bf16(o[t], ref_bits)
