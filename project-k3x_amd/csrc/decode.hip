@@ -877,6 +877,7 @@ struct GateUpArgs {
     const uint16_t* xn;        // [T][H]
     const uint32_t* n_active;
     const uint4* arec;         // per active slot {expert, rows, offset, row tokens}
+    const uint32_t* pair_token;  // ROWS kernels: token of each CSR row
     uint16_t* act;             // [pairs][act_stride] bf16, CSR row order
     uint32_t act_stride;       // elements per act row
     uint32_t act_lo;           // element offset of the lo halves (split activations), 0: none
@@ -895,13 +896,37 @@ struct GateUpArgs {
 constexpr int kGuWaves = 8;
 constexpr int kGuTiles = 8;       // K tiles per wave: H <= 128 * 8 * 8
 constexpr int kGuActLoads = 7;    // 16-byte xn loads per thread: T * H / 8 <= 7 * 512
+// Rows of a slot in LDS at once (ROWS kernels: chunks of this many rows).
+constexpr uint32_t kRowChunk = kMaxDecodeTokens;
+
+// v[i] = src[min(tid + step i, chunks - 1)], and the matching store into
+// LDS (chunks of rows staged by a workgroup; clamped indices keep every load
+// unconditional).  Native vectors: the compiler keeps them in registers
+// across the row-chunk loop, where copies of uint4 went to the stack.
+template <int N>
+__device__ __forceinline__ void load_chunks(u32x4 (&v)[N], const void* src, uint32_t tid,
+                                            uint32_t step, uint32_t chunks) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] = reinterpret_cast<const u32x4*>(src)[min(tid + step * i, chunks - 1)];
+}
+template <int N>
+__device__ __forceinline__ void store_chunks(const u32x4 (&v)[N], void* dst, uint32_t tid,
+                                             uint32_t step, uint32_t chunks) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) reinterpret_cast<u32x4*>(dst)[min(tid + step * i, chunks - 1)] = v[i];
+}
 
 // RB > 1: the workgroup takes RB consecutive 16-row blocks, each over
 // kGuWaves / RB waves (the xn rows in LDS serve them all; for short K ranges,
 // where a one-block unit's fixed cost would dominate).
-template <int RB>
+// ROWS: a slot of any number of rows (the general path's verification
+// windows): its rows pass through LDS kRowChunk at a time, tokens read from
+// pair_token, while the wave's code tiles and scales stay in registers, so
+// the weights stream once per slot.
+template <int RB, bool ROWS = false>
 __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs a) {
-    extern __shared__ uint4 s_x4[];  // [cnt][H] bf16
+    extern __shared__ uint4 s_x4[];  // [rows][H] bf16
     __shared__ f32x4 red[kGuWaves][2][64];
     constexpr uint32_t kWpr = kGuWaves / RB;  // waves per row block
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -917,16 +942,30 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
     if (st || ai >= na) return;
     const uint32_t e = rec.x, cnt = rec.y, toks = rec.w;
     const uint32_t H = a.H, kt = a.kt;
-    // 1. xn rows of the slot's tokens (cnt <= 4 rows): chunk c of row r.
-    const uint32_t rowc = H / 8, chunks = cnt * rowc;
-    uint4 v[kGuActLoads];
+    // 1. xn rows [m0, m0 + rows) of the slot (rows <= kRowChunk): chunk c of
+    //    row r.
+    const uint32_t rowc = H / 8;
+    u32x4 v[kGuActLoads];
+    auto load_rows = [&](uint32_t m0, uint32_t rows) __attribute__((always_inline)) {
+        // Tokens of the rows, 8 bits each (ROWS: T <= kChunkedMaxTokens).
+        uint32_t tk = toks;
+        if constexpr (ROWS) {
+            tk = 0;
 #pragma unroll
-    for (int i = 0; i < kGuActLoads; ++i) {
-        const uint32_t c = min(tid + 64 * kGuWaves * i, chunks - 1);
-        const uint32_t r = (c >= rowc) + (c >= 2 * rowc) + (c >= 3 * rowc);
-        const uint32_t tok = (toks >> (8 * r)) & 0xffu;
-        v[i] = reinterpret_cast<const uint4*>(a.xn + (size_t)tok * H)[c - r * rowc];
-    }
+            for (uint32_t r = 0; r < kRowChunk; ++r)
+                tk |= a.pair_token[rec.z + m0 + min(r, rows - 1)] << (8 * r);
+        }
+        const uint32_t chunks = rows * rowc;
+#pragma unroll
+        for (int i = 0; i < kGuActLoads; ++i) {
+            const uint32_t c = min(tid + 64 * kGuWaves * i, chunks - 1);
+            const uint32_t r = (c >= rowc) + (c >= 2 * rowc) + (c >= 3 * rowc);
+            const uint32_t tok = (tk >> (8 * r)) & 0xffu;
+            v[i] = reinterpret_cast<const u32x4*>(a.xn + (size_t)tok * H)[c - r * rowc];
+        }
+    };
+    uint32_t rows = ROWS ? min(cnt, kRowChunk) : cnt;
+    load_rows(0, rows);
     // 2. This wave's K tiles [k0, k1) of the gate and up blocks, and the
     //    scale dwords of the (at most three) groups they touch.
     const uint32_t k0 = wv * kt / kWpr, k1 = (wv + 1) * kt / kWpr;
@@ -947,48 +986,80 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
         s0[i] = scales[grp * 128];
         s1[i] = scales[grp * 128 + 64];
     }
-#pragma unroll
-    for (int i = 0; i < kGuActLoads; ++i) s_x4[min(tid + 64 * kGuWaves * i, chunks - 1)] = v[i];
+    store_chunks(v, s_x4, tid, 64 * kGuWaves, rows * rowc);
     __syncthreads();
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(s_x4);
-    const uint16_t* xrow = s_x + (size_t)(n < cnt ? n : 0) * H + 32 * g;  // unused rows: row 0
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    for (uint32_t m0 = 0;;) {
+        if constexpr (ROWS) {
+            // The code tiles and scale dwords, as opaque values each pass:
+            // their dequantised forms are not kept across passes (the
+            // register file would not hold them).
 #pragma unroll
-    for (int i = 0; i < kGuTiles; ++i) {
-        if ((uint32_t)i < N) {
-            const uint32_t k = k0 + i, gi = (k >> 2) - (k0 >> 2), sh = 8 * (k & 3);
-            const uint32_t w0 = gi == 0 ? s0[0] : gi == 1 ? s0[1] : s0[2];
-            const uint32_t w1 = gi == 0 ? s1[0] : gi == 1 ? s1[1] : s1[2];
-            uint4 av[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                av[j] = *reinterpret_cast<const uint4*>(xrow + (size_t)k * 128 + 8 * j);
-            acc[0] = mxfp4_tile(c0[i], e8m0_to_f32((w0 >> sh) & 0xffu), av, acc[0]);
-            acc[1] = mxfp4_tile(c1[i], e8m0_to_f32((w1 >> sh) & 0xffu), av, acc[1]);
+            for (int i = 0; i < kGuTiles; ++i)
+                asm volatile("" : "+v"(c0[i].x), "+v"(c0[i].y), "+v"(c0[i].z), "+v"(c0[i].w),
+                                  "+v"(c1[i].x), "+v"(c1[i].y), "+v"(c1[i].z), "+v"(c1[i].w));
+            asm volatile("" : "+v"(s0[0]), "+v"(s0[1]), "+v"(s0[2]), "+v"(s1[0]), "+v"(s1[1]),
+                              "+v"(s1[2]));
         }
-    }
-    red[wave][0][lane] = acc[0];
-    red[wave][1][lane] = acc[1];
+        const uint16_t* xrow = s_x + (size_t)(n < rows ? n : 0) * H + 32 * g;  // unused rows: row 0
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (uint32_t h = kWpr / 2; h >= 1; h /= 2) {
+        for (int i = 0; i < kGuTiles; ++i) {
+            if ((uint32_t)i < N) {
+                const uint32_t k = k0 + i, gi = (k >> 2) - (k0 >> 2), sh = 8 * (k & 3);
+                const uint32_t w0 = gi == 0 ? s0[0] : gi == 1 ? s0[1] : s0[2];
+                const uint32_t w1 = gi == 0 ? s1[0] : gi == 1 ? s1[1] : s1[2];
+                uint4 av[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    av[j] = *reinterpret_cast<const uint4*>(xrow + (size_t)k * 128 + 8 * j);
+                acc[0] = mxfp4_tile(c0[i], e8m0_to_f32((w0 >> sh) & 0xffu), av, acc[0]);
+                acc[1] = mxfp4_tile(c1[i], e8m0_to_f32((w1 >> sh) & 0xffu), av, acc[1]);
+            }
+        }
+        red[wave][0][lane] = acc[0];
+        red[wave][1][lane] = acc[1];
+#pragma unroll
+        for (uint32_t h = kWpr / 2; h >= 1; h /= 2) {
+            __syncthreads();
+            if (wv < h) {
+                red[wave][0][lane] = red[wave][0][lane] + red[wave + h][0][lane];
+                red[wave][1][lane] = red[wave][1][lane] + red[wave + h][1][lane];
+            }
+        }
+        if (!ROWS && wv != 0) return;
+        if (wv == 0) {
+            const f32x4 gs = red[wave][0][lane], us = red[wave][1][lane];
+            auto out = [&](int i) __attribute__((always_inline)) {
+                const uint32_t row = 4 * g + i;
+                if (row < rows) {
+                    const float v = glu(gs[i], us[i], a.glu);
+                    uint16_t* dst =
+                        a.act + (size_t)(rec.z + m0 + row) * a.act_stride + rb * 16 + n;
+                    const uint16_t hi = f32_to_bf16(v);
+                    *dst = hi;
+                    if (a.act_lo) dst[a.act_lo] = act_lo_bf16(v, hi);
+                }
+            };
+            if constexpr (ROWS) {
+                // One row at a time: the held weight registers leave no room
+                // for four GLUs in flight.
+#pragma unroll 1
+                for (int i = 0; i < 4; ++i) out(i);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) out(i);
+            }
+        }
+        if (!ROWS) return;
+        m0 += rows;
+        if (m0 >= cnt) return;  // block-uniform
+        // The next rows, once every wave is past its reads of s_x and red.
+        rows = min(cnt - m0, kRowChunk);
+        load_rows(m0, rows);
         __syncthreads();
-        if (wv < h) {
-            red[wave][0][lane] = red[wave][0][lane] + red[wave + h][0][lane];
-            red[wave][1][lane] = red[wave][1][lane] + red[wave + h][1][lane];
-        }
-    }
-    if (wv != 0) return;
-    const f32x4 gs = red[wave][0][lane], us = red[wave][1][lane];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = 4 * g + i;
-        if (row < cnt) {
-            const float v = glu(gs[i], us[i], a.glu);
-            uint16_t* dst = a.act + (size_t)(rec.z + row) * a.act_stride + rb * 16 + n;
-            const uint16_t hi = f32_to_bf16(v);
-            *dst = hi;
-            if (a.act_lo) dst[a.act_lo] = act_lo_bf16(v, hi);
-        }
+        store_chunks(v, s_x4, tid, 64 * kGuWaves, rows * rowc);
+        __syncthreads();
     }
 }
 
@@ -1083,9 +1154,9 @@ constexpr int kDownWaves = 4;
 constexpr int kDownTilesDecode = 16, kDownActDecode = 4;  // the decode path: I <= 2048
 constexpr int kDownTilesFew = 24, kDownActFew = 12;       // general path: I <= 3072, split
 
-template <int TILES, int ACT, bool SPLIT>
+template <int TILES, int ACT, bool SPLIT, bool ROWS = false>
 __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
-    extern __shared__ uint4 s_act4[];  // [cnt][I] bf16
+    extern __shared__ uint4 s_act4[];  // [rows][a_stride] bf16
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t per_expert = a.H / (16 * kDownWaves);
@@ -1097,14 +1168,27 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     if (st || ai >= na) return;
     const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
     const uint32_t kt = a.kt;
-    // 1. Activation rows: chunks c < cnt * a_stride / 8 (at most ACT per
-    //    thread, checked by the host).
-    const uint32_t chunks = cnt * (a.a_stride / 8);
-    const uint4* src = reinterpret_cast<const uint4*>(a.act + (size_t)off * a.a_stride);
-    uint4 v[ACT];
-#pragma unroll
-    for (int i = 0; i < ACT; ++i) v[i] = src[min(tid + 64 * kDownWaves * i, chunks - 1)];
-    // 2. Code tiles and scale dwords of this wave's 16-row block.
+    // 1. Activation rows [m0, m0 + rows) of the slot, contiguous in CSR
+    //    order: chunks c < rows * a_stride / 8 (at most ACT per thread,
+    //    checked by the host).  ROWS: kRowChunk rows at a time.
+    u32x4 v[ACT];
+#define K3X_DOWN_LOAD_ROWS(m0, rows)                                                           \
+    load_chunks(v, a.act + (size_t)(off + (m0)) * a.a_stride, tid, 64 * kDownWaves,            \
+                (rows) * (a.a_stride / 8))
+#define K3X_DOWN_STORE_ROWS(rows) store_chunks(v, s_act4, tid, 64 * kDownWaves, (rows) * (a.a_stride / 8))
+    // Pair rows of the outputs (needed at the end).
+    uint32_t yrow[4];
+#define K3X_DOWN_LOAD_YROWS(m0, rows)                                                          \
+    {                                                                                          \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                        \
+            const uint32_t r_ = off + (m0) + min(4 * g + q, (rows) - 1);                       \
+            yrow[q] = a.pair_token[r_] * a.K + a.pair_slot[r_];                                \
+        }                                                                                      \
+    }
+    uint32_t rows = ROWS ? min(cnt, kRowChunk) : cnt;
+    K3X_DOWN_LOAD_ROWS(0, rows);
+    // 2. Code tiles and scale dwords of this wave's 16-row block, then the
+    //    pair rows.
     const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
     const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
     uint4 c[TILES];
@@ -1113,44 +1197,52 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     for (int i = 0; i < TILES; ++i) c[i] = codes[(size_t)min((uint32_t)i, kt - 1) * 64];
 #pragma unroll
     for (int i = 0; i < TILES / 4; ++i) sw[i] = scales[(size_t)min((uint32_t)i, a.ks - 1) * 64];
-    // 3. Pair rows of the outputs (needed at the end).
-    uint32_t yrow[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t r = off + min(4 * g + q, cnt - 1);
-        yrow[q] = a.pair_token[r] * a.K + a.pair_slot[r];
-    }
-#pragma unroll
-    for (int i = 0; i < ACT; ++i) s_act4[min(tid + 64 * kDownWaves * i, chunks - 1)] = v[i];
+    K3X_DOWN_LOAD_YROWS(0, rows);
+    K3X_DOWN_STORE_ROWS(rows);
     __syncthreads();
     const uint16_t* s_act = reinterpret_cast<const uint16_t*>(s_act4);
-    const uint16_t* arow =
-        s_act + (size_t)(n < cnt ? n : 0) * a.a_stride + 32 * g;  // unused rows: row 0
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t m0 = 0;;) {
+        const uint16_t* arow =
+            s_act + (size_t)(n < rows ? n : 0) * a.a_stride + 32 * g;  // unused rows: row 0
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < TILES; ++i) {
-        if ((uint32_t)i < kt) {
-            uint4 av[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                av[j] = *reinterpret_cast<const uint4*>(arow + (size_t)i * 128 + 8 * j);
-            const float sc = e8m0_to_f32((sw[i / 4] >> (8 * (i & 3))) & 0xffu);
-            if constexpr (SPLIT) {
-                uint4 al[4];
+        for (int i = 0; i < TILES; ++i) {
+            if ((uint32_t)i < kt) {
+                uint4 av[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    al[j] = *reinterpret_cast<const uint4*>(arow + a.I + (size_t)i * 128 + 8 * j);
-                acc = mxfp4_tile2(c[i], sc, av, al, acc);
-            } else {
-                acc = mxfp4_tile(c[i], sc, av, acc);
+                    av[j] = *reinterpret_cast<const uint4*>(arow + (size_t)i * 128 + 8 * j);
+                const float sc = e8m0_to_f32((sw[i / 4] >> (8 * (i & 3))) & 0xffu);
+                if constexpr (SPLIT) {
+                    uint4 al[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        al[j] = *reinterpret_cast<const uint4*>(arow + a.I + (size_t)i * 128 + 8 * j);
+                    acc = mxfp4_tile2(c[i], sc, av, al, acc);
+                } else {
+                    acc = mxfp4_tile(c[i], sc, av, acc);
+                }
             }
         }
-    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        if (4 * g + q < cnt)
-            __hip_atomic_store(a.y + (size_t)yrow[q] * a.H + rb * 16 + n, acc[q], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = 0; q < 4; ++q)
+            if (4 * g + q < rows)
+                __hip_atomic_store(a.y + (size_t)yrow[q] * a.H + rb * 16 + n, acc[q],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!ROWS) break;
+        m0 += rows;
+        if (m0 >= cnt) return;  // block-uniform; no mix (checked on the host)
+        // The next rows, once every wave is past its reads of s_act.
+        rows = min(cnt - m0, kRowChunk);
+        K3X_DOWN_LOAD_ROWS(m0, rows);
+        K3X_DOWN_LOAD_YROWS(m0, rows);
+        __syncthreads();
+        K3X_DOWN_STORE_ROWS(rows);
+        __syncthreads();
+    }
+#undef K3X_DOWN_LOAD_ROWS
+#undef K3X_DOWN_STORE_ROWS
+#undef K3X_DOWN_LOAD_YROWS
     // The device-scope stores above are complete (so visible to every XCD)
     // once this wave's vector-memory counter is zero; the barrier extends
     // that to the workgroup before any increment.
@@ -1345,7 +1437,7 @@ bool few_row_experts_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, 
 
 int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
                            const LayerBuffers& b, const uint16_t* xn, const GluParams& glu,
-                           bool split) {
+                           bool split, bool chunked) {
     const auto& d = bank->desc;
     GateUpArgs gu{};
     gu.gu_codes = reinterpret_cast<const uint4*>(bank->gu_codes);
@@ -1359,26 +1451,31 @@ int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t 
     gu.xn = xn;
     gu.n_active = b.n_active;
     gu.arec = b.arec;
+    gu.pair_token = b.pair_token;
     gu.act = b.act;
     gu.act_stride = split ? 2 * d.inter : d.inter;
     gu.act_lo = split ? d.inter : 0;
     gu.glu = glu;
     gu.status = ctx->status;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
+    const size_t lds = (size_t)(chunked ? kRowChunk : T) * d.hidden * 2;
     // Two row blocks a workgroup when each one's K range fits half the waves.
     const bool two = gu.kt <= (uint32_t)(kGuWaves / 2 * kGuTiles) && (d.inter / 16) % 2 == 0;
-    if (two)
-        hipLaunchKernelGGL(decode_gateup_kernel<2>, dim3(max_active * (d.inter / 32)),
-                           dim3(64 * kGuWaves), (size_t)T * d.hidden * 2, ctx->stream, gu);
+    const dim3 grid(max_active * (d.inter / (two ? 32 : 16))), block(64 * kGuWaves);
+    if (two && chunked)
+        hipLaunchKernelGGL((decode_gateup_kernel<2, true>), grid, block, lds, ctx->stream, gu);
+    else if (two)
+        hipLaunchKernelGGL((decode_gateup_kernel<2, false>), grid, block, lds, ctx->stream, gu);
+    else if (chunked)
+        hipLaunchKernelGGL((decode_gateup_kernel<1, true>), grid, block, lds, ctx->stream, gu);
     else
-        hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(max_active * (d.inter / 16)),
-                           dim3(64 * kGuWaves), (size_t)T * d.hidden * 2, ctx->stream, gu);
+        hipLaunchKernelGGL((decode_gateup_kernel<1, false>), grid, block, lds, ctx->stream, gu);
     ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 
 int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
-                        const LayerBuffers& b, bool split) {
+                        const LayerBuffers& b, bool split, bool chunked) {
     const auto& d = bank->desc;
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
@@ -1400,14 +1497,31 @@ int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, 
     dn.mix = nullptr;  // the general path's combine follows
     dn.status = ctx->status;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
-    const dim3 grid(max_active * (d.hidden / (16 * kDownWaves)));
-    const size_t lds = (size_t)T * dn.a_stride * 2;
-    if (split)
-        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true>), grid,
-                           dim3(64 * kDownWaves), lds, ctx->stream, dn);
+    const uint32_t rows = chunked ? kRowChunk : T;
+    const dim3 grid(max_active * (d.hidden / (16 * kDownWaves))), block(64 * kDownWaves);
+    const size_t lds = (size_t)rows * dn.a_stride * 2;
+    // The decode kernel's shape (16 tiles, 4 activation loads a thread)
+    // where it holds the rows: fewer registers than the 24-tile one.
+    const bool small = !split && d.inter <= 128u * kDownTilesDecode &&
+                       (size_t)rows * dn.a_stride / 8 <= (size_t)64 * kDownWaves * kDownActDecode;
+    if (small && chunked)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false, true>),
+                           grid, block, lds, ctx->stream, dn);
+    else if (small)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false, false>),
+                           grid, block, lds, ctx->stream, dn);
+    else if (split && chunked)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true, true>), grid,
+                           block, lds, ctx->stream, dn);
+    else if (split)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true, false>), grid,
+                           block, lds, ctx->stream, dn);
+    else if (chunked)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, false, true>), grid,
+                           block, lds, ctx->stream, dn);
     else
-        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, false>), grid,
-                           dim3(64 * kDownWaves), lds, ctx->stream, dn);
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, false, false>), grid,
+                           block, lds, ctx->stream, dn);
     ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }

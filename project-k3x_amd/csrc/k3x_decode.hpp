@@ -25,18 +25,23 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
                    const LayerBuffers& b, const uint16_t* x, uint16_t* out, float* out_f32,
                    bool group_taps);
 
-// The routed experts of a general-path call with few tokens (T <=
-// kMaxDecodeTokens) on the decode path's gate/up and down kernels: b.arec
-// holds the active slots' records (the small-route grouping writes them),
-// act rows [P][I] or, split, [P][2 I] as [hi | lo]; y receives the per-pair
-// rows.  Whether the bank's shapes fit those kernels:
+// The routed experts of a general-path call on the decode path's gate/up
+// and down kernels: b.arec holds the active slots' records {expert, rows, CSR
+// offset, tokens} (the grouping writes them), act rows [P][I] or, split,
+// [P][2 I] as [hi | lo]; y receives the per-pair rows.  Few tokens (T <=
+// kMaxDecodeTokens): a slot's rows at once, tokens from the record.
+// chunked: slots of any size (T <= kChunkedMaxTokens), their rows through LDS
+// kMaxDecodeTokens at a time with the weights held in registers, tokens from
+// b.pair_token.  Whether the bank's shapes fit those kernels (T: the rows in
+// LDS at once):
+constexpr uint32_t kChunkedMaxTokens = 64;
 bool few_row_experts_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T,
                               bool split);
 int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
                            const LayerBuffers& b, const uint16_t* xn,
-                           const k3x_dev::GluParams& glu, bool split);
+                           const k3x_dev::GluParams& glu, bool split, bool chunked = false);
 int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
-                        const LayerBuffers& b, bool split);
+                        const LayerBuffers& b, bool split, bool chunked = false);
 
 // out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
 // + shared[t][h]) on the context stream (the combine of both paths).

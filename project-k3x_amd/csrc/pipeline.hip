@@ -934,7 +934,8 @@ __device__ inline bool group_scan_body(
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
     uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
     uint32_t* __restrict__ active_fu, uint32_t* __restrict__ witems,
-    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint32_t* status) {
+    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint4* __restrict__ arec,
+    uint32_t* status) {
     extern __shared__ uint32_t smem[];
     uint32_t* s_cnt = smem;          // [E]
     uint32_t* s_fu = s_cnt + E;      // [E]
@@ -991,6 +992,7 @@ __device__ inline bool group_scan_body(
         if (c) {
             active_asc[act] = e;
             s_alist[act] = e;
+            if (arec) arec[act] = make_uint4(e, c, row, 0u);
         }
         pre += c | (uint64_t)((c + chunk_rows - 1) / chunk_rows) << kScanItemShift |
                (uint64_t)(c != 0) << kScanActiveShift;
@@ -1063,9 +1065,10 @@ __global__ __launch_bounds__(1024) void group_scan_kernel(
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
     uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
     uint32_t* __restrict__ active_fu, uint32_t* __restrict__ witems,
-    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint32_t* status) {
+    uint32_t* __restrict__ n_witems, uint32_t chunk_rows, uint4* __restrict__ arec,
+    uint32_t* status) {
     (void)group_scan_body(T, K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active,
-                          active_asc, active_fu, witems, n_witems, chunk_rows, status);
+                          active_asc, active_fu, witems, n_witems, chunk_rows, arec, status);
 }
 
 __device__ inline void group_scatter_body(uint32_t c, 
@@ -1102,11 +1105,12 @@ __global__ __launch_bounds__(1024) void group_single_kernel(
     uint32_t* __restrict__ first_use, uint32_t* __restrict__ n_active,
     uint32_t* __restrict__ active_asc, uint32_t* __restrict__ active_fu,
     uint32_t* __restrict__ witems, uint32_t* __restrict__ n_witems, uint32_t chunk_rows,
-    uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot, uint32_t* status) {
+    uint4* __restrict__ arec, uint32_t* __restrict__ pair_token, uint32_t* __restrict__ pair_slot,
+    uint32_t* status) {
     if (!group_count_body(0, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, status)) return;
     __syncthreads();
     if (!group_scan_body(T, K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active,
-                         active_asc, active_fu, witems, n_witems, chunk_rows, status))
+                         active_asc, active_fu, witems, n_witems, chunk_rows, arec, status))
         return;
     __syncthreads();
     group_scatter_body(0, ids, T, K, E, chunk_cnt, rank, offsets, pair_token, pair_slot, status);
@@ -1602,8 +1606,8 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 // active_asc (rank among the first uses of smaller experts) and active_fu
 // (rank among earlier first uses).  Validation as group_count_body: an id
 // past E, a slot that holds no admitted expert, or an expert twice in one
-// token latches K3X_ERR_INVALID_STATE.  arec (T <= 4): the active slot
-// records of the decode kernels, {expert, rows, CSR offset, tokens of the
+// token latches K3X_ERR_INVALID_STATE.  arec: the active slot records of
+// the decode kernels, {expert, rows, CSR offset, tokens of the first four
 // rows (8 bits each)}, in active_asc order.
 constexpr uint32_t kGroupSmallPairs = 256;
 
@@ -1701,8 +1705,7 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
     if (!witems && T * K <= kGroupSmallPairs) {
         hipLaunchKernelGGL(group_small_kernel, dim3(1), dim3(kGroupSmallPairs), 0, ctx->stream,
                            ids, T, K, E, ready, counts, offsets, first_use, n_active, active_asc,
-                           active_fu, pair_token, pair_slot, T <= 4 ? arec : nullptr,
-                           ctx->status);
+                           active_fu, pair_token, pair_slot, arec, ctx->status);
         return launched(ctx, 1);
     }
     if (nch == 1) {
@@ -1710,29 +1713,74 @@ int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, 
                            ctx->stream, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, counts,
                            offsets,
                            first_use, n_active, active_asc, active_fu, witems, n_witems,
-                           k3x_hip::kWideRows, pair_token, pair_slot, ctx->status);
+                           k3x_hip::kWideRows, arec, pair_token, pair_slot, ctx->status);
         return launched(ctx, 1);
     }
     hipLaunchKernelGGL(group_count_kernel, dim3(nch), dim3(1024), (size_t)(1024 + 3 * E) * 4,
                        ctx->stream, ids, T, K, E, ready, chunk_cnt, chunk_fu, rank, ctx->status);
     hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(1024), (size_t)3 * E * 4, ctx->stream, T,
                        K, E, chunk_cnt, chunk_fu, counts, offsets, first_use, n_active, active_asc,
-                       active_fu, witems, n_witems, k3x_hip::kWideRows, ctx->status);
+                       active_fu, witems, n_witems, k3x_hip::kWideRows, arec, ctx->status);
     hipLaunchKernelGGL(group_scatter_kernel, dim3(nch), dim3(1024), 0, ctx->stream, ids, T, K, E,
                        chunk_cnt, rank, offsets, pair_token, pair_slot, ctx->status);
     return launched(ctx, 3);
 }
 
 template <bool FP4, bool GATEUP, int MT, int NT>
-void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32_t rows) {
+void launch_gemm(k3x_hip_ctx* ctx, GemmArgs& g, uint32_t experts_in_grid, uint32_t rows,
+                 hipStream_t stream = nullptr) {
     g.blocks_per_expert = rows / 16 / (4 * NT);
     const dim3 grid(experts_in_grid * g.blocks_per_expert);
+    if (!stream) stream = ctx->stream;
     if (g.a_lo)
-        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, true>), grid, dim3(256), 0,
-                           ctx->stream, g);
+        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, true>), grid, dim3(256), 0, stream,
+                           g);
     else
-        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, false>), grid, dim3(256), 0,
-                           ctx->stream, g);
+        hipLaunchKernelGGL((expert_gemm<FP4, GATEUP, MT, NT, false>), grid, dim3(256), 0, stream,
+                           g);
+}
+
+// The shared expert below the wide GEMM's row counts: gate/up + GLU -> sact,
+// down -> sy, each as one block of T rows on the narrow GEMM, on `stream`
+// (stage marks only on the context stream).
+int run_shared_narrow(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                      const Scratch& s, const uint16_t* xn, const GluParams& glu, bool split_in,
+                      hipStream_t stream) {
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens;
+    const bool wide = T > 16;  // more than one 16-row MFMA tile
+    const bool marks = stream == ctx->stream;
+    GemmArgs sg{};
+    sg.status = ctx->status;
+    sg.glu = glu;
+    sg.top_k = p->top_k;
+    sg.codes = bank->sh_gu;
+    sg.kt = bank->sgate.kt;
+    sg.a = xn;
+    sg.a_stride = split_in ? 2 * d.hidden : d.hidden;
+    sg.a_lo = split_in ? d.hidden : 0;
+    sg.tokens = T;
+    sg.act = s.sact;
+    sg.act_stride = d.shared_inter;
+    sg.act_lo = 0;  // the bank's shared expert keeps bf16 activations
+    int mark = marks ? begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP) : -1;
+    if (wide) launch_gemm<false, true, 4, 1>(ctx, sg, 1, d.shared_inter, stream);
+    else launch_gemm<false, true, 1, 1>(ctx, sg, 1, d.shared_inter, stream);
+    if (marks) end_stage(ctx, mark);
+    GemmArgs sd = sg;
+    sd.codes = bank->sh_dn;
+    sd.kt = bank->sdown.kt;
+    sd.a = s.sact;
+    sd.a_stride = d.shared_inter;
+    sd.a_lo = 0;
+    sd.y = s.sy;
+    sd.y_stride = d.hidden;
+    sd.scatter = 0;
+    mark = marks ? begin_stage(ctx, K3X_STAGE_SHARED_DOWN) : -1;
+    if (wide) launch_gemm<false, false, 4, 2>(ctx, sd, 1, d.hidden, stream);
+    else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden, stream);
+    if (marks) end_stage(ctx, mark);
+    return launched(ctx, 2);
 }
 
 // Many rows per expert: the wide grouped GEMM (128-row chunks, activations
@@ -1911,7 +1959,15 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     // halves.
     const bool split_in = (p->flags & K3X_FLAG_SPLIT_INPUT) != 0;
     const bool wide_path = !split_in && use_wide_gemm(d, T, K, split);
-    const bool side = wide_path && d.shared_inter && !ctx->profiling && ctx->side_stream;
+    // Verification windows on the decode kernels (below): the routed experts
+    // stream for hundreds of microseconds, the shared expert's narrow GEMMs
+    // run a few dozen workgroups; on the side stream they overlap.
+    const bool chunked_rows = !wide_path && !split_in && T > k3x_hip::kMaxDecodeTokens &&
+                              T <= k3x_hip::kChunkedMaxTokens &&
+                              k3x_hip::few_row_experts_eligible(ctx, bank,
+                                                                k3x_hip::kMaxDecodeTokens, split);
+    const bool side = (wide_path || chunked_rows) && d.shared_inter && !ctx->profiling &&
+                      ctx->side_stream;
     struct Join {
         k3x_hip_ctx* ctx;
         bool armed = false;
@@ -1928,7 +1984,10 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         if (hipEventRecord(ctx->fork_ev, ctx->stream) != hipSuccess ||
             hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0) != hipSuccess)
             return K3X_ERR_BACKEND_UNAVAILABLE;
-        const int sst = run_shared_wide(ctx, bank, p, s, xn, glu, ctx->side_stream);
+        const int sst = wide_path
+                            ? run_shared_wide(ctx, bank, p, s, xn, glu, ctx->side_stream)
+                            : run_shared_narrow(ctx, bank, p, s, xn, glu, split_in,
+                                                ctx->side_stream);
         if (hipEventRecord(ctx->join_ev, ctx->side_stream) != hipSuccess) {
             // Without the event, order the streams the blunt way.
             (void)hipStreamSynchronize(ctx->side_stream);
@@ -1942,12 +2001,15 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     // route is grouped by one workgroup).
     // Few tokens: the routed experts on the decode path's kernels, fed by
     // the active-slot records of the small-route grouping.
+    // Up to kChunkedMaxTokens tokens (verification windows): the same
+    // kernels over slots of any size, rows through LDS a few at a time.
     const bool few = !wide_path && !split_in && T * K <= kGroupSmallPairs &&
                      k3x_hip::few_row_experts_eligible(ctx, bank, T, split);
+    const bool chunked = !few && chunked_rows;
     int st = launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts, s.offsets,
                           s.pair_token, s.pair_slot, s.first_use, s.n_active, s.active_asc,
                           s.active_fu, s.gscratch, wide_path ? s.witems : nullptr,
-                          wide_path ? s.n_witems : nullptr, few ? s.arec : nullptr);
+                          wide_path ? s.n_witems : nullptr, few || chunked ? s.arec : nullptr);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -1985,34 +2047,15 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     g.act_stride = split ? 2 * d.inter : d.inter;
     g.act_lo = split ? d.inter : 0;
     mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
-    if (few) {
-        if ((st = k3x_hip::launch_few_row_gate_up(ctx, bank, T, K, s, xn, glu, split))) return st;
+    if (few || chunked) {
+        if ((st = k3x_hip::launch_few_row_gate_up(ctx, bank, T, K, s, xn, glu, split, chunked)))
+            return st;
     } else if (wide) {
         launch_gemm<true, true, 4, 1>(ctx, g, max_active, d.inter);
     } else {
         launch_gemm<true, true, 1, 1>(ctx, g, max_active, d.inter);
     }
     end_stage(ctx, mark);
-    // Shared gate/up + GLU (single block of T rows).
-    if (d.shared_inter) {
-        GemmArgs sg = g;
-        sg.codes = bank->sh_gu;
-        sg.scales = nullptr;
-        sg.codes_per_expert = 0;
-        sg.kt = bank->sgate.kt;
-        sg.a_lo = split_in ? d.hidden : 0;
-        sg.gather = 0;
-        sg.n_active = nullptr;
-        sg.active = nullptr;
-        sg.tokens = T;
-        sg.act = s.sact;
-        sg.act_stride = d.shared_inter;
-        sg.act_lo = 0;  // the bank's shared expert keeps bf16 activations
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_GATE_UP);
-        if (wide) launch_gemm<false, true, 4, 1>(ctx, sg, 1, d.shared_inter);
-        else launch_gemm<false, true, 1, 1>(ctx, sg, 1, d.shared_inter);
-        end_stage(ctx, mark);
-    }
     // Routed down, scattered to [token][slot].
     GemmArgs dn = g;
     dn.codes = bank->dn_codes;
@@ -2029,34 +2072,19 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.y_stride = d.hidden;
     dn.scatter = 1;
     mark = begin_stage(ctx, K3X_STAGE_DOWN);
-    if (few) {
-        if ((st = k3x_hip::launch_few_row_down(ctx, bank, T, K, s, split))) return st;
+    if (few || chunked) {
+        if ((st = k3x_hip::launch_few_row_down(ctx, bank, T, K, s, split, chunked))) return st;
     } else if (wide) {
         launch_gemm<true, false, 4, 2>(ctx, dn, max_active, d.hidden);
     } else {
         launch_gemm<true, false, 1, 2>(ctx, dn, max_active, d.hidden);
     }
     end_stage(ctx, mark);
-    if (d.shared_inter) {
-        GemmArgs sd = dn;
-        sd.codes = bank->sh_dn;
-        sd.scales = nullptr;
-        sd.codes_per_expert = 0;
-        sd.kt = bank->sdown.kt;
-        sd.a_lo = 0;
-        sd.a = s.sact;
-        sd.a_stride = d.shared_inter;
-        sd.n_active = nullptr;
-        sd.active = nullptr;
-        sd.tokens = T;
-        sd.y = s.sy;
-        sd.scatter = 0;
-        mark = begin_stage(ctx, K3X_STAGE_SHARED_DOWN);
-        if (wide) launch_gemm<false, false, 4, 2>(ctx, sd, 1, d.hidden);
-        else launch_gemm<false, false, 1, 2>(ctx, sd, 1, d.hidden);
-        end_stage(ctx, mark);
-    }
-    if ((st = launched(ctx, (few ? 0 : 2) + (d.shared_inter ? 2 : 0)))) return st;
+    if ((st = launched(ctx, few || chunked ? 0 : 2))) return st;
+    if (d.shared_inter && !side &&
+        (st = run_shared_narrow(ctx, bank, p, s, xn, glu, split_in, ctx->stream)))
+        return st;
+    if ((st = joiner.join())) return st;
     return k3x_hip::launch_combine(ctx, s.y, weights, d.shared_inter ? s.sy : nullptr, K,
                                    d.hidden, T, out, out_f32,
                                        (p->flags & K3X_FLAG_ROUND_EXPERT_OUT) != 0);

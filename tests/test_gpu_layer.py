@@ -572,6 +572,39 @@ def test_c4_verification_window(hip, oracle, parity_report):
     bank.close()
 
 
+# Verification windows between the decode path and the wide GEMM (4 < T <=
+# 64): the routed experts run on the decode gate/up and down kernels with a
+# slot's rows staged through LDS four at a time.  Cases: few rows per expert
+# (T=9); Zipf-skewed slots of many rows, most not a multiple of four (T=40);
+# I=3072, whose down projection holds 24 code tiles (T=64, 16 experts).
+WINDOWS = {
+    "t9": dict(tokens=9, hidden=1024, inter=512, experts=64, top_k=8, shared_inter=256),
+    "t40_skew": dict(tokens=40, hidden=2048, inter=1024, experts=32, top_k=4, shared_inter=0,
+                     zipf_b0=0.45),
+    "t64_i3072": dict(tokens=64, hidden=1024, inter=3072, experts=16, top_k=4,
+                      shared_inter=512),
+}
+
+
+@pytest.mark.parametrize("name", list(WINDOWS))
+def test_verification_window_rows(hip, oracle, name, parity_report):
+    from synth import Config, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = Config(f"window_{name}", scale_lo=120, scale_hi=124, routed_scale=2.5,
+                 **WINDOWS[name])
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg, layer)
+    got = run_layer(k3x_amd, ctx, cfg, bank, layer.x_bits())
+    counts = got["counts"]
+    say(f"window {name}: T={cfg.tokens} rows per expert max {counts.max()}, "
+        f"active {int((counts > 0).sum())}, slots over four rows "
+        f"{int((counts > 4).sum())}, not a multiple of four {int((counts % 4 != 0).sum())}")
+    if name != "t9":
+        assert (counts > 4).any() and (counts[counts > 4] % 4 != 0).any()
+    check_layer(oracle, layer, got, report=parity_report)
+    bank.close()
+
+
 def test_c5_prefill_chunk(hip, oracle, parity_report):
     """Config 5: T=2048 prefill chunk.  Device Top-16 ids equal the ids the
     reference's CPU functions chose (golden fixture); grouping bit-exact;
