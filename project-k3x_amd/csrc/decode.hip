@@ -149,6 +149,12 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
     // Every block of the launch reads the same x and gamma: each starts at
     // its own offset so that they do not all request the same lines at once.
     const uint32_t rot = (blockIdx.x * 613u) % all;
+    // Slot c of the rotated order (c < all, rot < all): one compare and
+    // subtract, not a division.
+    auto rotated = [&](uint32_t c) {
+        c += rot;
+        return c >= all ? c - all : c;
+    };
     for (uint32_t c0 = 0; c0 < all; c0 += kLoads * kThreads) {
         // One unconditional load and store per slot (slots past the end
         // copy the last chunk again, the same value to the same place): no
@@ -156,7 +162,7 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         uint4 v[kLoads];
 #pragma unroll
         for (int it = 0; it < kLoads; ++it) {
-            const uint32_t c = (min(c0 + tid + kThreads * it, all - 1) + rot) % all;
+            const uint32_t c = rotated(min(c0 + tid + kThreads * it, all - 1));
             const uint4* src = c < chunks ? reinterpret_cast<const uint4*>(x) + c
                                           : reinterpret_cast<const uint4*>(gamma) + (c - chunks);
             v[it] = *src;
@@ -167,7 +173,7 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
         }
 #pragma unroll
         for (int it = 0; it < kLoads; ++it)
-            s_x4[(min(c0 + tid + kThreads * it, all - 1) + rot) % all] = v[it];
+            s_x4[rotated(min(c0 + tid + kThreads * it, all - 1))] = v[it];
     }
     // x and gamma have arrived (this wave's, and the block's after the
     // barrier): late() may now request what the block needs after xn.
@@ -263,13 +269,9 @@ __device__ __forceinline__ bool build_xn(const uint16_t* x, const float* gamma, 
             const uint32_t in[4] = {w[t2].x, w[t2].y, w[t2].z, w[t2].w};
             uint32_t o[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t lo =
-                    f32_to_bf16(__fmul_rn(__fmul_rn(lo_bf16(in[q]), inv[t2]), g[2 * q]));
-                const uint32_t hi =
-                    f32_to_bf16(__fmul_rn(__fmul_rn(hi_bf16(in[q]), inv[t2]), g[2 * q + 1]));
-                o[q] = lo | (hi << 16);
-            }
+            for (int q = 0; q < 4; ++q)
+                o[q] = pack_bf16x2(__fmul_rn(__fmul_rn(lo_bf16(in[q]), inv[t2]), g[2 * q]),
+                                   __fmul_rn(__fmul_rn(hi_bf16(in[q]), inv[t2]), g[2 * q + 1]));
             const uint4 ov = make_uint4(o[0], o[1], o[2], o[3]);
             s_x4[t2 * rc + k8] = ov;
             if (xn_out) reinterpret_cast<uint4*>(xn_out)[t2 * rc + k8] = ov;
@@ -302,7 +304,7 @@ struct FrontArgs {
 };
 
 constexpr int kRouterBatch = 14;  // float4 row loads per lane per buffer (two buffers)
-constexpr int kRouterRows = 4;    // router rows per router block (waves 0-3; all 8 build xn)
+constexpr int kRouterRows = 4;    // router rows per router block (all 8 waves build xn)
 constexpr int kSharedGuDepth = 2; // shared gate/up tiles in flight per wave
 
 struct FrontLds {
@@ -310,26 +312,31 @@ struct FrontLds {
     f32x4 red[kFrontWaves][2][64];  // shared blocks: K-split partials
 };
 
-// Router block: waves 0-3 take one expert row each (fewer fp64 row waves
-// per SIMD), all eight build xn.  A row wave's first two batches of row
-// loads are issued right after the xn prologue's loads, so the row fetch
-// overlaps the prologue;
-// each partial 4l + c still accumulates j = 0, 1, ... in order (the
-// canonical order).  TT bounds the token count (register arrays sized by it).
+// Router block: kRouterRows expert rows; wave w takes row w % kRouterRows
+// for the tokens t = w / kRouterRows, w / kRouterRows + 2, ... (so with two
+// or more tokens all eight waves form dot products, each over half the
+// tokens; both waves of a row fetch it), and all eight build xn.  A row
+// wave's two batches of row loads are issued right after the xn prologue's
+// loads, so the row fetch overlaps the prologue; each partial 4l + c still
+// accumulates j = 0, 1, ... in order (the canonical order).  TT bounds the
+// token count (register arrays sized by it).
 template <int TT>
 __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, uint4* dyn_lds,
                                              NormShared& ns) {
+    constexpr uint32_t kPhases = kFrontWaves / kRouterRows;  // waves per row
+    constexpr int NT = (TT + kPhases - 1) / kPhases;         // tokens per wave
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.T, H = a.H, J = H / 256;
-    const uint32_t e = blk * kRouterRows + wave;
-    const bool row = wave < (uint32_t)kRouterRows && e < a.E;
+    const uint32_t ph = wave / kRouterRows, e = blk * kRouterRows + wave % kRouterRows;
+    const bool dots = ph < T;  // wave-uniform: this wave has tokens
+    const bool row = dots && e < a.E;
     // Loads are unconditional (a row past E reads row 0, a batch index past
     // the row end reads its last chunk; neither is used), so that they are
     // all in flight together.
     const float* wr = a.router_w + (size_t)(row ? e : 0) * H + 4 * lane;
     float4 wb[2][kRouterBatch];
     auto prefetch = [&]() {
-        if (wave < (uint32_t)kRouterRows)  // wave-uniform
+        if (dots)
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -343,11 +350,11 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
         return;
     if (!row) return;
     const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
-    double p[TT][4];
+    double p[NT][4];
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+    for (int i = 0; i < NT; ++i)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) p[t][c] = 0.0;
+        for (int c = 0; c < 4; ++c) p[i][c] = 0.0;
     for (uint32_t j0 = 0; j0 < J; j0 += 2 * kRouterBatch) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -355,16 +362,18 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
             for (int u = 0; u < kRouterBatch; ++u) {
                 const uint32_t j = j0 + b * kRouterBatch + u;
                 if (j >= J) continue;
-                const float wv[4] = {wb[b][u].x, wb[b][u].y, wb[b][u].z, wb[b][u].w};
+                const double wv[4] = {(double)wb[b][u].x, (double)wb[b][u].y, (double)wb[b][u].z,
+                                      (double)wb[b][u].w};
 #pragma unroll
-                for (int t = 0; t < TT; ++t) {
-                    if ((uint32_t)t >= T) continue;
+                for (int i = 0; i < NT; ++i) {
+                    const uint32_t t = ph + kPhases * i;
+                    if (t >= T) continue;
                     const uint2 xv =
                         *reinterpret_cast<const uint2*>(s_x + (size_t)t * H + 256 * j + 4 * lane);
                     const float f[4] = {lo_bf16(xv.x), hi_bf16(xv.x), lo_bf16(xv.y),
                                         hi_bf16(xv.y)};
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) p[t][c] = __builtin_fma((double)wv[c], (double)f[c], p[t][c]);
+                    for (int c = 0; c < 4; ++c) p[i][c] = __builtin_fma(wv[c], (double)f[c], p[i][c]);
                 }
             }
             // Refill this buffer with the batch two ahead (clamped).
@@ -377,9 +386,10 @@ __device__ __forceinline__ void router_block(const FrontArgs& a, uint32_t blk, u
         }
     }
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        if ((uint32_t)t >= T) continue;
-        const double v = canon_reduce(p[t]);
+    for (int i = 0; i < NT; ++i) {
+        const uint32_t t = ph + kPhases * i;
+        if (t >= T) continue;
+        const double v = canon_reduce(p[i]);
         if (lane == 0) a.logits[(size_t)t * a.E + e] = (float)v;
     }
 }

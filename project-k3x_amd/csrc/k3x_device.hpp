@@ -43,6 +43,17 @@ __device__ inline uint16_t f32_to_bf16(float v) {
     return (uint16_t)(b >> 16);
 }
 
+// Two floats -> packed bf16 bits {lo, hi}, the rule of f32_to_bf16: the
+// conversion instruction (v_cvt_pk_bf16_f32, round to nearest even) for
+// numbers and infinities, f32_to_bf16 itself for NaN (quiet bit set, low
+// payload bits dropped).
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    if (__builtin_isnan(lo) || __builtin_isnan(hi))
+        return (uint32_t)f32_to_bf16(lo) | (uint32_t)f32_to_bf16(hi) << 16;
+    const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // E8M0 byte -> 2^(s-127) as an fp32 (s = 0 gives the subnormal 2^-127).
 __device__ inline float e8m0_to_f32(uint32_t s) {
     return __uint_as_float(s ? (s << 23) : 0x00400000u);
