@@ -109,7 +109,11 @@ __device__ inline void end_step(int d) {
 template <bool FP4, bool GATEUP, int NT, bool SPLIT, bool Q>
 __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     static_assert(!Q || (FP4 && !SPLIT), "q8 rows meet MXFP4 weights, one term pair per tile");
-    __shared__ u32x4 s_a4[kWideStages * kTileChunks];  // 128 KiB ring
+    // 128 KiB ring; the split gate/up's epilogue stages 128 rows of fp32
+    // values in one pass, 16 bytes of pitch padding a row more than that.
+    constexpr uint32_t kRingChunks = kWideStages * kTileChunks;
+    constexpr uint32_t kStageChunks = GATEUP && SPLIT ? kWideRows * (kWaves * NT * 4 + 1) : 0;
+    __shared__ u32x4 s_a4[kRingChunks > kStageChunks ? kRingChunks : kStageChunks];
     __shared__ uint32_t s_yrow[kWideRows];              // down: output row of each chunk row
     // Q: scale dwords {hi, lo} of the chunk's rows per ring stage.
     __shared__ uint32_t s_qs[Q ? kWideStages * kWideRows * 2 : 1];
@@ -396,8 +400,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         // the four row groups of a write land 16 banks apart.  Down tiles
         // larger than the ring go in passes of RP rows.
         constexpr uint32_t kCols = kWaves * NT * 16;
-        // Output element bytes (split gate/up: the hi row, then the lo row).
-        constexpr uint32_t kEs = GATEUP ? (SPLIT ? 4 : 2) : 4;
+        // Output element bytes: bf16 act, or fp32 (down's rows; split
+        // gate/up's GLU values, rounded to the hi and lo halves as they are
+        // copied out -- rounding them while the accumulators are live took
+        // more registers than the step loop leaves).
+        constexpr uint32_t kEs = GATEUP && !SPLIT ? 2 : 4;
         constexpr uint32_t kChunks = kCols * kEs / 16;              // 16-byte chunks per row
         constexpr uint32_t kPitch = kCols * kEs + 16;               // staged row bytes
         constexpr uint32_t kRing = sizeof(s_a4);
@@ -418,12 +425,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         const uint32_t row = 16 * mt + 4 * g + i - p0;
                         const uint32_t col = (wave * NT + nt) * 16 + n;
-                        if constexpr (GATEUP) {
-                            const float v = glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
+                        if constexpr (GATEUP && SPLIT) {
+                            *reinterpret_cast<float*>(stage + row * kPitch + col * 4) =
+                                glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu);
+                        } else if constexpr (GATEUP) {
                             uint16_t* sp = reinterpret_cast<uint16_t*>(stage + row * kPitch) + col;
-                            const uint16_t hi = f32_to_bf16(v);
-                            sp[0] = hi;
-                            if constexpr (SPLIT) sp[kCols] = act_lo_bf16(v, hi);
+                            *sp = f32_to_bf16(glu(acc[mt][nt][0][i], acc[mt][nt][1][i], a.glu));
                         } else {
                             *reinterpret_cast<float*>(stage + row * kPitch + col * 4) =
                                 acc[mt][nt][0][i];
@@ -435,13 +442,23 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
             for (uint32_t c = tid; c < prow * kChunks; c += kThreads) {
                 const uint32_t row = c / kChunks, ch = c % kChunks;
                 const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * kPitch + ch * 16);
-                if constexpr (GATEUP) {
-                    // Chunks past the hi row's kCols / 8 carry the lo row.
-                    constexpr uint32_t kHiChunks = kCols / 8;
-                    const uint32_t lo = SPLIT && ch >= kHiChunks;
+                if constexpr (GATEUP && SPLIT) {
+                    // Four GLU values -> their hi and lo halves.
+                    uint32_t h[2], l[2];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const float v0 = __uint_as_float(v[2 * q]), v1 = __uint_as_float(v[2 * q + 1]);
+                        const uint16_t h0 = f32_to_bf16(v0), h1 = f32_to_bf16(v1);
+                        h[q] = (uint32_t)h0 | (uint32_t)h1 << 16;
+                        l[q] = (uint32_t)act_lo_bf16(v0, h0) | (uint32_t)act_lo_bf16(v1, h1) << 16;
+                    }
                     uint16_t* dst = a.act + (size_t)(off + m0 + p0 + row) * a.act_stride + col0 +
-                                    (lo ? a.act_lo : 0u);
-                    *reinterpret_cast<u32x4*>(dst + (ch - (lo ? kHiChunks : 0u)) * 8) = v;
+                                    ch * 4;
+                    *reinterpret_cast<uint2*>(dst) = make_uint2(h[0], h[1]);
+                    *reinterpret_cast<uint2*>(dst + a.act_lo) = make_uint2(l[0], l[1]);
+                } else if constexpr (GATEUP) {
+                    uint16_t* dst = a.act + (size_t)(off + m0 + p0 + row) * a.act_stride + col0;
+                    *reinterpret_cast<u32x4*>(dst + ch * 8) = v;
                 } else {
                     float* dst = a.y + (size_t)s_yrow[p0 + row] * a.y_stride + col0;
                     *reinterpret_cast<u32x4*>(dst + ch * 4) = v;
