@@ -276,6 +276,9 @@ def main() -> int:
                      "algorithmic_bytes": round(stage_bytes[dom]),
                      "traffic_source": TRAFFIC_JSON_REL if traffic else None},
     }
+    ceiling = read_ceiling(ctx, k3x_amd, torch)
+    result["roofline"]["read_ceiling"] = ceiling
+    result["roofline"]["frac_of_read_ceiling"] = round(achieved / ceiling["gbps"], 4)
 
     if not args.no_prefill:
         result["prefill"] = prefill(args, ctx, banks[0], k3x_amd, torch)
@@ -292,6 +295,27 @@ def main() -> int:
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def read_ceiling(ctx, k3x_amd, torch) -> dict:
+    """The device's plain streaming-read rate (k3x_hip_stream_read over 4 GiB
+    resident in HBM, 20 calls back to back): the practical ceiling a
+    streaming kernel's rate is read against, beside the nominal 8 TB/s."""
+    n, calls = 4 << 30, 20
+    buf = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    fold = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    for _ in range(3):
+        k3x_amd.check(ctx.stream_read(buf, fold), "stream_read")
+    k3x_amd.check(ctx.synchronize(), "synchronize")
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        k3x_amd.check(ctx.stream_read(buf, fold), "stream_read")
+    k3x_amd.check(ctx.synchronize(), "synchronize")
+    dt = (time.perf_counter() - t0) / calls
+    del buf
+    return {"gbps": round(n / dt / 1e9, 1), "bytes": n, "calls": calls,
+            "frac_of_peak": round(n / dt / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel": "stream_read_kernel (k3x_hip_stream_read)"}
 
 
 def prefill(args, ctx, bank, k3x_amd, torch) -> dict:

@@ -519,6 +519,17 @@ int k3x_hip_resident_moe_layer(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
                                const uint32_t* host_ids, const float* host_contributions,
                                float* out, float* mixed_out);
 
+/* ---- Measurement --------------------------------------------------------- */
+
+/* Streams `bytes` device bytes at `data` (16-byte aligned, a multiple of 16)
+ * through the vector memory path once, on the context stream, and XORs
+ * every 32-bit word of them into *fold (device memory, left as is
+ * otherwise): the device's plain streaming-read rate, the practical ceiling
+ * that a streaming kernel's HBM rate is read against beside the nominal
+ * 8 TB/s.  No counterpart in the reference (measurement only).
+ * Asynchronous. */
+int k3x_hip_stream_read(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* fold);
+
 /* ---- K3X storage records -------------------------------------------------- */
 
 /* CRC32C (Castagnoli, reflected, preset and final inversion 0xFFFFFFFF) of

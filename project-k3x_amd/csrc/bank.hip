@@ -122,6 +122,31 @@ __global__ void fill_const_f32(size_t n, float v, float* __restrict__ out) {
 // Read-back of rows [row0, row0+nrows) as fp32 through dequant8, the same
 // conversion the GEMM kernels feed to the MFMA.  One thread per 32-column
 // block.
+// Streaming read: workgroup b reads the contiguous span [b per, (b + 1) per)
+// of 16-byte words, U words a thread in flight per step (indices clamped,
+// so no load sits behind a branch), and every wave XORs its words into
+// *fold once.  8192 workgroups of 512 threads, U = 4: the best of a sweep
+// over 256..8192 workgroups and 4..16 words in flight on MI355X.
+constexpr uint32_t kStreamReadBlocks = 8192, kStreamReadThreads = 512;
+__global__ __launch_bounds__(kStreamReadThreads) void stream_read_kernel(
+    const uint4* __restrict__ p, size_t n16, size_t per_block, uint32_t* fold) {
+    constexpr int U = 4;
+    const size_t b0 = (size_t)blockIdx.x * per_block;
+    const size_t b1 = min(b0 + per_block, n16);
+    uint32_t acc = 0;
+    for (size_t i = b0 + threadIdx.x; i < b1; i += (size_t)kStreamReadThreads * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = p[min(i + (size_t)kStreamReadThreads * u, b1 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (i + (size_t)kStreamReadThreads * u < b1) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) acc ^= __shfl_xor(acc, d);
+    if ((threadIdx.x & 63) == 0 && acc) atomicXor(fold, acc);
+}
+
 __global__ void dequant_rows(const uint4* __restrict__ codes, const uint32_t* __restrict__ scales,
                              uint32_t cols, uint32_t kt, uint32_t ks, uint32_t S,
                              uint32_t which, uint32_t row0, uint32_t nrows,
@@ -794,6 +819,20 @@ int k3x_hip_bank_fill_synthetic(k3x_hip_bank* bank, const k3x_hip_synth_desc* s)
     bank->router_ready = true;
     bank->shared_ready = d.shared_inter != 0;
     return K3X_OK;
+}
+
+int k3x_hip_stream_read(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* fold) {
+    if (!ctx || !data || !fold || !bytes || bytes % 16 || reinterpret_cast<uintptr_t>(data) % 16)
+        return K3X_ERR_INVALID_EXTENT;
+    if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
+    const size_t n16 = bytes / 16;
+    const uint32_t blocks = (uint32_t)std::min<size_t>(kStreamReadBlocks,
+                                                       (n16 + kStreamReadThreads - 1) /
+                                                           kStreamReadThreads);
+    const size_t per_block = (n16 + blocks - 1) / blocks;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(kStreamReadThreads), 0, ctx->stream,
+                       static_cast<const uint4*>(data), n16, per_block, fold);
+    return check_launch(ctx);
 }
 
 int k3x_hip_synth_normal_bf16(k3x_hip_ctx* ctx, uint64_t seed, uint64_t stream, float sigma,

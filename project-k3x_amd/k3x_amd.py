@@ -135,6 +135,7 @@ _SIGS = {
     "k3x_hip_bank_upload_expert": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64), _vp, _vp,
                                              _vp, _vp, _vp, _vp]),
     "k3x_hip_crc32c": (C.c_int, [_vp, _vp, C.c_size_t, C.POINTER(C.c_uint32)]),
+    "k3x_hip_stream_read": (C.c_int, [_vp, _vp, C.c_size_t, _vp]),
     "k3x_hip_storage_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "k3x_hip_storage_close": (C.c_int, [_vp]),
     "k3x_hip_storage_upload_expert": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
@@ -246,6 +247,12 @@ class Context:
         out = C.c_uint32(0)
         st = self.lib.k3x_hip_crc32c(self.handle, ptr(data), n, C.byref(out))
         return st, out.value
+
+    def stream_read(self, data, fold, nbytes: int | None = None) -> int:
+        """Enqueues k3x_hip_stream_read over a device tensor's bytes, XOR-folding
+        its 32-bit words into the device dword `fold`."""
+        n = data.numel() * data.element_size() if nbytes is None else nbytes
+        return self.lib.k3x_hip_stream_read(self.handle, ptr(data), n, ptr(fold))
 
     def stats(self) -> Stats:
         s = Stats()

@@ -46,6 +46,25 @@ def test_device_crc32c(hip, oracle, n):
     assert st == 0 and crc == oracle.crc32c(host[:n].tobytes())
 
 
+@pytest.mark.parametrize("n", [16, 4096 + 16, 8192 * 512 * 16 + 48, (64 << 20) + 32])
+def test_stream_read_fold(hip, n):
+    """k3x_hip_stream_read (the bench's read-ceiling measurement) reads every
+    word exactly once: its XOR fold equals numpy's over the same words, for
+    sizes below, at and past one word per thread of the full grid; misaligned
+    or ragged extents are rejected."""
+    k3x_amd, ctx = hip
+    say(f"stream_read n={n}")
+    rng = np.random.default_rng(n)
+    host = rng.integers(0, 1 << 32, n // 4, dtype=np.uint32)
+    dev = torch.from_numpy(host.view(np.int32)).to("cuda:0")
+    fold = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    assert ctx.stream_read(dev, fold, n) == 0
+    assert ctx.synchronize() == 0
+    assert int(fold.cpu().numpy().view(np.uint32)[0]) == int(np.bitwise_xor.reduce(host))
+    assert ctx.stream_read(dev, fold, n - 4) == k3x_amd.ERR_INVALID_EXTENT
+    assert ctx.stream_read(dev[1:], fold, 16) == k3x_amd.ERR_INVALID_EXTENT
+
+
 def make_expert(seed, inter, hidden):
     rng = np.random.default_rng(seed)
     ex = {f"{r}_packed": rng.integers(0, 256, inter * hidden // 2, dtype=np.uint8)
