@@ -1449,6 +1449,11 @@ int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t 
                            const LayerBuffers& b, const uint16_t* xn, const GluParams& glu,
                            bool split, bool chunked) {
     const auto& d = bank->desc;
+    // Row tokens travel as 8-bit fields (the records' packed tokens, or the
+    // chunk's tokens packed in the kernel).
+    if (T > (chunked ? kChunkedMaxTokens : (uint32_t)kMaxDecodeTokens) ||
+        !few_row_experts_eligible(ctx, bank, chunked ? kRowChunk : T, split))
+        return K3X_ERR_INVALID_EXTENT;
     GateUpArgs gu{};
     gu.gu_codes = reinterpret_cast<const uint4*>(bank->gu_codes);
     gu.gu_scales = bank->gu_scales;
@@ -1487,6 +1492,9 @@ int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t 
 int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
                         const LayerBuffers& b, bool split, bool chunked) {
     const auto& d = bank->desc;
+    if (T > (chunked ? kChunkedMaxTokens : (uint32_t)kMaxDecodeTokens) ||
+        !few_row_experts_eligible(ctx, bank, chunked ? kRowChunk : T, split))
+        return K3X_ERR_INVALID_EXTENT;
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
     dn.dn_scales = bank->dn_scales;
