@@ -113,8 +113,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     // values in one pass, 16 bytes of pitch padding a row more than that.
     constexpr uint32_t kRingChunks = kWideStages * kTileChunks;
     constexpr uint32_t kStageChunks = GATEUP && SPLIT ? kWideRows * (kWaves * NT * 4 + 1) : 0;
-    __shared__ u32x4 s_a4[kRingChunks > kStageChunks ? kRingChunks : kStageChunks];
-    __shared__ uint32_t s_yrow[kWideRows];              // down: output row of each chunk row
+    // Down's output row of each chunk row sits past the ring (or the split
+    // epilogue's staging) in the same LDS array: as a second LDS variable it
+    // made the compiler's wait counting fall back to a full drain of the
+    // ring's LDS-DMA requests twice per four steps.  (Q's row scales stay a
+    // variable of their own: folded in as well, the q8 kernels spilled.)
+    constexpr uint32_t kA4 = kRingChunks > kStageChunks ? kRingChunks : kStageChunks;
+    constexpr uint32_t kYrowChunks = GATEUP ? 0 : kWideRows * 4 / 16;
+    __shared__ u32x4 s_a4[kA4 + kYrowChunks];
+    uint32_t* const s_yrow = reinterpret_cast<uint32_t*>(s_a4 + kA4);
     // Q: scale dwords {hi, lo} of the chunk's rows per ring stage.
     __shared__ uint32_t s_qs[Q ? kWideStages * kWideRows * 2 : 1];
     constexpr int S = GATEUP ? 2 : 1;  // matrices per output row block (gate, up)
@@ -407,7 +414,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
         constexpr uint32_t kEs = GATEUP && !SPLIT ? 2 : 4;
         constexpr uint32_t kChunks = kCols * kEs / 16;              // 16-byte chunks per row
         constexpr uint32_t kPitch = kCols * kEs + 16;               // staged row bytes
-        constexpr uint32_t kRing = sizeof(s_a4);
+        constexpr uint32_t kRing = kA4 * 16;  // the staging stays clear of s_yrow
         constexpr uint32_t RP0 = kRing / kPitch / 16 * 16;
         constexpr uint32_t RP = RP0 < MT * 16 ? RP0 : MT * 16;     // rows per pass
         static_assert(RP >= 16, "one row tile per pass at least");
