@@ -1186,15 +1186,18 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
     constexpr int H2 = SPLIT ? 2 : 1;  // activation halves
 
     for (uint32_t m0 = 0; m0 < cnt; m0 += 16 * MT) {
+        // Rows past the block's end read its last row (their products are
+        // zeroed): every activation load is unconditional, so none waits
+        // behind a branch for all older loads.
         const uint16_t* arow[MT];
+        bool live[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const uint32_t row = m0 + 16 * mt + n;
-            arow[mt] = nullptr;
-            if (row < cnt) {
-                const uint32_t src = a.gather ? a.pair_token[off + row] : off + row;
-                arow[mt] = a.a + (size_t)src * a.a_stride + 32 * g;
-            }
+            live[mt] = row < cnt;
+            const uint32_t r = min(row, cnt - 1);
+            const uint32_t src = a.gather ? a.pair_token[off + r] : off + r;
+            arow[mt] = a.a + (size_t)src * a.a_stride + 32 * g;
         }
         f32x4 acc[MT][NT][S];
 #pragma unroll
@@ -1232,15 +1235,13 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                     for (int h = 0; h < H2; ++h) {
-                        if (arow[mt] && k0 + d < a.kt) {
-                            const uint4* p = reinterpret_cast<const uint4*>(
-                                arow[mt] + (h ? a.a_lo : 0u) + (size_t)k * 128);
+                        const uint4* p = reinterpret_cast<const uint4*>(
+                            arow[mt] + (h ? a.a_lo : 0u) + (size_t)k * 128);
+                        const bool use = live[mt] && k0 + d < a.kt;
 #pragma unroll
-                            for (int j = 0; j < 4; ++j) af[d][mt][h][j] = as_bf16x8(p[j]);
-                        } else {
-#pragma unroll
-                            for (int j = 0; j < 4; ++j)
-                                af[d][mt][h][j] = as_bf16x8(make_uint4(0, 0, 0, 0));
+                        for (int j = 0; j < 4; ++j) {
+                            const uint4 v = p[j];
+                            af[d][mt][h][j] = as_bf16x8(use ? v : make_uint4(0, 0, 0, 0));
                         }
                     }
             }
