@@ -1943,9 +1943,53 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
 
 // Grouping, expert GEMMs, shared expert, combine.  xn is the bf16 input of
 // the experts; ids/weights [T][K] device.
+// Whether a call's shared expert runs on the context's second stream: the
+// wide path (the routed GEMMs run for milliseconds) and the verification
+// windows on the decode kernels (hundreds of microseconds of routed
+// streaming beside a few dozen shared workgroups).  With stage profiling on,
+// everything stays on the context stream.
+bool shared_on_side(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, const k3x_hip_moe_params* p) {
+    const auto& d = bank->desc;
+    const uint32_t T = p->tokens, K = p->top_k;
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    const bool split_in = (p->flags & K3X_FLAG_SPLIT_INPUT) != 0;
+    const bool wide_path = !split_in && use_wide_gemm(d, T, K, split);
+    const bool chunked_rows = !wide_path && !split_in && T > k3x_hip::kMaxDecodeTokens &&
+                              T <= k3x_hip::kChunkedMaxTokens &&
+                              k3x_hip::few_row_experts_eligible(ctx, bank,
+                                                                k3x_hip::kMaxDecodeTokens, split);
+    return (wide_path || chunked_rows) && d.shared_inter && !ctx->profiling && ctx->side_stream;
+}
+
+// Launches the shared expert on the second stream after the context
+// stream's work so far (it needs xn only) and records the event the context
+// stream joins on.
+int fork_shared(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                const Scratch& s, const uint16_t* xn, const GluParams& glu) {
+    const auto& d = bank->desc;
+    const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
+    const bool split_in = (p->flags & K3X_FLAG_SPLIT_INPUT) != 0;
+    const bool wide_path = !split_in && use_wide_gemm(d, p->tokens, p->top_k, split);
+    if (hipEventRecord(ctx->fork_ev, ctx->stream) != hipSuccess ||
+        hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0) != hipSuccess)
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    const int sst = wide_path ? run_shared_wide(ctx, bank, p, s, xn, glu, ctx->side_stream)
+                              : run_shared_narrow(ctx, bank, p, s, xn, glu, split_in,
+                                                  ctx->side_stream);
+    if (hipEventRecord(ctx->join_ev, ctx->side_stream) != hipSuccess) {
+        // Without the event, order the streams the blunt way.
+        (void)hipStreamSynchronize(ctx->side_stream);
+        return K3X_ERR_BACKEND_UNAVAILABLE;
+    }
+    return sst;
+}
+
+// forked: the caller has already launched the shared expert on the second
+// stream (fork_shared); the context stream still joins it before the
+// combine and on every return.
 int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              const Scratch& s, const uint16_t* xn, const uint32_t* ids, const float* weights,
-             uint16_t* out, float* out_f32) {
+             uint16_t* out, float* out_f32, bool forked = false) {
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
     GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
@@ -1967,8 +2011,7 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
                               T <= k3x_hip::kChunkedMaxTokens &&
                               k3x_hip::few_row_experts_eligible(ctx, bank,
                                                                 k3x_hip::kMaxDecodeTokens, split);
-    const bool side = (wide_path || chunked_rows) && d.shared_inter && !ctx->profiling &&
-                      ctx->side_stream;
+    const bool side = shared_on_side(ctx, bank, p);
     struct Join {
         k3x_hip_ctx* ctx;
         bool armed = false;
@@ -1982,20 +2025,11 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         ~Join() { (void)join(); }
     } joiner{ctx};
     if (side) {
-        if (hipEventRecord(ctx->fork_ev, ctx->stream) != hipSuccess ||
-            hipStreamWaitEvent(ctx->side_stream, ctx->fork_ev, 0) != hipSuccess)
-            return K3X_ERR_BACKEND_UNAVAILABLE;
-        const int sst = wide_path
-                            ? run_shared_wide(ctx, bank, p, s, xn, glu, ctx->side_stream)
-                            : run_shared_narrow(ctx, bank, p, s, xn, glu, split_in,
-                                                ctx->side_stream);
-        if (hipEventRecord(ctx->join_ev, ctx->side_stream) != hipSuccess) {
-            // Without the event, order the streams the blunt way.
-            (void)hipStreamSynchronize(ctx->side_stream);
-            return K3X_ERR_BACKEND_UNAVAILABLE;
-        }
         joiner.armed = true;
-        if (sst) return sst;
+        if (!forked) {
+            const int sst = fork_shared(ctx, bank, p, s, xn, glu);
+            if (sst) return sst;
+        }
     }
     int mark = begin_stage(ctx, K3X_STAGE_GROUP);
     // Work items of the wide GEMM only where it runs (without them a small
@@ -2440,14 +2474,29 @@ int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_mo
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, ctx->stream, x, bank->gamma,
                        d.hidden, p->rms_epsilon, s.xn, mfma_router ? s.xp : nullptr,
                        ctx->status);
+    // The shared expert needs xn only: on the second stream it runs beside
+    // the router, the Top-K and the grouping, not only the routed GEMMs.
+    const bool forked = shared_on_side(ctx, bank, p);
+    if (forked) {
+        const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear,
+                            p->situ_linear_beta};
+        if ((st = fork_shared(ctx, bank, p, s, s.xn, glu))) {
+            (void)hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0);
+            return st;
+        }
+    }
     st = launch_router(ctx, bank->router_w, mfma_router ? bank->router_wp : nullptr, s.xn, s.xp,
                        d.experts, d.hidden, T, s.logits);
     st = st ? st : launch_topk_any(ctx, s.logits, bank->router_bias, d.experts, K, T,
                                    p->routed_scale, p->renorm, s.ids, s.weights);
-    if (st) return st;
-    k3x_hip::end_stage(ctx, mark);
-    if ((st = launched(ctx, 1))) return st;
-    if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr)))
+    if (!st) k3x_hip::end_stage(ctx, mark);
+    if (!st) st = launched(ctx, 1);
+    if (st) {
+        if (forked) (void)hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0);
+        return st;
+    }
+    if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr,
+                       forked)))
         return st;
     ++ctx->forward_calls;
     return copy_taps(ctx, bank, p, s, s.xn, s.ids, s.weights, taps);
