@@ -190,9 +190,13 @@ int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, 
                   bool split = false);
 // Up to kDenseDirectTokens rows the projections run as a split-K GEMV on
 // any stream, and dense_down can round its output to bf16 itself (y_bf16;
-// y is then unused); above, y_bf16 must be null and the narrow GEMM runs on
-// the context stream only.
+// y is then unused); above, y_bf16 must be null, and the projections run on
+// the wide GEMM (any stream) where its shape rules allow, else on the narrow
+// GEMM (the context stream only).
 constexpr uint32_t kDenseDirectTokens = 16;
+// True when both projections of a dense GLU MLP (gate/up I x H, down H x I)
+// may be enqueued on a stream other than the context's for T rows.
+bool dense_mlp_any_stream(uint32_t I, uint32_t H, uint32_t T);
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
                uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr,
                bool split = false);

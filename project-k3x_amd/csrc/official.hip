@@ -631,11 +631,12 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     carve(static_cast<uint8_t*>(o->scratch), o, T, K, &b);
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
     // Shared FFN on hidden (official_moe.cpp:105-117, :307): on the side
-    // stream beside the route and the experts when the projections run as
-    // GEMVs (few rows: the routed kernels leave the device half idle), joined
-    // before the output; in line otherwise.
-    const bool side = o->I_s && T <= k3x_hip::kDenseDirectTokens && ctx->side_stream &&
-                      !ctx->profiling;
+    // stream beside the route and the experts (few rows: the routed kernels
+    // leave the device half idle; many rows: the latency-bound route steps
+    // and the experts' tails do), joined before the output; in line when
+    // its projections cannot leave the context stream.
+    const bool side = o->I_s && ctx->side_stream && !ctx->profiling &&
+                      k3x_hip::dense_mlp_any_stream(o->I_s, o->H, T);
     struct Join {
         k3x_hip_official* o;
         bool armed = false;

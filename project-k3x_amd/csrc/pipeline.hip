@@ -2316,6 +2316,11 @@ bool dense_wide_ok(WideKind kind, uint32_t N, uint32_t K, uint32_t T) {
            (uint64_t)T * std::max(N, K) * 4 < (1ull << 32) && (uint64_t)N * K * 4 < (1ull << 32);
 }
 
+bool dense_mlp_any_stream(uint32_t I, uint32_t H, uint32_t T) {
+    return T <= kDenseDirectTokens ||
+           (dense_wide_ok(kWideSharedGateUp, I, H, T) && dense_wide_ok(kWideSharedDown, H, I, T));
+}
+
 int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
                   uint32_t T, const GluParams& glu, uint16_t* act, hipStream_t stream,
                   bool split) {
