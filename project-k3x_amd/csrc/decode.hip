@@ -104,6 +104,19 @@ __device__ inline void load_act(const uint16_t* ap, bool arow, uint32_t k, uint4
         for (int j = 0; j < 4; ++j) av[j] = *reinterpret_cast<const uint4*>(ap + k * 128 + 8 * j);
 }
 
+
+// Routed expert weights are read once per call (each expert's tiles by one
+// workgroup set) and not again before other layers' weights have passed
+// through the caches: non-temporal loads, which do not keep the lines in
+// the L2 / MALL, leave those caches to the activations, per-pair rows and
+// counters that are re-read (C3 decode: gate/up 76.3 -> 74.8 us, down
+// 47.0 -> 44.1 us).
+__device__ inline uint4 ntl(const uint4* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint32_t ntl(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
 // Wave index as a wave-uniform (scalar) value.
 __device__ inline uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -987,14 +1000,14 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
 #pragma unroll
     for (int i = 0; i < kGuTiles; ++i) {
         const size_t k = min(k0 + i, kt - 1);  // tiles past k1 are loaded, not used
-        c0[i] = codes[k * 128];
-        c1[i] = codes[k * 128 + 64];
+        c0[i] = ntl(codes + k * 128);
+        c1[i] = ntl(codes + k * 128 + 64);
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const size_t grp = min(k0 / 4 + i, a.ks - 1);
-        s0[i] = scales[grp * 128];
-        s1[i] = scales[grp * 128 + 64];
+        s0[i] = ntl(scales + grp * 128);
+        s1[i] = ntl(scales + grp * 128 + 64);
     }
     store_chunks(v, s_x4, tid, 64 * kGuWaves, rows * rowc);
     __syncthreads();
@@ -1204,9 +1217,9 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     uint4 c[TILES];
     uint32_t sw[TILES / 4];
 #pragma unroll
-    for (int i = 0; i < TILES; ++i) c[i] = codes[(size_t)min((uint32_t)i, kt - 1) * 64];
+    for (int i = 0; i < TILES; ++i) c[i] = ntl(codes + (size_t)min((uint32_t)i, kt - 1) * 64);
 #pragma unroll
-    for (int i = 0; i < TILES / 4; ++i) sw[i] = scales[(size_t)min((uint32_t)i, a.ks - 1) * 64];
+    for (int i = 0; i < TILES / 4; ++i) sw[i] = ntl(scales + (size_t)min((uint32_t)i, a.ks - 1) * 64);
     K3X_DOWN_LOAD_YROWS(0, rows);
     K3X_DOWN_STORE_ROWS(rows);
     __syncthreads();

@@ -11,8 +11,14 @@
 //     batch, grid and slot-ordered mix, the resident latent layer, the
 //     official layer's four methods, the fp32 dense / MXFP4 matrix-vector
 //     products and the fp32 SiTU MLP.  A shape the device path does not run
-//     (backend_unavailable from the library) is computed by the reference's
-//     CPU backend instead, so a caller never loses a result to it.
+//     -- a result the library marks declined(), returned by its argument
+//     checks before any upload or launch -- is computed by the reference's
+//     CPU backend instead and counted (runtime_stats().resident_grid_fallbacks;
+//     the latent layer's also in resident_moe_layer_fallbacks).  Every other
+//     failure, device, allocation and launch failures included, is returned
+//     as the failure it is, as the CUDA backend returns them
+//     (runtime/cuda/backend_cuda.cu:1806-1883) for the caller to raise
+//     (runtime/src/model.cpp:1034-1037).
 //   * Every other method -- the prefetch trio, official_kda and the layer
 //     front / tail -- forwards to make_cpu_backend(), the reference's exact
 //     path.
@@ -83,13 +89,16 @@ T from_hip(T&& v) {
     return std::move(v);
 }
 
-// The library's result as the reference's; where the device path does not
-// run the shape, the CPU backend's.
+// The library's result as the reference's; where the library declined the
+// shape (before any device work), the CPU backend's, counted in *declined.
 template <class H, class F>
-auto or_cpu(hip::Result<H>&& r, F&& cpu) -> decltype(cpu()) {
+auto or_cpu(hip::Result<H>&& r, std::uint64_t* declined, F&& cpu) -> decltype(cpu()) {
     using R = decltype(cpu());
     if (r) return R::success(from_hip(std::move(r.value())));
-    if (r.error() == hip::ErrorCode::backend_unavailable) return cpu();
+    if (r.declined()) {
+        ++*declined;
+        return cpu();
+    }
     return R::failure(code(r.error()), r.message());
 }
 
@@ -106,33 +115,38 @@ public:
         r.weight_h2d_bytes = s.weight_h2d_bytes;
         r.weight_cache_hits = s.residency_hits;
         r.weight_cache_misses = s.experts_admitted + s.dense_uploads;
-        r.resident_moe_layer_fallbacks = s.resident_layer_fallbacks;
+        r.resident_moe_layer_fallbacks = s.resident_layer_fallbacks + layer_declined_;
         r.resident_grid_kernel_launches = s.kernel_launches;
+        // Calls the device path declined by shape, computed by the CPU
+        // backend instead.
+        r.resident_grid_fallbacks = declined_;
+        r.resident_weight_bytes = s.device_bytes;
+        r.peak_resident_weight_bytes = s.peak_device_bytes;
         return r;
     }
 
     Result<std::vector<float>> dense_matvec(std::span<const float> input, DenseWeightView weight,
                                             std::uint32_t layer, ProfilePhase phase) override {
-        return or_cpu(be_->dense_matvec(input, to_hip(weight), layer, to_hip(phase)),
+        return or_cpu(be_->dense_matvec(input, to_hip(weight), layer, to_hip(phase)), &declined_,
                       [&] { return cpu_->dense_matvec(input, weight, layer, phase); });
     }
     Result<std::vector<float>> mxfp4_matvec(std::span<const float> input, Mxfp4WeightView weight,
                                             std::uint32_t layer, ProfilePhase phase) override {
-        return or_cpu(be_->mxfp4_matvec(input, to_hip(weight), layer, to_hip(phase)),
+        return or_cpu(be_->mxfp4_matvec(input, to_hip(weight), layer, to_hip(phase)), &declined_,
                       [&] { return cpu_->mxfp4_matvec(input, weight, layer, phase); });
     }
     Result<std::vector<std::vector<float>>> dense_matvec_group(
         std::span<const float> input, std::span<const DenseWeightView> weights,
         std::uint32_t layer, ProfilePhase phase) override {
         const auto w = to_hip_all(weights);
-        return or_cpu(be_->dense_matvec_group(input, w, layer, to_hip(phase)),
+        return or_cpu(be_->dense_matvec_group(input, w, layer, to_hip(phase)), &declined_,
                       [&] { return cpu_->dense_matvec_group(input, weights, layer, phase); });
     }
     Result<std::vector<std::vector<float>>> mxfp4_matvec_group(
         std::span<const float> input, std::span<const Mxfp4WeightView> weights,
         std::uint32_t layer, ProfilePhase phase) override {
         const auto w = to_hip_all(weights);
-        return or_cpu(be_->mxfp4_matvec_group(input, w, layer, to_hip(phase)),
+        return or_cpu(be_->mxfp4_matvec_group(input, w, layer, to_hip(phase)), &declined_,
                       [&] { return cpu_->mxfp4_matvec_group(input, weights, layer, phase); });
     }
     Result<std::vector<float>> dense_situ_mlp(std::span<const float> input, DenseMlpView weights,
@@ -140,7 +154,7 @@ public:
                                               std::uint32_t layer, ProfilePhase phase) override {
         return or_cpu(
             be_->dense_situ_mlp(input, to_hip(weights), situ_beta, situ_linear, layer,
-                                to_hip(phase)),
+                                to_hip(phase)), &declined_,
             [&] { return cpu_->dense_situ_mlp(input, weights, situ_beta, situ_linear, layer, phase); });
     }
     Result<std::vector<std::vector<float>>> mxfp4_situ_mlp_group(
@@ -148,7 +162,7 @@ public:
         std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) override {
         const auto e = to_hip_all(experts);
         return or_cpu(be_->mxfp4_situ_mlp_group(input, e, situ_beta, situ_linear, layer,
-                                                to_hip(phase)),
+                                                to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->mxfp4_situ_mlp_group(input, experts, situ_beta, situ_linear,
                                                             layer, phase);
@@ -159,7 +173,7 @@ public:
         float situ_beta, std::optional<float> situ_linear, std::uint32_t layer,
         ProfilePhase phase) override {
         return or_cpu(be_->mxfp4_situ_mlp_batch(inputs, batch_size, to_hip(expert), situ_beta,
-                                                situ_linear, layer, to_hip(phase)),
+                                                situ_linear, layer, to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->mxfp4_situ_mlp_batch(inputs, batch_size, expert, situ_beta,
                                                             situ_linear, layer, phase);
@@ -171,7 +185,7 @@ public:
         std::uint32_t layer, ProfilePhase phase) override {
         const auto e = to_hip_all(experts);
         return or_cpu(be_->mxfp4_situ_mlp_grid(inputs, token_count, e, situ_beta, situ_linear,
-                                               layer, to_hip(phase)),
+                                               layer, to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->mxfp4_situ_mlp_grid(inputs, token_count, experts, situ_beta,
                                                            situ_linear, layer, phase);
@@ -184,7 +198,7 @@ public:
                                               std::uint32_t layer, ProfilePhase phase) override {
         const auto e = to_hip_all(experts);
         return or_cpu(be_->mxfp4_situ_moe(input, e, contributions, situ_beta, situ_linear, layer,
-                                          to_hip(phase)),
+                                          to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->mxfp4_situ_moe(input, experts, contributions, situ_beta,
                                                       situ_linear, layer, phase);
@@ -198,8 +212,9 @@ public:
         const auto e = to_hip_all(experts);
         return or_cpu(be_->resident_mxfp4_moe_layer(input, to_hip(weights), e, contributions,
                                                     epsilon, situ_beta, situ_linear, layer,
-                                                    to_hip(phase)),
+                                                    to_hip(phase)), &declined_,
                       [&] {
+                          ++layer_declined_;
                           return cpu_->resident_mxfp4_moe_layer(input, weights, experts,
                                                                 contributions, epsilon, situ_beta,
                                                                 situ_linear, layer, phase);
@@ -213,7 +228,7 @@ public:
         const auto e = to_hip_all(experts);
         return or_cpu(be_->official_mxfp4_moe_ffn(hidden, prefix, to_hip(weights), e, expert_ids,
                                                   contributions, epsilon, situ_beta, situ_linear,
-                                                  layer, to_hip(phase)),
+                                                  layer, to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->official_mxfp4_moe_ffn(hidden, prefix, weights, experts,
                                                               expert_ids, contributions, epsilon,
@@ -225,7 +240,7 @@ public:
         OfficialMoeRoutePrepareView weights, float epsilon, std::uint32_t layer,
         ProfilePhase phase) override {
         return or_cpu(be_->prepare_official_moe_route(prefix, block_residual, to_hip(weights),
-                                                      epsilon, layer, to_hip(phase)),
+                                                      epsilon, layer, to_hip(phase)), &declined_,
                       [&] {
                           return cpu_->prepare_official_moe_route(prefix, block_residual, weights,
                                                                   epsilon, layer, phase);
@@ -306,9 +321,11 @@ public:
                                              layer, phase);
     }
 
+    // The device bytes this backend holds now (banks, resident dense
+    // weights, scratch, per-call buffers) and their peak.
     BackendMemoryStats memory_stats() const noexcept override {
         const hip::HipBackendStats s = be_->runtime_stats();
-        return {s.weight_h2d_bytes, s.weight_h2d_bytes};
+        return {s.device_bytes, s.peak_device_bytes};
     }
     std::string_view device_name() const noexcept override { return be_->device_name(); }
 
@@ -316,9 +333,26 @@ private:
     std::unique_ptr<hip::HipMoeBackend> be_;
     std::unique_ptr<ComputeBackend> cpu_;
     BackendOptions options_;
+    std::uint64_t declined_ = 0;        // calls declined by shape, run on the CPU backend
+    std::uint64_t layer_declined_ = 0;  // of them, resident_mxfp4_moe_layer calls
 };
 
 }  // namespace
+
+// The factory with the device-side options given explicitly (device index,
+// bank slots, resident byte budget; HipBackendOptions::kNoDevice gives a
+// backend with no device, whose declined shapes still run on the CPU
+// backend and whose other calls fail with backend_unavailable).
+Result<std::unique_ptr<ComputeBackend>> make_hip_backend(const BackendOptions& options,
+                                                         Profiler* profiler,
+                                                         const k3x_amd::HipBackendOptions& o) {
+    auto be = hip::make_hip_backend(o);
+    if (!be) {
+        return Result<std::unique_ptr<ComputeBackend>>::failure(code(be.error()), be.message());
+    }
+    return Result<std::unique_ptr<ComputeBackend>>::success(
+        std::make_unique<HipBackend>(std::move(be.value()), options, profiler));
+}
 
 // The factory a maintainer declares beside make_cuda_backend
 // (backend.hpp:465-466).  Slots: every routed expert of a K3-shaped layer
@@ -329,12 +363,7 @@ Result<std::unique_ptr<ComputeBackend>> make_hip_backend(const BackendOptions& o
     o.device = 0;
     o.resident_experts = 384;
     if (options.cuda_resident_bytes) o.resident_dense_bytes = options.cuda_resident_bytes;
-    auto be = hip::make_hip_backend(o);
-    if (!be) {
-        return Result<std::unique_ptr<ComputeBackend>>::failure(code(be.error()), be.message());
-    }
-    return Result<std::unique_ptr<ComputeBackend>>::success(
-        std::make_unique<HipBackend>(std::move(be.value()), options, profiler));
+    return make_hip_backend(options, profiler, o);
 }
 
 }  // namespace k3x

@@ -128,6 +128,20 @@ struct HipMoeBackend::Impl {
     Dev prep_prefix, prep_block, prep_hidden, prep_logits, o_hidden, o_prefix, o_ids, o_contrib,
         o_out;
 
+    // Device bytes held now: the banks (routed and official), the resident
+    // single matrices, the per-call buffers and the context's scratch.
+    std::uint64_t device_bytes(std::uint64_t ctx_scratch) const {
+        std::uint64_t n = ctx_scratch + resident_total;
+        for (const auto& kv : banks) n += k3x_hip_bank_bytes(kv.second.bank);
+        for (const auto& kv : official_ffns) n += k3x_hip_bank_bytes(kv.second.bank.bank);
+        for (const Dev* d : {&xn, &ids, &w, &out, &out_f32, &pairs, &prep_prefix, &prep_block,
+                             &prep_hidden, &prep_logits, &o_hidden, &o_prefix, &o_ids, &o_contrib,
+                             &o_out, &transient[0], &transient[1], &transient[2], &vin, &vout,
+                             &vact, &vids, &vc})
+            n += d->bytes;
+        return n;
+    }
+
     ~Impl() {
         for (auto& kv : official_ffns) {
             k3x_hip_official_destroy(kv.second.obj);
@@ -146,7 +160,21 @@ struct HipMoeBackend::Impl {
 
     std::uint64_t owner() const { return reinterpret_cast<std::uintptr_t>(this); }
 
+    // A shape the device path does not run, found before any device work.
+    template <class R>
+    R decline(const char* what) {
+        ++stats.declined_shapes;
+        return R::declined_shape(what);
+    }
+    // supported()'s answer as a method result: backend_unavailable is a
+    // declined shape, anything else a failure.
+    template <class R>
+    R shape_failure(ErrorCode c, const char* what) {
+        return c == ErrorCode::backend_unavailable ? decline<R>(what) : R::failure(c);
+    }
+
     ErrorCode ensure(Dev& d, std::size_t n) {
+        if (!ctx) return ErrorCode::backend_unavailable;  // no device attached
         if (d.bytes >= n) return ErrorCode::ok;
         if (d.p) (void)hipFree(d.p);
         d.p = nullptr;
@@ -185,7 +213,18 @@ struct HipMoeBackend::Impl {
             return ErrorCode::ok;
         }
         if (ErrorCode c = check(); c != ErrorCode::ok) return c;
-        if (it != resident.end()) {  // same id, other data: replaced
+        if (it != resident.end()) {
+            // Tensor ids name one tensor: another shape under a resident id
+            // is rejected, as the reference table's compatible() does
+            // (runtime/cuda/resident_weights.cu:110-114); and an entry this
+            // call already uses is never freed under it (one id given for two
+            // different host tensors in one call).
+            if (it->second.rows != rows || it->second.cols != cols ||
+                it->second.host_bytes != total || it->second.last_use == dense_tick)
+                return ErrorCode::invalid_extent;
+        }
+        if (!ctx) return ErrorCode::backend_unavailable;  // no device attached
+        if (it != resident.end()) {  // same id and shape, other host data: replaced
             (void)hipFree(it->second.p);
             resident_total -= it->second.bytes;
             resident.erase(it);
@@ -255,8 +294,9 @@ struct HipMoeBackend::Impl {
     }
 
     // The layer's shapes this library runs: group size 32 (as the CUDA
-    // backend), hidden and intermediate multiples of 128, a square layer
-    // (down rows = hidden).
+    // backend; another is invalid_mxfp4), hidden and intermediate multiples
+    // of 128, a square layer (down rows = hidden); other shapes are
+    // backend_unavailable, which the methods return as declined.
     static ErrorCode supported(const Mxfp4MlpView& e) {
         for (const Mxfp4WeightView* m : {&e.gate, &e.up, &e.down})
             if (m->group_size != 32) return ErrorCode::invalid_mxfp4;
@@ -270,6 +310,7 @@ struct HipMoeBackend::Impl {
         auto key = std::make_tuple(layer, H, I);
         auto it = banks.find(key);
         if (it != banks.end()) return Result<Bank*>::success(&it->second);
+        if (!ctx) return Result<Bank*>::failure(ErrorCode::backend_unavailable, "no device");
         k3x_hip_layer_desc d{};
         d.hidden = (std::uint32_t)H;
         d.inter = (std::uint32_t)I;
@@ -466,6 +507,10 @@ Result<std::unique_ptr<HipMoeBackend>> make_hip_backend(const HipBackendOptions&
     if (!options.resident_experts) return R::failure(ErrorCode::invalid_extent, "resident_experts");
     auto impl = std::make_unique<HipMoeBackend::Impl>();
     impl->opt = options;
+    if (options.device == HipBackendOptions::kNoDevice) {
+        impl->name = "none (no device attached)";
+        return R::success(std::unique_ptr<HipMoeBackend>(new HipMoeBackend(std::move(impl))));
+    }
     if (int st = k3x_hip_ctx_create(options.device, &impl->ctx)) {
         impl->ctx = nullptr;
         return R::failure(code_of(st), "k3x_hip_ctx_create");
@@ -485,10 +530,11 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_group(std::span<const float> input
         if (!valid_mxfp4_mlp(input.size(), e)) return Result<Outputs>::failure(ErrorCode::invalid_mxfp4);
     if (experts.empty()) return Result<Outputs>::success({});
     for (const auto& e : experts)
-        if (ErrorCode c = Impl::supported(e); c != ErrorCode::ok) return Result<Outputs>::failure(c);
+        if (ErrorCode c = Impl::supported(e); c != ErrorCode::ok)
+            return impl_->shape_failure<Result<Outputs>>(c, "expert shape");
     for (const auto& e : experts)
         if (e.gate.cols != experts.front().gate.cols || e.gate.rows != experts.front().gate.rows)
-            return Result<Outputs>::failure(ErrorCode::backend_unavailable, "mixed shapes");
+            return impl_->decline<Result<Outputs>>("mixed shapes");
     // Each distinct expert once (a layer call takes an expert once per token).
     std::vector<Mxfp4MlpView> uniq;
     std::vector<std::size_t> of(experts.size());
@@ -517,7 +563,8 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_batch(std::span<const float> input
         inputs.size() != batch_size * expert.gate.cols || !valid_situ(situ_beta, situ_linear) ||
         !valid_mxfp4_mlp(expert.gate.cols, expert))
         return Result<Outputs>::failure(ErrorCode::invalid_mxfp4);
-    if (ErrorCode c = Impl::supported(expert); c != ErrorCode::ok) return Result<Outputs>::failure(c);
+    if (ErrorCode c = Impl::supported(expert); c != ErrorCode::ok)
+        return impl_->shape_failure<Result<Outputs>>(c, "expert shape");
     Outputs per;
     const Mxfp4MlpView one[1] = {expert};
     if (ErrorCode c = impl_->grid(layer, inputs, batch_size, one, situ_beta, situ_linear, per);
@@ -559,7 +606,8 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_grid(std::span<const float> inputs
         }
     }
     if (!mul_fits(token_count, out_w)) return R::failure(ErrorCode::invalid_mxfp4);
-    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok) return R::failure(c);
+    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok)
+        return impl_->shape_failure<R>(c, "expert shape");
     Outputs out;
     if (ErrorCode c = impl_->grid(layer, inputs, token_count, experts, situ_beta, situ_linear, out);
         c != ErrorCode::ok)
@@ -604,10 +652,11 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe(std::span<const float> 
         return R::success(std::move(mixed));
     }
     for (const auto& e : experts)
-        if (ErrorCode c = Impl::supported(e); c != ErrorCode::ok) return R::failure(c);
+        if (ErrorCode c = Impl::supported(e); c != ErrorCode::ok)
+            return impl_->shape_failure<R>(c, "expert shape");
     for (const auto& e : experts)
         if (e.gate.cols != experts.front().gate.cols || e.gate.rows != experts.front().gate.rows)
-            return R::failure(ErrorCode::backend_unavailable, "mixed shapes");
+            return impl_->decline<R>("mixed shapes");
     if (!valid_situ(situ_beta, situ_linear)) return R::failure(ErrorCode::invalid_mxfp4);
     std::vector<std::uint32_t> routes(experts.size());
     for (std::size_t k = 0; k < routes.size(); ++k) routes[k] = (std::uint32_t)k;
@@ -647,7 +696,8 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe_tokens(
                 if (same_expert(experts[routes[t * top_k + q]], experts[r]))
                     return R::failure(ErrorCode::invalid_state);
         }
-    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok) return R::failure(c);
+    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok)
+        return impl_->shape_failure<R>(c, "expert shape");
     std::vector<float> out(token_count * H);
     for (std::size_t t0 = 0; t0 < token_count; t0 += kTokensPerCall) {
         const std::size_t Tc = std::min(kTokensPerCall, token_count - t0);
@@ -784,7 +834,8 @@ Result<OfficialMoeRoutePrepareResult> HipMoeBackend::prepare_official_moe_route(
         !finite_bf16_words(wv.post_norm.values) || !finite_bf16_words(wv.router.values))
         return R::failure(ErrorCode::invalid_extent);
     const std::size_t E = wv.router.rows;
-    if (H % 128 || H > (1u << 20) || E > (1u << 20)) return R::failure(ErrorCode::backend_unavailable);
+    if (H % 128 || H > (1u << 20) || E > (1u << 20)) return m.decline<R>("hidden / router shape");
+    if (!m.ctx) return R::failure(ErrorCode::backend_unavailable, "no device");
     // A new preparation replaces a pending one (backend_cuda.cu:3609-3616).
     m.prepared_active = false;
     auto& rt = m.official_routes[layer];
@@ -933,11 +984,12 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
     if (out_w != L) return bad();
     if (H % 128 || L % 128 || I % 128 || Is % 128 || experts.size() > kMaxSlotsPerToken ||
         experts.size() > m.opt.resident_experts)
-        return R::failure(ErrorCode::backend_unavailable);
+        return m.decline<R>("official layer shape");
     if (!finite_bf16_words(wv.routed_down.values) || !finite_bf16_words(wv.routed_up.values) ||
         !finite_bf16_words(wv.routed_norm.values) || !finite_bf16_words(wv.shared.gate.values) ||
         !finite_bf16_words(wv.shared.up.values) || !finite_bf16_words(wv.shared.down.values))
         return bad();
+    if (!m.ctx) return R::failure(ErrorCode::backend_unavailable, "no device");
     if (prepared) m.prepared_active = false;  // consumed (backend_cuda.cu:3875-3878)
     // The FFN object and its latent experts.
     const auto key = std::make_tuple(layer, H, L, I, Is);
@@ -1042,7 +1094,7 @@ Result<std::vector<float>> HipMoeBackend::dense_matvec(std::span<const float> in
     if (!valid_dense(input.size(), weight)) return R::failure(ErrorCode::invalid_extent);
     if (!weight.rows || !weight.cols) return R::success(std::vector<float>(weight.rows, 0.0f));
     if (weight.rows > (1u << 24) || weight.cols > (1u << 24))
-        return R::failure(ErrorCode::backend_unavailable);
+        return impl_->decline<R>("matrix size");
     Impl& m = *impl_;
     ++m.dense_tick;
     const void* W = nullptr;
@@ -1077,7 +1129,7 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> in
         weight.scales.size() != weight.rows * weight.cols / weight.group_size)
         return R::failure(ErrorCode::invalid_mxfp4);
     if (weight.group_size != 32 || weight.rows > (1u << 24) || weight.cols > (1u << 24))
-        return R::failure(ErrorCode::backend_unavailable, "group size 32 only");
+        return impl_->decline<R>("group size 32 only");
     Impl& m = *impl_;
     ++m.dense_tick;
     auto scales_ok = [&] {
@@ -1143,10 +1195,12 @@ Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> 
                                                          std::optional<float> situ_linear,
                                                          std::uint32_t, ProfilePhase) {
     using R = Result<std::vector<float>>;
-    if (!valid_dense_mlp(input.size(), weights)) return R::failure(ErrorCode::invalid_extent);
+    if (!valid_dense_mlp(input.size(), weights) ||
+        !checks::consistent_ids({&weights.gate, &weights.up, &weights.down}))
+        return R::failure(ErrorCode::invalid_extent);
     const std::size_t H = input.size(), I = weights.gate.rows, O = weights.down.rows;
     if (!H || H > (1u << 24) || I > (1u << 24) || O > (1u << 24))
-        return R::failure(ErrorCode::backend_unavailable);
+        return impl_->decline<R>("matrix size");
     Impl& m = *impl_;
     ++m.dense_tick;
     auto none = [] { return ErrorCode::ok; };
@@ -1188,12 +1242,17 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
         return bad();
     const std::size_t H = input.size(), L = weights.routed_down.rows,
                       W = experts.front().down.rows, I = experts.front().gate.rows;
+    // (valid_resident_layer rejects a tensor id given twice, as the
+    // reference does, so no resident entry is replaced under this call.)
+    const DenseWeightView norm_view{weights.routed_norm.tensor_id, weights.routed_norm.values, 1,
+                                    weights.routed_norm.values.size()};
     // Shapes the device path runs: routed width = latent (a square expert
     // bank), widths multiples of 128, one layer call of at most 64 slots.
     if (W != L || experts.size() > kMaxSlotsPerToken || H > (1u << 24) ||
         weights.shared.gate.rows > (1u << 24))
-        return R::failure(ErrorCode::backend_unavailable);
-    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok) return R::failure(c);
+        return impl_->decline<R>("latent layer shape");
+    if (ErrorCode c = Impl::supported(experts.front()); c != ErrorCode::ok)
+        return impl_->shape_failure<R>(c, "expert shape");
     Impl& m = *impl_;
     auto bypass = [&] {
         ++m.stats.resident_layer_fallbacks;
@@ -1208,8 +1267,6 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     if (ErrorCode c = m.admit(*bank.value(), experts, slot); c != ErrorCode::ok) return R::failure(c);
     // The six dense weights resident, or the bypass.
     ++m.dense_tick;
-    const DenseWeightView norm_view{weights.routed_norm.tensor_id, weights.routed_norm.values, 1,
-                                    W};
     const DenseWeightView* dv[6] = {&weights.routed_down, &norm_view,          &weights.routed_up,
                                     &weights.shared.gate, &weights.shared.up, &weights.shared.down};
     const void* dp[6] = {};
@@ -1265,9 +1322,13 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
 }
 
 HipBackendStats HipMoeBackend::runtime_stats() const noexcept {
-    HipBackendStats s = impl_->stats;
+    Impl& m = *impl_;
+    HipBackendStats s = m.stats;
     k3x_hip_stats cs{};
-    if (k3x_hip_ctx_stats(impl_->ctx, &cs) == 0) s.kernel_launches = cs.kernel_launches;
+    if (m.ctx && k3x_hip_ctx_stats(m.ctx, &cs) == 0) s.kernel_launches = cs.kernel_launches;
+    s.device_bytes = m.device_bytes(cs.scratch_bytes);
+    m.stats.peak_device_bytes = std::max(m.stats.peak_device_bytes, s.device_bytes);
+    s.peak_device_bytes = m.stats.peak_device_bytes;
     return s;
 }
 

@@ -72,11 +72,22 @@ public:
     static Result failure(ErrorCode code, std::string message = {}) {
         return Result(code, std::move(message));
     }
+    // A shape (or size) the device path does not run, found by the argument
+    // checks before anything was uploaded or launched: error() is
+    // backend_unavailable, as for a device failure, and declined() tells the
+    // two apart (a caller may compute a declined call elsewhere; a device
+    // failure is a failure).
+    static Result declined_shape(std::string message = {}) {
+        Result r(ErrorCode::backend_unavailable, std::move(message));
+        r.declined_ = true;
+        return r;
+    }
     explicit operator bool() const { return value_.has_value(); }
     T& value() { return *value_; }
     const T& value() const { return *value_; }
     ErrorCode error() const { return error_; }
     const std::string& message() const { return message_; }
+    bool declined() const { return declined_; }
 
 private:
     explicit Result(T value) : value_(std::move(value)) {}
@@ -84,6 +95,7 @@ private:
     std::optional<T> value_;
     ErrorCode error_{ErrorCode::ok};
     std::string message_;
+    bool declined_ = false;
 };
 
 enum class ProfilePhase { prefill, decode };  // runtime/include/k3x/profile.hpp:11
@@ -206,6 +218,11 @@ struct ExpertMajorBlockMoe {
 };
 
 struct HipBackendOptions {
+    // HIP device index; kNoDevice builds a backend with no device attached,
+    // whose methods run their argument and shape checks and then fail with
+    // backend_unavailable (not declined) where they would touch the device
+    // (host-only tests of the checks and of the declined-shape contract).
+    static constexpr int kNoDevice = -1;
     int device = 0;
     // Bank slots per (layer, hidden, intermediate) shape; each slot holds
     // one expert (hidden * intermediate * 3 * 17 / 32 bytes, 23.4 MB at
@@ -227,6 +244,11 @@ struct HipBackendStats {
     std::uint64_t weight_h2d_bytes = 0;
     std::uint64_t dense_uploads = 0;             // dense / single-matrix uploads
     std::uint64_t resident_layer_fallbacks = 0;  // latent layer calls returned executed=false
+    std::uint64_t declined_shapes = 0;   // calls declined by shape before any device work
+    // Device memory this backend holds now (banks, resident dense weights,
+    // the context's scratch, the per-call buffers) and its peak.
+    std::uint64_t device_bytes = 0;
+    std::uint64_t peak_device_bytes = 0;
 };
 
 class HipMoeBackend {

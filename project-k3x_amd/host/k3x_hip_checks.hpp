@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
 #include <cstddef>
 #include <cstdint>
 #include <limits>
@@ -63,6 +64,20 @@ inline bool valid_dense_size(std::size_t input_size, const DenseWeightView& w) {
 inline bool valid_dense_mlp(std::size_t input_size, const DenseMlpView& m) {
     return valid_dense(input_size, m.gate) && valid_dense(input_size, m.up) && m.gate.rows != 0 &&
            m.gate.rows == m.up.rows && valid_dense_size(m.gate.rows, m.down);
+}
+
+// Tensor ids name one tensor each: views of one call that share a nonzero id
+// must be the same tensor (same data, same shape), as the reference's
+// resident table keys them (runtime/cuda/resident_weights.cu:107-114).
+inline bool consistent_ids(std::initializer_list<const DenseWeightView*> views) {
+    for (auto a = views.begin(); a != views.end(); ++a)
+        for (auto b = views.begin(); b != a; ++b)
+            if ((*a)->tensor_id && (*a)->tensor_id == (*b)->tensor_id &&
+                ((*a)->values.data() != (*b)->values.data() ||
+                 (*a)->values.size() != (*b)->values.size() || (*a)->rows != (*b)->rows ||
+                 (*a)->cols != (*b)->cols))
+                return false;
+    return true;
 }
 
 inline bool all_finite(std::span<const float> v) {

@@ -42,3 +42,15 @@ def test_factory_fails_closed_without_a_device():
     assert os.path.exists(EXE), "tests/cpp/test_hip_backend not built (__graft_entry__.build())"
     r = subprocess.run([EXE], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2 and "BACKEND_UNAVAILABLE" in r.stdout, (r.returncode, r.stdout)
+
+
+def test_host_checks_without_a_device():
+    """Argument and shape contract on a backend with no device attached
+    (tests/cpp/host_checks_driver.cpp): declined shapes are marked declined
+    before any device work; a device failure is not; one tensor id for two
+    tensors of a call is rejected before any upload."""
+    exe = os.path.join(ROOT, "tests", "cpp", "host_checks_driver")
+    assert os.path.exists(exe), "tests/cpp/host_checks_driver not built (__graft_entry__.build())"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, (r.returncode, r.stdout)
+    assert r.stdout.count(": ok") == 4, r.stdout

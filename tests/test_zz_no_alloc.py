@@ -4,7 +4,10 @@ The no-allocation entry point runs the same kernels over a fixed device
 array instead of the context's grow-only scratch, so its results must be
 bit-identical: two calls in a row, the second with fewer tokens, on the
 decode path (T <= 4) and on the general path, then a call whose buffers do
-not fit the array, which is refused before anything is enqueued.
+not fit the array, which is refused before anything is enqueued.  Each
+no-allocation call runs first on its context (before any allocating call
+could have grown the context's scratch) and must leave the context's
+scratch (0 on the first call) and the bank's bytes unchanged.
 """
 from __future__ import annotations
 
@@ -29,6 +32,7 @@ def say(msg: str) -> None:
 
 def call(k3x_amd, ctx, bank, cfg, x_bits, flags, noalloc):
     dev = "cuda:0"
+    scratch0, bank_bytes0 = ctx.stats().scratch_bytes, bank.bytes()
     T, H, I, E, K, S = cfg
     x = torch.from_numpy(np.ascontiguousarray(x_bits).view(np.int16)).to(dev)
     out = torch.full((T, H), -1, dtype=torch.int16, device=dev)
@@ -47,6 +51,11 @@ def call(k3x_amd, ctx, bank, cfg, x_bits, flags, noalloc):
     assert fwd(ctx, bank, params, x, out, taps) == 0
     assert ctx.synchronize() == 0
     torch.cuda.synchronize()
+    if noalloc:
+        # Nothing allocated by the call: the context's grow-only scratch and
+        # the bank's device bytes are unchanged.
+        assert ctx.stats().scratch_bytes == scratch0, "context scratch grew"
+        assert bank.bytes() == bank_bytes0, "bank grew"
     got = {k: v.cpu().numpy() for k, v in taps.items()}
     got["out"] = out.cpu().numpy()
     return got
@@ -62,6 +71,7 @@ def test_noalloc_matches_forward(general, oracle):
     bank = k3x_amd.Bank(ctx, k3x_amd.LayerShape(H, I, E, S))
     bank.fill_synthetic(0x5107, 119, 123, 0.02, 0.1, 0.02, 1.0)
     flags = k3x_amd.FLAG_GENERAL_PATH if general else 0
+    assert ctx.stats().scratch_bytes == 0  # a fresh context: no scratch yet
     for i, T in enumerate((4, 2) if not general else (40, 9)):
         x = oracle.synth_normal_bf16(oracle.stream_key(0xA110C + i, 12 << 32), T * H,
                                      1.0).reshape(T, H)
