@@ -98,20 +98,33 @@ class SynthLayer:
 
     def expert(self, e: int) -> dict:
         if e not in self._experts:
-            o, c = self.o, self.cfg
-            key = lambda kind: o.stream_key(c.seed, sid(kind, e))
-            n = c.inter * c.hidden
-            self._experts[e] = dict(
-                gate_packed=o.synth_codes(key(STREAM_GATE_CODES), n // 2),
-                gate_scales=o.synth_scales(key(STREAM_GATE_SCALES), n // 32, c.scale_lo,
-                                           c.scale_hi),
-                up_packed=o.synth_codes(key(STREAM_UP_CODES), n // 2),
-                up_scales=o.synth_scales(key(STREAM_UP_SCALES), n // 32, c.scale_lo, c.scale_hi),
-                down_packed=o.synth_codes(key(STREAM_DOWN_CODES), n // 2),
-                down_scales=o.synth_scales(key(STREAM_DOWN_SCALES), n // 32, c.scale_lo,
-                                           c.scale_hi),
-            )
+            self._experts[e] = self._make_expert(e)
         return self._experts[e]
+
+    def prefetch(self, experts, threads: int = 16) -> None:
+        """Generates the given experts ahead of use on `threads` host threads
+        (the generator's C calls run without the interpreter lock)."""
+        from concurrent.futures import ThreadPoolExecutor
+        todo = sorted({int(e) for e in experts} - set(self._experts))
+        if not todo:
+            return
+        with ThreadPoolExecutor(max(1, threads)) as ex:
+            for e, d in zip(todo, ex.map(self._make_expert, todo)):
+                self._experts[e] = d
+
+    def _make_expert(self, e: int) -> dict:
+        o, c = self.o, self.cfg
+        key = lambda kind: o.stream_key(c.seed, sid(kind, e))
+        n = c.inter * c.hidden
+        return dict(
+            gate_packed=o.synth_codes(key(STREAM_GATE_CODES), n // 2),
+            gate_scales=o.synth_scales(key(STREAM_GATE_SCALES), n // 32, c.scale_lo,
+                                       c.scale_hi),
+            up_packed=o.synth_codes(key(STREAM_UP_CODES), n // 2),
+            up_scales=o.synth_scales(key(STREAM_UP_SCALES), n // 32, c.scale_lo, c.scale_hi),
+            down_packed=o.synth_codes(key(STREAM_DOWN_CODES), n // 2),
+            down_scales=o.synth_scales(key(STREAM_DOWN_SCALES), n // 32, c.scale_lo, c.scale_hi),
+        )
 
     def x_bits(self) -> np.ndarray:
         c = self.cfg

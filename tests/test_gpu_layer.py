@@ -204,59 +204,124 @@ def check_routing(oracle, layer, got, x_bits):
     return xn, ids, w, csr
 
 
+def check_threads() -> int:
+    """Host threads for the checker's per-expert work (the box's CPU share)."""
+    import os
+    return max(1, min(16, os.cpu_count() or 1))
+
+
 def check_layer(oracle, layer, got, x_bits=None, tokens_checked=None, report=None):
     """Layer outputs against the oracle (see the module docstring); `report`,
-    when given, receives the figures the checks rest on."""
+    when given, receives the figures the checks rest on.  The checked pairs
+    are grouped by expert and each expert's oracle work (its pairs' double
+    GEMVs, its decoded down projection and the bound products over all its
+    pairs at once) runs on a pool of host threads, so that every token of a
+    verification window, or hundreds of a prefill chunk, can be checked."""
+    from collections import defaultdict
+    from concurrent.futures import ThreadPoolExecutor
     cfg = layer.cfg
     x_bits = layer.x_bits() if x_bits is None else x_bits
-    T, K = x_bits.shape[0], cfg.top_k
+    T, K, H, I = x_bits.shape[0], cfg.top_k, cfg.hidden, cfg.inter
     P = T * K
     xn, ids, w, csr = check_routing(oracle, layer, got, x_bits)
-    # Per-pair activations and outputs.
-    tokens = range(T) if tokens_checked is None else tokens_checked
-    act_ref, y_ref = layer.pair_outputs(xn, ids, tokens)
+    tokens = list(range(T)) if tokens_checked is None else sorted(set(tokens_checked))
     act_gpu = got["act"]  # CSR rows
-    # Activations: the bf16 roundings of the GPU's fp32 sums and the oracle's
-    # double sums agree except near rounding boundaries (one ulp apart) and
-    # on values near zero, where the absolute accumulation error of gate/up
-    # (~2^-18 of the row's scale) spans more than one ulp; a layout or
-    # indexing error would be O(1) of the row's scale.
-    worst_act, multi = 0, 0
-    for r in range(P):
-        t, s = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
-        if t not in tokens:
-            continue
-        ref_bits = (act_ref[t, s].view(np.uint32) >> 16).astype(np.uint16)
-        d = ulp_diff_bf16(act_gpu[r], ref_bits)
-        worst_act = max(worst_act, int(d.max()))
-        frac = np.count_nonzero(d) / d.size
-        assert frac < 0.02, f"pair ({t},{s}): {frac:.4f} of activations off"
-        big = d > 1
-        multi += int(big.sum())
-        if big.any():
-            scale = float(np.abs(act_ref[t, s]).max())
-            diff = np.abs(bf16_to_f32(act_gpu[r]) - act_ref[t, s])[big]
-            assert (np.abs(act_ref[t, s][big]) <= 2.0 ** -6 * scale).all()
-            assert (diff <= 2.0 ** -12 * scale).all()
-    say(f"activations: max {worst_act} bf16 ulp, {multi} elements over 1 ulp (all near zero)")
-    if "expert_out" in got:
-        # Down projection on the GPU's own activations (isolates the GEMM).
-        for r in range(P):
-            t, s = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
-            if t not in tokens:
-                continue
-            ex = layer.expert(int(ids[t, s]))
-            a = bf16_to_f32(act_gpu[r])
-            st, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], cfg.hidden,
-                                        cfg.inter, 32)
-            yd = (W.astype(np.float64) @ a.astype(np.float64))
-            # fp32 accumulation over K terms: |error| <= K * 2^-24 * sum|a_k w_k|
+    row_of = {(int(csr["pair_token"][r]), int(csr["pair_slot"][r])): r for r in range(P)}
+    by_expert = defaultdict(list)
+    for t in tokens:
+        for s_ in range(K):
+            by_expert[int(ids[t, s_])].append((t, s_))
+    threads = check_threads()
+    layer.prefetch(by_expert.keys(), threads)
+
+    def expert_work(e):
+        """Activations of expert e's checked pairs against the oracle's, its
+        down projection on the GPU's activations (when the per-pair outputs
+        were tapped), and the propagated-bound terms |W| |da| and |W| |a|."""
+        ex = layer.expert(e)
+        pairs = by_expert[e]
+        refs, a_cols, da_cols, stats = [], [], [], [0, 0]
+        for (t, s_) in pairs:
+            st, act_ref, y_ref = oracle.expert_ffn(xn[t], ex, H, I, cfg.glu, cfg.beta,
+                                                   cfg.linear, round_act=True)
+            assert st == 0, st
+            r = row_of[(t, s_)]
+            # Activations: the bf16 roundings of the GPU's fp32 sums and the
+            # oracle's double sums agree except near rounding boundaries (one
+            # ulp apart) and on values near zero, where the absolute
+            # accumulation error of gate/up (~2^-18 of the row's scale) spans
+            # more than one ulp; a layout or indexing error would be O(1) of
+            # the row's scale.
+            ref_bits = (act_ref.view(np.uint32) >> 16).astype(np.uint16)
+            d = ulp_diff_bf16(act_gpu[r], ref_bits)
+            stats[0] = max(stats[0], int(d.max()))
+            frac = np.count_nonzero(d) / d.size
+            assert frac < 0.02, f"pair ({t},{s_}): {frac:.4f} of activations off"
+            big = d > 1
+            stats[1] += int(big.sum())
+            if big.any():
+                scale = float(np.abs(act_ref).max())
+                diff = np.abs(bf16_to_f32(act_gpu[r]) - act_ref)[big]
+                assert (np.abs(act_ref[big]) <= 2.0 ** -6 * scale).all()
+                assert (diff <= 2.0 ** -12 * scale).all()
+            a = bf16_to_f32(act_gpu[r]).astype(np.float64)
+            a_cols.append(a)
+            da_cols.append(np.abs(a - act_ref.astype(np.float64)))
+            refs.append(y_ref)
+        st, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], H, I, 32)
+        assert st == 0
+        W64 = W.astype(np.float64)
+        Wa = np.abs(W64)
+        A = np.stack(a_cols, axis=1)
+        P_da = Wa @ np.stack(da_cols, axis=1)
+        P_a = Wa @ np.abs(A)
+        if "expert_out" in got:
+            # Down projection on the GPU's own activations (isolates the
+            # GEMM): fp32 accumulation over K terms is within K 2^-24 sum|w a|
             # in the worst case; 2^-16 (K = 2048 -> 2^-13 worst, ~2^-18.5
             # typical) flags any indexing or layout error, which is O(1).
-            bound = 2.0 ** -16 * (np.abs(W).astype(np.float64) @ np.abs(a).astype(np.float64))
-            err = np.abs(got["expert_out"][t, s].astype(np.float64) - yd)
-            assert (err <= bound + 1e-30).all(), f"pair ({t},{s}): max excess {(err - bound).max()}"
+            Y = W64 @ A
+            for j, (t, s_) in enumerate(pairs):
+                err = np.abs(got["expert_out"][t, s_].astype(np.float64) - Y[:, j])
+                excess = err - 2.0 ** -16 * P_a[:, j]
+                assert (excess <= 1e-30).all(), f"pair ({t},{s_}): max excess {excess.max()}"
+        return {pair: (refs[j], P_da[:, j], P_a[:, j]) for j, pair in enumerate(pairs)}, stats
+
+    with ThreadPoolExecutor(threads) as pool:
+        done = list(pool.map(expert_work, sorted(by_expert)))
+    per_pair, worst_act, multi = {}, 0, 0
+    for res, stats in done:
+        per_pair.update(res)
+        worst_act = max(worst_act, stats[0])
+        multi += stats[1]
+    say(f"activations of {len(per_pair)} pairs over {len(by_expert)} experts: max {worst_act} "
+        f"bf16 ulp, {multi} elements over 1 ulp (all near zero)")
+    if "expert_out" in got:
         say("down projection within the fp32 accumulation bound on GPU activations")
+
+    # The shared expert of every checked token: the oracle's output and
+    # activation, and the bound terms of the activation differences.
+    Wd = None
+    if cfg.shared_inter:
+        sg, su, sd = layer.shared
+        Wd = np.abs(bf16_to_f32(sd)).astype(np.float64)
+
+    def shared_work(t):
+        if not cfg.shared_inter:
+            return np.zeros(H, np.float32), np.zeros(H), np.zeros(H)
+        sh = layer.shared_out(xn, [t])[t]
+        sa_ref = round_bf16_np(oracle, xn[t], sg, su, cfg)
+        sa_gpu = bf16_to_f32(got["shared_act"][t]).astype(np.float64)
+        # One bf16 ulp, or near zero (as the routed activations above).
+        close_acts(got["shared_act"][t][None], bf16_bits(sa_ref.astype(np.float32))[None])
+        sb = Wd @ np.abs(sa_gpu - sa_ref) + 2.0 ** -15 * (Wd @ np.abs(sa_gpu))
+        np.testing.assert_array_less(np.abs(got["shared_out"][t] - sh) - sb,
+                                     1e-30 + 4 * 2.0 ** -24 * np.abs(sh))
+        return sh, sb, np.abs(sh.astype(np.float64))
+
+    with ThreadPoolExecutor(threads) as pool:
+        shared = dict(zip(tokens, pool.map(shared_work, tokens)))
+
     # Against the fully independent CPU layer, element by element, with a
     # bound that accounts for every source of difference: the activation
     # elements whose bf16 rounding differs (GPU fp32 MFMA sums vs the
@@ -265,42 +330,23 @@ def check_layer(oracle, layer, got, x_bits=None, tokens_checked=None, report=Non
     # through |W_down|; fp32 accumulation of the down projections (2^-15 of
     # sum |w_rk a_k|; K = 2048 gives at most 2^-13, typically ~2^-18.5); and
     # the float rounding of the slot-ordered combine on both sides.
-    shared = layer.shared_out(xn, tokens)
-    out_ref = layer.combine(y_ref, w, shared, tokens)
-    row_of = {(int(csr["pair_token"][r]), int(csr["pair_slot"][r])): r for r in range(P)}
     within = total = 0
     u = 2.0 ** -24
     for t in tokens:
-        bound = np.zeros(cfg.hidden)
-        mag = np.zeros(cfg.hidden)
+        y_t = np.stack([per_pair[(t, s_)][0] for s_ in range(K)])
+        sh, sb, smag = shared[t]
+        out_ref = oracle.ordered_mix(y_t, w[t]) + sh
+        bound = sb.copy()
+        mag = smag.copy()
         for s_ in range(K):
-            ex = layer.expert(int(ids[t, s_]))
-            _, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], cfg.hidden,
-                                       cfg.inter, 32)
-            Wa = np.abs(W).astype(np.float64)
-            a_gpu = bf16_to_f32(act_gpu[row_of[(t, s_)]]).astype(np.float64)
-            da = np.abs(a_gpu - act_ref[t, s_].astype(np.float64))
+            y_ref, p_da, p_a = per_pair[(t, s_)]
             ws = abs(float(w[t, s_]))
-            bound += ws * (Wa @ da + 2.0 ** -15 * (Wa @ np.abs(a_gpu)))
-            mag += ws * np.abs(y_ref[t, s_].astype(np.float64))
-        if cfg.shared_inter:
-            from oracle import GLU_SWIGLU
-            sg, su, sd = layer.shared
-            sa_ref = round_bf16_np(oracle, xn[t], sg, su, cfg)
-            sa_gpu = bf16_to_f32(got["shared_act"][t]).astype(np.float64)
-            dsa = np.abs(sa_gpu - sa_ref)
-            # One bf16 ulp, or near zero (as the routed activations above).
-            close_acts(got["shared_act"][t][None], bf16_bits(sa_ref.astype(np.float32))[None])
-            Wd = np.abs(bf16_to_f32(sd)).astype(np.float64)
-            bound += Wd @ dsa + 2.0 ** -15 * (Wd @ np.abs(sa_gpu))
-            mag += np.abs(shared[t].astype(np.float64))
-            np.testing.assert_array_less(
-                np.abs(got["shared_out"][t] - shared[t]) - (Wd @ dsa + 2.0 ** -15 * (Wd @ np.abs(sa_gpu))),
-                1e-30 + 4 * u * np.abs(shared[t]))
-        bound += 2 * (K + 1) * u * mag + 2 * u * np.abs(out_ref[t])
-        err = np.abs(got["out_f32"][t].astype(np.float64) - out_ref[t])
+            bound += ws * (p_da + 2.0 ** -15 * p_a)
+            mag += ws * np.abs(y_ref.astype(np.float64))
+        bound += 2 * (K + 1) * u * mag + 2 * u * np.abs(out_ref)
+        err = np.abs(got["out_f32"][t].astype(np.float64) - out_ref)
         assert (err <= bound).all(), f"token {t}: {int((err > bound).sum())} outputs beyond the bound"
-        ok = np.abs(got["out_f32"][t] - out_ref[t]) <= ATOL + RTOL * np.abs(out_ref[t])
+        ok = np.abs(got["out_f32"][t] - out_ref) <= ATOL + RTOL * np.abs(out_ref)
         within += int(ok.sum())
         total += ok.size
         assert np.array_equal(got["out"][t], bf16_bits(got["out_f32"][t]))
@@ -549,9 +595,9 @@ def tokens_by_row_class(got, K, classes):
 
 def test_c4_verification_window(hip, oracle, parity_report):
     """Config 4: T=64, Zipf-skewed routing (0..~40 rows per expert).  Routing
-    and grouping bit-exact for all 1024 pairs; activations and outputs on
-    tokens that cover the busiest expert, a mid-sized one and single-row
-    experts, plus the first and last token."""
+    and grouping bit-exact for all 1024 pairs; activations and outputs of
+    every token (their pairs cover the busiest expert, mid-sized ones and
+    single-row experts)."""
     from synth import CONFIGS, SynthLayer
     k3x_amd, ctx = hip
     cfg = CONFIGS[4]
@@ -565,10 +611,9 @@ def test_c4_verification_window(hip, oracle, parity_report):
     picked = tokens_by_row_class(got, cfg.top_k, {
         "busiest": (1 << 30, big), "mid_8_to_29": (1 << 30, lambda r, l: 8 <= r < 30),
         "two_to_seven": (1 << 30, lambda r, l: 2 <= r < 8), "single": (1 << 30, lambda r, l: r == 1)})
-    tokens = sorted(set(picked.values()) | {0, cfg.tokens - 1})
-    say(f"c4 tokens checked {tokens} for row classes {picked}")
+    say(f"c4 row classes {picked}; checking all {cfg.tokens} tokens")
     assert len(picked) == 4
-    check_layer(oracle, layer, got, tokens_checked=tokens, report=parity_report)
+    check_layer(oracle, layer, got, tokens_checked=range(cfg.tokens), report=parity_report)
     bank.close()
 
 
@@ -608,9 +653,10 @@ def test_verification_window_rows(hip, oracle, name, parity_report):
 def test_c5_prefill_chunk(hip, oracle, parity_report):
     """Config 5: T=2048 prefill chunk.  Device Top-16 ids equal the ids the
     reference's CPU functions chose (golden fixture); grouping bit-exact;
-    outputs on tokens chosen so that a checked pair falls in each work-item
-    class of the wide grouped GEMM (128-row chunks: full, 97-127, 65-96 and
-    at most 64 rows; partial last chunks), plus the first and last token;
+    outputs of every 16th token (128 tokens, 2048 pairs) plus tokens chosen
+    so that a checked pair falls in each work-item class of the wide grouped
+    GEMM (128-row chunks: full, 97-127, 65-96 and at most 64 rows; partial
+    last chunks) and the last token;
     permuting the tokens permutes the output bit for bit (rows of the grouped
     GEMMs are independent)."""
     import os
@@ -630,9 +676,9 @@ def test_c5_prefill_chunk(hip, oracle, parity_report):
         "partial_97_127": (ch, lambda r, last: 96 < r < ch),
         "partial_65_96": (ch, lambda r, last: 64 < r <= 96),
         "partial_le_64": (ch, lambda r, last: r <= 64 and last)})
-    tokens = sorted(set(picked.values()) | {0, cfg.tokens - 1})
-    say(f"c5 tokens checked {tokens} for item classes {picked}")
-    assert len(picked) == 4
+    tokens = sorted(set(picked.values()) | set(range(0, cfg.tokens, 16)) | {cfg.tokens - 1})
+    say(f"c5: {len(tokens)} tokens checked, item classes {picked}")
+    assert len(picked) == 4 and len(tokens) >= 128
     check_layer(oracle, layer, got, x, tokens_checked=tokens, report=parity_report)
     perm = np.random.default_rng(5).permutation(cfg.tokens)
     gp = run_layer(k3x_amd, ctx, cfg, bank, x[perm], per_pair=False)
