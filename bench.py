@@ -72,10 +72,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the GPU legs of configs 1, 2 and 4")
-    ap.add_argument("--cpu-all", action="store_true",
-                    help="CPU baseline also on config 4 (full, N threads; one thread on a "
-                         "1/16 token sample) and a 1/16 token sample of config 5 (several "
-                         "minutes of CPU work)")
+    ap.add_argument("--cpu-quick", action="store_true",
+                    help="CPU baseline on configs 1-3 only (by default also config 4 in full "
+                         "at N threads, one thread on a 1/16 token sample, and a labelled "
+                         "1/16 token sample of config 5)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass: a 256 MiB device copy "
                          "(counter calibration), then decode layer calls")
@@ -291,7 +291,7 @@ def main() -> int:
     if not args.no_storage:
         result["storage"] = storage(ctx, k3x_amd, torch, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"], result["cpu_configs"] = cpu_baseline(args.cpu_all)
+        result["cpu_baseline"], result["cpu_configs"] = cpu_baseline(not args.cpu_quick)
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0
@@ -744,6 +744,7 @@ def cpu_baseline(all_configs: bool) -> tuple[dict, dict]:
             st, ids, _, _ = o.route(o.router_logits(layer.router, xn, ORDER_SEQ), layer.bias,
                                     cfg.top_k, cfg.renorm, cfg.routed_scale, SIGMOID_REF)
             need |= {int(e) for e in ids}
+        layer.prefetch(need, n_thr)
         experts = [layer.expert(e) if e in need else None for e in range(cfg.experts)]
         row = {"tokens": T, "pairs": T * cfg.top_k, "experts_touched": len(need)}
         for n in threads:
@@ -763,6 +764,9 @@ def cpu_baseline(all_configs: bool) -> tuple[dict, dict]:
         table[f"c{cid}"] = run(cid)
         table[f"c{cid}"]["sample"] = "full layer call"
     if all_configs:
+        # Config 4 in full at N threads (one thread on every 16th token,
+        # x16); config 5 on every 16th token at N threads (x16, labelled
+        # derived).
         table["c4"] = run(4, threads=(n_thr,))
         table["c4"]["sample"] = "full layer call, N threads"
         sub = run(4, tokens=list(range(0, 64, 16)), threads=(1,))

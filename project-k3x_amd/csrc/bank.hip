@@ -126,7 +126,9 @@ __global__ void fill_const_f32(size_t n, float v, float* __restrict__ out) {
 // of 16-byte words, U words a thread in flight per step (indices clamped,
 // so no load sits behind a branch), and every wave XORs its words into
 // *fold once.  8192 workgroups of 512 threads, U = 4: the best of a sweep
-// over 256..8192 workgroups and 4..16 words in flight on MI355X.
+// over 256..8192 workgroups and 4..16 words in flight on MI355X.  The loads
+// are non-temporal (data read once, not kept in the L2 / MALL): 6.80 TB/s
+// against 6.27 TB/s for plain loads on 4 GiB.
 constexpr uint32_t kStreamReadBlocks = 8192, kStreamReadThreads = 512;
 __global__ __launch_bounds__(kStreamReadThreads) void stream_read_kernel(
     const uint4* __restrict__ p, size_t n16, size_t per_block, uint32_t* fold) {
@@ -137,7 +139,11 @@ __global__ __launch_bounds__(kStreamReadThreads) void stream_read_kernel(
     for (size_t i = b0 + threadIdx.x; i < b1; i += (size_t)kStreamReadThreads * U) {
         uint4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = p[min(i + (size_t)kStreamReadThreads * u, b1 - 1)];
+        for (int u = 0; u < U; ++u) {
+            const u32x4 w = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(p + min(i + (size_t)kStreamReadThreads * u, b1 - 1)));
+            v[u] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u)
             if (i + (size_t)kStreamReadThreads * u < b1) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
