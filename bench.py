@@ -82,10 +82,22 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short workload for a rocprofv3 --pmc pass over the T=2048 prefill "
                          "chunk: the calibration copy, then --steps prefill layer calls")
+    ap.add_argument("--pmc-c4", action="store_true",
+                    help="short workload for a rocprofv3 --pmc pass over the T=64 "
+                         "verification window (config 4's Zipf-skewed router on one bank): "
+                         "the calibration copy, then --steps layer calls on one stream")
+    ap.add_argument("--scaled-fp4", action="store_true",
+                    help="with --pmc-prefill: the routed experts on the scaled FP4 MFMA "
+                         "(K3X_FLAG_SCALED_FP4)")
     ap.add_argument("--counters-from", nargs="+", metavar="DIR",
-                    help="summarise rocprofv3 --pmc passes over --pmc-prefill (per-kernel "
-                         "medians, HBM bytes from FETCH_SIZE / WRITE_SIZE against the "
-                         "calibration copy) into " + "profiles/prefill_c5_counters.json")
+                    help="summarise rocprofv3 --pmc passes over one of the --pmc-* workloads "
+                         "(per-kernel medians, HBM bytes from FETCH_SIZE / WRITE_SIZE against "
+                         "the calibration copy, the memory-unit busy share) into "
+                         "--counters-out")
+    ap.add_argument("--counters-out", default=os.path.join("profiles", "prefill_c5_counters.json"),
+                    help="JSON file (relative to the repo root) --counters-from writes")
+    ap.add_argument("--counters-workload", default="bench.py --pmc-prefill (c5 prefill chunk, "
+                    "T=2048, one stream)", help="workload named in the --counters-out file")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the FETCH_SIZE and WRITE_SIZE pass outputs into " + TRAFFIC_JSON_REL)
     return ap.parse_args()
@@ -97,7 +109,8 @@ def main() -> int:
         print(json.dumps(traffic_from(*args.traffic_from)))
         return 0
     if args.counters_from:
-        print(json.dumps(counters_from(args.counters_from)))
+        print(json.dumps(counters_from(args.counters_from, args.counters_out,
+                                       args.counters_workload)))
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the layer and its resident "
@@ -142,7 +155,8 @@ def main() -> int:
                                   1.0, xp)
         outp = torch.empty((Tp, H), dtype=torch.int16, device=dev)
         pp = k3x_amd.make_params(Tp, K, 2.5, 1e-6, k3x_amd.GLU_SWIGLU, 4.0, None,
-                                 k3x_amd.RENORM_FLOAT)
+                                 k3x_amd.RENORM_FLOAT,
+                                 k3x_amd.FLAG_SCALED_FP4 if args.scaled_fp4 else 0)
         ctx.set_profiling(True)  # one stream: every kernel in stream order, no overlap
         for i in range(max(args.steps, 1)):
             k3x_amd.check(k3x_amd.moe_forward(ctx, banks[0], pp, xp, outp), "prefill")
@@ -151,6 +165,33 @@ def main() -> int:
             b.close()
         ctx.close()
         log("pmc prefill pass done")
+        return 0
+    if args.pmc_c4:
+        src = torch.empty(CALIB_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # the calibration copy: reads and writes CALIB_BYTES
+        torch.cuda.synchronize()
+        sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
+        from oracle import Oracle
+        from synth import CONFIGS, SynthLayer
+        cfg = CONFIGS[4]
+        layer = SynthLayer(Oracle(), cfg)
+        k3x_amd.check(banks[0].upload_router(layer.router, layer.bias, layer.gamma), "c4 router")
+        x4 = torch.empty((cfg.tokens, H), dtype=torch.int16, device=dev)
+        k3x_amd.synth_normal_bf16(ctx, cfg.x_seed, k3x_amd.stream_id(k3x_amd.STREAM_INPUT), 1.0,
+                                  x4)
+        out4 = torch.empty((cfg.tokens, H), dtype=torch.int16, device=dev)
+        p4 = k3x_amd.make_params(cfg.tokens, cfg.top_k, cfg.routed_scale, cfg.eps, cfg.glu,
+                                 cfg.beta, cfg.linear, cfg.renorm)
+        ctx.set_profiling(True)  # one stream: every kernel in stream order, no overlap
+        for i in range(max(args.steps, 1)):
+            k3x_amd.check(k3x_amd.moe_forward(ctx, banks[0], p4, x4, out4), "c4")
+            k3x_amd.check(ctx.synchronize(), "pmc c4")
+        for b in banks:
+            b.close()
+        ctx.close()
+        log("pmc c4 pass done")
         return 0
     if args.pmc_pass:
         src = torch.empty(CALIB_BYTES // 4, dtype=torch.int32, device=dev).fill_(1)
@@ -648,14 +689,19 @@ def traffic_from(fetch_dir: str, write_dir: str) -> dict:
 
 
 COUNTERS_JSON_REL = os.path.join("profiles", "prefill_c5_counters.json")
+XCD_COUNT = 8  # MI355X: GRBM_GUI_ACTIVE reports DIMENSION_XCC[0:7], summed
 
 
-def counters_from(dirs: list[str]) -> dict:
-    """Per-kernel medians of every counter in rocprofv3 --pmc passes over
-    `bench.py --pmc-prefill` (one directory per pass), with HBM bytes per
-    dispatch from FETCH_SIZE / WRITE_SIZE scaled by the calibration copy, and
-    for the MFMA kernels the MFMA-busy share of the busy cycles.  Writes
-    COUNTERS_JSON_REL."""
+def counters_from(dirs: list[str], out_rel: str = COUNTERS_JSON_REL,
+                  workload: str = "bench.py --pmc-prefill (c5 prefill chunk, T=2048, one stream)"
+                  ) -> dict:
+    """Per-kernel medians of every counter in rocprofv3 --pmc passes over one
+    of the --pmc-* workloads (one directory per pass), with HBM bytes per
+    dispatch from FETCH_SIZE / WRITE_SIZE scaled by the calibration copy, for
+    the MFMA kernels the MFMA-busy share of the busy cycles, and the memory
+    unit's busy share (TA_BUSY_avr over the per-XCD GRBM_GUI_ACTIVE: the
+    texture addresser, which every vector memory instruction passes; the
+    MemUnitBusy of earlier profilers).  Writes out_rel."""
     import csv
     import glob
     import re
@@ -690,13 +736,18 @@ def counters_from(dirs: list[str]) -> dict:
         if cs.get("SQ_BUSY_CYCLES") and cs.get("SQ_VALU_MFMA_BUSY_CYCLES"):
             row["mfma_busy_over_sq_busy"] = round(row["SQ_VALU_MFMA_BUSY_CYCLES"] /
                                                   max(row["SQ_BUSY_CYCLES"], 1.0), 4)
+        if cs.get("TA_BUSY_avr") and cs.get("GRBM_GUI_ACTIVE"):
+            # GRBM_GUI_ACTIVE is summed over the XCDs' instances; the TA
+            # average is per TA, so per-XCD active cycles divide it.
+            row["mem_unit_busy_pct"] = round(100.0 * row["TA_BUSY_avr"] * XCD_COUNT /
+                                             max(row["GRBM_GUI_ACTIVE"], 1.0), 1)
         kernels[k] = row
-    out = {"workload": "bench.py --pmc-prefill (c5 prefill chunk, T=2048, one stream)",
+    out = {"workload": workload,
            "calibration": {"copy_bytes": CALIB_BYTES, **calib,
                            "fetch_scale": round(kf, 4) if kf else None,
                            "write_scale": round(kw, 4) if kw else None},
            "kernels": kernels}
-    with open(os.path.join(ROOT, COUNTERS_JSON_REL), "w") as f:
+    with open(os.path.join(ROOT, out_rel), "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
     return out

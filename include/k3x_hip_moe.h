@@ -498,6 +498,12 @@ typedef struct k3x_hip_latent_weights {
     const float* shared_up;    /* [shared_inter][hidden] */
     const float* shared_down;  /* [hidden][shared_inter] */
     uint32_t hidden, latent, shared_inter;
+    /* The width routed_norm's RMSNorm divides the sum of squares by: 0 means
+     * latent.  A caller that pads the latent to the bank's width with zeros
+     * (zero routed_down rows, zero expert codes in the padded rows and
+     * columns, zero routed_norm entries and routed_up columns) passes the
+     * unpadded width, so the padded layer computes the unpadded one. */
+    uint32_t latent_norm;
 } k3x_hip_latent_weights;
 
 /* The resident latent MoE layer for T tokens: latent = routed_down x; the

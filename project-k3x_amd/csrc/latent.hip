@@ -217,7 +217,8 @@ __global__ __launch_bounds__(kThreads) void mxfp4_gemv_kernel(
 // inverse = 1 / sqrt(float(sum / n) + eps) in fp32, out = x * inverse * w.
 __global__ __launch_bounds__(kThreads) void rmsnorm_f32_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ w,
-                                                               uint32_t n, float eps,
+                                                               uint32_t n, uint32_t n_div,
+                                                               float eps,
                                                                float* __restrict__ out,
                                                                const uint32_t* status) {
     __shared__ double part[kWaves];
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_f32_kernel(const float* __re
     double tot = 0.0;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) tot += part[i];
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n), eps)));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)(tot / (double)n_div), eps)));
     float* orow = out + (size_t)blockIdx.x * n;
     for (uint32_t i = threadIdx.x; i < n; i += kThreads)
         orow[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
@@ -353,9 +354,10 @@ int k3x_hip_resident_moe_layer(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
     if (!ctx || !bank || !w || !p || !x || !ids || !contributions || !out || bank->ctx != ctx)
         return K3X_ERR_INVALID_EXTENT;
     const uint32_t H = w->hidden, L = w->latent, S = w->shared_inter, T = p->tokens;
+    const uint32_t Ln = w->latent_norm ? w->latent_norm : L;  // RMSNorm divisor
     if (!w->routed_down || !w->routed_norm || !w->routed_up || !w->shared_gate ||
         !w->shared_up || !w->shared_down || !dims_ok(L, H, T) || !dims_ok(S, H, T) ||
-        bank->desc.hidden != L || bank->desc.shared_inter != 0 || p->flags)
+        bank->desc.hidden != L || bank->desc.shared_inter != 0 || p->flags || Ln > L)
         return K3X_ERR_INVALID_EXTENT;
     if (p->glu != K3X_GLU_SITU || !std::isfinite(p->rms_epsilon) || !(p->rms_epsilon > 0.0f))
         return K3X_ERR_INVALID_MXFP4;
@@ -407,7 +409,7 @@ int k3x_hip_resident_moe_layer(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
         return st;
     // normalized = rms_norm(mixed, routed_norm) (backend_cpu.cpp:327-328).
     hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3(T), dim3(kThreads), 0, ctx->stream, mixed,
-                       w->routed_norm, L, p->rms_epsilon, normed, ctx->status);
+                       w->routed_norm, L, Ln, p->rms_epsilon, normed, ctx->status);
     if ((st = launched(ctx, 1))) return st;
     // routed = routed_up . normalized (backend_cpu.cpp:329-330).
     GemvArgs r{};

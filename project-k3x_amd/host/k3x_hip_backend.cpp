@@ -57,6 +57,31 @@ const std::uint8_t* bytes(std::span<const std::byte> s) {
     return reinterpret_cast<const std::uint8_t*>(s.data());
 }
 
+// Widths of the bank's tile layout: multiples of 128 (one MFMA tile of K).
+std::size_t pad128(std::size_t n) { return (n + 127) / 128 * 128; }
+
+// An MXFP4 matrix [rows][cols] in the reference layout (cols % 32 == 0) as
+// [prows][pcols]: zero codes in the added rows and columns (+0.0 whatever
+// the scale) and scale byte 127 (1.0) in their blocks.
+void pad_mxfp4(const Mxfp4WeightView& m, std::size_t prows, std::size_t pcols,
+               std::vector<std::uint8_t>& packed, std::vector<std::uint8_t>& scales) {
+    packed.assign(prows * pcols / 2, 0);
+    scales.assign(prows * pcols / 32, 127);
+    for (std::size_t r = 0; r < m.rows; ++r) {
+        std::memcpy(packed.data() + r * pcols / 2, bytes(m.packed) + r * m.cols / 2, m.cols / 2);
+        std::memcpy(scales.data() + r * pcols / 32, bytes(m.scales) + r * m.cols / 32, m.cols / 32);
+    }
+}
+
+// fp32 row-major [rows][cols] as [prows][pcols], zeros added.
+std::vector<float> pad_dense(std::span<const float> v, std::size_t rows, std::size_t cols,
+                             std::size_t prows, std::size_t pcols) {
+    std::vector<float> out(prows * pcols, 0.0f);
+    for (std::size_t r = 0; r < rows; ++r)
+        std::memcpy(out.data() + r * pcols, v.data() + r * cols, cols * sizeof(float));
+    return out;
+}
+
 }  // namespace
 
 struct HipMoeBackend::Impl {
@@ -67,9 +92,14 @@ struct HipMoeBackend::Impl {
         std::uint64_t ids[3] = {0, 0, 0};
         std::uint64_t last_use = 0;
     };
+    // One bank per (layer, hidden, intermediate): widths padded to
+    // multiples of 128 (hp, ip) when the layer's are not; the padded rows
+    // and columns hold zero codes, and callers pad activations with zeros.
     struct Bank {
         k3x_hip_bank* bank = nullptr;
         std::vector<Slot> slots;
+        std::size_t h = 0, i = 0, hp = 0, ip = 0;
+        bool padded() const { return h != hp || i != ip; }
     };
     std::map<std::tuple<std::uint32_t, std::size_t, std::size_t>, Bank> banks;
     std::uint64_t tick = 0;
@@ -192,17 +222,20 @@ struct HipMoeBackend::Impl {
     // the host data before any upload and rejects it with its error code.
     // Returns the device base, or nullptr with ok when the resident budget
     // cannot hold it (then `fallback`, if given, receives a transient copy).
+    // `identity` (default: the first segment's data) is the host tensor the
+    // entry stands for, when the segments are a padded copy of it.
     struct Segment {
         const void* data;
         std::size_t bytes;
     };
     template <typename Check>
     ErrorCode acquire(std::uint64_t id, std::initializer_list<Segment> segs, std::size_t rows,
-                      std::size_t cols, Check check, Dev* fallback, const void** out) {
+                      std::size_t cols, Check check, Dev* fallback, const void** out,
+                      const void* identity = nullptr) {
         *out = nullptr;
         std::size_t total = 0;
         for (const Segment& g : segs) total += (g.bytes + 255) & ~(std::size_t)255;
-        const Segment first = *segs.begin();
+        const Segment first{identity ? identity : segs.begin()->data, segs.begin()->bytes};
         // Tensor id 0 names no tensor (the reference's convenience overloads
         // pass it): always a transient copy.
         auto it = id ? resident.find(id) : resident.end();
@@ -294,14 +327,15 @@ struct HipMoeBackend::Impl {
     }
 
     // The layer's shapes this library runs: group size 32 (as the CUDA
-    // backend; another is invalid_mxfp4), hidden and intermediate multiples
-    // of 128, a square layer (down rows = hidden); other shapes are
-    // backend_unavailable, which the methods return as declined.
+    // backend; another is invalid_mxfp4), any hidden and intermediate the
+    // MXFP4 format allows (multiples of 32; the bank pads them to multiples
+    // of 128 with zero codes), a square layer (down rows = hidden); other
+    // shapes are backend_unavailable, which the methods return as declined.
     static ErrorCode supported(const Mxfp4MlpView& e) {
         for (const Mxfp4WeightView* m : {&e.gate, &e.up, &e.down})
             if (m->group_size != 32) return ErrorCode::invalid_mxfp4;
         const std::size_t H = e.gate.cols, I = e.gate.rows;
-        if (H % 128 || I % 128 || e.down.rows != H || H > (1u << 20) || I > (1u << 20))
+        if (H % 32 || I % 32 || e.down.rows != H || H > (1u << 20) || I > (1u << 20))
             return ErrorCode::backend_unavailable;
         return ErrorCode::ok;
     }
@@ -312,12 +346,16 @@ struct HipMoeBackend::Impl {
         if (it != banks.end()) return Result<Bank*>::success(&it->second);
         if (!ctx) return Result<Bank*>::failure(ErrorCode::backend_unavailable, "no device");
         k3x_hip_layer_desc d{};
-        d.hidden = (std::uint32_t)H;
-        d.inter = (std::uint32_t)I;
+        d.hidden = (std::uint32_t)pad128(H);
+        d.inter = (std::uint32_t)pad128(I);
         d.experts = opt.resident_experts;
         d.group_size = 32;
         d.shared_inter = 0;
         Bank b;
+        b.h = H;
+        b.i = I;
+        b.hp = d.hidden;
+        b.ip = d.inter;
         const int st = k3x_hip_bank_create(ctx, &d, &b.bank);
         if (st) return Result<Bank*>::failure(code_of(st), "bank_create");
         b.slots.resize(opt.resident_experts);
@@ -372,9 +410,21 @@ struct HipMoeBackend::Impl {
             }
             if (victim == n) return ErrorCode::backend_unavailable;  // more experts than slots
             const std::uint64_t tid[3] = {e.gate.tensor_id, e.up.tensor_id, e.down.tensor_id};
-            const int st = k3x_hip_bank_upload_expert(
-                b.bank, (std::uint32_t)victim, tid, bytes(e.gate.packed), bytes(e.gate.scales),
-                bytes(e.up.packed), bytes(e.up.scales), bytes(e.down.packed), bytes(e.down.scales));
+            int st;
+            if (b.padded()) {
+                std::vector<std::uint8_t> p[6];
+                pad_mxfp4(e.gate, b.ip, b.hp, p[0], p[1]);
+                pad_mxfp4(e.up, b.ip, b.hp, p[2], p[3]);
+                pad_mxfp4(e.down, b.hp, b.ip, p[4], p[5]);
+                st = k3x_hip_bank_upload_expert(b.bank, (std::uint32_t)victim, tid, p[0].data(),
+                                                p[1].data(), p[2].data(), p[3].data(),
+                                                p[4].data(), p[5].data());
+            } else {
+                st = k3x_hip_bank_upload_expert(
+                    b.bank, (std::uint32_t)victim, tid, bytes(e.gate.packed), bytes(e.gate.scales),
+                    bytes(e.up.packed), bytes(e.up.scales), bytes(e.down.packed),
+                    bytes(e.down.scales));
+            }
             if (st) {
                 // Rejected arguments leave the slot as it was; a failure
                 // after the slot was touched leaves it empty.
@@ -400,7 +450,10 @@ struct HipMoeBackend::Impl {
 
     // One layer call: T tokens, K slots each, routes index `experts`
     // (distinct within a token), weights = contributions (or 1).  Fills
-    // pairs_out [T][K][H] and/or mix_out [T][H].
+    // pairs_out [T][K][H] and/or mix_out [T][H].  On a padded bank the rows
+    // of x are padded with zeros to the bank's hidden width (the padded
+    // codes are zero, so the padded activations are GLU(0, 0) = 0 and the
+    // products are those of the unpadded layer) and the outputs cropped.
     ErrorCode run(std::uint32_t layer, std::span<const float> inputs, std::size_t T,
                   std::size_t K, std::span<const Mxfp4MlpView> experts,
                   std::span<const std::uint32_t> routes, std::span<const float> contributions,
@@ -417,16 +470,18 @@ struct HipMoeBackend::Impl {
             hid[p] = slot[routes[p]];
             if (!contributions.empty()) hw[p] = contributions[p];
         }
-        std::vector<std::uint16_t> xb(T * H);
-        for (std::size_t i = 0; i < T * H; ++i) xb[i] = to_bf16(inputs[i]);
-        for (auto [d, n] : {std::pair<Dev*, std::size_t>{&xn, T * H * 2}, {&ids, T * K * 4},
-                            {&w, T * K * 4}, {&out, T * H * 2}})
+        const std::size_t Hp = bank.value()->hp;
+        std::vector<std::uint16_t> xb(T * Hp, 0);
+        for (std::size_t t = 0; t < T; ++t)
+            for (std::size_t i = 0; i < H; ++i) xb[t * Hp + i] = to_bf16(inputs[t * H + i]);
+        for (auto [d, n] : {std::pair<Dev*, std::size_t>{&xn, T * Hp * 2}, {&ids, T * K * 4},
+                            {&w, T * K * 4}, {&out, T * Hp * 2}})
             if (ErrorCode c = ensure(*d, n); c != ErrorCode::ok) return c;
         if (mix_out)
-            if (ErrorCode c = ensure(out_f32, T * H * 4); c != ErrorCode::ok) return c;
+            if (ErrorCode c = ensure(out_f32, T * Hp * 4); c != ErrorCode::ok) return c;
         if (pairs_out)
-            if (ErrorCode c = ensure(pairs, T * K * H * 4); c != ErrorCode::ok) return c;
-        if (hipMemcpy(xn.p, xb.data(), T * H * 2, hipMemcpyHostToDevice) != hipSuccess ||
+            if (ErrorCode c = ensure(pairs, T * K * Hp * 4); c != ErrorCode::ok) return c;
+        if (hipMemcpy(xn.p, xb.data(), T * Hp * 2, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(ids.p, hid.data(), T * K * 4, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(w.p, hw.data(), T * K * 4, hipMemcpyHostToDevice) != hipSuccess)
             return ErrorCode::backend_unavailable;
@@ -450,18 +505,14 @@ struct HipMoeBackend::Impl {
         if (!st) st = k3x_hip_ctx_synchronize(ctx);
         if (st) return code_of(st);
         ++stats.layer_calls;
-        if (pairs_out) {
-            pairs_out->resize(T * K * H);
-            if (hipMemcpy(pairs_out->data(), pairs.p, T * K * H * 4, hipMemcpyDeviceToHost) !=
-                hipSuccess)
-                return ErrorCode::backend_unavailable;
-        }
-        if (mix_out) {
-            mix_out->resize(T * H);
-            if (hipMemcpy(mix_out->data(), out_f32.p, T * H * 4, hipMemcpyDeviceToHost) !=
-                hipSuccess)
-                return ErrorCode::backend_unavailable;
-        }
+        // Rows of Hp values on the device, H of each kept.
+        auto fetch = [&](std::vector<float>& dst, const void* src, std::size_t rows) {
+            dst.resize(rows * H);
+            return hipMemcpy2D(dst.data(), H * 4, src, Hp * 4, H * 4, rows,
+                               hipMemcpyDeviceToHost) == hipSuccess;
+        };
+        if (pairs_out && !fetch(*pairs_out, pairs.p, T * K)) return ErrorCode::backend_unavailable;
+        if (mix_out && !fetch(*mix_out, out_f32.p, T)) return ErrorCode::backend_unavailable;
         return ErrorCode::ok;
     }
 
@@ -1270,14 +1321,27 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     const DenseWeightView* dv[6] = {&weights.routed_down, &norm_view,          &weights.routed_up,
                                     &weights.shared.gate, &weights.shared.up, &weights.shared.down};
     const void* dp[6] = {};
+    // On a padded bank (latent Lp = a multiple of 128 above L) the latent's
+    // dense weights are padded with zeros to match: routed_down [Lp][H],
+    // routed_norm [Lp], routed_up [H][Lp]; the RMSNorm divides by L.
+    const std::size_t Lp = bank.value()->hp;
+    std::vector<float> padded[3];
+    if (Lp != L) {
+        padded[0] = pad_dense(weights.routed_down.values, L, H, Lp, H);
+        padded[1] = pad_dense(weights.routed_norm.values, 1, L, 1, Lp);
+        padded[2] = pad_dense(weights.routed_up.values, H, L, H, Lp);
+    }
     for (int i = 0; i < 6; ++i) {
         const DenseWeightView& v = *dv[i];
         auto finite = [&] {
             return all_finite(as_span(v.values.data(), v.values.size())) ? ErrorCode::ok
                                                                           : ErrorCode::invalid_mxfp4;
         };
-        if (ErrorCode c = m.acquire(v.tensor_id, {{v.values.data(), v.values.size_bytes()}}, v.rows,
-                                    v.cols, finite, nullptr, &dp[i]);
+        const bool pad = i < 3 && Lp != L;
+        const float* data = pad ? padded[i].data() : v.values.data();
+        const std::size_t nbytes = pad ? padded[i].size() * sizeof(float) : v.values.size_bytes();
+        if (ErrorCode c = m.acquire(v.tensor_id, {{data, nbytes}}, v.rows, v.cols, finite, nullptr,
+                                    &dp[i], v.values.data());
             c != ErrorCode::ok)
             return R::failure(c);
         if (!dp[i]) return bypass();
@@ -1297,8 +1361,9 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     lw.shared_up = static_cast<const float*>(dp[4]);
     lw.shared_down = static_cast<const float*>(dp[5]);
     lw.hidden = (std::uint32_t)H;
-    lw.latent = (std::uint32_t)L;
+    lw.latent = (std::uint32_t)Lp;
     lw.shared_inter = (std::uint32_t)weights.shared.gate.rows;
+    lw.latent_norm = (std::uint32_t)L;
     k3x_hip_moe_params p{};
     p.tokens = 1;
     p.top_k = (std::uint32_t)K;

@@ -77,7 +77,8 @@ FLAG_SCALED_FP4 = 16
 class LatentWeights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("routed_down", "routed_norm", "routed_up",
                                          "shared_gate", "shared_up", "shared_down")] + \
-               [("hidden", C.c_uint32), ("latent", C.c_uint32), ("shared_inter", C.c_uint32)]
+               [("hidden", C.c_uint32), ("latent", C.c_uint32), ("shared_inter", C.c_uint32),
+                ("latent_norm", C.c_uint32)]
 
 
 TAP_FIELDS = ["normed_x", "logits", "ids", "weights", "counts", "offsets", "pair_token",
@@ -540,7 +541,7 @@ def resident_moe_layer(ctx: Context, bank: "Bank", weights: dict, params: MoePar
     S = weights["shared_gate"].shape[0]
     w = LatentWeights(*[ptr(weights[k]) for k in ("routed_down", "routed_norm", "routed_up",
                                                   "shared_gate", "shared_up", "shared_down")],
-                      H, L, S)
+                      H, L, S, 0)
     return load().k3x_hip_resident_moe_layer(
         ctx.handle, bank.handle, C.byref(w), C.byref(params), ptr(x), ptr(ids),
         ptr(contributions), host_ptr(host_ids), host_ptr(host_contributions), ptr(out),

@@ -2,9 +2,10 @@
 // laid out like the reference's own backend test
 // (tests/cpp/test_backend.cpp:205-390): expert group, batch, grid and
 // slot-ordered mix, then the same rejections.  Shapes are configuration 1's
-// expert (hidden 256, intermediate 512): the reference test's 32-wide
-// literals are below what the MI355X kernels run (multiples of 128), which
-// the backend reports as backend_unavailable (checked last).
+// expert (hidden 256, intermediate 512), and the reference's synthetic model
+// (hidden 64, latent 32, intermediate 32), which the backend pads to the
+// tile layout's multiples of 128; a non-square expert is declined
+// (backend_unavailable, checked last).
 //
 // Expected values come from the oracle's expert FFN (double sums) at the
 // layer's rounding points: the input and the GLU output rounded to bf16.
@@ -287,6 +288,115 @@ int latent_checks(k3x_amd::HipMoeBackend& b) {
             .error() != ErrorCode::invalid_mxfp4)
         return 144;
     std::printf("resident latent layer (+rejections): ok\n");
+    return 0;
+}
+
+// ---- widths below the tile layout's 128 ---------------------------------------
+// The reference's synthetic model (reference/k3x_ref/config.py:7-30: hidden
+// 64, routed latent 32, expert intermediate 32, 8 experts, Top-2, SiTU
+// beta 4 / 25, RMSNorm eps 1e-5): the backend pads the bank to multiples of
+// 128 with zero codes and the activations with zeros, so these shapes run on
+// the device (not declined) and match the oracle as the 128-multiple shapes
+// do: the expert group and mix at hidden 64, and the resident latent layer
+// at latent 32 (its RMSNorm over the 32 unpadded values).
+int padded_checks(k3x_amd::HipMoeBackend& b) {
+    constexpr std::size_t PH = 64, PL = 32, PI = 32, PS = 96, PE = 8;
+    constexpr float kB = 4.0f, kLin = 25.0f, kEps = 1e-5f;
+    auto codes = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& x : v) x = std::byte(next_u32() & 0xff);
+        return v;
+    };
+    auto scales = [](std::size_t n) {
+        std::vector<std::byte> v(n);
+        for (auto& x : v) x = std::byte(121 + next_u32() % 5);
+        return v;
+    };
+    auto u8 = [](const std::vector<std::byte>& v) {
+        return reinterpret_cast<const std::uint8_t*>(v.data());
+    };
+    struct Pe {
+        std::vector<std::byte> m[6];
+    };
+    // Experts of hidden `h`, intermediate PI, square (down rows h).
+    auto make = [&](std::size_t h) {
+        Pe e;
+        e.m[0] = codes(PI * h / 2);
+        e.m[1] = scales(PI * h / 32);
+        e.m[2] = codes(PI * h / 2);
+        e.m[3] = scales(PI * h / 32);
+        e.m[4] = codes(h * PI / 2);
+        e.m[5] = scales(h * PI / 32);
+        return e;
+    };
+    auto view = [&](const Pe& e, std::uint64_t id, std::size_t h) {
+        return Mxfp4MlpView{{id, e.m[0], e.m[1], PI, h, 32}, {id + 1, e.m[2], e.m[3], PI, h, 32},
+                            {id + 2, e.m[4], e.m[5], h, PI, 32}};
+    };
+    // Expert group and slot-ordered mix at hidden 64.
+    std::vector<Pe> ge;
+    std::vector<Mxfp4MlpView> gv;
+    for (std::size_t k = 0; k < 2; ++k) ge.push_back(make(PH));
+    for (std::size_t k = 0; k < 2; ++k) gv.push_back(view(ge[k], 901 + 3 * k, PH));
+    const auto x = rand_f32(PH, 1.0f);
+    std::vector<float> xb(PH);
+    for (std::size_t i = 0; i < PH; ++i) xb[i] = bf16_round(x[i]);
+    auto g = b.mxfp4_situ_mlp_group(x, gv, kB, kLin, 21, ProfilePhase::decode);
+    if (!g) {
+        std::printf("padded group: %s%s\n", k3x_amd::error_code_name(g.error()),
+                    g.declined() ? " (declined)" : "");
+        return 150;
+    }
+    std::vector<float> want_mix(PH, 0.0f);
+    const float c[2] = {0.625f, 0.375f};
+    for (std::size_t k = 0; k < 2; ++k) {
+        std::vector<float> act(PI), out(PH);
+        k3xo_expert_ffn(xb.data(), PH, PI, u8(ge[k].m[0]), u8(ge[k].m[1]), u8(ge[k].m[2]),
+                        u8(ge[k].m[3]), u8(ge[k].m[4]), u8(ge[k].m[5]), K3XO_GLU_SITU, kB, 1, kLin,
+                        1, act.data(), out.data());
+        if (!close_to(g.value()[k], out, "padded group (hidden 64, intermediate 32)")) return 151;
+        for (std::size_t i = 0; i < PH; ++i) want_mix[i] = want_mix[i] + c[k] * g.value()[k][i];
+    }
+    auto mx = b.mxfp4_situ_moe(x, gv, c, kB, kLin, 21, ProfilePhase::decode);
+    if (!mx || !close_to(mx.value(), want_mix, "padded mix")) return 152;
+    std::printf("hidden 64 / intermediate 32 expert group and mix on the device: ok\n");
+
+    // The resident latent layer of the synthetic model's shape.
+    std::vector<Pe> le;
+    std::vector<Mxfp4MlpView> lv;
+    for (std::size_t k = 0; k < PE; ++k) le.push_back(make(PL));
+    const std::size_t route[2] = {5, 2};
+    for (std::size_t k : route) lv.push_back(view(le[k], 951 + 3 * k, PL));
+    const auto Rd = rand_f32(PL * PH, 0.1f), Ru = rand_f32(PH * PL, 0.1f);
+    const auto Sg = rand_f32(PS * PH, 0.1f), Su = rand_f32(PS * PH, 0.1f),
+               Sd = rand_f32(PH * PS, 0.1f);
+    std::vector<float> Rn(PL);
+    for (auto& v : Rn) v = 0.5f + (float)(next_u32() % 1000) / 1000.0f;
+    const k3x_amd::ResidentMoeLayerView w{{941, Rd, PL, PH},
+                                          {942, Rn},
+                                          {943, Ru, PH, PL},
+                                          {{944, Sg, PS, PH}, {945, Su, PS, PH}, {946, Sd, PH, PS}}};
+    std::vector<const std::uint8_t*> eptrs;
+    for (std::size_t k : route)
+        for (int m = 0; m < 6; ++m) eptrs.push_back(u8(le[k].m[m]));
+    const float lc[2] = {0.7f, 0.3f};
+    std::vector<float> want(PH), want_mixed(PL);
+    if (k3xo_resident_layer(x.data(), PH, PL, PI, PS, Rd.data(), Rn.data(), Ru.data(), Sg.data(),
+                            Su.data(), Sd.data(), eptrs.data(), lc, 2, kEps, kB, 1, kLin,
+                            want_mixed.data(), want.data()) != 0)
+        return 153;
+    auto rl = b.resident_mxfp4_moe_layer(x, w, lv, lc, kEps, kB, kLin, 22, ProfilePhase::decode);
+    if (!rl || !rl.value().executed) {
+        std::printf("padded latent layer: %s%s\n",
+                    rl ? "not executed" : k3x_amd::error_code_name(rl.error()),
+                    !rl && rl.declined() ? " (declined)" : "");
+        return 154;
+    }
+    if (!near(rl.value().output, want, 1e-3f, 1e-3f, "padded latent layer")) return 155;
+    auto rl2 = b.resident_mxfp4_moe_layer(x, w, lv, lc, kEps, kB, kLin, 22, ProfilePhase::decode);
+    if (!rl2 || !identical(rl2.value().output, rl.value().output)) return 156;
+    std::printf("latent layer of the synthetic model (hidden 64, latent 32, intermediate 32) on "
+                "the device: ok\n");
     return 0;
 }
 
@@ -770,6 +880,7 @@ int main() {
 
     if (int rc = official_checks(*backend)) return rc;
     if (int rc = latent_checks(*backend)) return rc;
+    if (int rc = padded_checks(*backend)) return rc;
     if (int rc = latent_bypass_checks()) return rc;
     // More slots than routed experts (the normal configuration): the official
     // FFN admits only the called experts and leaves the other slots empty,

@@ -1,6 +1,7 @@
 """GPU run of the C++ host side's test program (tests/cpp/test_hip_backend.cpp):
 HipMoeBackend's group / batch / grid / mix methods against the oracle, the
-reference's rejections, residency hits and replacement.  Exit status 0 is a
+reference's rejections, residency hits and replacement, and the reference's
+synthetic-model widths (below the tile layout's 128) through the padded bank.  Exit status 0 is a
 pass; any other status names the failed check (see the program)."""
 from __future__ import annotations
 
@@ -22,3 +23,7 @@ def test_hip_backend_program():
     r = subprocess.run([EXE], capture_output=True, text=True, timeout=110)
     sys.stdout.write(r.stdout)
     assert r.returncode == 0, f"exit {r.returncode}: {r.stdout[-2000:]} {r.stderr[-2000:]}"
+    # The reference's synthetic-model widths (hidden 64, latent 32,
+    # intermediate 32) ran on the device, padded, not declined.
+    assert "hidden 64 / intermediate 32 expert group and mix on the device: ok" in r.stdout
+    assert "latent layer of the synthetic model" in r.stdout
