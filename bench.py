@@ -736,6 +736,10 @@ def counters_from(dirs: list[str], out_rel: str = COUNTERS_JSON_REL,
         if cs.get("SQ_BUSY_CYCLES") and cs.get("SQ_VALU_MFMA_BUSY_CYCLES"):
             row["mfma_busy_over_sq_busy"] = round(row["SQ_VALU_MFMA_BUSY_CYCLES"] /
                                                   max(row["SQ_BUSY_CYCLES"], 1.0), 4)
+        mops = sum(row.get(f"SQ_INSTS_VALU_MFMA_MOPS_{t}", 0.0) for t in ("BF16", "F8", "F6F4", "F64"))
+        if mops:
+            # Each MOPS unit is 512 floating-point operations.
+            row["mfma_tflop_issued_per_dispatch"] = round(mops * 512 / 1e12, 4)
         if cs.get("TA_BUSY_avr") and cs.get("GRBM_GUI_ACTIVE"):
             # GRBM_GUI_ACTIVE is summed over the XCDs' instances; the TA
             # average is per TA, so per-XCD active cycles divide it.

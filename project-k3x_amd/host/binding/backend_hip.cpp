@@ -24,7 +24,9 @@
 //     path.
 // Views convert member by member (the structs hold the same members) and
 // error codes by value (the enumerations list the same codes in the same
-// order).
+// order).  With a Profiler, every device method's operations are recorded
+// into it as ProfileEvents (stage device times where the library stages
+// the call), beside the CPU backend's own for the calls it runs.
 #include "k3x/backend.hpp"
 #include "k3x_hip_backend.hpp"
 
@@ -105,7 +107,20 @@ auto or_cpu(hip::Result<H>&& r, std::uint64_t* declined, F&& cpu) -> decltype(cp
 class HipBackend final : public ComputeBackend {
 public:
     HipBackend(std::unique_ptr<hip::HipMoeBackend> be, BackendOptions options, Profiler* profiler)
-        : be_(std::move(be)), cpu_(make_cpu_backend(profiler)), options_(options) {}
+        : be_(std::move(be)), cpu_(make_cpu_backend(profiler)), options_(options) {
+        // The device methods' operations reach the same Profiler as the CPU
+        // backend's (the enumerations list the same members in the same
+        // order), as the CUDA backend records them (backend_cuda.cu:2505-2542).
+        if (profiler)
+            be_->set_profile_sink([profiler](const hip::ProfileEvent& e) {
+                profiler->record(ProfileEvent{
+                    e.phase == hip::ProfilePhase::prefill ? ProfilePhase::prefill
+                                                          : ProfilePhase::decode,
+                    static_cast<ProfileOperation>(e.operation),
+                    static_cast<NumericPrecision>(e.precision), e.layer, e.wall_nanoseconds,
+                    e.device_nanoseconds, e.logical_bytes, e.transfer_bytes, e.success});
+            });
+    }
 
     BackendKind kind() const noexcept override { return options_.kind; }
     const BackendOptions& options() const noexcept override { return options_; }

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -189,6 +190,64 @@ struct HipMoeBackend::Impl {
     }
 
     std::uint64_t owner() const { return reinterpret_cast<std::uintptr_t>(this); }
+
+    // Profile events of the current call (set_profile_sink).
+    ProfileSink sink;
+    ProfilePhase call_phase = ProfilePhase::decode;
+    using Clock = std::chrono::steady_clock;
+    static std::uint64_t ns_since(Clock::time_point t0) {
+        return (std::uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - t0)
+            .count();
+    }
+    void emit(ProfileOperation op, NumericPrecision pr, std::uint32_t layer, std::uint64_t wall,
+              std::uint64_t device, std::uint64_t logical, std::uint64_t transfer, bool ok = true) {
+        if (sink) sink(ProfileEvent{call_phase, op, pr, layer, wall, device, logical, transfer, ok});
+    }
+    // One call without stage events: its launch-to-completion time on its
+    // main operation (op, the bytes it reads), then the rest of its
+    // operations' bytes with no time of their own.
+    struct OpBytes {
+        ProfileOperation op;
+        NumericPrecision precision;
+        std::uint64_t bytes;
+    };
+    void emit_call(std::uint32_t layer, Clock::time_point t0, std::initializer_list<OpBytes> ops) {
+        if (!sink) return;
+        const std::uint64_t t = ns_since(t0);
+        bool first = true;
+        for (const OpBytes& o : ops) {
+            emit(o.op, o.precision, layer, t, first ? t : 0, o.bytes, 0);
+            first = false;
+        }
+    }
+    // The library's stage totals since the last read, cleared.
+    void take_stage_ms(double (&ms)[K3X_STAGE_COUNT]) {
+        std::uint64_t n[K3X_STAGE_COUNT];
+        if (!ctx || k3x_hip_ctx_stage_times(ctx, ms, n, 1) != 0)
+            for (double& v : ms) v = 0.0;
+    }
+    // Events of one layer call from its stages: routed gate/up (+ the fused
+    // GLU) and down as mxfp4_matvec over the distinct experts' weights, the
+    // slot-ordered combine as moe_mix, the decode front as rms_norm.
+    void emit_layer_stages(std::uint32_t layer, std::uint64_t wall, std::size_t experts,
+                           std::size_t T, std::size_t K, std::size_t H, std::size_t I) {
+        double ms[K3X_STAGE_COUNT];
+        take_stage_ms(ms);
+        const std::uint64_t gu = experts * 2 * (I * H / 2 + I * H / 32) + T * H * 2;
+        const std::uint64_t dn = experts * (H * I / 2 + H * I / 32) + T * K * I * 2;
+        auto ns = [&](int a, int b) { return (std::uint64_t)((ms[a] + ms[b]) * 1e6); };
+        const auto fp4 = NumericPrecision::mxfp4_e2m1_e8m0;
+        if (ms[K3X_STAGE_DECODE_FRONT] > 0 || ms[K3X_STAGE_ROUTE] > 0)
+            emit(ProfileOperation::rms_norm, NumericPrecision::bf16_rounded, layer, wall,
+                 ns(K3X_STAGE_DECODE_FRONT, K3X_STAGE_ROUTE), T * H * 2, 0);
+        emit(ProfileOperation::mxfp4_matvec, fp4, layer, wall,
+             ns(K3X_STAGE_GATE_UP, K3X_STAGE_DECODE_GATE_UP), gu, 0);
+        emit(ProfileOperation::mxfp4_matvec, fp4, layer, wall,
+             ns(K3X_STAGE_DOWN, K3X_STAGE_DECODE_DOWN), dn, 0);
+        if (ms[K3X_STAGE_COMBINE] > 0)
+            emit(ProfileOperation::moe_mix, NumericPrecision::fp32, layer, wall,
+                 (std::uint64_t)(ms[K3X_STAGE_COMBINE] * 1e6), T * K * H * 4 + T * K * 4, 0);
+    }
 
     // A shape the device path does not run, found before any device work.
     template <class R>
@@ -460,10 +519,17 @@ struct HipMoeBackend::Impl {
                   float beta, std::optional<float> linear, std::vector<float>* pairs_out,
                   std::vector<float>* mix_out) {
         const std::size_t H = experts.front().gate.cols, I = experts.front().gate.rows;
+        const auto t_call = Clock::now();
         auto bank = bank_for(layer, H, I);
         if (!bank) return bank.error();
         std::vector<std::uint32_t> slot;
+        const std::uint64_t h2d0 = stats.weight_h2d_bytes;
         if (ErrorCode c = admit(*bank.value(), experts, slot); c != ErrorCode::ok) return c;
+        if (sink && stats.weight_h2d_bytes != h2d0)
+            emit(ProfileOperation::weight_host_to_device, NumericPrecision::mxfp4_e2m1_e8m0, layer,
+                 ns_since(t_call), 0, 0, stats.weight_h2d_bytes - h2d0);
+        double stale[K3X_STAGE_COUNT];
+        if (sink) take_stage_ms(stale);  // this call's stages only
         std::vector<std::uint32_t> hid(T * K);
         std::vector<float> hw(T * K, 1.0f);
         for (std::size_t p = 0; p < T * K; ++p) {
@@ -505,6 +571,15 @@ struct HipMoeBackend::Impl {
         if (!st) st = k3x_hip_ctx_synchronize(ctx);
         if (st) return code_of(st);
         ++stats.layer_calls;
+        if (sink) {
+            std::vector<std::uint32_t> u(hid);
+            std::sort(u.begin(), u.end());
+            const std::size_t distinct = (std::size_t)(std::unique(u.begin(), u.end()) - u.begin());
+            emit(ProfileOperation::activation_host_to_device, NumericPrecision::bf16_rounded, layer,
+                 ns_since(t_call), 0, 0, T * Hp * 2 + T * K * 8);
+            emit_layer_stages(layer, ns_since(t_call), distinct, T, K, Hp, bank.value()->ip);
+        }
+        const auto t_d2h = Clock::now();
         // Rows of Hp values on the device, H of each kept.
         auto fetch = [&](std::vector<float>& dst, const void* src, std::size_t rows) {
             dst.resize(rows * H);
@@ -513,6 +588,9 @@ struct HipMoeBackend::Impl {
         };
         if (pairs_out && !fetch(*pairs_out, pairs.p, T * K)) return ErrorCode::backend_unavailable;
         if (mix_out && !fetch(*mix_out, out_f32.p, T)) return ErrorCode::backend_unavailable;
+        if (sink)
+            emit(ProfileOperation::device_to_host, NumericPrecision::fp32, layer, ns_since(t_d2h), 0,
+                 0, ((pairs_out ? T * K : 0) + (mix_out ? T : 0)) * H * 4);
         return ErrorCode::ok;
     }
 
@@ -576,7 +654,8 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_group(std::span<const float> input
                                                     std::span<const Mxfp4MlpView> experts,
                                                     float situ_beta,
                                                     std::optional<float> situ_linear,
-                                                    std::uint32_t layer, ProfilePhase) {
+                                                    std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     for (const auto& e : experts)
         if (!valid_mxfp4_mlp(input.size(), e)) return Result<Outputs>::failure(ErrorCode::invalid_mxfp4);
     if (experts.empty()) return Result<Outputs>::success({});
@@ -608,7 +687,8 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_batch(std::span<const float> input
                                                     std::size_t batch_size, Mxfp4MlpView expert,
                                                     float situ_beta,
                                                     std::optional<float> situ_linear,
-                                                    std::uint32_t layer, ProfilePhase) {
+                                                    std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     // backend_cpu.cpp:161-171.
     if (batch_size == 0 || expert.gate.cols == 0 || !mul_fits(batch_size, expert.gate.cols) ||
         inputs.size() != batch_size * expert.gate.cols || !valid_situ(situ_beta, situ_linear) ||
@@ -634,7 +714,8 @@ Result<Outputs> HipMoeBackend::mxfp4_situ_mlp_grid(std::span<const float> inputs
                                                    std::span<const Mxfp4MlpView> experts,
                                                    float situ_beta,
                                                    std::optional<float> situ_linear,
-                                                   std::uint32_t layer, ProfilePhase) {
+                                                   std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     // backend_cpu.cpp:197-246.
     using R = Result<Outputs>;
     if (token_count == 0 || experts.empty() || experts.front().gate.cols == 0 ||
@@ -673,6 +754,7 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe(std::span<const float> 
                                                          float situ_beta,
                                                          std::optional<float> situ_linear,
                                                          std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     // backend_cpu.cpp:271-288.
     using R = Result<std::vector<float>>;
     if (experts.empty() || experts.size() != contributions.size())
@@ -724,7 +806,8 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_situ_moe_tokens(
     std::span<const float> inputs, std::size_t token_count, std::size_t top_k,
     std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> routes,
     std::span<const float> contributions, float situ_beta, std::optional<float> situ_linear,
-    std::uint32_t layer, ProfilePhase) {
+    std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<std::vector<float>>;
     if (token_count == 0 || top_k == 0 || top_k > kMaxSlotsPerToken || experts.empty() ||
         !mul_fits(token_count, top_k) || routes.size() != token_count * top_k ||
@@ -771,6 +854,7 @@ Result<ExpertMajorBlockMoe> HipMoeBackend::expert_major_block_moe(
     std::span<const float> latents, std::size_t positions,
     std::span<const ExpertMajorTokenRoute> routes, std::span<const Mxfp4MlpView> experts,
     float situ_beta, std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<ExpertMajorBlockMoe>;
     if (routes.empty() || routes.size() != positions) return R::failure(ErrorCode::invalid_extent);
     ExpertMajorBlockMoe res;
@@ -862,7 +946,8 @@ float bf16_word_to_f32(std::uint16_t w) {
 
 Result<OfficialMoeRoutePrepareResult> HipMoeBackend::prepare_official_moe_route(
     std::span<const float> prefix, std::span<const float> block, OfficialMoeRoutePrepareView wv,
-    float epsilon, std::uint32_t layer, ProfilePhase) {
+    float epsilon, std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<OfficialMoeRoutePrepareResult>;
     Impl& m = *impl_;
     const std::size_t H = prefix.size();
@@ -926,6 +1011,7 @@ Result<OfficialMoeRoutePrepareResult> HipMoeBackend::prepare_official_moe_route(
     if (hipMemcpy(m.prep_prefix.p, prefix.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(m.prep_block.p, block.data(), H * 4, hipMemcpyHostToDevice) != hipSuccess)
         return R::failure(ErrorCode::backend_unavailable);
+    const auto t_launch = Impl::Clock::now();
     int st = k3x_hip_official_prepare(m.ctx, rt.obj, 1, epsilon,
                                       static_cast<const float*>(m.prep_prefix.p),
                                       static_cast<const float*>(m.prep_block.p),
@@ -933,6 +1019,9 @@ Result<OfficialMoeRoutePrepareResult> HipMoeBackend::prepare_official_moe_route(
                                       static_cast<float*>(m.prep_logits.p));
     if (!st) st = k3x_hip_ctx_synchronize(m.ctx);
     if (st) return R::failure(code_of(st));
+    m.emit_call(layer, t_launch,
+                {{ProfileOperation::rms_norm, NumericPrecision::bf16_rounded, (3 * H + H * H) * 2},
+                 {ProfileOperation::dense_matvec, NumericPrecision::bf16_rounded, E * H * 2}});
     OfficialMoeRoutePrepareResult r;
     r.executed = true;
     r.router_logits.resize(E);
@@ -961,7 +1050,8 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_mxfp4_moe_ffn(
     std::span<const float> hidden, std::span<const float> prefix, OfficialMoeFfnView weights,
     std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
     std::span<const float> contributions, float epsilon, float situ_beta,
-    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     impl_->prepared_active = false;  // backend_cuda.cu:3723-3731
     return official_ffn(hidden, prefix, std::nullopt, weights, experts, expert_ids, contributions,
                         epsilon, situ_beta, situ_linear, layer);
@@ -971,7 +1061,8 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_mxfp4_moe_ffn_prepared(
     OfficialMoePreparedToken prepared, OfficialMoeFfnView weights,
     std::span<const Mxfp4MlpView> experts, std::span<const std::uint32_t> expert_ids,
     std::span<const float> contributions, float epsilon, float situ_beta,
-    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     return official_ffn({}, {}, prepared, weights, experts, expert_ids, contributions, epsilon,
                         situ_beta, situ_linear, layer);
 }
@@ -1112,6 +1203,7 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
     p.has_situ_linear = linear.has_value();
     p.situ_linear_beta = linear.value_or(0.0f);
     p.renorm = K3X_RENORM_DOUBLE;
+    const auto t_launch = Impl::Clock::now();
     int st = k3x_hip_official_ffn(m.ctx, f.obj, &p, static_cast<const std::uint16_t*>(hid),
                                   static_cast<const float*>(pre),
                                   static_cast<const std::uint32_t*>(m.o_ids.p),
@@ -1119,6 +1211,13 @@ Result<OfficialMoeFfnResult> HipMoeBackend::official_ffn(
                                   static_cast<std::uint16_t*>(m.o_out.p), nullptr);
     if (!st) st = k3x_hip_ctx_synchronize(m.ctx);
     if (st) return R::failure(code_of(st));
+    m.emit_call(layer, t_launch,
+                {{ProfileOperation::mxfp4_matvec, NumericPrecision::mxfp4_e2m1_e8m0,
+                  K * 3 * (I * L / 2 + I * L / 32)},
+                 {ProfileOperation::dense_matvec, NumericPrecision::bf16_rounded,
+                  (2 * L * H + 3 * Is * H) * 2},
+                 {ProfileOperation::rms_norm, NumericPrecision::bf16_rounded, L * 2 + L * 2},
+                 {ProfileOperation::moe_mix, NumericPrecision::bf16_rounded, K * L * 2}});
     std::vector<std::uint16_t> ob(H);
     if (hipMemcpy(ob.data(), m.o_out.p, H * 2, hipMemcpyDeviceToHost) != hipSuccess)
         return R::failure(ErrorCode::backend_unavailable);
@@ -1139,8 +1238,9 @@ std::span<const float> as_span(const float* p, std::size_t n) { return {p, n}; }
 }  // namespace
 
 Result<std::vector<float>> HipMoeBackend::dense_matvec(std::span<const float> input,
-                                                       DenseWeightView weight, std::uint32_t,
-                                                       ProfilePhase) {
+                                                       DenseWeightView weight, std::uint32_t layer,
+                                                       ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<std::vector<float>>;
     if (!valid_dense(input.size(), weight)) return R::failure(ErrorCode::invalid_extent);
     if (!weight.rows || !weight.cols) return R::success(std::vector<float>(weight.rows, 0.0f));
@@ -1157,6 +1257,7 @@ Result<std::vector<float>> HipMoeBackend::dense_matvec(std::span<const float> in
     if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
         return R::failure(c);
     if (ErrorCode c = m.ensure(m.vout, weight.rows * 4); c != ErrorCode::ok) return R::failure(c);
+    const auto t_launch = Impl::Clock::now();
     if (int st = k3x_hip_dense_f32_matvec(m.ctx, static_cast<const float*>(W),
                                           (std::uint32_t)weight.rows, (std::uint32_t)weight.cols,
                                           static_cast<const float*>(m.vin.p), 1,
@@ -1164,13 +1265,16 @@ Result<std::vector<float>> HipMoeBackend::dense_matvec(std::span<const float> in
         return R::failure(code_of(st));
     std::vector<float> out;
     if (ErrorCode c = m.finish(m.vout, out, weight.rows); c != ErrorCode::ok) return R::failure(c);
+    m.emit_call(layer, t_launch,
+                {{ProfileOperation::dense_matvec, NumericPrecision::fp32, weight.values.size_bytes()}});
     ++m.stats.calls;
     return R::success(std::move(out));
 }
 
 Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> input,
-                                                       Mxfp4WeightView weight, std::uint32_t,
-                                                       ProfilePhase) {
+                                                       Mxfp4WeightView weight, std::uint32_t layer,
+                                                       ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<std::vector<float>>;
     // mxfp4_matmul and decode_mxfp4 (runtime/src/ops.cpp:32-76): extents
     // first, then the scale bytes (at upload; a resident copy was checked).
@@ -1200,6 +1304,7 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> in
     if (ErrorCode c = m.upload(m.vin, input.data(), input.size_bytes()); c != ErrorCode::ok)
         return R::failure(c);
     if (ErrorCode c = m.ensure(m.vout, weight.rows * 4); c != ErrorCode::ok) return R::failure(c);
+    const auto t_launch = Impl::Clock::now();
     if (int st = k3x_hip_mxfp4_matvec(m.ctx, packed, scales, (std::uint32_t)weight.rows,
                                       (std::uint32_t)weight.cols,
                                       static_cast<const float*>(m.vin.p), 1,
@@ -1207,6 +1312,8 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> in
         return R::failure(code_of(st));
     std::vector<float> out;
     if (ErrorCode c = m.finish(m.vout, out, weight.rows); c != ErrorCode::ok) return R::failure(c);
+    m.emit_call(layer, t_launch, {{ProfileOperation::mxfp4_matvec, NumericPrecision::mxfp4_e2m1_e8m0,
+                                   weight.packed.size() + weight.scales.size()}});
     ++m.stats.calls;
     return R::success(std::move(out));
 }
@@ -1214,6 +1321,7 @@ Result<std::vector<float>> HipMoeBackend::mxfp4_matvec(std::span<const float> in
 Result<Outputs> HipMoeBackend::dense_matvec_group(std::span<const float> input,
                                                   std::span<const DenseWeightView> weights,
                                                   std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     for (const auto& w : weights)
         if (!valid_dense(input.size(), w)) return Result<Outputs>::failure(ErrorCode::invalid_extent);
     Outputs out;
@@ -1229,6 +1337,7 @@ Result<Outputs> HipMoeBackend::dense_matvec_group(std::span<const float> input,
 Result<Outputs> HipMoeBackend::mxfp4_matvec_group(std::span<const float> input,
                                                   std::span<const Mxfp4WeightView> weights,
                                                   std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     for (const auto& w : weights)
         if (!valid_mxfp4(input.size(), w)) return Result<Outputs>::failure(ErrorCode::invalid_mxfp4);
     Outputs out;
@@ -1244,7 +1353,8 @@ Result<Outputs> HipMoeBackend::mxfp4_matvec_group(std::span<const float> input,
 Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> input,
                                                          DenseMlpView weights, float situ_beta,
                                                          std::optional<float> situ_linear,
-                                                         std::uint32_t, ProfilePhase) {
+                                                         std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<std::vector<float>>;
     if (!valid_dense_mlp(input.size(), weights) ||
         !checks::consistent_ids({&weights.gate, &weights.up, &weights.down}))
@@ -1266,6 +1376,7 @@ Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> 
         return R::failure(c);
     if (ErrorCode c = m.ensure(m.vact, I * 4); c != ErrorCode::ok) return R::failure(c);
     if (ErrorCode c = m.ensure(m.vout, O * 4); c != ErrorCode::ok) return R::failure(c);
+    const auto t_launch = Impl::Clock::now();
     if (int st = k3x_hip_dense_situ_mlp(
             m.ctx, static_cast<const float*>(W[0]), static_cast<const float*>(W[1]),
             static_cast<const float*>(W[2]), (std::uint32_t)H, (std::uint32_t)I, (std::uint32_t)O,
@@ -1275,6 +1386,11 @@ Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> 
         return R::failure(code_of(st));
     std::vector<float> out;
     if (ErrorCode c = m.finish(m.vout, out, O); c != ErrorCode::ok) return R::failure(c);
+    m.emit_call(layer, t_launch,
+                {{ProfileOperation::dense_matvec, NumericPrecision::fp32,
+                  weights.gate.values.size_bytes() + weights.up.values.size_bytes() +
+                      weights.down.values.size_bytes()},
+                 {ProfileOperation::situ_glu, NumericPrecision::fp32, I * 8}});
     ++m.stats.calls;
     return R::success(std::move(out));
 }
@@ -1282,7 +1398,8 @@ Result<std::vector<float>> HipMoeBackend::dense_situ_mlp(std::span<const float> 
 Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     std::span<const float> input, ResidentMoeLayerView weights,
     std::span<const Mxfp4MlpView> experts, std::span<const float> contributions, float epsilon,
-    float situ_beta, std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase) {
+    float situ_beta, std::optional<float> situ_linear, std::uint32_t layer, ProfilePhase phase) {
+    impl_->call_phase = phase;
     using R = Result<ResidentMoeLayerResult>;
     const auto bad = [] { return R::failure(ErrorCode::invalid_mxfp4); };
     // valid_resident_moe_layer (backend_cpu.cpp:441-497); the finiteness of
@@ -1374,6 +1491,7 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
     p.has_situ_linear = situ_linear.has_value();
     p.situ_linear_beta = situ_linear.value_or(0.0f);
     p.renorm = K3X_RENORM_FLOAT;
+    const auto t_launch = Impl::Clock::now();
     if (int st = k3x_hip_resident_moe_layer(
             m.ctx, bank.value()->bank, &lw, &p, static_cast<const float*>(m.vin.p),
             static_cast<const std::uint32_t*>(m.vids.p), static_cast<const float*>(m.vc.p),
@@ -1381,6 +1499,14 @@ Result<ResidentMoeLayerResult> HipMoeBackend::resident_mxfp4_moe_layer(
         return R::failure(code_of(st));
     ResidentMoeLayerResult res{true, {}};
     if (ErrorCode c = m.finish(m.vout, res.output, H); c != ErrorCode::ok) return R::failure(c);
+    m.emit_call(layer, t_launch,
+                {{ProfileOperation::mxfp4_matvec, NumericPrecision::mxfp4_e2m1_e8m0,
+                  K * 3 * (I * L / 2 + I * L / 32)},
+                 {ProfileOperation::dense_matvec, NumericPrecision::fp32,
+                  (2 * L * H + 3 * weights.shared.gate.rows * H) * 4},
+                 {ProfileOperation::moe_mix, NumericPrecision::fp32, K * L * 4},
+                 {ProfileOperation::rms_norm, NumericPrecision::fp32, L * 8},
+                 {ProfileOperation::residual_add, NumericPrecision::fp32, H * 8}});
     ++m.stats.calls;
     ++m.stats.layer_calls;
     return R::success(std::move(res));
@@ -1398,5 +1524,10 @@ HipBackendStats HipMoeBackend::runtime_stats() const noexcept {
 }
 
 std::string_view HipMoeBackend::device_name() const noexcept { return impl_->name; }
+
+void HipMoeBackend::set_profile_sink(ProfileSink sink) {
+    impl_->sink = std::move(sink);
+    if (impl_->ctx) (void)k3x_hip_ctx_set_profiling(impl_->ctx, impl_->sink ? 1 : 0);
+}
 
 }  // namespace k3x_amd

@@ -25,6 +25,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <optional>
 #include <span>
@@ -99,6 +100,42 @@ private:
 };
 
 enum class ProfilePhase { prefill, decode };  // runtime/include/k3x/profile.hpp:11
+
+// Same enumerators in the same order as k3x::ProfileOperation and
+// k3x::NumericPrecision (runtime/include/k3x/profile.hpp:13-27).
+enum class ProfileOperation {
+    tensor_read,
+    dense_matvec,
+    mxfp4_matvec,
+    situ_glu,
+    moe_mix,
+    rms_norm,
+    residual_add,
+    host_to_device,
+    weight_host_to_device,
+    activation_host_to_device,
+    device_to_host,
+};
+enum class NumericPrecision { none, fp32, bf16_rounded, mxfp4_e2m1_e8m0 };
+
+// One operation of a method call, the members of k3x::ProfileEvent
+// (profile.hpp:32-42).  device_nanoseconds comes from the library's stage
+// events (hipEvent pairs on the context stream) where the call's kernels are
+// staged, and is the host-measured launch-to-completion time of the call
+// otherwise; logical_bytes are the bytes the operation reads by definition
+// (weights and activations), transfer_bytes the bytes a copy moved.
+struct ProfileEvent {
+    ProfilePhase phase;
+    ProfileOperation operation;
+    NumericPrecision precision;
+    std::uint32_t layer;
+    std::uint64_t wall_nanoseconds;
+    std::uint64_t device_nanoseconds;
+    std::uint64_t logical_bytes;
+    std::uint64_t transfer_bytes;
+    bool success;
+};
+using ProfileSink = std::function<void(const ProfileEvent&)>;
 
 // One MXFP4 matrix in the K3X layout: packed [rows][cols/2] (low nibble =
 // even column), scales [rows][cols/group_size] E8M0 (backend.hpp:150-157).
@@ -382,6 +419,11 @@ public:
 
     HipBackendStats runtime_stats() const noexcept;
     std::string_view device_name() const noexcept;
+    // Every later method call reports its operations to `sink` (the
+    // reference backends' Profiler::record, backend_cuda.cu:2505-2542); the
+    // library's stage timing is on while a sink is set.  An empty sink turns
+    // it off.
+    void set_profile_sink(ProfileSink sink);
 
     struct Impl;
 

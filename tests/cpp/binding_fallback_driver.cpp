@@ -12,7 +12,9 @@
 //      the call fails with backend_unavailable and is NOT recomputed on the
 //      CPU (the CUDA backend's contract, runtime/cuda/backend_cuda.cu:
 //      1806-1883; the caller raises, runtime/src/model.cpp:1034-1037);
-//   3. invalid arguments fail with invalid_mxfp4 on either shape.
+//   3. invalid arguments fail with invalid_mxfp4 on either shape;
+//   4. the Profiler given to the factory receives the CPU backend's events
+//      for the declined call.
 // Exit code 0 when every check holds; prints one line per check.
 #include "k3x/backend.hpp"
 #include "k3x_hip_backend.hpp"
@@ -70,7 +72,8 @@ int main() {
     k3x_amd::HipBackendOptions ho;
     ho.device = k3x_amd::HipBackendOptions::kNoDevice;
     ho.resident_experts = 4;
-    auto made = k3x::make_hip_backend(options, nullptr, ho);
+    k3x::Profiler profiler;
+    auto made = k3x::make_hip_backend(options, &profiler, ho);
     if (!made) {
         std::printf("factory failed: %d\n", (int)made.error());
         return 1;
@@ -97,6 +100,11 @@ int main() {
         return 3;
     }
     std::printf("declined shape: CPU backend's result, counted: ok\n");
+    const std::size_t declined_events = profiler.events().size();
+    if (declined_events == 0) {
+        std::printf("declined shape: no profile events recorded\n");
+        return 8;
+    }
 
     // 2. A shape the device runs, no device: the failure is returned.
     const k3x::Mxfp4MlpView sq[1] = {{g.view(21), u.view(22), d_sq.view(23)}};
@@ -128,5 +136,6 @@ int main() {
         }
     }
     std::printf("invalid arguments: invalid_mxfp4: ok\n");
+    std::printf("profiler: %zu events of the declined call: ok\n", declined_events);
     return 0;
 }

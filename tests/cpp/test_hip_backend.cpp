@@ -881,6 +881,37 @@ int main() {
     if (int rc = official_checks(*backend)) return rc;
     if (int rc = latent_checks(*backend)) return rc;
     if (int rc = padded_checks(*backend)) return rc;
+    // Profile events: a sink on the backend receives the call's operations,
+    // the routed projections with their stage device times and the bytes of
+    // the experts' weights.
+    {
+        std::vector<k3x_amd::ProfileEvent> ev;
+        backend->set_profile_sink([&](const k3x_amd::ProfileEvent& e) { ev.push_back(e); });
+        const Expert pe[2] = {make_expert(611), make_expert(614)};
+        const Mxfp4MlpView pv[2] = {pe[0].view(), pe[1].view()};
+        const auto xp = rand_f32(H, 1.0f);
+        auto r = backend->mxfp4_situ_mlp_group(xp, pv, kBeta, kLinear, 15, ProfilePhase::prefill);
+        backend->set_profile_sink({});
+        if (!r) return 160;
+        std::size_t mx = 0, h2d = 0;
+        std::uint64_t bytes = 0, dev = 0;
+        for (const auto& e : ev) {
+            if (e.layer != 15 || e.phase != ProfilePhase::prefill || !e.success) return 161;
+            if (e.operation == k3x_amd::ProfileOperation::mxfp4_matvec) {
+                ++mx;
+                bytes += e.logical_bytes;
+                dev += e.device_nanoseconds;
+            }
+            if (e.operation == k3x_amd::ProfileOperation::weight_host_to_device) ++h2d;
+        }
+        const std::uint64_t want = 2 * 3 * (I * H / 2 + I * H / 32);
+        if (mx != 2 || h2d != 1 || dev == 0 || bytes < want) {
+            std::printf("profile events: %zu mxfp4_matvec (%llu B, %llu ns), %zu uploads\n", mx,
+                        (unsigned long long)bytes, (unsigned long long)dev, h2d);
+            return 162;
+        }
+        std::printf("profile events (%zu, device time and expert bytes): ok\n", ev.size());
+    }
     if (int rc = latent_bypass_checks()) return rc;
     // More slots than routed experts (the normal configuration): the official
     // FFN admits only the called experts and leaves the other slots empty,

@@ -57,4 +57,4 @@ def test_binding_falls_back_only_on_declined_shapes():
         assert r.returncode == 0, r.stderr[-4000:]
         run = subprocess.run([exe], capture_output=True, text=True, timeout=120)
         assert run.returncode == 0, (run.returncode, run.stdout)
-        assert run.stdout.count(": ok") == 3, run.stdout
+        assert run.stdout.count(": ok") == 4, run.stdout
