@@ -43,6 +43,8 @@ enum k3x_status {
     K3X_ERR_INVALID_EXTENT = 9,
     K3X_ERR_DATA_CRC_MISMATCH = 10,
     K3X_ERR_AUXILIARY_CRC_MISMATCH = 11,
+    K3X_ERR_DIRECTORY_SHA256_MISMATCH = 12,
+    K3X_ERR_ROOT_SHA256_MISMATCH = 13,
     K3X_ERR_TENSOR_NOT_FOUND = 14,
     K3X_ERR_INVALID_MXFP4 = 15,
     K3X_ERR_INVALID_STATE = 16,
@@ -565,11 +567,19 @@ int k3x_hip_bank_upload_expert_device(k3x_hip_bank* bank, uint32_t expert,
  * ranges and headers, model-config invariants, tensor record fields,
  * distinct tensor ids; every tensor extent in range, 4 KiB aligned and
  * disjoint from the others.  Status codes are the reader's (K3X_ERR_IO ..
- * K3X_ERR_INVALID_EXTENT).  The directory and root SHA-256 digests are not
- * checked. */
+ * K3X_ERR_INVALID_EXTENT).  Host work only. */
 typedef struct k3x_hip_storage k3x_hip_storage;
 int k3x_hip_storage_open(const char* path, k3x_hip_storage** out);
 int k3x_hip_storage_close(k3x_hip_storage* storage);
+/* The checks Reader::open adds with VerifyMode::checksums
+ * (runtime/src/reader.cpp:672-721), in its order: every tensor's data and
+ * auxiliary CRC32C (K3X_ERR_DATA_CRC_MISMATCH, K3X_ERR_AUXILIARY_CRC_MISMATCH),
+ * the SHA-256 of the tensor, layer and expert directories and the model
+ * config concatenated against superblock bytes 168..199
+ * (K3X_ERR_DIRECTORY_SHA256_MISMATCH), the SHA-256 of the whole file with
+ * bytes 200..231 and 4092..4095 read as zeros against bytes 200..231
+ * (K3X_ERR_ROOT_SHA256_MISMATCH).  Host work only (SHA-256 is sequential). */
+int k3x_hip_storage_verify(k3x_hip_storage* storage);
 
 /* load_storage_expert (runtime/src/storage_slice.cpp:42-92) into bank slot
  * `expert`: the tensors model.layers.<layer>.feed_forward.experts.<id>.
@@ -581,9 +591,14 @@ int k3x_hip_storage_close(k3x_hip_storage* storage);
  * into pinned host memory, copied to the device once, checked against their
  * records' CRC32C on the device and uploaded with
  * k3x_hip_bank_upload_expert_device; the slot's tensor ids are the records'.
- * *bytes_read (may be NULL): the six extents' total.  Synchronous. */
+ * *bytes_read (may be NULL): the six extents' total.  ordered_sha256 (may be
+ * NULL; 32 bytes): the SHA-256 of the six extents in their order (gate data,
+ * gate scales, up data, up scales, down data, down scales), the digest
+ * load_storage_expert returns (storage_slice.cpp:80-90), formed on the host
+ * from the bytes read.  Synchronous. */
 int k3x_hip_storage_upload_expert(k3x_hip_storage* storage, k3x_hip_bank* bank, uint32_t expert,
-                                  uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read);
+                                  uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read,
+                                  uint8_t* ordered_sha256);
 
 #ifdef __cplusplus
 }

@@ -297,8 +297,14 @@ int k3x_hip_storage_close(k3x_hip_storage* s) {
     return K3X_OK;
 }
 
+int k3x_hip_storage_verify(k3x_hip_storage* s) {
+    if (!s) return K3X_ERR_INVALID_EXTENT;
+    return k3x_reader::verify_checksums(s->dir);
+}
+
 int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32_t expert,
-                                  uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read) {
+                                  uint32_t layer_id, uint32_t expert_id, uint64_t* bytes_read,
+                                  uint8_t* ordered_sha256) {
     if (!s || !bank) return K3X_ERR_INVALID_EXTENT;
     if (!(s->dir.optional_features & 1u)) return K3X_ERR_INVALID_EXTENT;  // not a storage fixture
     const auto& d = bank->desc;
@@ -380,6 +386,13 @@ int k3x_hip_storage_upload_expert(k3x_hip_storage* s, k3x_hip_bank* bank, uint32
     // while this copy still reads or writes it.
     if (st && hipStreamSynchronize(ctx->stream) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     if (!st && bytes_read) *bytes_read = len[0] + len[1] + len[2] + len[3] + len[4] + len[5];
+    if (!st && ordered_sha256) {
+        // The digest load_storage_expert returns (storage_slice.cpp:80-90):
+        // the six extents in order, from the bytes read into pinned memory.
+        k3x_reader::Sha256 h;
+        for (int i = 0; i < 6; ++i) h.update(s->pinned + at[i], len[i]);
+        h.finish(ordered_sha256);
+    }
     return st;
 }
 

@@ -140,7 +140,8 @@ _SIGS = {
     "k3x_hip_storage_open": (C.c_int, [C.c_char_p, C.POINTER(_vp)]),
     "k3x_hip_storage_close": (C.c_int, [_vp]),
     "k3x_hip_storage_upload_expert": (C.c_int, [_vp, _vp, C.c_uint32, C.c_uint32, C.c_uint32,
-                                                C.POINTER(C.c_uint64)]),
+                                                C.POINTER(C.c_uint64), C.c_void_p]),
+    "k3x_hip_storage_verify": (C.c_int, [_vp]),
     "k3x_hip_bank_upload_expert_device": (C.c_int, [_vp, C.c_uint32, C.POINTER(C.c_uint64),
                                                     C.POINTER(_vp), C.POINTER(C.c_uint32)]),
     "k3x_hip_bank_find": (C.c_int, [_vp, C.c_uint64, C.POINTER(C.c_uint32),
@@ -568,8 +569,21 @@ class Storage:
         """(status, bytes read) of load_storage_expert into bank slot `slot`."""
         n = C.c_uint64(0)
         st = self.lib.k3x_hip_storage_upload_expert(self.handle, bank.handle, slot, layer_id,
-                                                    expert_id, C.byref(n))
+                                                    expert_id, C.byref(n), None)
         return st, n.value
+
+    def upload_expert_digest(self, bank: "Bank", slot: int, layer_id: int, expert_id: int):
+        """(status, bytes read, the six extents' ordered SHA-256 as 32 bytes)."""
+        n = C.c_uint64(0)
+        d = (C.c_uint8 * 32)()
+        st = self.lib.k3x_hip_storage_upload_expert(self.handle, bank.handle, slot, layer_id,
+                                                    expert_id, C.byref(n), C.cast(d, C.c_void_p))
+        return st, n.value, bytes(d)
+
+    def verify(self) -> int:
+        """Reader::open's checksums verification: tensor CRC32Cs, directory and
+        root SHA-256 (status code)."""
+        return self.lib.k3x_hip_storage_verify(self.handle)
 
     def close(self) -> None:
         if self.handle:

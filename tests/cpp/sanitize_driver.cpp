@@ -102,17 +102,24 @@ int run_checks(std::uint64_t seed, long n) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc >= 2 && !std::strcmp(argv[1], "reader")) {
+    if (argc >= 2 && (!std::strcmp(argv[1], "reader") || !std::strcmp(argv[1], "verify"))) {
+        // reader: the open status of each file; verify: also the checksum
+        // verification of each file that opens (-1 when it does not).
+        const bool verify = argv[1][0] == 'v';
         for (int i = 2; i < argc; ++i) {
             k3x_reader::Directory d;
             const int st = k3x_reader::open_checked(&d, argv[i]);
+            const int vst = verify ? (st ? -1 : k3x_reader::verify_checksums(d)) : 0;
             k3x_reader::close(&d);
-            std::printf("%d\n", st);
+            if (verify)
+                std::printf("%d %d\n", st, vst);
+            else
+                std::printf("%d\n", st);
         }
         return 0;
     }
     if (argc == 4 && !std::strcmp(argv[1], "checks"))
         return run_checks(std::stoull(argv[2]), std::stol(argv[3]));
-    std::fprintf(stderr, "usage: %s reader FILE... | checks SEED N\n", argv[0]);
+    std::fprintf(stderr, "usage: %s reader|verify FILE... | checks SEED N\n", argv[0]);
     return 2;
 }

@@ -4,10 +4,14 @@ Layout follows K3X_FORMAT.md: 4 KiB superblock (magic K3XCHKPT, version
 1.0, finalized, CRC32C over bytes 0..4091 at 4092), 4 KiB-aligned payload
 extents, then the tensor (TENS, 128-byte records), layer (LAYR, 64-byte),
 expert (EXPT, 64-byte) directories and the 256-byte model config, each 4 KiB
-aligned.  The digests at 168..231 are left zero (the loader does not check
-them).  `crc` is a CRC32C function (the oracle's)."""
+aligned.  The digests at 168..231 are those Reader::open checks with
+VerifyMode::checksums (runtime/src/reader.cpp:672-721), computed here with
+Python's hashlib: the SHA-256 of the four directories concatenated, and of
+the whole file with bytes 200..231 and 4092..4095 taken as zeros.  `crc` is
+a CRC32C function (the oracle's)."""
 from __future__ import annotations
 
+import hashlib
 import struct
 
 
@@ -35,8 +39,10 @@ def expert_tensors(layer: int, expert: int, ex: dict, inter: int, hidden: int) -
 
 
 def write_k3x(path: str, tensors: list[dict], crc, optional_features: int = 1,
-              layers: int = 1, required_features: int = 0) -> dict:
-    """Writes the file; returns the offsets it used (for corruption tests)."""
+              layers: int = 1, required_features: int = 0, bad_directory_digest: bool = False,
+              bad_root_digest: bool = False) -> dict:
+    """Writes the file; returns the offsets it used (for corruption tests).
+    bad_*_digest: store that digest with its first byte flipped."""
     at = 4096
     payload = []
     recs = []
@@ -75,11 +81,19 @@ def write_k3x(path: str, tensors: list[dict], crc, optional_features: int = 1,
     for off, blob in dirs:
         vals += [off, len(blob)]
     struct.pack_into("<10Q", sb, 88, *vals, 4096, total)
-    struct.pack_into("<I", sb, 4092, crc(bytes(sb[:4092])))
+    dir_digest = bytearray(hashlib.sha256(b"".join(blob for _, blob in dirs)).digest())
+    if bad_directory_digest:
+        dir_digest[0] ^= 0xFF
+    sb[168:200] = dir_digest
     buf = bytearray(total)
     buf[:4096] = sb
     for off, blob in payload + dirs:
         buf[off:off + len(blob)] = blob
+    root_digest = bytearray(hashlib.sha256(bytes(buf)).digest())  # 200..231, 4092.. still zero
+    if bad_root_digest:
+        root_digest[0] ^= 0xFF
+    buf[200:232] = root_digest
+    struct.pack_into("<I", buf, 4092, crc(bytes(buf[:4092])))
     with open(path, "wb") as f:
         f.write(buf)
     return {"payload": [o for o, _ in payload], "dirs": [o for o, _ in dirs], "total": total}

@@ -3,7 +3,8 @@ CRC32C (itself pinned to the published check values and to the reference's
 crc32c.cpp, tests/test_storage.py) over ragged and multi-chunk sizes, and
 k3x_hip_storage_upload_expert (load_storage_expert, runtime/src/
 storage_slice.cpp:42-92) against a host upload of the same expert: the bank
-slots dequantise bit-identically and a layer call through each gives the
+slots dequantise bit-identically, the load's ordered SHA-256 equals
+hashlib's over the six extents, and a layer call through each gives the
 same output; corrupted CRCs, a missing tensor, a wrong shape and a file
 without the STORAGE_FIXTURE feature are rejected with the reader's codes."""
 from __future__ import annotations
@@ -89,9 +90,15 @@ def test_storage_upload(hip, oracle, tmp_path, hidden, inter):
     a, b = k3x_amd.Bank(ctx, shape), k3x_amd.Bank(ctx, shape)
     store = k3x_amd.Storage(path)
     assert store.open_status == 0
+    import hashlib
     for e, ex in enumerate(experts):
-        st, n = store.upload_expert(a, e, 3, e)
+        st, n, digest = store.upload_expert_digest(a, e, 3, e)
         assert st == 0 and n == 3 * (inter * hidden // 2 + inter * hidden // 32)
+        # The ordered SHA-256 load_storage_expert returns (storage_slice.cpp:
+        # 80-90): the six extents in order, against Python's hashlib.
+        want = hashlib.sha256(b"".join(bytes(ex[f"{r}_{k}"]) for r in ("gate", "up", "down")
+                                       for k in ("packed", "scales"))).digest()
+        assert digest == want, e
         assert b.upload_expert(e, ex, tensor_ids=(100 + 3 * e, 101 + 3 * e, 102 + 3 * e)) == 0
         for m, rows in ((0, inter), (1, inter), (2, hidden)):
             ra = a.dequant_rows(e, m, 0, rows)

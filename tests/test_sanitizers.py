@@ -4,7 +4,9 @@ UndefinedBehaviorSanitizer and run on the CPU (tests/cpp/sanitize_driver.cpp):
 * the K3X reader's open-time checks (project-k3x_amd/csrc/k3x_reader.cpp) over
   the corrupted files of tests/test_storage.py and 300 seeded mutants of a
   good file (byte changes in the superblock, the directories and the payload,
-  and truncations); every status must equal the library's own open;
+  and truncations); every status must equal the library's own open; then the
+  checksum verification (CRC32C, directory and root SHA-256) of every mutant
+  that opens, which must equal the library's own k3x_hip_storage_verify;
 * HipMoeBackend's argument checks (project-k3x_amd/host/k3x_hip_checks.hpp)
   over 20,000 randomised views: extents that disagree with their spans,
   products past SIZE_MAX, zero and odd sizes, 0xFF scales, non-finite values.
@@ -88,3 +90,22 @@ def test_reader_under_sanitizers(driver, oracle, tmp_path):
 def test_backend_checks_under_sanitizers(driver):
     out = run(driver, "checks", "1", "20000")
     assert out.startswith("checks: 20000 views")
+
+
+def test_reader_verification_under_sanitizers(driver, oracle, tmp_path):
+    import k3x_amd
+    cases = reader_cases(oracle, tmp_path)
+    paths = [p for p, _ in cases] + mutants(cases[0][0], tmp_path, 120)
+    got = [tuple(int(v) for v in line.split()) for line in
+           run(driver, "verify", *paths).strip().splitlines()]
+    assert got[0] == (0, 0)  # the good file opens and verifies
+    opened = 0
+    for path, (st, vst) in zip(paths, got):
+        s = k3x_amd.Storage(path)
+        assert s.open_status == st
+        if st == 0:
+            opened += 1
+            assert s.verify() == vst, os.path.basename(path)
+        s.close()
+    # Payload mutants open and then fail their CRC: the verification runs.
+    assert opened > 10 and any(v in (10, 11, 12, 13) for _, v in got)

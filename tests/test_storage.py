@@ -132,3 +132,41 @@ def test_reader_open_checks(oracle, tmp_path):
     for path, want in reader_cases(oracle, tmp_path):
         assert open_status(path) == want, os.path.basename(path)
     del k3x_amd
+
+
+def test_reader_checksum_verification(oracle, tmp_path):
+    """k3x_hip_storage_verify: Reader::open's checksums mode
+    (runtime/src/reader.cpp:672-721) in its order -- tensor data and
+    auxiliary CRC32C, the directories' SHA-256, the whole file's SHA-256 --
+    on a good file (digests written with Python's hashlib, an independent
+    SHA-256) and on one file per failing check."""
+    import k3x_amd
+    crc = oracle.crc32c
+    t = small_tensors(oracle)
+    good = str(tmp_path / "good.k3x")
+    layout = write_k3x(good, t, crc)
+    cases = [(good, 0)]
+    p = str(tmp_path / "dir_digest.k3x")
+    write_k3x(p, t, crc, bad_directory_digest=True)
+    cases.append((p, 12))
+    p = str(tmp_path / "root_digest.k3x")
+    write_k3x(p, t, crc, bad_root_digest=True)
+    cases.append((p, 13))
+    # A payload byte changed: the data CRC fails first (the digests too).
+    p = str(tmp_path / "data.k3x")
+    write_k3x(p, t, crc)
+    rewrite(p, layout["payload"][0] + 5, b"\x5a", False, oracle)
+    cases.append((p, 10))
+    # A scale byte of the second extent: the auxiliary CRC.
+    p = str(tmp_path / "aux.k3x")
+    write_k3x(p, t, crc)
+    b = bytearray(open(p, "rb").read())
+    at = layout["payload"][1] + 3
+    b[at] ^= 0x01
+    open(p, "wb").write(bytes(b))
+    cases.append((p, 11))
+    for path, want in cases:
+        s = k3x_amd.Storage(path)
+        assert s.open_status == 0, os.path.basename(path)
+        assert s.verify() == want, os.path.basename(path)
+        s.close()
