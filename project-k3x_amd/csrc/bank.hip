@@ -421,8 +421,8 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
         hipMemset(ctx->status, 0, 256) != hipSuccess ||
-        hipMalloc((void**)&ctx->mix_counts, k3x_hip::kDecodeMixBytes) != hipSuccess ||
-        hipMemset(ctx->mix_counts, 0, k3x_hip::kDecodeMixBytes) != hipSuccess ||
+        hipMalloc((void**)&ctx->mix_counts, k3x_hip::kDecodeMixBytes + 256) != hipSuccess ||
+        hipMemset(ctx->mix_counts, 0, k3x_hip::kDecodeMixBytes + 256) != hipSuccess ||
         hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
             hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
@@ -436,6 +436,8 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         delete ctx;
         return K3X_ERR_BACKEND_UNAVAILABLE;
     }
+    ctx->route_counter = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ctx->mix_counts) +
+                                                     k3x_hip::kDecodeMixBytes);
     ctx->max_lds_per_block = (size_t)lds;
     ctx->cu_count = (uint32_t)cus;
     ctx->stream = ctx->own_stream;
@@ -517,7 +519,12 @@ int k3x_hip_ctx_synchronize(k3x_hip_ctx* ctx) {
         return K3X_ERR_BACKEND_UNAVAILABLE;
     }
     if (status) {
+        // A latched error leaves every later launch of the calls in flight
+        // idle; the arrival counters are cleared with the word, whatever
+        // state such a call left them in.
         if (hipMemsetAsync(ctx->status, 0, sizeof(uint32_t), ctx->stream) != hipSuccess ||
+            hipMemsetAsync(ctx->mix_counts, 0, k3x_hip::kDecodeMixBytes + 256, ctx->stream) !=
+                hipSuccess ||
             hipStreamSynchronize(ctx->stream) != hipSuccess)
             return K3X_ERR_BACKEND_UNAVAILABLE;
         return (int)status;

@@ -1112,6 +1112,7 @@ struct DownArgs {
     uint16_t* out;
     float* out_f32;            // optional
     uint32_t* mix;
+    uint32_t round_y;          // each y rounded to bf16 before its product
     const uint32_t* status;
 };
 
@@ -1123,9 +1124,11 @@ struct DownArgs {
 // around them).
 constexpr int kCombineBatch = 16;
 
+// round_y: the official layer rounds each expert output to bf16 first
+// (runtime/src/official_moe.cpp:99-101), as combine_kernel does.
 __device__ inline void decode_mix(const float* y, const float* weights, const float* shared_y,
                                   uint32_t K, uint32_t H, uint32_t t, uint32_t h, uint16_t* out,
-                                  float* out_f32) {
+                                  float* out_f32, bool round_y) {
     const float* yr = y + (size_t)t * K * H + h;
     const float* wr = weights + (size_t)t * K;
     const float sh = shared_y ? shared_y[(size_t)t * H + h] : 0.0f;
@@ -1142,8 +1145,11 @@ __device__ inline void decode_mix(const float* y, const float* weights, const fl
             wv[u] = wr[s];
         }
 #pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u)
-            if (s0 + u < K) mix = __fadd_rn(mix, __fmul_rn(wv[u], yv[u]));
+        for (int u = 0; u < kCombineBatch; ++u) {
+            const float yu =
+                round_y ? __uint_as_float((uint32_t)f32_to_bf16(yv[u]) << 16) : yv[u];
+            if (s0 + u < K) mix = __fadd_rn(mix, __fmul_rn(wv[u], yu));
+        }
     }
     const float v = shared_y ? __fadd_rn(mix, sh) : mix;
     out[(size_t)t * H + h] = f32_to_bf16(v);
@@ -1280,7 +1286,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
         old = __shfl(old, 0);
         if (old == a.K - 1) {  // issued after the increment returned
             decode_mix(a.y, a.weights, a.shared_y, a.K, a.H, t, hg * 64 + lane, a.out,
-                       a.out_f32);
+                       a.out_f32, a.round_y != 0);
             if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
@@ -1502,11 +1508,17 @@ int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t 
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 
+bool few_row_mix_eligible(const k3x_hip_bank* bank, uint32_t T) {
+    return T <= (uint32_t)kDownWaves && bank->desc.hidden / 64 <= kMixGroupsMax;
+}
+
 int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
-                        const LayerBuffers& b, bool split, bool chunked) {
+                        const LayerBuffers& b, bool split, bool chunked, const FewRowMix* mix) {
     const auto& d = bank->desc;
     if (T > (chunked ? kChunkedMaxTokens : (uint32_t)kMaxDecodeTokens) ||
         !few_row_experts_eligible(ctx, bank, chunked ? kRowChunk : T, split))
+        return K3X_ERR_INVALID_EXTENT;
+    if (mix && (chunked || !few_row_mix_eligible(bank, T) || !b.mix || !mix->out))
         return K3X_ERR_INVALID_EXTENT;
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
@@ -1525,7 +1537,15 @@ int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, 
     dn.pair_token = b.pair_token;
     dn.pair_slot = b.pair_slot;
     dn.y = b.y;
-    dn.mix = nullptr;  // the general path's combine follows
+    dn.mix = nullptr;  // without mix, the general path's combine follows
+    if (mix) {
+        dn.weights = mix->weights;
+        dn.shared_y = mix->shared_y;
+        dn.out = mix->out;
+        dn.out_f32 = mix->out_f32;
+        dn.round_y = mix->round_y ? 1u : 0u;
+        dn.mix = b.mix;
+    }
     dn.status = ctx->status;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     const uint32_t rows = chunked ? kRowChunk : T;

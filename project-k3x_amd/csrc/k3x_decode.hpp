@@ -40,8 +40,22 @@ bool few_row_experts_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank, 
 int launch_few_row_gate_up(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
                            const LayerBuffers& b, const uint16_t* xn,
                            const k3x_dev::GluParams& glu, bool split, bool chunked = false);
+// mix (optional): the combine fused into the down launch, as on the decode
+// path (b.mix's counters, zero before and after): out = bf16(sum over slots
+// in router order of w * y (y rounded to bf16 first with round_y) +
+// shared_y), out_f32 (may be null) the same sum in fp32.  Few tokens only
+// (few_row_mix_eligible), not chunked.
+struct FewRowMix {
+    const float* weights;   // [T][K]
+    const float* shared_y;  // [T][H] or null
+    uint16_t* out;          // [T][H]
+    float* out_f32;
+    bool round_y;
+};
+bool few_row_mix_eligible(const k3x_hip_bank* bank, uint32_t T);
 int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, uint32_t K,
-                        const LayerBuffers& b, bool split, bool chunked = false);
+                        const LayerBuffers& b, bool split, bool chunked = false,
+                        const FewRowMix* mix = nullptr);
 
 // out[t][h] = bf16(sum over slots in router order of w[t][s] * y[t][s][h]
 // + shared[t][h]) on the context stream (the combine of both paths).

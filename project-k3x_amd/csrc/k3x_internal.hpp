@@ -41,6 +41,9 @@ struct k3x_hip_ctx {
     // Decode combine counters of k3x_hip_moe_forward (zeroed at creation,
     // left zero by every call).
     uint32_t* mix_counts = nullptr;
+    // Arrival counter of the fused Top-K and grouping launch (zeroed at
+    // creation, left zero by every launch).
+    uint32_t* route_counter = nullptr;
     uint64_t forward_calls = 0;
     uint64_t kernel_launches = 0;
     uint64_t weight_h2d_bytes = 0;
@@ -139,9 +142,66 @@ struct LayerBuffers {
     // Decode path: arrival counters of the fused combine (kDecodeMixBytes,
     // zero between calls); set by the entry point, not by the carve.
     uint32_t* mix;
+    // The route was grouped into these buffers already (the fused Top-K and
+    // grouping launch); the routed call skips its own grouping.
+    bool grouped = false;
 };
 
 inline int fail_hip(hipError_t e) { return e == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE; }
+
+// The routed call of k3x_hip_moe_forward_routed in two halves, for a caller
+// that groups the route itself in between (the official layer's fused
+// Top-K and grouping): routed_begin checks the parameters and carves the
+// call's scratch into *s; routed_finish groups the route (unless
+// s.grouped), runs the experts and the combine, and copies the taps.
+int routed_begin(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                 LayerBuffers* s);
+int routed_finish(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                  const LayerBuffers& s, const uint16_t* xn, const uint32_t* ids,
+                  const float* weights, uint16_t* out, const k3x_hip_moe_taps* taps);
+// Whether the Top-K of T tokens over E experts and the grouping of its
+// T * K pairs run as one launch (topk_group_kernel): the threshold Top-K's
+// expert counts (256 < E <= 1024), the pairs within one grouping workgroup,
+// fewer tokens than the wide GEMM takes.
+bool topk_group_eligible(uint32_t E, uint32_t K, uint32_t T);
+// That launch: ids and weights of the route, and the grouping into s's
+// buffers (counts, offsets, CSR rows, first uses, active lists, active-slot
+// records); ready (may be null) as launch_group.
+int launch_topk_group(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E,
+                      uint32_t K, uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids,
+                      float* weights, const uint32_t* ready, const LayerBuffers& s);
+
+// The official layer's route, latent projection and shared FFN for a few
+// tokens in two launches on the context stream (the shared FFN's weight
+// streams beside the route's latency-bound steps):
+//   front   logits = router . hidden (fp64, canonical order), latent =
+//           bf16(latent_tiles . hidden), sact = GLU(shared gate/up . hidden)
+//           as split [hi | lo] rows of 2 I_s;
+//   select  the Top-K (sigmoid + correction, double contributions, scale 1)
+//           grouped into s's buffers as launch_topk_group, and shared =
+//           shared_dn . sact (fp32).
+// I_s = 0: no shared FFN.
+struct OfficialDecode {
+    const float* router;
+    const float* correction;
+    uint32_t E, H, L, I_s, K, T;
+    const uint16_t* hidden;    // [T][H]
+    const uint4* latent_tiles; // L x H
+    uint16_t* latent;          // [T][L]
+    const uint4* shared_gu;    // 2 I_s x H (gate, up)
+    const uint4* shared_dn;    // H x I_s
+    k3x_dev::GluParams glu;
+    uint16_t* sact;            // [T][2 I_s]
+    float* shared;             // [T][H]
+    float* logits;             // [T][E]
+    uint32_t* ids;             // [T][K]
+    float* weights;            // [T][K]
+    const uint32_t* ready;     // the bank's admitted-slot words
+};
+bool official_decode_eligible(uint32_t E, uint32_t H, uint32_t L, uint32_t I_s, uint32_t K,
+                              uint32_t T);
+int launch_official_front(k3x_hip_ctx* ctx, const OfficialDecode& d);
+int launch_official_select(k3x_hip_ctx* ctx, const OfficialDecode& d, const LayerBuffers& s);
 
 // Makes sure ctx->scratch holds at least `bytes`; grow-only.
 int ensure_scratch(k3x_hip_ctx* ctx, size_t bytes);
@@ -197,6 +257,9 @@ constexpr uint32_t kDenseDirectTokens = 16;
 // True when both projections of a dense GLU MLP (gate/up I x H, down H x I)
 // may be enqueued on a stream other than the context's for T rows.
 bool dense_mlp_any_stream(uint32_t I, uint32_t H, uint32_t T);
+// True when dense_down of an N x K projection over T rows may be enqueued on
+// a stream other than the context's.
+bool dense_down_any_stream(uint32_t N, uint32_t K, uint32_t T);
 int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, const uint16_t* a,
                uint32_t T, float* y, hipStream_t stream, uint16_t* y_bf16 = nullptr,
                bool split = false);

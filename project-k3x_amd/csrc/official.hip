@@ -54,8 +54,9 @@ struct k3x_hip_official {
     size_t scratch_bytes = 0;
     uint16_t* xp = nullptr;
     size_t xp_bytes = 0;
-    // The shared FFN runs on the context's side stream between these.
-    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    // The latent projection and the shared FFN run on the context's side
+    // stream between fork_ev and join_ev; latent_ev marks the latent done.
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr, latent_ev = nullptr;
 };
 
 namespace {
@@ -302,6 +303,7 @@ void free_all(k3x_hip_official* o) {
         if (p) (void)hipFree(p);
     if (o->fork_ev) (void)hipEventDestroy(o->fork_ev);
     if (o->join_ev) (void)hipEventDestroy(o->join_ev);
+    if (o->latent_ev) (void)hipEventDestroy(o->latent_ev);
 }
 
 // Work of an earlier call may still use the per-call buffers on either stream.
@@ -460,7 +462,8 @@ int k3x_hip_official_create(k3x_hip_ctx* ctx, k3x_hip_bank* experts,
         st = st ? st : alloc(&o->router_wp, k3x_hip::router_wp_floats(o->E) * 4);
     st = st ? st : alloc(&o->correction, (size_t)o->E * 4);
     if (!st && (hipEventCreateWithFlags(&o->fork_ev, hipEventDisableTiming) != hipSuccess ||
-                hipEventCreateWithFlags(&o->join_ev, hipEventDisableTiming) != hipSuccess))
+                hipEventCreateWithFlags(&o->join_ev, hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&o->latent_ev, hipEventDisableTiming) != hipSuccess))
         st = K3X_ERR_BACKEND_UNAVAILABLE;
     if (st) {
         free_all(o);
@@ -629,14 +632,34 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     int st = ensure(o, carve(nullptr, o, T, K, &b));
     if (st) return st;
     carve(static_cast<uint8_t*>(o->scratch), o, T, K, &b);
+    // Experts on the latent: the bank's grouped path with fp32 activations
+    // into the down projection, each expert output rounded to bf16 before the
+    // slot-ordered mix, the mix rounded (official_moe.cpp:82-103, :313-326).
+    k3x_hip_moe_params ep = *p;
+    ep.routed_scale = 1.0f;
+    ep.renorm = K3X_RENORM_DOUBLE;
+    ep.flags = K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT;
+    k3x_hip::LayerBuffers rs;
+    // Its scratch is carved (and grown) before any launch of this call.
+    if ((st = k3x_hip::routed_begin(ctx, o->bank, &ep, &rs))) return st;
     const GluParams glu{(int)p->glu, p->situ_beta, (int)p->has_situ_linear, p->situ_linear_beta};
     // Shared FFN on hidden (official_moe.cpp:105-117, :307): on the side
     // stream beside the route and the experts (few rows: the routed kernels
     // leave the device half idle; many rows: the latency-bound route steps
     // and the experts' tails do), joined before the output; in line when
     // its projections cannot leave the context stream.
-    const bool side = o->I_s && ctx->side_stream && !ctx->profiling &&
+    // Few tokens with the route found here: the route, the latent projection
+    // and the shared FFN in two launches on the context stream (the
+    // projections' workgroups beside the route's), no second stream.
+    const bool fused = !ids && o->bank->desc.experts == o->E &&
+                       k3x_hip::official_decode_eligible(o->E, o->H, o->L, o->I_s, K, T);
+    const bool side = !fused && o->I_s && ctx->side_stream && !ctx->profiling &&
                       k3x_hip::dense_mlp_any_stream(o->I_s, o->H, T);
+    // The latent projection needs hidden only: with the route found here it
+    // goes first on the side stream, beside the route's latency-bound
+    // launches, and the experts wait for it alone.
+    const bool latent_side = !fused && !ids && ctx->side_stream && !ctx->profiling &&
+                             k3x_hip::dense_down_any_stream(o->L, o->H, T);
     struct Join {
         k3x_hip_official* o;
         bool armed = false;
@@ -660,11 +683,27 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
         return r ? r : k3x_hip::dense_down(ctx, o->shared_dn, o->H, o->I_s, b.sact, T, b.shared,
                                            stream, nullptr, true);
     };
-    if (side) {
+    // latent = bf16(routed_down . hidden) (official_moe.cpp:305); few rows
+    // round in the GEMV's own epilogue.
+    auto latent = [&](hipStream_t stream) {
+        if (T <= k3x_hip::kDenseDirectTokens)
+            return k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, nullptr, stream,
+                                       b.latent);
+        const int r = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T,
+                                          b.latent_f32, stream);
+        if (r) return r;
+        hipLaunchKernelGGL(round_bf16_kernel, dim3(blocks_for((size_t)T * o->L)), dim3(kThreads),
+                           0, stream, b.latent_f32, (size_t)T * o->L, b.latent);
+        return launched(ctx, 1);
+    };
+    if (side || latent_side) {
         if (hipEventRecord(o->fork_ev, ctx->stream) != hipSuccess ||
             hipStreamWaitEvent(ctx->side_stream, o->fork_ev, 0) != hipSuccess)
             return K3X_ERR_BACKEND_UNAVAILABLE;
-        const int sst = shared_ffn(ctx->side_stream);
+        int sst = latent_side ? latent(ctx->side_stream) : K3X_OK;
+        if (!sst && latent_side && hipEventRecord(o->latent_ev, ctx->side_stream) != hipSuccess)
+            sst = K3X_ERR_BACKEND_UNAVAILABLE;
+        if (!sst && side) sst = shared_ffn(ctx->side_stream);
         if (hipEventRecord(o->join_ev, ctx->side_stream) != hipSuccess) {
             (void)hipStreamSynchronize(ctx->side_stream);
             return K3X_ERR_BACKEND_UNAVAILABLE;
@@ -674,39 +713,45 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     }
     // Route (official_moe.cpp:211-269): logits over hidden, sigmoid +
     // correction, natural Top-K, contributions s / sum s in double.
-    if (!ids) {
+    if (fused) {
+        const k3x_hip::OfficialDecode od{o->router,      o->correction, o->E,       o->H,
+                                         o->L,           o->I_s,        K,          T,
+                                         hidden,         o->routed_down, b.latent,  o->shared_gu,
+                                         o->shared_dn,   sglu,          b.sact,     b.shared,
+                                         b.logits,       b.ids,         b.contrib,
+                                         o->bank->ready_dev};
+        st = k3x_hip::launch_official_front(ctx, od);
+        st = st ? st : k3x_hip::launch_official_select(ctx, od, rs);
+        if (st) return st;
+        rs.grouped = true;
+        ids = b.ids;
+        contributions = b.contrib;
+    } else if (!ids) {
+        // Few pairs: the Top-K groups the route into the routed call's
+        // buffers in the same launch (the routed call skips its grouping).
+        rs.grouped = o->bank->desc.experts == o->E && k3x_hip::topk_group_eligible(o->E, K, T);
         st = route_logits(o, hidden, T, b.logits);
-        st = st ? st : k3x_hip::launch_topk(ctx, b.logits, o->correction, o->E, K, T, 1.0f,
-                                            K3X_RENORM_DOUBLE, b.ids, b.contrib);
+        if (rs.grouped)
+            st = st ? st : k3x_hip::launch_topk_group(ctx, b.logits, o->correction, o->E, K, T,
+                                                      1.0f, K3X_RENORM_DOUBLE, b.ids, b.contrib,
+                                                      o->bank->ready_dev, rs);
+        else
+            st = st ? st : k3x_hip::launch_topk(ctx, b.logits, o->correction, o->E, K, T, 1.0f,
+                                                K3X_RENORM_DOUBLE, b.ids, b.contrib);
         if (st) return st;
         ids = b.ids;
         contributions = b.contrib;
     }
-    // latent = bf16(routed_down . hidden) (official_moe.cpp:305); few rows
-    // round in the GEMV's own epilogue.
-    if (T <= k3x_hip::kDenseDirectTokens) {
-        st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, nullptr, ctx->stream,
-                                 b.latent);
-        if (st) return st;
-    } else {
-        st = k3x_hip::dense_down(ctx, o->routed_down, o->L, o->H, hidden, T, b.latent_f32,
-                                 ctx->stream);
-        if (st) return st;
-        hipLaunchKernelGGL(round_bf16_kernel, dim3(blocks_for((size_t)T * o->L)), dim3(kThreads),
-                           0, ctx->stream, b.latent_f32, (size_t)T * o->L, b.latent);
-        if ((st = launched(ctx, 1))) return st;
+    if (latent_side) {
+        if (hipStreamWaitEvent(ctx->stream, o->latent_ev, 0) != hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+    } else if (!fused && (st = latent(ctx->stream))) {
+        return st;
     }
-    // Experts on the latent: the bank's grouped path with fp32 activations
-    // into the down projection, each expert output rounded to bf16 before the
-    // slot-ordered mix, the mix rounded (official_moe.cpp:82-103, :313-326).
-    k3x_hip_moe_params ep = *p;
-    ep.routed_scale = 1.0f;
-    ep.renorm = K3X_RENORM_DOUBLE;
-    ep.flags = K3X_FLAG_ROUND_EXPERT_OUT | K3X_FLAG_SPLIT_ACT;
     k3x_hip_moe_taps et{};
     if (taps) et.expert_out = taps->expert_out;
-    st = k3x_hip_moe_forward_routed(ctx, o->bank, &ep, b.latent, ids, contributions, nullptr,
-                                    nullptr, b.mixed, taps ? &et : nullptr);
+    st = k3x_hip::routed_finish(ctx, o->bank, &ep, rs, b.latent, ids, contributions, b.mixed,
+                                taps ? &et : nullptr);
     if (st) return st;
     // routed = routed_up . RMSNorm(mixed, routed_norm) (official_moe.cpp:327-333).
     st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon, b.normed);
@@ -714,7 +759,7 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     if (T <= k3x_hip::kDenseDirectTokens) {
         // Few rows: the output formula in the routed_up GEMV's epilogue, after
         // the shared FFN (long finished on the side stream by now).
-        if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
+        if (!st && o->I_s && !side && !fused) st = shared_ffn(ctx->stream);
         st = st ? st : joiner.join();
         st = st ? st : k3x_hip::dense_down_output(ctx, o->routed_up, o->H, o->L, b.normed, T,
                                                   prefix, o->I_s ? b.shared : nullptr, b.routed,
@@ -723,7 +768,7 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     } else {
         st = st ? st : k3x_hip::dense_down(ctx, o->routed_up, o->H, o->L, b.normed, T, b.routed,
                                            ctx->stream);
-        if (!st && o->I_s && !side) st = shared_ffn(ctx->stream);
+        if (!st && o->I_s && !side && !fused) st = shared_ffn(ctx->stream);
         st = st ? st : joiner.join();
         if (st) return st;
         const bool vec = n % 4 == 0 && reinterpret_cast<uintptr_t>(prefix) % 16 == 0 &&

@@ -206,15 +206,16 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ W
 // loads in turn).  Buffer loads: rows and terms past the ends read 0, and
 // their +0 terms come after the last real one, leaving each partial
 // unchanged (a partial started at +0 is never -0).
+// Experts [blk * EPB, blk * EPB + EPB) by a workgroup of 256 threads.
 template <int EPB, int TPB>
-__global__ __launch_bounds__(256) void router_reg_kernel(const float* __restrict__ W,
-                                                         const uint16_t* __restrict__ xn,
-                                                         uint32_t E, uint32_t H, uint32_t T,
-                                                         float* __restrict__ logits,
-                                                         const uint32_t* status) {
+__device__ __forceinline__ void router_reg_body(const float* __restrict__ W,
+                                                const uint16_t* __restrict__ xn, uint32_t E,
+                                                uint32_t H, uint32_t T,
+                                                float* __restrict__ logits,
+                                                const uint32_t* status, uint32_t blk) {
     __shared__ double red[4][EPB * TPB];
     if (*(volatile const uint32_t*)status) return;
-    const uint32_t tid = threadIdx.x, e0 = blockIdx.x * EPB;
+    const uint32_t tid = threadIdx.x, e0 = blk * EPB;
     float w[EPB][32];
     uint32_t xb[TPB][32];
 #pragma unroll
@@ -266,6 +267,15 @@ __global__ __launch_bounds__(256) void router_reg_kernel(const float* __restrict
             logits[(size_t)b * E + e0 + a] =
                 (float)((red[0][i] + red[1][i]) + (red[2][i] + red[3][i]));
     }
+}
+
+template <int EPB, int TPB>
+__global__ __launch_bounds__(256) void router_reg_kernel(const float* __restrict__ W,
+                                                         const uint16_t* __restrict__ xn,
+                                                         uint32_t E, uint32_t H, uint32_t T,
+                                                         float* __restrict__ logits,
+                                                         const uint32_t* status) {
+    router_reg_body<EPB, TPB>(W, xn, E, H, T, logits, status, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -676,11 +686,14 @@ __global__ __launch_bounds__(64) void topk_reg_kernel(const float* __restrict__ 
 constexpr uint32_t kTopkThrThreads = 256;
 constexpr uint32_t kTopkThrMaxTokens = 256;  // tokens up to which launch_topk_any uses it
 
-template <int EPT>
-__global__ __launch_bounds__(kTopkThrThreads) void topk_thr_kernel(
+// PUBLISH: ids and weights are stored at device scope (coherent across the
+// XCDs' L2s), for a workgroup of the same launch to read them.
+// Token t by a workgroup of kTopkThrThreads.
+template <int EPT, bool PUBLISH>
+__device__ __forceinline__ void topk_thr_body(
     const float* __restrict__ logits, const float* __restrict__ bias, uint32_t E, uint32_t K,
     float routed_scale, uint32_t renorm, uint32_t* __restrict__ ids,
-    float* __restrict__ weights, uint32_t* status) {
+    float* __restrict__ weights, uint32_t* status, uint32_t t) {
     constexpr uint32_t kN = kTopkThrThreads * EPT;
     __shared__ __align__(16) uint64_t ckey[kN];  // survivors' keys, compacted, 0 past them
     __shared__ uint32_t cid[kN];
@@ -689,7 +702,7 @@ __global__ __launch_bounds__(kTopkThrThreads) void topk_thr_kernel(
     __shared__ uint32_t sel[64];
     __shared__ float selsc[64];
     __shared__ uint32_t ncand, thr, bad, prior;
-    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool dbl = renorm == K3X_RENORM_DOUBLE;
     constexpr uint32_t kErrExtent = K3X_ERR_INVALID_EXTENT, kErrState = K3X_ERR_INVALID_STATE;
     float lv[EPT], bv[EPT];
@@ -811,11 +824,27 @@ __global__ __launch_bounds__(kTopkThrThreads) void topk_thr_kernel(
         return;
     }
     if (lane < K) {
-        ids[(size_t)t * K + lane] = sel[lane];
-        weights[(size_t)t * K + lane] =
-            dbl ? __fmul_rn((float)__ddiv_rn((double)v, den_d), routed_scale)
-                : __fmul_rn(__fdiv_rn(v, den_f), routed_scale);
+        const float w = dbl ? __fmul_rn((float)__ddiv_rn((double)v, den_d), routed_scale)
+                            : __fmul_rn(__fdiv_rn(v, den_f), routed_scale);
+        if constexpr (PUBLISH) {
+            __hip_atomic_store(ids + (size_t)t * K + lane, sel[lane], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(weights + (size_t)t * K + lane, w, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            ids[(size_t)t * K + lane] = sel[lane];
+            weights[(size_t)t * K + lane] = w;
+        }
     }
+}
+
+template <int EPT>
+__global__ __launch_bounds__(kTopkThrThreads) void topk_thr_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, uint32_t E, uint32_t K,
+    float routed_scale, uint32_t renorm, uint32_t* __restrict__ ids,
+    float* __restrict__ weights, uint32_t* status) {
+    topk_thr_body<EPT, false>(logits, bias, E, K, routed_scale, renorm, ids, weights, status,
+                              blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1333,8 +1362,9 @@ struct GemvArgs {
     uint32_t out_lo;
 };
 
-template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false>
-__global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
+// Output rows [16 rb, 16 rb + 16) by a workgroup of W waves.
+template <int S, int D, int OUT, int W, bool SPLIT>
+__device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) {
     __shared__ f32x4 part[W][S][64];
     if (*(volatile const uint32_t*)a.status) return;
     const int lane = threadIdx.x & 63;
@@ -1343,7 +1373,6 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
     const uint32_t row = min((uint32_t)n, a.tokens - 1);
     const bool live_row = (uint32_t)n < a.tokens;
     const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + 32 * g);
-    const uint32_t rb = blockIdx.x;
     const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
     f32x4 acc[S];
 #pragma unroll
@@ -1411,6 +1440,11 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
         const float combined = r16(__fadd_rn(r16(v[0]), sh));
         static_cast<uint16_t*>(a.out)[at] = f32_to_bf16(__fadd_rn(r16(a.prefix[at]), combined));
     }
+}
+
+template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false>
+__global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
+    dense_gemv_body<S, D, OUT, W, SPLIT>(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1611,8 +1645,12 @@ int launched(k3x_hip_ctx* ctx, unsigned n) {
 // the decode kernels, {expert, rows, CSR offset, tokens of the first four
 // rows (8 bits each)}, in active_asc order.
 constexpr uint32_t kGroupSmallPairs = 256;
+static_assert(kGroupSmallPairs == kTopkThrThreads, "the fused Top-K launch groups with its threads");
 
-__global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
+// ATOMIC: the ids are read at device scope (written in the same launch by
+// other workgroups).
+template <bool ATOMIC>
+__device__ __forceinline__ void group_small_body(
     const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
     const uint32_t* __restrict__ ready, uint32_t* __restrict__ counts,
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
@@ -1623,8 +1661,13 @@ __global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
     __shared__ __align__(16) uint32_t s_first[kGroupSmallPairs];  // 1: pair is its expert's first use
     __shared__ uint32_t prior;
     const uint32_t tid = threadIdx.x, P = T * K;
-    if (tid == 0) prior = *(volatile uint32_t*)status;
-    const uint32_t e = tid < P ? ids[tid] : 0xffffffffu;
+    if (tid == 0)
+        prior = ATOMIC ? __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : *(volatile uint32_t*)status;
+    uint32_t e = 0xffffffffu;
+    if (tid < P)
+        e = ATOMIC ? __hip_atomic_load(ids + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : ids[tid];
     s_id[tid] = e;
     __syncthreads();
     if (prior) return;
@@ -1691,6 +1734,126 @@ __global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
         for (uint32_t q = 0; q < P; ++q) na += s_first[q];
         *n_active = na;
     }
+}
+
+__global__ __launch_bounds__(kGroupSmallPairs) void group_small_kernel(
+    const uint32_t* __restrict__ ids, uint32_t T, uint32_t K, uint32_t E,
+    const uint32_t* __restrict__ ready, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ first_use,
+    uint32_t* __restrict__ n_active, uint32_t* __restrict__ active_asc,
+    uint32_t* __restrict__ active_fu, uint32_t* __restrict__ pair_token,
+    uint32_t* __restrict__ pair_slot, uint4* __restrict__ arec, uint32_t* status) {
+    group_small_body<false>(ids, T, K, E, ready, counts, offsets, first_use, n_active, active_asc,
+                            active_fu, pair_token, pair_slot, arec, status);
+}
+
+// The Top-K of T tokens (topk_thr_body, one workgroup a token) and the
+// small-route grouping (group_small_body) in one launch: every workgroup
+// publishes its token's ids at device scope, waits for the stores, and
+// counts itself in; the workgroup whose count completes T groups all T * K
+// pairs, reading the ids at device scope, then resets the counter to zero
+// for the next launch.  Every workgroup counts itself, whatever its Top-K
+// found (a latched error makes the grouping return at once), so the
+// counter always completes and is left at zero.  No workgroup waits for
+// another.
+struct TopkGroupArgs {
+    const float* logits;
+    const float* bias;
+    uint32_t E, K, T;
+    float routed_scale;
+    uint32_t renorm;
+    uint32_t* ids;
+    float* weights;
+    const uint32_t* ready;
+    uint32_t *counts, *offsets, *first_use, *n_active, *active_asc, *active_fu, *pair_token,
+        *pair_slot;
+    uint4* arec;
+    uint32_t* counter;
+    uint32_t* status;
+};
+
+// Token t's workgroup (t < T).
+template <int EPT>
+__device__ __forceinline__ void topk_group_body(const TopkGroupArgs& a, uint32_t t) {
+    __shared__ uint32_t last;
+    topk_thr_body<EPT, true>(a.logits, a.bias, a.E, a.K, a.routed_scale, a.renorm, a.ids,
+                             a.weights, a.status, t);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               a.T - 1;
+    __syncthreads();
+    if (!last) return;  // block-uniform
+    group_small_body<true>(a.ids, a.T, a.K, a.E, a.ready, a.counts, a.offsets, a.first_use,
+                           a.n_active, a.active_asc, a.active_fu, a.pair_token, a.pair_slot,
+                           a.arec, a.status);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int EPT>
+__global__ __launch_bounds__(kTopkThrThreads) void topk_group_kernel(TopkGroupArgs a) {
+    topk_group_body<EPT>(a, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// The official layer's few-token launches: each a set of roles by workgroup
+// index, 256 threads a workgroup, every role reading only what an earlier
+// launch wrote (so no workgroup waits for another role).
+//   front   router logits (router_reg_body, 2 experts a workgroup); the
+//           latent projection, bf16 out; the shared gate/up + GLU, split
+//           [hi | lo] activation rows (a GEMV row block of 16 outputs a
+//           workgroup, 4 waves over the K tiles);
+//   select  the Top-K and grouping of topk_group_kernel (one workgroup a
+//           token, the last to arrive groups); the shared down projection
+//           over the split rows, fp32 out.
+// The router's workgroups come first, then the Top-K's: the latency-bound
+// route starts at once and the projections' weight streams fill the rest of
+// the device meanwhile.
+// ---------------------------------------------------------------------------
+constexpr int kOfficialWaves = 4;
+#ifndef K3X_OFFICIAL_EPB
+#define K3X_OFFICIAL_EPB 1
+#endif
+constexpr int kOfficialRouterEpb = K3X_OFFICIAL_EPB;  // experts a router workgroup
+static_assert(64 * kOfficialWaves == kTopkThrThreads, "one workgroup size for every role");
+
+struct OfficialFrontArgs {
+    const float* router;  // [E][H] fp32
+    const uint16_t* hidden;
+    uint32_t E, H, T;
+    float* logits;
+    GemvArgs latent;  // 1 matrix, bf16 out
+    GemvArgs shared;  // gate + up, GLU out (tiles null: no shared FFN)
+    uint32_t n_router, n_latent;
+    const uint32_t* status;
+};
+
+template <int TPB>
+__global__ __launch_bounds__(64 * kOfficialWaves) void official_front_kernel(OfficialFrontArgs a) {
+    const uint32_t b = blockIdx.x;
+    if (b < a.n_router)
+        router_reg_body<kOfficialRouterEpb, TPB>(a.router, a.hidden, a.E, a.H, a.T, a.logits,
+                                                 a.status, b);
+    else if (b < a.n_router + a.n_latent)
+        dense_gemv_body<1, 3, 1, kOfficialWaves, false>(a.latent, b - a.n_router);
+    else
+        dense_gemv_body<2, 2, 2, kOfficialWaves, false>(a.shared, b - a.n_router - a.n_latent);
+}
+
+struct OfficialSelectArgs {
+    TopkGroupArgs route;
+    GemvArgs shared_down;  // split rows, fp32 out (tiles null: none)
+};
+
+template <int EPT>
+__global__ __launch_bounds__(64 * kOfficialWaves) void official_select_kernel(
+    OfficialSelectArgs a) {
+    if (blockIdx.x < a.route.T)
+        topk_group_body<EPT>(a.route, blockIdx.x);
+    else
+        dense_gemv_body<1, 2, 0, kOfficialWaves, true>(a.shared_down, blockIdx.x - a.route.T);
 }
 
 int launch_group(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t T, uint32_t K, uint32_t E,
@@ -2041,10 +2204,16 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     const bool few = !wide_path && !split_in && T * K <= kGroupSmallPairs &&
                      k3x_hip::few_row_experts_eligible(ctx, bank, T, split);
     const bool chunked = !few && chunked_rows;
-    int st = launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts, s.offsets,
-                          s.pair_token, s.pair_slot, s.first_use, s.n_active, s.active_asc,
-                          s.active_fu, s.gscratch, wide_path ? s.witems : nullptr,
-                          wide_path ? s.n_witems : nullptr, few || chunked ? s.arec : nullptr);
+    // A route grouped with its Top-K (topk_group_kernel) holds what the
+    // small-route grouping below would write: no wide path there.
+    if (s.grouped && (wide_path || T * K > kGroupSmallPairs)) return K3X_ERR_INVALID_EXTENT;
+    int st = s.grouped ? K3X_OK
+                       : launch_group(ctx, ids, T, K, d.experts, bank->ready_dev, s.counts,
+                                      s.offsets, s.pair_token, s.pair_slot, s.first_use,
+                                      s.n_active, s.active_asc, s.active_fu, s.gscratch,
+                                      wide_path ? s.witems : nullptr,
+                                      wide_path ? s.n_witems : nullptr,
+                                      few || chunked ? s.arec : nullptr);
     end_stage(ctx, mark);
     if (st) return st;
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
@@ -2106,6 +2275,20 @@ int run_tail(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
     dn.y = s.y;
     dn.y_stride = d.hidden;
     dn.scatter = 1;
+    // Few tokens: the combine rides in the down launch (the decode path's
+    // fused mix), after the shared expert, whose output it adds.
+    if (few && k3x_hip::few_row_mix_eligible(bank, T)) {
+        if (d.shared_inter && !side &&
+            (st = run_shared_narrow(ctx, bank, p, s, xn, glu, split_in, ctx->stream)))
+            return st;
+        if ((st = joiner.join())) return st;
+        const k3x_hip::FewRowMix mix{weights, d.shared_inter ? s.sy : nullptr, out, out_f32,
+                                     (p->flags & K3X_FLAG_ROUND_EXPERT_OUT) != 0};
+        mark = begin_stage(ctx, K3X_STAGE_DOWN);
+        st = k3x_hip::launch_few_row_down(ctx, bank, T, K, s, split, false, &mix);
+        end_stage(ctx, mark);
+        return st;
+    }
     mark = begin_stage(ctx, K3X_STAGE_DOWN);
     if (few || chunked) {
         if ((st = k3x_hip::launch_few_row_down(ctx, bank, T, K, s, split, chunked))) return st;
@@ -2241,6 +2424,26 @@ int launch_topk_any(k3x_hip_ctx* ctx, const float* logits, const float* bias, ui
     return launched(ctx, 1);
 }
 
+// The fused Top-K and grouping launch (topk_group_kernel) over the routed
+// call's grouping buffers and the context's arrival counter.
+int launch_topk_group_impl(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E,
+                           uint32_t K, uint32_t T, float routed_scale, uint32_t renorm,
+                           uint32_t* ids, float* weights, const uint32_t* ready,
+                           const Scratch& s) {
+    TopkGroupArgs a{logits,        bias,        E,         K,           T,
+                    routed_scale,  renorm,      ids,       weights,     ready,
+                    s.counts,      s.offsets,   s.first_use, s.n_active, s.active_asc,
+                    s.active_fu,   s.pair_token, s.pair_slot, s.arec,    ctx->route_counter,
+                    ctx->status};
+    if (E <= 512)
+        hipLaunchKernelGGL(topk_group_kernel<2>, dim3(T), dim3(kTopkThrThreads), 0, ctx->stream,
+                           a);
+    else
+        hipLaunchKernelGGL(topk_group_kernel<4>, dim3(T), dim3(kTopkThrThreads), 0, ctx->stream,
+                           a);
+    return launched(ctx, 1);
+}
+
 int prepare(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p, Scratch* s) {
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
     const bool split = (p->flags & K3X_FLAG_SPLIT_ACT) != 0;
@@ -2271,6 +2474,72 @@ int permute_router(k3x_hip_bank* bank) {
 }
 
 bool router_mfma_eligible(uint32_t hidden) { return hidden <= kRouterMaxHidden; }
+
+bool official_decode_eligible(uint32_t E, uint32_t H, uint32_t L, uint32_t I_s, uint32_t K,
+                              uint32_t T) {
+    return T >= 1 && T <= 4 && topk_group_eligible(E, K, T) && H <= kRouterMaxHidden &&
+           !router_uses_mfma(H, T) && H % 128 == 0 && L % 128 == 0 && I_s % 128 == 0;
+}
+
+int launch_official_front(k3x_hip_ctx* ctx, const OfficialDecode& d) {
+    if (!official_decode_eligible(d.E, d.H, d.L, d.I_s, d.K, d.T)) return K3X_ERR_INVALID_EXTENT;
+    OfficialFrontArgs a{};
+    a.router = d.router;
+    a.hidden = d.hidden;
+    a.E = d.E;
+    a.H = d.H;
+    a.T = d.T;
+    a.logits = d.logits;
+    a.latent = GemvArgs{d.latent_tiles, d.H / 128, d.hidden, d.H, d.T, d.latent, d.L, {},
+                        ctx->status};
+    a.shared = GemvArgs{d.shared_gu, d.H / 128, d.hidden, d.H, d.T, d.sact, 2 * d.I_s, d.glu,
+                        ctx->status};
+    a.shared.out_lo = d.I_s;
+    a.n_router = (d.E + kOfficialRouterEpb - 1) / kOfficialRouterEpb;
+    a.n_latent = d.L / 16;
+    a.status = ctx->status;
+    const dim3 grid(a.n_router + a.n_latent + d.I_s / 16), block(64 * kOfficialWaves);
+    if (d.T == 1)
+        hipLaunchKernelGGL(official_front_kernel<1>, grid, block, 0, ctx->stream, a);
+    else if (d.T == 2)
+        hipLaunchKernelGGL(official_front_kernel<2>, grid, block, 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(official_front_kernel<4>, grid, block, 0, ctx->stream, a);
+    return launched(ctx, 1);
+}
+
+int launch_official_select(k3x_hip_ctx* ctx, const OfficialDecode& d, const LayerBuffers& s) {
+    if (!official_decode_eligible(d.E, d.H, d.L, d.I_s, d.K, d.T) || !ctx->route_counter)
+        return K3X_ERR_INVALID_EXTENT;
+    OfficialSelectArgs a{};
+    a.route = TopkGroupArgs{d.logits,   d.correction, d.E,          d.K,          d.T,
+                            1.0f,       K3X_RENORM_DOUBLE, d.ids,   d.weights,    d.ready,
+                            s.counts,   s.offsets,    s.first_use,  s.n_active,   s.active_asc,
+                            s.active_fu, s.pair_token, s.pair_slot, s.arec,       ctx->route_counter,
+                            ctx->status};
+    a.shared_down = GemvArgs{d.shared_dn, d.I_s / 128, d.sact, 2 * d.I_s, d.T, d.shared, d.H, {},
+                             ctx->status};
+    a.shared_down.x_lo = d.I_s;
+    const dim3 grid(d.T + (d.I_s ? d.H / 16 : 0)), block(64 * kOfficialWaves);
+    if (d.E <= 512)
+        hipLaunchKernelGGL(official_select_kernel<2>, grid, block, 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(official_select_kernel<4>, grid, block, 0, ctx->stream, a);
+    return launched(ctx, 1);
+}
+
+bool topk_group_eligible(uint32_t E, uint32_t K, uint32_t T) {
+    return E > 256 && E <= 1024 && T >= 1 && T <= kTopkThrMaxTokens && K >= 1 && K <= 64 &&
+           (size_t)T * K <= kGroupSmallPairs && T < kWideMinTokens;
+}
+
+int launch_topk_group(k3x_hip_ctx* ctx, const float* logits, const float* bias, uint32_t E,
+                      uint32_t K, uint32_t T, float routed_scale, uint32_t renorm, uint32_t* ids,
+                      float* weights, const uint32_t* ready, const LayerBuffers& s) {
+    if (!topk_group_eligible(E, K, T) || !ctx->route_counter) return K3X_ERR_INVALID_EXTENT;
+    return launch_topk_group_impl(ctx, logits, bias, E, K, T, routed_scale, renorm, ids, weights,
+                                  ready, s);
+}
 
 int launch_rmsnorm(k3x_hip_ctx* ctx, const uint16_t* x, const float* gamma, uint32_t T,
                    uint32_t H, float eps, uint16_t* xn) {
@@ -2319,6 +2588,10 @@ bool dense_wide_ok(WideKind kind, uint32_t N, uint32_t K, uint32_t T) {
 bool dense_mlp_any_stream(uint32_t I, uint32_t H, uint32_t T) {
     return T <= kDenseDirectTokens ||
            (dense_wide_ok(kWideSharedGateUp, I, H, T) && dense_wide_ok(kWideSharedDown, H, I, T));
+}
+
+bool dense_down_any_stream(uint32_t N, uint32_t K, uint32_t T) {
+    return T <= kDenseDirectTokens || dense_wide_ok(kWideSharedDown, N, K, T);
 }
 
 int dense_gate_up(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t I, uint32_t H, const uint16_t* x,
@@ -2492,15 +2765,25 @@ int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_mo
     }
     st = launch_router(ctx, bank->router_w, mfma_router ? bank->router_wp : nullptr, s.xn, s.xp,
                        d.experts, d.hidden, T, s.logits);
-    st = st ? st : launch_topk_any(ctx, s.logits, bank->router_bias, d.experts, K, T,
-                                   p->routed_scale, p->renorm, s.ids, s.weights);
+    // Few pairs: the Top-K groups its own route (one launch fewer); the
+    // routed tail then skips its grouping.
+    Scratch g = s;
+    g.grouped = k3x_hip::topk_group_eligible(d.experts, K, T) && ctx->route_counter &&
+                !(p->flags & K3X_FLAG_SPLIT_INPUT);
+    if (g.grouped)
+        st = st ? st : launch_topk_group_impl(ctx, s.logits, bank->router_bias, d.experts, K, T,
+                                              p->routed_scale, p->renorm, s.ids, s.weights,
+                                              bank->ready_dev, s);
+    else
+        st = st ? st : launch_topk_any(ctx, s.logits, bank->router_bias, d.experts, K, T,
+                                       p->routed_scale, p->renorm, s.ids, s.weights);
     if (!st) k3x_hip::end_stage(ctx, mark);
     if (!st) st = launched(ctx, 1);
     if (st) {
         if (forked) (void)hipStreamWaitEvent(ctx->stream, ctx->join_ev, 0);
         return st;
     }
-    if ((st = run_tail(ctx, bank, p, s, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr,
+    if ((st = run_tail(ctx, bank, p, g, s.xn, s.ids, s.weights, out, taps ? taps->out_f32 : nullptr,
                        forked)))
         return st;
     ++ctx->forward_calls;
@@ -2519,6 +2802,23 @@ int forward_device_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_mo
 static __device__ __align__(256) uint8_t scratch[K3X_HIP_NOALLOC_SCRATCH_BYTES];
 
 namespace k3x_hip {
+
+int routed_begin(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                 LayerBuffers* s) {
+    if (!ctx || !bank || !p || !s || bank->ctx != ctx) return K3X_ERR_INVALID_EXTENT;
+    const int st = validate_params(bank, p, false);
+    return st ? st : prepare(ctx, bank, p, s);
+}
+
+int routed_finish(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
+                  const LayerBuffers& s, const uint16_t* xn, const uint32_t* ids,
+                  const float* weights, uint16_t* out, const k3x_hip_moe_taps* taps) {
+    if (!xn || !ids || !weights || !out) return K3X_ERR_INVALID_EXTENT;
+    int st = run_tail(ctx, bank, p, s, xn, ids, weights, out, taps ? taps->out_f32 : nullptr);
+    if (st) return st;
+    ++ctx->forward_calls;
+    return copy_taps(ctx, bank, p, s, xn, ids, weights, taps);
+}
 
 int noalloc_scratch(int device, void** out) {
     static std::mutex mu;
@@ -2610,10 +2910,7 @@ int k3x_hip_moe_forward_routed(k3x_hip_ctx* ctx, k3x_hip_bank* bank,
             if (!std::isfinite(host_weights[i])) return K3X_ERR_INVALID_STATE;
     Scratch s;
     if ((st = prepare(ctx, bank, p, &s))) return st;
-    if ((st = run_tail(ctx, bank, p, s, xn, ids, weights, out, taps ? taps->out_f32 : nullptr)))
-        return st;
-    ++ctx->forward_calls;
-    return copy_taps(ctx, bank, p, s, xn, ids, weights, taps);
+    return k3x_hip::routed_finish(ctx, bank, p, s, xn, ids, weights, out, taps);
 }
 
 int k3x_hip_expert_major_plan(k3x_hip_ctx* ctx, const uint32_t* ids, uint32_t tokens,
