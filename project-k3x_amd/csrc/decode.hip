@@ -520,6 +520,7 @@ struct SelectArgs {
     uint32_t* active_fu;
     uint4* arec;         // [E] per active slot: {expert, rows, offset, row tokens}
     uint32_t group_taps; // nonzero: also counts, offsets, first_use, active_asc, active_fu
+    uint32_t local_only; // nonzero: the results stay in LDS (rec, na, selw), no global store
     uint32_t* status;
 };
 
@@ -571,6 +572,8 @@ struct SelectShared {
     float selw[kSelMaxPairs];        // its contribution
     uint32_t first[kSelMaxPairs];    // 1: the pair is its expert's first use
     uint32_t rowtok[kSelMaxPairs];   // token of CSR row r
+    uint4 rec[kSelMaxPairs];         // active slot records {expert, rows, offset, row tokens}
+    uint32_t na;                     // active slots
     uint32_t bad;
 };
 
@@ -759,7 +762,7 @@ __device__ void select_group(const SelectArgs& a, SelectShared& sh) {
     // no barrier waits for stores to drain.
     __syncthreads();
     if (sh.bad) return;
-    if (tid < P) {
+    if (tid < P && !a.local_only) {
         const uint32_t r = below + rin;  // CSR row
         a.pair_token[r] = tid / K;
         a.pair_slot[r] = tid % K;
@@ -778,6 +781,9 @@ __device__ void select_group(const SelectArgs& a, SelectShared& sh) {
         }
         uint32_t toks = 0;  // tokens of e's first four rows, 8 bits each
         for (uint32_t j = 0; j < min(cnt, 4u); ++j) toks |= sh.rowtok[below + j] << (8 * j);
+        sh.rec[ai] = make_uint4(e, cnt, below, toks);
+        if (ai == 0) sh.na = na;
+        if (a.local_only) return;
         a.arec[ai] = make_uint4(e, cnt, below, toks);
         if (ai == 0) *a.n_active = na;
         if (a.group_taps) {
@@ -785,7 +791,7 @@ __device__ void select_group(const SelectArgs& a, SelectShared& sh) {
             a.active_fu[fr] = e;
         }
     }
-    if (!a.group_taps) return;
+    if (!a.group_taps || a.local_only) return;
     // Per expert: count, CSR offset, first use (0xffffffff when unused).
     for (uint32_t x = tid; x < E; x += kFrontThreads) {
         uint32_t c = 0, o = 0, fu = 0xffffffffu;
@@ -1086,6 +1092,192 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
     }
 }
 
+// One gate/up unit of the two-launch decode form (RB = 1): the whole block
+// on 16-row block rb of active slot ai = blk / (I / 16), its K range split
+// over the waves, every token's xn row already in LDS (s_x as [T][H]; row
+// n of the slot is token (rec.w >> 8 n) & 0xff), the slot records in LDS.
+// The loads, the MFMA steps, the wave tree and the GLU are those of
+// decode_gateup_kernel<1>.
+__device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t blk,
+                                                const uint16_t* s_x, const uint4* lrec,
+                                                uint32_t lna, f32x4 (&red)[kGuWaves][2][64]) {
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t per_expert = a.I / 16;
+    const uint32_t ai = blk / per_expert, rb = blk % per_expert, wv = wave;
+    if (ai >= lna) return;  // block-uniform
+    const uint4 rec = lrec[ai];
+    const uint32_t e = rec.x, rows = rec.y, toks = rec.w;
+    const uint32_t H = a.H, kt = a.kt;
+    const uint32_t k0 = wv * kt / kGuWaves, k1 = (wv + 1) * kt / kGuWaves;
+    const uint32_t N = k1 - k0;
+    const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
+    const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
+    uint4 c0[kGuTiles], c1[kGuTiles];
+    uint32_t s0[3], s1[3];
+#pragma unroll
+    for (int i = 0; i < kGuTiles; ++i) {
+        const size_t k = min(k0 + i, kt - 1);  // tiles past k1 are loaded, not used
+        c0[i] = ntl(codes + k * 128);
+        c1[i] = ntl(codes + k * 128 + 64);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const size_t grp = min(k0 / 4 + i, a.ks - 1);
+        s0[i] = ntl(scales + grp * 128);
+        s1[i] = ntl(scales + grp * 128 + 64);
+    }
+    const uint32_t tok = (toks >> (8 * (n < rows ? n : 0))) & 0xffu;  // unused rows: row 0's
+    const uint16_t* xrow = s_x + (size_t)tok * H + 32 * g;
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < kGuTiles; ++i) {
+        if ((uint32_t)i < N) {
+            const uint32_t k = k0 + i, gi = (k >> 2) - (k0 >> 2), sh = 8 * (k & 3);
+            const uint32_t w0 = gi == 0 ? s0[0] : gi == 1 ? s0[1] : s0[2];
+            const uint32_t w1 = gi == 0 ? s1[0] : gi == 1 ? s1[1] : s1[2];
+            uint4 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[j] = *reinterpret_cast<const uint4*>(xrow + (size_t)k * 128 + 8 * j);
+            acc[0] = mxfp4_tile(c0[i], e8m0_to_f32((w0 >> sh) & 0xffu), av, acc[0]);
+            acc[1] = mxfp4_tile(c1[i], e8m0_to_f32((w1 >> sh) & 0xffu), av, acc[1]);
+        }
+    }
+    red[wave][0][lane] = acc[0];
+    red[wave][1][lane] = acc[1];
+#pragma unroll
+    for (uint32_t h = kGuWaves / 2; h >= 1; h /= 2) {
+        __syncthreads();
+        if (wv < h) {
+            red[wave][0][lane] = red[wave][0][lane] + red[wave + h][0][lane];
+            red[wave][1][lane] = red[wave][1][lane] + red[wave + h][1][lane];
+        }
+    }
+    if (wv != 0) return;
+    const f32x4 gs = red[0][0][lane], us = red[0][1][lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 4 * g + i;
+        if (row < rows) {
+            const float v = glu(gs[i], us[i], a.glu);
+            uint16_t* dst = a.act + (size_t)(rec.z + row) * a.act_stride + rb * 16 + n;
+            const uint16_t hi = f32_to_bf16(v);
+            *dst = hi;
+            if (a.act_lo) dst[a.act_lo] = act_lo_bf16(v, hi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Few experts (E <= kSmallMaxExperts, no shared expert): every workgroup of
+// the routed gate/up launch finds the route itself -- xn, the E router rows
+// (fp64, canonical order), Top-K and grouping, all in LDS, the same
+// functions as the front and select kernels -- so that the route costs no
+// launch of its own; block 0 also stores the route (ids, weights, CSR rows,
+// active-slot records) for the down launch and xn and the logits for the
+// taps.  A few router rows per wave are requested with the xn prologue's
+// loads.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kSmallMaxExperts = 2 * kFrontWaves;  // two router rows a wave at most
+constexpr int kSmallRowLoads = 32;  // float4 router loads per lane, its rows together
+
+struct SmallArgs {
+    const uint16_t* x;
+    const float* gamma;
+    const float* router_w;  // [E][H] fp32
+    float eps;
+    SelectArgs sel;         // shapes, bias, scale, renorm; block 0's route outputs
+    GateUpArgs gu;
+    uint16_t* xn;           // block 0: the xn copy
+    float* logits;          // block 0: [T][E]
+};
+
+struct SmallLds {
+    NormShared ns;
+    SelectShared sel;
+    float lg[kMaxDecodeTokens][kSmallMaxExperts];
+    f32x4 red[kGuWaves][2][64];
+};
+
+// NE router rows per wave (experts wave + kFrontWaves i); TT bounds T.
+template <int TT, int NE>
+__global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(SmallArgs a) {
+    static_assert(kFrontThreads == 64 * kGuWaves, "one workgroup shape for route and gate/up");
+    extern __shared__ uint4 dyn_lds[];  // xn [T][H] bf16, then gamma
+    __shared__ SmallLds sh;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t T = a.sel.T, H = a.gu.H, E = a.sel.E, J = H / 256;
+    constexpr int kPer = kSmallRowLoads / NE;  // J <= kPer (checked on the host)
+    float4 wb[NE][kPer];
+    auto prefetch = [&]() {
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const uint32_t e = wave + kFrontWaves * i;
+            const float* wr = a.router_w + (size_t)(e < E ? e : 0) * H + 4 * lane;
+#pragma unroll
+            for (int q = 0; q < kPer; ++q)
+                wb[i][q] = *reinterpret_cast<const float4*>(wr + 256 * min((uint32_t)q, J - 1));
+        }
+    };
+    if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns,
+                                 blockIdx.x == 0 ? a.xn : nullptr, a.sel.status, a.sel.status,
+                                 prefetch, [] {}))
+        return;
+    // Logits of this wave's experts: partial 4 l + c sums j = 0, 1, ... in
+    // sequence, then the canonical tree (router_block's order).
+    const uint16_t* s_x = reinterpret_cast<const uint16_t*>(dyn_lds);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const uint32_t e = wave + kFrontWaves * i;
+        if (e >= E) continue;  // wave-uniform
+        double p[TT][4];
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) p[t][c] = 0.0;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            if ((uint32_t)q >= J) continue;
+            const double wv[4] = {(double)wb[i][q].x, (double)wb[i][q].y, (double)wb[i][q].z,
+                                  (double)wb[i][q].w};
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                if ((uint32_t)t >= T) continue;
+                const uint2 xv =
+                    *reinterpret_cast<const uint2*>(s_x + (size_t)t * H + 256 * q + 4 * lane);
+                const float f[4] = {lo_bf16(xv.x), hi_bf16(xv.x), lo_bf16(xv.y), hi_bf16(xv.y)};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) p[t][c] = __builtin_fma(wv[c], (double)f[c], p[t][c]);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            if ((uint32_t)t >= T) continue;
+            const float v = (float)canon_reduce(p[t]);
+            if (lane == 0) {
+                sh.lg[t][e] = v;
+                if (blockIdx.x == 0) a.logits[(size_t)t * E + e] = v;
+            }
+        }
+    }
+    __syncthreads();
+    // Top-K and grouping, as decode_select_kernel's block 0 (this block's
+    // copy in LDS; block 0 stores it).
+    const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
+    float lg[kMaxDecodeTokens];
+#pragma unroll
+    for (int t = 0; t < kMaxDecodeTokens; ++t) lg[t] = sh.lg[min((uint32_t)t, T - 1)][ee];
+    SelectArgs sa = a.sel;
+    sa.local_only = blockIdx.x != 0;
+    if (!select_topk(sa, sh.sel, lg, a.sel.bias[ee])) return;
+    select_group(sa, sh.sel);
+    __syncthreads();
+    if (sh.sel.bad) return;
+    gateup_unit_lds(a.gu, blockIdx.x, reinterpret_cast<const uint16_t*>(dyn_lds), sh.sel.rec,
+                    sh.sel.na, sh.red);
+}
+
 // ---------------------------------------------------------------------------
 // Routed down projection -> per-pair rows; slot-ordered combine
 // ---------------------------------------------------------------------------
@@ -1305,6 +1497,18 @@ constexpr uint32_t kMaxDecodePairs = 256;
 
 }  // namespace
 
+// The two-launch form of the decode path (small_route_gateup_kernel): few
+// experts whose router rows fit a wave's registers, no shared expert, no
+// per-expert grouping taps; within decode_eligible's shapes.
+bool small_route_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
+                          const k3x_hip_moe_params* p, bool group_taps) {
+    const auto& d = bank->desc;
+    const uint32_t ne = d.experts > (uint32_t)kFrontWaves ? 2 : 1;
+    return !group_taps && d.shared_inter == 0 && d.experts <= kSmallMaxExperts &&
+           d.hidden / 256 <= (uint32_t)kSmallRowLoads / ne &&
+           xn_lds_bytes(p->tokens, d.hidden) + sizeof(SmallLds) <= ctx->max_lds_per_block;
+}
+
 bool decode_eligible(const k3x_hip_ctx* ctx, const k3x_hip_bank* bank,
                      const k3x_hip_moe_params* p, const void* x) {
     const auto& d = bank->desc;
@@ -1352,14 +1556,6 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     f.status = ctx->status;
     const dim3 front_grid(f.router_blocks + S / 16);
     const size_t xn_lds = xn_lds_bytes(T, d.hidden);
-    int mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT);
-    if (T <= 2)
-        hipLaunchKernelGGL((decode_front_kernel<2>), front_grid, dim3(kFrontThreads), xn_lds,
-                           main, f);
-    else
-        hipLaunchKernelGGL((decode_front_kernel<kMaxDecodeTokens>), front_grid,
-                           dim3(kFrontThreads), xn_lds, main, f);
-    end_stage(ctx, mark);
 
     SelectArgs sa{};
     sa.logits = b.logits;
@@ -1390,10 +1586,6 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     sd.S = S;
     sd.sy = b.sy;
     sd.status = ctx->status;
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT);
-    hipLaunchKernelGGL(decode_select_kernel, dim3(1 + (S ? d.hidden / 16 : 0)),
-                       dim3(kFrontThreads), 0, main, sa, sd);
-    end_stage(ctx, mark);
 
     const uint32_t max_active = std::min<uint32_t>(d.experts, T * K);
     GateUpArgs gu{};
@@ -1414,10 +1606,6 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     gu.glu = glu;
     gu.status = ctx->status;
     const uint32_t gu_blocks = max_active * (d.inter / 16);
-    mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
-    hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(gu_blocks), dim3(64 * kGuWaves),
-                       (size_t)T * d.hidden * 2, main, gu);
-    end_stage(ctx, mark);
 
     DownArgs dn{};
     dn.dn_codes = reinterpret_cast<const uint4*>(bank->dn_codes);
@@ -1442,12 +1630,59 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
     dn.out_f32 = out_f32;
     dn.mix = b.mix;
     dn.status = ctx->status;
+
+    int mark = 0;
+    const bool small = small_route_eligible(ctx, bank, p, group_taps);
+    if (small) {
+        // Route + routed gate/up in one launch (every workgroup routes).
+        SmallArgs sm{};
+        sm.x = x;
+        sm.gamma = bank->gamma;
+        sm.router_w = bank->router_w;
+        sm.eps = p->rms_epsilon;
+        sm.sel = sa;
+        sm.gu = gu;
+        sm.xn = b.xn;
+        sm.logits = b.logits;
+        mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
+        const bool two = d.experts > (uint32_t)kFrontWaves;
+        if (T <= 2 && !two)
+            hipLaunchKernelGGL((small_route_gateup_kernel<2, 1>), dim3(gu_blocks),
+                               dim3(kFrontThreads), xn_lds, main, sm);
+        else if (T <= 2)
+            hipLaunchKernelGGL((small_route_gateup_kernel<2, 2>), dim3(gu_blocks),
+                               dim3(kFrontThreads), xn_lds, main, sm);
+        else if (!two)
+            hipLaunchKernelGGL((small_route_gateup_kernel<kMaxDecodeTokens, 1>), dim3(gu_blocks),
+                               dim3(kFrontThreads), xn_lds, main, sm);
+        else
+            hipLaunchKernelGGL((small_route_gateup_kernel<kMaxDecodeTokens, 2>), dim3(gu_blocks),
+                               dim3(kFrontThreads), xn_lds, main, sm);
+        end_stage(ctx, mark);
+    } else {
+        mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT);
+        if (T <= 2)
+            hipLaunchKernelGGL((decode_front_kernel<2>), front_grid, dim3(kFrontThreads), xn_lds,
+                               main, f);
+        else
+            hipLaunchKernelGGL((decode_front_kernel<kMaxDecodeTokens>), front_grid,
+                               dim3(kFrontThreads), xn_lds, main, f);
+        end_stage(ctx, mark);
+        mark = begin_stage(ctx, K3X_STAGE_DECODE_SELECT);
+        hipLaunchKernelGGL(decode_select_kernel, dim3(1 + (S ? d.hidden / 16 : 0)),
+                           dim3(kFrontThreads), 0, main, sa, sd);
+        end_stage(ctx, mark);
+        mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
+        hipLaunchKernelGGL(decode_gateup_kernel<1>, dim3(gu_blocks), dim3(64 * kGuWaves),
+                           (size_t)T * d.hidden * 2, main, gu);
+        end_stage(ctx, mark);
+    }
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
     hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false>),
                        dim3(max_active * (d.hidden / (16 * kDownWaves))), dim3(64 * kDownWaves),
                        (size_t)T * d.inter * 2, main, dn);
     end_stage(ctx, mark);
-    ctx->kernel_launches += 4;
+    ctx->kernel_launches += small ? 2 : 4;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;
 }
 

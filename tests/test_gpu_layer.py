@@ -139,9 +139,11 @@ def test_upload_replaces_slot_identity(hip):
 # ---------------------------------------------------------------------------
 # Full layer on the seeded benchmark configurations.
 # ---------------------------------------------------------------------------
-def run_layer(k3x_amd, ctx, cfg, bank, x_bits, flags=0, per_pair=True, glu=None, linear=None):
+def run_layer(k3x_amd, ctx, cfg, bank, x_bits, flags=0, per_pair=True, glu=None, linear=None,
+              group=True):
     """One forward call with taps.  per_pair=False skips the [T][K][H] expert
-    output tap (939 MB at T=2048)."""
+    output tap (939 MB at T=2048); group=False the per-expert grouping taps
+    (counts, offsets, first uses, active first uses)."""
     dev = "cuda:0"
     T, H, I, E, K = cfg.tokens, cfg.hidden, cfg.inter, cfg.experts, cfg.top_k
     x = torch.from_numpy(np.ascontiguousarray(x_bits).view(np.int16)).to(dev)
@@ -156,6 +158,9 @@ def run_layer(k3x_amd, ctx, cfg, bank, x_bits, flags=0, per_pair=True, glu=None,
                 out_f32=z((T, H), torch.float32))
     if per_pair:
         taps["expert_out"] = z((T, K, H), torch.float32)
+    if not group:
+        for k in ("counts", "offsets", "first_use", "active_first_use"):
+            del taps[k]
     if cfg.shared_inter:
         taps["shared_out"] = z((T, H), torch.float32)
         taps["shared_act"] = z((T, cfg.shared_inter), torch.int16)
@@ -169,7 +174,8 @@ def run_layer(k3x_amd, ctx, cfg, bank, x_bits, flags=0, per_pair=True, glu=None,
     got["out"] = to_np(out)
     for k in ("ids", "counts", "offsets", "pair_token", "pair_slot", "first_use", "n_active",
               "active_first_use"):
-        got[k] = got[k].view(np.uint32)
+        if k in got:
+            got[k] = got[k].view(np.uint32)
     for k in ("normed_x", "act", "out", "shared_act"):
         if k in got:
             got[k] = got[k].view(np.uint16)
@@ -545,6 +551,39 @@ def test_decode_deterministic(hip, c3):
     b = run_layer(k3x_amd, ctx, cfg, bank, x, 0, per_pair=False)
     for k in a:
         assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
+
+
+@pytest.mark.parametrize("cid,T", [(1, 1), (1, 2), (1, 4), (2, 1), (2, 3)])
+def test_small_route_two_launches(hip, oracle, cid, T):
+    """Few experts, no shared expert (configs 1 and 2): without the
+    per-expert grouping taps the decode path runs in two launches, every
+    gate/up workgroup finding the route itself.  Everything it writes equals
+    the four-launch form's (taken with those taps, whose routing is checked
+    against the oracle here) bit for bit: the same xn, logits, Top-K,
+    grouping, activations, per-pair rows and output."""
+    import dataclasses
+    from synth import CONFIGS, SynthLayer
+    k3x_amd, ctx = hip
+    cfg = dataclasses.replace(CONFIGS[cid], tokens=T)
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    x = layer.x_bits()
+    say(f"two-launch decode config {cid} T={T}")
+    launches = lambda: ctx.stats().kernel_launches
+    n0 = launches()
+    a = run_layer(k3x_amd, ctx, cfg, bank, x, 0, group=False)
+    n1 = launches()
+    b = run_layer(k3x_amd, ctx, cfg, bank, x, 0, group=True)
+    n2 = launches()
+    assert (n1 - n0, n2 - n1) == (2, 4), (n1 - n0, n2 - n1)
+    check_routing(oracle, layer, b, x)
+    for k in ("normed_x", "logits", "ids", "weights", "pair_token", "pair_slot", "n_active",
+              "act", "expert_out", "out_f32", "out"):
+        assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
+    # Back-to-back calls leave nothing behind: the same call again.
+    c = run_layer(k3x_amd, ctx, cfg, bank, x, 0, group=False)
+    assert np.array_equal(c["out"], a["out"])
+    bank.close()
 
 
 def test_c1_situ_against_reference_golden(hip, oracle):
