@@ -2,6 +2,10 @@
 //   sanitize_driver reader FILE...   the K3X reader's open-time checks
 //                                    (k3x_reader.cpp) on each file; prints one
 //                                    status code per line
+//   sanitize_driver sha256 FILE...   the reader's SHA-256 of each file, fed in
+//                                    pieces of 1, 63, 64, 65 and 1000 bytes
+//                                    in turn (every buffering path); prints
+//                                    one hex digest per line
 //   sanitize_driver checks SEED N    HipMoeBackend's argument checks
 //                                    (k3x_hip_checks.hpp) over N randomised
 //                                    views: extents that disagree with their
@@ -9,6 +13,7 @@
 //                                    odd sizes, 0xFF scales, non-finite values
 // tests/test_sanitizers.py builds it with -fsanitize=address,undefined and
 // fails on any sanitizer report.  Exit status 0 when every step ran.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -101,7 +106,33 @@ int run_checks(std::uint64_t seed, long n) {
 
 }  // namespace
 
+int sha256_files(int argc, char** argv) {
+    static const size_t pieces[] = {1, 63, 64, 65, 1000};
+    for (int i = 2; i < argc; ++i) {
+        FILE* f = std::fopen(argv[i], "rb");
+        if (!f) return 1;
+        std::vector<uint8_t> data;
+        uint8_t chunk[4096];
+        size_t n;
+        while ((n = std::fread(chunk, 1, sizeof(chunk), f)) > 0) data.insert(data.end(), chunk, chunk + n);
+        std::fclose(f);
+        k3x_reader::Sha256 h;
+        size_t at = 0, k = 0;
+        while (at < data.size()) {
+            const size_t take = std::min(pieces[k++ % 5], data.size() - at);
+            h.update(data.data() + at, take);
+            at += take;
+        }
+        uint8_t out[32];
+        h.finish(out);
+        for (uint8_t b : out) std::printf("%02x", b);
+        std::printf("\n");
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
+    if (argc >= 2 && !std::strcmp(argv[1], "sha256")) return sha256_files(argc, argv);
     if (argc >= 2 && (!std::strcmp(argv[1], "reader") || !std::strcmp(argv[1], "verify"))) {
         // reader: the open status of each file; verify: also the checksum
         // verification of each file that opens (-1 when it does not).

@@ -109,3 +109,29 @@ def test_reader_verification_under_sanitizers(driver, oracle, tmp_path):
         s.close()
     # Payload mutants open and then fail their CRC: the verification runs.
     assert opened > 10 and any(v in (10, 11, 12, 13) for _, v in got)
+
+
+def test_sha256_under_sanitizers(driver, tmp_path):
+    """The reader's SHA-256 (FIPS 180-4, round constants derived at first
+    use) against Python's hashlib: the FIPS 180-4 example messages ("abc", the
+    448-bit two-block message, one million "a"), the empty message, every
+    length around the 55/56/64-byte padding boundaries, and random lengths, each
+    fed to the hash in pieces of several sizes."""
+    import hashlib
+    rng = np.random.default_rng(7)
+    msgs = [b"abc", b"abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq",
+            b"a" * 1_000_000, b""]
+    msgs += [bytes(rng.integers(0, 256, n, dtype=np.uint8)) for n in
+             list(range(50, 75)) + list(range(115, 135)) + [1000, 4095, 4096, 4097, 65537]]
+    paths = []
+    for i, m in enumerate(msgs):
+        p = tmp_path / f"m{i}.bin"
+        p.write_bytes(m)
+        paths.append(str(p))
+    got = run(driver, "sha256", *paths).split()
+    want = [hashlib.sha256(m).hexdigest() for m in msgs]
+    assert got == want
+    # The FIPS 180-4 published digests themselves.
+    assert got[0] == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+    assert got[1] == "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1"
+    assert got[2] == "cdc76e5c9914fb9281a1c7e284d73e67f1809a48a497200e046d39ccc7112cd0"
