@@ -241,6 +241,21 @@ def main() -> int:
     k3x_amd.check(ctx.synchronize(), "timed steps")
     us = elapsed / args.steps * 1e6
 
+    # The same number of steps on the device's own clock: hipEvents on the
+    # layer's stream around steps 2 .. K + 1 of a run of K + 1, so that the
+    # host's start-up (the first call's submission after the synchronisation,
+    # which the wall clock above includes) is not in the interval.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    step(0)
+    ev0.record()
+    for i in range(1, args.steps + 1):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    event_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
+    k3x_amd.check(ctx.synchronize(), "event-timed steps")
+
     # Same steps again with per-stage hipEvent pairs on the layer's stream.
     ctx.set_profiling(True)
     ctx.stage_times(reset=True)
@@ -310,6 +325,7 @@ def main() -> int:
         "hbm_gbps_all": round(all_bytes / (us * 1e-6) / 1e9, 1),
         "hbm_frac_all": round(all_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "profiled_us_per_layer": round(prof_elapsed / args.steps * 1e6, 3),
+        "event_us_per_layer": round(event_us, 3),
         "stages": stage_report,
         "roofline": {"bound": "hbm", "kernel": dom,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
