@@ -80,11 +80,13 @@ def build(k3x_amd, ctx, oracle, shape, seed):
 
 # (H, L, I, Is, E): the second shape puts routed_down and the shared FFN on
 # the wide grouped GEMM from 128 tokens; the third has no shared FFN.
-# The fourth has enough experts for the 16-keys-per-lane Top-K.  Few rows
-# run the projections as split-K GEMVs with the shared FFN on the side
-# stream, 300 rows the router on the matrix cores.
+# The fourth has enough experts for the 16-keys-per-lane Top-K, and for the
+# few-token path (T <= 4: route, latent projection and shared FFN in two
+# launches); the fifth is that path without a shared FFN.  Few rows run the
+# projections as split-K GEMVs, 300 rows the router on the matrix cores.
 SHAPES = {"small": (256, 128, 128, 128, 8), "wide": (1024, 512, 512, 512, 16),
-          "no_shared": (512, 256, 256, 0, 12), "many": (256, 128, 128, 128, 600)}
+          "no_shared": (512, 256, 256, 0, 12), "many": (256, 128, 128, 128, 600),
+          "many_no_shared": (256, 128, 128, 0, 600)}
 
 
 # Cases: (shape, T, K, prefix offset in floats).  A prefix view 4 bytes off
@@ -93,10 +95,14 @@ SHAPES = {"small": (256, 128, 128, 128, 8), "wide": (1024, 512, 512, 512, 16),
 @pytest.mark.parametrize("name,T,K,poff", [("small", 1, 4, 0), ("small", 5, 3, 0),
                                            ("wide", 2, 8, 0), ("wide", 160, 8, 0),
                                            ("no_shared", 33, 4, 0), ("no_shared", 2, 4, 0),
-                                           ("many", 2, 8, 0), ("small", 300, 4, 0),
+                                           ("many", 2, 8, 0), ("many", 1, 8, 0), ("many", 3, 8, 0),
+                                           ("many", 4, 16, 0), ("many_no_shared", 3, 8, 0),
+                                           ("many", 6, 8, 0), ("small", 300, 4, 0),
                                            ("wide", 40, 4, 1)],
                          ids=["small_t1", "small_t5", "wide_t2", "wide_t160", "no_shared_t33",
-                              "no_shared_t2", "many_t2", "small_t300", "wide_t40_offset_prefix"])
+                              "no_shared_t2", "many_t2", "many_t1", "many_t3", "many_t4_k16",
+                              "many_no_shared_t3", "many_t6", "small_t300",
+                              "wide_t40_offset_prefix"])
 def test_official_layer(hip, oracle, name, T, K, poff, parity_report):
     k3x_amd, ctx = hip
     H, L, I, Is, E = SHAPES[name]
