@@ -1813,10 +1813,10 @@ __global__ __launch_bounds__(kTopkThrThreads) void topk_group_kernel(TopkGroupAr
 // the device meanwhile.
 // ---------------------------------------------------------------------------
 constexpr int kOfficialWaves = 4;
-#ifndef K3X_OFFICIAL_EPB
-#define K3X_OFFICIAL_EPB 1
-#endif
-constexpr int kOfficialRouterEpb = K3X_OFFICIAL_EPB;  // experts a router workgroup
+// One expert a router workgroup: router_reg_body<2, 2> alone takes 205
+// VGPRs (two waves a SIMD), <1, 2> 110 (four), which the GEMV roles beside
+// it need.
+constexpr int kOfficialRouterEpb = 1;
 static_assert(64 * kOfficialWaves == kTopkThrThreads, "one workgroup size for every role");
 
 struct OfficialFrontArgs {
