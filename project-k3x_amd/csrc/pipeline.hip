@@ -1363,7 +1363,12 @@ struct GemvArgs {
 };
 
 // Output rows [16 rb, 16 rb + 16) by a workgroup of W waves.
-template <int S, int D, int OUT, int W, bool SPLIT>
+// LDSX: the T activation rows (x 16-byte aligned, x_stride == K, at most
+// 64 W 16-byte chunks, K tiles <= W D: one step) are copied into LDS once by
+// the workgroup, their loads issued before the weights', so a wave holds only
+// its weight tiles in registers (the kernel then fits two workgroups a
+// compute unit).  The products and sums are those of the register path.
+template <int S, int D, int OUT, int W, bool SPLIT, bool LDSX = false>
 __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) {
     __shared__ f32x4 part[W][S][64];
     if (*(volatile const uint32_t*)a.status) return;
@@ -1372,45 +1377,86 @@ __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) 
     const int g = lane >> 4, n = lane & 15;
     const uint32_t row = min((uint32_t)n, a.tokens - 1);
     const bool live_row = (uint32_t)n < a.tokens;
-    const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + 32 * g);
-    const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
-    f32x4 acc[S];
-#pragma unroll
-    for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int H2 = SPLIT ? 2 : 1;  // activation halves
-    const uint4* xl = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + a.x_lo +
-                                                     32 * g);
-    for (uint32_t k0 = wave; k0 < a.kt; k0 += W * D) {
-        uint4 b[D][S][4], xa[D][H2][4];
+    if constexpr (LDSX) {
+        static_assert(!SPLIT, "one activation half");
+        extern __shared__ uint4 s_gx[];                // [T][K] bf16
+        const uint32_t chunks = a.tokens * a.kt * 16;  // 16-byte chunks of the T rows
+        const uint4 xv =
+            reinterpret_cast<const uint4*>(a.x)[min((uint32_t)threadIdx.x, chunks - 1)];
+        const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
+        uint4 b[D][S][4];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const uint32_t k = min(k0 + d * W, a.kt - 1);
+            const uint32_t k = min(wave + d * W, a.kt - 1);
 #pragma unroll
             for (int w = 0; w < S; ++w)
 #pragma unroll
                 for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
+        }
+        if (threadIdx.x < chunks) s_gx[threadIdx.x] = xv;
+        __syncthreads();
+        const uint16_t* xrow =
+            reinterpret_cast<const uint16_t*>(s_gx) + (size_t)row * a.kt * 128 + 32 * g;
+        f32x4 acc[S];
+#pragma unroll
+        for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const uint32_t k = wave + d * W;
+            const bool live = live_row && k < a.kt;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                xa[d][0][j] = xr[(size_t)k * 16 + j];
-                if constexpr (SPLIT) xa[d][H2 - 1][j] = xl[(size_t)k * 16 + j];
+                const uint4 xv4 =
+                    live ? *reinterpret_cast<const uint4*>(xrow + (size_t)k * 128 + 8 * j)
+                         : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int w = 0; w < S; ++w)
+                    acc[w] = mfma16x16x32(as_bf16x8(xv4), as_bf16x8(b[d][w][j]), acc[w]);
             }
         }
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const bool live = live_row && k0 + d * W < a.kt;
+        for (int w = 0; w < S; ++w) part[wave][w][lane] = acc[w];
+    } else {
+        const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + 32 * g);
+        const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
+        f32x4 acc[S];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+        for (int w = 0; w < S; ++w) acc[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+        constexpr int H2 = SPLIT ? 2 : 1;  // activation halves
+        const uint4* xl = reinterpret_cast<const uint4*>(a.x + (size_t)row * a.x_stride + a.x_lo +
+                                                         32 * g);
+        for (uint32_t k0 = wave; k0 < a.kt; k0 += W * D) {
+            uint4 b[D][S][4], xa[D][H2][4];
 #pragma unroll
-                for (int h = 0; h < H2; ++h) {
-                    const uint4 xv = live ? xa[d][h][j] : make_uint4(0, 0, 0, 0);
+            for (int d = 0; d < D; ++d) {
+                const uint32_t k = min(k0 + d * W, a.kt - 1);
 #pragma unroll
-                    for (int w = 0; w < S; ++w)
-                        acc[w] = mfma16x16x32(as_bf16x8(xv), as_bf16x8(b[d][w][j]), acc[w]);
+                for (int w = 0; w < S; ++w)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    xa[d][0][j] = xr[(size_t)k * 16 + j];
+                    if constexpr (SPLIT) xa[d][H2 - 1][j] = xl[(size_t)k * 16 + j];
                 }
-        }
-    }
+            }
 #pragma unroll
-    for (int w = 0; w < S; ++w) part[wave][w][lane] = acc[w];
+            for (int d = 0; d < D; ++d) {
+                const bool live = live_row && k0 + d * W < a.kt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int h = 0; h < H2; ++h) {
+                        const uint4 xv = live ? xa[d][h][j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                        for (int w = 0; w < S; ++w)
+                            acc[w] = mfma16x16x32(as_bf16x8(xv), as_bf16x8(b[d][w][j]), acc[w]);
+                    }
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < S; ++w) part[wave][w][lane] = acc[w];
+    }
     __syncthreads();
     // Thread 16 t + c finishes output (t, c): lane 16 (t / 4) + c, element
     // t % 4 of every wave's accumulator, summed in wave order.
@@ -1442,9 +1488,9 @@ __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) 
     }
 }
 
-template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false>
+template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false, bool LDSX = false>
 __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
-    dense_gemv_body<S, D, OUT, W, SPLIT>(a, blockIdx.x);
+    dense_gemv_body<S, D, OUT, W, SPLIT, LDSX>(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2574,8 +2620,13 @@ int dense_down_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t
                       float* routed, uint16_t* out) {
     if (!T || T > kGemvMaxTokens || N % 128 || K % 128) return K3X_ERR_INVALID_EXTENT;
     GemvArgs g{tiles, K / 128, a, K, T, out, N, {}, ctx->status, prefix, shared, routed};
-    hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 3>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
-                       ctx->stream, g);
+    if (K / 128 <= 2 * kGemvWaves && (size_t)T * K / 8 <= 64 * kGemvWaves &&
+        (uintptr_t)a % 16 == 0)
+        hipLaunchKernelGGL((dense_gemv_kernel<1, 2, 3, kGemvWaves, false, true>), dim3(N / 16),
+                           dim3(64 * kGemvWaves), (size_t)T * K * 2, ctx->stream, g);
+    else
+        hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 3>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
+                           ctx->stream, g);
     return launched(ctx, 1);
 }
 
