@@ -269,6 +269,14 @@ int dense_down(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K, con
 int dense_down_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K,
                       const uint16_t* a, uint32_t T, const float* prefix, const float* shared,
                       float* routed, uint16_t* out);
+// The same output from the raw rows x: RMSNorm(x, gamma, eps) (bit for bit
+// as launch_rmsnorm) formed by every workgroup in LDS, then the projection,
+// in one launch.  x and gamma 16-byte aligned; shapes per
+// dense_norm_output_ok.
+bool dense_norm_output_ok(uint32_t N, uint32_t K, uint32_t T);
+int dense_norm_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K,
+                      const uint16_t* x, const float* gamma, float eps, uint32_t T,
+                      const float* prefix, const float* shared, float* routed, uint16_t* out);
 
 // CRC32C of device bytes (storage.hip); *crc the standard value.
 int crc32c_device(k3x_hip_ctx* ctx, const void* data, size_t bytes, uint32_t* crc);

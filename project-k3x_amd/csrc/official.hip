@@ -754,9 +754,21 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
                                 taps ? &et : nullptr);
     if (st) return st;
     // routed = routed_up . RMSNorm(mixed, routed_norm) (official_moe.cpp:327-333).
-    st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon, b.normed);
+    // Up to four tokens, one launch: every routed_up workgroup normalises the
+    // mixed rows itself.
+    const bool norm_out = k3x_hip::dense_norm_output_ok(o->H, o->L, T);
+    if (!norm_out)
+        st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon,
+                                     b.normed);
     const size_t n = (size_t)T * o->H;
-    if (T <= k3x_hip::kDenseDirectTokens) {
+    if (norm_out) {
+        if (!st && o->I_s && !side && !fused) st = shared_ffn(ctx->stream);
+        st = st ? st : joiner.join();
+        st = st ? st : k3x_hip::dense_norm_output(ctx, o->routed_up, o->H, o->L, b.mixed,
+                                                  o->routed_norm, p->rms_epsilon, T, prefix,
+                                                  o->I_s ? b.shared : nullptr, b.routed, out);
+        if (st) return st;
+    } else if (T <= k3x_hip::kDenseDirectTokens) {
         // Few rows: the output formula in the routed_up GEMV's epilogue, after
         // the shared FFN (long finished on the side stream by now).
         if (!st && o->I_s && !side && !fused) st = shared_ffn(ctx->stream);

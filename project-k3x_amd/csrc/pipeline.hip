@@ -1360,7 +1360,17 @@ struct GemvArgs {
     // stores lo = bf16(v - hi) out_lo elements after hi (0: none).
     uint32_t x_lo;
     uint32_t out_lo;
+    // NORM kernels: x is the T raw rows; each workgroup applies RMSNorm with
+    // these weights to them in LDS first.
+    const float* gamma;
+    float eps;
 };
+
+// NORM: tokens a workgroup normalises (256 threads each) and 16-byte chunks
+// of the raw rows and of gamma its threads load (two and one a thread).
+constexpr uint32_t kNormOutTokens = 4;
+constexpr uint32_t kNormOutRowChunks = 2 * 64 * kGemvWaves;
+constexpr uint32_t kNormOutGammaChunks = 64 * kGemvWaves;
 
 // Output rows [16 rb, 16 rb + 16) by a workgroup of W waves.
 // LDSX: the T activation rows (x 16-byte aligned, x_stride == K, at most
@@ -1368,7 +1378,15 @@ struct GemvArgs {
 // the workgroup, their loads issued before the weights', so a wave holds only
 // its weight tiles in registers (the kernel then fits two workgroups a
 // compute unit).  The products and sums are those of the register path.
-template <int S, int D, int OUT, int W, bool SPLIT, bool LDSX = false>
+// NORM (LDSX, W = kGemvWaves, T <= kNormOutTokens): the rows are first
+// normalised in LDS by rmsnorm_kernel's arithmetic in its order -- 256
+// threads a token, thread r summing the squares of elements r + 256 j in
+// fp64 (j ascending), the wave butterfly, then (w0 + w1) + (w2 + w3) --
+// so the GEMV meets the same bf16 rows as after a separate RMSNorm launch;
+// a non-finite element latches K3X_ERR_INVALID_MXFP4, as there.  The
+// workgroup's barriers wait for LDS only: its weight tiles stay in flight
+// through the norm.
+template <int S, int D, int OUT, int W, bool SPLIT, bool LDSX = false, bool NORM = false>
 __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) {
     __shared__ f32x4 part[W][S][64];
     if (*(volatile const uint32_t*)a.status) return;
@@ -1379,10 +1397,17 @@ __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) 
     const bool live_row = (uint32_t)n < a.tokens;
     if constexpr (LDSX) {
         static_assert(!SPLIT, "one activation half");
-        extern __shared__ uint4 s_gx[];                // [T][K] bf16
+        static_assert(!NORM || W == kGemvWaves, "256 threads a token");
+        extern __shared__ uint4 s_gx[];                // [T][K] bf16 (NORM: then [K] fp32)
+        const uint32_t tid = threadIdx.x;
         const uint32_t chunks = a.tokens * a.kt * 16;  // 16-byte chunks of the T rows
-        const uint4 xv =
-            reinterpret_cast<const uint4*>(a.x)[min((uint32_t)threadIdx.x, chunks - 1)];
+        const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
+        const uint4 xv = x4[min(tid, chunks - 1)];
+        uint4 xv2, gv;
+        if constexpr (NORM) {
+            xv2 = x4[min(tid + 64 * W, chunks - 1)];
+            gv = reinterpret_cast<const uint4*>(a.gamma)[min(tid, a.kt * 32 - 1)];
+        }
         const uint4* wt = a.tiles + (size_t)rb * a.kt * S * 256 + lane;
         uint4 b[D][S][4];
 #pragma unroll
@@ -1393,8 +1418,53 @@ __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) 
 #pragma unroll
                 for (int u = 0; u < 4; ++u) b[d][w][u] = wt[((size_t)k * S + w) * 256 + u * 64];
         }
-        if (threadIdx.x < chunks) s_gx[threadIdx.x] = xv;
-        __syncthreads();
+        if (tid < chunks) s_gx[tid] = xv;
+        if constexpr (NORM) {
+            __shared__ double nred[W];
+            __shared__ uint32_t nbad[W];
+            const uint32_t K = a.kt * 128;
+            uint16_t* xs = reinterpret_cast<uint16_t*>(s_gx);
+            const float* gs = reinterpret_cast<const float*>(s_gx + chunks);
+            if (tid + 64 * W < chunks) s_gx[tid + 64 * W] = xv2;
+            if (tid < a.kt * 32) s_gx[chunks + tid] = gv;
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            const uint32_t t = tid / 256, r = tid % 256;  // token, its thread
+            const bool mine = t < a.tokens;               // wave-uniform
+            double sq = 0.0;
+            bool bad = false;
+            if (mine) {
+                for (uint32_t k = r; k < K; k += 256) {
+                    const float v = bf16_to_f32(xs[(size_t)t * K + k]);
+                    bad |= !__builtin_isfinite(v);
+                    sq = __builtin_fma((double)v, (double)v, sq);
+                }
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) sq += __shfl_xor(sq, d);
+            }
+            const bool wbad = __any(bad);
+            if (lane == 0) {
+                nred[wave] = sq;
+                nbad[wave] = wbad;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            uint32_t any_bad = 0;
+            for (uint32_t q = 0; q < 4 * a.tokens; ++q) any_bad |= nbad[q];
+            if (any_bad) {
+                if (tid == 0) latch(const_cast<uint32_t*>(a.status), K3X_ERR_INVALID_MXFP4);
+                return;
+            }
+            if (mine) {
+                const double* nr = nred + 4 * t;
+                const double tot = (nr[0] + nr[1]) + (nr[2] + nr[3]);
+                const float mean = (float)__ddiv_rn(tot, (double)K);
+                const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+                for (uint32_t k = r; k < K; k += 256) {
+                    uint16_t* e = xs + (size_t)t * K + k;
+                    *e = f32_to_bf16(__fmul_rn(__fmul_rn(bf16_to_f32(*e), inv), gs[k]));
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         const uint16_t* xrow =
             reinterpret_cast<const uint16_t*>(s_gx) + (size_t)row * a.kt * 128 + 32 * g;
         f32x4 acc[S];
@@ -1488,9 +1558,10 @@ __device__ __forceinline__ void dense_gemv_body(const GemvArgs& a, uint32_t rb) 
     }
 }
 
-template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false, bool LDSX = false>
+template <int S, int D, int OUT, int W = kGemvWaves, bool SPLIT = false, bool LDSX = false,
+          bool NORM = false>
 __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
-    dense_gemv_body<S, D, OUT, W, SPLIT, LDSX>(a, blockIdx.x);
+    dense_gemv_body<S, D, OUT, W, SPLIT, LDSX, NORM>(a, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2627,6 +2698,25 @@ int dense_down_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t
     else
         hipLaunchKernelGGL((dense_gemv_kernel<1, 3, 3>), dim3(N / 16), dim3(64 * kGemvWaves), 0,
                            ctx->stream, g);
+    return launched(ctx, 1);
+}
+
+bool dense_norm_output_ok(uint32_t N, uint32_t K, uint32_t T) {
+    return T && T <= kNormOutTokens && N % 128 == 0 && K % 128 == 0 &&
+           K / 128 <= 2 * kGemvWaves && (size_t)T * K / 8 <= kNormOutRowChunks &&
+           K / 4 <= kNormOutGammaChunks;
+}
+
+int dense_norm_output(k3x_hip_ctx* ctx, const uint4* tiles, uint32_t N, uint32_t K,
+                      const uint16_t* x, const float* gamma, float eps, uint32_t T,
+                      const float* prefix, const float* shared, float* routed, uint16_t* out) {
+    if (!dense_norm_output_ok(N, K, T) || (uintptr_t)x % 16 || (uintptr_t)gamma % 16)
+        return K3X_ERR_INVALID_EXTENT;
+    GemvArgs g{tiles, K / 128, x, K, T, out, N, {}, ctx->status, prefix, shared, routed};
+    g.gamma = gamma;
+    g.eps = eps;
+    hipLaunchKernelGGL((dense_gemv_kernel<1, 2, 3, kGemvWaves, false, true, true>), dim3(N / 16),
+                       dim3(64 * kGemvWaves), (size_t)T * K * 2 + (size_t)K * 4, ctx->stream, g);
     return launched(ctx, 1);
 }
 
