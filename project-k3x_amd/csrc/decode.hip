@@ -1374,6 +1374,9 @@ constexpr int kDownWaves = 4;
 // SPLIT: activation rows [hi | lo], two MFMAs per weight fragment.
 constexpr int kDownTilesDecode = 16, kDownActDecode = 4;  // the decode path: I <= 2048
 constexpr int kDownTilesFew = 24, kDownActFew = 12;       // general path: I <= 3072, split
+// Split rows that fit half the loads (two tokens at I = 3072): 162 VGPRs,
+// three workgroups a compute unit where the 12-load kernel fits two.
+constexpr int kDownActFewHalf = kDownActFew / 2;
 
 template <int TILES, int ACT, bool SPLIT, bool ROWS = false>
 __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
@@ -1799,6 +1802,10 @@ int launch_few_row_down(k3x_hip_ctx* ctx, const k3x_hip_bank* bank, uint32_t T, 
     else if (split && chunked)
         hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true, true>), grid,
                            block, lds, ctx->stream, dn);
+    else if (split &&
+             (size_t)rows * dn.a_stride / 8 <= (size_t)64 * kDownWaves * kDownActFewHalf)
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFewHalf, true, false>),
+                           grid, block, lds, ctx->stream, dn);
     else if (split)
         hipLaunchKernelGGL((decode_down_kernel<kDownTilesFew, kDownActFew, true, false>), grid,
                            block, lds, ctx->stream, dn);
