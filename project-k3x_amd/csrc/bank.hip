@@ -419,6 +419,8 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         hipStreamCreateWithFlags(&ctx->side_stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->class_fork_ev, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->class_join_ev, hipEventDisableTiming) != hipSuccess ||
         hipMalloc((void**)&ctx->status, 256) != hipSuccess ||
         hipMemset(ctx->status, 0, 256) != hipSuccess ||
         hipMalloc((void**)&ctx->mix_counts, k3x_hip::kDecodeMixBytes + 256) != hipSuccess ||
@@ -431,6 +433,8 @@ int k3x_hip_ctx_create(int device, k3x_hip_ctx** out) {
         if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
         if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
         if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
+        if (ctx->class_fork_ev) (void)hipEventDestroy(ctx->class_fork_ev);
+        if (ctx->class_join_ev) (void)hipEventDestroy(ctx->class_join_ev);
         if (ctx->status) (void)hipFree(ctx->status);
         if (ctx->mix_counts) (void)hipFree(ctx->mix_counts);
         delete ctx;
@@ -470,6 +474,8 @@ int k3x_hip_ctx_destroy(k3x_hip_ctx* ctx) {
     if (ctx->side_stream) (void)hipStreamDestroy(ctx->side_stream);
     if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
     if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
+    if (ctx->class_fork_ev) (void)hipEventDestroy(ctx->class_fork_ev);
+    if (ctx->class_join_ev) (void)hipEventDestroy(ctx->class_join_ev);
     delete ctx;
     return K3X_OK;
 }

@@ -106,7 +106,12 @@ __device__ inline void end_step(int d) {
 // (row tile, weight block) pair takes two v_mfma_scale_f32_16x16x128_f8f6f4
 // per K tile (hi, lo) on the weight codes as stored, in place of four bf16
 // MFMAs on dequantised weights.
-template <bool FP4, bool GATEUP, int NT, bool SPLIT, bool Q>
+// MTC > 0 (routed kinds): a launch over one size class of the grouping's
+// work items (each class's items in a list segment of its own, the class
+// counts after the total in n_items), every chunk multiplied as MTC row
+// tiles; MTC = 0 (shared kinds): every row chunk of the batch, the row tiles
+// chosen per chunk below.
+template <bool FP4, bool GATEUP, int NT, bool SPLIT, bool Q, int MTC = 0>
 __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     static_assert(!Q || (FP4 && !SPLIT), "q8 rows meet MXFP4 weights, one term pair per tile");
     // 128 KiB ring; the split gate/up's epilogue stages 128 rows of fp32
@@ -138,14 +143,19 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     // of idling whole XCDs.
     if (prior_status(a.status)) return;
     const uint32_t nblk = a.nrb / (kWaves * NT);
-    const uint32_t nvalid = a.items ? min(*a.n_items * nblk, gridDim.x) : gridDim.x;
+    uint32_t ibase = 0, nlisted = a.items ? *a.n_items : 0;
+    if constexpr (MTC > 0) {
+        for (uint32_t c = 0; c < a.item_class; ++c) ibase += a.n_items[1 + c];
+        nlisted = a.n_items[1 + a.item_class];
+    }
+    const uint32_t nvalid = a.items ? min(nlisted * nblk, gridDim.x) : gridDim.x;
     if (blockIdx.x >= nvalid) return;
     const uint32_t xcd = blockIdx.x % 8, per = nvalid / 8, rem = nvalid % 8;
     const uint32_t lb = xcd * per + min(xcd, rem) + blockIdx.x / 8;
     const uint32_t item = lb / nblk, jb = lb % nblk;
     uint32_t e = 0, cnt = a.tokens, off = 0, m0 = item * kWideRows;
     if (a.items) {
-        const uint32_t it = a.items[item];
+        const uint32_t it = a.items[ibase + item];
         e = it >> 16;
         m0 = (it & 0xffffu) * kWideRows;
         cnt = a.counts[e];
@@ -257,10 +267,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
             (k) * 8, 0, 0);
 #define WIDE_ORDER() asm volatile("" ::: "memory")
 
-    // MT = row tiles multiplied: the chunk's rows rounded up to 64, 96 or
-    // 128 rows, see the dispatch at the end (a workgroup-uniform choice made
-    // once, so the step loop has no branches; tiles past the chunk's rows
-    // hold copies of its last row and are not stored).
+    // MT = row tiles multiplied: the chunk's rows rounded up to 32, 64, 96
+    // or 128 rows, see the dispatch at the end (a workgroup-uniform choice
+    // made once, so the step loop has no branches; tiles past the chunk's
+    // rows hold copies of its last row and are not stored).
     auto run = [&](auto mt_count) {
         constexpr int MT = decltype(mt_count)::value;
         f32x4 acc[MT][NT][S];
@@ -473,17 +483,28 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
             }
         }
     };
-    // Four, six or eight row tiles; the routed gate/up kernel (the most
-    // registers) keeps to four or eight: a third variant there makes the
-    // register allocator spill inside the step loop.  (Two tiles as a fourth
-    // variant does the same in the others.)
-    constexpr bool kSix = !(FP4 && GATEUP);
-    if (rows > kWideRows * 3 / 4 || (!kSix && rows > kWideRows / 2))
-        run(std::integral_constant<int, kMTiles>{});
-    else if (kSix && rows > kWideRows / 2)
-        run(std::integral_constant<int, kSix ? kMTiles * 3 / 4 : kMTiles>{});
-    else
-        run(std::integral_constant<int, kMTiles / 2>{});
+    // Routed kinds: the launch's class fixes the row tiles, one step loop a
+    // kernel (with a choice of three or four row-tile counts inside one
+    // kernel, the register allocator spilled in the routed gate/up's step
+    // loop).  Shared kinds: four, six or eight row tiles, by the chunk's rows.
+    if constexpr (MTC > 0) {
+        // The grouping's class rule bounds the chunk's rows; a chunk past it
+        // would lose rows, so it is an error, never a silent result.
+        if (rows > 16u * MTC) {
+            if (tid == 0)
+                atomicCAS(const_cast<uint32_t*>(a.status), 0u, (uint32_t)K3X_ERR_INVALID_STATE);
+            return;
+        }
+        run(std::integral_constant<int, MTC>{});
+    } else {
+        static_assert(!FP4, "routed kinds launch per size class");
+        if (rows > kWideRows * 3 / 4)
+            run(std::integral_constant<int, kMTiles>{});
+        else if (rows > kWideRows / 2)
+            run(std::integral_constant<int, kMTiles * 3 / 4>{});
+        else
+            run(std::integral_constant<int, kMTiles / 2>{});
+    }
 }
 
 #undef WIDE_LOAD_A
@@ -553,36 +574,52 @@ uint32_t wide_rb_per_block(WideKind kind) {
     }
 }
 
-int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items,
-                     hipStream_t stream) {
+int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& args,
+                     uint32_t max_items, hipStream_t stream, int item_class) {
     if (!stream) stream = ctx->stream;
     const uint32_t per = wide_rb_per_block(kind);
-    if (a.nrb % per || a.kt % kWideStages || !a.kt || !max_items) return K3X_ERR_INVALID_EXTENT;
+    if (args.nrb % per || args.kt % kWideStages || !args.kt || !max_items)
+        return K3X_ERR_INVALID_EXTENT;
+    // Routed kinds: one size class of the grouping's items a launch; the
+    // shared kinds take every row of the batch.
+    const bool routed = kind == kWideRoutedGateUp || kind == kWideRoutedDown;
+    if (routed ? (!args.items || item_class < 0 || item_class >= (int)kWideClasses)
+               : item_class != -1)
+        return K3X_ERR_INVALID_EXTENT;
     // The epilogue stores 16-byte row pieces.
     const bool gu = kind == kWideRoutedGateUp || kind == kWideSharedGateUp;
-    if (gu ? ((uintptr_t)a.act % 16 || a.act_stride % 8 || a.act_lo % 8)
-           : ((uintptr_t)a.y % 16 || a.y_stride % 4))
+    if (gu ? ((uintptr_t)args.act % 16 || args.act_stride % 8 || args.act_lo % 8)
+           : ((uintptr_t)args.y % 16 || args.y_stride % 4))
         return K3X_ERR_INVALID_EXTENT;
-    if (a.kta && (a.kta != 2 * a.kt || gu)) return K3X_ERR_INVALID_EXTENT;
-    const bool split = gu ? a.act_lo != 0 : a.kta != 0;
+    if (args.kta && (args.kta != 2 * args.kt || gu)) return K3X_ERR_INVALID_EXTENT;
+    const bool split = gu ? args.act_lo != 0 : args.kta != 0;
     // q8 rows: routed kinds only, no split halves, a scale dword pair per
     // row and K tile.
-    const bool q8 = a.qs != nullptr;
-    if (q8 && (split || (kind != kWideRoutedGateUp && kind != kWideRoutedDown) ||
-               (uintptr_t)a.qs % 8 || a.a_stride != a.kt * 128))
+    const bool q8 = args.qs != nullptr;
+    if (q8 && (split || !routed || (uintptr_t)args.qs % 8 || args.a_stride != args.kt * 128))
         return K3X_ERR_INVALID_EXTENT;
+    WideGemmArgs a = args;
+    a.item_class = routed ? (uint32_t)item_class : 0u;
     const dim3 grid(max_items * (a.nrb / per));
 #define K3X_GO(...) hipLaunchKernelGGL((__VA_ARGS__), grid, dim3(kThreads), 0, stream, a)
+    // Row tiles of the classes: 8, 6, 4, 2.
+#define K3X_CLASS(GU_, NT_, SPLIT_, Q_)                                          \
+    switch (item_class) {                                                       \
+        case 0: K3X_GO(wide_gemm<true, GU_, NT_, SPLIT_, Q_, 8>); break;         \
+        case 1: K3X_GO(wide_gemm<true, GU_, NT_, SPLIT_, Q_, 6>); break;         \
+        case 2: K3X_GO(wide_gemm<true, GU_, NT_, SPLIT_, Q_, 4>); break;         \
+        default: K3X_GO(wide_gemm<true, GU_, NT_, SPLIT_, Q_, 2>); break;        \
+    }
     switch (kind) {
         case kWideRoutedGateUp:
-            if (q8) K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, false, true>);
-            else if (split) K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, true, false>);
-            else K3X_GO(wide_gemm<true, true, kNtRoutedGateUp, false, false>);
+            if (q8) K3X_CLASS(true, kNtRoutedGateUp, false, true)
+            else if (split) K3X_CLASS(true, kNtRoutedGateUp, true, false)
+            else K3X_CLASS(true, kNtRoutedGateUp, false, false)
             break;
         case kWideRoutedDown:
-            if (q8) K3X_GO(wide_gemm<true, false, kNtRoutedDown, false, true>);
-            else if (split) K3X_GO(wide_gemm<true, false, kNtRoutedDown, true, false>);
-            else K3X_GO(wide_gemm<true, false, kNtRoutedDown, false, false>);
+            if (q8) K3X_CLASS(false, kNtRoutedDown, false, true)
+            else if (split) K3X_CLASS(false, kNtRoutedDown, true, false)
+            else K3X_CLASS(false, kNtRoutedDown, false, false)
             break;
         case kWideSharedGateUp:
             if (split) K3X_GO(wide_gemm<false, true, kNtSharedGateUp, true, false>);
@@ -593,6 +630,7 @@ int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uin
             else K3X_GO(wide_gemm<false, false, kNtSharedDown, false, false>);
             break;
     }
+#undef K3X_CLASS
 #undef K3X_GO
     ctx->kernel_launches += 1;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;

@@ -49,6 +49,7 @@ struct WideGemmArgs {
     uint32_t scatter;            // y row = token * top_k + slot (1) or off + m (0)
     k3x_dev::GluParams glu;
     const uint32_t* status;
+    uint32_t item_class;         // routed kinds: the size class of the launch's items
 };
 
 enum WideKind {
@@ -68,11 +69,19 @@ constexpr uint32_t kWideStages = 4;
 // nrb to be a multiple of it).
 uint32_t wide_rb_per_block(WideKind kind);
 
+// Size classes of the routed work items: chunks of more than 96 rows (every
+// chunk but an expert's last is full), of 65-96, 33-64 and 1-32 rows,
+// multiplied as 8, 6, 4 and 2 row tiles of 16.
+constexpr uint32_t kWideClasses = 4;
+
 // Enqueues one wide GEMM on `stream` (the context stream when null):
-// max_items row chunks (an upper bound of *n_items for the routed kinds) x
-// the output row blocks, one workgroup each.
+// max_items row chunks x the output row blocks, one workgroup each.  Routed
+// kinds: the items of size class item_class (0 .. kWideClasses - 1), listed
+// in the class segments the grouping writes (n_items[1 + c] items of class c
+// after those of the classes before it), max_items an upper bound of their
+// count.  Shared kinds: item_class -1, every 128-row chunk of the batch.
 int launch_wide_gemm(k3x_hip_ctx* ctx, WideKind kind, const WideGemmArgs& a, uint32_t max_items,
-                     hipStream_t stream = nullptr);
+                     hipStream_t stream = nullptr, int item_class = -1);
 
 // bf16 rows [rows][cols] (row stride `stride` elements) -> q8 rows q
 // ([rows][cols] 16-bit units: 2 cols bytes a row) and their scale dwords qs

@@ -26,6 +26,9 @@ struct k3x_hip_ctx {
     // forked from and joined back into `stream` with these events.
     hipStream_t side_stream = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    // The wide path's smaller size classes run on side_stream beside the
+    // full chunks: forked after the grouping, joined after their down GEMMs.
+    hipEvent_t class_fork_ev = nullptr, class_join_ev = nullptr;
     uint32_t* status = nullptr;  // device word, latched kernel errors
     size_t max_lds_per_block = 65536;
     uint32_t cu_count = 256;
@@ -130,7 +133,7 @@ struct LayerBuffers {
     uint4* arec;           // [E] decode path: per active slot {expert, rows, CSR offset,
                            //     tokens of the rows, 8 bits each}
     uint32_t* witems;      // wide GEMM work items (expert << 16 | 128-row chunk)
-    uint32_t* n_witems;    // [1]
+    uint32_t* n_witems;    // [1 + kWideClasses]: all items, then each size class's
     uint8_t* gscratch;     // grouping: per-chunk counts and first uses, pair ranks
     uint16_t* xp;          // [T/16][256][16][4][8] bf16 tile/residue-major xn (in y's bytes)
     // K3X_FLAG_SCALED_FP4 only (else null): q8 rows of xn and act, and their

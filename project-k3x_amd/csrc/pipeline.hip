@@ -1034,32 +1034,49 @@ __device__ inline bool group_scan_body(
         if (witems) *n_witems = n_items;
     }
     if (witems) {
-        // Wide GEMM work items, balanced over the XCDs.  Rank k orders the
-        // items by size class -- full chunks and partial chunks of > 3/4,
-        // then > 1/2, then <= 1/2 of chunk_rows (a chunk's time follows its
-        // row tiles) -- and by expert within a class.  Item k goes to list
-        // segment k % 8, position k / 8: the GEMM hands each XCD one
-        // contiguous eighth of the list, so every XCD gets the same mix.
+        // Wide GEMM work items in kWideClasses segments, one launch each:
+        // class 0 holds every full chunk and the last chunks of more than
+        // 3/4 of chunk_rows, classes 1, 2 and 3 the last chunks of more than
+        // 1/2, more than 1/4 and at most 1/4 of it (a launch multiplies its
+        // class's chunks as 8, 6, 4 or 2 row tiles).  Rank k of a class (by
+        // expert) goes to segment position k % 8 * q + min(k % 8, r) + k / 8
+        // (q, r = the class's count / 8, % 8): the GEMM hands each XCD one
+        // contiguous eighth of the segment, so each XCD gets every eighth
+        // item.
         auto cls = [&](uint32_t c) -> uint32_t {  // class of an expert's last chunk
             const uint32_t last = c - (c - 1) / chunk_rows * chunk_rows;
-            return last * 4 > chunk_rows * 3 ? 0u : last * 2 > chunk_rows ? 1u : 2u;
+            return last * 4 > chunk_rows * 3 ? 0u
+                   : last * 2 > chunk_rows   ? 1u
+                   : last * 4 > chunk_rows   ? 2u
+                                             : 3u;
         };
-        auto counts3 = [&](uint32_t c) -> uint64_t {  // class counts, 24 | 16 | 16 bits
+        auto counts01 = [&](uint32_t c) -> uint64_t {  // items of classes 0 | 1
             if (!c) return 0;
             const uint32_t nq = (c + chunk_rows - 1) / chunk_rows, k = cls(c);
-            return (uint64_t)(nq - 1 + (k == 0)) | (uint64_t)(k == 1) << 24 |
-                   (uint64_t)(k == 2) << 40;
+            return (uint64_t)(nq - 1 + (k == 0)) | (uint64_t)(k == 1) << 32;
         };
-        uint64_t mine3 = 0;
+        auto counts23 = [&](uint32_t c) -> uint64_t {  // items of classes 2 | 3
+            if (!c) return 0;
+            const uint32_t k = cls(c);
+            return (uint64_t)(k == 2) | (uint64_t)(k == 3) << 32;
+        };
+        uint64_t mine01 = 0, mine23 = 0;
         for (uint32_t i = 0; i < per; ++i)
-            if (e0 + i < E) mine3 += counts3(s_cnt[e0 + i]);
-        uint64_t total3;
-        uint64_t pre3 = block_exclusive_scan(mine3, red, &total3);
-        const uint32_t n0 = (uint32_t)(total3 & 0xffffffu), n1 = (uint32_t)((total3 >> 24) & 0xffffu);
-        const uint32_t q8 = n_items / 8, r8 = n_items % 8;
-        auto place = [&](uint32_t k) {  // list position of rank k
+            if (e0 + i < E) {
+                mine01 += counts01(s_cnt[e0 + i]);
+                mine23 += counts23(s_cnt[e0 + i]);
+            }
+        uint64_t total01, total23;
+        uint64_t pre01 = block_exclusive_scan(mine01, red, &total01);
+        uint64_t pre23 = block_exclusive_scan(mine23, red, &total23);
+        const uint32_t ncls[4] = {(uint32_t)total01, (uint32_t)(total01 >> 32), (uint32_t)total23,
+                                  (uint32_t)(total23 >> 32)};
+        const uint32_t base[4] = {0u, ncls[0], ncls[0] + ncls[1], ncls[0] + ncls[1] + ncls[2]};
+        if (tid == 0)
+            for (int c = 0; c < 4; ++c) n_witems[1 + c] = ncls[c];
+        auto place = [&](uint32_t c, uint32_t k) {  // list position of rank k of class c
             const uint32_t x = k % 8;
-            return x * q8 + min(x, r8) + k / 8;
+            return base[c] + x * (ncls[c] / 8) + min(x, ncls[c] % 8) + k / 8;
         };
         for (uint32_t i = 0; i < per; ++i) {
             const uint32_t e = e0 + i;
@@ -1067,14 +1084,16 @@ __device__ inline bool group_scan_body(
             const uint32_t c = s_cnt[e];
             if (c) {
                 const uint32_t nq = (c + chunk_rows - 1) / chunk_rows, k = cls(c);
-                const uint32_t p0 = (uint32_t)(pre3 & 0xffffffu);
-                for (uint32_t q = 0; q + 1 < nq; ++q) witems[place(p0 + q)] = (e << 16) | q;
+                const uint32_t p0 = (uint32_t)pre01;
+                for (uint32_t q = 0; q + 1 < nq; ++q) witems[place(0, p0 + q)] = (e << 16) | q;
                 const uint32_t kl = k == 0   ? p0 + nq - 1
-                                    : k == 1 ? n0 + (uint32_t)((pre3 >> 24) & 0xffffu)
-                                             : n0 + n1 + (uint32_t)(pre3 >> 40);
-                witems[place(kl)] = (e << 16) | (nq - 1);
+                                    : k == 1 ? (uint32_t)(pre01 >> 32)
+                                    : k == 2 ? (uint32_t)pre23
+                                             : (uint32_t)(pre23 >> 32);
+                witems[place(k, kl)] = (e << 16) | (nq - 1);
             }
-            pre3 += counts3(c);
+            pre01 += counts01(c);
+            pre23 += counts23(c);
         }
     }
     __syncthreads();
@@ -1703,7 +1722,7 @@ size_t carve(uint8_t* base, const k3x_hip_layer_desc& d, uint32_t T, uint32_t K,
     s->sy = (float*)take((size_t)T * d.hidden * 4);
     s->arec = (uint4*)take((size_t)d.experts * 16);
     s->witems = (uint32_t*)take((size_t)wide_max_items(d, T, K) * 4);
-    s->n_witems = (uint32_t*)take(4);
+    s->n_witems = (uint32_t*)take(4 * (1 + k3x_hip::kWideClasses));
     s->gscratch = take(group_scratch_bytes(T, K, d.experts));
     s->qx = q8 ? (uint16_t*)take((size_t)T * d.hidden * 2) : nullptr;
     s->qxs = q8 ? (uint32_t*)take((size_t)T * (d.hidden / 128) * 8) : nullptr;
@@ -2164,19 +2183,58 @@ int run_shared_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_para
 }
 
 // Routed gate/up + GLU, then down; with shared_inline the shared expert's
-// GEMMs run on the context stream after each routed one.
+// GEMMs run on the context stream after each routed one.  The routed GEMMs
+// run per size class of the grouping's items (kWideClasses): class 0 (full
+// chunks) on the context stream; classes 1-3 (the experts' partial last
+// chunks at 6, 4 and 2 row tiles) on the side stream beside it, forked
+// after the grouping and joined before the return -- their down GEMMs need
+// only their own gate/up rows.  In line with stage profiling.
 int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              const Scratch& s, const uint16_t* xn, const GluParams& glu, bool shared_inline) {
     using namespace k3x_hip;
     const auto& d = bank->desc;
     const uint32_t T = p->tokens, K = p->top_k;
     // Routed: one workgroup column per (expert, 128-row chunk) item the
-    // grouping listed (up to wide_max_items).
+    // grouping listed, up to wide_max_items in class 0 and one an active
+    // expert (its last chunk) in each of the others.
     const uint32_t routed_chunks = wide_max_items(d, T, K);
+    const uint32_t last_chunks = std::min(routed_chunks, std::min(d.experts, T * K));
+    // q8 rows are quantised for all classes at once on the context stream.
+    const bool q8 = s.qx != nullptr;
+    const bool beside = !ctx->profiling && ctx->side_stream && !q8;
+    hipStream_t cstream = beside ? ctx->side_stream : ctx->stream;
+    struct ClassJoin {
+        k3x_hip_ctx* ctx;
+        bool armed = false;
+        int join() {
+            if (!armed) return K3X_OK;
+            armed = false;
+            if (hipEventRecord(ctx->class_join_ev, ctx->side_stream) != hipSuccess) {
+                (void)hipStreamSynchronize(ctx->side_stream);
+                return K3X_ERR_BACKEND_UNAVAILABLE;
+            }
+            return hipStreamWaitEvent(ctx->stream, ctx->class_join_ev, 0) == hipSuccess
+                       ? K3X_OK
+                       : K3X_ERR_BACKEND_UNAVAILABLE;
+        }
+        ~ClassJoin() { (void)join(); }
+    } cjoin{ctx};
+    if (beside) {
+        if (hipEventRecord(ctx->class_fork_ev, ctx->stream) != hipSuccess ||
+            hipStreamWaitEvent(ctx->side_stream, ctx->class_fork_ev, 0) != hipSuccess)
+            return K3X_ERR_BACKEND_UNAVAILABLE;
+        cjoin.armed = true;
+    }
+    auto routed = [&](WideKind kind, const WideGemmArgs& a, bool full) {
+        if (full) return launch_wide_gemm(ctx, kind, a, routed_chunks, ctx->stream, 0);
+        int r = K3X_OK;
+        for (int c = 1; !r && c < (int)kWideClasses; ++c)
+            r = launch_wide_gemm(ctx, kind, a, last_chunks, cstream, c);
+        return r;
+    };
     WideGemmArgs g = wide_gate_up_args(ctx, bank, p, s, xn, glu);
     // Scaled FP4: the experts read q8 rows of xn, then of act (quantised
     // in the stage that consumes them).
-    const bool q8 = s.qx != nullptr;
     int mark = begin_stage(ctx, K3X_STAGE_GATE_UP);
     int st = K3X_OK;
     if (q8) {
@@ -2185,7 +2243,8 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         g.qs = s.qxs;
         g.qs_bytes = T * (d.hidden / 128) * 8;
     }
-    if (!st) st = launch_wide_gemm(ctx, kWideRoutedGateUp, g, routed_chunks);
+    if (!st) st = routed(kWideRoutedGateUp, g, false);
+    if (!st) st = routed(kWideRoutedGateUp, g, true);
     end_stage(ctx, mark);
     if (st) return st;
     if (shared_inline && d.shared_inter &&
@@ -2216,9 +2275,11 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
         dn.qs = s.qacts;
         dn.qs_bytes = T * K * (d.inter / 128) * 8;
     }
-    if (!st) st = launch_wide_gemm(ctx, kWideRoutedDown, dn, routed_chunks);
+    if (!st) st = routed(kWideRoutedDown, dn, false);
+    if (!st) st = routed(kWideRoutedDown, dn, true);
     end_stage(ctx, mark);
-    return st;
+    const int jst = cjoin.join();
+    return st ? st : jst;
 }
 
 // Grouping, expert GEMMs, shared expert, combine.  xn is the bf16 input of
