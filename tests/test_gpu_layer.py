@@ -693,9 +693,10 @@ def test_c5_prefill_chunk(hip, oracle, parity_report):
     """Config 5: T=2048 prefill chunk.  Device Top-16 ids equal the ids the
     reference's CPU functions chose (golden fixture); grouping bit-exact;
     outputs of every 16th token (128 tokens, 2048 pairs) plus tokens chosen
-    so that a checked pair falls in each work-item class of the wide grouped
-    GEMM (128-row chunks: full, 97-127, 65-96 and at most 64 rows; partial
-    last chunks) and the last token;
+    so that a checked pair falls in each size class of the wide grouped
+    GEMM's launches (128-row chunks: full and 97-127 rows at 8 row tiles,
+    65-96 at 6, 33-64 at 4, at most 32 at 2; partial last chunks) and the
+    last token;
     permuting the tokens permutes the output bit for bit (rows of the grouped
     GEMMs are independent)."""
     import os
@@ -714,10 +715,11 @@ def test_c5_prefill_chunk(hip, oracle, parity_report):
         "full_128": (ch, lambda r, last: r == ch),
         "partial_97_127": (ch, lambda r, last: 96 < r < ch),
         "partial_65_96": (ch, lambda r, last: 64 < r <= 96),
-        "partial_le_64": (ch, lambda r, last: r <= 64 and last)})
+        "partial_33_64": (ch, lambda r, last: 32 < r <= 64 and last),
+        "partial_le_32": (ch, lambda r, last: r <= 32 and last)})
     tokens = sorted(set(picked.values()) | set(range(0, cfg.tokens, 16)) | {cfg.tokens - 1})
     say(f"c5: {len(tokens)} tokens checked, item classes {picked}")
-    assert len(picked) == 4 and len(tokens) >= 128
+    assert len(picked) == 5 and len(tokens) >= 128
     check_layer(oracle, layer, got, x, tokens_checked=tokens, report=parity_report)
     perm = np.random.default_rng(5).permutation(cfg.tokens)
     gp = run_layer(k3x_amd, ctx, cfg, bank, x[perm], per_pair=False)
@@ -750,9 +752,10 @@ def test_c5_prefill_scaled_fp4(hip, oracle, parity_report):
         "full_128": (ch, lambda r, last: r == ch),
         "partial_97_127": (ch, lambda r, last: 96 < r < ch),
         "partial_65_96": (ch, lambda r, last: 64 < r <= 96),
-        "partial_le_64": (ch, lambda r, last: r <= 64 and last)})
+        "partial_33_64": (ch, lambda r, last: 32 < r <= 64 and last),
+        "partial_le_32": (ch, lambda r, last: r <= 32 and last)})
     tokens = sorted(set(picked.values()) | {0, cfg.tokens - 1})
-    assert len(picked) == 4
+    assert len(picked) == 5
     act_ref, y_ref = layer.pair_outputs(xn, ids, tokens)
     shared = layer.shared_out(xn, tokens)
     out_ref = layer.combine(y_ref, w, shared, tokens)
