@@ -2200,9 +2200,11 @@ int run_shared_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_para
 // GEMMs run on the context stream after each routed one.  The routed GEMMs
 // run per size class of the grouping's items (kWideClasses): class 0 (full
 // chunks) on the context stream; classes 1-3 (the experts' partial last
-// chunks at 6, 4 and 2 row tiles) on the side stream beside it, forked
-// after the grouping and joined before the return -- their down GEMMs need
-// only their own gate/up rows.  In line with stage profiling.
+// chunks at 6, 4 and 2 row tiles) on the side stream beside it (behind the
+// shared expert's GEMMs when they run there), forked after the grouping and
+// joined before the return -- their down GEMMs need only their own gate/up
+// rows.  In line with stage profiling and with q8 rows (quantised for every
+// class at once on the context stream).
 int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              const Scratch& s, const uint16_t* xn, const GluParams& glu, bool shared_inline) {
     using namespace k3x_hip;
