@@ -756,7 +756,9 @@ int k3x_hip_official_ffn(k3x_hip_ctx* ctx, k3x_hip_official* o, const k3x_hip_mo
     // routed = routed_up . RMSNorm(mixed, routed_norm) (official_moe.cpp:327-333).
     // Up to four tokens, one launch: every routed_up workgroup normalises the
     // mixed rows itself.
-    const bool norm_out = k3x_hip::dense_norm_output_ok(o->H, o->L, T);
+    const bool norm_out = k3x_hip::dense_norm_output_ok(o->H, o->L, T) &&
+                          reinterpret_cast<uintptr_t>(b.mixed) % 16 == 0 &&
+                          reinterpret_cast<uintptr_t>(o->routed_norm) % 16 == 0;
     if (!norm_out)
         st = k3x_hip::launch_rmsnorm(ctx, b.mixed, o->routed_norm, T, o->L, p->rms_epsilon,
                                      b.normed);
