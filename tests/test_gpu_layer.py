@@ -632,6 +632,88 @@ def tokens_by_row_class(got, K, classes):
     return picked
 
 
+def test_wide_class_boundaries(hip, oracle):
+    """The wide path's per-class launches at every class boundary: a host
+    route (k3x_hip_moe_forward_routed, T = 1028, Top-2, 16 experts) gives the
+    experts 32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193, 224, 225,
+    256 and 1 rows, so the 128-row chunks' last parts fall on both sides of
+    each boundary of the classes (<= 32, 33-64, 65-96, > 96 rows) and full
+    chunks come one, two and three to an expert.  Grouping bit-exact against
+    the oracle's CSR; every pair's activations against the oracle's expert
+    FFN; every pair's fp32 output against the down projection of the GPU's
+    own activations within 2^-16 of sum |w a|; the ordered mix bit-exact on
+    the GPU's per-pair rows."""
+    from synth import Config, SynthLayer
+    k3x_amd, ctx = hip
+    counts = [32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193, 224, 225, 256, 1]
+    E, K = len(counts), 2
+    T = sum(counts) // K
+    H = I = 512
+    cfg = Config("wide_classes", T, H, I, E, K, 0, 119, 123)
+    layer = SynthLayer(oracle, cfg)
+    bank = make_bank(k3x_amd, ctx, cfg)
+    # Pair list sorted by expert, split in halves: token t takes entries t and
+    # t + T (distinct experts: no expert holds more than T rows).
+    flat = np.repeat(np.arange(E, dtype=np.uint32), counts)
+    ids = np.stack([flat[:T], flat[T:]], axis=1)
+    assert (ids[:, 0] != ids[:, 1]).all()
+    rng = np.random.default_rng(11)
+    w = rng.uniform(0.2, 1.0, (T, K)).astype(np.float32)
+    xn = layer.normed(layer.x_bits())
+    xn_bits = (xn.view(np.uint32) >> 16).astype(np.uint16)
+    dev = "cuda:0"
+    d_xn = torch.from_numpy(xn_bits.view(np.int16)).to(dev)
+    d_ids = torch.from_numpy(ids.view(np.int32)).to(dev)
+    d_w = torch.from_numpy(w).to(dev)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    z = lambda shape, dt: torch.empty(shape, dtype=dt, device=dev)
+    taps = dict(counts=z((E,), torch.int32), offsets=z((E + 1,), torch.int32),
+                pair_token=z((T * K,), torch.int32), pair_slot=z((T * K,), torch.int32),
+                act=z((T * K, I), torch.int16), expert_out=z((T, K, H), torch.float32),
+                out_f32=z((T, H), torch.float32))
+    params = k3x_amd.make_params(T, K, 1.0, cfg.eps, cfg.glu, cfg.beta, cfg.linear, cfg.renorm)
+    say(f"wide class boundaries: T={T} K={K} E={E} H={H} I={I}, rows per expert {counts}")
+    st = k3x_amd.moe_forward_routed(ctx, bank, params, d_xn, d_ids, d_w, out, taps=taps)
+    assert st == 0, st
+    assert ctx.synchronize() == 0
+    got = {k: to_np(v) for k, v in taps.items()}
+    for k in ("counts", "offsets", "pair_token", "pair_slot"):
+        got[k] = got[k].view(np.uint32)
+    act = got["act"].view(np.uint16)
+    st, csr = oracle.expert_major_csr(ids, E)
+    assert st == 0
+    assert np.array_equal(got["counts"], np.array(counts, np.uint32))
+    for k in ("counts", "offsets", "pair_token", "pair_slot"):
+        assert np.array_equal(got[k][:len(csr[k])], csr[k]), k
+    worst_act = 0
+    for e in range(E):
+        ex = layer.expert(e)
+        st, W = oracle.decode_mxfp4(ex["down_packed"], ex["down_scales"], H, I, 32)
+        assert st == 0
+        W64 = W.astype(np.float64)
+        r0, r1 = int(csr["offsets"][e]), int(csr["offsets"][e + 1])
+        for r in range(r0, r1):
+            t, s_ = int(csr["pair_token"][r]), int(csr["pair_slot"][r])
+            st, act_ref, _ = oracle.expert_ffn(xn[t], ex, H, I, cfg.glu, cfg.beta, cfg.linear,
+                                               round_act=True)
+            assert st == 0, st
+            ref_bits = (act_ref.view(np.uint32) >> 16).astype(np.uint16)
+            d = ulp_diff_bf16(act[r], ref_bits)
+            worst_act = max(worst_act, int(d.max()))
+            assert np.count_nonzero(d) / d.size < 0.02, f"expert {e} row {r - r0}: activations off"
+            a = bf16_to_f32(act[r]).astype(np.float64)
+            y = W64 @ a
+            err = np.abs(got["expert_out"][t, s_].astype(np.float64) - y)
+            assert (err <= 2.0 ** -16 * (np.abs(W64) @ np.abs(a)) + 1e-30).all(), \
+                f"expert {e} row {r - r0} (token {t} slot {s_}): down output off"
+    for t in range(T):
+        mix = oracle.ordered_mix(got["expert_out"][t], w[t])
+        assert np.array_equal(got["out_f32"][t].view(np.uint32), mix.view(np.uint32)), t
+    say(f"wide class boundaries: grouping bit-exact, {T * K} pairs checked "
+        f"(activations within {worst_act} bf16 ulp), ordered mix bit-exact")
+    bank.close()
+
+
 def test_c4_verification_window(hip, oracle, parity_report):
     """Config 4: T=64, Zipf-skewed routing (0..~40 rows per expert).  Routing
     and grouping bit-exact for all 1024 pairs; activations and outputs of
