@@ -2198,13 +2198,13 @@ int run_shared_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_para
 
 // Routed gate/up + GLU, then down; with shared_inline the shared expert's
 // GEMMs run on the context stream after each routed one.  The routed GEMMs
-// run per size class of the grouping's items (kWideClasses): class 0 (full
-// chunks) on the context stream; classes 1-3 (the experts' partial last
-// chunks at 6, 4 and 2 row tiles) on the side stream beside it (behind the
-// shared expert's GEMMs when they run there), forked after the grouping and
-// joined before the return -- their down GEMMs need only their own gate/up
-// rows.  In line with stage profiling and with q8 rows (quantised for every
-// class at once on the context stream).
+// run per size class of the grouping's items (kWideClasses): classes 0 (full
+// chunks) and 1 (last chunks of 65-96 rows) on the context stream; classes 2
+// and 3 (last chunks at 4 and 2 row tiles) on the side stream beside them
+// (behind the shared expert's GEMMs when they run there), forked after the
+// grouping and joined before the return -- a class's down GEMM needs only its
+// own gate/up rows.  In line with stage profiling and with q8 rows (quantised
+// for every class at once on the context stream).
 int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
              const Scratch& s, const uint16_t* xn, const GluParams& glu, bool shared_inline) {
     using namespace k3x_hip;
@@ -2241,11 +2241,17 @@ int run_wide(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_params* p,
             return K3X_ERR_BACKEND_UNAVAILABLE;
         cjoin.armed = true;
     }
-    auto routed = [&](WideKind kind, const WideGemmArgs& a, bool full) {
-        if (full) return launch_wide_gemm(ctx, kind, a, routed_chunks, ctx->stream, 0);
+    // Classes 0 and 1 on the context stream, 2 and 3 beside them (class 1
+    // beside as well left the side stream finishing last: prefill c5
+    // 3594-3624 against 3571-3610 us, the official layer at T=2048 5512-5530
+    // against 5415-5428; class 2 moved too, c5 3679-3704).
+    auto beside_class = [](int c) { return c >= 2; };
+    auto routed = [&](WideKind kind, const WideGemmArgs& a, bool main) {
         int r = K3X_OK;
-        for (int c = 1; !r && c < (int)kWideClasses; ++c)
-            r = launch_wide_gemm(ctx, kind, a, last_chunks, cstream, c);
+        for (int c = 0; !r && c < (int)kWideClasses; ++c)
+            if (beside_class(c) != main)
+                r = launch_wide_gemm(ctx, kind, a, c ? last_chunks : routed_chunks,
+                                     main ? ctx->stream : cstream, c);
         return r;
     };
     WideGemmArgs g = wide_gate_up_args(ctx, bank, p, s, xn, glu);
