@@ -4,10 +4,10 @@
 // with the reference's unmodified CPU sources (runtime/src/{ops,
 // routing_policy,expert_major,official_moe,backend_cpu,profile}.cpp, read
 // in place under /root/reference) into oracle/_ref/libk3x_ref.so.  Tests use
-// it to pin the C restatement in k3x_oracle.c, in this container only: the
-// library never travels to the GPU box (.gpurunignore lists oracle/_ref) and
-// nothing there loads or times it.  Nothing from the reference is copied
-// into this repository.
+// it to pin the C restatement in k3x_oracle.c, on the build machine only:
+// oracle/_ref is excluded from what is copied to GPU machines, and nothing
+// there loads or times it.  Nothing from the reference is copied into this
+// repository.
 #include "k3x/checksums.hpp"
 #include "k3x/backend.hpp"
 #include "k3x/expert_major.hpp"
