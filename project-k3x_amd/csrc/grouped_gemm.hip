@@ -163,13 +163,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     }
     if (m0 >= cnt) return;
     const uint32_t kt = a.kt;  // multiple of kWideStages (checked on the host)
-    // Activation tiles: kt, or 2 kt for split [hi | lo] rows, whose tile k
-    // meets weight tile k mod kt (a multiple of four tiles: a block of four
-    // never straddles the two halves, nor its scale dword).
+    // Activation tiles: kt, or 2 kt for split [hi | lo] rows, interleaved:
+    // step k multiplies weight tile k / 2 with the hi (k even) or lo (k odd)
+    // half's tile k / 2, so each weight tile is requested twice in a row and
+    // its second request finds it in the L2 (a block of four steps covers two
+    // weight tiles of one scale dword).
     constexpr bool kSplitIn = SPLIT && !GATEUP;
     const uint32_t kta = kSplitIn ? 2 * kt : kt;
     auto wtile = [&](uint32_t k) {
-        if constexpr (kSplitIn) return k >= kt ? k - kt : k;
+        if constexpr (kSplitIn) return k >> 1;
         else return k;
     };
     const uint32_t rows = min(cnt - m0, kWideRows);
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
     _Pragma("unroll") for (int q = 0; q < kALoads; ++q)                                      \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                            \
             arsrc, (lds_ptr_t)&s_a4[(buf) * kTileChunks + (16 * wave + 4 * q) * 16], 16,      \
-            aoff[q], (k) * 256, 0, 0);
+            aoff[q], (kSplitIn ? ((k) & 1) * kt + ((k) >> 1) : (k)) * 256, 0, 0);
 #define WIDE_LOAD_B(d, k)                                                                    \
     _Pragma("unroll") for (int nt = 0; nt < NT; ++nt)                                        \
         _Pragma("unroll") for (int w = 0; w < S; ++w) {                                      \
@@ -361,8 +363,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_gemm(WideGemmArgs a) {
                             for (int w = 0; w < S; ++w) {
                                 if constexpr (FP4) {
                                     const uint32_t word = bc[d][nt][w][0][j];
+                                    // Scale byte of weight tile wtile(k)
+                                    // in the block's dword.
+                                    const uint32_t sb =
+                                        kSplitIn ? 8 * (((kb >> 1) & 3) + (d >> 1)) : 8 * d;
                                     bw[nt][w] = dequant8(
-                                        word, e8m0_to_f32((sc[nt][w] >> (8 * d)) & 0xffu));
+                                        word, e8m0_to_f32((sc[nt][w] >> sb) & 0xffu));
                                 } else {
                                     bw[nt][w] = as_bf16x8(bc[d][nt][w][j]);
                                 }
