@@ -1098,34 +1098,53 @@ __global__ __launch_bounds__(64 * kGuWaves) void decode_gateup_kernel(GateUpArgs
 // n of the slot is token (rec.w >> 8 n) & 0xff), the slot records in LDS.
 // The loads, the MFMA steps, the wave tree and the GLU are those of
 // decode_gateup_kernel<1>.
-__device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t blk,
-                                                const uint16_t* s_x, const uint4* lrec,
-                                                uint32_t lna, f32x4 (&red)[kGuWaves][2][64]) {
-    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
-    const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t per_expert = a.I / 16;
-    const uint32_t ai = blk / per_expert, rb = blk % per_expert, wv = wave;
-    if (ai >= lna) return;  // block-uniform
-    const uint4 rec = lrec[ai];
-    const uint32_t e = rec.x, rows = rec.y, toks = rec.w;
-    const uint32_t H = a.H, kt = a.kt;
-    const uint32_t k0 = wv * kt / kGuWaves, k1 = (wv + 1) * kt / kGuWaves;
-    const uint32_t N = k1 - k0;
-    const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
-    const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
+// A wave's code tiles and scale dwords of one gate/up unit (expert e, 16-row
+// block rb): every load issued at once, none waited for here.
+struct GuUnitRegs {
     uint4 c0[kGuTiles], c1[kGuTiles];
     uint32_t s0[3], s1[3];
+};
+
+__device__ __forceinline__ void gateup_unit_load(const GateUpArgs& a, uint32_t e, uint32_t rb,
+                                                 GuUnitRegs& w) {
+    const uint32_t lane = threadIdx.x & 63, wv = wave_id();
+    const uint32_t kt = a.kt, k0 = wv * kt / kGuWaves;
+    const uint4* codes = a.gu_codes + e * a.codes_per_expert + (size_t)rb * kt * 2 * 64 + lane;
+    const uint32_t* scales = a.gu_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 2 * 64 + lane;
 #pragma unroll
     for (int i = 0; i < kGuTiles; ++i) {
-        const size_t k = min(k0 + i, kt - 1);  // tiles past k1 are loaded, not used
-        c0[i] = ntl(codes + k * 128);
-        c1[i] = ntl(codes + k * 128 + 64);
+        const size_t k = min(k0 + i, kt - 1);  // tiles past the wave's range are loaded, not used
+        w.c0[i] = ntl(codes + k * 128);
+        w.c1[i] = ntl(codes + k * 128 + 64);
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const size_t grp = min(k0 / 4 + i, a.ks - 1);
-        s0[i] = ntl(scales + grp * 128);
-        s1[i] = ntl(scales + grp * 128 + 64);
+        w.s0[i] = ntl(scales + grp * 128);
+        w.s1[i] = ntl(scales + grp * 128 + 64);
+    }
+}
+
+// The unit's products over the LDS xn rows of the slot record rec, the wave
+// tree, GLU and the bf16 activation stores.
+__device__ __forceinline__ void gateup_unit_compute(const GateUpArgs& a, uint32_t rb, uint4 rec,
+                                                    const uint16_t* s_x, const GuUnitRegs& w,
+                                                    f32x4 (&red)[kGuWaves][2][64]) {
+    const uint32_t lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t g = lane >> 4, n = lane & 15, wv = wave;
+    const uint32_t rows = rec.y, toks = rec.w;
+    const uint32_t H = a.H, kt = a.kt;
+    const uint32_t k0 = wv * kt / kGuWaves, k1 = (wv + 1) * kt / kGuWaves;
+    const uint32_t N = k1 - k0;
+    // Plain local copies: a select between struct members would become a
+    // load through a selected address and keep the struct in scratch.
+    const uint32_t s0[3] = {w.s0[0], w.s0[1], w.s0[2]};
+    const uint32_t s1[3] = {w.s1[0], w.s1[1], w.s1[2]};
+    uint4 c0[kGuTiles], c1[kGuTiles];
+#pragma unroll
+    for (int i = 0; i < kGuTiles; ++i) {
+        c0[i] = w.c0[i];
+        c1[i] = w.c1[i];
     }
     const uint32_t tok = (toks >> (8 * (n < rows ? n : 0))) & 0xffu;  // unused rows: row 0's
     const uint16_t* xrow = s_x + (size_t)tok * H + 32 * g;
@@ -1169,6 +1188,19 @@ __device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t bl
     }
 }
 
+// Unit blk = (active slot, 16-row block) of the slot records lrec[0, lna).
+__device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t blk,
+                                                const uint16_t* s_x, const uint4* lrec,
+                                                uint32_t lna, f32x4 (&red)[kGuWaves][2][64]) {
+    const uint32_t per_expert = a.I / 16;
+    const uint32_t ai = blk / per_expert, rb = blk % per_expert;
+    if (ai >= lna) return;  // block-uniform
+    const uint4 rec = lrec[ai];
+    GuUnitRegs w;
+    gateup_unit_load(a, rec.x, rb, w);
+    gateup_unit_compute(a, rb, rec, s_x, w, red);
+}
+
 // ---------------------------------------------------------------------------
 // Few experts (E <= kSmallMaxExperts, no shared expert): every workgroup of
 // the routed gate/up launch finds the route itself -- xn, the E router rows
@@ -1201,13 +1233,20 @@ struct SmallLds {
 };
 
 // NE router rows per wave (experts wave + kFrontWaves i); TT bounds T.
-template <int TT, int NE>
+// Workgroup b is unit (active slot, 16-row block).  ALL: every expert is
+// active (E <= K), so slot s holds expert s (the slots ascend by expert):
+// the unit's code tiles and scales are requested once the router products
+// are done, beside the Top-K and the grouping, instead of after them.
+template <int TT, int NE, bool ALL>
 __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(SmallArgs a) {
     static_assert(kFrontThreads == 64 * kGuWaves, "one workgroup shape for route and gate/up");
     extern __shared__ uint4 dyn_lds[];  // xn [T][H] bf16, then gamma
     __shared__ SmallLds sh;
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.sel.T, H = a.gu.H, E = a.sel.E, J = H / 256;
+    const uint32_t per_expert = a.gu.I / 16;
+    const uint32_t all_e = blockIdx.x / per_expert, all_rb = blockIdx.x % per_expert;
+    GuUnitRegs gw;
     constexpr int kPer = kSmallRowLoads / NE;  // J <= kPer (checked on the host)
     float4 wb[NE][kPer];
     auto prefetch = [&]() {
@@ -1261,21 +1300,31 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
             }
         }
     }
+    // The unit's weights stream while the block finds the Top-K and the
+    // grouping (LDS work only; the bias is requested first, since loads
+    // complete in order).
+    const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
+    const float bias_e = a.sel.bias[ee];
+    if constexpr (ALL) gateup_unit_load(a.gu, all_e, all_rb, gw);
     __syncthreads();
     // Top-K and grouping, as decode_select_kernel's block 0 (this block's
     // copy in LDS; block 0 stores it).
-    const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
     float lg[kMaxDecodeTokens];
 #pragma unroll
     for (int t = 0; t < kMaxDecodeTokens; ++t) lg[t] = sh.lg[min((uint32_t)t, T - 1)][ee];
     SelectArgs sa = a.sel;
     sa.local_only = blockIdx.x != 0;
-    if (!select_topk(sa, sh.sel, lg, a.sel.bias[ee])) return;
+    if (!select_topk(sa, sh.sel, lg, bias_e)) return;
     select_group(sa, sh.sel);
     __syncthreads();
     if (sh.sel.bad) return;
-    gateup_unit_lds(a.gu, blockIdx.x, reinterpret_cast<const uint16_t*>(dyn_lds), sh.sel.rec,
-                    sh.sel.na, sh.red);
+    const uint16_t* s_xn = reinterpret_cast<const uint16_t*>(dyn_lds);
+    if constexpr (ALL) {
+        // Every expert active: slot all_e holds expert all_e.
+        gateup_unit_compute(a.gu, all_rb, sh.sel.rec[all_e], s_xn, gw, sh.red);
+    } else {
+        gateup_unit_lds(a.gu, blockIdx.x, s_xn, sh.sel.rec, sh.sel.na, sh.red);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1378,7 +1427,10 @@ constexpr int kDownTilesFew = 24, kDownActFew = 12;       // general path: I <= 
 // three workgroups a compute unit where the 12-load kernel fits two.
 constexpr int kDownActFewHalf = kDownActFew / 2;
 
-template <int TILES, int ACT, bool SPLIT, bool ROWS = false>
+// ALL: every expert is active (E <= K), so slot ai holds expert ai (the
+// slots ascend by expert) and the weights are requested before the slot
+// record arrives.
+template <int TILES, int ACT, bool SPLIT, bool ROWS = false, bool ALL = false>
 __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a) {
     extern __shared__ uint4 s_act4[];  // [rows][a_stride] bf16
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -1386,12 +1438,32 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     const uint32_t per_expert = a.H / (16 * kDownWaves);
     const uint32_t ai = blockIdx.x / per_expert;
     const uint32_t rb = (blockIdx.x % per_expert) * kDownWaves + wave;
+    const uint32_t kt = a.kt;
+    // Code tiles and scale dwords of this wave's 16-row block of expert e.
+    uint4 c[TILES];
+    uint32_t sw[TILES / 4];
+    auto load_weights = [&](uint32_t e) {
+        const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
+        const uint32_t* scales =
+            a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < TILES; ++i) c[i] = ntl(codes + (size_t)min((uint32_t)i, kt - 1) * 64);
+#pragma unroll
+        for (int i = 0; i < TILES / 4; ++i)
+            sw[i] = ntl(scales + (size_t)min((uint32_t)i, a.ks - 1) * 64);
+    };
     const uint32_t st = prior_status(a.status);
     const uint32_t na = *a.n_active;
     const uint4 rec = a.arec[ai];  // ai < min(E, T*K): in bounds
+    if constexpr (ALL) {
+        load_weights(ai);
+        // Keeps the loads ahead of the early return below (the compiler
+        // would otherwise sink them past it, behind the record's arrival);
+        // the three scalar loads above are issued before it.
+        asm volatile("" ::: "memory");
+    }
     if (st || ai >= na) return;
     const uint32_t e = rec.x, cnt = rec.y, off = rec.z;
-    const uint32_t kt = a.kt;
     // 1. Activation rows [m0, m0 + rows) of the slot, contiguous in CSR
     //    order: chunks c < rows * a_stride / 8 (at most ACT per thread,
     //    checked by the host).  ROWS: kRowChunk rows at a time.
@@ -1411,16 +1483,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
     }
     uint32_t rows = ROWS ? min(cnt, kRowChunk) : cnt;
     K3X_DOWN_LOAD_ROWS(0, rows);
-    // 2. Code tiles and scale dwords of this wave's 16-row block, then the
-    //    pair rows.
-    const uint4* codes = a.dn_codes + e * a.codes_per_expert + (size_t)rb * kt * 64 + lane;
-    const uint32_t* scales = a.dn_scales + e * a.scales_per_expert + (size_t)rb * a.ks * 64 + lane;
-    uint4 c[TILES];
-    uint32_t sw[TILES / 4];
-#pragma unroll
-    for (int i = 0; i < TILES; ++i) c[i] = ntl(codes + (size_t)min((uint32_t)i, kt - 1) * 64);
-#pragma unroll
-    for (int i = 0; i < TILES / 4; ++i) sw[i] = ntl(scales + (size_t)min((uint32_t)i, a.ks - 1) * 64);
+    // 2. The weights (unless requested already), then the pair rows.
+    if constexpr (!ALL) load_weights(e);
     K3X_DOWN_LOAD_YROWS(0, rows);
     K3X_DOWN_STORE_ROWS(rows);
     __syncthreads();
@@ -1649,18 +1713,27 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
         sm.logits = b.logits;
         mark = begin_stage(ctx, K3X_STAGE_DECODE_GATE_UP);
         const bool two = d.experts > (uint32_t)kFrontWaves;
+        // Every expert picked (E <= K): the weights stream beside the route.
+        const bool all = d.experts <= K;
+        const dim3 grid(gu_blocks);
+#define K3X_SMALL(TT_, NE_)                                                                 \
+    do {                                                                                   \
+        if (all)                                                                          \
+            hipLaunchKernelGGL((small_route_gateup_kernel<TT_, NE_, true>), grid,          \
+                               dim3(kFrontThreads), xn_lds, main, sm);                     \
+        else                                                                               \
+            hipLaunchKernelGGL((small_route_gateup_kernel<TT_, NE_, false>), grid,         \
+                               dim3(kFrontThreads), xn_lds, main, sm);                     \
+    } while (0)
         if (T <= 2 && !two)
-            hipLaunchKernelGGL((small_route_gateup_kernel<2, 1>), dim3(gu_blocks),
-                               dim3(kFrontThreads), xn_lds, main, sm);
+            K3X_SMALL(2, 1);
         else if (T <= 2)
-            hipLaunchKernelGGL((small_route_gateup_kernel<2, 2>), dim3(gu_blocks),
-                               dim3(kFrontThreads), xn_lds, main, sm);
+            K3X_SMALL(2, 2);
         else if (!two)
-            hipLaunchKernelGGL((small_route_gateup_kernel<kMaxDecodeTokens, 1>), dim3(gu_blocks),
-                               dim3(kFrontThreads), xn_lds, main, sm);
+            K3X_SMALL(kMaxDecodeTokens, 1);
         else
-            hipLaunchKernelGGL((small_route_gateup_kernel<kMaxDecodeTokens, 2>), dim3(gu_blocks),
-                               dim3(kFrontThreads), xn_lds, main, sm);
+            K3X_SMALL(kMaxDecodeTokens, 2);
+#undef K3X_SMALL
         end_stage(ctx, mark);
     } else {
         mark = begin_stage(ctx, K3X_STAGE_DECODE_FRONT);
@@ -1681,9 +1754,13 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
         end_stage(ctx, mark);
     }
     mark = begin_stage(ctx, K3X_STAGE_DECODE_DOWN);
-    hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false>),
-                       dim3(max_active * (d.hidden / (16 * kDownWaves))), dim3(64 * kDownWaves),
-                       (size_t)T * d.inter * 2, main, dn);
+    const dim3 dn_grid(max_active * (d.hidden / (16 * kDownWaves)));
+    if (d.experts <= K)  // every expert active
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false, false, true>),
+                           dn_grid, dim3(64 * kDownWaves), (size_t)T * d.inter * 2, main, dn);
+    else
+        hipLaunchKernelGGL((decode_down_kernel<kDownTilesDecode, kDownActDecode, false>), dn_grid,
+                           dim3(64 * kDownWaves), (size_t)T * d.inter * 2, main, dn);
     end_stage(ctx, mark);
     ctx->kernel_launches += small ? 2 : 4;
     return hipGetLastError() == hipSuccess ? K3X_OK : K3X_ERR_BACKEND_UNAVAILABLE;

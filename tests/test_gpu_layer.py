@@ -553,18 +553,24 @@ def test_decode_deterministic(hip, c3):
         assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
 
 
-@pytest.mark.parametrize("cid,T", [(1, 1), (1, 2), (1, 4), (2, 1), (2, 3)])
-def test_small_route_two_launches(hip, oracle, cid, T):
+@pytest.mark.parametrize("cid,T,E", [(1, 1, None), (1, 2, None), (1, 4, None), (2, 1, None),
+                                     (2, 3, None), (1, 2, 4), (1, 3, 3)])
+def test_small_route_two_launches(hip, oracle, cid, T, E):
     """Few experts, no shared expert (configs 1 and 2): without the
     per-expert grouping taps the decode path runs in two launches, every
     gate/up workgroup finding the route itself.  Everything it writes equals
     the four-launch form's (taken with those taps, whose routing is checked
     against the oracle here) bit for bit: the same xn, logits, Top-K,
-    grouping, activations, per-pair rows and output."""
+    grouping, activations, per-pair rows and output.  E <= K (config 2, and
+    config 1 cut to 4 or 3 experts with Top-4 / Top-3) takes the form where
+    every expert is active and its weights are requested before the route
+    is known."""
     import dataclasses
     from synth import CONFIGS, SynthLayer
     k3x_amd, ctx = hip
     cfg = dataclasses.replace(CONFIGS[cid], tokens=T)
+    if E is not None:
+        cfg = dataclasses.replace(cfg, experts=E, top_k=E)
     layer = SynthLayer(oracle, cfg)
     bank = make_bank(k3x_amd, ctx, cfg)
     x = layer.x_bits()
