@@ -392,12 +392,15 @@ def make_bank(k3x_amd, ctx, cfg, layer=None):
 
 
 # Router on the fp64 matrix cores (T >= 256, H <= 8192) and its fallback:
-# ragged expert and token tiles, hidden sizes with padded terms, and every
-# path that writes the router weights (synthetic fill, host upload, device
-# copy) refreshes the residue-major copy the matrix-core router reads.
+# ragged expert and token tiles (among them 8 and 16 expert tiles, the
+# latter ragged), hidden sizes with padded terms, and every path that
+# writes the router weights (synthetic fill, host upload, device copy)
+# refreshes the residue-major copy the matrix-core router reads.
 @pytest.mark.parametrize("T,H,E", [(256, 1152, 20), (300, 7168, 40), (272, 8192, 16),
-                                   (257, 128, 33), (260, 8320, 18)],
-                         ids=["h1152", "h7168", "h8192", "h128", "h8320_fallback"])
+                                   (257, 128, 33), (260, 8320, 18), (300, 7168, 128),
+                                   (257, 1152, 250)],
+                         ids=["h1152", "h7168", "h8192", "h128", "h8320_fallback",
+                              "h7168_e128", "h1152_e250"])
 def test_router_shapes(hip, oracle, T, H, E):
     from synth import Config, SynthLayer
     k3x_amd, ctx = hip
