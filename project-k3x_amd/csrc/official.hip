@@ -146,6 +146,8 @@ __global__ __launch_bounds__(kThreads) void official_prepare_kernel(
 // resource, and their zero terms come after the row's last term, leaving
 // every sum unchanged.
 constexpr uint32_t kPrepRegHidden = 8192;
+// Up to this many tokens the prepare runs 1024 threads a token.
+constexpr uint32_t kPrepWideTokens = 64;
 
 __global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
     const float* __restrict__ prefix, const float* __restrict__ residual,
@@ -213,6 +215,118 @@ __global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
 #pragma unroll
     for (int j = 0; j < 32; ++j)
         if (tid + 256u * j < H) out[tid + 256 * j] = f32_to_bf16(__fmul_rn(__fmul_rn(v[0][j], inv2), nw[j]));
+}
+
+// Fp64 block sum over TPB threads in a fixed order: xor butterfly in each
+// wave, then the balanced pairwise tree over the waves; every thread gets
+// the result.
+// red: TPB / 64 + 1 doubles.
+template <int TPB>
+__device__ inline double block_sum_tpb(double v, double* red) {
+    constexpr int W = TPB / 64;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    if (wave == 0) {
+        // Lane i < W holds wave i's sum; level h adds lane i + h into lane i
+        // for i a multiple of 2 h.
+        double w = red[lane < W ? lane : 0];
+#pragma unroll
+        for (int h = 1; h < W; h *= 2) {
+            const double o = __shfl_down(w, h);
+            if (lane % (2 * h) == 0) w = w + o;
+        }
+        if (lane == 0) red[W] = w;
+    }
+    __syncthreads();
+    const double r = red[W];
+    __syncthreads();
+    return r;
+}
+
+// official_prepare_reg_kernel with TPB threads a token (thread tid holds k =
+// tid + TPB j, j < 8192 / TPB): for few tokens, more threads issue a row's
+// loads at once and run shorter sequential sums.  The same formulas; the
+// sums' order is this kernel's own (per-thread sequential, then
+// block_sum_tpb), within the contract's one bf16 ulp of the reference's
+// sequential sums.
+template <int TPB>
+__global__ __launch_bounds__(TPB) void official_prepare_tpb_kernel(
+    const float* __restrict__ prefix, const float* __restrict__ residual,
+    const float* __restrict__ res_norm, const float* __restrict__ res_proj,
+    const float* __restrict__ post_norm, uint32_t H, float eps, uint16_t* __restrict__ hidden,
+    uint32_t* status) {
+    constexpr int J = kPrepRegHidden / TPB;
+    __shared__ double red[TPB / 64 + 1];
+    if (*(volatile uint32_t*)status) return;
+    const uint32_t tid = threadIdx.x;
+    auto rsrc = [&](const float* base) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, H * 4,
+                                                 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t r0 = rsrc(residual + (size_t)blockIdx.x * H);
+    const __amdgpu_buffer_rsrc_t r1 = rsrc(prefix + (size_t)blockIdx.x * H);
+    const __amdgpu_buffer_rsrc_t rn = rsrc(res_norm), rp = rsrc(res_proj), pn = rsrc(post_norm);
+    // Loads past the row read 0 (their terms come after the row's last).
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, int j) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, tid * 4, j * TPB * 4, 0));
+    };
+    float v[2][J], nw[J], pw[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        v[0][j] = ld(r0, j);
+        v[1][j] = ld(r1, j);
+        nw[j] = ld(rn, j);
+        pw[j] = ld(rp, j);
+    }
+    int bad = 0;
+    float inv[2], score[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        double sq = 0.0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            bad |= !__builtin_isfinite(v[r][j]);
+            v[r][j] = bf16_round(v[r][j]);
+            sq = __builtin_fma((double)v[r][j], (double)v[r][j], sq);
+        }
+        sq = block_sum_tpb<TPB>(sq, red);
+        inv[r] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+        double sc = 0.0;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            sc = sc + ((double)__fmul_rn(v[r][j], inv[r]) * (double)nw[j]) * (double)pw[j];
+        score[r] = (float)block_sum_tpb<TPB>(sc, red);
+    }
+    if (__syncthreads_or(bad)) {
+        if (tid == 0) latch(status, K3X_ERR_INVALID_EXTENT);
+        return;
+    }
+    const float mx = score[0] >= score[1] ? score[0] : score[1];
+    float p0 = expf_cr(__fsub_rn(score[0], mx)), p1 = expf_cr(__fsub_rn(score[1], mx));
+    const float den = __fadd_rn(p0, p1);
+    p0 = __fdiv_rn(p0, den);
+    p1 = __fdiv_rn(p1, den);
+    // The post-norm weights are requested only now (not hoisted above the
+    // sums), so that they take no registers until then.
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < J; ++j) nw[j] = ld(pn, j);
+    double sq = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        v[0][j] = bf16_round(__fadd_rn(__fmul_rn(p0, v[0][j]), __fmul_rn(p1, v[1][j])));
+        sq = __builtin_fma((double)v[0][j], (double)v[0][j], sq);
+    }
+    sq = block_sum_tpb<TPB>(sq, red);
+    const float inv2 = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
+    uint16_t* out = hidden + (size_t)blockIdx.x * H;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if (tid + (uint32_t)TPB * j < H)
+            out[tid + TPB * j] = f32_to_bf16(__fmul_rn(__fmul_rn(v[0][j], inv2), nw[j]));
 }
 
 // fp32 values rounded to bf16 in place (synthetic bf16 weights held as fp32).
@@ -598,7 +712,11 @@ int k3x_hip_official_prepare(k3x_hip_ctx* ctx, k3x_hip_official* o, uint32_t T, 
     if (o->H > kPrepRegHidden && (size_t)o->H * 4 > ctx->max_lds_per_block)
         return K3X_ERR_INVALID_EXTENT;
     if (hipSetDevice(ctx->device) != hipSuccess) return K3X_ERR_BACKEND_UNAVAILABLE;
-    if (o->H <= kPrepRegHidden)
+    if (o->H <= kPrepRegHidden && T <= kPrepWideTokens)
+        hipLaunchKernelGGL(official_prepare_tpb_kernel<1024>, dim3(T), dim3(1024), 0, ctx->stream,
+                           prefix, block_residual, o->residual_norm, o->residual_proj,
+                           o->post_norm, o->H, eps, hidden, ctx->status);
+    else if (o->H <= kPrepRegHidden)
         hipLaunchKernelGGL(official_prepare_reg_kernel, dim3(T), dim3(kThreads), 0, ctx->stream,
                            prefix, block_residual, o->residual_norm, o->residual_proj,
                            o->post_norm, o->H, eps, hidden, ctx->status);
