@@ -149,7 +149,8 @@ constexpr uint32_t kPrepRegHidden = 8192;
 // Up to this many tokens the prepare runs 1024 threads a token.
 constexpr uint32_t kPrepWideTokens = 64;
 
-__global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void official_prepare_reg_kernel(
     const float* __restrict__ prefix, const float* __restrict__ residual,
     const float* __restrict__ res_norm, const float* __restrict__ res_proj,
     const float* __restrict__ post_norm, uint32_t H, float eps, uint16_t* __restrict__ hidden,
@@ -164,33 +165,61 @@ __global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
     const __amdgpu_buffer_rsrc_t r0 = rsrc(residual + (size_t)blockIdx.x * H);
     const __amdgpu_buffer_rsrc_t r1 = rsrc(prefix + (size_t)blockIdx.x * H);
     const __amdgpu_buffer_rsrc_t rn = rsrc(res_norm), rp = rsrc(res_proj), pn = rsrc(post_norm);
-    float v[2][32], nw[32], pw[32];
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, int j) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, tid * 4, j * 1024, 0));
+    };
+    auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
+    auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+    // Both rows, rounded to bf16 as they arrive, held packed in LDS
+    // (residual in the low half, prefix in the high half of word j, 32 KiB
+    // a token; each thread reads only its own words); the weight vectors,
+    // the same for every token, are read from the cache in batches where
+    // they are used.  Four tokens then share a compute unit.
+    __shared__ uint32_t s_pk[32][kThreads];
+    int bad = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        v[0][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r0, tid * 4, j * 1024, 0));
-        v[1][j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r1, tid * 4, j * 1024, 0));
-        nw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rn, tid * 4, j * 1024, 0));
-        pw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, tid * 4, j * 1024, 0));
+        const float a = ld(r0, j), b = ld(r1, j);
+        bad |= !__builtin_isfinite(a) | !__builtin_isfinite(b);
+        // Round to nearest even by the conversion instruction (f32_to_bf16's
+        // rule for every finite value; a non-finite one fails the call).
+        const bf16x2 h = {(__bf16)a, (__bf16)b};
+        s_pk[j][tid] = __builtin_bit_cast(uint32_t, h);
     }
-    int bad = 0;
+    // bad now, so that the raw values are not kept for it.
+    asm volatile("" : "+v"(bad));
+    constexpr int kB = 8;
     float inv[2], score[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         double sq = 0.0;
-#pragma unroll
+#pragma unroll 4
         for (int j = 0; j < 32; ++j) {
-            bad |= !__builtin_isfinite(v[r][j]);
-            v[r][j] = bf16_round(v[r][j]);
-            sq = __builtin_fma((double)v[r][j], (double)v[r][j], sq);
+            const double f = (double)(r ? hi(s_pk[j][tid]) : lo(s_pk[j][tid]));
+            sq = __builtin_fma(f, f, sq);
         }
         sq = block_sum(sq, red);
         inv[r] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
-        double sc = 0.0;
-#pragma unroll
-        for (int j = 0; j < 32; ++j)
-            sc = sc + ((double)__fmul_rn(v[r][j], inv[r]) * (double)nw[j]) * (double)pw[j];
-        score[r] = (float)block_sum(sc, red);
     }
+    double sc[2] = {0.0, 0.0};
+#pragma unroll 1
+    for (int j0 = 0; j0 < 32; j0 += kB) {
+        asm volatile("" ::: "memory");  // the batch's loads stay here
+        float nw[kB], pw[kB];
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            nw[j] = ld(rn, j0 + j);
+            pw[j] = ld(rp, j0 + j);
+        }
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const uint32_t w = s_pk[j0 + j][tid];
+            sc[0] = sc[0] + ((double)__fmul_rn(lo(w), inv[0]) * (double)nw[j]) * (double)pw[j];
+            sc[1] = sc[1] + ((double)__fmul_rn(hi(w), inv[1]) * (double)nw[j]) * (double)pw[j];
+        }
+    }
+    score[0] = (float)block_sum(sc[0], red);
+    score[1] = (float)block_sum(sc[1], red);
     if (__syncthreads_or(bad)) {
         if (tid == 0) latch(status, K3X_ERR_INVALID_EXTENT);
         return;
@@ -200,21 +229,30 @@ __global__ __launch_bounds__(kThreads) void official_prepare_reg_kernel(
     const float den = __fadd_rn(p0, p1);
     p0 = __fdiv_rn(p0, den);
     p1 = __fdiv_rn(p1, den);
-#pragma unroll
-    for (int j = 0; j < 32; ++j)
-        nw[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pn, tid * 4, j * 1024, 0));
+    // The mix replaces the pair in LDS (fp32 bits).
     double sq = 0.0;
-#pragma unroll
+#pragma unroll 4
     for (int j = 0; j < 32; ++j) {
-        v[0][j] = bf16_round(__fadd_rn(__fmul_rn(p0, v[0][j]), __fmul_rn(p1, v[1][j])));
-        sq = __builtin_fma((double)v[0][j], (double)v[0][j], sq);
+        const uint32_t w = s_pk[j][tid];
+        const float m = bf16_round(__fadd_rn(__fmul_rn(p0, lo(w)), __fmul_rn(p1, hi(w))));
+        s_pk[j][tid] = __float_as_uint(m);
+        sq = __builtin_fma((double)m, (double)m, sq);
     }
     sq = block_sum(sq, red);
     const float inv2 = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn((float)__ddiv_rn(sq, (double)H), eps)));
     uint16_t* out = hidden + (size_t)blockIdx.x * H;
+#pragma unroll 1
+    for (int j0 = 0; j0 < 32; j0 += kB) {
+        asm volatile("" ::: "memory");
+        float g[kB];
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
-        if (tid + 256u * j < H) out[tid + 256 * j] = f32_to_bf16(__fmul_rn(__fmul_rn(v[0][j], inv2), nw[j]));
+        for (int j = 0; j < kB; ++j) g[j] = ld(pn, j0 + j);
+#pragma unroll
+        for (int j = 0; j < kB; ++j)
+            if (tid + 256u * (j0 + j) < H)
+                out[tid + 256 * (j0 + j)] = f32_to_bf16(
+                    __fmul_rn(__fmul_rn(__uint_as_float(s_pk[j0 + j][tid]), inv2), g[j]));
+    }
 }
 
 // Fp64 block sum over TPB threads in a fixed order: xor butterfly in each
