@@ -1233,10 +1233,15 @@ struct SmallLds {
 };
 
 // NE router rows per wave (experts wave + kFrontWaves i); TT bounds T.
-// Workgroup b is unit (active slot, 16-row block).  ALL: every expert is
-// active (E <= K), so slot s holds expert s (the slots ascend by expert):
-// the unit's code tiles and scales are requested once the router products
-// are done, beside the Top-K and the grouping, instead of after them.
+// Workgroup b is unit (active slot, 16-row block), and routes by itself.
+// ALL: every expert is active (E <= K), so slot s holds expert s (the slots
+// ascend by expert) and its CSR rows are s T .. s T + T - 1, token by token
+// (every token routes to every expert once): the units need no route.
+// Workgroups [0, E I / 16) are then units that request their code tiles
+// and scales with the x / gamma loads and go straight from xn to their
+// products, and the one workgroup after them finds the route and stores it
+// for the down launch (which alone reads it, for the slot order and the
+// weights of the mix).
 template <int TT, int NE, bool ALL>
 __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(SmallArgs a) {
     static_assert(kFrontThreads == 64 * kGuWaves, "one workgroup shape for route and gate/up");
@@ -1245,8 +1250,25 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
     const uint32_t lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t T = a.sel.T, H = a.gu.H, E = a.sel.E, J = H / 256;
     const uint32_t per_expert = a.gu.I / 16;
-    const uint32_t all_e = blockIdx.x / per_expert, all_rb = blockIdx.x % per_expert;
-    GuUnitRegs gw;
+    if constexpr (ALL) {
+        if (blockIdx.x < E * per_expert) {
+            const uint32_t e = blockIdx.x / per_expert, rb = blockIdx.x % per_expert;
+            GuUnitRegs gw;
+            // A non-finite x (or an earlier launch's error) ends every
+            // workgroup here; the route workgroup latches it.
+            if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns, nullptr,
+                                         nullptr, a.sel.status,
+                                         [&]() { gateup_unit_load(a.gu, e, rb, gw); }, [] {}))
+                return;
+            uint32_t toks = 0;  // tokens of the slot's first four rows: 0, 1, ...
+            for (uint32_t j = 1; j < min(T, 4u); ++j) toks |= j << (8 * j);
+            gateup_unit_compute(a.gu, rb, make_uint4(e, T, e * T, toks),
+                                reinterpret_cast<const uint16_t*>(dyn_lds), gw, sh.red);
+            return;
+        }
+    }
+    // The workgroup that stores the route (and xn and the logits).
+    const bool store = ALL || blockIdx.x == 0;
     constexpr int kPer = kSmallRowLoads / NE;  // J <= kPer (checked on the host)
     float4 wb[NE][kPer];
     auto prefetch = [&]() {
@@ -1260,7 +1282,7 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
         }
     };
     if (!build_xn<kFrontThreads>(a.x, a.gamma, T, H, a.eps, dyn_lds, sh.ns,
-                                 blockIdx.x == 0 ? a.xn : nullptr, a.sel.status, a.sel.status,
+                                 store ? a.xn : nullptr, a.sel.status, a.sel.status,
                                  prefetch, [] {}))
         return;
     // Logits of this wave's experts: partial 4 l + c sums j = 0, 1, ... in
@@ -1296,35 +1318,27 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
             const float v = (float)canon_reduce(p[t]);
             if (lane == 0) {
                 sh.lg[t][e] = v;
-                if (blockIdx.x == 0) a.logits[(size_t)t * E + e] = v;
+                if (store) a.logits[(size_t)t * E + e] = v;
             }
         }
     }
-    // The unit's weights stream while the block finds the Top-K and the
-    // grouping (LDS work only; the bias is requested first, since loads
-    // complete in order).
     const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
     const float bias_e = a.sel.bias[ee];
-    if constexpr (ALL) gateup_unit_load(a.gu, all_e, all_rb, gw);
     __syncthreads();
     // Top-K and grouping, as decode_select_kernel's block 0 (this block's
-    // copy in LDS; block 0 stores it).
+    // copy in LDS; the storing block stores it).
     float lg[kMaxDecodeTokens];
 #pragma unroll
     for (int t = 0; t < kMaxDecodeTokens; ++t) lg[t] = sh.lg[min((uint32_t)t, T - 1)][ee];
     SelectArgs sa = a.sel;
-    sa.local_only = blockIdx.x != 0;
+    sa.local_only = !store;
     if (!select_topk(sa, sh.sel, lg, bias_e)) return;
     select_group(sa, sh.sel);
+    if constexpr (ALL) return;  // the route workgroup has no unit
     __syncthreads();
     if (sh.sel.bad) return;
-    const uint16_t* s_xn = reinterpret_cast<const uint16_t*>(dyn_lds);
-    if constexpr (ALL) {
-        // Every expert active: slot all_e holds expert all_e.
-        gateup_unit_compute(a.gu, all_rb, sh.sel.rec[all_e], s_xn, gw, sh.red);
-    } else {
-        gateup_unit_lds(a.gu, blockIdx.x, s_xn, sh.sel.rec, sh.sel.na, sh.red);
-    }
+    gateup_unit_lds(a.gu, blockIdx.x, reinterpret_cast<const uint16_t*>(dyn_lds), sh.sel.rec,
+                    sh.sel.na, sh.red);
 }
 
 // ---------------------------------------------------------------------------
@@ -1517,6 +1531,33 @@ __global__ __launch_bounds__(64 * kDownWaves) void decode_down_kernel(DownArgs a
             if (4 * g + q < rows)
                 __hip_atomic_store(a.y + (size_t)yrow[q] * a.H + rb * 16 + n, acc[q],
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (!ROWS) {
+            if (a.mix && a.K == 1) {
+                // One router slot: each row's value is its token's whole
+                // mix, formed here as decode_mix forms it (0 + w y, then the
+                // shared row), with no counter (they stay zero) and no
+                // reload of y.  yrow[q] is the token (slot 0).
+                const uint32_t h = rb * 16 + n;
+                float w[4], sh[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = a.weights[yrow[q]];
+                    sh[q] = a.shared_y ? a.shared_y[(size_t)yrow[q] * a.H + h] : 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (4 * g + q >= rows) continue;
+                    const float yu = a.round_y
+                                         ? __uint_as_float((uint32_t)f32_to_bf16(acc[q]) << 16)
+                                         : acc[q];
+                    const float mix = __fadd_rn(0.0f, __fmul_rn(w[q], yu));
+                    const float v = a.shared_y ? __fadd_rn(mix, sh[q]) : mix;
+                    a.out[(size_t)yrow[q] * a.H + h] = f32_to_bf16(v);
+                    if (a.out_f32) a.out_f32[(size_t)yrow[q] * a.H + h] = v;
+                }
+                return;
+            }
+        }
         if (!ROWS) break;
         m0 += rows;
         if (m0 >= cnt) return;  // block-uniform; no mix (checked on the host)
@@ -1715,7 +1756,8 @@ int decode_forward(k3x_hip_ctx* ctx, k3x_hip_bank* bank, const k3x_hip_moe_param
         const bool two = d.experts > (uint32_t)kFrontWaves;
         // Every expert picked (E <= K): the weights stream beside the route.
         const bool all = d.experts <= K;
-        const dim3 grid(gu_blocks);
+        // ALL: one more workgroup, the route's.
+        const dim3 grid(gu_blocks + (all ? 1 : 0));
 #define K3X_SMALL(TT_, NE_)                                                                 \
     do {                                                                                   \
         if (all)                                                                          \
