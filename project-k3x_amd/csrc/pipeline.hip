@@ -1604,14 +1604,12 @@ __global__ __launch_bounds__(64 * W) void dense_gemv_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 // VEC adjacent h per thread; the slots' loads are issued in batches of 16
 // ahead of the slot-ordered multiply-adds.  H % VEC == 0.
+// The per-pair rows are read once, with non-temporal loads (they pass
+// through the L2 without being kept).
 template <int VEC>
-struct CombineVec;
+struct CombineVec { typedef float T __attribute__((ext_vector_type(VEC))); };
 template <>
 struct CombineVec<1> { typedef float T; };
-template <>
-struct CombineVec<2> { typedef float2 T; };
-template <>
-struct CombineVec<4> { typedef float4 T; };
 
 template <int VEC>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y,
@@ -1639,7 +1637,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 #pragma unroll
         for (uint32_t i = 0; i < kBatch; ++i) {
             const uint32_t s = min(s0 + i, K - 1);  // clamped: loads stay unconditional
-            v[i] = *reinterpret_cast<const vec_t*>(yt + (size_t)s * H);
+            v[i] = __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(yt + (size_t)s * H));
             ws[i] = wt[s];
         }
 #pragma unroll
