@@ -1214,6 +1214,79 @@ __device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t bl
 constexpr uint32_t kSmallMaxExperts = 2 * kFrontWaves;  // two router rows a wave at most
 constexpr int kSmallRowLoads = 32;  // float4 router loads per lane, its rows together
 
+// The route when every expert is picked (E == K <= 16, T <= 4), by one
+// wave: lane 16 t + e holds expert e of token t.  The same keys, checks,
+// exact ranking (rank r = number of larger keys = router slot), slot-order
+// renormalisation and stores as select_topk and select_group, which it
+// replaces for this shape: every token routes to every expert once, so the
+// CSR row of (token t, expert e) is e T + t and slot e's record is {e, T,
+// e T, tokens 0, 1, ...}.  Nothing is stored when a check fails (the error
+// latched as there).
+__device__ void select_all(const SelectArgs& a, const float (&lgs)[kMaxDecodeTokens][16],
+                           uint32_t lane) {
+    const uint32_t T = a.T, E = a.E, K = a.K;
+    const uint32_t t = lane >> 4, e = lane & 15;
+    const bool valid = t < T && e < E;
+    const bool dbl = a.renorm == K3X_RENORM_DOUBLE;
+    const float lg = lgs[min(t, T - 1)][min(e, E - 1)];
+    const float b = a.bias[min(e, E - 1)];
+    uint32_t err = 0;
+    float s = 0.0f;
+    uint64_t key = 0;
+    if (valid) {
+        if (dbl && (!__builtin_isfinite(lg) || !__builtin_isfinite(b))) err = K3X_ERR_INVALID_EXTENT;
+        s = sigmoid_cr(lg);
+        const float adj = __fadd_rn(s, b);
+        if (!dbl && (!__builtin_isfinite(s) || s < 0.0f || s > 1.0f || !__builtin_isfinite(b) ||
+                     !__builtin_isfinite(adj)))
+            err = K3X_ERR_INVALID_STATE;
+        key = topk_key(adj, e);
+    }
+    err = wave_max_u32(err);
+    if (err) {
+        if (lane == 0) latch(a.status, err);
+        return;
+    }
+    // Rank among the token's E keys (distinct: the low half holds the expert).
+    const uint32_t row0 = lane & ~15u;
+    uint32_t r = 0;
+    for (uint32_t j = 0; j < E; ++j) {
+        const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)key, (int)(row0 + j));
+        const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(key >> 32), (int)(row0 + j));
+        r += (((uint64_t)hi << 32) | lo) > key;
+    }
+    // Denominator: the scores in slot order, summed in sequence.
+    float den_f = 0.0f;
+    double den_d = 0.0;
+    for (uint32_t q = 0; q < K; ++q) {
+        const uint64_t m = __ballot(valid && r == q);
+        const uint32_t src = row0 + (uint32_t)__builtin_ctzll(((m >> row0) & 0xffffull) | 0x10000ull);
+        const float x = __shfl(s, (int)min(src, 63u));
+        den_f = __fadd_rn(den_f, x);
+        den_d = __dadd_rn(den_d, (double)x);
+    }
+    const bool ok = dbl ? (__builtin_isfinite(den_d) && den_d > 0.0)
+                        : (__builtin_isfinite(den_f) && den_f > 0.0f);
+    if (__ballot(valid && !ok)) {
+        if (lane == 0) latch(a.status, dbl ? K3X_ERR_INVALID_EXTENT : K3X_ERR_INVALID_STATE);
+        return;
+    }
+    if (!valid || a.local_only) return;
+    const float w = dbl ? __fmul_rn((float)__ddiv_rn((double)s, den_d), a.routed_scale)
+                        : __fmul_rn(__fdiv_rn(s, den_f), a.routed_scale);
+    const uint32_t p = t * K + r, row = e * T + t;
+    a.pair_token[row] = t;
+    a.pair_slot[row] = r;
+    a.ids[p] = e;
+    a.weights[p] = w;
+    if (t == 0) {
+        uint32_t toks = 0;
+        for (uint32_t j = 1; j < min(T, 4u); ++j) toks |= j << (8 * j);
+        a.arec[e] = make_uint4(e, T, e * T, toks);
+        if (e == 0) *a.n_active = E;
+    }
+}
+
 struct SmallArgs {
     const uint16_t* x;
     const float* gamma;
@@ -1322,6 +1395,13 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
             }
         }
     }
+    if constexpr (ALL) {
+        // The route workgroup: its first wave finds the route from the
+        // logits in LDS.
+        __syncthreads();
+        if (wave == 0) select_all(a.sel, sh.lg, lane);
+        return;
+    }
     const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
     const float bias_e = a.sel.bias[ee];
     __syncthreads();
@@ -1334,7 +1414,6 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
     sa.local_only = !store;
     if (!select_topk(sa, sh.sel, lg, bias_e)) return;
     select_group(sa, sh.sel);
-    if constexpr (ALL) return;  // the route workgroup has no unit
     __syncthreads();
     if (sh.sel.bad) return;
     gateup_unit_lds(a.gu, blockIdx.x, reinterpret_cast<const uint16_t*>(dyn_lds), sh.sel.rec,
