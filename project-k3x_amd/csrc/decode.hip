@@ -1214,16 +1214,18 @@ __device__ __forceinline__ void gateup_unit_lds(const GateUpArgs& a, uint32_t bl
 constexpr uint32_t kSmallMaxExperts = 2 * kFrontWaves;  // two router rows a wave at most
 constexpr int kSmallRowLoads = 32;  // float4 router loads per lane, its rows together
 
-// The route when every expert is picked (E == K <= 16, T <= 4), by one
-// wave: lane 16 t + e holds expert e of token t.  The same keys, checks,
-// exact ranking (rank r = number of larger keys = router slot), slot-order
-// renormalisation and stores as select_topk and select_group, which it
-// replaces for this shape: every token routes to every expert once, so the
-// CSR row of (token t, expert e) is e T + t and slot e's record is {e, T,
-// e T, tokens 0, 1, ...}.  Nothing is stored when a check fails (the error
-// latched as there).
-__device__ void select_all(const SelectArgs& a, const float (&lgs)[kMaxDecodeTokens][16],
-                           uint32_t lane) {
+// The route of a few experts (E <= 16, T <= 4) by one wave: lane 16 t + e
+// holds expert e of token t.  The same keys, checks, exact ranking (rank r =
+// number of larger keys; r < K is router slot r), slot-order
+// renormalisation and CSR grouping as select_topk and select_group, which it
+// replaces for these shapes.  With M the ballot of the selected lanes, every
+// grouping quantity is a population count: the CSR row of a selected (t, e)
+// is (pairs of experts below e) + (earlier tokens that picked e), and the
+// active slots ascend by expert.  The slot records and their count go to
+// LDS (sh.rec, sh.na, and sh.bad: nonzero when a check failed, the error
+// latched as there); store: the route also goes to the global outputs.
+__device__ void select_small(const SelectArgs& a, const float (&lgs)[kMaxDecodeTokens][16],
+                             uint32_t lane, SelectShared& sh, bool store) {
     const uint32_t T = a.T, E = a.E, K = a.K;
     const uint32_t t = lane >> 4, e = lane & 15;
     const bool valid = t < T && e < E;
@@ -1244,7 +1246,10 @@ __device__ void select_all(const SelectArgs& a, const float (&lgs)[kMaxDecodeTok
     }
     err = wave_max_u32(err);
     if (err) {
-        if (lane == 0) latch(a.status, err);
+        if (lane == 0) {
+            latch(a.status, err);
+            sh.bad = 1;
+        }
         return;
     }
     // Rank among the token's E keys (distinct: the low half holds the expert).
@@ -1255,6 +1260,7 @@ __device__ void select_all(const SelectArgs& a, const float (&lgs)[kMaxDecodeTok
         const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(key >> 32), (int)(row0 + j));
         r += (((uint64_t)hi << 32) | lo) > key;
     }
+    const bool sel = valid && r < K;
     // Denominator: the scores in slot order, summed in sequence.
     float den_f = 0.0f;
     double den_d = 0.0;
@@ -1268,23 +1274,42 @@ __device__ void select_all(const SelectArgs& a, const float (&lgs)[kMaxDecodeTok
     const bool ok = dbl ? (__builtin_isfinite(den_d) && den_d > 0.0)
                         : (__builtin_isfinite(den_f) && den_f > 0.0f);
     if (__ballot(valid && !ok)) {
-        if (lane == 0) latch(a.status, dbl ? K3X_ERR_INVALID_EXTENT : K3X_ERR_INVALID_STATE);
+        if (lane == 0) {
+            latch(a.status, dbl ? K3X_ERR_INVALID_EXTENT : K3X_ERR_INVALID_STATE);
+            sh.bad = 1;
+        }
         return;
     }
-    if (!valid || a.local_only) return;
+    // Grouping.  Bit 16 t' + e' of M: token t' picked expert e'.
+    const uint64_t M = __ballot(sel);
+    constexpr uint64_t kRows = 0x0001000100010001ull;
+    const uint64_t col = kRows << e;
+    const uint32_t below = (uint32_t)__popcll(M & (kRows * ((1ull << e) - 1)));
+    const uint32_t rin = (uint32_t)__popcll(M & col & ((1ull << (16 * t)) - 1));
+    const uint32_t cnt = (uint32_t)__popcll(M & col);
+    const uint32_t act = (uint32_t)((M | M >> 16 | M >> 32 | M >> 48) & 0xffffu);
+    if (t == 0 && (act >> e) & 1u) {  // one lane per active expert: its slot record
+        const uint32_t ai = (uint32_t)__popc(act & ((1u << e) - 1));
+        uint32_t toks = 0, j = 0;
+        for (uint32_t tt = 0; tt < T; ++tt)
+            if ((M >> (16 * tt + e)) & 1ull) toks |= tt << (8 * j++);
+        const uint4 rec = make_uint4(e, cnt, below, toks);
+        sh.rec[ai] = rec;
+        if (store) a.arec[ai] = rec;
+    }
+    if (lane == 0) {
+        sh.na = (uint32_t)__popc(act);
+        sh.bad = 0;
+        if (store) *a.n_active = (uint32_t)__popc(act);
+    }
+    if (!sel || !store) return;
     const float w = dbl ? __fmul_rn((float)__ddiv_rn((double)s, den_d), a.routed_scale)
                         : __fmul_rn(__fdiv_rn(s, den_f), a.routed_scale);
-    const uint32_t p = t * K + r, row = e * T + t;
+    const uint32_t p = t * K + r, row = below + rin;
     a.pair_token[row] = t;
     a.pair_slot[row] = r;
     a.ids[p] = e;
     a.weights[p] = w;
-    if (t == 0) {
-        uint32_t toks = 0;
-        for (uint32_t j = 1; j < min(T, 4u); ++j) toks |= j << (8 * j);
-        a.arec[e] = make_uint4(e, T, e * T, toks);
-        if (e == 0) *a.n_active = E;
-    }
 }
 
 struct SmallArgs {
@@ -1395,25 +1420,11 @@ __global__ __launch_bounds__(kFrontThreads) void small_route_gateup_kernel(Small
             }
         }
     }
-    if constexpr (ALL) {
-        // The route workgroup: its first wave finds the route from the
-        // logits in LDS.
-        __syncthreads();
-        if (wave == 0) select_all(a.sel, sh.lg, lane);
-        return;
-    }
-    const uint32_t ee = min((uint32_t)threadIdx.x, E - 1);
-    const float bias_e = a.sel.bias[ee];
+    // The route, by the first wave from the logits in LDS (this block's
+    // copy of the slot records in LDS; the storing block stores it).
     __syncthreads();
-    // Top-K and grouping, as decode_select_kernel's block 0 (this block's
-    // copy in LDS; the storing block stores it).
-    float lg[kMaxDecodeTokens];
-#pragma unroll
-    for (int t = 0; t < kMaxDecodeTokens; ++t) lg[t] = sh.lg[min((uint32_t)t, T - 1)][ee];
-    SelectArgs sa = a.sel;
-    sa.local_only = !store;
-    if (!select_topk(sa, sh.sel, lg, bias_e)) return;
-    select_group(sa, sh.sel);
+    if (wave == 0) select_small(a.sel, sh.lg, lane, sh.sel, store);
+    if constexpr (ALL) return;  // the route workgroup has no unit
     __syncthreads();
     if (sh.sel.bad) return;
     gateup_unit_lds(a.gu, blockIdx.x, reinterpret_cast<const uint16_t*>(dyn_lds), sh.sel.rec,
